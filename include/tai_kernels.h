@@ -1,0 +1,249 @@
+/*
+ * tai_kernels.h - C ABI of libtai_kernels.so, the gfx950 (MI355X) kernels that serve
+ * the fused inference operators TorchAir lowers FX graphs onto.
+ *
+ * Conventions shared by every entry point
+ *   - Plain device pointers and sizes; no framework types cross this boundary.
+ *   - dtype codes are torch ScalarType codes, the same integers TorchAir's converters
+ *     pass as dst_type / output_dtype (python/torchair/ge/_ge_graph.py:215,
+ *     python/torchair/_ge_concrete_graph/ge_converter/custom/grouped_matmul.py:178-195).
+ *   - The caller owns every buffer. The library never allocates device memory and never
+ *     synchronises; every kernel is enqueued on `stream` (a hipStream_t), so a call may be
+ *     captured into a hipGraph. Data-dependent sizes (sequence lengths, block tables,
+ *     group lists) are read on the device, so a graph replay with new values is correct.
+ *   - Return 0 on success; otherwise a TAI_ERR_* code, with a message in tai_last_error()
+ *     (thread-local).
+ *   - Entry points that need scratch memory take (workspace, ws_bytes) and export a
+ *     *_workspace_size() query (the role of the reference's
+ *     _npu_fused_infer_attention_score_get_max_workspace, python/torchair/_acl_concrete_graph/acl_graph.py:100-108).
+ */
+#ifndef TAI_KERNELS_H_
+#define TAI_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* torch ScalarType codes */
+#define TAI_DT_UINT8 0
+#define TAI_DT_INT8 1
+#define TAI_DT_INT16 2
+#define TAI_DT_INT32 3
+#define TAI_DT_INT64 4
+#define TAI_DT_FP16 5
+#define TAI_DT_FP32 6
+#define TAI_DT_BF16 15
+#define TAI_DT_NONE (-1)
+
+#define TAI_OK 0
+#define TAI_ERR_INVALID 1     /* bad argument (shape, dtype, null pointer) */
+#define TAI_ERR_UNSUPPORTED 2 /* valid for the reference, not implemented here */
+#define TAI_ERR_LAUNCH 3      /* HIP runtime error */
+#define TAI_ERR_WORKSPACE 4   /* workspace smaller than *_workspace_size() */
+
+/* Layout of the second GEMM operand. */
+#define TAI_LAYOUT_KN 0 /* row-major [K, N] (N contiguous) */
+#define TAI_LAYOUT_NK 1 /* row-major [N, K] (K contiguous): the transpose_x2 / weight.t() view */
+
+const char* tai_last_error(void);
+int tai_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_dynamic_quant: symmetric per-row int8 quantisation.
+ * Replaces ge.DynamicQuant emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dynamic_quant.py:8-42
+ *   (prototype third_party/ascend/include/ops/op_proto/inc/nn_quantize.h:47-56).
+ * x: [rows, cols] of x_dtype (BF16/FP16/FP32). smooth_scales: NULL, [cols] or
+ * [num_groups, cols] fp32. group_index: NULL or [num_groups] cumulative row ends
+ * (index dtype INT32/INT64); row r uses smooth row g = first g with r < group_index[g].
+ * y: [rows, cols] int8, scale: [rows] fp32.
+ * ------------------------------------------------------------------------------------- */
+int tai_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                      const float* smooth_scales, const void* group_index, int group_index_dtype,
+                      int64_t num_groups, int8_t* y, float* scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_dequant_swiglu_quant (quant_mode=1 dynamic, swiglu_mode=0, round_mode=0 rint).
+ * Replaces ge.DequantSwigluQuant emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dequant_swiglu_quant.py:5-47
+ *   (prototype experiment_ops.h:3765-3812; meta
+ *   python/torchair/_contrib/custom_torch_ops/auto_register_custom_torch_ops.py:155-191).
+ * x: [rows, 2n] int32. weight_scale: [2n] fp32 or, with group_index, [num_groups, 2n].
+ * activation_scale: NULL or [rows] fp32. bias: NULL or [2n] / [num_groups, 2n] of
+ * bias_dtype (INT32 added before dequant; FP32 added after). quant_scale: NULL, [n] or
+ * [num_groups, n] fp32. group_index: NULL or [num_groups] per-group row COUNTS (INT32/INT64);
+ * rows past the total are written as y=0, scale=0.
+ * y: [rows, n] int8, scale: [rows] fp32.
+ * ------------------------------------------------------------------------------------- */
+int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t n2,
+                             const float* weight_scale, const float* activation_scale,
+                             const void* bias, int bias_dtype, const float* quant_scale,
+                             const void* group_index, int group_index_dtype, int64_t num_groups,
+                             int activate_left, int8_t* y, float* scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_quant_matmul (W8A8): acc = x1 @ x2 with exact int32 accumulation, then
+ *   out_dtype INT32: acc (+ int32 bias)
+ *   out_dtype BF16/FP16/FP32: (acc [+ int32 bias]) * scale[n] * pertoken_scale[m] [+ fp32 bias]
+ * Replaces ge.QuantBatchMatmulV3 emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/quantmatmul.py:63-255
+ *   (prototype third_party/ascend/include/ops/op_proto/inc/fusion_ops.h:440-451).
+ * x1: [M, K] int8 row-major; x2: int8, layout x2_layout (TAI_LAYOUT_KN / _NK).
+ * scale: [N] or [1] fp32 (scale_len 1 or N), may be NULL for INT32 output.
+ * pertoken_scale: NULL or [M] fp32. bias: NULL or [N] of bias_dtype (INT32 or FP32).
+ * out: [M, N] of out_dtype.
+ * ------------------------------------------------------------------------------------- */
+int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n,
+                     int x2_layout, const float* scale, int64_t scale_len,
+                     const float* pertoken_scale, const void* bias, int bias_dtype,
+                     int out_dtype, void* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_grouped_matmul, int8 path with split_item 2/3 and group_type 0 (groups along M):
+ * rows [off_e, off_{e+1}) of x multiply weight[e].
+ * Replaces ge.GroupedMatmul emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/grouped_matmul.py:210-365
+ *   (prototype experiment_ops.h:3636-3662).
+ * x: [m, k] int8. weight: [num_groups, k, n] (TAI_LAYOUT_KN) or [num_groups, n, k] (_NK).
+ * group_list: [num_groups] int64 on the device; group_list_type 0 = cumulative row ends,
+ * 1 = per-group counts. Rows past the last group end are written as zero.
+ * scale: NULL or [num_groups, n] fp32; per_token_scale: NULL or [m] fp32;
+ * bias: NULL or [num_groups, n] of bias_dtype (INT32 or FP32).
+ * out: [m, n] of out_dtype (INT32, BF16, FP16, FP32).
+ * ------------------------------------------------------------------------------------- */
+size_t tai_grouped_matmul_workspace_size(int64_t m, int64_t n, int64_t num_groups);
+int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                       int64_t num_groups, int w_layout, const int64_t* group_list,
+                       int group_list_type, const float* scale, const float* per_token_scale,
+                       const void* bias, int bias_dtype, int out_dtype, void* out,
+                       void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_moe_gating_top_k: grouped top-k expert selection (DeepSeek-V3 "noaux_tc").
+ * Replaces ge.MoeGatingTopK emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_moe_gating_top_k.py:4-22
+ *   (prototype experiment_ops.h:3723-3764; meta auto_register_custom_torch_ops.py:103-114).
+ * x: [t, e] of x_dtype; bias: NULL or [e] of bias_dtype. norm_type 0 softmax, 1 sigmoid;
+ * group_select_mode 0 group max, 1 sum of the group's top two.
+ * y: [t, k] x_dtype; expert_idx: [t, k] int32; out: [t, e] fp32 (written when out_flag).
+ * ------------------------------------------------------------------------------------- */
+int tai_moe_gating_top_k(const void* x, int x_dtype, int64_t t, int64_t e, int k,
+                         const void* bias, int bias_dtype, int k_group, int group_count,
+                         int group_select_mode, int renorm, int norm_type, int out_flag,
+                         float routed_scaling_factor, float eps, void* y, int32_t* expert_idx,
+                         float* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_moe_init_routing_v2 (dropless, drop_pad_mode 0, quant_mode -1).
+ * Replaces ge.MoeInitRoutingV3 emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_moe_init_routing_v2.py:41-91
+ *   (prototype experiment_ops.h:2138-2190).
+ * Source slot p = token * k + j. Slots whose expert lies in [expert_start, expert_end)
+ * are sorted stably by expert (ties: ascending p); the first `active_rows` of them are
+ * materialised. expanded_x: [active_rows, h] (elem_bytes per element) with
+ * expanded_x[i] = x[src(i) / k]. expanded_row_idx: [t*k] int32 -
+ *   row_idx_type 0: indexed by p, the destination row of slot p (-1 when dropped);
+ *   row_idx_type 1: indexed by destination row i, the source slot src(i) (-1 past the end).
+ * expert_tokens: [expert_end - expert_start] int64, counts (type 1) or cumsum (type 0).
+ * scale: NULL or [t] fp32 -> expanded_scale [active_rows] = scale[src(i) / k].
+ * ------------------------------------------------------------------------------------- */
+size_t tai_moe_init_routing_workspace_size(int64_t t, int k, int64_t num_experts);
+int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t, int64_t h,
+                            const int32_t* expert_idx, int k, const float* scale,
+                            int64_t active_rows, int expert_start, int expert_end,
+                            int expert_tokens_num_type, int row_idx_type, void* expanded_x,
+                            int32_t* expanded_row_idx, int64_t* expert_tokens,
+                            float* expanded_scale, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_moe_init_routing (legacy). Replaces ge.MoeInitRouting emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/moe_init_routing.py:10-21
+ *   (prototype experiment_ops.h:2112-2135).
+ * row_idx: [t, k] int32 (conventionally arange(k*t).view(k, t).T). Slots p = token*k + j
+ * are sorted stably by expert. Outputs (active_rows = min(active_num, t) * k rows):
+ *   expanded_x[i] = x[row_idx_flat[src(i)] % t]; expanded_row_idx[row_idx_flat[src(i)]] = i;
+ *   expanded_expert_idx[i] = expert of src(i).
+ * ------------------------------------------------------------------------------------- */
+int tai_moe_init_routing(const void* x, int elem_bytes, int64_t t, int64_t h,
+                         const int32_t* row_idx, const int32_t* expert_idx, int k,
+                         int64_t num_experts, int64_t active_rows, void* expanded_x,
+                         int32_t* expanded_row_idx, int32_t* expanded_expert_idx,
+                         void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_moe_finalize_routing. Replaces ge.MoeFinalizeRouting(V2) emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_moe_finalize_routing.py:21-41
+ *   (prototype experiment_ops.h:2196-2219).
+ * y[t] = skip1[t] + skip2[t] + sum_j scales[t,j] * (expanded[src_to_dst[p(t,j)]] + bias[expert[t,j]])
+ * with p(t,j) = j*t_rows + t for drop_pad_mode 0 and t*k + j for drop_pad_mode 2.
+ * All row tensors share `dtype` (BF16/FP16/FP32); scales has scales_dtype; optional
+ * inputs may be NULL (absent scales means 1). Accumulation is fp32.
+ * ------------------------------------------------------------------------------------- */
+int tai_moe_finalize_routing(const void* expanded, int dtype, int64_t t, int64_t h, int k,
+                             const void* skip1, const void* skip2, const void* bias,
+                             const void* scales, int scales_dtype, const int32_t* src_to_dst,
+                             const int32_t* expert_for_source_row, int drop_pad_mode, void* y,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_fused_infer_attention_score, paged decode (one query token per sequence, GQA).
+ * Replaces ge.FusedInferAttentionScore emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/fused_infer_attention_score.py:4-109
+ *   and python/torchair/ops/_npu_fused_infer_attention_score.py:14-34 (prototype
+ *   experiment_ops.h:3878-3965; output shape rules :160-374 of the latter file).
+ * q: [b, hq, d] bf16 (BSH with S=1 and BNSD with S=1 share this memory order).
+ * k_cache / v_cache: bf16, element (block, slot, kv_head, dim) at
+ *   block*stride_block + slot*stride_slot + kv_head*stride_head + dim (elements).
+ * block_table: [b, max_blocks] int32; seq_lens_kv: [b] int64 (device).
+ * out: [b, hq, d] bf16; lse: NULL or [b, hq] fp32 (natural-log logsumexp of scaled scores).
+ * ------------------------------------------------------------------------------------- */
+size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, int64_t max_blocks,
+                                           int block_size);
+int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                         int64_t stride_block, int64_t stride_slot, int64_t stride_head,
+                         const int32_t* block_table, int64_t max_blocks,
+                         const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
+                         int block_size, float scale, void* out, float* lse, void* workspace,
+                         size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_fused_infer_attention_score, dense prefill (GQA, optional causal mask).
+ * q / k / v / out: bf16 with element (batch, pos, head, dim) at
+ *   batch*sb + pos*ss + head*sh + dim (per-tensor strides, elements).
+ * seq_lens_q / seq_lens_kv: NULL (full length) or [b] int64 on the device.
+ * causal: 0 none, 1 = query i sees kv j <= i + (len_kv - len_q) (sparse_mode 2/3).
+ * Query rows at or past seq_lens_q[b] are written as zero.
+ * lse: NULL or [b, hq, s_q] fp32.
+ * ------------------------------------------------------------------------------------- */
+int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q,
+                    int64_t s_kv, int hq, int hkv, int d, const int64_t* q_strides,
+                    const int64_t* k_strides, const int64_t* v_strides,
+                    const int64_t* out_strides, const int64_t* seq_lens_q,
+                    const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache
+ * (query_rope/key_rope given, key_antiquant_mode 1 = per-token scale).
+ * q_nope: [b, hq, dn] bf16, q_rope: [b, hq, dr] bf16.
+ * ckv_cache: [num_blocks, block_size, dn] int8, ckv_scale: [num_blocks, block_size] fp32,
+ * krope_cache: [num_blocks, block_size, dr] bf16. Latent c = int8 * scale is both key
+ * (with k_rope appended) and value. out: [b, hq, dn] bf16; lse: NULL or [b, hq] fp32.
+ * ------------------------------------------------------------------------------------- */
+size_t tai_fia_mla_decode_workspace_size(int64_t b, int hq, int dn, int64_t max_blocks,
+                                         int block_size);
+int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const int8_t* ckv_cache,
+                       const float* ckv_scale, const void* krope_cache,
+                       const int32_t* block_table, int64_t max_blocks,
+                       const int64_t* seq_lens_kv, int64_t b, int hq, int dn, int dr,
+                       int block_size, float scale, void* out, float* lse, void* workspace,
+                       size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TAI_KERNELS_H_ */

@@ -1,0 +1,122 @@
+"""CPU ("debug path") kernels of the npu fused ops, backed by the oracle - TEST INFRASTRUCTURE ONLY.
+
+``register()`` installs the oracle as the CPU implementation of the torch.library ops, so that
+``torch.compile(backend=get_npu_backend())`` can run a model on CPU tensors. Used by tests and
+by bench.py's cpu_baseline leg; the product never imports it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import golden as G
+
+_DONE = False
+_NAMES = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+
+
+def _np(t):
+    if t is None:
+        return None
+    if t.dtype in (torch.bfloat16, torch.float16):
+        t = t.float()
+    return t.detach().cpu().numpy()
+
+
+def _t(a, dtype=None):
+    out = torch.from_numpy(np.ascontiguousarray(a))
+    return out.to(dtype) if dtype is not None else out
+
+
+def _code(v):
+    from torchair_amd._ops_impl import scalar_type_code
+    return scalar_type_code(v)
+
+
+def register() -> None:
+    global _DONE
+    if _DONE:
+        return
+    import torchair_amd  # noqa: F401  (defines the ops)
+    from torchair_amd._ops_impl import LIBS, dtype_of_code
+
+    def dq(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken", dst_type_max=0.0):
+        y, s = G.dynamic_quant(_np(input), _np(smooth_scales), _np(group_index))
+        return _t(y), _t(s)
+
+    def dsq(x, *, weight_scale=None, activation_scale=None, bias=None, quant_scale=None, quant_offset=None,
+            group_index=None, activate_left=False, quant_mode=0, dst_type=None, round_mode=None, activate_dim=None,
+            swiglu_mode=0, clamp_limit=7.0, glu_alpha=1.702, glu_bias=1.0):
+        b = None if bias is None else (bias.numpy() if bias.dtype == torch.int32 else _np(bias))
+        y, s = G.dequant_swiglu_quant(x.numpy(), _np(weight_scale), _np(activation_scale), b, _np(quant_scale),
+                                      _np(group_index), activate_left)
+        return _t(y), _t(s)
+
+    def qmm(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None, x1_dtype=None,
+            x2_dtype=None, pertoken_scale_dtype=None, scale_dtype=None, group_sizes=None):
+        od = dtype_of_code(_code(output_dtype))
+        name = "int32" if od == torch.int32 else _NAMES[od]
+        b = None if bias is None else (bias.numpy() if bias.dtype == torch.int32 else _np(bias))
+        k = x1.shape[-1]
+        out = G.quant_matmul(x1.reshape(-1, k).numpy(), x2.numpy(), _np(scale).reshape(-1) if scale is not None
+                             else None, _np(pertoken_scale), b, name)
+        return _t(out, od).reshape(list(x1.shape[:-1]) + [x2.shape[-1]])
+
+    def gmm(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
+            per_token_scale=None, group_list=None, activation_input=None, activation_quant_scale=None,
+            activation_quant_offset=None, split_item=0, group_type=None, group_list_type=0, act_type=0,
+            tuning_config=None, output_dtype=None):
+        od = dtype_of_code(_code(output_dtype))
+        name = "int32" if od == torch.int32 else _NAMES[od]
+        w = weight[0] if len(weight) == 1 else torch.stack(list(weight))
+        gl = group_list.numpy() if isinstance(group_list, torch.Tensor) else np.asarray(group_list)
+        b = None
+        if bias:
+            b = bias[0].numpy() if bias[0].dtype == torch.int32 else _np(bias[0])
+        out = G.grouped_matmul(x[0].numpy(), w.numpy(), gl, group_list_type, _np(scale[0]) if scale else None,
+                               _np(per_token_scale[0]) if per_token_scale else None, b, name)
+        return [_t(out, od)]
+
+    def gate(x, k, *, bias=None, k_group=1, group_count=1, group_select_mode=0, renorm=0, norm_type=0,
+             out_flag=False, routed_scaling_factor=1.0, eps=1e-20):
+        y, idx, out = G.moe_gating_top_k(_np(x), k, _np(bias), k_group, group_count, group_select_mode, renorm,
+                                         norm_type, out_flag, routed_scaling_factor, eps, _NAMES[x.dtype])
+        return _t(y, x.dtype), _t(idx), _t(out)
+
+    def init_v2(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1, expert_num=-1,
+                drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False, quant_mode=-1,
+                active_expert_range=(), row_idx_type=0):
+        t, k = expert_idx.shape
+        n = t * k
+        rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
+        lo, hi = (active_expert_range[0], active_expert_range[1]) if active_expert_range else (0, expert_num)
+        ex, ri, tok, es = G.moe_init_routing_v2(_np(x), expert_idx.numpy(), _np(scale), rows, lo, hi,
+                                                expert_tokens_num_type, row_idx_type)
+        es_t = _t(es) if es is not None else torch.empty(0, dtype=torch.float32)
+        return _t(ex, x.dtype), _t(ri), _t(tok), es_t
+
+    def init_legacy(x, row_idx, expert_idx, active_num):
+        ex, ri, ei = G.moe_init_routing(_np(x), row_idx.numpy(), expert_idx.numpy(), active_num)
+        return _t(ex, x.dtype), _t(ri), _t(ei)
+
+    def finalize(expanded_permuted_rows, skip1, skip2, bias, scales, expanded_src_to_dst_row,
+                 export_for_source_row, drop_pad_mode=0):
+        ex = expanded_permuted_rows
+        y = G.moe_finalize_routing(_np(ex), _np(skip1), _np(skip2), _np(bias), _np(scales),
+                                   expanded_src_to_dst_row.numpy(),
+                                   None if export_for_source_row is None else export_for_source_row.numpy(),
+                                   0 if drop_pad_mode is None else drop_pad_mode, _NAMES[ex.dtype])
+        return _t(y, ex.dtype)
+
+    for ns in ("npu",):
+        lib = LIBS[ns]
+        lib.impl("npu_dynamic_quant", dq, "CPU")
+        lib.impl("npu_quant_matmul", qmm, "CPU")
+        lib.impl("npu_grouped_matmul", gmm, "CPU")
+        lib.impl("npu_moe_init_routing_v2", init_v2, "CPU")
+        lib.impl("npu_moe_init_routing", init_legacy, "CPU")
+        lib.impl("npu_moe_finalize_routing", finalize, "CPU")
+    for ns in ("npu", "npu_inference"):
+        LIBS[ns].impl("npu_dequant_swiglu_quant", dsq, "CPU")
+        LIBS[ns].impl("npu_moe_gating_top_k", gate, "CPU")
+    _DONE = True

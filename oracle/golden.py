@@ -1,0 +1,472 @@
+"""CPU oracle for the fused inference ops - TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
+and only as the checker (or as the timed CPU baseline). The product path never calls it.
+
+The reference ships no arithmetic for these ops: its converters emit opaque GE nodes whose
+kernels live in closed CANN packages (python/torchair/_ge_concrete_graph/ge_converter/custom/*.py),
+so this module restates each op from its prototype, converter arguments and meta rules
+(file:line cited per function). Where those leave a choice open the choice is written here
+and frozen by tests/golden fixtures:
+  * quantisation: scale = amax/127 (fp32 divide), y = clamp(rint(xs/scale), -128, 127),
+    rint = round half to even; an all-zero row gives scale 0 and y 0;
+  * dequant_swiglu_quant: d = (float(x [+ int32 bias]) * weight_scale) * activation_scale
+    [+ fp32 bias]; activate_left=True -> silu(A)*B else A*silu(B); silu(a) = a/(1+exp(-a));
+    group_index holds per-group row COUNTS; rows past the total -> y 0, scale 0;
+  * dynamic_quant group_index holds cumulative row ENDS;
+  * gating: sigmoid / softmax evaluated in float64 and rounded once to fp32; group score =
+    max (mode 0) or top1+top2 (mode 1); ties go to the lower group / expert index; rows are
+    ordered by descending score; sigmoid weights are divided by (sequential fp32 sum + eps);
+  * routing: slot p = token*k + j, stable sort by expert; finalize drop_pad_mode 0 indexes
+    slots k-major (p = j*T + t, legacy routing), 2 token-major (p = t*k + j);
+  * attention: padded query rows and empty sequences give zero output and lse = -inf.
+All float arithmetic is numpy float32 unless stated (numpy never fuses multiply-add).
+Integer GEMMs are exact (float64 products and sums stay below 2**53 for int8 inputs).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import numpy as np
+
+F32 = np.float32
+
+
+# ----------------------------------------------------------------------------- bf16 helpers
+def bf16_bits_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Rounds fp32 values to the output dtype ('bf16', 'fp16', 'fp32'), returned as fp32."""
+    if dtype == "bf16":
+        return round_bf16(x)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float32)
+    return x.astype(np.float32)
+
+
+# ----------------------------------------------------------------------------- quantisation
+def _quant_rows(v: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    amax = np.max(np.abs(v), axis=1) if v.shape[1] else np.zeros(v.shape[0], F32)
+    scale = (amax.astype(F32) / F32(127.0)).astype(F32)
+    safe = np.where(scale == 0, F32(1.0), scale).astype(F32)
+    q = np.rint(v / safe[:, None])
+    q = np.where(scale[:, None] == 0, 0, q)
+    q = np.clip(q, -128, 127).astype(np.int8)
+    return q, scale
+
+
+def dynamic_quant(x: np.ndarray, smooth_scales: Optional[np.ndarray] = None,
+                  group_index: Optional[np.ndarray] = None) -> Tuple[np.ndarray, np.ndarray]:
+    """npu_dynamic_quant, symmetric per-token int8.
+
+    Follows python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dynamic_quant.py:8-42
+    (pertoken branch -> ge.DynamicQuant) and its prototype
+    third_party/ascend/include/ops/op_proto/inc/nn_quantize.h:47-56 (y int8, scale fp32 of
+    shape x.shape[:-1]).
+    """
+    x = np.asarray(x, F32)
+    h = x.shape[-1]
+    xr = x.reshape(-1, h)
+    if smooth_scales is not None:
+        sm = np.asarray(smooth_scales, F32)
+        if group_index is None:
+            xr = (xr * sm.reshape(1, h)).astype(F32)
+        else:
+            ends = np.asarray(group_index, np.int64)
+            g = np.searchsorted(ends, np.arange(xr.shape[0]), side="right")
+            g = np.minimum(g, len(ends) - 1)
+            xr = (xr * sm.reshape(-1, h)[g]).astype(F32)
+    q, s = _quant_rows(xr)
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+def silu(a: np.ndarray) -> np.ndarray:
+    a = np.asarray(a, F32)
+    return (a / (F32(1.0) + np.exp(-a))).astype(F32)
+
+
+def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None, bias=None, quant_scale=None,
+                         group_index=None, activate_left: bool = False) -> Tuple[np.ndarray, np.ndarray]:
+    """npu_dequant_swiglu_quant, quant_mode=1 (dynamic), swiglu_mode 0, round_mode 0 (rint).
+
+    Follows .../custom/npu_dequant_swiglu_quant.py:5-47 (round_mode 0 -> "rint", quant_mode 1 ->
+    "dynamic"), prototype experiment_ops.h:3765-3812 (activate_left semantics) and the meta rule
+    python/torchair/_contrib/custom_torch_ops/auto_register_custom_torch_ops.py:155-191 (last dim
+    halved, int8 y, fp32 scale of y.shape[:-1]).
+    """
+    x = np.asarray(x, np.int32)
+    n2 = x.shape[-1]
+    n = n2 // 2
+    xr = x.reshape(-1, n2)
+    rows = xr.shape[0]
+    if group_index is not None:
+        counts = np.asarray(group_index, np.int64).reshape(-1)
+        ends = np.cumsum(counts)
+        grp = np.searchsorted(ends, np.arange(rows), side="right")
+        live = grp < len(counts)
+        grp = np.minimum(grp, len(counts) - 1)
+    else:
+        grp = np.zeros(rows, np.int64)
+        live = np.ones(rows, bool)
+    ng = 1 if group_index is None else len(np.asarray(group_index).reshape(-1))
+    xi = xr.copy()
+    bias_f = None
+    if bias is not None:
+        b = np.asarray(bias)
+        if b.dtype == np.int32:
+            xi = (xi + b.reshape(ng, n2)[grp]).astype(np.int32)
+        else:
+            bias_f = np.asarray(b, F32).reshape(ng, n2)[grp]
+    d = xi.astype(F32)
+    if weight_scale is not None:
+        d = (d * np.asarray(weight_scale, F32).reshape(ng, n2)[grp]).astype(F32)
+    if activation_scale is not None:
+        d = (d * np.asarray(activation_scale, F32).reshape(rows, 1)).astype(F32)
+    if bias_f is not None:
+        d = (d + bias_f).astype(F32)
+    a, b2 = d[:, :n], d[:, n:]
+    r = (silu(a) * b2).astype(F32) if activate_left else (a * silu(b2)).astype(F32)
+    if quant_scale is not None:
+        r = (r * np.asarray(quant_scale, F32).reshape(ng, n)[grp]).astype(F32)
+    q, s = _quant_rows(r)
+    q[~live] = 0
+    s[~live] = 0
+    return q.reshape(x.shape[:-1] + (n,)), s.reshape(x.shape[:-1])
+
+
+# ----------------------------------------------------------------------------- int8 GEMMs
+def int_matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Exact int8 x int8 -> int64 product (float64 BLAS; |partial sums| < 2**53)."""
+    return np.rint(np.asarray(a, np.float64) @ np.asarray(b, np.float64)).astype(np.int64)
+
+
+def _epilogue(acc: np.ndarray, scale, pts, bias, out_dtype: str, col_scale_rows=None) -> np.ndarray:
+    acc32 = acc.astype(np.int64)
+    bias_f = None
+    if bias is not None:
+        bb = np.asarray(bias)
+        if bb.dtype == np.int32:
+            acc32 = acc32 + bb.astype(np.int64)
+        else:
+            bias_f = np.asarray(bb, F32)
+    acc32 = ((acc32 + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)  # int32 wrap-around
+    if out_dtype == "int32":
+        return acc32
+    v = acc32.astype(F32)
+    if scale is not None:
+        v = (v * np.asarray(scale, F32)).astype(F32)
+    if pts is not None:
+        v = (v * np.asarray(pts, F32).reshape(-1, 1)).astype(F32)
+    if bias_f is not None:
+        v = (v + bias_f).astype(F32)
+    return round_to(v, out_dtype)
+
+
+def quant_matmul(x1, x2, scale=None, pertoken_scale=None, bias=None, out_dtype: str = "bf16") -> np.ndarray:
+    """npu_quant_matmul W8A8: exact int32 accumulation, then (acc [+int32 bias]) * scale[n] * pertoken[m]
+    [+ fp32 bias], rounded to out_dtype.
+
+    Follows .../custom/quantmatmul.py:63-255 (x2 is [K, N]: trans_x2 = x1[-1] == x2[-2] at :129;
+    ge.QuantBatchMatmulV3(x1, x2, scale, offset, bias, pertoken_scale, dtype) at :244-254) and
+    the dtype table of fusion_ops.h:380-451.
+    """
+    acc = int_matmul(x1, x2)
+    sc = None if scale is None else np.asarray(scale, F32).reshape(1, -1)
+    return _epilogue(acc, sc, pertoken_scale, bias, out_dtype)
+
+
+def group_offsets(group_list, list_type: int, m: int) -> Tuple[np.ndarray, np.ndarray]:
+    gl = np.asarray(group_list, np.int64).reshape(-1)
+    if list_type == 1:
+        ends = np.cumsum(np.maximum(gl, 0))
+    else:
+        ends = np.maximum.accumulate(gl)
+    begins = np.concatenate([[0], ends[:-1]])
+    return np.minimum(begins, m), np.minimum(ends, m)
+
+
+def grouped_matmul(x, w, group_list, group_list_type: int = 0, scale=None, per_token_scale=None, bias=None,
+                   out_dtype: str = "int32") -> np.ndarray:
+    """npu_grouped_matmul int8 path, split_item 2/3, group_type 0: rows [off_e, off_e+1) use w[e].
+
+    Follows .../custom/grouped_matmul.py:210-365 (int8 bias filled as int32 :252-258; output_dtype
+    -> y_dtype table convert_ydtype_in_a8 :178-195) and prototype experiment_ops.h:3636-3662.
+    group_list_type 0 = cumulative ends, 1 = counts. Rows past the last group are zero.
+    """
+    x = np.asarray(x)
+    w = np.asarray(w)
+    m = x.shape[0]
+    e_cnt, _, n = w.shape
+    out = np.zeros((m, n), np.int32 if out_dtype == "int32" else F32)
+    b, en = group_offsets(group_list, group_list_type, m)
+    for e in range(e_cnt):
+        if en[e] <= b[e]:
+            continue
+        acc = int_matmul(x[b[e]:en[e]], w[e])
+        sc = None if scale is None else np.asarray(scale, F32).reshape(e_cnt, n)[e].reshape(1, n)
+        pts = None if per_token_scale is None else np.asarray(per_token_scale, F32)[b[e]:en[e]]
+        bi = None if bias is None else np.asarray(bias).reshape(e_cnt, n)[e].reshape(1, n)
+        out[b[e]:en[e]] = _epilogue(acc, sc, pts, bi, out_dtype)
+    return out
+
+
+# ----------------------------------------------------------------------------- MoE gating / routing
+def moe_gating_top_k(x, k: int, bias=None, k_group: int = 1, group_count: int = 1, group_select_mode: int = 0,
+                     renorm: int = 0, norm_type: int = 0, out_flag: bool = False,
+                     routed_scaling_factor: float = 1.0, eps: float = 1e-20, out_dtype: str = "fp32"):
+    """npu_moe_gating_top_k (DeepSeek-V3 grouped "noaux_tc" selection).
+
+    Follows .../custom/npu_moe_gating_top_k.py:4-22 (attributes passed to ge.MoeGatingTopK),
+    prototype experiment_ops.h:3723-3764, meta auto_register_custom_torch_ops.py:103-114
+    (y [T,k] of x dtype, expert_idx int32 [T,k], out fp32 [T,E]).
+    Returns (y, expert_idx, out).
+    """
+    if renorm != 0:
+        raise NotImplementedError("renorm must be 0")
+    x = np.asarray(x, F32)
+    t, e = x.shape
+    x64 = x.astype(np.float64)
+    if norm_type == 1:
+        s = (1.0 / (1.0 + np.exp(-x64))).astype(F32)
+    else:
+        m = np.max(x, axis=1, keepdims=True).astype(np.float64)
+        ex = np.exp(x64 - m)
+        s = (ex / np.sum(ex, axis=1, keepdims=True)).astype(F32)
+    sb = s if bias is None else (s + np.asarray(bias, F32).reshape(1, e)).astype(F32)
+    sb = sb.copy()
+    if group_count > 1:
+        gsz = e // group_count
+        g = sb.reshape(t, group_count, gsz)
+        if group_select_mode == 1 and gsz > 1:
+            srt = -np.sort(-g, axis=2)
+            gs = (srt[:, :, 0] + srt[:, :, 1]).astype(F32)
+        else:
+            gs = np.max(g, axis=2)
+        order = np.argsort(-gs, axis=1, kind="stable")
+        keep = np.zeros((t, group_count), bool)
+        np.put_along_axis(keep, order[:, :k_group], True, axis=1)
+        sb[~np.repeat(keep, gsz, axis=1)] = -np.inf
+    idx = np.argsort(-sb, axis=1, kind="stable")[:, :k].astype(np.int32)
+    w = np.take_along_axis(s, idx.astype(np.int64), axis=1).astype(F32)
+    if norm_type == 1:
+        tot = np.zeros(t, F32)
+        for j in range(k):
+            tot = (tot + w[:, j]).astype(F32)
+        w = (w / (tot + F32(eps))[:, None]).astype(F32)
+    w = (w * F32(routed_scaling_factor)).astype(F32)
+    return round_to(w, out_dtype), idx, s
+
+
+def moe_init_routing_v2(x, expert_idx, scale=None, active_rows: Optional[int] = None, expert_start: int = 0,
+                        expert_end: Optional[int] = None, expert_tokens_num_type: int = 0, row_idx_type: int = 0):
+    """npu_moe_init_routing_v2, dropless (drop_pad_mode 0), quant_mode -1.
+
+    Follows .../custom/npu_moe_init_routing_v2.py:41-91 (-> ge.MoeInitRoutingV3) and prototype
+    experiment_ops.h:2138-2190 (row_idx_type 0 gather / 1 scatter, expert_tokens_num_type 0
+    cumsum / 1 count, active_expert_range). Returns
+    (expanded_x, expanded_row_idx, expert_tokens, expanded_scale_or_None).
+    """
+    x = np.asarray(x)
+    ei = np.asarray(expert_idx, np.int64)
+    t, k = ei.shape
+    n = t * k
+    if expert_end is None:
+        expert_end = int(ei.max()) + 1 if n else 1
+    rows = n if active_rows is None else active_rows
+    flat = ei.reshape(-1)
+    valid = (flat >= expert_start) & (flat < expert_end)
+    slots = np.nonzero(valid)[0]
+    order = slots[np.argsort(flat[slots], kind="stable")]
+    total = len(order)
+    ex = np.zeros((rows,) + x.shape[1:], x.dtype)
+    live = min(rows, total)
+    ex[:live] = x[order[:live] // k]
+    ri = np.full(n, -1, np.int32)
+    if row_idx_type == 0:
+        ri[order] = np.arange(total, dtype=np.int32)
+    else:
+        ri[:total] = order.astype(np.int32)
+    counts = np.bincount(flat[valid] - expert_start, minlength=expert_end - expert_start).astype(np.int64)
+    tokens = np.cumsum(counts) if expert_tokens_num_type == 0 else counts
+    es = None
+    if scale is not None:
+        es = np.zeros(rows, F32)
+        es[:live] = np.asarray(scale, F32)[order[:live] // k]
+    return ex, ri, tokens, es
+
+
+def moe_init_routing(x, row_idx, expert_idx, active_num: int):
+    """npu_moe_init_routing (legacy). Follows .../custom/moe_init_routing.py:4-21 and prototype
+    experiment_ops.h:2112-2135. Returns (expanded_x, expanded_row_idx, expanded_expert_idx)."""
+    x = np.asarray(x)
+    ri = np.asarray(row_idx, np.int64).reshape(-1)
+    ei = np.asarray(expert_idx, np.int64)
+    t, k = ei.shape
+    flat = ei.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    n = t * k
+    rows = min(t, active_num) * k if active_num >= 0 else n
+    ex = x[ri[order[:rows]] % t]
+    eri = np.zeros(n, np.int32)
+    eri[ri[order]] = np.arange(n, dtype=np.int32)
+    eei = flat[order].astype(np.int32)
+    return ex, eri, eei
+
+
+def moe_finalize_routing(expanded, skip1, skip2, bias, scales, src_to_dst, expert_for_source_row,
+                         drop_pad_mode: int = 0, out_dtype: str = "bf16") -> np.ndarray:
+    """npu_moe_finalize_routing: y[t] = skip1 + skip2 + sum_j scales[t,j]*(expanded[src_to_dst[p]] + bias[expert]).
+
+    Follows .../custom/npu_moe_finalize_routing.py:4-41 (declared cases: arange row index, optional
+    skip2/bias/scales) and prototype experiment_ops.h:2196-2219. fp32 accumulation in the order
+    skip1, skip2, j = 0..k-1.
+    """
+    ex = np.asarray(expanded, F32)
+    s2d = np.asarray(src_to_dst, np.int64).reshape(-1)
+    if scales is not None:
+        t, k = np.asarray(scales).shape
+    else:
+        t = np.asarray(skip1).shape[0]
+        k = len(s2d) // t
+    h = ex.shape[-1]
+    acc = np.zeros((t, h), F32)
+    if skip1 is not None:
+        acc = np.asarray(skip1, F32).copy()
+    if skip2 is not None:
+        acc = (acc + np.asarray(skip2, F32)).astype(F32)
+    tt = np.arange(t)
+    for j in range(k):
+        p = j * t + tt if drop_pad_mode == 0 else tt * k + j
+        d = s2d[p]
+        ok = d >= 0
+        v = np.zeros((t, h), F32)
+        v[ok] = ex[d[ok]]
+        if bias is not None:
+            e = np.asarray(expert_for_source_row, np.int64).reshape(t, k)[:, j]
+            v = (v + np.asarray(bias, F32)[e]).astype(F32)
+        w = np.ones(t, F32) if scales is None else np.asarray(scales, F32)[:, j]
+        contrib = (w[:, None] * v).astype(F32)
+        acc = np.where(ok[:, None], (acc + contrib).astype(F32), acc)
+    return round_to(acc, out_dtype)
+
+
+# ----------------------------------------------------------------------------- attention
+def _softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, mask: Optional[np.ndarray] = None):
+    """q [n, d], k [L, d], v [L, dv] -> (out [n, dv], lse [n]); fp32, masked entries excluded."""
+    s = (q.astype(F32) @ k.astype(F32).T) * F32(scale)
+    if mask is not None:
+        s = np.where(mask, s, -np.inf)
+    m = np.max(s, axis=1, keepdims=True) if s.shape[1] else np.full((s.shape[0], 1), -np.inf, F32)
+    m_safe = np.where(np.isfinite(m), m, 0).astype(F32)
+    p = np.exp(s - m_safe)
+    den = np.sum(p, axis=1, keepdims=True)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        o = np.where(den > 0, (p @ v.astype(F32)) / np.where(den > 0, den, 1), 0).astype(F32)
+        lse = np.where(den[:, 0] > 0, m_safe[:, 0] + np.log(np.where(den[:, 0] > 0, den[:, 0], 1)), -np.inf)
+    return o, lse.astype(F32)
+
+
+def paged_decode_attention(q, k_cache, v_cache, block_table, seq_lens, scale: float):
+    """npu_fused_infer_attention_score, paged decode (one query token, GQA).
+
+    Follows .../custom/fused_infer_attention_score.py:4-109 (block_table / block_size /
+    actual_seq_lengths_kv / num_key_value_heads arguments), prototype experiment_ops.h:3878-3965
+    and the output rules of python/torchair/ops/_npu_fused_infer_attention_score.py:160-374.
+    q [B, Hq, D]; caches [blocks, bs, Hkv, D]; token t of sequence b lives at
+    cache[block_table[b, t // bs], t % bs]. Returns (out [B,Hq,D] fp32, lse [B,Hq]).
+    """
+    q = np.asarray(q, F32)
+    b_cnt, hq, d = q.shape
+    _, bs, hkv, _ = k_cache.shape
+    g = hq // hkv
+    out = np.zeros((b_cnt, hq, d), F32)
+    lse = np.full((b_cnt, hq), -np.inf, F32)
+    for b in range(b_cnt):
+        L = int(seq_lens[b])
+        if L <= 0:
+            continue
+        pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
+        kk = np.asarray(k_cache[pages], F32).reshape(-1, hkv, d)[:L]
+        vv = np.asarray(v_cache[pages], F32).reshape(-1, hkv, d)[:L]
+        for h in range(hkv):
+            o, l = _softmax_attend(q[b, h * g:(h + 1) * g], kk[:, h], vv[:, h], scale)
+            out[b, h * g:(h + 1) * g] = o
+            lse[b, h * g:(h + 1) * g] = l
+    return out, lse
+
+
+def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float):
+    """npu_fused_infer_attention_score, dense prefill. q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D].
+
+    causal 1 (sparse_mode 3, right-down): query i sees kv j <= i + (Lkv - Lq); causal 2
+    (sparse_mode 2, left-up): j <= i; 0: no mask. Rows at or past Lq are zero.
+    Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
+    """
+    q = np.asarray(q, F32)
+    b_cnt, sq, hq, d = q.shape
+    skv, hkv = k.shape[1], k.shape[2]
+    g = hq // hkv
+    out = np.zeros_like(q)
+    lse = np.full((b_cnt, hq, sq), -np.inf, F32)
+    for b in range(b_cnt):
+        lq = sq if seq_q is None else int(seq_q[b])
+        lk = skv if seq_kv is None else int(seq_kv[b])
+        ii = np.arange(lq)[:, None]
+        jj = np.arange(lk)[None, :]
+        mask = None
+        if causal == 1:
+            mask = jj <= ii + (lk - lq)
+        elif causal == 2:
+            mask = jj <= ii
+        for h in range(hq):
+            o, l = _softmax_attend(q[b, :lq, h], np.asarray(k[b, :lk, h // g], F32),
+                                   np.asarray(v[b, :lk, h // g], F32), scale, mask)
+            out[b, :lq, h] = o
+            lse[b, h, :lq] = l
+    return out, lse
+
+
+def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_lens, scale: float):
+    """npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache.
+
+    Follows the query_rope / key_rope / key_antiquant_scale / key_antiquant_mode arguments of
+    .../custom/fused_infer_attention_score.py:4-109 and get_value_d in
+    python/torchair/ops/_npu_fused_infer_attention_score.py:242-264 (output head dim = latent dim).
+    Latent c[t] = int8[t] * scale[t] serves as key (with k_rope appended) and value.
+    q_nope [B,H,Dn], q_rope [B,H,Dr], ckv [blocks,bs,Dn] int8, ckv_scale [blocks,bs], krope [blocks,bs,Dr].
+    """
+    qn = np.asarray(q_nope, F32)
+    qr = np.asarray(q_rope, F32)
+    b_cnt, h, dn = qn.shape
+    bs = ckv.shape[1]
+    out = np.zeros((b_cnt, h, dn), F32)
+    lse = np.full((b_cnt, h), -np.inf, F32)
+    for b in range(b_cnt):
+        L = int(seq_lens[b])
+        if L <= 0:
+            continue
+        pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
+        c = (np.asarray(ckv[pages], F32).reshape(-1, dn)[:L] *
+             np.asarray(ckv_scale[pages], F32).reshape(-1)[:L, None]).astype(F32)
+        kr = np.asarray(krope[pages], F32).reshape(-1, krope.shape[-1])[:L]
+        qk = np.concatenate([qn[b], qr[b]], axis=1)
+        kk = np.concatenate([c, kr], axis=1)
+        o, l = _softmax_attend(qk, kk, c, scale)
+        out[b] = o
+        lse[b] = l
+    return out, lse

@@ -1,0 +1,166 @@
+"""CPU checks of the drop-in boundary: the C ABI library, op schemas and meta rules, the
+converter extension surface and the Dynamo backend on the CPU debug path."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd
+from torchair_amd import CompilerConfig, _lib, get_npu_backend, register_fx_node_ge_converter
+from torchair_amd.converter import _get_converter
+from torchair_amd.npu_fx_compiler import lower_graph
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _header_symbols():
+    text = (ROOT / "include" / "tai_kernels.h").read_text()
+    return sorted(set(re.findall(r"\b(tai_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    syms = _header_symbols()
+    assert len(syms) >= 17
+    for s in syms:
+        assert hasattr(lib, s), f"{s} missing from libtai_kernels.so"
+    assert set(syms) == set(_lib.exported_symbols())
+    assert lib.tai_abi_version() == 1
+
+
+def test_library_rejects_bad_arguments_without_gpu():
+    with pytest.raises(RuntimeError, match="dtype"):
+        _lib.call("tai_dynamic_quant", 1, 99, 4, 4, None, None, -1, 0, 1, 1, None)
+    with pytest.raises(RuntimeError, match="last dim must be even"):
+        _lib.call("tai_dequant_swiglu_quant", 1, 4, 7, None, None, None, -1, None, None, -1, 0, 0, 1, 1, None)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("tai_grouped_matmul", 1, 1, 4, 16, 16, 2, 0, 1, 0, None, None, None, -1, 3, 1, None, 0, None)
+    with pytest.raises(RuntimeError, match="drop-pad"):
+        _lib.call("tai_moe_finalize_routing", 1, 15, 4, 8, 2, None, None, None, None, -1, 1, None, 1, 1, None)
+    assert _lib.query("tai_grouped_matmul_workspace_size", 32768, 4096, 256) > 0
+
+
+def test_ops_refuse_cpu_tensors_without_the_debug_path():
+    x = torch.randn(4, 16)
+    if torch.ops.npu.npu_dynamic_quant.default.has_kernel_for_dispatch_key("CPU"):
+        pytest.skip("oracle CPU kernels registered in this process")
+    with pytest.raises(NotImplementedError):
+        torch.ops.npu.npu_dynamic_quant(x)
+
+
+def test_meta_shapes_follow_reference_rules():
+    m = torch.device("meta")
+    y, s = torch.ops.npu.npu_dynamic_quant(torch.empty(3, 5, 64, device=m, dtype=torch.bfloat16))
+    assert y.shape == (3, 5, 64) and y.dtype == torch.int8 and s.shape == (3, 5)
+    y, s = torch.ops.npu.npu_dequant_swiglu_quant(torch.empty(128, 11264, device=m, dtype=torch.int32), quant_mode=1)
+    assert y.shape == (128, 5632) and s.shape == (128,)
+    with pytest.raises(RuntimeError, match="even"):
+        torch.ops.npu.npu_dequant_swiglu_quant(torch.empty(4, 7, device=m, dtype=torch.int32))
+    out = torch.ops.npu.npu_quant_matmul(torch.empty(128, 2048, device=m, dtype=torch.int8),
+                                         torch.empty(2048, 11264, device=m, dtype=torch.int8),
+                                         torch.empty(1, device=m), output_dtype=torch.int32)
+    assert out.shape == (128, 11264) and out.dtype == torch.int32
+    y, idx, o = torch.ops.npu.npu_moe_gating_top_k(torch.empty(4096, 256, device=m), 8)
+    assert y.shape == (4096, 8) and idx.dtype == torch.int32 and o.shape == (4096, 256)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(torch.empty(4096, 7168, device=m, dtype=torch.bfloat16),
+                                                            torch.empty(4096, 8, device=m, dtype=torch.int32),
+                                                            expert_num=256)
+    assert ex.shape == (32768, 7168) and ri.shape == (32768,) and tok.shape == (256,)
+    q = torch.empty(64, 1, 32 * 128, device=m, dtype=torch.bfloat16)
+    kc = torch.empty(100, 128, 8 * 128, device=m, dtype=torch.bfloat16)
+    out, lse = torch.ops.air.npu_fused_infer_attention_score(
+        q, kc, kc, block_table=torch.empty(64, 32, device=m, dtype=torch.int32), num_heads=32,
+        num_key_value_heads=8, input_layout="BSH", block_size=128, softmax_lse_flag=True)
+    assert out.shape == (64, 1, 4096) and lse.shape == (64, 32, 1, 1)
+    qn = torch.empty(128, 1, 128, 512, device=m, dtype=torch.bfloat16)
+    lat = torch.empty(10, 128, 1, 512, device=m, dtype=torch.int8)
+    out, lse = torch.ops.npu.npu_fused_infer_attention_score(
+        qn, lat, lat, block_table=torch.empty(128, 64, device=m, dtype=torch.int32), num_heads=128,
+        num_key_value_heads=1, input_layout="BSND", query_rope=torch.empty(128, 1, 128, 64, device=m,
+                                                                            dtype=torch.bfloat16))
+    assert out.shape == (128, 1, 128, 512) and out.dtype == torch.bfloat16 and lse.shape == (0,)
+
+
+def test_converter_registration_surface():
+    conv = _get_converter(torch.ops.npu.npu_dynamic_quant.default)
+    assert conv is not None and conv.require_meta is True
+
+    lib = torch.library.Library("tai_test", "FRAGMENT")
+    lib.define("twice(Tensor x) -> Tensor")
+    lib.impl("twice", lambda x: x * 2, "CompositeExplicitAutograd")
+
+    @register_fx_node_ge_converter(torch.ops.tai_test.twice.default)
+    def convert_twice(x, meta_outputs=None):
+        assert meta_outputs is not None and meta_outputs.shape == x.node.meta["val"].shape
+        return torch.ops.aten.add.Tensor(x, x)
+
+    assert _get_converter(torch.ops.tai_test.twice.default).require_meta is True
+    assert register_fx_node_ge_converter(None)(lambda: 1) is None
+
+
+def test_backend_lowers_user_converter_and_runs_on_cpu():
+    lib = torch.library.Library("tai_test2", "FRAGMENT")
+    lib.define("scaled(Tensor x, float s) -> Tensor")
+    lib.impl("scaled", lambda x, s: x * 1000.0, "CompositeExplicitAutograd")  # deliberately wrong eager impl
+
+    @register_fx_node_ge_converter(torch.ops.tai_test2.scaled.default)
+    def convert_scaled(x, s, meta_outputs=None):
+        return torch.ops.aten.mul.Tensor(x, s)
+
+    def f(x):
+        return torch.ops.tai_test2.scaled(x, 3.0) + 1
+
+    cfg = CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    fn = torch.compile(f, backend=get_npu_backend(compiler_config=cfg), fullgraph=True)
+    x = torch.randn(5)
+    torch.testing.assert_close(fn(x), x * 3 + 1)  # the converter, not the eager impl, ran
+
+
+def test_cpu_debug_path_mlp_matches_oracle():
+    """cfg1 composition through torch.compile(backend=get_npu_backend()) on CPU (oracle kernels)."""
+    from oracle import cpu_ops, golden as G
+    cpu_ops.register()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(16, 64, generator=g).to(torch.bfloat16)
+    wgu = torch.randint(-127, 128, (64, 96), generator=g, dtype=torch.int8)
+    sgu = torch.rand(96, generator=g) * 9e-3 + 1e-3
+    wd = torch.randint(-127, 128, (48, 64), generator=g, dtype=torch.int8)
+    sd = torch.rand(64, generator=g) * 9e-3 + 1e-3
+
+    def mlp(x):
+        q, s = torch.ops.npu.npu_dynamic_quant(x)
+        h = torch.ops.npu.npu_quant_matmul(q, wgu, torch.ones(1), output_dtype=torch.int32)
+        q2, s2 = torch.ops.npu.npu_dequant_swiglu_quant(h, weight_scale=sgu, activation_scale=s, quant_mode=1,
+                                                        activate_left=True)
+        return torch.ops.npu.npu_quant_matmul(q2, wd, sd, pertoken_scale=s2, output_dtype=torch.bfloat16)
+
+    fn = torch.compile(mlp, backend=get_npu_backend(), fullgraph=True)
+    got = fn(x)
+    q, s = G.dynamic_quant(x.float().numpy())
+    h = G.quant_matmul(q, wgu.numpy(), out_dtype="int32")
+    q2, s2 = G.dequant_swiglu_quant(h, sgu.numpy(), s, activate_left=True)
+    want = G.quant_matmul(q2, wd.numpy(), sd.numpy(), s2, None, "bf16")
+    np.testing.assert_array_equal(got.float().numpy(), want)
+
+
+def test_lowering_keeps_fused_nodes():
+    gm = torch.fx.symbolic_trace(lambda x: torch.ops.npu.npu_dynamic_quant(x)[0])
+    low = lower_graph(gm)
+    targets = [n.target for n in low.graph.nodes if n.op == "call_function"]
+    assert torch.ops.npu.npu_dynamic_quant.default in targets or torch.ops.npu.npu_dynamic_quant in targets
+
+
+def test_compiler_config_validation():
+    cfg = CompilerConfig()
+    assert cfg.mode.value == "max-autotune"
+    cfg.mode = "npugraph_ex"
+    with pytest.raises(ValueError):
+        cfg.mode = "fast"
+    cfg.debug.aclgraph.static_capture_size_limit = 4
+    with pytest.raises(ValueError):
+        cfg.debug.aclgraph.static_capture_size_limit = 0
+    assert CompilerConfig() != cfg and CompilerConfig() == CompilerConfig()
+    assert torchair_amd.get_compiler(cfg).config is cfg

@@ -1,0 +1,125 @@
+"""GPU parity: npu_quant_matmul and npu_grouped_matmul (W8A8, exact int32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_close, f32np, gen, rand_i8, uniform
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _exact_f64(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Exact integer product on the GPU through float64 (|sums| < 2**53): a size-independent checker."""
+    return torch.matmul(a.to(torch.float64), b.to(torch.float64)).round().to(torch.int64)
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 2048, 11264), (128, 5632, 2048), (1, 64, 64), (300, 80, 260),
+                                   (129, 1024, 384), (5, 48, 100), (17, 50, 36)])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_quant_matmul_int32_exact(m, k, n, layout):
+    g = gen(10)
+    x1 = rand_i8((m, k), g)
+    w = rand_i8((k, n), g)
+    x2 = w if layout == "kn" else w.t().contiguous().t()  # [K,N] view of a [N,K] storage
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), x2.to(DEV), torch.ones(1, device=DEV),
+                                         output_dtype=torch.int32)
+    want = G.quant_matmul(x1.numpy(), w.numpy(), out_dtype="int32")
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("out_dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")])
+def test_quant_matmul_dequant_epilogue(out_dtype, name):
+    g = gen(11)
+    m, k, n = 128, 5632, 2048
+    x1, w = rand_i8((m, k), g), rand_i8((k, n), g)
+    scale, pts = uniform((n,), g, 1e-3, 1e-2), uniform((m,), g, 1e-3, 1e-2)
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), scale.to(DEV), pertoken_scale=pts.to(DEV),
+                                         output_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    want = G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), pts.numpy(), None, name)
+    assert_close(f32np(out), want)
+
+
+def test_quant_matmul_bias():
+    g = gen(12)
+    x1, w = rand_i8((64, 256), g), rand_i8((256, 192), g)
+    bi = torch.randint(-5000, 5000, (192,), generator=g, dtype=torch.int32)
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), torch.ones(1, device=DEV), bias=bi.to(DEV),
+                                         output_dtype=torch.int32)
+    np.testing.assert_array_equal(out.cpu().numpy(), G.quant_matmul(x1.numpy(), w.numpy(), bias=bi.numpy(),
+                                                                     out_dtype="int32"))
+    scale = uniform((192,), g, 1e-3, 1e-2)
+    bf = uniform((192,), g, -1, 1)
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), scale.to(DEV), bias=bf.to(DEV),
+                                         output_dtype=torch.bfloat16)
+    assert_close(f32np(out), G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), None, bf.numpy(), "bf16"))
+
+
+def test_quant_matmul_large_exact_vs_f64():
+    """8192^3 demonstrator shape: exact against a float64 GPU product."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(13)
+    a = torch.randint(-127, 128, (8192, 8192), generator=g, device=DEV, dtype=torch.int8)
+    b = torch.randint(-127, 128, (8192, 8192), generator=g, device=DEV, dtype=torch.int8)
+    out = torch.ops.npu.npu_quant_matmul(a, b, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    ref = _exact_f64(a, b)
+    assert torch.equal(out.to(torch.int64), ref)
+
+
+def _gmm_case(g, e, m_rows, k, n, counts=None):
+    if counts is None:
+        counts = torch.randint(0, 2 * m_rows // e + 1, (e,), generator=g, dtype=torch.int64)
+    m = int(counts.sum()) + 5
+    x = rand_i8((m, k), g)
+    w = rand_i8((e, k, n), g)
+    return x, w, counts
+
+
+@pytest.mark.parametrize("list_type", [0, 1])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_grouped_matmul_int32_exact(list_type, layout):
+    g = gen(20)
+    x, w, counts = _gmm_case(g, 8, 600, 512, 256)
+    counts[3] = 0  # an empty group
+    gl = counts if list_type == 1 else torch.cumsum(counts, 0)
+    wd = w.to(DEV) if layout == "kn" else w.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    out = torch.ops.npu.npu_grouped_matmul([x.to(DEV)], [wd], group_list=gl.to(DEV), split_item=3, group_type=0,
+                                           group_list_type=list_type, output_dtype=torch.int32)[0]
+    want = G.grouped_matmul(x.numpy(), w.numpy(), gl.numpy(), list_type, out_dtype="int32")
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+def test_grouped_matmul_bf16_epilogue():
+    g = gen(21)
+    x, w, counts = _gmm_case(g, 16, 900, 256, 384)
+    scale = uniform((16, 384), g, 1e-3, 1e-2)
+    pts = uniform((x.shape[0],), g, 1e-3, 1e-2)
+    out = torch.ops.npu.npu_grouped_matmul([x.to(DEV)], [w.to(DEV)], scale=[scale.to(DEV)],
+                                           per_token_scale=[pts.to(DEV)], group_list=counts.to(DEV), split_item=3,
+                                           group_type=0, group_list_type=1, output_dtype=torch.bfloat16)[0]
+    want = G.grouped_matmul(x.numpy(), w.numpy(), counts.numpy(), 1, scale.numpy(), pts.numpy(), None, "bf16")
+    assert_close(f32np(out), want)
+
+
+def test_grouped_matmul_cfg4_gate_up_exact_vs_f64():
+    """Full cfg4 gate_up shape (256 experts, 7168 -> 4096): exact against float64 per expert."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(22)
+    e, k, n, m = 256, 7168, 4096, 32768
+    counts = torch.bincount(torch.randint(0, e, (m,), generator=g, device=DEV), minlength=e).to(torch.int64)
+    x = torch.randint(-127, 128, (m, k), generator=g, device=DEV, dtype=torch.int8)
+    w = torch.randint(-127, 128, (e, k, n), generator=g, device=DEV, dtype=torch.int8)
+    out = torch.ops.npu.npu_grouped_matmul([x], [w], group_list=counts, split_item=3, group_type=0,
+                                           group_list_type=1, output_dtype=torch.int32)[0]
+    ends = torch.cumsum(counts, 0).tolist()
+    begin = 0
+    for ei in list(range(0, e, 37)) + [e - 1]:
+        b0 = 0 if ei == 0 else ends[ei - 1]
+        b1 = ends[ei]
+        if b1 > b0:
+            ref = _exact_f64(x[b0:b1], w[ei])
+            assert torch.equal(out[b0:b1].to(torch.int64), ref), f"expert {ei}"
+    del begin

@@ -1,0 +1,145 @@
+"""GPU parity: MoE gating top-k, init routing (v2 and legacy) and finalize routing."""
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_close, f32np, gen, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _gate_check(x, k, bias=None, **kw):
+    y, idx, out = torch.ops.npu.npu_moe_gating_top_k(x.to(DEV), k, bias=None if bias is None else bias.to(DEV), **kw)
+    name = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[x.dtype]
+    wy, widx, wout = G.moe_gating_top_k(f32np(x), k, None if bias is None else f32np(bias),
+                                        kw.get("k_group", 1), kw.get("group_count", 1),
+                                        kw.get("group_select_mode", 0), kw.get("renorm", 0), kw.get("norm_type", 0),
+                                        kw.get("out_flag", False), kw.get("routed_scaling_factor", 1.0),
+                                        kw.get("eps", 1e-20), name)
+    np.testing.assert_array_equal(idx.cpu().numpy(), widx)
+    np.testing.assert_allclose(f32np(y), wy, rtol=1e-6, atol=1e-7)
+    if kw.get("out_flag", False):
+        np.testing.assert_allclose(out.cpu().numpy(), wout, rtol=1e-6, atol=1e-7)
+    return idx
+
+
+def test_gating_cfg4_deepseek():
+    g = gen(30)
+    x = torch.randn(4096, 256, generator=g)
+    bias = torch.randn(256, generator=g) * 0.1
+    _gate_check(x, 8, bias, k_group=4, group_count=8, group_select_mode=1, norm_type=1, out_flag=True,
+                routed_scaling_factor=2.5)
+
+
+def test_gating_variants():
+    g = gen(31)
+    x = torch.randn(513, 64, generator=g)
+    _gate_check(x, 6)  # softmax, plain top-k
+    _gate_check(x, 4, k_group=2, group_count=4, group_select_mode=0, norm_type=1)
+    _gate_check(x.to(torch.bfloat16), 8, torch.randn(64, generator=g).to(torch.bfloat16), k_group=3, group_count=8,
+                group_select_mode=1, norm_type=1)
+
+
+def test_gating_ties_pick_lower_index():
+    x = torch.zeros(3, 32)
+    x[1, 5] = x[1, 9] = x[1, 30] = 1.0
+    idx = _gate_check(x, 4, k_group=2, group_count=4, group_select_mode=1, norm_type=1)
+    assert idx.cpu()[0].tolist() == [0, 1, 2, 3]
+
+
+def _routing_inputs(t, h, e, k, g):
+    x = randn((t, h), g)
+    logits = torch.randn(t, e, generator=g)
+    idx = torch.argsort(torch.rand(t, e, generator=g), dim=1)[:, :k].to(torch.int32)
+    del logits
+    return x, idx
+
+
+@pytest.mark.parametrize("row_idx_type", [0, 1])
+@pytest.mark.parametrize("tokens_type", [0, 1])
+def test_init_routing_v2_cfg4(row_idx_type, tokens_type):
+    g = gen(32)
+    t, h, e, k = 4096, 7168, 256, 8
+    x, idx = _routing_inputs(t, h, e, k, g)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), active_num=t * k, expert_num=e, expert_tokens_num_type=tokens_type,
+        expert_tokens_num_flag=True, row_idx_type=row_idx_type)
+    wex, wri, wtok, _ = G.moe_init_routing_v2(f32np(x), idx.numpy(), None, t * k, 0, e, tokens_type, row_idx_type)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    np.testing.assert_array_equal(f32np(ex), wex)
+
+
+def test_init_routing_v2_range_active_and_scale():
+    g = gen(33)
+    t, h, e, k = 333, 96, 32, 4
+    x, idx = _routing_inputs(t, h, e, k, g)
+    scale = torch.rand(t, generator=g)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), scale=scale.to(DEV), active_num=700, expert_num=e, active_expert_range=[4, 20],
+        expert_tokens_num_type=1, row_idx_type=0)
+    wex, wri, wtok, wes = G.moe_init_routing_v2(f32np(x), idx.numpy(), scale.numpy(), 700, 4, 20, 1, 0)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    np.testing.assert_array_equal(f32np(ex), wex)
+    np.testing.assert_array_equal(es.cpu().numpy(), wes)
+
+
+def test_init_routing_legacy():
+    g = gen(34)
+    t, h, k = 250, 64, 3
+    x = randn((t, h), g, torch.float32)
+    idx = torch.randint(0, 10, (t, k), generator=g, dtype=torch.int32)
+    row = torch.arange(t * k, dtype=torch.int32).view(k, t).t().contiguous()
+    for active in (t, 100):
+        ex, ri, ei = torch.ops.npu.npu_moe_init_routing(x.to(DEV), row.to(DEV), idx.to(DEV), active)
+        wex, wri, wei = G.moe_init_routing(x.numpy(), row.numpy(), idx.numpy(), active)
+        np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+        np.testing.assert_array_equal(ei.cpu().numpy(), wei)
+        np.testing.assert_array_equal(ex.cpu().numpy(), wex)
+
+
+def test_finalize_cfg4():
+    g = gen(35)
+    t, h, k = 4096, 7168, 8
+    n = t * k
+    expanded = randn((n, h), g)
+    perm = torch.randperm(n, generator=g).to(torch.int32)
+    scales = torch.rand(t, k, generator=g)
+    y = torch.ops.npu.npu_moe_finalize_routing(expanded.to(DEV), None, None, None, scales.to(DEV), perm.to(DEV), None,
+                                               drop_pad_mode=2)
+    want = G.moe_finalize_routing(f32np(expanded), None, None, None, scales.numpy(), perm.numpy(), None, 2, "bf16")
+    assert_close(f32np(y), want)
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")])
+def test_finalize_declared_cases(dtype, name):
+    """Shapes of the reference's declared cases (npu_moe_finalize_routing.py:4-20)."""
+    g = gen(36)
+    ex = randn((24, 7), g, dtype)
+    s1, s2, bias = randn((12, 7), g, dtype), randn((12, 7), g, dtype), randn((3, 7), g, dtype)
+    scales = randn((12, 2), g, dtype)
+    row = torch.arange(24, dtype=torch.int32)
+    exp = torch.randint(0, 3, (12, 2), generator=g, dtype=torch.int32)
+    for args in ((s1, s2, bias, scales), (s1, None, bias, scales), (None, None, None, scales)):
+        a1, a2, b, sc = args
+        y = torch.ops.npu.npu_moe_finalize_routing(ex.to(DEV), *(None if v is None else v.to(DEV) for v in (a1, a2, b, sc)),
+                                                   row.to(DEV), exp.to(DEV), drop_pad_mode=0)
+        want = G.moe_finalize_routing(f32np(ex), *(None if v is None else f32np(v) for v in (a1, a2, b, sc)),
+                                      row.numpy(), exp.numpy(), 0, name)
+        assert_close(f32np(y), want, rtol=2e-2, atol=2e-2)
+
+
+def test_routing_round_trip():
+    """finalize(init(x)) with weights summing to one returns x (token-major slots)."""
+    g = gen(37)
+    t, h, e, k = 1000, 256, 64, 8
+    x, idx = _routing_inputs(t, h, e, k, g)
+    ex, ri, tok, _ = torch.ops.npu.npu_moe_init_routing_v2(x.to(DEV), idx.to(DEV), expert_num=e)
+    w = torch.full((t, k), 1.0 / k, device=DEV)
+    y = torch.ops.npu.npu_moe_finalize_routing(ex, None, None, None, w, ri, idx.to(DEV), drop_pad_mode=2)
+    assert_close(f32np(y), f32np(x))
+    assert int(tok[-1]) == t * k

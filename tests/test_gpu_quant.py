@@ -1,0 +1,93 @@
+"""GPU parity: npu_dynamic_quant and npu_dequant_swiglu_quant against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_int8_close, f32np, gen, randn, uniform
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _dq_check(x, smooth=None, gidx=None):
+    y, s = torch.ops.npu.npu_dynamic_quant(x.to(DEV), smooth_scales=None if smooth is None else smooth.to(DEV),
+                                           group_index=None if gidx is None else gidx.to(DEV))
+    wy, ws = G.dynamic_quant(f32np(x), None if smooth is None else f32np(smooth),
+                             None if gidx is None else gidx.numpy())
+    assert y.dtype == torch.int8 and y.shape == x.shape and s.shape == x.shape[:-1]
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), ws, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("shape", [(128, 2048), (8192, 7168), (64, 16384), (3, 5, 1000), (1, 20000), (7, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dynamic_quant_shapes(shape, dtype):
+    g = gen(1)
+    _dq_check(randn(shape, g, dtype))
+
+
+def test_dynamic_quant_smooth_and_groups():
+    g = gen(2)
+    x = randn((300, 512), g)
+    _dq_check(x, smooth=uniform((512,), g, 0.5, 2.0))
+    gidx = torch.tensor([50, 50, 200, 300], dtype=torch.int32)
+    _dq_check(x, smooth=uniform((4, 512), g, 0.5, 2.0), gidx=gidx)
+    _dq_check(x, smooth=uniform((4, 512), g, 0.5, 2.0), gidx=gidx.to(torch.int64))
+
+
+def test_dynamic_quant_zero_and_constant_rows():
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    x[1] = 3.0
+    x[2] = -0.25
+    y, s = torch.ops.npu.npu_dynamic_quant(x.to(DEV))
+    y, s = y.cpu(), s.cpu()
+    assert s[0] == 0 and (y[0] == 0).all()
+    assert (y[1] == 127).all() and (y[2] == -127).all()
+    assert torch.ops.npu.npu_dynamic_quant(torch.empty(0, 64, dtype=torch.bfloat16, device=DEV))[0].numel() == 0
+
+
+def _dsq_inputs(rows, n, g, groups=None):
+    x = torch.randint(-200000, 200000, (rows, 2 * n), generator=g, dtype=torch.int32)
+    ws_shape = (2 * n,) if groups is None else (groups, 2 * n)
+    ws = uniform(ws_shape, g, 1e-3, 1e-2)
+    act = uniform((rows,), g, 0.005, 0.05)
+    return x, ws, act
+
+
+def _dsq_check(x, ws, act, left, bias=None, qs=None, gidx=None):
+    y, s = torch.ops.npu.npu_dequant_swiglu_quant(
+        x.to(DEV), weight_scale=ws.to(DEV), activation_scale=None if act is None else act.to(DEV),
+        bias=None if bias is None else bias.to(DEV), quant_scale=None if qs is None else qs.to(DEV),
+        group_index=None if gidx is None else gidx.to(DEV), activate_left=left, quant_mode=1)
+    wy, wsc = G.dequant_swiglu_quant(x.numpy(), ws.numpy(), None if act is None else act.numpy(),
+                                     None if bias is None else bias.numpy(), None if qs is None else qs.numpy(),
+                                     None if gidx is None else gidx.numpy(), left)
+    assert y.shape == (x.shape[0], x.shape[1] // 2)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=1e-30)
+
+
+@pytest.mark.parametrize("left", [True, False])
+def test_dsq_cfg1(left):
+    g = gen(3)
+    x, ws, act = _dsq_inputs(128, 5632, g)
+    _dsq_check(x, ws, act, left)
+
+
+def test_dsq_grouped_cfg4_slice():
+    g = gen(4)
+    counts = torch.randint(0, 40, (64,), generator=g, dtype=torch.int64)
+    rows = int(counts.sum()) + 17  # rows past the grouped total come out as zero
+    x, ws, act = _dsq_inputs(rows, 2048, g, groups=64)
+    _dsq_check(x, ws, act, True, gidx=counts)
+
+
+def test_dsq_bias_quant_scale_and_odd_n():
+    g = gen(5)
+    x, ws, act = _dsq_inputs(33, 100, g)
+    _dsq_check(x, ws, act, False, bias=torch.randint(-1000, 1000, (200,), generator=g, dtype=torch.int32))
+    _dsq_check(x, ws, None, True, bias=uniform((200,), g, -1, 1), qs=uniform((100,), g, 0.5, 2))
+    x2, ws2, act2 = _dsq_inputs(9, 7, g)  # n not a multiple of 4 -> generic kernel
+    _dsq_check(x2, ws2, act2, True)

@@ -1,0 +1,295 @@
+"""Pins the CPU oracle with checks independent of its own formulas: closed forms, invariants,
+brute force on tiny inputs and special cases that reduce to library routines."""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import scipy.special
+
+from oracle import golden as G
+
+RNG = np.random.default_rng(0)
+
+
+# ----------------------------------------------------------------------------- quantisation
+def test_dynamic_quant_closed_form_and_round_half_even():
+    # scale = 127/127 = 1 exactly, so y = rint(x): halves go to the even neighbour.
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.49]], np.float32)
+    y, s = G.dynamic_quant(x)
+    assert s[0] == 1.0
+    assert y[0].tolist() == [127, 0, 2, 2, 0, -2, -2, 3]
+
+
+def test_dynamic_quant_invariants():
+    x = RNG.standard_normal((64, 333)).astype(np.float32)
+    x[3] = 0.0
+    x[5] = 2.0
+    y, s = G.dynamic_quant(x)
+    assert np.abs(y.astype(int)).max() <= 127
+    nz = np.abs(x).max(axis=1) > 0
+    assert (np.abs(y[nz].astype(int)).max(axis=1) == 127).all()
+    assert s[3] == 0 and (y[3] == 0).all()
+    assert (y[5] == 127).all()
+    # dequantised value within half a step of the input (plus fp32 rounding slack)
+    err = np.abs(y.astype(np.float64) * s[:, None] - x)
+    assert (err <= s[:, None] * 0.5 * (1 + 1e-5) + 1e-12).all()
+
+
+def test_dynamic_quant_smooth_is_prescaling():
+    x = RNG.standard_normal((10, 32)).astype(np.float32)
+    sm = RNG.uniform(0.5, 2, 32).astype(np.float32)
+    y1, s1 = G.dynamic_quant(x, sm)
+    y2, s2 = G.dynamic_quant(x * sm)
+    assert (y1 == y2).all() and (s1 == s2).all()
+    # grouped smooth scales: rows [0,3) use row 0, [3,10) row 1 (cumulative ends)
+    sm2 = RNG.uniform(0.5, 2, (2, 32)).astype(np.float32)
+    y3, _ = G.dynamic_quant(x, sm2, np.array([3, 10]))
+    assert (y3[:3] == G.dynamic_quant(x[:3] * sm2[0])[0]).all()
+    assert (y3[3:] == G.dynamic_quant(x[3:] * sm2[1])[0]).all()
+
+
+def _silu64(a):
+    return a / (1.0 + math.exp(-a))
+
+
+def test_dequant_swiglu_quant_brute_force():
+    x = RNG.integers(-3000, 3000, (4, 16)).astype(np.int32)
+    ws = RNG.uniform(1e-3, 1e-2, 16).astype(np.float32)
+    act = RNG.uniform(0.01, 0.1, 4).astype(np.float32)
+    for left in (True, False):
+        y, s = G.dequant_swiglu_quant(x, ws, act, activate_left=left)
+        for r in range(4):
+            vals = []
+            for j in range(8):
+                a = float(x[r, j]) * float(ws[j]) * float(act[r])
+                b = float(x[r, 8 + j]) * float(ws[8 + j]) * float(act[r])
+                vals.append(_silu64(a) * b if left else a * _silu64(b))
+            sc = max(abs(v) for v in vals) / 127.0
+            assert s[r] == pytest.approx(sc, rel=1e-5)
+            want = [max(-128, min(127, round(v / sc))) for v in vals]
+            assert np.abs(y[r].astype(int) - np.array(want)).max() <= 1
+
+
+def test_dequant_swiglu_quant_groups_and_zero_half():
+    x = RNG.integers(-1000, 1000, (6, 8)).astype(np.int32)
+    x[:, :4] = 0  # A half zero: silu(A)*B == 0 -> zero rows when activating the left half
+    ws = RNG.uniform(1e-3, 1e-2, (2, 8)).astype(np.float32)
+    y, s = G.dequant_swiglu_quant(x, ws, None, group_index=np.array([2, 3]), activate_left=True)
+    assert (y == 0).all() and (s == 0).all()
+    y, s = G.dequant_swiglu_quant(x, ws, None, group_index=np.array([2, 3]), activate_left=False)
+    assert (s[5] == 0) and (y[5] == 0).all()  # row past the grouped total
+    assert s[0] == 0  # A*silu(B) with A == 0
+    # rows 0-1 use weight row 0, rows 2-4 weight row 1
+    x2 = RNG.integers(-1000, 1000, (5, 8)).astype(np.int32)
+    y2, _ = G.dequant_swiglu_quant(x2, ws, None, group_index=np.array([2, 3]))
+    assert (y2[:2] == G.dequant_swiglu_quant(x2[:2], ws[0])[0]).all()
+    assert (y2[2:] == G.dequant_swiglu_quant(x2[2:], ws[1])[0]).all()
+
+
+# ----------------------------------------------------------------------------- GEMMs
+def test_int_matmul_exact_at_cfg_k():
+    a = np.full((2, 7168), -127, np.int8)
+    b = np.full((7168, 3), -127, np.int8)
+    acc = G.int_matmul(a, b)
+    assert (acc == 127 * 127 * 7168).all()
+    a = RNG.integers(-127, 128, (9, 700), dtype=np.int8)
+    b = RNG.integers(-127, 128, (700, 5), dtype=np.int8)
+    assert (G.int_matmul(a, b) == a.astype(np.int64) @ b.astype(np.int64)).all()
+
+
+def test_quant_matmul_identity_and_epilogue():
+    a = RNG.integers(-127, 128, (8, 16), dtype=np.int8)
+    eye = np.eye(16, dtype=np.int8)
+    assert (G.quant_matmul(a, eye, out_dtype="int32") == a.astype(np.int32)).all()
+    scale = RNG.uniform(1e-3, 1e-2, 16).astype(np.float32)
+    pts = RNG.uniform(1e-3, 1e-2, 8).astype(np.float32)
+    out = G.quant_matmul(a, eye, scale, pts, None, "fp32")
+    np.testing.assert_allclose(out, a.astype(np.float64) * scale[None] * pts[:, None], rtol=1e-6)
+    bf = G.quant_matmul(a, eye, scale, pts, None, "bf16")
+    np.testing.assert_allclose(bf, out, rtol=2 ** -8)
+
+
+def test_grouped_matmul_is_per_group_matmul():
+    x = RNG.integers(-127, 128, (20, 12), dtype=np.int8)
+    w = RNG.integers(-127, 128, (3, 12, 5), dtype=np.int8)
+    counts = np.array([7, 0, 10])
+    out = G.grouped_matmul(x, w, counts, 1)
+    assert (out[:7] == x[:7].astype(int) @ w[0].astype(int)).all()
+    assert (out[7:17] == x[7:17].astype(int) @ w[2].astype(int)).all()
+    assert (out[17:] == 0).all()
+    assert (G.grouped_matmul(x, w, np.cumsum(counts), 0) == out).all()
+
+
+# ----------------------------------------------------------------------------- gating
+def _gate_brute(x, bias, k, k_group, group_count, mode):
+    """Brute force over every choice of k_group groups, plain Python."""
+    e = len(x)
+    s = [1.0 / (1.0 + math.exp(-v)) for v in x]
+    sb = [s[i] + bias[i] for i in range(e)]
+    gsz = e // group_count
+    def gscore(gi):
+        vals = sorted(sb[gi * gsz:(gi + 1) * gsz], reverse=True)
+        return vals[0] + vals[1] if mode == 1 else vals[0]
+    scores = [gscore(gi) for gi in range(group_count)]
+    best = None
+    for combo in itertools.combinations(range(group_count), k_group):
+        key = (sorted([-scores[c] for c in combo]), combo)
+        if best is None or key < best:
+            best = key
+    cand = [i for c in best[1] for i in range(c * gsz, (c + 1) * gsz)]
+    chosen = sorted(cand, key=lambda i: (-sb[i], i))[:k]
+    w = [s[i] for i in chosen]
+    tot = sum(w)
+    return chosen, [v / tot for v in w]
+
+
+def test_gating_brute_force():
+    for trial in range(20):
+        x = RNG.standard_normal((1, 16)).astype(np.float32)
+        bias = (RNG.standard_normal(16) * 0.1).astype(np.float32)
+        y, idx, _ = G.moe_gating_top_k(x, 3, bias, k_group=2, group_count=4, group_select_mode=trial % 2,
+                                       norm_type=1)
+        want_idx, want_w = _gate_brute(x[0].astype(np.float64), bias.astype(np.float64), 3, 2, 4, trial % 2)
+        assert idx[0].tolist() == want_idx
+        np.testing.assert_allclose(y[0], want_w, rtol=1e-5)
+
+
+def test_gating_single_group_is_topk_and_softmax():
+    x = RNG.standard_normal((50, 40)).astype(np.float32)
+    y, idx, out = G.moe_gating_top_k(x, 5, norm_type=0, out_flag=True)
+    p = scipy.special.softmax(x.astype(np.float64), axis=1)
+    np.testing.assert_allclose(out, p, rtol=1e-6)
+    want = np.argsort(-p, axis=1, kind="stable")[:, :5]
+    assert (idx == want).all()
+    np.testing.assert_allclose(y, np.take_along_axis(p, want, 1), rtol=1e-6)
+
+
+def test_gating_ties_lower_index():
+    x = np.zeros((1, 16), np.float32)
+    _, idx, _ = G.moe_gating_top_k(x, 4, k_group=2, group_count=4, group_select_mode=1, norm_type=1)
+    assert idx[0].tolist() == [0, 1, 2, 3]
+
+
+# ----------------------------------------------------------------------------- routing
+def test_init_routing_v2_invariants_and_round_trip():
+    t, k, e, h = 50, 4, 9, 6
+    idx = np.stack([RNG.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+    x = RNG.standard_normal((t, h)).astype(np.float32)
+    ex, ri, tok, _ = G.moe_init_routing_v2(x, idx, None, t * k, 0, e, 0, 0)
+    assert sorted(ri.tolist()) == list(range(t * k))  # bijection
+    src = np.empty(t * k, np.int64)
+    src[ri] = np.arange(t * k)
+    exp_sorted = idx.reshape(-1)[src]
+    assert (np.diff(exp_sorted) >= 0).all()  # sorted by expert
+    same = np.diff(exp_sorted) == 0
+    assert (np.diff(src)[same] > 0).all()  # stable: slot order inside an expert
+    assert tok[-1] == t * k and (np.diff(tok) >= 0).all()
+    assert (ex == x[src // k]).all()
+    _, ri1, cnt, _ = G.moe_init_routing_v2(x, idx, None, t * k, 0, e, 1, 1)
+    assert (ri1 == src).all() and (np.cumsum(cnt) == tok).all()
+    w = np.full((t, k), 1.0 / k, np.float32)
+    y = G.moe_finalize_routing(ex, None, None, None, w, ri, idx, 2, "fp32")
+    np.testing.assert_allclose(y, x, rtol=1e-6, atol=1e-6)
+
+
+def test_init_routing_legacy_declared_case():
+    """Declared case of moe_init_routing.py:4-9: F32(3,4), I32(3,2), I32(3,2), active_num=3."""
+    x = RNG.standard_normal((3, 4)).astype(np.float32)
+    row = np.arange(6, dtype=np.int32).reshape(2, 3).T
+    idx = np.array([[2, 0], [1, 2], [0, 1]], np.int32)
+    ex, eri, eei = G.moe_init_routing(x, row, idx, 3)
+    assert eei.tolist() == [0, 0, 1, 1, 2, 2]
+    # slot order (t*k+j): (0,1)->row 3,(2,0)->row 2 for expert 0; (1,0)->1,(2,1)->5; (0,0)->0,(1,1)->4
+    assert (ex == x[np.array([3, 2, 1, 5, 0, 4]) % 3]).all()
+    assert sorted(eri.tolist()) == list(range(6))
+
+
+def test_finalize_declared_case_by_hand():
+    ex = RNG.standard_normal((24, 7)).astype(np.float32)
+    s1 = RNG.standard_normal((12, 7)).astype(np.float32)
+    bias = RNG.standard_normal((3, 7)).astype(np.float32)
+    sc = RNG.standard_normal((12, 2)).astype(np.float32)
+    row = np.arange(24, dtype=np.int32)
+    exp = RNG.integers(0, 3, (12, 2)).astype(np.int32)
+    y = G.moe_finalize_routing(ex, s1, None, bias, sc, row, exp, 0, "fp32")
+    for t in range(12):
+        want = s1[t].astype(np.float64).copy()
+        for j in range(2):
+            want += sc[t, j] * (ex[j * 12 + t] + bias[exp[t, j]])
+        np.testing.assert_allclose(y[t], want, rtol=1e-5, atol=1e-5)
+
+
+# ----------------------------------------------------------------------------- attention
+def _paged(L_list, hkv, d, bs, rng):
+    nblk = sum((L + bs - 1) // bs for L in L_list) + 2
+    k = rng.standard_normal((nblk, bs, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((nblk, bs, hkv, d)).astype(np.float32)
+    perm = rng.permutation(nblk)
+    width = max((L + bs - 1) // bs for L in L_list)
+    bt = np.zeros((len(L_list), width), np.int32)
+    o = 0
+    for b, L in enumerate(L_list):
+        nb = (L + bs - 1) // bs
+        bt[b, :nb] = perm[o:o + nb]
+        o += nb
+    return k, v, bt
+
+
+def test_paged_decode_matches_dense_and_lse():
+    L = [5, 17, 1]
+    k, v, bt = _paged(L, 2, 8, 4, RNG)
+    q = RNG.standard_normal((3, 4, 8)).astype(np.float32)
+    out, lse = G.paged_decode_attention(q, k, v, bt, L, 0.3)
+    for b in range(3):
+        kk = k[bt[b]].reshape(-1, 2, 8)[:L[b]]
+        vv = v[bt[b]].reshape(-1, 2, 8)[:L[b]]
+        for h in range(4):
+            s = kk[:, h // 2].astype(np.float64) @ q[b, h] * 0.3
+            p = scipy.special.softmax(s)
+            np.testing.assert_allclose(out[b, h], p @ vv[:, h // 2], rtol=1e-4, atol=1e-5)
+            assert lse[b, h] == pytest.approx(scipy.special.logsumexp(s), rel=1e-5)
+    # L == 1 -> the single value row
+    np.testing.assert_allclose(out[2, 0], v[bt[2, 0], 0, 0], rtol=1e-6)
+
+
+def test_paged_decode_constant_values():
+    k, v, bt = _paged([9, 12], 1, 4, 4, RNG)
+    v[:] = np.arange(4, dtype=np.float32)
+    out, _ = G.paged_decode_attention(RNG.standard_normal((2, 3, 4)).astype(np.float32), k, v, bt, [9, 12], 1.0)
+    np.testing.assert_allclose(out, np.broadcast_to(np.arange(4, dtype=np.float32), out.shape), rtol=1e-5)
+
+
+def test_prefill_causal_prefix_property():
+    q = RNG.standard_normal((1, 6, 2, 4)).astype(np.float32)
+    k = RNG.standard_normal((1, 6, 1, 4)).astype(np.float32)
+    v = RNG.standard_normal((1, 6, 1, 4)).astype(np.float32)
+    out, _ = G.prefill_attention(q, k, v, None, None, 1, 0.5)
+    k2, v2 = k.copy(), v.copy()
+    k2[0, 4:] = 100.0
+    v2[0, 4:] = -50.0
+    out2, _ = G.prefill_attention(q, k2, v2, None, None, 1, 0.5)
+    np.testing.assert_allclose(out[0, :4], out2[0, :4], rtol=1e-6)  # rows < 4 never see kv >= 4
+    np.testing.assert_allclose(out[0, 0, 0], v[0, 0, 0], rtol=1e-6)  # first row sees only kv 0
+    # padded query rows are zero
+    out3, lse3 = G.prefill_attention(q, k, v, [3], [3], 1, 0.5)
+    assert (out3[0, 3:] == 0).all() and np.isneginf(lse3[0, :, 3:]).all()
+
+
+def test_mla_equals_gqa_on_dequantised_latent():
+    L = [7, 20]
+    bs, dn, dr, h = 4, 16, 4, 3
+    nblk = 10
+    ckv = RNG.integers(-127, 128, (nblk, bs, dn), dtype=np.int8)
+    cs = RNG.uniform(1e-3, 1e-2, (nblk, bs)).astype(np.float32)
+    kr = RNG.standard_normal((nblk, bs, dr)).astype(np.float32)
+    bt = np.array([[3, 1, 0, 0, 0], [2, 5, 7, 9, 4]], np.int32)
+    qn = RNG.standard_normal((2, h, dn)).astype(np.float32)
+    qr = RNG.standard_normal((2, h, dr)).astype(np.float32)
+    out, lse = G.mla_decode_attention(qn, qr, ckv, cs, kr, bt, L, 0.2)
+    kfull = np.concatenate([ckv.astype(np.float32) * cs[..., None], kr], -1)[:, :, None, :]
+    vfull = np.concatenate([ckv.astype(np.float32) * cs[..., None], np.zeros((nblk, bs, dr), np.float32)],
+                           -1)[:, :, None, :]
+    o2, l2 = G.paged_decode_attention(np.concatenate([qn, qr], -1), kfull, vfull, bt, L, 0.2)
+    np.testing.assert_allclose(out, o2[..., :dn], rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(lse, l2, rtol=1e-5)

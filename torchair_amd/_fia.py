@@ -1,0 +1,300 @@
+"""npu_fused_infer_attention_score: output-shape rules and dispatch onto the HIP kernels.
+
+Output shapes follow python/torchair/ops/_npu_fused_infer_attention_score.py:160-374
+(layout table, value head dim, attention_out and softmax_lse shapes). The ROCm
+implementation serves three cases:
+  * paged GQA decode   - block_table given, one query token per sequence;
+  * MLA absorbed decode - block_table + query_rope/key_rope, int8 latent cache with a
+                          per-token fp32 scale (key_antiquant_mode 1);
+  * dense prefill       - no block_table; optional causal mask (sparse_mode 2 / 3).
+Sequence lengths stay on the device (tensor arguments of air::npu_fused_infer_attention_score),
+so a captured graph replays correctly with new lengths.
+"""
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import DT_NONE
+
+# input_layout -> (query layout, output layout, query rank)
+_LAYOUTS: Dict[str, Tuple[str, str, int]] = {
+    "BSH": ("BSH", "BSH", 3), "BSND": ("BSND", "BSND", 4), "BNSD": ("BNSD", "BNSD", 4),
+    "TND": ("TND", "TND", 3), "NTD": ("NTD", "NTD", 3), "BNSD_BSND": ("BNSD", "BSND", 4),
+    "BSH_BNSD": ("BSH", "BNSD", 3), "BSND_BNSD": ("BSND", "BNSD", 4), "NTD_TND": ("NTD", "TND", 3),
+    "BSH_NBSD": ("BSH", "NBSD", 3), "BSND_NBSD": ("BSND", "NBSD", 4), "BNSD_NBSD": ("BNSD", "NBSD", 4),
+    "TND_NTD": ("TND", "NTD", 3), "NSD": ("NSD", "NSD", 3),
+}
+
+
+def _layouts(query, input_layout):
+    if input_layout not in _LAYOUTS:
+        raise ValueError(f"Layout {input_layout} is not supported!")
+    ql, ol, qdim = _LAYOUTS[input_layout]
+    if query.dim() != qdim:
+        raise ValueError(f"Layout {ql}, queryDims({query.dim()}) must be {qdim}!")
+    return ql, ol
+
+
+def _bsnd(query, ql, num_heads):
+    """(batch, seq, heads, head_dim) of the query in layout ql."""
+    if ql == "BSH":
+        return query.size(0), query.size(1), num_heads, query.size(2) // num_heads
+    if ql == "BSND":
+        return query.size(0), query.size(1), query.size(2), query.size(3)
+    if ql == "BNSD":
+        return query.size(0), query.size(2), query.size(1), query.size(3)
+    if ql == "NSD":
+        return 1, query.size(1), query.size(0), query.size(2)
+    raise ValueError(f"Layout {ql} is not supported in get_query_b_s_n_d function!")
+
+
+def _tnd(query, ql):
+    if ql == "TND":
+        return query.size(0), query.size(1), query.size(2)
+    if ql == "NTD":
+        return query.size(1), query.size(0), query.size(2)
+    raise ValueError(f"Layout {ql} is not supported in get_query_t_n_d function!")
+
+
+def _value_d(block_table, value, query, ql, n_kv):
+    if block_table is not None:
+        if value.dim() == 3:
+            return value.size(2) // n_kv
+        if value.dim() == 4:
+            return value.size(3)
+        if value.dim() == 5:
+            return value.size(2) * value.size(4)
+        raise ValueError(f"when Page Attention enabled, value dim should be 3/4/5, but got {value.dim()}!")
+    if value.dim() != query.dim():
+        raise ValueError(f"when Page Attention not enabled, value dim{value.dim()} should equal to query dim{query.dim()}!")
+    if ql == "BSH":
+        return value.size(2) // n_kv
+    if ql in ("BNSD", "BSND"):
+        return value.size(3)
+    return value.size(2)
+
+
+def _out_shape(ol, query, ql, num_heads, value_d):
+    def od(d1):
+        return d1 if (value_d == 0 or d1 == 0) else value_d
+    if ol in ("TND", "NTD"):
+        t, n1, d1 = _tnd(query, ql)
+        return [t, n1, od(d1)] if ol == "TND" else [n1, t, od(d1)]
+    b, s1, n1, d1 = _bsnd(query, ql, num_heads)
+    if ol == "BSH":
+        h = n1 * value_d
+        return [b, s1, h if (h != 0 and query.size(2) != 0) else query.size(2)]
+    if ol == "BSND":
+        return [b, s1, n1, od(d1)]
+    if ol == "BNSD":
+        return [b, n1, s1, od(d1)]
+    if ol == "NBSD":
+        return [n1, b, s1, od(d1)]
+    if ol == "NSD":
+        return [n1, s1, od(d1)]
+    raise ValueError(f"output layout {ol} not supported")
+
+
+def _lse_shape(query, input_layout, ql, num_heads):
+    if input_layout in ("TND", "NTD", "TND_NTD", "NTD_TND"):
+        t, n1, _ = _tnd(query, ql)
+        return [t, n1, 1]
+    b, s1, n1, _ = _bsnd(query, ql, num_heads)
+    return [b, n1, s1, 1]
+
+
+def fia_fake(query, key, value, **kw):
+    num_heads = kw.get("num_heads", 1)
+    if num_heads <= 0:
+        raise ValueError(f"numHeads should be greater than 0, but got {num_heads}!")
+    n_kv = kw.get("num_key_value_heads", 0) or num_heads
+    input_layout = kw.get("input_layout", "BSH")
+    ql, ol = _layouts(query, input_layout)
+    vd = _value_d(kw.get("block_table"), value, query, ql, n_kv)
+    if value is not None and value.dtype == torch.int32:  # int4 packed in int32
+        vd *= 8
+    shape = _out_shape(ol, query, ql, num_heads, vd)
+    if kw.get("quant_scale2") is not None:
+        dt = torch.int8
+    elif query.dtype == torch.int8:
+        qr = kw.get("query_rope")
+        dt = qr.dtype if qr is not None else torch.half
+    else:
+        dt = query.dtype
+    out = query.new_empty(shape, dtype=dt)
+    if kw.get("softmax_lse_flag", False):
+        lse = query.new_empty(_lse_shape(query, input_layout, ql, num_heads), dtype=torch.float32)
+    else:
+        lse = query.new_empty([0], dtype=torch.float32)
+    return out, lse
+
+
+_UNSUPPORTED = ("pse_shift", "dequant_scale1", "quant_scale1", "dequant_scale2", "quant_scale2", "quant_offset2",
+                "antiquant_scale", "antiquant_offset", "query_padding_size", "kv_padding_size", "key_antiquant_offset",
+                "value_antiquant_offset", "key_shared_prefix", "value_shared_prefix", "actual_shared_prefix_len",
+                "key_rope_antiquant_scale")
+
+
+def _lens_tensor(v, device) -> Optional[torch.Tensor]:
+    if v is None:
+        return None
+    if isinstance(v, torch.Tensor):
+        return v.to(device=device, dtype=torch.int64).contiguous()
+    return torch.tensor([int(x) for x in v], dtype=torch.int64, device=device)
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _strides_bshd(t: torch.Tensor, layout: str, heads: int):
+    """Element strides (batch, seq, head) of q/k/v/out in the given layout; the last dim must be dense."""
+    _check(t.stride(-1) == 1, "npu_fused_infer_attention_score: head_dim must be contiguous")
+    if layout == "BSH":
+        d = t.size(2) // heads
+        return [t.stride(0), t.stride(1), d]
+    if layout == "BSND":
+        return [t.stride(0), t.stride(1), t.stride(2)]
+    if layout == "BNSD":
+        return [t.stride(0), t.stride(2), t.stride(1)]
+    raise RuntimeError(f"npu_fused_infer_attention_score: layout {layout} not supported for prefill")
+
+
+def fia_cuda(query, key, value, **kw):
+    """ROCm implementation of npu_fused_infer_attention_score (fused_infer_attention_score.py:4-109)."""
+    for name in _UNSUPPORTED:
+        v = kw.get(name)
+        _check(v is None or (isinstance(v, (list, tuple)) and len(v) == 0),
+               f"npu_fused_infer_attention_score: {name} is not supported")
+    for t in (query, key, value):
+        _check(t.device.type == "cuda", "npu_fused_infer_attention_score runs on the ROCm device only")
+    out, lse = fia_fake(query, key, value, **kw)
+    num_heads = kw.get("num_heads", 1)
+    n_kv = kw.get("num_key_value_heads", 0) or num_heads
+    input_layout = kw.get("input_layout", "BSH")
+    ql, ol = _layouts(query, input_layout)
+    scale = float(kw.get("scale", 1.0))
+    block_table = kw.get("block_table")
+    want_lse = bool(kw.get("softmax_lse_flag", False))
+    stream = torch.cuda.current_stream(query.device).cuda_stream
+    seq_kv = _lens_tensor(kw.get("actual_seq_lengths_kv"), query.device)
+    seq_q = _lens_tensor(kw.get("actual_seq_lengths"), query.device)
+
+    if block_table is not None:
+        _check(ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql,
+               "npu_fused_infer_attention_score: paged attention supports BSH/BSND/BNSD/TND without layout change")
+        b = query.size(0)
+        s = 1 if ql == "TND" else _bsnd(query, ql, num_heads)[1]
+        _check(s == 1, "npu_fused_infer_attention_score: paged attention serves one query token per sequence")
+        _check(seq_kv is not None and seq_kv.numel() == b,
+               "npu_fused_infer_attention_score: actual_seq_lengths_kv is required with block_table")
+        bt = block_table.to(torch.int32).contiguous()
+        _check(bt.dim() == 2 and bt.size(0) == b, "npu_fused_infer_attention_score: block_table must be [B, max_blocks]")
+        if kw.get("query_rope") is not None:
+            return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
+        _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
+               "npu_fused_infer_attention_score: paged decode takes bf16 query/key/value")
+        _check(kw.get("atten_mask") is None, "npu_fused_infer_attention_score: atten_mask is not used in decode")
+        q = query.contiguous()
+        d = q.numel() // (b * num_heads)
+        if key.dim() == 3:
+            bs = key.size(1)
+            _check(key.size(2) == n_kv * d, "npu_fused_infer_attention_score: key cache must be [blocks, bs, Hkv*D]")
+            sb, ss, sh = key.stride(0), key.stride(1), d
+        else:
+            _check(key.dim() == 4 and key.size(1) == n_kv and key.size(3) == d,
+                   "npu_fused_infer_attention_score: key cache must be [blocks, Hkv, bs, D]")
+            bs = key.size(2)
+            sb, ss, sh = key.stride(0), key.stride(2), key.stride(1)
+        _check(key.stride(-1) == 1 and value.stride() == key.stride() and value.shape == key.shape,
+               "npu_fused_infer_attention_score: key/value caches must share shape and a dense head dim")
+        blk = kw.get("block_size", 0) or bs
+        _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
+        ws_bytes = _lib.query("tai_fia_paged_decode_workspace_size", b, num_heads, d, bt.size(1), bs)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.call("tai_fia_paged_decode", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh, bt.data_ptr(),
+                  bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, bs, scale, out.data_ptr(),
+                  lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+        return out, lse
+
+    # ---------------------------------------------------------------- dense prefill
+    _check(ql in ("BSH", "BSND", "BNSD") and ol == ql,
+           "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
+    _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
+           "npu_fused_infer_attention_score: prefill takes bf16 query/key/value")
+    sparse_mode = int(kw.get("sparse_mode", 0))
+    mask = kw.get("atten_mask")
+    if sparse_mode in (2, 3):
+        causal = 1 if sparse_mode == 3 else 2
+    elif sparse_mode == 0:
+        _check(mask is None, "npu_fused_infer_attention_score: explicit atten_mask with sparse_mode 0 is not supported;"
+                             " use sparse_mode 2/3 for causal masks")
+        pre, nxt = int(kw.get("pre_tokens", 2147483647)), int(kw.get("next_tokens", 2147483647))
+        if nxt == 0 and pre >= 2147483647 // 2:
+            causal = 2
+        else:
+            _check(pre >= 2147483647 // 2 and nxt >= 2147483647 // 2,
+                   "npu_fused_infer_attention_score: band masks (pre/next tokens) are not supported")
+            causal = 0
+    else:
+        raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported")
+    b, s_q, hq, d = _bsnd(query, ql, num_heads)
+    if ql == "BSH":
+        s_kv = key.size(1)
+    elif ql == "BSND":
+        s_kv = key.size(1)
+    else:
+        s_kv = key.size(2)
+    qs = _strides_bshd(query, ql, hq)
+    ks = _strides_bshd(key, ql, n_kv)
+    vs = _strides_bshd(value, ql, n_kv)
+    os_ = _strides_bshd(out, ol, hq)
+    _check(hq % n_kv == 0, "npu_fused_infer_attention_score: num_heads must be a multiple of num_key_value_heads")
+    arr = [(_ctypes_i64(qs)), _ctypes_i64(ks), _ctypes_i64(vs), _ctypes_i64(os_)]
+    _lib.call("tai_fia_prefill", query.data_ptr(), key.data_ptr(), value.data_ptr(), b, s_q, s_kv, hq, n_kv, d,
+              arr[0], arr[1], arr[2], arr[3], seq_q.data_ptr() if seq_q is not None else None,
+              seq_kv.data_ptr() if seq_kv is not None else None, causal, scale, out.data_ptr(),
+              lse.data_ptr() if want_lse else None, stream)
+    return out, lse
+
+
+def _ctypes_i64(vals):
+    import ctypes
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream):
+    q_rope = kw["query_rope"]
+    k_rope = kw.get("key_rope")
+    k_scale = kw.get("key_antiquant_scale")
+    _check(k_rope is not None, "npu_fused_infer_attention_score: MLA needs key_rope")
+    _check(n_kv == 1, "npu_fused_infer_attention_score: MLA latent cache has one kv head")
+    _check(key.dtype == torch.int8 and k_scale is not None and int(kw.get("key_antiquant_mode", 0)) == 1,
+           "npu_fused_infer_attention_score: MLA serves an int8 latent cache with per-token scales "
+           "(key_antiquant_mode=1)")
+    _check(query.dtype == torch.bfloat16 and q_rope.dtype == torch.bfloat16 and k_rope.dtype == torch.bfloat16,
+           "npu_fused_infer_attention_score: MLA query/query_rope/key_rope must be bf16")
+    b = query.size(0)
+    qn = query.contiguous()
+    qr = q_rope.contiguous()
+    dn = qn.numel() // (b * num_heads)
+    dr = qr.numel() // (b * num_heads)
+    kc = key.contiguous()
+    nblk = kc.size(0)
+    bs = kc.numel() // (nblk * dn)
+    _check(kc.numel() == nblk * bs * dn, "npu_fused_infer_attention_score: latent cache must be [blocks, bs, 1, Dn]")
+    kr = k_rope.contiguous()
+    _check(kr.numel() == nblk * bs * dr, "npu_fused_infer_attention_score: key_rope must be [blocks, bs, 1, Dr]")
+    ks = k_scale.to(torch.float32).contiguous()
+    _check(ks.numel() == nblk * bs, "npu_fused_infer_attention_score: key_antiquant_scale must hold one fp32 per "
+                                    "cached token ([blocks, bs])")
+    ws_bytes = _lib.query("tai_fia_mla_decode_workspace_size", b, num_heads, dn, bt.size(1), bs)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=qn.device)
+    _lib.call("tai_fia_mla_decode", qn.data_ptr(), qr.data_ptr(), kc.data_ptr(), ks.data_ptr(), kr.data_ptr(),
+              bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, dn, dr, bs, scale, out.data_ptr(),
+              lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+    return out, lse

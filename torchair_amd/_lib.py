@@ -1,0 +1,99 @@
+"""ctypes binding of libtai_kernels.so (the C ABI declared in include/tai_kernels.h).
+
+The library is loaded lazily on the first kernel call. A missing or stale library is an
+error: there is no fallback implementation behind these entry points.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtai_kernels.so"
+
+# torch ScalarType codes used as dtype tags across the C ABI
+DT_UINT8, DT_INT8, DT_INT16, DT_INT32, DT_INT64, DT_FP16, DT_FP32, DT_BF16 = 0, 1, 2, 3, 4, 5, 6, 15
+DT_NONE = -1
+LAYOUT_KN, LAYOUT_NK = 0, 1
+
+_P = c_void_p
+_SIGS = {
+    "tai_last_error": (c_char_p, []),
+    "tai_abi_version": (c_int, []),
+    "tai_dynamic_quant": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P]),
+    "tai_dequant_swiglu_quant": (
+        c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, c_int, c_int64, c_int, _P, _P, _P]),
+    "tai_quant_matmul": (
+        c_int, [_P, _P, c_int64, c_int64, c_int64, c_int, _P, c_int64, _P, _P, c_int, c_int, _P, _P]),
+    "tai_grouped_matmul_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "tai_grouped_matmul": (
+        c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P,
+                _P, c_size_t, _P]),
+    "tai_moe_gating_top_k": (
+        c_int, [_P, c_int, c_int64, c_int64, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                c_float, c_float, _P, _P, _P, _P]),
+    "tai_moe_init_routing_workspace_size": (c_size_t, [c_int64, c_int, c_int64]),
+    "tai_moe_init_routing_v2": (
+        c_int, [_P, c_int, c_int64, c_int64, _P, c_int, _P, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P,
+                _P, _P, c_size_t, _P]),
+    "tai_moe_init_routing": (
+        c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P, _P, _P, c_size_t, _P]),
+    "tai_moe_finalize_routing": (
+        c_int, [_P, c_int, c_int64, c_int64, c_int, _P, _P, _P, _P, c_int, _P, _P, c_int, _P, _P]),
+    "tai_fia_paged_decode_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int]),
+    "tai_fia_paged_decode": (
+        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int,
+                c_float, _P, _P, _P, c_size_t, _P]),
+    "tai_fia_prefill": (
+        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int,
+                c_float, _P, _P, _P]),
+    "tai_fia_mla_decode_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int]),
+    "tai_fia_mla_decode": (
+        c_int, [_P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_float, _P, _P, _P,
+                c_size_t, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def exported_symbols():
+    """Names of every entry point the header declares."""
+    return list(_SIGS)
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "(hipcc --offload-arch=gfx950). The fused npu ops have no other implementation.")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in _SIGS.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+class KernelError(RuntimeError):
+    pass
+
+
+def call(name: str, *args) -> None:
+    """Calls a status-returning entry point; raises RuntimeError with the library's message."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.tai_last_error().decode(errors="replace")
+        raise KernelError(f"{name} failed (status {rc}): {msg}")
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))

@@ -1,0 +1,587 @@
+"""torch.library registration of the torch_npu-style fused ops served by libtai_kernels.so.
+
+Namespaces and schemas follow the ops TorchAir's converters accept:
+  npu::          torch_npu fused ops (converters in
+                 python/torchair/_ge_concrete_graph/ge_converter/custom/*.py)
+  npu_inference:: gating / dequant_swiglu_quant twins
+                 (python/torchair/_contrib/custom_torch_ops/auto_register_custom_torch_ops.py:42-191)
+  air::          npu_fused_infer_attention_score with tensor sequence lengths
+                 (python/torchair/ops/_npu_fused_infer_attention_score.py:14-34)
+Each op has a fake (meta) implementation with the reference's output-shape rules and a
+ROCm (``CUDA`` dispatch key) implementation that checks arguments, allocates outputs with
+the caching allocator and calls the C ABI on the current stream. No CPU implementation is
+registered here: calling these ops on CPU tensors raises.
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import DT_BF16, DT_FP16, DT_FP32, DT_INT32, DT_INT64, DT_INT8, DT_NONE, LAYOUT_KN, LAYOUT_NK
+
+_DT = {
+    torch.uint8: 0, torch.int8: DT_INT8, torch.int16: 2, torch.int32: DT_INT32, torch.int64: DT_INT64,
+    torch.float16: DT_FP16, torch.float32: DT_FP32, torch.bfloat16: DT_BF16,
+}
+_CODE_TO_DTYPE = {v: k for k, v in _DT.items()}
+
+
+def scalar_type_code(v) -> Optional[int]:
+    """ScalarType argument (torch.dtype or its integer code) -> integer code."""
+    if v is None:
+        return None
+    if isinstance(v, torch.dtype):
+        return _DT[v]
+    return int(v)
+
+
+def dtype_of_code(code: int) -> torch.dtype:
+    if code not in _CODE_TO_DTYPE:
+        raise ValueError(f"unsupported ScalarType code {code}")
+    return _CODE_TO_DTYPE[code]
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    return t.to(torch.float32).contiguous()
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _on_gpu(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("npu fused ops run on the ROCm device only; got a tensor on " + str(t.device))
+
+
+LIBS = {
+    "npu": torch.library.Library("npu", "FRAGMENT"),
+    "npu_inference": torch.library.Library("npu_inference", "FRAGMENT"),
+    "air": torch.library.Library("air", "FRAGMENT"),
+}
+
+
+def _define(ns: str, schema: str, fake, cuda, name: Optional[str] = None):
+    lib = LIBS[ns]
+    lib.define(schema)
+    op_name = name or schema.split("(")[0]
+    torch.library.register_fake(f"{ns}::{op_name}", fake, lib=lib)
+    lib.impl(op_name, cuda, "CUDA")
+
+
+# ============================================================================ npu_dynamic_quant
+def _dynamic_quant_fake(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                        dst_type_max=0.0):
+    return (torch.empty(input.shape, dtype=torch.int8, device=input.device),
+            torch.empty(input.shape[:-1], dtype=torch.float32, device=input.device))
+
+
+def _dynamic_quant_cuda(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                        dst_type_max=0.0):
+    """npu_dynamic_quant: symmetric per-token int8 (npu_dynamic_quant.py:8-42)."""
+    _on_gpu(input, smooth_scales, group_index)
+    code = scalar_type_code(dst_type)
+    _check(code in (None, DT_INT8), f"npu_dynamic_quant: dst_type {dst_type} not supported (int8 only)")
+    _check(quant_mode in (None, "pertoken") and math.isclose(dst_type_max or 0.0, 0.0, abs_tol=1e-12),
+           "npu_dynamic_quant: only quant_mode='pertoken' with dst_type_max=0 is supported")
+    _check(input.dtype in (torch.bfloat16, torch.float16, torch.float32),
+           "npu_dynamic_quant: input must be bf16, fp16 or fp32")
+    _check(input.dim() >= 1, "npu_dynamic_quant: input must have at least one dim")
+    x = input.contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    y = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    sm = _f32(smooth_scales)
+    ng = 0
+    gi = None
+    if sm is not None:
+        if group_index is not None:
+            _check(sm.dim() == 2 and sm.shape[1] == cols, "npu_dynamic_quant: smooth_scales must be [G, H] with group_index")
+            gi = group_index.contiguous()
+            _check(gi.dtype in (torch.int32, torch.int64) and gi.numel() == sm.shape[0],
+                   "npu_dynamic_quant: group_index must be int32/int64 with G entries")
+            ng = gi.numel()
+        else:
+            _check(sm.numel() == cols, "npu_dynamic_quant: smooth_scales must have H entries")
+    if rows == 0:
+        return y, scale
+    _lib.call("tai_dynamic_quant", _p(x), _DT[x.dtype], rows, cols, _p(sm), _p(gi),
+              _DT[gi.dtype] if gi is not None else DT_NONE, ng, _p(y), _p(scale), _stream(x))
+    return y, scale
+
+
+_define("npu", "npu_dynamic_quant(Tensor input, *, Tensor? smooth_scales=None, Tensor? group_index=None, "
+               "ScalarType? dst_type=None, str? quant_mode=\"pertoken\", float dst_type_max=0.0) -> (Tensor, Tensor)",
+        _dynamic_quant_fake, _dynamic_quant_cuda)
+
+
+# ============================================================================ npu_dequant_swiglu_quant
+_DSQ_SCHEMA = ("npu_dequant_swiglu_quant(Tensor x, *, Tensor? weight_scale=None, Tensor? activation_scale=None, "
+               "Tensor? bias=None, Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? group_index=None, "
+               "bool activate_left=False, int quant_mode=0, int? dst_type=None, int? round_mode=None, "
+               "int? activate_dim=None, int swiglu_mode=0, float clamp_limit=7.0, float glu_alpha=1.702, "
+               "float glu_bias=1.0) -> (Tensor, Tensor)")
+
+
+def _dsq_fake(x, *, weight_scale=None, activation_scale=None, bias=None, quant_scale=None, quant_offset=None,
+              group_index=None, activate_left=False, quant_mode=0, dst_type=None, round_mode=None, activate_dim=None,
+              swiglu_mode=0, clamp_limit=7.0, glu_alpha=1.702, glu_bias=1.0):
+    """Output shapes of auto_register_custom_torch_ops.py:155-191."""
+    activate_dim = -1 if activate_dim is None else activate_dim
+    sel = activate_dim if activate_dim >= 0 else activate_dim + x.dim()
+    if x.dim() <= 1:
+        raise RuntimeError("x dim should larger than 1")
+    if sel < 0 or sel >= x.dim():
+        raise RuntimeError("activate dim should less than x dim")
+    if x.size(sel) % 2 != 0:
+        raise RuntimeError("x last dim should be even")
+    if quant_mode not in (0, 1):
+        raise RuntimeError("quant_mode only support 0 or 1, but got " + str(quant_mode))
+    y_size = [x.size(i) // 2 if i == sel else x.size(i) for i in range(x.dim())]
+    return (torch.empty(y_size, dtype=torch.int8, device=x.device),
+            torch.empty(y_size[:-1], dtype=torch.float32, device=x.device))
+
+
+def _dsq_cuda(x, *, weight_scale=None, activation_scale=None, bias=None, quant_scale=None, quant_offset=None,
+              group_index=None, activate_left=False, quant_mode=0, dst_type=None, round_mode=None, activate_dim=None,
+              swiglu_mode=0, clamp_limit=7.0, glu_alpha=1.702, glu_bias=1.0):
+    """npu_dequant_swiglu_quant, dynamic mode (npu_dequant_swiglu_quant.py:5-47)."""
+    _on_gpu(x, weight_scale, activation_scale, bias, quant_scale, group_index)
+    y, scale = _dsq_fake(x, activate_dim=activate_dim, quant_mode=quant_mode)
+    _check(activate_dim in (None, -1, x.dim() - 1), "npu_dequant_swiglu_quant: only the last dim can be activated")
+    _check(quant_mode == 1, "npu_dequant_swiglu_quant: only quant_mode=1 (dynamic) is supported")
+    _check(dst_type in (None, 1), "npu_dequant_swiglu_quant: only int8 output (dst_type 1) is supported")
+    _check(round_mode in (None, 0), "npu_dequant_swiglu_quant: only round_mode 0 (rint) is supported")
+    _check(swiglu_mode == 0, "npu_dequant_swiglu_quant: only swiglu_mode 0 is supported")
+    _check(quant_offset is None, "npu_dequant_swiglu_quant: quant_offset (asymmetric) is not supported")
+    _check(x.dtype == torch.int32, "npu_dequant_swiglu_quant: x must be int32")
+    xc = x.contiguous()
+    n2 = xc.shape[-1]
+    n = n2 // 2
+    rows = xc.numel() // n2 if n2 else 0
+    ng = group_index.numel() if group_index is not None else 1
+    ws = _f32(weight_scale)
+    if ws is not None:
+        _check(ws.numel() == ng * n2, "npu_dequant_swiglu_quant: weight_scale must have G*2H entries")
+    act = _f32(activation_scale)
+    if act is not None:
+        _check(act.numel() == rows, "npu_dequant_swiglu_quant: activation_scale must have one entry per row")
+    bi = None
+    bias_dt = DT_NONE
+    if bias is not None:
+        bi = bias.contiguous() if bias.dtype == torch.int32 else _f32(bias)
+        bias_dt = _DT[bi.dtype]
+        _check(bi.numel() == ng * n2, "npu_dequant_swiglu_quant: bias must have G*2H entries")
+    qs = _f32(quant_scale)
+    if qs is not None:
+        _check(qs.numel() == ng * n, "npu_dequant_swiglu_quant: quant_scale must have G*H entries")
+    gi = None
+    if group_index is not None:
+        gi = group_index.contiguous()
+        _check(gi.dtype in (torch.int32, torch.int64), "npu_dequant_swiglu_quant: group_index must be int32/int64")
+    if rows == 0:
+        return y, scale
+    _lib.call("tai_dequant_swiglu_quant", _p(xc), rows, n2, _p(ws), _p(act), _p(bi), bias_dt, _p(qs), _p(gi),
+              _DT[gi.dtype] if gi is not None else DT_NONE, ng, 1 if activate_left else 0, _p(y), _p(scale),
+              _stream(xc))
+    return y, scale
+
+
+_define("npu", _DSQ_SCHEMA, _dsq_fake, _dsq_cuda)
+_define("npu_inference", _DSQ_SCHEMA, _dsq_fake, _dsq_cuda)
+
+
+# ============================================================================ npu_quant_matmul
+def _qmm_out_dtype(output_dtype) -> torch.dtype:
+    code = scalar_type_code(output_dtype)
+    if code is None or code == DT_INT8:
+        return torch.int8
+    return dtype_of_code(code)
+
+
+def _qmm_fake(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None, x1_dtype=None,
+              x2_dtype=None, pertoken_scale_dtype=None, scale_dtype=None, group_sizes=None):
+    shape = list(x1.shape[:-1]) + [x2.shape[-1]]
+    return torch.empty(shape, dtype=_qmm_out_dtype(output_dtype), device=x1.device)
+
+
+def _weight_layout(w: torch.Tensor):
+    """Returns (tensor, layout) with the last two dims either [K,N] row-major or a [N,K] row-major storage."""
+    if w.is_contiguous():
+        return w, LAYOUT_KN
+    wt = w.transpose(-1, -2)
+    if wt.is_contiguous():
+        return wt, LAYOUT_NK
+    return w.contiguous(), LAYOUT_KN
+
+
+def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None, x1_dtype=None,
+              x2_dtype=None, pertoken_scale_dtype=None, scale_dtype=None, group_sizes=None):
+    """npu_quant_matmul W8A8 (quantmatmul.py:63-255)."""
+    _on_gpu(x1, x2, scale, pertoken_scale, bias)
+    _check(x1.dtype == torch.int8 and x2.dtype == torch.int8, "npu_quant_matmul: x1 and x2 must be int8")
+    _check(x2.dim() == 2, "npu_quant_matmul: x2 must be 2-D [K, N]")
+    _check(offset is None, "npu_quant_matmul: offset is not supported")
+    _check(group_sizes is None, "npu_quant_matmul: group_sizes is not supported")
+    out_dtype = _qmm_out_dtype(output_dtype)
+    _check(out_dtype in (torch.int32, torch.bfloat16, torch.float16, torch.float32),
+           "npu_quant_matmul: output_dtype must be int32, bf16, fp16 or fp32 (int8 requantisation is not supported)")
+    k = x1.shape[-1]
+    _check(x2.shape[0] == k, f"npu_quant_matmul: K mismatch {k} vs {x2.shape[0]}")
+    n = x2.shape[1]
+    a = x1.contiguous()
+    m = a.numel() // k if k else 0
+    w, layout = _weight_layout(x2)
+    sc = _f32(scale) if scale is not None else None
+    if sc is not None:
+        _check(scale.dtype != torch.int64, "npu_quant_matmul: packed int64 scales are not supported; pass fp32")
+        _check(sc.numel() in (1, n), "npu_quant_matmul: scale must have 1 or N entries")
+    pts = _f32(pertoken_scale)
+    if pts is not None:
+        _check(pts.numel() == m, "npu_quant_matmul: pertoken_scale must have M entries")
+    bi = None
+    bias_dt = DT_NONE
+    if bias is not None:
+        bi = bias.contiguous() if bias.dtype == torch.int32 else _f32(bias)
+        bias_dt = _DT[bi.dtype]
+        _check(bi.numel() == n, "npu_quant_matmul: bias must have N entries")
+    out = torch.empty(list(x1.shape[:-1]) + [n], dtype=out_dtype, device=x1.device)
+    if m == 0 or n == 0:
+        return out
+    if k == 0:
+        return out.zero_()
+    _lib.call("tai_quant_matmul", _p(a), _p(w), m, k, n, layout, _p(sc), sc.numel() if sc is not None else 0,
+              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _stream(a))
+    return out
+
+
+_define("npu", "npu_quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None, "
+               "Tensor? pertoken_scale=None, Tensor? bias=None, ScalarType? output_dtype=None, "
+               "ScalarType? x1_dtype=None, ScalarType? x2_dtype=None, ScalarType? pertoken_scale_dtype=None, "
+               "ScalarType? scale_dtype=None, int[]? group_sizes=None) -> Tensor",
+        _qmm_fake, _qmm_cuda)
+
+
+# ============================================================================ npu_grouped_matmul
+_GMM_TAIL = ("*, Tensor[]? bias=None, Tensor[]? scale=None, Tensor[]? offset=None, Tensor[]? antiquant_scale=None, "
+             "Tensor[]? antiquant_offset=None, Tensor[]? per_token_scale=None, {gl}, "
+             "Tensor[]? activation_input=None, Tensor[]? activation_quant_scale=None, "
+             "Tensor[]? activation_quant_offset=None, int? split_item=0, int? group_type=None, "
+             "int? group_list_type=0, int? act_type=0, int[]? tuning_config=None, ScalarType? output_dtype=None"
+             ") -> Tensor[]")
+
+
+def _gmm_out_dtype(x, output_dtype):
+    code = scalar_type_code(output_dtype)
+    if code is None:
+        return torch.int8 if x[0].dtype == torch.int8 else x[0].dtype
+    return dtype_of_code(code)
+
+
+def _gmm_fake(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
+              per_token_scale=None, group_list=None, activation_input=None, activation_quant_scale=None,
+              activation_quant_offset=None, split_item=0, group_type=None, group_list_type=0, act_type=0,
+              tuning_config=None, output_dtype=None):
+    n = weight[0].shape[-1]
+    m = x[0].shape[0]
+    return [torch.empty([m, n], dtype=_gmm_out_dtype(x, output_dtype), device=x[0].device)]
+
+
+def _gmm_cuda(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
+              per_token_scale=None, group_list=None, activation_input=None, activation_quant_scale=None,
+              activation_quant_offset=None, split_item=0, group_type=None, group_list_type=0, act_type=0,
+              tuning_config=None, output_dtype=None):
+    """npu_grouped_matmul int8 path, split_item 2/3, group_type 0 (grouped_matmul.py:210-365)."""
+    _check(len(x) == 1, "npu_grouped_matmul: a single x tensor (split_item 2/3) is supported")
+    _check(split_item in (2, 3), "npu_grouped_matmul: split_item must be 2 or 3")
+    _check(group_type in (None, 0), "npu_grouped_matmul: only group_type 0 (groups along M) is supported")
+    _check(group_list is not None, "npu_grouped_matmul: group_list is required")
+    _check(not (offset or antiquant_scale or antiquant_offset or activation_input or activation_quant_scale
+                or activation_quant_offset), "npu_grouped_matmul: offset/antiquant/activation inputs are not supported")
+    _check(act_type in (None, 0), "npu_grouped_matmul: act_type must be 0")
+    _check(group_list_type in (0, 1), "npu_grouped_matmul: group_list_type must be 0 (cumsum) or 1 (count)")
+    xt = x[0]
+    _on_gpu(xt, *weight)
+    _check(xt.dtype == torch.int8, "npu_grouped_matmul: only the int8 (W8A8) path is supported")
+    if len(weight) == 1:
+        w3 = weight[0]
+        _check(w3.dim() == 3, "npu_grouped_matmul: stacked weight must be [E, K, N]")
+    else:
+        w3 = torch.stack(list(weight))
+    _check(w3.dtype == torch.int8, "npu_grouped_matmul: weight must be int8")
+    e, k, n = w3.shape
+    _check(xt.dim() == 2 and xt.shape[1] == k, "npu_grouped_matmul: x must be [M, K] with K matching the weight")
+    out_dtype = _gmm_out_dtype(x, output_dtype)
+    _check(out_dtype in (torch.int32, torch.bfloat16, torch.float16, torch.float32),
+           "npu_grouped_matmul: output_dtype must be int32, bf16, fp16 or fp32 for int8 inputs")
+    if isinstance(group_list, torch.Tensor):
+        gl = group_list.to(torch.int64).contiguous()
+    else:
+        gl = torch.tensor(list(group_list), dtype=torch.int64, device=xt.device)
+    _check(gl.numel() == e, f"npu_grouped_matmul: group_list has {gl.numel()} entries, weight has {e} groups")
+    if w3.is_contiguous():
+        wl, layout = w3, LAYOUT_KN
+    elif w3.transpose(1, 2).is_contiguous():
+        wl, layout = w3.transpose(1, 2), LAYOUT_NK
+    else:
+        wl, layout = w3.contiguous(), LAYOUT_KN
+    sc = None
+    if scale:
+        sc = _f32(scale[0] if len(scale) == 1 else torch.stack(list(scale)))
+        _check(scale[0].dtype != torch.int64, "npu_grouped_matmul: packed int64 scales are not supported; pass fp32")
+        _check(sc.numel() == e * n, "npu_grouped_matmul: scale must be [E, N]")
+    pts = _f32(per_token_scale[0]) if per_token_scale else None
+    m = xt.shape[0]
+    if pts is not None:
+        _check(pts.numel() == m, "npu_grouped_matmul: per_token_scale must have M entries")
+    bi = None
+    bias_dt = DT_NONE
+    if bias:
+        b = bias[0] if len(bias) == 1 else torch.stack(list(bias))
+        bi = b.contiguous() if b.dtype == torch.int32 else _f32(b)
+        bias_dt = _DT[bi.dtype]
+        _check(bi.numel() == e * n, "npu_grouped_matmul: bias must be [E, N]")
+    _check(out_dtype == torch.int32 or sc is not None, "npu_grouped_matmul: floating output needs scale")
+    xc = xt.contiguous()
+    out = torch.empty([m, n], dtype=out_dtype, device=xt.device)
+    if m == 0 or n == 0:
+        return [out]
+    ws_bytes = _lib.query("tai_grouped_matmul_workspace_size", m, n, e)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xt.device)
+    _lib.call("tai_grouped_matmul", _p(xc), _p(wl), m, k, n, e, layout, _p(gl), int(group_list_type), _p(sc),
+              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _p(ws), ws_bytes, _stream(xc))
+    return [out]
+
+
+_define("npu", "npu_grouped_matmul(Tensor[] x, Tensor[] weight, " + _GMM_TAIL.format(gl="Tensor? group_list=None"),
+        _gmm_fake, _gmm_cuda)
+LIBS["npu"].define("npu_grouped_matmul.List(Tensor[] x, Tensor[] weight, " +
+                   _GMM_TAIL.format(gl="int[]? group_list=None"))
+torch.library.register_fake("npu::npu_grouped_matmul.List", _gmm_fake, lib=LIBS["npu"])
+LIBS["npu"].impl("npu_grouped_matmul.List", _gmm_cuda, "CUDA")
+
+
+# ============================================================================ npu_moe_gating_top_k
+_GATE_SCHEMA = ("npu_moe_gating_top_k(Tensor x, int k, *, Tensor? bias=None, int k_group=1, int group_count=1, "
+                "int group_select_mode=0, int renorm=0, int norm_type=0, bool out_flag=False, "
+                "float routed_scaling_factor=1.0, float eps=1e-20) -> (Tensor, Tensor, Tensor)")
+
+
+def _gate_fake(x, k, *, bias=None, k_group=1, group_count=1, group_select_mode=0, renorm=0, norm_type=0,
+               out_flag=False, routed_scaling_factor=1.0, eps=1e-20):
+    """Output shapes of auto_register_custom_torch_ops.py:103-114."""
+    return (x.new_empty((x.size(0), k), dtype=x.dtype), x.new_empty((x.size(0), k), dtype=torch.int32),
+            x.new_empty((x.size(0), x.size(1)), dtype=torch.float32))
+
+
+def _gate_cuda(x, k, *, bias=None, k_group=1, group_count=1, group_select_mode=0, renorm=0, norm_type=0,
+               out_flag=False, routed_scaling_factor=1.0, eps=1e-20):
+    """npu_moe_gating_top_k (npu_moe_gating_top_k.py:4-22)."""
+    _on_gpu(x, bias)
+    _check(x.dim() == 2, "npu_moe_gating_top_k: x must be [T, E]")
+    y, idx, out = _gate_fake(x, k)
+    xc = x.contiguous()
+    bc = bias.contiguous() if bias is not None else None
+    if bc is not None:
+        _check(bc.numel() == x.shape[1], "npu_moe_gating_top_k: bias must have E entries")
+    if x.shape[0] == 0:
+        return y, idx, out
+    _lib.call("tai_moe_gating_top_k", _p(xc), _DT[xc.dtype], xc.shape[0], xc.shape[1], int(k), _p(bc),
+              _DT[bc.dtype] if bc is not None else DT_NONE, int(k_group), int(group_count), int(group_select_mode),
+              int(renorm), int(norm_type), 1 if out_flag else 0, float(routed_scaling_factor), float(eps), _p(y),
+              _p(idx), _p(out), _stream(xc))
+    return y, idx, out
+
+
+_define("npu", _GATE_SCHEMA, _gate_fake, _gate_cuda)
+_define("npu_inference", _GATE_SCHEMA, _gate_fake, _gate_cuda)
+
+
+# ============================================================================ npu_moe_init_routing(_v2)
+LEGACY_ROUTING_EXPERT_BINS = 1024  # legacy init_routing carries no expert count: ids must be < 1024
+
+
+def _init_routing_fake(x, row_idx, expert_idx, active_num):
+    t, k = expert_idx.shape
+    rows = min(t, active_num) * k if active_num >= 0 else t * k
+    return (x.new_empty((rows, x.shape[1])), x.new_empty((t * k,), dtype=torch.int32),
+            x.new_empty((t * k,), dtype=torch.int32))
+
+
+def _init_routing_cuda(x, row_idx, expert_idx, active_num):
+    """npu_moe_init_routing (moe_init_routing.py:10-21)."""
+    _on_gpu(x, row_idx, expert_idx)
+    _check(x.dim() == 2 and expert_idx.dim() == 2 and row_idx.shape == expert_idx.shape,
+           "npu_moe_init_routing: x [T,H], row_idx and expert_idx [T,k]")
+    _check(row_idx.dtype == torch.int32 and expert_idx.dtype == torch.int32,
+           "npu_moe_init_routing: row_idx and expert_idx must be int32")
+    ex, ri, ei = _init_routing_fake(x, row_idx, expert_idx, active_num)
+    t, k = expert_idx.shape
+    if t == 0:
+        return ex, ri, ei
+    xc, rc, ec = x.contiguous(), row_idx.contiguous(), expert_idx.contiguous()
+    bins = LEGACY_ROUTING_EXPERT_BINS
+    ws_bytes = _lib.query("tai_moe_init_routing_workspace_size", t, k, bins)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    _lib.call("tai_moe_init_routing", _p(xc), xc.element_size(), t, xc.shape[1], _p(rc), _p(ec), k, bins,
+              ex.shape[0], _p(ex), _p(ri), _p(ei), _p(ws), ws_bytes, _stream(xc))
+    return ex, ri, ei
+
+
+_define("npu", "npu_moe_init_routing(Tensor x, Tensor row_idx, Tensor expert_idx, int active_num) "
+               "-> (Tensor, Tensor, Tensor)", _init_routing_fake, _init_routing_cuda)
+
+
+def _v2_expert_range(expert_num, active_expert_range):
+    if active_expert_range:
+        lo, hi = int(active_expert_range[0]), int(active_expert_range[1])
+    else:
+        lo, hi = 0, int(expert_num)
+    return lo, hi
+
+
+def _init_routing_v2_fake(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1,
+                          expert_num=-1, drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False,
+                          quant_mode=-1, active_expert_range=(), row_idx_type=0):
+    t, k = expert_idx.shape
+    n = t * k
+    rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
+    lo, hi = _v2_expert_range(expert_num, active_expert_range)
+    return (x.new_empty((rows, x.shape[1])), x.new_empty((n,), dtype=torch.int32),
+            x.new_empty((max(hi - lo, 0),), dtype=torch.int64),
+            x.new_empty((rows if scale is not None else 0,), dtype=torch.float32))
+
+
+def _init_routing_v2_cuda(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1,
+                          expert_num=-1, drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False,
+                          quant_mode=-1, active_expert_range=(), row_idx_type=0):
+    """npu_moe_init_routing_v2, dropless (npu_moe_init_routing_v2.py:41-91)."""
+    _on_gpu(x, expert_idx, scale)
+    _check(drop_pad_mode == 0, "npu_moe_init_routing_v2: only drop_pad_mode 0 (dropless) is supported")
+    _check(quant_mode == -1, "npu_moe_init_routing_v2: only quant_mode -1 (no fused quant) is supported")
+    _check(offset is None, "npu_moe_init_routing_v2: offset is not supported")
+    _check(expert_tokens_num_type in (0, 1), "npu_moe_init_routing_v2: expert_tokens_num_type must be 0 or 1")
+    _check(x.dim() == 2 and expert_idx.dim() == 2 and expert_idx.shape[0] == x.shape[0],
+           "npu_moe_init_routing_v2: x [T,H] and expert_idx [T,k]")
+    _check(expert_idx.dtype == torch.int32, "npu_moe_init_routing_v2: expert_idx must be int32")
+    lo, hi = _v2_expert_range(expert_num, active_expert_range)
+    _check(hi > lo >= 0, "npu_moe_init_routing_v2: expert_num or active_expert_range is required")
+    ex, ri, tok, es = _init_routing_v2_fake(x, expert_idx, scale=scale, active_num=active_num, expert_num=expert_num,
+                                            active_expert_range=active_expert_range)
+    t, k = expert_idx.shape
+    if t == 0:
+        return ex, ri, tok.zero_(), es
+    xc, ec = x.contiguous(), expert_idx.contiguous()
+    sc = _f32(scale)
+    if sc is not None:
+        _check(sc.numel() == t, "npu_moe_init_routing_v2: scale must have T entries")
+    ws_bytes = _lib.query("tai_moe_init_routing_workspace_size", t, k, hi - lo)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    _lib.call("tai_moe_init_routing_v2", _p(xc), xc.element_size(), t, xc.shape[1], _p(ec), k, _p(sc), ex.shape[0],
+              lo, hi, int(expert_tokens_num_type), int(row_idx_type), _p(ex), _p(ri), _p(tok),
+              _p(es) if sc is not None else None, _p(ws), ws_bytes, _stream(xc))
+    return ex, ri, tok, es
+
+
+_define("npu", "npu_moe_init_routing_v2(Tensor x, Tensor expert_idx, *, Tensor? scale=None, Tensor? offset=None, "
+               "int active_num=-1, int expert_capacity=-1, int expert_num=-1, int drop_pad_mode=0, "
+               "int expert_tokens_num_type=0, bool expert_tokens_num_flag=False, int quant_mode=-1, "
+               "int[] active_expert_range=[], int row_idx_type=0) -> (Tensor, Tensor, Tensor, Tensor)",
+        _init_routing_v2_fake, _init_routing_v2_cuda)
+
+
+# ============================================================================ npu_moe_finalize_routing
+def _finalize_dims(expanded, skip1, scales, src_to_dst):
+    if scales is not None:
+        t, k = scales.shape
+    elif skip1 is not None:
+        t = skip1.shape[0]
+        k = src_to_dst.numel() // max(t, 1)
+    else:
+        raise RuntimeError("npu_moe_finalize_routing: scales or skip1 is needed to know the token count")
+    return t, k
+
+
+def _finalize_fake(expanded_permuted_rows, skip1, skip2, bias, scales, expanded_src_to_dst_row,
+                   export_for_source_row, drop_pad_mode=0):
+    t, _ = _finalize_dims(expanded_permuted_rows, skip1, scales, expanded_src_to_dst_row)
+    return expanded_permuted_rows.new_empty((t, expanded_permuted_rows.shape[-1]))
+
+
+def _finalize_cuda(expanded_permuted_rows, skip1, skip2, bias, scales, expanded_src_to_dst_row,
+                   export_for_source_row, drop_pad_mode=0):
+    """npu_moe_finalize_routing (npu_moe_finalize_routing.py:21-41)."""
+    ex = expanded_permuted_rows
+    _on_gpu(ex, skip1, skip2, bias, scales, expanded_src_to_dst_row, export_for_source_row)
+    mode = 0 if drop_pad_mode is None else int(drop_pad_mode)
+    _check(mode in (0, 2), "npu_moe_finalize_routing: drop_pad_mode must be 0 (k-major slots) or 2 (token-major)")
+    t, k = _finalize_dims(ex, skip1, scales, expanded_src_to_dst_row)
+    h = ex.shape[-1]
+    y = ex.new_empty((t, h))
+    dt = ex.dtype
+    for name, tt in (("skip1", skip1), ("skip2", skip2), ("bias", bias)):
+        if tt is not None:
+            _check(tt.dtype == dt and tt.shape[-1] == h, f"npu_moe_finalize_routing: {name} must match the rows' dtype/H")
+    _check(expanded_src_to_dst_row.dtype == torch.int32 and expanded_src_to_dst_row.numel() == t * k,
+           "npu_moe_finalize_routing: expanded_src_to_dst_row must be int32 with T*k entries")
+    if bias is not None:
+        _check(export_for_source_row is not None, "npu_moe_finalize_routing: bias needs export_for_source_row")
+    if t == 0:
+        return y
+    c = lambda a: None if a is None else a.contiguous()  # noqa: E731
+    exc, s1, s2, bi, sc, s2d, efs = map(c, (ex, skip1, skip2, bias, scales, expanded_src_to_dst_row,
+                                            export_for_source_row))
+    _lib.call("tai_moe_finalize_routing", _p(exc), _DT[dt], t, h, k, _p(s1), _p(s2), _p(bi), _p(sc),
+              _DT[sc.dtype] if sc is not None else DT_NONE, _p(s2d), _p(efs), mode, _p(y), _stream(exc))
+    return y
+
+
+_define("npu", "npu_moe_finalize_routing(Tensor expanded_permuted_rows, Tensor? skip1, Tensor? skip2, Tensor? bias, "
+               "Tensor? scales, Tensor expanded_src_to_dst_row, Tensor? export_for_source_row, "
+               "int? drop_pad_mode=0) -> Tensor", _finalize_fake, _finalize_cuda)
+
+
+# ============================================================================ fused_infer_attention_score
+from . import _fia  # noqa: E402  (attention dispatch lives in its own module)
+
+_FIA_ARGS = ("Tensor query, Tensor key, Tensor value, *, Tensor? pse_shift=None, Tensor? atten_mask=None, "
+             "{seq} actual_seq_lengths=None, {seq} actual_seq_lengths_kv=None, Tensor? dequant_scale1=None, "
+             "Tensor? quant_scale1=None, Tensor? dequant_scale2=None, Tensor? quant_scale2=None, "
+             "Tensor? quant_offset2=None, Tensor? antiquant_scale=None, Tensor? antiquant_offset=None, "
+             "{bt_first}"
+             "Tensor? key_antiquant_scale=None, Tensor? key_antiquant_offset=None, "
+             "Tensor? value_antiquant_scale=None, Tensor? value_antiquant_offset=None, {bt_second}"
+             "Tensor? key_shared_prefix=None, Tensor? value_shared_prefix=None, {seq} actual_shared_prefix_len=None, "
+             "Tensor? query_rope=None, Tensor? key_rope=None, Tensor? key_rope_antiquant_scale=None, "
+             "int num_heads=1, float scale=1.0, int pre_tokens=2147483647, int next_tokens=2147483647, "
+             "str input_layout=\"BSH\", int num_key_value_heads=0, int sparse_mode=0, int inner_precise=0, "
+             "int block_size=0, int antiquant_mode=0, {tail}) -> (Tensor, Tensor)")
+_BT = "Tensor? block_table=None, Tensor? query_padding_size=None, Tensor? kv_padding_size=None, "
+
+# torch_npu order: block_table after antiquant_offset; lse flag before the key/value antiquant modes.
+_define("npu", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
+    seq="SymInt[]?", bt_first=_BT, bt_second="",
+    tail="bool softmax_lse_flag=False, int key_antiquant_mode=0, int value_antiquant_mode=0"),
+    _fia.fia_fake, _fia.fia_cuda)
+# air:: (python/torchair/ops/_npu_fused_infer_attention_score.py:14-34): tensor sequence lengths,
+# block_table after the value antiquant tensors, lse flag last.
+_define("air", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
+    seq="Tensor?", bt_first="", bt_second=_BT,
+    tail="int key_antiquant_mode=0, int value_antiquant_mode=0, bool softmax_lse_flag=False"),
+    _fia.fia_fake, _fia.fia_cuda)

@@ -1,0 +1,57 @@
+"""Converters for the fused ops on the hot path.
+
+Each mirrors the reference converter of the same op (file:line below) but lowers the FX
+node onto the ``torch.library`` op served by libtai_kernels.so instead of a GE node, so the
+lowered graph calls the HIP kernels directly and can be captured into a hipGraph.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _ops_impl  # noqa: F401  (defines the ops)
+from .converter import Support, declare_supported, register_fx_node_ge_converter
+
+npu = torch.ops.npu
+air = torch.ops.air
+npu_inference = torch.ops.npu_inference
+
+
+def _identity(op):
+    def convert(*args, meta_outputs=None, **kwargs):
+        return op(*args, **kwargs)
+    convert.__name__ = f"convert_{op}"
+    return convert
+
+
+# python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dynamic_quant.py:4-8
+declare_supported([
+    Support(torch.empty(64, 16384, dtype=torch.float16)),
+    Support(torch.empty(64, 16384, dtype=torch.bfloat16)),
+])(register_fx_node_ge_converter(npu.npu_dynamic_quant.default)(_identity(npu.npu_dynamic_quant.default)))
+# .../custom/npu_dequant_swiglu_quant.py:5
+register_fx_node_ge_converter(npu.npu_dequant_swiglu_quant.default)(_identity(npu.npu_dequant_swiglu_quant.default))
+register_fx_node_ge_converter(npu_inference.npu_dequant_swiglu_quant.default)(
+    _identity(npu_inference.npu_dequant_swiglu_quant.default))
+# .../custom/quantmatmul.py:63
+register_fx_node_ge_converter(npu.npu_quant_matmul.default)(_identity(npu.npu_quant_matmul.default))
+# .../custom/grouped_matmul.py:364-365
+register_fx_node_ge_converter(npu.npu_grouped_matmul.default)(_identity(npu.npu_grouped_matmul.default))
+register_fx_node_ge_converter(npu.npu_grouped_matmul.List)(_identity(npu.npu_grouped_matmul.List))
+# .../custom/npu_moe_gating_top_k.py:4
+register_fx_node_ge_converter(npu.npu_moe_gating_top_k.default)(_identity(npu.npu_moe_gating_top_k.default))
+register_fx_node_ge_converter(npu_inference.npu_moe_gating_top_k.default)(
+    _identity(npu_inference.npu_moe_gating_top_k.default))
+# .../custom/moe_init_routing.py:4-10
+declare_supported([
+    Support(torch.empty(3, 4), torch.empty(3, 2, dtype=torch.int32), torch.empty(3, 2, dtype=torch.int32),
+            active_num=3),
+])(register_fx_node_ge_converter(npu.npu_moe_init_routing.default)(_identity(npu.npu_moe_init_routing.default)))
+# .../custom/npu_moe_init_routing_v2.py:41
+register_fx_node_ge_converter(npu.npu_moe_init_routing_v2.default)(_identity(npu.npu_moe_init_routing_v2.default))
+# .../custom/npu_moe_finalize_routing.py:4-21
+register_fx_node_ge_converter(npu.npu_moe_finalize_routing.default)(_identity(npu.npu_moe_finalize_routing.default))
+# .../custom/fused_infer_attention_score.py:4 and python/torchair/ops/_npu_fused_infer_attention_score.py:46-58
+register_fx_node_ge_converter(npu.npu_fused_infer_attention_score.default)(
+    _identity(npu.npu_fused_infer_attention_score.default))
+register_fx_node_ge_converter(air.npu_fused_infer_attention_score.default)(
+    _identity(air.npu_fused_infer_attention_score.default))

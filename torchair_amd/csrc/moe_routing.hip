@@ -1,0 +1,515 @@
+// MoE routing on one GPU: npu_moe_gating_top_k, npu_moe_init_routing(_v2) and
+// npu_moe_finalize_routing - the single-GPU share of expert dispatch/combine.
+//
+// gating_top_k : one wave per token row; scores staged in LDS, group scores and the
+//                iterative arg-max run with wave shuffles. Sigmoid/softmax are evaluated in
+//                fp64 and rounded once to fp32 so the expert choice is reproducible.
+// init_routing : stable counting sort of the t*k routing slots by expert, in four launches
+//                (chunk histograms -> per-expert scan -> in-chunk ranks -> row gather).
+//                Every kernel writes all of its outputs, so no memset is needed and the
+//                sequence may be captured into a hipGraph.
+// finalize     : one workgroup per token row, fp32 accumulation of the k weighted rows.
+#include "common.h"
+
+namespace tai {
+namespace {
+
+// ============================================================================ gating top-k
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxGroups = 64;
+
+struct GateArgs {
+  const void* x;
+  int x_dt;
+  int64_t t, e;
+  int k;
+  const void* bias;
+  int bias_dt;
+  int k_group, group_count, group_select_mode, norm_type, out_flag;
+  float rsf, eps;
+  void* y;
+  int32_t* idx;
+  float* out;
+};
+
+// Larger (value, lower index) wins.
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// 4 waves per workgroup, one row per wave.
+__global__ __launch_bounds__(256) void gating_topk_kernel(GateArgs a) {
+  __shared__ float s_sc[4][kMaxExperts];   // normalised scores s
+  __shared__ float s_sb[4][kMaxExperts];   // selection scores s + bias
+  __shared__ float s_gs[4][kMaxGroups];    // group scores
+  __shared__ int s_keep[4][kMaxGroups];
+  __shared__ float s_selw[4][32];
+  __shared__ int s_seli[4][32];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  const bool valid = row < a.t;
+  const int E = static_cast<int>(a.e);
+  float* sc = s_sc[w];
+  float* sb = s_sb[w];
+
+  if (valid) {
+    if (a.norm_type == 1) {
+      for (int j = lane; j < E; j += 64) {
+        double xv = static_cast<double>(load_as_f32(a.x, a.x_dt, row * E + j));
+        sc[j] = static_cast<float>(1.0 / (1.0 + exp(-xv)));
+      }
+    } else {
+      float m = -INFINITY;
+      for (int j = lane; j < E; j += 64) m = fmaxf(m, load_as_f32(a.x, a.x_dt, row * E + j));
+      m = wave_max(m);
+      double sum = 0.0;
+      for (int j = lane; j < E; j += 64) sum += exp(static_cast<double>(load_as_f32(a.x, a.x_dt, row * E + j)) - m);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      for (int j = lane; j < E; j += 64) {
+        double ev = exp(static_cast<double>(load_as_f32(a.x, a.x_dt, row * E + j)) - m);
+        sc[j] = static_cast<float>(ev / sum);
+      }
+    }
+    for (int j = lane; j < E; j += 64) {
+      float v = sc[j];
+      if (a.bias) v = v + load_as_f32(a.bias, a.bias_dt, j);
+      sb[j] = v;
+    }
+  }
+  __syncthreads();
+
+  const int G = a.group_count;
+  const int gsz = E / G;
+  if (G > 1) {
+    if (valid) {
+      for (int g = lane; g < G; g += 64) {
+        float b1 = -INFINITY, b2 = -INFINITY;
+        for (int j = g * gsz; j < (g + 1) * gsz; ++j) {
+          float v = sb[j];
+          if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
+        }
+        s_gs[w][g] = (a.group_select_mode == 1 && gsz > 1) ? b1 + b2 : b1;
+      }
+    }
+    __syncthreads();
+    if (valid) {
+      for (int g = lane; g < G; g += 64) {
+        const float v = s_gs[w][g];
+        int rank = 0;
+        for (int h = 0; h < G; ++h) rank += better(s_gs[w][h], h, v, g) ? 1 : 0;
+        s_keep[w][g] = rank < a.k_group;
+      }
+    }
+    __syncthreads();
+    if (valid) {
+      for (int j = lane; j < E; j += 64)
+        if (!s_keep[w][j / gsz]) sb[j] = -INFINITY;
+    }
+    __syncthreads();
+  }
+
+  // k rounds of arg-max: larger score wins, equal scores go to the lower expert id.
+  float wsum = 0.0f;
+  for (int r = 0; r < a.k; ++r) {
+    float bv = -INFINITY;
+    int bi = kMaxExperts;
+    if (valid) {
+      for (int j = lane; j < E; j += 64) {
+        float v = sb[j];
+        if (better(v, j, bv, bi)) { bv = v; bi = j; }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      float ov = __shfl_xor(bv, o, 64);
+      int oi = __shfl_xor(bi, o, 64);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    __syncthreads();
+    if (valid && lane == 0) {
+      sb[bi] = -INFINITY;
+      s_seli[w][r] = bi;
+      s_selw[w][r] = sc[bi];
+    }
+    __syncthreads();
+    if (valid) wsum = wsum + s_selw[w][r];
+  }
+  if (!valid) return;
+  if (lane < a.k) {
+    float v = s_selw[w][lane];
+    if (a.norm_type == 1) v = v / (wsum + a.eps);
+    v = v * a.rsf;
+    store_from_f32(a.y, a.x_dt, row * a.k + lane, v);
+    a.idx[row * a.k + lane] = s_seli[w][lane];
+  }
+  if (a.out_flag && a.out)
+    for (int j = lane; j < E; j += 64) a.out[row * E + j] = sc[j];
+}
+
+// ============================================================================ init routing
+constexpr int kChunk = 256;  // routing slots per chunk (one per thread)
+
+struct RouteWs {
+  int32_t* hist;      // [bins][chunks]: counts, then exclusive destination offsets
+  int32_t* dst2src;   // [n] source slot of each destination row
+  int32_t* total;     // [1] rows that fall in the expert range
+};
+
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+inline RouteWs carve_route_ws(void* ws, int64_t n, int64_t bins) {
+  const int64_t chunks = cdiv(n, kChunk);
+  char* p = static_cast<char*>(ws);
+  RouteWs r;
+  r.hist = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * bins * chunks);
+  r.dst2src = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * n);
+  r.total = reinterpret_cast<int32_t*>(p);
+  return r;
+}
+
+inline size_t route_ws_bytes(int64_t n, int64_t bins) {
+  const int64_t chunks = cdiv(n, kChunk);
+  return align256(sizeof(int32_t) * bins * chunks) + align256(sizeof(int32_t) * n) + 256;
+}
+
+// K1: per-chunk histogram over experts in [e0, e0 + bins).
+__global__ __launch_bounds__(kChunk) void route_hist_kernel(const int32_t* __restrict__ eidx, int64_t n,
+                                                            int e0, int bins, int32_t* __restrict__ hist) {
+  extern __shared__ int32_t h[];
+  const int64_t chunks = gridDim.x;
+  for (int b = threadIdx.x; b < bins; b += blockDim.x) h[b] = 0;
+  __syncthreads();
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+  if (p < n) {
+    const int e = eidx[p] - e0;
+    if (e >= 0 && e < bins) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < bins; b += blockDim.x) hist[static_cast<int64_t>(b) * chunks + blockIdx.x] = h[b];
+}
+
+// K2: one workgroup. Turns counts into exclusive destination offsets (expert-major,
+// chunk-minor) and writes the per-expert token counts / cumsum.
+__global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ hist, int64_t chunks, int bins,
+                                                          int64_t* __restrict__ tokens, int tokens_cumsum,
+                                                          int32_t* __restrict__ total) {
+  extern __shared__ int32_t tot[];  // [bins] then scan scratch
+  for (int b = threadIdx.x; b < bins; b += blockDim.x) {
+    int32_t s = 0;
+    int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
+    for (int64_t c = 0; c < chunks; ++c) s += hb[c];
+    tot[b] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // bins <= 1024: a serial scan is a few microseconds at most
+    int32_t run = 0;
+    for (int b = 0; b < bins; ++b) {
+      int32_t c = tot[b];
+      tot[bins + b] = run;
+      run += c;
+    }
+    *total = run;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < bins; b += blockDim.x) {
+    int32_t run = tot[bins + b];
+    int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
+    for (int64_t c = 0; c < chunks; ++c) {
+      int32_t v = hb[c];
+      hb[c] = run;
+      run += v;
+    }
+    if (tokens) tokens[b] = tokens_cumsum ? static_cast<int64_t>(run) : static_cast<int64_t>(tot[b]);
+  }
+}
+
+// K3: stable in-chunk rank -> destination row of every slot.
+// mode 0 (v2, row_idx_type 0): row_idx[p] = dst or -1.
+// mode 1 (v2, row_idx_type 1): row_idx[dst] = p (tail filled by the gather kernel).
+// mode 2 (legacy): row_idx[legacy_row[p]] = dst; eout[dst] = expert.
+__global__ __launch_bounds__(kChunk) void route_place_kernel(const int32_t* __restrict__ eidx, int64_t n, int e0,
+                                                             int bins, const int32_t* __restrict__ hist,
+                                                             int32_t* __restrict__ dst2src, int mode,
+                                                             int32_t* __restrict__ row_idx,
+                                                             const int32_t* __restrict__ legacy_row,
+                                                             int32_t* __restrict__ eout) {
+  __shared__ int32_t se[kChunk];
+  const int64_t chunks = gridDim.x;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+  int e = -1;
+  if (p < n) {
+    e = eidx[p] - e0;
+    if (e < 0 || e >= bins) e = -1;
+  }
+  se[threadIdx.x] = e;
+  __syncthreads();
+  if (p >= n) return;
+  if (e < 0) {
+    if (mode == 0) row_idx[p] = -1;
+    return;
+  }
+  int rank = 0;
+  for (int i = 0; i < static_cast<int>(threadIdx.x); ++i) rank += (se[i] == e);
+  const int32_t dst = hist[static_cast<int64_t>(e) * chunks + blockIdx.x] + rank;
+  dst2src[dst] = static_cast<int32_t>(p);
+  if (mode == 0) row_idx[p] = dst;
+  else if (mode == 1) row_idx[dst] = static_cast<int32_t>(p);
+  else {
+    row_idx[legacy_row[p]] = dst;
+    eout[dst] = e + e0;
+  }
+}
+
+// K4: expanded_x[i] = x[src(i) / k] (legacy: x[legacy_row[src] % t]); one wave per row.
+__global__ __launch_bounds__(256) void route_gather_kernel(const void* __restrict__ x, int64_t row_bytes, int64_t t, int k,
+                                                           const int32_t* __restrict__ dst2src, const int32_t* __restrict__ total,
+                                                           int64_t active_rows, int64_t n, void* __restrict__ ex,
+                                                           const float* __restrict__ scale, float* __restrict__ escale,
+                                                           int tail_mode, int32_t* __restrict__ row_idx,
+                                                           const int32_t* __restrict__ legacy_row) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (i >= n) return;
+  const int32_t valid = *total;
+  if (tail_mode == 1 && i >= valid && lane == 0) row_idx[i] = -1;
+  if (i >= active_rows) return;
+  char* dst = static_cast<char*>(ex) + i * row_bytes;
+  if (i >= valid) {  // rows past the routed total are zero
+    if ((row_bytes & 15) == 0) {
+      for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16) *reinterpret_cast<uint4*>(dst + o) = make_uint4(0, 0, 0, 0);
+    } else {
+      for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = 0;
+    }
+    if (escale && lane == 0) escale[i] = 0.0f;
+    return;
+  }
+  const int32_t p = dst2src[i];
+  const int64_t src_row = legacy_row ? static_cast<int64_t>(legacy_row[p]) % t : p / k;
+  const char* src = static_cast<const char*>(x) + src_row * row_bytes;
+  if ((row_bytes & 15) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ex)) & 15) == 0) {
+    for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
+      *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
+  } else {
+    for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src[o];
+  }
+  if (escale && lane == 0) escale[i] = scale[src_row];
+}
+
+// ============================================================================ finalize
+struct FinArgs {
+  const void* ex;
+  int dt;
+  int64_t t, h;
+  int k;
+  const void* skip1;
+  const void* skip2;
+  const void* bias;
+  const void* scales;
+  int scales_dt;
+  const int32_t* s2d;
+  const int32_t* expert;
+  int mode;
+  void* y;
+};
+
+__device__ __forceinline__ void load8_bf16(const void* base, int64_t off, float (&v)[8]) {
+  uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+  uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+    v[2 * i + 1] = bf16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
+// bf16 rows, h % 8 == 0: 16-byte loads.
+__global__ __launch_bounds__(256) void finalize_bf16_kernel(FinArgs a) {
+  const int64_t t = blockIdx.x;
+  __shared__ int32_t s_dst[64];
+  __shared__ int32_t s_exp[64];
+  __shared__ float s_w[64];
+  if (threadIdx.x < a.k) {
+    const int j = threadIdx.x;
+    const int64_t p = a.mode == 0 ? static_cast<int64_t>(j) * a.t + t : t * a.k + j;
+    s_dst[j] = a.s2d[p];
+    s_exp[j] = a.expert ? a.expert[t * a.k + j] : 0;
+    s_w[j] = a.scales ? load_as_f32(a.scales, a.scales_dt, t * a.k + j) : 1.0f;
+  }
+  __syncthreads();
+  const int64_t h8 = a.h / 8;
+  for (int64_t c = threadIdx.x; c < h8; c += blockDim.x) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float v[8];
+    if (a.skip1) {
+      load8_bf16(a.skip1, t * a.h + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = v[e];
+    }
+    if (a.skip2) {
+      load8_bf16(a.skip2, t * a.h + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + v[e];
+    }
+    for (int j = 0; j < a.k; ++j) {
+      const int32_t d = s_dst[j];
+      if (d < 0) continue;
+      load8_bf16(a.ex, static_cast<int64_t>(d) * a.h + 8 * c, v);
+      if (a.bias) {
+        float b[8];
+        load8_bf16(a.bias, static_cast<int64_t>(s_exp[j]) * a.h + 8 * c, b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = v[e] + b[e];
+      }
+      const float wgt = s_w[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + wgt * v[e];
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = static_cast<uint32_t>(f32_to_bf16(acc[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.y) + t * a.h + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void finalize_generic_kernel(FinArgs a) {
+  const int64_t t = blockIdx.x;
+  for (int64_t c = threadIdx.x; c < a.h; c += blockDim.x) {
+    float acc = 0.0f;
+    if (a.skip1) acc = load_as_f32(a.skip1, a.dt, t * a.h + c);
+    if (a.skip2) acc = acc + load_as_f32(a.skip2, a.dt, t * a.h + c);
+    for (int j = 0; j < a.k; ++j) {
+      const int64_t p = a.mode == 0 ? static_cast<int64_t>(j) * a.t + t : t * a.k + j;
+      const int32_t d = a.s2d[p];
+      if (d < 0) continue;
+      float v = load_as_f32(a.ex, a.dt, static_cast<int64_t>(d) * a.h + c);
+      if (a.bias) v = v + load_as_f32(a.bias, a.dt, static_cast<int64_t>(a.expert[t * a.k + j]) * a.h + c);
+      const float wgt = a.scales ? load_as_f32(a.scales, a.scales_dt, t * a.k + j) : 1.0f;
+      acc = acc + wgt * v;
+    }
+    store_from_f32(a.y, a.dt, t * a.h + c, acc);
+  }
+}
+
+}  // namespace
+}  // namespace tai
+
+using namespace tai;
+
+extern "C" int tai_moe_gating_top_k(const void* x, int x_dtype, int64_t t, int64_t e, int k,
+                                    const void* bias, int bias_dtype, int k_group, int group_count,
+                                    int group_select_mode, int renorm, int norm_type, int out_flag,
+                                    float routed_scaling_factor, float eps, void* y,
+                                    int32_t* expert_idx, float* out, void* stream) {
+  TAI_CHECK_ARG(t >= 0 && e > 0 && e <= kMaxExperts, "tai_moe_gating_top_k: expert count must be in [1, %d]", kMaxExperts);
+  TAI_CHECK_ARG(k > 0 && k <= e && k <= 32, "tai_moe_gating_top_k: k must be in [1, min(E, 32)]");
+  TAI_CHECK_ARG(group_count >= 1 && group_count <= kMaxGroups && e % group_count == 0,
+                "tai_moe_gating_top_k: group_count must divide E and be <= %d", kMaxGroups);
+  TAI_CHECK_ARG(k_group >= 1 && k_group <= group_count, "tai_moe_gating_top_k: k_group must be in [1, group_count]");
+  TAI_CHECK_ARG(k <= k_group * (e / group_count), "tai_moe_gating_top_k: k exceeds the experts in the kept groups");
+  TAI_CHECK_ARG(group_select_mode == 0 || group_select_mode == 1, "tai_moe_gating_top_k: group_select_mode must be 0 or 1");
+  TAI_CHECK_ARG(norm_type == 0 || norm_type == 1, "tai_moe_gating_top_k: norm_type must be 0 (softmax) or 1 (sigmoid)");
+  TAI_UNSUPPORTED(renorm != 0, "tai_moe_gating_top_k: only renorm=0 (norm before top-k) is supported");
+  TAI_CHECK_ARG(x_dtype == TAI_DT_FP32 || x_dtype == TAI_DT_BF16 || x_dtype == TAI_DT_FP16, "tai_moe_gating_top_k: x dtype");
+  if (t == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && y && expert_idx, "tai_moe_gating_top_k: null pointer");
+  GateArgs a{x, x_dtype, t, e, k, bias, bias_dtype, k_group, group_count, group_select_mode, norm_type,
+             out_flag, routed_scaling_factor, eps, y, expert_idx, out};
+  gating_topk_kernel<<<dim3(static_cast<unsigned>(cdiv(t, 4))), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return launch_status("tai_moe_gating_top_k");
+}
+
+extern "C" size_t tai_moe_init_routing_workspace_size(int64_t t, int k, int64_t num_experts) {
+  return route_ws_bytes(t * k, num_experts);
+}
+
+namespace tai {
+static int run_routing(const void* x, int elem_bytes, int64_t t, int64_t h, const int32_t* eidx, int k,
+                       int e0, int bins, int64_t active_rows, int mode, int32_t* row_idx,
+                       const int32_t* legacy_row, int32_t* eout, int64_t* tokens, int tokens_cumsum,
+                       const float* scale, float* escale, void* ex, void* ws, size_t ws_bytes,
+                       hipStream_t st, const char* name) {
+  const int64_t n = t * k;
+  TAI_CHECK_ARG(n < (1ll << 31), "%s: t*k must be < 2^31", name);
+  TAI_CHECK_ARG(bins >= 1 && bins <= 1024, "%s: expert range must hold 1..1024 experts", name);
+  if (ws_bytes < route_ws_bytes(n, bins) || ws == nullptr) {
+    set_error("%s: workspace of %zu bytes, need %zu", name, ws_bytes, route_ws_bytes(n, bins));
+    return TAI_ERR_WORKSPACE;
+  }
+  RouteWs w = carve_route_ws(ws, n, bins);
+  const int64_t chunks = cdiv(n, kChunk);
+  TAI_CHECK_ARG(chunks < (1ll << 31), "%s: too many slots", name);
+  if (n == 0) return TAI_OK;
+  route_hist_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, sizeof(int32_t) * bins, st>>>(eidx, n, e0, bins, w.hist);
+  route_scan_kernel<<<1, 1024, sizeof(int32_t) * 2 * bins, st>>>(w.hist, chunks, bins, tokens, tokens_cumsum, w.total);
+  route_place_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, 0, st>>>(eidx, n, e0, bins, w.hist, w.dst2src,
+                                                                          mode, row_idx, legacy_row, eout);
+  const int tail_mode = (mode == 1) ? 1 : 0;
+  route_gather_kernel<<<dim3(static_cast<unsigned>(cdiv(n, 4))), 256, 0, st>>>(
+      x, static_cast<int64_t>(elem_bytes) * h, t, k, w.dst2src, w.total, active_rows, n, ex, scale, escale,
+      tail_mode, row_idx, legacy_row);
+  return launch_status(name);
+}
+}  // namespace tai
+
+extern "C" int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t, int64_t h,
+                                       const int32_t* expert_idx, int k, const float* scale,
+                                       int64_t active_rows, int expert_start, int expert_end,
+                                       int expert_tokens_num_type, int row_idx_type, void* expanded_x,
+                                       int32_t* expanded_row_idx, int64_t* expert_tokens,
+                                       float* expanded_scale, void* workspace, size_t ws_bytes,
+                                       void* stream) {
+  TAI_CHECK_ARG(t >= 0 && h >= 0 && k > 0, "tai_moe_init_routing_v2: bad sizes");
+  TAI_CHECK_ARG(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4, "tai_moe_init_routing_v2: elem_bytes");
+  TAI_CHECK_ARG(expert_start >= 0 && expert_end > expert_start, "tai_moe_init_routing_v2: expert range");
+  TAI_CHECK_ARG(row_idx_type == 0 || row_idx_type == 1, "tai_moe_init_routing_v2: row_idx_type must be 0 or 1");
+  TAI_CHECK_ARG(expert_tokens_num_type == 0 || expert_tokens_num_type == 1,
+                "tai_moe_init_routing_v2: expert_tokens_num_type must be 0 (cumsum) or 1 (count)");
+  TAI_CHECK_ARG(active_rows >= 0 && active_rows <= t * k, "tai_moe_init_routing_v2: active rows");
+  TAI_CHECK_ARG(scale == nullptr || expanded_scale != nullptr, "tai_moe_init_routing_v2: expanded_scale missing");
+  return run_routing(x, elem_bytes, t, h, expert_idx, k, expert_start, expert_end - expert_start, active_rows,
+                     row_idx_type, expanded_row_idx, nullptr, nullptr, expert_tokens, expert_tokens_num_type == 0,
+                     scale, expanded_scale, expanded_x, workspace, ws_bytes, static_cast<hipStream_t>(stream),
+                     "tai_moe_init_routing_v2");
+}
+
+extern "C" int tai_moe_init_routing(const void* x, int elem_bytes, int64_t t, int64_t h,
+                                    const int32_t* row_idx, const int32_t* expert_idx, int k,
+                                    int64_t num_experts, int64_t active_rows, void* expanded_x,
+                                    int32_t* expanded_row_idx, int32_t* expanded_expert_idx,
+                                    void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(t >= 0 && h >= 0 && k > 0, "tai_moe_init_routing: bad sizes");
+  TAI_CHECK_ARG(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4, "tai_moe_init_routing: elem_bytes");
+  TAI_CHECK_ARG(active_rows >= 0 && active_rows <= t * k, "tai_moe_init_routing: active rows");
+  TAI_CHECK_ARG(row_idx && expanded_row_idx && expanded_expert_idx, "tai_moe_init_routing: null pointer");
+  return run_routing(x, elem_bytes, t, h, expert_idx, k, 0, static_cast<int>(num_experts), active_rows, 2,
+                     expanded_row_idx, row_idx, expanded_expert_idx, nullptr, 0, nullptr, nullptr, expanded_x,
+                     workspace, ws_bytes, static_cast<hipStream_t>(stream), "tai_moe_init_routing");
+}
+
+extern "C" int tai_moe_finalize_routing(const void* expanded, int dtype, int64_t t, int64_t h, int k,
+                                        const void* skip1, const void* skip2, const void* bias,
+                                        const void* scales, int scales_dtype, const int32_t* src_to_dst,
+                                        const int32_t* expert_for_source_row, int drop_pad_mode, void* y,
+                                        void* stream) {
+  TAI_CHECK_ARG(t >= 0 && h >= 0 && k > 0 && k <= 64, "tai_moe_finalize_routing: k must be in [1, 64]");
+  TAI_UNSUPPORTED(drop_pad_mode != 0 && drop_pad_mode != 2,
+                  "tai_moe_finalize_routing: drop_pad_mode %d (drop-pad) not supported; use 0 or 2", drop_pad_mode);
+  TAI_CHECK_ARG(dtype == TAI_DT_BF16 || dtype == TAI_DT_FP16 || dtype == TAI_DT_FP32, "tai_moe_finalize_routing: dtype");
+  TAI_CHECK_ARG(bias == nullptr || expert_for_source_row != nullptr,
+                "tai_moe_finalize_routing: bias needs expert_for_source_row");
+  if (t == 0 || h == 0) return TAI_OK;
+  TAI_CHECK_ARG(expanded && src_to_dst && y, "tai_moe_finalize_routing: null pointer");
+  FinArgs a{expanded, dtype, t, h, k, skip1, skip2, bias, scales, scales_dtype, src_to_dst, expert_for_source_row,
+            drop_pad_mode == 0 ? 0 : 2, y};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
+  if (dtype == TAI_DT_BF16 && h % 8 == 0 && al(expanded) && al(skip1) && al(skip2) && al(bias) && al(y))
+    finalize_bf16_kernel<<<dim3(static_cast<unsigned>(t)), 256, 0, st>>>(a);
+  else
+    finalize_generic_kernel<<<dim3(static_cast<unsigned>(t)), 256, 0, st>>>(a);
+  return launch_status("tai_moe_finalize_routing");
+}

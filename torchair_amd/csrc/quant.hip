@@ -1,0 +1,399 @@
+// Per-row int8 quantisers: npu_dynamic_quant and npu_dequant_swiglu_quant.
+//
+// Both are HBM-bound: one read of the input row, one write of the int8 row and a scale.
+// A row lives in registers between the max-reduction and the quantising pass, so every
+// input byte is read from HBM exactly once. Row -> workgroup mapping:
+//   narrow rows (<= 4096 elements): one wave per row, 4 rows per 256-thread workgroup;
+//   wide rows: one 256-thread workgroup per row.
+// Arithmetic order (fixed so results are bit-reproducible against the CPU oracle):
+//   xs = x * smooth;  scale = amax(|xs|) / 127;  y = clamp(rint(xs / scale), -128, 127)
+// with IEEE fp32 division; an all-zero row gives scale 0 and y 0.
+#include "common.h"
+
+namespace tai {
+namespace {
+
+constexpr int kVec = 8;  // elements per vector load
+
+template <int DT>
+struct Vec8 {
+  static __device__ __forceinline__ void load(const void* base, int64_t idx, float (&v)[kVec]) {
+    if constexpr (DT == TAI_DT_FP32) {
+      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+      float4 a = p[0], b = p[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+      uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
+        if constexpr (DT == TAI_DT_BF16) {
+          v[2 * i] = bf16_to_f32(lo);
+          v[2 * i + 1] = bf16_to_f32(hi);
+        } else {
+          v[2 * i] = f16_to_f32(lo);
+          v[2 * i + 1] = f16_to_f32(hi);
+        }
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ int8_t quant1(float v, float scale) {
+  if (scale == 0.0f) return 0;
+  float q = rintf(v / scale);
+  q = fminf(fmaxf(q, -128.0f), 127.0f);
+  return static_cast<int8_t>(static_cast<int>(q));
+}
+
+__device__ __forceinline__ uint2 pack8(const float (&v)[kVec], float scale) {
+  uint32_t w[2] = {0, 0};
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) {
+    uint32_t b = static_cast<uint8_t>(quant1(v[i], scale));
+    w[i >> 2] |= b << (8 * (i & 3));
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+// Smallest g with row < ends[g] (ends ascending, cumulative). Rows past the end use the last group.
+__device__ __forceinline__ int64_t group_of_row_cumsum(const void* ends, int dt, int64_t n, int64_t row) {
+  int64_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int64_t mid = (lo + hi) >> 1;
+    if (row < load_index(ends, dt, mid)) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+// ----------------------------------------------------------------------------- dynamic quant
+// TPR threads per row (64 or 256); NV vectors of 8 per thread held in registers.
+template <int DT, int TPR, int NV>
+__global__ __launch_bounds__(256) void dynamic_quant_kernel(
+    const void* __restrict__ x, int64_t rows, int64_t cols, const float* __restrict__ smooth,
+    const void* __restrict__ gidx, int gidx_dt, int64_t ngroups, int8_t* __restrict__ y,
+    float* __restrict__ scale_out) {
+  constexpr int RPB = 256 / TPR;
+  __shared__ float red[RPB][TPR / 64];
+  const int sub = threadIdx.x / TPR;
+  const int lane = threadIdx.x % TPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + sub;
+  const bool active = row < rows;
+  const int64_t nvec = cols / kVec;
+
+  const float* sm = nullptr;
+  if (smooth != nullptr && active) {
+    int64_t g = (gidx != nullptr) ? group_of_row_cumsum(gidx, gidx_dt, ngroups, row) : 0;
+    sm = smooth + g * cols;
+  }
+
+  float v[NV][kVec];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t vi = lane + static_cast<int64_t>(i) * TPR;
+    if (active && vi < nvec) {
+      Vec8<DT>::load(x, row * cols + vi * kVec, v[i]);
+      if (sm != nullptr) {
+        const float4* sp = reinterpret_cast<const float4*>(sm + vi * kVec);
+        float4 a = sp[0], b = sp[1];
+        v[i][0] *= a.x; v[i][1] *= a.y; v[i][2] *= a.z; v[i][3] *= a.w;
+        v[i][4] *= b.x; v[i][5] *= b.y; v[i][6] *= b.z; v[i][7] *= b.w;
+      }
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+    }
+  }
+  amax = wave_max(amax);
+  if constexpr (TPR > 64) {
+    if ((lane & 63) == 0) red[sub][lane >> 6] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPR / 64; ++i) amax = fmaxf(amax, red[sub][i]);
+  }
+  if (!active) return;
+  const float scale = amax / 127.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t vi = lane + static_cast<int64_t>(i) * TPR;
+    if (vi < nvec) *reinterpret_cast<uint2*>(y + row * cols + vi * kVec) = pack8(v[i], scale);
+  }
+  if (lane == 0) scale_out[row] = scale;
+}
+
+// Any shape / alignment: one workgroup per row, two passes over global memory.
+__global__ __launch_bounds__(256) void dynamic_quant_generic_kernel(
+    const void* __restrict__ x, int dt, int64_t rows, int64_t cols, const float* __restrict__ smooth,
+    const void* __restrict__ gidx, int gidx_dt, int64_t ngroups, int8_t* __restrict__ y,
+    float* __restrict__ scale_out) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const float* sm = nullptr;
+  if (smooth != nullptr) {
+    int64_t g = (gidx != nullptr) ? group_of_row_cumsum(gidx, gidx_dt, ngroups, row) : 0;
+    sm = smooth + g * cols;
+  }
+  float amax = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    float v = load_as_f32(x, dt, row * cols + c);
+    if (sm) v *= sm[c];
+    amax = fmaxf(amax, fabsf(v));
+  }
+  amax = block_max(amax, red);
+  const float scale = amax / 127.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    float v = load_as_f32(x, dt, row * cols + c);
+    if (sm) v *= sm[c];
+    y[row * cols + c] = quant1(v, scale);
+  }
+  if (threadIdx.x == 0) scale_out[row] = scale;
+}
+
+template <int DT>
+int launch_dynamic_quant(const void* x, int64_t rows, int64_t cols, const float* smooth,
+                         const void* gidx, int gidx_dt, int64_t ng, int8_t* y, float* scale,
+                         hipStream_t st) {
+  const bool aligned = (cols % kVec) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
+                       (reinterpret_cast<uintptr_t>(y) % 8) == 0 &&
+                       (smooth == nullptr || (reinterpret_cast<uintptr_t>(smooth) % 16) == 0);
+  const int64_t nvec = cols / kVec;
+  if (aligned && nvec <= 64 * 8) {
+    dim3 grid(static_cast<unsigned>(cdiv(rows, 4)));
+    if (nvec <= 64 * 2)
+      dynamic_quant_kernel<DT, 64, 2><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+    else if (nvec <= 64 * 4)
+      dynamic_quant_kernel<DT, 64, 4><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+    else
+      dynamic_quant_kernel<DT, 64, 8><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+  } else if (aligned && nvec <= 256 * 8) {
+    dim3 grid(static_cast<unsigned>(rows));
+    if (nvec <= 256 * 4)
+      dynamic_quant_kernel<DT, 256, 4><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+    else
+      dynamic_quant_kernel<DT, 256, 8><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+  } else {
+    dynamic_quant_generic_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, st>>>(
+        x, DT, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
+  }
+  return launch_status("tai_dynamic_quant");
+}
+
+// ----------------------------------------------------------------------------- dequant-swiglu-quant
+struct DsqArgs {
+  const int32_t* x;
+  int64_t rows, n;  // x is [rows, 2n]
+  const float* ws;
+  const float* as;
+  const void* bias;
+  int bias_dt;
+  const float* qs;
+  const void* gidx;
+  int gidx_dt;
+  int64_t ngroups;
+  int left;
+  int8_t* y;
+  float* scale;
+};
+
+__device__ __forceinline__ float silu(float a) { return a / (1.0f + expf(-a)); }
+
+// Finds the group of `row` from per-group row counts with a workgroup-wide scan.
+// Returns -1 when the row is past the total.
+__device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, int64_t row, int64_t* sh) {
+  __shared__ int64_t carry;
+  __shared__ int64_t found;
+  if (threadIdx.x == 0) { carry = 0; found = -1; }
+  __syncthreads();
+  for (int64_t base = 0; base < ng; base += blockDim.x) {
+    const int64_t g = base + threadIdx.x;
+    int64_t c = g < ng ? load_index(counts, dt, g) : 0;
+    sh[threadIdx.x] = c;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over blockDim.x entries.
+    for (int o = 1; o < static_cast<int>(blockDim.x); o <<= 1) {
+      int64_t add = threadIdx.x >= static_cast<unsigned>(o) ? sh[threadIdx.x - o] : 0;
+      __syncthreads();
+      sh[threadIdx.x] += add;
+      __syncthreads();
+    }
+    const int64_t end = carry + sh[threadIdx.x];
+    const int64_t begin = end - c;
+    if (g < ng && row >= begin && row < end) found = g;
+    __syncthreads();
+    if (threadIdx.x == blockDim.x - 1) carry = end;
+    __syncthreads();
+    if (found >= 0) break;
+  }
+  return found;
+}
+
+// One workgroup of 256 threads per row; each thread owns NV groups of 4 output columns.
+template <int NV>
+__global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
+  __shared__ int64_t scan[256];
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t n = a.n, n2 = 2 * a.n;
+  int64_t g = 0;
+  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row, scan);
+  const int64_t ng4 = n / 4;
+  if (g < 0) {  // row beyond the grouped rows
+    for (int64_t c = tid; c < ng4; c += 256)
+      *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = 0u;
+    if (tid == 0) a.scale[row] = 0.0f;
+    return;
+  }
+  const float* ws = a.ws ? a.ws + g * n2 : nullptr;
+  const float* qs = a.qs ? a.qs + g * n : nullptr;
+  const float act = a.as ? a.as[row] : 1.0f;
+  const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
+  const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
+  const int32_t* xr = a.x + row * n2;
+
+  float v[NV][4];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    if (c < ng4) {
+      const int64_t j = 4 * c;
+      int4 xa = *reinterpret_cast<const int4*>(xr + j);
+      int4 xb = *reinterpret_cast<const int4*>(xr + n + j);
+      int ia[4] = {xa.x, xa.y, xa.z, xa.w}, ib[4] = {xb.x, xb.y, xb.z, xb.w};
+      if (bi) {
+        int4 ba = *reinterpret_cast<const int4*>(bi + j), bb = *reinterpret_cast<const int4*>(bi + n + j);
+        ia[0] += ba.x; ia[1] += ba.y; ia[2] += ba.z; ia[3] += ba.w;
+        ib[0] += bb.x; ib[1] += bb.y; ib[2] += bb.z; ib[3] += bb.w;
+      }
+      float wa[4] = {1.f, 1.f, 1.f, 1.f}, wb[4] = {1.f, 1.f, 1.f, 1.f};
+      if (ws) {
+        float4 p = *reinterpret_cast<const float4*>(ws + j), q = *reinterpret_cast<const float4*>(ws + n + j);
+        wa[0] = p.x; wa[1] = p.y; wa[2] = p.z; wa[3] = p.w;
+        wb[0] = q.x; wb[1] = q.y; wb[2] = q.z; wb[3] = q.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float da = static_cast<float>(ia[e]) * wa[e];
+        float db = static_cast<float>(ib[e]) * wb[e];
+        if (a.as) { da *= act; db *= act; }
+        if (bf) { da += bf[j + e]; db += bf[n + j + e]; }
+        float r = a.left ? silu(da) * db : da * silu(db);
+        if (qs) r *= qs[j + e];
+        v[i][e] = r;
+        amax = fmaxf(amax, fabsf(r));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float scale = amax / 127.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    if (c < ng4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w |= static_cast<uint32_t>(static_cast<uint8_t>(quant1(v[i][e], scale))) << (8 * e);
+      *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = w;
+    }
+  }
+  if (tid == 0) a.scale[row] = scale;
+}
+
+// Any n: two passes over global memory.
+__global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
+  __shared__ int64_t scan[256];
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int64_t n = a.n, n2 = 2 * a.n;
+  int64_t g = 0;
+  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row, scan);
+  if (g < 0) {
+    for (int64_t c = threadIdx.x; c < n; c += blockDim.x) a.y[row * n + c] = 0;
+    if (threadIdx.x == 0) a.scale[row] = 0.0f;
+    return;
+  }
+  const float* ws = a.ws ? a.ws + g * n2 : nullptr;
+  const float* qs = a.qs ? a.qs + g * n : nullptr;
+  const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
+  const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
+  const float act = a.as ? a.as[row] : 1.0f;
+  auto value = [&](int64_t j) {
+    int xa = a.x[row * n2 + j], xb = a.x[row * n2 + n + j];
+    if (bi) { xa += bi[j]; xb += bi[n + j]; }
+    float da = static_cast<float>(xa) * (ws ? ws[j] : 1.0f);
+    float db = static_cast<float>(xb) * (ws ? ws[n + j] : 1.0f);
+    if (a.as) { da *= act; db *= act; }
+    if (bf) { da += bf[j]; db += bf[n + j]; }
+    float r = a.left ? silu(da) * db : da * silu(db);
+    if (qs) r *= qs[j];
+    return r;
+  };
+  float amax = 0.0f;
+  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) amax = fmaxf(amax, fabsf(value(j)));
+  amax = block_max(amax, red);
+  const float scale = amax / 127.0f;
+  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) a.y[row * n + j] = quant1(value(j), scale);
+  if (threadIdx.x == 0) a.scale[row] = scale;
+}
+
+}  // namespace
+}  // namespace tai
+
+using namespace tai;
+
+extern "C" int tai_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                 const float* smooth_scales, const void* group_index,
+                                 int group_index_dtype, int64_t num_groups, int8_t* y, float* scale,
+                                 void* stream) {
+  TAI_CHECK_ARG(rows >= 0 && cols >= 0, "tai_dynamic_quant: negative size");
+  if (rows == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && y && scale, "tai_dynamic_quant: null pointer");
+  TAI_CHECK_ARG(rows < (1ll << 31), "tai_dynamic_quant: rows must be < 2^31");
+  TAI_CHECK_ARG(group_index == nullptr || (smooth_scales != nullptr && num_groups > 0),
+                "tai_dynamic_quant: group_index needs smooth_scales with num_groups > 0");
+  TAI_CHECK_ARG(group_index == nullptr || group_index_dtype == TAI_DT_INT32 || group_index_dtype == TAI_DT_INT64,
+                "tai_dynamic_quant: group_index must be int32 or int64");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case TAI_DT_BF16: return launch_dynamic_quant<TAI_DT_BF16>(x, rows, cols, smooth_scales, group_index, group_index_dtype, num_groups, y, scale, st);
+    case TAI_DT_FP16: return launch_dynamic_quant<TAI_DT_FP16>(x, rows, cols, smooth_scales, group_index, group_index_dtype, num_groups, y, scale, st);
+    case TAI_DT_FP32: return launch_dynamic_quant<TAI_DT_FP32>(x, rows, cols, smooth_scales, group_index, group_index_dtype, num_groups, y, scale, st);
+    default: set_error("tai_dynamic_quant: x dtype %d not supported (bf16, fp16, fp32)", x_dtype); return TAI_ERR_INVALID;
+  }
+}
+
+extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t n2,
+                                        const float* weight_scale, const float* activation_scale,
+                                        const void* bias, int bias_dtype, const float* quant_scale,
+                                        const void* group_index, int group_index_dtype,
+                                        int64_t num_groups, int activate_left, int8_t* y,
+                                        float* scale, void* stream) {
+  TAI_CHECK_ARG(rows >= 0 && n2 >= 0 && n2 % 2 == 0, "tai_dequant_swiglu_quant: last dim must be even");
+  if (rows == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && y && scale, "tai_dequant_swiglu_quant: null pointer");
+  TAI_CHECK_ARG(rows < (1ll << 31), "tai_dequant_swiglu_quant: rows must be < 2^31");
+  TAI_CHECK_ARG(bias == nullptr || bias_dtype == TAI_DT_INT32 || bias_dtype == TAI_DT_FP32,
+                "tai_dequant_swiglu_quant: bias must be int32 or fp32");
+  TAI_CHECK_ARG(group_index == nullptr || num_groups > 0, "tai_dequant_swiglu_quant: empty group_index");
+  TAI_CHECK_ARG(group_index == nullptr || group_index_dtype == TAI_DT_INT32 || group_index_dtype == TAI_DT_INT64,
+                "tai_dequant_swiglu_quant: group_index must be int32 or int64");
+  DsqArgs a{x, rows, n2 / 2, weight_scale, activation_scale, bias, bias_dtype, quant_scale,
+            group_index, group_index_dtype, group_index ? num_groups : 1, activate_left, y, scale};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = n2 / 2;
+  auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
+  const bool aligned = n % 4 == 0 && al(x) && al(weight_scale) && al(bias) && (reinterpret_cast<uintptr_t>(y) % 4) == 0;
+  const int64_t ng4 = n / 4;
+  dim3 grid(static_cast<unsigned>(rows));
+  if (aligned && ng4 <= 256 * 2) dsq_kernel<2><<<grid, 256, 0, st>>>(a);
+  else if (aligned && ng4 <= 256 * 4) dsq_kernel<4><<<grid, 256, 0, st>>>(a);
+  else if (aligned && ng4 <= 256 * 8) dsq_kernel<8><<<grid, 256, 0, st>>>(a);
+  else dsq_generic_kernel<<<grid, 256, 0, st>>>(a);
+  return launch_status("tai_dequant_swiglu_quant");
+}

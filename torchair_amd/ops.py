@@ -1,0 +1,19 @@
+"""Eager entry points of the fused ops (the ``torch_npu.npu_*`` / ``torchair.ops`` surface)."""
+import torch
+
+from . import _ops_impl  # noqa: F401
+
+
+def npu_fused_infer_attention_score(*args, **kwargs):
+    """torchair.ops.npu_fused_infer_attention_score (tensor sequence lengths), air:: namespace."""
+    return torch.ops.air.npu_fused_infer_attention_score(*args, **kwargs)
+
+
+npu_dynamic_quant = torch.ops.npu.npu_dynamic_quant
+npu_dequant_swiglu_quant = torch.ops.npu.npu_dequant_swiglu_quant
+npu_quant_matmul = torch.ops.npu.npu_quant_matmul
+npu_grouped_matmul = torch.ops.npu.npu_grouped_matmul
+npu_moe_gating_top_k = torch.ops.npu.npu_moe_gating_top_k
+npu_moe_init_routing = torch.ops.npu.npu_moe_init_routing
+npu_moe_init_routing_v2 = torch.ops.npu.npu_moe_init_routing_v2
+npu_moe_finalize_routing = torch.ops.npu.npu_moe_finalize_routing
