@@ -1,0 +1,306 @@
+"""Benchmark of the fused-op hot path on one MI355X.
+
+Headline (value): DeepSeek-V3-shaped quantized MoE layer in tokens/s:
+  gating_top_k -> init_routing_v2 -> dynamic_quant -> grouped_matmul (W8A8 gate_up, int32)
+  -> dequant_swiglu_quant -> grouped_matmul (W8A8 down, bf16) -> finalize_routing,
+with every input resident in HBM before the timed region. Side measurements in the same JSON
+line: paged GQA decode attention (config 2) HBM GB/s, the W8A8 GEMM at M=N=K=8192 and the
+config-1 MLP. `roofline` is for the dominant kernel (the gate_up grouped GEMM), timed with HIP
+events on its stream inside the timed region; `cpu_baseline` times the CPU oracle on a bounded
+sample of the same layer.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "MoE-layer tokens/s; decode-attn HBM GB/s & int8 GEMM TOPS (% of peak)"
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+# ----------------------------------------------------------------------------- MoE layer (config 4)
+class MoeLayer:
+    T, H, E, K, I = 4096, 7168, 256, 8, 2048
+
+    def __init__(self, torch, dev):
+        self.torch = torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        T, H, E, I = self.T, self.H, self.E, self.I
+        self.x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+        self.logits = torch.randn(T, E, generator=g, device=dev)
+        self.bias = torch.randn(E, generator=g, device=dev) * 0.1
+        self.w_gu = torch.randint(-127, 128, (E, H, 2 * I), generator=g, device=dev, dtype=torch.int8)
+        self.w_d = torch.randint(-127, 128, (E, I, H), generator=g, device=dev, dtype=torch.int8)
+        self.s_gu = torch.rand(E, 2 * I, generator=g, device=dev) * 9e-3 + 1e-3
+        self.s_d = torch.rand(E, H, generator=g, device=dev) * 9e-3 + 1e-3
+        self.gmm1_events = []
+
+    def step(self, record=False):
+        torch = self.torch
+        npu = torch.ops.npu
+        y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
+                                             group_select_mode=1, renorm=0, norm_type=1,
+                                             routed_scaling_factor=1.0, eps=1e-20)
+        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
+                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                        row_idx_type=0)
+        q, s = npu.npu_dynamic_quant(ex)
+        if record:
+            e0, e1 = _events(torch)
+            e0.record()
+        acc = npu.npu_grouped_matmul([q], [self.w_gu], group_list=counts, split_item=3, group_type=0,
+                                     group_list_type=1, output_dtype=torch.int32)[0]
+        if record:
+            e1.record()
+            self.gmm1_events.append((e0, e1))
+        q2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=self.s_gu, activation_scale=s, group_index=counts,
+                                              activate_left=True, quant_mode=1)
+        out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
+                                     split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.bfloat16)[0]
+        return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
+
+    def gmm1_bytes(self):
+        T, H, E, K, I = self.T, self.H, self.E, self.K, self.I
+        return E * H * 2 * I + T * K * H + T * K * 2 * I * 4  # weights + int8 rows + int32 out
+
+
+def bench_moe(torch, dev, steps, warmup):
+    layer = MoeLayer(torch, dev)
+    for _ in range(warmup):
+        layer.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer.step(record=True)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    gmm_ms = sum(a.elapsed_time(b) for a, b in layer.gmm1_events) / len(layer.gmm1_events)
+    achieved = layer.gmm1_bytes() / (gmm_ms * 1e-3) / 1e9
+    roof = {"kernel": "tai_grouped_matmul (gate_up, int32 out)", "bound": "hbm", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None, "avg_ms": round(gmm_ms, 4),
+            "algorithmic_bytes": layer.gmm1_bytes()}
+    return layer, dt, roof
+
+
+# ----------------------------------------------------------------------------- W8A8 GEMM 8192^3
+def bench_gemm(torch, dev, iters=20):
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    n = 8192
+    a = torch.randint(-127, 128, (n, n), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, n), generator=g, device=dev, dtype=torch.int8)
+    one = torch.ones(1, device=dev)
+    res = {}
+    for name, bb in (("kn", b), ("nk", b.t().contiguous().t())):
+        for _ in range(3):
+            torch.ops.npu.npu_quant_matmul(a, bb, one, output_dtype=torch.int32)
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(iters):
+            torch.ops.npu.npu_quant_matmul(a, bb, one, output_dtype=torch.int32)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
+        tops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+    return res
+
+
+# ----------------------------------------------------------------------------- config-1 MLP
+def bench_mlp(torch, dev, iters=50):
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    T, H, I = 128, 2048, 5632
+    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    wgu = torch.randint(-127, 128, (H, 2 * I), generator=g, device=dev, dtype=torch.int8)
+    sgu = torch.rand(2 * I, generator=g, device=dev) * 9e-3 + 1e-3
+    wd = torch.randint(-127, 128, (I, H), generator=g, device=dev, dtype=torch.int8)
+    sd = torch.rand(H, generator=g, device=dev) * 9e-3 + 1e-3
+    one = torch.ones(1, device=dev)
+    npu = torch.ops.npu
+
+    def mlp(x):
+        q, s = npu.npu_dynamic_quant(x)
+        h = npu.npu_quant_matmul(q, wgu, one, output_dtype=torch.int32)
+        q2, s2 = npu.npu_dequant_swiglu_quant(h, weight_scale=sgu, activation_scale=s, quant_mode=1,
+                                              activate_left=True)
+        return npu.npu_quant_matmul(q2, wd, sd, pertoken_scale=s2, output_dtype=torch.bfloat16)
+
+    from torchair_amd.graph import HipGraphRunner
+    runner = HipGraphRunner(mlp)
+    for _ in range(3):
+        runner(x)
+        mlp(x)
+    torch.cuda.synchronize()
+    out = {}
+    for name, fn in (("eager", mlp), ("hipgraph", runner)):
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(iters):
+            fn(x)
+        e1.record()
+        torch.cuda.synchronize()
+        out[name + "_us"] = round(e0.elapsed_time(e1) / iters * 1e3, 2)
+    algo = T * H * 2 + H * 2 * I + T * 2 * I * 4 * 2 + I * H + T * I + T * H * 2
+    out["algorithmic_MB"] = round(algo / 1e6, 2)
+    out["hbm_frac_hipgraph"] = round(algo / (out["hipgraph_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    return out
+
+
+# ----------------------------------------------------------------------------- paged decode (config 2)
+def make_decode_case(torch, dev, seed=3, B=64, HQ=32, HKV=8, D=128, BS=128):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    lens = torch.randint(512, 4097, (B,), generator=g, device=dev)
+    nb = ((lens + BS - 1) // BS)
+    total = int(nb.sum())
+    width = int(nb.max())
+    perm = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    bt = torch.zeros(B, width, dtype=torch.int32, device=dev)
+    off = 0
+    for b, n in enumerate(nb.tolist()):
+        bt[b, :n] = perm[off:off + n]
+        off += n
+    kc = torch.randn(total, BS, HKV * D, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(total, BS, HKV * D, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, 1, HQ * D, generator=g, device=dev).to(torch.bfloat16)
+    return q, kc, vc, bt, lens
+
+
+def bench_decode(torch, dev, iters=50):
+    q, kc, vc, bt, lens = make_decode_case(torch, dev)
+    B, HQ, HKV, D, BS = 64, 32, 8, 128, 128
+
+    def run():
+        return torch.ops.air.npu_fused_infer_attention_score(
+            q, kc, vc, actual_seq_lengths_kv=lens, block_table=bt, num_heads=HQ, num_key_value_heads=HKV,
+            input_layout="BSH", block_size=BS, scale=1.0 / D ** 0.5)
+
+    try:
+        run()
+    except RuntimeError as e:
+        return {"status": "unavailable", "error": str(e)[:200]}
+    for _ in range(3):
+        run()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    kv_bytes = int(lens.sum()) * HKV * D * 2 * 2 + 2 * B * HQ * D * 2 + bt.numel() * 4
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": kv_bytes}
+
+
+# ----------------------------------------------------------------------------- CPU baseline (oracle)
+def cpu_baseline(sample_experts=4):
+    """Oracle MoE layer on the host: full gating/routing/quant for all T tokens plus the expert
+    GEMMs of `sample_experts` of the 256 experts, scaled to the whole layer."""
+    import numpy as np
+    from oracle import golden as G
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count()
+    L = MoeLayer
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((L.T, L.H), dtype=np.float32)
+    x = G.round_bf16(x)
+    logits = rng.standard_normal((L.T, L.E), dtype=np.float32)
+    bias = (rng.standard_normal(L.E) * 0.1).astype(np.float32)
+    t0 = time.perf_counter()
+    y, idx, _ = G.moe_gating_top_k(logits, L.K, bias, 4, 8, 1, 0, 1, False, 1.0, 1e-20)
+    ex, ri, counts, _ = G.moe_init_routing_v2(x, idx, None, L.T * L.K, 0, L.E, 1, 0)
+    q, s = G.dynamic_quant(ex)
+    t_route = time.perf_counter() - t0
+    ends = np.cumsum(counts)
+    t1 = time.perf_counter()
+    outs = []
+    for e in range(sample_experts):
+        b0 = 0 if e == 0 else int(ends[e - 1])
+        b1 = int(ends[e])
+        w_gu = rng.integers(-127, 128, (L.H, 2 * L.I), dtype=np.int8)
+        w_d = rng.integers(-127, 128, (L.I, L.H), dtype=np.int8)
+        s_gu = rng.uniform(1e-3, 1e-2, 2 * L.I).astype(np.float32)
+        s_d = rng.uniform(1e-3, 1e-2, L.H).astype(np.float32)
+        acc = G.quant_matmul(q[b0:b1], w_gu, out_dtype="int32")
+        q2, s2 = G.dequant_swiglu_quant(acc, s_gu, s[b0:b1], activate_left=True)
+        outs.append(G.quant_matmul(q2, w_d, s_d, s2, None, "bf16"))
+    t_exp = time.perf_counter() - t1
+    t2 = time.perf_counter()
+    out = np.zeros((L.T * L.K, L.H), np.float32)
+    G.moe_finalize_routing(out, None, None, None, y, ri, idx, 2, "bf16")
+    t_fin = time.perf_counter() - t2
+    total = t_route + t_fin + t_exp * (L.E / sample_experts)
+    return {"value": round(L.T / total, 2), "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"numpy oracle: gating+routing+quant+finalize for all {L.T} tokens "
+                      f"({t_route + t_fin:.1f}s) + expert GEMMs of {sample_experts}/{L.E} experts "
+                      f"({t_exp:.1f}s) scaled x{L.E // sample_experts}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of side benches to run (gemm,mlp,decode)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (no multi-GPU path is built)"}))
+        sys.exit(2)
+    import torch
+    import torchair_amd  # noqa: F401
+
+    dev = "cuda:0"
+    torch.cuda.synchronize()
+    layer, dt, roof = bench_moe(torch, dev, args.steps, args.warmup)
+    del layer
+    torch.cuda.empty_cache()
+    extra = {}
+    only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode"}
+    if "gemm" in only:
+        extra["w8a8_gemm_8192"] = bench_gemm(torch, dev)
+    if "mlp" in only:
+        extra["mlp_cfg1"] = bench_mlp(torch, dev)
+    if "decode" in only:
+        extra["paged_decode_cfg2"] = bench_decode(torch, dev)
+    torch.cuda.empty_cache()
+    cpu = None if args.skip_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC, "value": round(MoeLayer.T / dt, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 (W8A8, int32 accumulate; bf16 activations)",
+        "data": "synthetic (seeded randn/randint of the config shapes, random-init weights)",
+        "config": {"workload": "DeepSeek-V3-shaped quantized MoE layer, T=4096 H=7168 E=256 top-8 I=2048 "
+                               "(BASELINE config 4), all experts on one GPU", "global_batch": MoeLayer.T,
+                   "seq_len": 1, "parallelism": "single GPU"},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+"""GPU parity: npu_fused_infer_attention_score (paged GQA decode, causal prefill, MLA decode)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_close, f32np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _paged_case(lens, hq, hkv, d, bs, seed, layout="BSH"):
+    g = torch.Generator().manual_seed(seed)
+    b = len(lens)
+    nb = [(L + bs - 1) // bs for L in lens]
+    total = sum(nb) + 3
+    width = max(max(nb), 1)
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(b, width, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    k4 = torch.randn(total, bs, hkv, d, generator=g).to(torch.bfloat16)
+    v4 = torch.randn(total, bs, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b, hq, d, generator=g).to(torch.bfloat16)
+    return q, k4, v4, bt, torch.tensor(lens, dtype=torch.int64)
+
+
+def _decode(q, k4, v4, bt, lens, hq, hkv, d, bs, cache_layout="BSH", api="air", lse=True):
+    b = q.shape[0]
+    if cache_layout == "BSH":
+        kc = k4.reshape(k4.shape[0], bs, hkv * d).to(DEV)
+        vc = v4.reshape(v4.shape[0], bs, hkv * d).to(DEV)
+    else:  # [blocks, Hkv, bs, D]
+        kc = k4.permute(0, 2, 1, 3).contiguous().to(DEV)
+        vc = v4.permute(0, 2, 1, 3).contiguous().to(DEV)
+    qd = q.reshape(b, 1, hq * d).to(DEV)
+    kw = dict(block_table=bt.to(DEV), num_heads=hq, num_key_value_heads=hkv, input_layout="BSH", block_size=bs,
+              scale=1.0 / math.sqrt(d), softmax_lse_flag=lse)
+    if api == "air":
+        out, l = torch.ops.air.npu_fused_infer_attention_score(qd, kc, vc, actual_seq_lengths_kv=lens.to(DEV), **kw)
+    else:
+        out, l = torch.ops.npu.npu_fused_infer_attention_score(qd, kc, vc, actual_seq_lengths_kv=lens.tolist(), **kw)
+    return out.reshape(b, hq, d), l
+
+
+def _check_decode(lens, hq, hkv, d, bs, seed, **kw):
+    q, k4, v4, bt, L = _paged_case(lens, hq, hkv, d, bs, seed)
+    out, lse = _decode(q, k4, v4, bt, L, hq, hkv, d, bs, **kw)
+    want, wl = G.paged_decode_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lens, 1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    wl_fin = np.where(np.isfinite(wl), wl, -1e30)
+    got = lse.reshape(len(lens), hq).cpu().numpy()
+    np.testing.assert_allclose(np.where(np.isfinite(got), got, -1e30), wl_fin, rtol=1e-3, atol=1e-3)
+
+
+def test_paged_decode_cfg2():
+    g = torch.Generator().manual_seed(100)
+    lens = torch.randint(512, 4097, (64,), generator=g).tolist()
+    _check_decode(lens, 32, 8, 128, 128, 101)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 2, 64), (16, 1, 128), (4, 2, 256)])
+def test_paged_decode_shapes(hq, hkv, d):
+    _check_decode([1, 33, 300, 0, 257], hq, hkv, d, 64, 102)
+
+
+def test_paged_decode_bnsd_cache_and_list_lengths():
+    _check_decode([77, 130, 512], 8, 2, 128, 32, 103, cache_layout="BNSD", api="npu", lse=True)
+
+
+def _prefill_ref_torch(q, k, v, lq, lkv, causal, scale):
+    """fp32 PyTorch reference on the GPU: q [B,S,Hq,D], k/v [B,S,Hkv,D]."""
+    b, s, hq, d = q.shape
+    hkv = k.shape[2]
+    out = torch.zeros(b, s, hq, d, dtype=torch.float32, device=q.device)
+    for i in range(b):
+        a, c = int(lq[i]), int(lkv[i])
+        qq = q[i, :a].float().permute(1, 0, 2)
+        kk = k[i, :c].float().permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        vv = v[i, :c].float().permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        sc = (qq @ kk.transpose(1, 2)) * scale
+        if causal:
+            ii = torch.arange(a, device=q.device)[:, None]
+            jj = torch.arange(c, device=q.device)[None, :]
+            sc = sc.masked_fill(jj > ii + (c - a), float("-inf"))
+        out[i, :a] = torch.softmax(sc, -1).matmul(vv).permute(1, 0, 2)
+    return out
+
+
+def _prefill(q, k, v, lq, lkv, hq, hkv, layout, sparse_mode, lse=False):
+    b, s = q.shape[0], q.shape[1]
+    d = q.shape[3]
+    if layout == "BSH":
+        qa, ka, va = q.reshape(b, s, hq * d), k.reshape(b, k.shape[1], hkv * d), v.reshape(b, v.shape[1], hkv * d)
+    elif layout == "BNSD":
+        qa, ka, va = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    else:
+        qa, ka, va = q, k, v
+    out, l = torch.ops.air.npu_fused_infer_attention_score(
+        qa, ka, va, actual_seq_lengths=lq.to(DEV), actual_seq_lengths_kv=lkv.to(DEV), num_heads=hq,
+        num_key_value_heads=hkv, input_layout=layout, scale=1.0 / math.sqrt(d), sparse_mode=sparse_mode,
+        softmax_lse_flag=lse)
+    if layout == "BSH":
+        out = out.reshape(b, s, hq, d)
+    elif layout == "BNSD":
+        out = out.transpose(1, 2)
+    return out, l
+
+
+def test_prefill_cfg3_full_size():
+    g = torch.Generator(device=DEV).manual_seed(110)
+    b, s, hq, hkv, d = 4, 4096, 32, 8, 128
+    q = torch.randn(b, s, hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=g, device=DEV).to(torch.bfloat16)
+    lens = torch.tensor([4096, 3072, 2048, 1024], dtype=torch.int64)
+    out, _ = _prefill(q, k, v, lens, lens, hq, hkv, "BSH", 3)
+    ref = _prefill_ref_torch(q, k, v, lens, lens, True, 1.0 / math.sqrt(d))
+    for i in range(b):
+        L = int(lens[i])
+        torch.testing.assert_close(out[i, :L].float(), ref[i, :L], rtol=1e-2, atol=1e-2)
+        assert (out[i, L:] == 0).all()
+
+
+@pytest.mark.parametrize("layout", ["BSH", "BSND", "BNSD"])
+@pytest.mark.parametrize("sparse_mode,causal", [(3, 1), (0, 0), (2, 2)])
+def test_prefill_oracle(layout, sparse_mode, causal):
+    gen = torch.Generator().manual_seed(111)
+    b, s, hq, hkv, d = 3, 200, 8, 2, 64 if layout == "BNSD" else 128
+    q = torch.randn(b, s, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    lq = torch.tensor([200, 150, 37])
+    lkv = torch.tensor([200, 180, 37]) if causal != 2 else lq.clone()
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lq, lkv, hq, hkv, layout, sparse_mode, lse=True)
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lq.numpy(), lkv.numpy(), causal, 1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    got = lse.cpu().numpy().reshape(b, hq, s)
+    np.testing.assert_allclose(np.where(np.isfinite(got), got, -1e30), np.where(np.isfinite(wl), wl, -1e30),
+                               rtol=1e-3, atol=1e-3)
+
+
+def _mla_case(lens, h, bs, seed):
+    g = torch.Generator().manual_seed(seed)
+    b = len(lens)
+    nb = [(L + bs - 1) // bs for L in lens]
+    total = sum(nb) + 2
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(b, max(nb), dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    qn = torch.randn(b, 1, h, 512, generator=g).to(torch.bfloat16)
+    qr = torch.randn(b, 1, h, 64, generator=g).to(torch.bfloat16)
+    ckv = torch.randint(-127, 128, (total, bs, 1, 512), generator=g, dtype=torch.int8)
+    cs = torch.rand(total, bs, generator=g) * 9e-3 + 1e-3
+    kr = torch.randn(total, bs, 1, 64, generator=g).to(torch.bfloat16)
+    return qn, qr, ckv, cs, kr, bt
+
+
+def _check_mla(lens, h, bs, seed):
+    qn, qr, ckv, cs, kr, bt = _mla_case(lens, h, bs, seed)
+    scale = 1.0 / math.sqrt(192)
+    out, lse = torch.ops.air.npu_fused_infer_attention_score(
+        qn.to(DEV), ckv.to(DEV), ckv.to(DEV), query_rope=qr.to(DEV), key_rope=kr.to(DEV),
+        key_antiquant_scale=cs.to(DEV), key_antiquant_mode=1, block_table=bt.to(DEV),
+        actual_seq_lengths_kv=torch.tensor(lens, device=DEV), num_heads=h, num_key_value_heads=1,
+        input_layout="BSND", block_size=bs, scale=scale, softmax_lse_flag=True)
+    assert out.shape == (len(lens), 1, h, 512)
+    want, wl = G.mla_decode_attention(f32np(qn[:, 0]), f32np(qr[:, 0]), ckv[:, :, 0].numpy(), cs.numpy(),
+                                      f32np(kr[:, :, 0]), bt.numpy(), lens, scale)
+    assert_close(f32np(out[:, 0]), want)
+    got = lse.reshape(len(lens), h).cpu().numpy()
+    np.testing.assert_allclose(np.where(np.isfinite(got), got, -1e30), np.where(np.isfinite(wl), wl, -1e30),
+                               rtol=1e-3, atol=1e-3)
+
+
+def test_mla_small():
+    _check_mla([1, 40, 1100, 0, 2049], 128, 64, 120)
+
+
+def test_mla_cfg5():
+    g = torch.Generator().manual_seed(121)
+    lens = torch.randint(2048, 8193, (128,), generator=g).tolist()
+    _check_mla(lens, 128, 128, 122)

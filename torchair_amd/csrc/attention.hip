@@ -1,23 +1,752 @@
-// npu_fused_infer_attention_score kernels (placeholder entry points until the kernels land).
+// npu_fused_infer_attention_score kernels: paged GQA decode, dense (causal) prefill and
+// MLA absorbed decode over an int8 latent cache.
 #include "common.h"
 
-extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t, int, int, int64_t, int) { return 0; }
-extern "C" int tai_fia_paged_decode(const void*, const void*, const void*, int64_t, int64_t, int64_t, const int32_t*,
-                                    int64_t, const int64_t*, int64_t, int, int, int, int, float, void*, float*, void*,
-                                    size_t, void*) {
-  tai::set_error("tai_fia_paged_decode: not implemented yet");
-  return TAI_ERR_UNSUPPORTED;
+namespace tai {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
+
+// ============================================================================ paged GQA decode
+// Work unit = (sequence b, kv head, split of kChunk tokens), one wave each. Per 32-token step:
+//   S = Q K^T with v_mfma_f32_16x16x32_bf16 (rows = the G query heads of this kv head, padded to
+//   16; columns = 16 tokens; K fragments loaded straight from the paged cache, 64 contiguous
+//   bytes per token row and lane group), online softmax in the exp2 domain, P staged through
+//   LDS as bf16, V staged through LDS and read transposed, O += P V with the same MFMA.
+// Each unit writes an unnormalised partial (O, running max, running sum); a second kernel
+// merges the splits of each (b, head) and writes bf16 output and the logsumexp.
+constexpr int kChunk = 256;  // tokens per split (multiple of the 32-token step)
+constexpr int kStep = 32;
+
+struct DecodeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t sb, ss, sh;  // cache strides (elements): block, slot, head
+  const int32_t* bt;
+  int64_t max_blocks;
+  const int64_t* lens;
+  int64_t b;
+  int hq, hkv, g;
+  int bs;
+  float scale_log2;  // softmax scale * log2(e)
+  int nsplit;
+  float* part_o;  // [b, hkv, nsplit, 16, D]
+  float* part_ml; // [b, hkv, nsplit, 16, 2]
+};
+
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
+  constexpr int VROW = 2 * D + 8;  // bytes per LDS V row (pad spreads the transposed reads over banks)
+  __shared__ __attribute__((aligned(16))) char s_v[kStep * VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[16 * kStep];
+  const int lane = threadIdx.x;
+  const int64_t unit = blockIdx.x;
+  const int split = static_cast<int>(unit % a.nsplit);
+  const int64_t bk = unit / a.nsplit;
+  const int kvh = static_cast<int>(bk % a.hkv);
+  const int64_t b = bk / a.hkv;
+  const int64_t L = a.lens[b];
+  const int64_t t_begin = static_cast<int64_t>(split) * kChunk;
+  const int64_t t_end = min<int64_t>(L, t_begin + kChunk);
+  const int row = lane & 15, grp = lane >> 4;
+
+  float* po = a.part_o + unit * 16 * D;
+  float* pml = a.part_ml + unit * 32;
+  if (t_begin >= t_end) {  // empty split: a neutral partial
+    if (lane < 16) { pml[2 * lane] = -INFINITY; pml[2 * lane + 1] = 0.0f; }
+    return;
+  }
+
+  // Q fragments: head row (padded to 16), d slots [(D/4)*grp + 8*m, +8) for MFMA m.
+  bf16x8 qf[D / 32];
+  {
+    const bool valid = row < a.g;
+    const uint16_t* qh = a.q + (b * a.hq + kvh * a.g + (valid ? row : 0)) * D;
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      uint4 v = valid ? *reinterpret_cast<const uint4*>(qh + (D / 4) * grp + 8 * m) : make_uint4(0, 0, 0, 0);
+      qf[m] = as_bf16x8(v);
+    }
+  }
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) acc[t] = f32x4{0, 0, 0, 0};
+  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  float l_run[4] = {0, 0, 0, 0};
+
+  const uint16_t* kbase = a.k + static_cast<int64_t>(kvh) * a.sh;
+  const uint16_t* vbase = a.v + static_cast<int64_t>(kvh) * a.sh;
+  const int32_t* btrow = a.bt + b * a.max_blocks;
+
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kStep) {
+    const int64_t page = btrow[t0 / a.bs];
+    const int64_t slot0 = t0 % a.bs;
+    const uint16_t* kp = kbase + page * a.sb + slot0 * a.ss;
+    const uint16_t* vp = vbase + page * a.sb + slot0 * a.ss;
+    // ---- V rows of this step into LDS (token = grp + 4*i, 8 dims per lane); zero past L.
+    constexpr int VL = (kStep * D) / (64 * 8);  // 16-byte loads per lane
+    uint4 vr[VL];
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      constexpr int LPR = D / 8;  // lanes per token row
+      const int tok = (lane / LPR) + i * (64 / LPR);
+      const int dd = (lane % LPR) * 8;
+      vr[i] = (t0 + tok < t_end) ? *reinterpret_cast<const uint4*>(vp + tok * a.ss + dd) : make_uint4(0, 0, 0, 0);
+    }
+    // ---- K fragments and S = Q K^T for two 16-token blocks.
+    f32x4 s[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      s[tb] = f32x4{0, 0, 0, 0};
+      const int tok = tb * 16 + row;
+      const uint16_t* kr = kp + tok * a.ss + (D / 4) * grp;
+#pragma unroll
+      for (int m = 0; m < D / 32; ++m) {
+        uint4 kv = *reinterpret_cast<const uint4*>(kr + 8 * m);
+        s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[m], as_bf16x8(kv), s[tb], 0, 0, 0);
+      }
+    }
+    // S layout: lane holds token (lane&15) of block tb, heads 4*grp + r.
+    float p[2][4];
+    float mx[4], alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v0 = (t0 + row < t_end) ? s[0][r] * a.scale_log2 : -INFINITY;
+      float v1 = (t0 + 16 + row < t_end) ? s[1][r] * a.scale_log2 : -INFINITY;
+      p[0][r] = v0;
+      p[1][r] = v1;
+      float mm = fmaxf(v0, v1);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o, 64));
+      const float mnew = fmaxf(m_run[r], mm);
+      alpha[r] = (m_run[r] == -INFINITY) ? 0.0f : exp2f(m_run[r] - mnew);
+      mx[r] = mnew;
+      m_run[r] = mnew;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e0 = exp2f(p[0][r] - mx[r]);
+      const float e1 = exp2f(p[1][r] - mx[r]);
+      p[0][r] = e0;
+      p[1][r] = e1;
+      float sum = e0 + e1;
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      l_run[r] = l_run[r] * alpha[r] + sum;
+    }
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] *= alpha[r];
+    // ---- stage P (bf16) and V in LDS.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int head = 4 * grp + r;
+      s_p[head * kStep + row] = bf16_bits(p[0][r]);
+      s_p[head * kStep + 16 + row] = bf16_bits(p[1][r]);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      constexpr int LPR = D / 8;
+      const int tok = (lane / LPR) + i * (64 / LPR);
+      const int dd = (lane % LPR) * 8;
+      uint2* dst = reinterpret_cast<uint2*>(s_v + tok * VROW + dd * 2);
+      dst[0] = make_uint2(vr[i].x, vr[i].y);
+      dst[1] = make_uint2(vr[i].z, vr[i].w);
+    }
+    __syncthreads();
+    // ---- O += P V: A = P (head rows, token slots 8*grp..+8), B = V^T read from LDS.
+    const bf16x8 pf = as_bf16x8(*reinterpret_cast<const uint4*>(s_p + row * kStep + 8 * grp));
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const int dcol = t * 16 + row;
+      u16x8 vv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vv[e] = *reinterpret_cast<const uint16_t*>(s_v + (8 * grp + e) * VROW + dcol * 2);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, __builtin_bit_cast(bf16x8, vv), acc[t], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // ---- partial out: heads 4*grp + r, d = 16*t + row.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int head = 4 * grp + r;
+    if (head < a.g) {
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) po[head * D + t * 16 + row] = acc[t][r];
+      if (row == 0) {
+        pml[2 * head] = m_run[r];
+        pml[2 * head + 1] = l_run[r];
+      }
+    }
+  }
 }
-extern "C" int tai_fia_prefill(const void*, const void*, const void*, int64_t, int64_t, int64_t, int, int, int,
-                               const int64_t*, const int64_t*, const int64_t*, const int64_t*, const int64_t*,
-                               const int64_t*, int, float, void*, float*, void*) {
-  tai::set_error("tai_fia_prefill: not implemented yet");
-  return TAI_ERR_UNSUPPORTED;
+
+// Merge the splits of one (b, q head): one workgroup of D threads.
+template <int D>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint16_t* out, float* lse) {
+  const int64_t bh = blockIdx.x;
+  const int h = static_cast<int>(bh % a.hq);
+  const int64_t b = bh / a.hq;
+  const int kvh = h / a.g, hi = h % a.g;
+  const int64_t base = (b * a.hkv + kvh) * a.nsplit;
+  const int64_t L = a.lens[b];
+  const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kChunk - 1) / kChunk));
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base + s) * 32 + 2 * hi]);
+  float den = 0.0f, num = 0.0f;
+  const int d = threadIdx.x;
+  for (int s = 0; s < ns; ++s) {
+    const float m = a.part_ml[(base + s) * 32 + 2 * hi];
+    if (m == -INFINITY) continue;
+    const float w = exp2f(m - M);
+    den += w * a.part_ml[(base + s) * 32 + 2 * hi + 1];
+    if (d < D) num += w * a.part_o[((base + s) * 16 + hi) * D + d];
+  }
+  if (d < D) out[(b * a.hq + h) * D + d] = f32_to_bf16(den > 0.0f ? num / den : 0.0f);
+  if (lse && d == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
-extern "C" size_t tai_fia_mla_decode_workspace_size(int64_t, int, int, int64_t, int) { return 0; }
-extern "C" int tai_fia_mla_decode(const void*, const void*, const int8_t*, const float*, const void*, const int32_t*,
-                                  int64_t, const int64_t*, int64_t, int, int, int, int, float, void*, float*, void*,
-                                  size_t, void*) {
-  tai::set_error("tai_fia_mla_decode: not implemented yet");
-  return TAI_ERR_UNSUPPORTED;
+
+size_t decode_ws(int64_t b, int hkv, int d, int nsplit) {
+  return static_cast<size_t>(b) * hkv * nsplit * (16 * d + 32) * sizeof(float);
+}
+
+
+// ============================================================================ dense prefill
+// Work: (batch b, kv head, group of 4 "wave units"); a wave unit is (query head, 32 query rows).
+// Units of one workgroup share the kv head, so K/V tiles of 64 tokens are staged once in LDS
+// and used by all four waves. Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 puts one
+// query per lane (column), so the online-softmax rescale of O^T is a per-lane scalar and P^T
+// leaves the S^T registers already in the B-operand layout of O^T = V^T P^T.
+constexpr int kPQ = 32;    // query rows per wave
+constexpr int kPKV = 64;   // kv tokens per LDS tile
+
+struct PrefillArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;
+  float* lse;
+  int64_t qs[3], ks[3], vs[3], os[3];  // element strides (batch, pos, head)
+  const int64_t* lq;
+  const int64_t* lkv;
+  int64_t s_q, s_kv;
+  int hq, hkv, g;
+  int causal;
+  float scale_log2;
+  int n_qt;            // query tiles per sequence
+  int units_per_bk;    // n_qt * g
+  int blocks_per_bk;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+  constexpr int ROW = 2 * D + 16;  // LDS row bytes: 4 rows apart shift 16 banks
+  __shared__ __attribute__((aligned(16))) char s_k[kPKV * ROW];
+  __shared__ __attribute__((aligned(16))) char s_v[kPKV * ROW];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int col = lane & 31, grp = lane >> 5;
+  // heavy (late) query tiles first
+  const int64_t blk = blockIdx.x;
+  const int jb = a.blocks_per_bk - 1 - static_cast<int>(blk % a.blocks_per_bk);
+  const int64_t bk = blk / a.blocks_per_bk;
+  const int kvh = static_cast<int>(bk % a.hkv);
+  const int64_t b = bk / a.hkv;
+  const int unit = jb * 4 + w;
+  const bool unit_ok = unit < a.units_per_bk;
+  const int qt = unit_ok ? unit / a.g : 0;
+  const int head = kvh * a.g + (unit_ok ? unit % a.g : 0);
+  const int64_t Lq = a.lq ? a.lq[b] : a.s_q;
+  const int64_t Lkv = a.lkv ? a.lkv[b] : a.s_kv;
+  const int64_t shift = Lkv - Lq;  // right-down causal offset
+  const int64_t q0 = static_cast<int64_t>(qt) * kPQ;
+  const int64_t myq = q0 + col;
+
+  // kv extent of this wave and of the whole workgroup (uniform across the workgroup)
+  auto kv_limit = [&](int64_t qlast) -> int64_t {
+    if (a.causal == 1) return min<int64_t>(Lkv, qlast + shift + 1);
+    if (a.causal == 2) return min<int64_t>(Lkv, qlast + 1);
+    return Lkv;
+  };
+  const bool wave_live = unit_ok && q0 < Lq;
+  const int64_t wave_kv = wave_live ? max<int64_t>(0, kv_limit(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
+  int64_t blk_kv = 0;
+  {
+    const int last_unit = min(jb * 4 + 3, a.units_per_bk - 1);
+    const int qt_hi = last_unit / a.g;  // units are qtile-major, so the last unit has the largest tile
+    const int64_t qlast = min<int64_t>(static_cast<int64_t>(qt_hi) * kPQ + kPQ, Lq) - 1;
+    blk_kv = qlast >= 0 ? max<int64_t>(0, kv_limit(qlast)) : 0;
+  }
+
+  // Q^T fragments (B operand): query = col, d slots 16*kd + 8*grp .. +8
+  bf16x8 qf[D / 16];
+  {
+    const bool ok = wave_live && myq < Lq;
+    const uint16_t* qp = a.q + b * a.qs[0] + (ok ? myq : 0) * a.qs[1] + head * a.qs[2];
+#pragma unroll
+    for (int kd = 0; kd < D / 16; ++kd)
+      qf[kd] = as_bf16x8(ok ? *reinterpret_cast<const uint4*>(qp + 16 * kd + 8 * grp) : make_uint4(0, 0, 0, 0));
+  }
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int64_t qlim = (a.causal == 1) ? myq + shift : (a.causal == 2 ? myq : INT64_MAX);
+
+  for (int64_t t0 = 0; t0 < blk_kv; t0 += kPKV) {
+    // ---- stage K and V tiles: 16 lanes per token row, 16 rows per pass
+    constexpr int LPR = D / 8;
+    constexpr int RPP = 256 / LPR;
+#pragma unroll
+    for (int pass = 0; pass < kPKV / RPP; ++pass) {
+      const int tok = pass * RPP + tid / LPR;
+      const int dd = (tid % LPR) * 8;
+      const int64_t t = t0 + tok;
+      uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
+      if (t < Lkv) {
+        kv4 = *reinterpret_cast<const uint4*>(a.k + b * a.ks[0] + t * a.ks[1] + kvh * a.ks[2] + dd);
+        vv4 = *reinterpret_cast<const uint4*>(a.v + b * a.vs[0] + t * a.vs[1] + kvh * a.vs[2] + dd);
+      }
+      *reinterpret_cast<uint4*>(s_k + tok * ROW + dd * 2) = kv4;
+      *reinterpret_cast<uint4*>(s_v + tok * ROW + dd * 2) = vv4;
+    }
+    __syncthreads();
+    if (wave_live && t0 < wave_kv) {
+      f32x16 s[2];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
+        if (t0 + 32 * st < wave_kv) {
+#pragma unroll
+          for (int kd = 0; kd < D / 16; ++kd) {
+            const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(s_k + (32 * st + col) * ROW + (16 * kd + 8 * grp) * 2));
+            s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kd], s[st], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t t = t0 + 32 * st + 8 * (r >> 2) + 4 * grp + (r & 3);
+          const bool ok = t < Lkv && t <= qlim;
+          const float v = ok ? s[st][r] * a.scale_log2 : -INFINITY;
+          s[st][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      float rs = 0.0f;
+      bf16x8 pf[4];
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float e = exp2f(s[st][8 * kb2 + j] - m_use);
+            rs += e;
+            pf[2 * st + kb2][j] = static_cast<__bf16>(e);
+          }
+      rs += __shfl_xor(rs, 32, 64);
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+      // ---- O^T += V^T P^T: k-slots of lane group grp in k-block kb are tokens
+      //      16kb + 4grp + {0..3} and 16kb + 8 + 4grp + {0..3}
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        if (t0 + 16 * kb >= wave_kv) break;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const int dcol = 32 * dt + col;
+          u16x8 vv;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int tok = 16 * kb + 8 * (j >> 2) + 4 * grp + (j & 3);
+            vv[j] = *reinterpret_cast<const uint16_t*>(s_v + tok * ROW + dcol * 2);
+          }
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pf[kb], acc[dt], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (!unit_ok || myq >= a.s_q) return;
+  // ---- write O (lane = query col, d = 32dt + 8(r/4) + 4grp + r%4) and lse
+  const bool live = wave_live && myq < Lq && l_run > 0.0f;
+  const float inv = live ? 1.0f / l_run : 0.0f;
+  uint16_t* op = a.out + b * a.os[0] + myq * a.os[1] + head * a.os[2];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d = 32 * dt + 8 * r4 + 4 * grp;
+      uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4] * inv)) |
+                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 1] * inv)) << 16);
+      uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 2] * inv)) |
+                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 3] * inv)) << 16);
+      *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
+    }
+  if (a.lse && grp == 0)
+    a.lse[(b * a.hq + head) * a.s_q + myq] = live ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
+}
+
+// ============================================================================ MLA absorbed decode
+// Work: (sequence b, split of kMlaChunk tokens, group of 64 query heads); 4 waves x 16 heads.
+// Per 32-token step the int8 latent rows (exactly representable in bf16) and the bf16 rope keys
+// are staged once in LDS ([token][Dn + Dr]) and shared by the four waves. The per-token scale
+// c[t] = int8[t] * scale[t] is folded into the scores (S = (q_nope.int8 * scale + q_rope.k_rope))
+// and into P before O^T = C^T P'^T, so the MFMAs see unscaled integers.
+constexpr int kMlaChunk = 1024;
+constexpr int kMlaStep = 32;
+constexpr int kMlaHeads = 64;  // heads per workgroup
+
+struct MlaArgs {
+  const uint16_t* qn;
+  const uint16_t* qr;
+  const int8_t* ckv;
+  const float* cs;
+  const uint16_t* kr;
+  const int32_t* bt;
+  int64_t max_blocks;
+  const int64_t* lens;
+  int64_t b;
+  int hq, bs, nsplit, hgroups;
+  float scale_log2;
+  float* part_o;   // [b, nsplit, hq, DN]
+  float* part_ml;  // [b, nsplit, hq, 2]
+};
+
+template <int DN, int DR>
+__global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
+  constexpr int DK = DN + DR;
+  constexpr int ROW = 2 * DK + 16;  // LDS bytes per token row
+  __shared__ __attribute__((aligned(16))) char s_lat[kMlaStep * ROW];
+  __shared__ float s_cs[kMlaStep];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int hcol = lane & 15, grp = lane >> 4;
+  const int64_t blk = blockIdx.x;
+  const int hg = static_cast<int>(blk % a.hgroups);
+  const int split = static_cast<int>((blk / a.hgroups) % a.nsplit);
+  const int64_t b = blk / (static_cast<int64_t>(a.hgroups) * a.nsplit);
+  const int64_t L = a.lens[b];
+  const int64_t t_begin = static_cast<int64_t>(split) * kMlaChunk;
+  const int64_t t_end = min<int64_t>(L, t_begin + kMlaChunk);
+  const int head = hg * kMlaHeads + w * 16 + hcol;
+  const bool head_ok = head < a.hq;
+  const int64_t pbase = (b * a.nsplit + split) * a.hq;
+  if (t_begin >= t_end) {
+    if (grp == 0 && head_ok) { a.part_ml[(pbase + head) * 2] = -INFINITY; a.part_ml[(pbase + head) * 2 + 1] = 0.0f; }
+    return;
+  }
+  // Q^T fragments (B operand): head = hcol, d slots 32*m + 8*grp .. +8
+  bf16x8 qf[DK / 32];
+  {
+    const uint16_t* qnp = a.qn + (b * a.hq + (head_ok ? head : 0)) * DN;
+    const uint16_t* qrp = a.qr + (b * a.hq + (head_ok ? head : 0)) * DR;
+#pragma unroll
+    for (int m = 0; m < DK / 32; ++m) {
+      const int d = 32 * m + 8 * grp;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (head_ok) v = d < DN ? *reinterpret_cast<const uint4*>(qnp + d) : *reinterpret_cast<const uint4*>(qrp + d - DN);
+      qf[m] = as_bf16x8(v);
+    }
+  }
+  f32x4 acc[DN / 16];
+#pragma unroll
+  for (int i = 0; i < DN / 16; ++i) acc[i] = f32x4{0, 0, 0, 0};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int32_t* btrow = a.bt + b * a.max_blocks;
+
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kMlaStep) {
+    const int64_t page = btrow[t0 / a.bs];
+    const int64_t slot0 = t0 % a.bs;
+    // ---- stage: int8 latent -> bf16 (16 values per thread per pass), rope rows, scales
+    {
+      constexpr int LPR = DN / 16;          // threads per latent row
+      constexpr int RPP = 256 / LPR;        // rows per pass
+#pragma unroll
+      for (int pass = 0; pass < kMlaStep / RPP; ++pass) {
+        const int tok = pass * RPP + tid / LPR;
+        const int dd = (tid % LPR) * 16;
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (t0 + tok < t_end) raw = *reinterpret_cast<const uint4*>(a.ckv + ((page * a.bs + slot0 + tok) * DN + dd));
+        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float f0 = static_cast<float>(static_cast<int8_t>(wv[i] & 0xff));
+          const float f1 = static_cast<float>(static_cast<int8_t>((wv[i] >> 8) & 0xff));
+          const float f2 = static_cast<float>(static_cast<int8_t>((wv[i] >> 16) & 0xff));
+          const float f3 = static_cast<float>(static_cast<int8_t>(wv[i] >> 24));
+          o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+          o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+        }
+        uint4* dst = reinterpret_cast<uint4*>(s_lat + tok * ROW + dd * 2);
+        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+      constexpr int RL = DR / 8;  // threads per rope row
+      if (tid < kMlaStep * RL) {
+        const int tok = tid / RL, dd = (tid % RL) * 8;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (t0 + tok < t_end) v = *reinterpret_cast<const uint4*>(a.kr + (page * a.bs + slot0 + tok) * DR + dd);
+        *reinterpret_cast<uint4*>(s_lat + tok * ROW + (DN + dd) * 2) = v;
+      }
+      if (tid < kMlaStep) s_cs[tid] = (t0 + tid < t_end) ? a.cs[page * a.bs + slot0 + tid] : 0.0f;
+    }
+    __syncthreads();
+    // ---- S^T = K Q^T, nope and rope parts kept apart (A = latent rows: token = 16tb + hcol)
+    f32x4 sn[2], sr[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      sn[tb] = f32x4{0, 0, 0, 0};
+      sr[tb] = f32x4{0, 0, 0, 0};
+      const char* rowp = s_lat + (16 * tb + hcol) * ROW;
+#pragma unroll
+      for (int m = 0; m < DK / 32; ++m) {
+        const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(rowp + (32 * m + 8 * grp) * 2));
+        if (32 * m < DN) sn[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], sn[tb], 0, 0, 0);
+        else sr[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], sr[tb], 0, 0, 0);
+      }
+    }
+    // S^T layout: lane holds head hcol, tokens 16tb + 4grp + r.
+    float sv[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 16 * tb + 4 * grp + r;
+        const float v = (t0 + tok < t_end) ? (sn[tb][r] * s_cs[tok] + sr[tb][r]) * a.scale_log2 : -INFINITY;
+        sv[tb][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+    float rs = 0.0f;
+    bf16x8 pf;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 16 * tb + 4 * grp + r;
+        const float e = exp2f(sv[tb][r] - m_new);
+        rs += e;
+        pf[4 * tb + r] = static_cast<__bf16>(e * s_cs[tok]);
+      }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+    // ---- O^T += C^T P'^T; k-slots of lane group grp: tokens 4grp + {0..3}, 16 + 4grp + {0..3}
+#pragma unroll
+    for (int dt = 0; dt < DN / 16; ++dt) {
+      const int dcol = 16 * dt + hcol;
+      u16x8 vv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tok = 16 * (j >> 2) + 4 * grp + (j & 3);
+        vv[j] = *reinterpret_cast<const uint16_t*>(s_lat + tok * ROW + dcol * 2);
+      }
+      acc[dt] = acc[dt] * alpha;
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pf, acc[dt], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  if (!head_ok) return;
+  // ---- partial: O^T[d = 16dt + 4grp + r][head]
+  float* po = a.part_o + (pbase + head) * DN;
+#pragma unroll
+  for (int dt = 0; dt < DN / 16; ++dt)
+    *reinterpret_cast<float4*>(po + 16 * dt + 4 * grp) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+  if (grp == 0) {
+    a.part_ml[(pbase + head) * 2] = m_run;
+    a.part_ml[(pbase + head) * 2 + 1] = l_run;
+  }
+}
+
+template <int DN>
+__global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* out, float* lse) {
+  const int64_t bh = blockIdx.x;
+  const int h = static_cast<int>(bh % a.hq);
+  const int64_t b = bh / a.hq;
+  const int64_t L = a.lens[b];
+  const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kMlaChunk - 1) / kMlaChunk));
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((b * a.nsplit + s) * a.hq + h) * 2]);
+  float den = 0.0f;
+  float num[DN / 256];
+#pragma unroll
+  for (int i = 0; i < DN / 256; ++i) num[i] = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const int64_t pi = (b * a.nsplit + s) * a.hq + h;
+    const float m = a.part_ml[pi * 2];
+    if (m == -INFINITY) continue;
+    const float wgt = exp2f(m - M);
+    den += wgt * a.part_ml[pi * 2 + 1];
+#pragma unroll
+    for (int i = 0; i < DN / 256; ++i) num[i] += wgt * a.part_o[pi * DN + threadIdx.x + 256 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < DN / 256; ++i)
+    out[(b * a.hq + h) * DN + threadIdx.x + 256 * i] = f32_to_bf16(den > 0.0f ? num[i] / den : 0.0f);
+  if (lse && threadIdx.x == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
+}
+
+size_t mla_ws(int64_t b, int hq, int dn, int nsplit) {
+  return static_cast<size_t>(b) * nsplit * hq * (dn + 2) * sizeof(float);
+}
+}  // namespace
+}  // namespace tai
+
+using namespace tai;
+
+extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, int64_t max_blocks, int block_size) {
+  (void)hq;
+  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kChunk));
+  // sized for hkv == hq (the largest the kernel can be asked for)
+  return decode_ws(b, hq, d, nsplit) + 256;
+}
+
+extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block,
+                                    int64_t stride_slot, int64_t stride_head, const int32_t* block_table,
+                                    int64_t max_blocks, const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
+                                    int block_size, float scale, void* out, float* lse, void* workspace,
+                                    size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(b >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_paged_decode: heads must be a multiple of kv heads");
+  TAI_UNSUPPORTED(hq / hkv > 16, "tai_fia_paged_decode: at most 16 query heads per kv head (got %d)", hq / hkv);
+  TAI_UNSUPPORTED(d != 64 && d != 128 && d != 256, "tai_fia_paged_decode: head_dim %d not supported (64/128/256)", d);
+  TAI_UNSUPPORTED(block_size <= 0 || block_size % kStep != 0, "tai_fia_paged_decode: block_size must be a multiple of %d", kStep);
+  TAI_CHECK_ARG((stride_slot % 8) == 0 && (stride_head % 8) == 0 && (stride_block % 8) == 0,
+                "tai_fia_paged_decode: cache strides must keep 16-byte alignment");
+  if (b == 0) return TAI_OK;
+  TAI_CHECK_ARG(q && k_cache && v_cache && block_table && seq_lens_kv && out, "tai_fia_paged_decode: null pointer");
+  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kChunk));
+  const size_t need = decode_ws(b, hkv, d, nsplit);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_fia_paged_decode: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k_cache);
+  a.v = static_cast<const uint16_t*>(v_cache);
+  a.sb = stride_block; a.ss = stride_slot; a.sh = stride_head;
+  a.bt = block_table; a.max_blocks = max_blocks; a.lens = seq_lens_kv;
+  a.b = b; a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.bs = block_size;
+  a.scale_log2 = scale * kLog2e;
+  a.nsplit = nsplit;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + static_cast<size_t>(b) * hkv * nsplit * 16 * d;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(b * hkv * nsplit));
+  const dim3 cgrid(static_cast<unsigned>(b * hq));
+  uint16_t* o = static_cast<uint16_t*>(out);
+  switch (d) {
+    case 64:
+      paged_decode_kernel<64><<<grid, 64, 0, st>>>(a);
+      decode_combine_kernel<64><<<cgrid, 64, 0, st>>>(a, o, lse);
+      break;
+    case 128:
+      paged_decode_kernel<128><<<grid, 64, 0, st>>>(a);
+      decode_combine_kernel<128><<<cgrid, 128, 0, st>>>(a, o, lse);
+      break;
+    default:
+      paged_decode_kernel<256><<<grid, 64, 0, st>>>(a);
+      decode_combine_kernel<256><<<cgrid, 256, 0, st>>>(a, o, lse);
+      break;
+  }
+  return launch_status("tai_fia_paged_decode");
+}
+
+extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q, int64_t s_kv, int hq,
+                               int hkv, int d, const int64_t* q_strides, const int64_t* k_strides,
+                               const int64_t* v_strides, const int64_t* out_strides, const int64_t* seq_lens_q,
+                               const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
+                               void* stream) {
+  TAI_CHECK_ARG(b >= 0 && s_q >= 0 && s_kv >= 0, "tai_fia_prefill: negative size");
+  TAI_CHECK_ARG(hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_prefill: heads must be a multiple of kv heads");
+  TAI_CHECK_ARG(causal >= 0 && causal <= 2, "tai_fia_prefill: causal must be 0, 1 (right-down) or 2 (left-up)");
+  TAI_UNSUPPORTED(d != 64 && d != 128, "tai_fia_prefill: head_dim %d not supported (64, 128)", d);
+  TAI_CHECK_ARG(q_strides && k_strides && v_strides && out_strides, "tai_fia_prefill: null strides");
+  for (int i = 0; i < 3; ++i)
+    TAI_CHECK_ARG(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && out_strides[i] % 4 == 0,
+                  "tai_fia_prefill: strides must keep 16-byte rows");
+  if (b == 0 || s_q == 0) return TAI_OK;
+  TAI_CHECK_ARG(q && k && v && out, "tai_fia_prefill: null pointer");
+  PrefillArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  for (int i = 0; i < 3; ++i) { a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = out_strides[i]; }
+  a.lq = seq_lens_q; a.lkv = seq_lens_kv; a.s_q = s_q; a.s_kv = s_kv;
+  a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.causal = causal; a.scale_log2 = scale * kLog2e;
+  a.n_qt = static_cast<int>(cdiv(s_q, kPQ));
+  a.units_per_bk = a.n_qt * a.g;
+  a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, 4));
+  const dim3 grid(static_cast<unsigned>(b * hkv * a.blocks_per_bk));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d == 64) prefill_kernel<64><<<grid, 256, 0, st>>>(a);
+  else prefill_kernel<128><<<grid, 256, 0, st>>>(a);
+  return launch_status("tai_fia_prefill");
+}
+
+extern "C" size_t tai_fia_mla_decode_workspace_size(int64_t b, int hq, int dn, int64_t max_blocks, int block_size) {
+  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kMlaChunk));
+  return mla_ws(b, hq, dn, nsplit) + 256;
+}
+
+extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const int8_t* ckv_cache, const float* ckv_scale,
+                                  const void* krope_cache, const int32_t* block_table, int64_t max_blocks,
+                                  const int64_t* seq_lens_kv, int64_t b, int hq, int dn, int dr, int block_size,
+                                  float scale, void* out, float* lse, void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(b >= 0 && hq > 0, "tai_fia_mla_decode: bad sizes");
+  TAI_UNSUPPORTED(dn != 512 || dr != 64, "tai_fia_mla_decode: only kv_lora_rank 512 with rope dim 64 is supported");
+  TAI_UNSUPPORTED(block_size <= 0 || block_size % kMlaStep != 0, "tai_fia_mla_decode: block_size must be a multiple of %d",
+                  kMlaStep);
+  if (b == 0) return TAI_OK;
+  TAI_CHECK_ARG(q_nope && q_rope && ckv_cache && ckv_scale && krope_cache && block_table && seq_lens_kv && out,
+                "tai_fia_mla_decode: null pointer");
+  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kMlaChunk));
+  const size_t need = mla_ws(b, hq, dn, nsplit);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_fia_mla_decode: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  MlaArgs a;
+  a.qn = static_cast<const uint16_t*>(q_nope);
+  a.qr = static_cast<const uint16_t*>(q_rope);
+  a.ckv = ckv_cache; a.cs = ckv_scale; a.kr = static_cast<const uint16_t*>(krope_cache);
+  a.bt = block_table; a.max_blocks = max_blocks; a.lens = seq_lens_kv; a.b = b; a.hq = hq; a.bs = block_size;
+  a.nsplit = nsplit; a.hgroups = static_cast<int>(cdiv(hq, kMlaHeads)); a.scale_log2 = scale * kLog2e;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + static_cast<size_t>(b) * nsplit * hq * dn;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  mla_decode_kernel<512, 64><<<dim3(static_cast<unsigned>(b * nsplit * a.hgroups)), 256, 0, st>>>(a);
+  mla_combine_kernel<512><<<dim3(static_cast<unsigned>(b * hq)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
+  return launch_status("tai_fia_mla_decode");
 }
