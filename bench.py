@@ -213,6 +213,80 @@ def bench_decode(torch, dev, iters=50):
             "algorithmic_bytes": kv_bytes}
 
 
+# ----------------------------------------------------------------------------- causal prefill (config 3)
+def bench_prefill(torch, dev, iters=10):
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    B, S, HQ, HKV, D = 4, 4096, 32, 8, 128
+    q = torch.randn(B, S, HQ * D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, S, HKV * D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, S, HKV * D, generator=g, device=dev).to(torch.bfloat16)
+    lens = torch.tensor([4096, 3072, 2048, 1024], device=dev)
+
+    def run():
+        return torch.ops.air.npu_fused_infer_attention_score(
+            q, k, v, actual_seq_lengths=lens, actual_seq_lengths_kv=lens, num_heads=HQ, num_key_value_heads=HKV,
+            input_layout="BSH", scale=1.0 / D ** 0.5, sparse_mode=3)
+
+    for _ in range(2):
+        run()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    flops = sum(8192 * L * (L + 1) for L in (4096, 3072, 2048, 1024))
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": flops}
+
+
+# ----------------------------------------------------------------------------- MLA decode (config 5)
+def bench_mla(torch, dev, iters=20):
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    B, H, DN, DR, BS = 128, 128, 512, 64, 128
+    lens = torch.randint(2048, 8193, (B,), generator=g, device=dev)
+    nb = (lens + BS - 1) // BS
+    total = int(nb.sum())
+    perm = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    bt = torch.zeros(B, int(nb.max()), dtype=torch.int32, device=dev)
+    off = 0
+    for b, n in enumerate(nb.tolist()):
+        bt[b, :n] = perm[off:off + n]
+        off += n
+    qn = torch.randn(B, 1, H, DN, generator=g, device=dev).to(torch.bfloat16)
+    qr = torch.randn(B, 1, H, DR, generator=g, device=dev).to(torch.bfloat16)
+    ckv = torch.randint(-127, 128, (total, BS, 1, DN), generator=g, device=dev, dtype=torch.int8)
+    cs = torch.rand(total, BS, generator=g, device=dev) * 9e-3 + 1e-3
+    kr = torch.randn(total, BS, 1, DR, generator=g, device=dev).to(torch.bfloat16)
+
+    def run():
+        return torch.ops.air.npu_fused_infer_attention_score(
+            qn, ckv, ckv, query_rope=qr, key_rope=kr, key_antiquant_scale=cs, key_antiquant_mode=1,
+            block_table=bt, actual_seq_lengths_kv=lens, num_heads=H, num_key_value_heads=1, input_layout="BSND",
+            block_size=BS, scale=1.0 / 192 ** 0.5)
+
+    for _ in range(2):
+        run()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    ltot = int(lens.sum())
+    flops = ltot * H * 2 * (DN + DR + DN)
+    byts = ltot * (DN + 2 * DR + 4) + B * H * (DN + DR) * 2 + B * H * DN * 2
+    tf = flops / (ms * 1e-3) / 1e12
+    gbs = byts / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 # ----------------------------------------------------------------------------- CPU baseline (oracle)
 def cpu_baseline(sample_experts=4):
     """Oracle MoE layer on the host: full gating/routing/quant for all T tokens plus the expert
@@ -266,7 +340,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of side benches to run (gemm,mlp,decode)")
+    ap.add_argument("--only", default="", help="comma list of side benches to run (gemm,mlp,decode,prefill,mla)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (no multi-GPU path is built)"}))
@@ -280,13 +354,17 @@ def main():
     del layer
     torch.cuda.empty_cache()
     extra = {}
-    only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode"}
+    only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode", "prefill", "mla"}
     if "gemm" in only:
         extra["w8a8_gemm_8192"] = bench_gemm(torch, dev)
     if "mlp" in only:
         extra["mlp_cfg1"] = bench_mlp(torch, dev)
     if "decode" in only:
         extra["paged_decode_cfg2"] = bench_decode(torch, dev)
+    if "prefill" in only:
+        extra["causal_prefill_cfg3"] = bench_prefill(torch, dev)
+    if "mla" in only:
+        extra["mla_decode_cfg5"] = bench_mla(torch, dev)
     torch.cuda.empty_cache()
     cpu = None if args.skip_cpu else cpu_baseline()
     line = {
