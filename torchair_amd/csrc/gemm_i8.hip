@@ -345,6 +345,317 @@ void launch_tile(const GemmArgs& g, int layout, hipStream_t st) {
   else gemm_i8_kernel<BM, BN, TAI_LAYOUT_KN><<<dim3(static_cast<unsigned>(nb)), 256, 0, st>>>(g);
 }
 
+
+// ----------------------------------------------------------------------------- big-tile kernel
+// Workgroup = WM x WN waves of 64x128 (2x4 MFMA tiles, 128 int32 accumulators per lane), tile
+// BM = 64*WM rows by BN = 128*WN columns. K advances 64 bytes per stage through a ring of S LDS
+// stages filled by global_load_lds_dwordx4 (global -> LDS without registers); S-1 stages are in
+// flight while one is multiplied. The 2x2 configuration (128x256, 72 KB of LDS) runs two
+// workgroups per CU, so one workgroup's barrier wait overlaps the other's MFMAs.
+// LDS layouts (each 16-byte chunk placed by the lane that loads it, so swizzles cost nothing):
+//   A and an [N,K] weight: [rows][64 B]; chunk c of row r stored at chunk c ^ ((r >> 2) & 3)
+//     -> 16-byte fragment reads of 16 consecutive rows cover the 64 banks once.
+//   a [K,N] weight: [64 k rows][BN B]; chunk c of row r stored at chunk c ^ (r & 7); fragments
+//     are read with ds_read_b64_tr_b8 (in each 16-lane group source lane L addresses
+//     B[k0 + L/2][n0 + 8*(L&1)] and output lane j receives B[k0..k0+7][n0 + j]).
+// Requires K % 64 == 0 (stage loads cannot zero-fill a K tail). Rows and columns past the end of
+// the tile are loaded from clamped addresses and never stored.
+template <int WM, int WN, int BK, int STAGES>
+struct BigCfg {
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kBM = 64 * WM, kBN = 128 * WN, kBK = BK;
+  static constexpr int kStage = (kBM + kBN) * BK;
+  static constexpr int kStages = STAGES;
+  static constexpr int kLds = kStage * kStages;
+  static constexpr int kCpr = BK / 16;                    // 16-byte chunks per A / NK-B row
+  static constexpr int kRowShift = BK == 128 ? 1 : 2;      // rows per 256-byte bank cycle = 1 << shift
+  static constexpr int kALoads = kBM * BK / 1024 / (WM * WN);  // 1 KB load instructions per wave per stage
+  static constexpr int kBLoads = kBN * BK / 1024 / (WM * WN);
+  static constexpr int kLoads = kALoads + kBLoads;
+  static_assert(kALoads * WM * WN * 1024 == kBM * BK && kBLoads * WM * WN * 1024 == kBN * BK, "load split");
+};
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+
+// s_waitcnt with only vmcnt limited (expcnt / lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Two ds_read_b64_tr_b8 into one 16-byte fragment (bytes 0-7 from `lo`, 8-15 from `hi`),
+// issued as inline asm: the builtin makes the compiler drain the in-flight global->LDS ring
+// before the read. The caller waits lgkmcnt(0) (lds_wait_frags) before using the result.
+__device__ __forceinline__ v4i ds_read_tr8_pair(const int8_t* lo, const int8_t* hi) {
+  v2i a, b;
+  const uint32_t alo = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const int8_t*)lo));
+  const uint32_t ahi = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const int8_t*)hi));
+  asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(a) : "v"(alo));
+  asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(b) : "v"(ahi));
+  return v4i{a[0], a[1], b[0], b[1]};
+}
+
+// Waits for outstanding LDS reads; the fragments are threaded through so their uses stay after it.
+__device__ __forceinline__ void lds_wait_frags(v4i (&f)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+}
+
+template <int LAYOUT, class C>
+__device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, int row0, int rows,
+                                                int64_t n0, int64_t k0, int8_t* stage, int w, int lane) {
+  constexpr int BK = C::kBK, CPR = C::kCpr, RPI = 1024 / BK;  // rows per 1 KB instruction
+#pragma unroll
+  for (int i = 0; i < C::kALoads; ++i) {
+    const int q = C::kALoads * w + i;
+    const int row = RPI * q + lane / CPR;
+    const int c = (lane % CPR) ^ ((row >> C::kRowShift) & (CPR - 1));
+    const int rr = row < rows ? row : (rows > 0 ? rows - 1 : 0);
+    const int8_t* src = g.a + static_cast<int64_t>(row0 + rr) * g.k + k0 + 16 * c;
+    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(stage + q * 1024), 16, 0, 0);
+  }
+  int8_t* bst = stage + C::kBM * BK;
+#pragma unroll
+  for (int i = 0; i < C::kBLoads; ++i) {
+    const int q = C::kBLoads * w + i;
+    const int8_t* src;
+    if constexpr (LAYOUT == TAI_LAYOUT_NK) {
+      const int row = RPI * q + lane / CPR;
+      const int c = (lane % CPR) ^ ((row >> C::kRowShift) & (CPR - 1));
+      const int64_t nn = n0 + row < g.n ? n0 + row : g.n - 1;
+      src = bgrp + nn * g.k + k0 + 16 * c;
+    } else {
+      constexpr int CPN = C::kBN / 16;  // chunks per k row
+      const int kr = (1024 / C::kBN) * q + lane / CPN;
+      const int c = (lane % CPN) ^ (kr & 7);
+      const int64_t nn = n0 + 16 * c < g.n ? n0 + 16 * c : g.n - 16;
+      src = bgrp + (k0 + kr) * g.n + nn;
+    }
+    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(bst + q * 1024), 16, 0, 0);
+  }
+}
+
+template <int LAYOUT, int OUT, class C>
+__global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g) {
+  constexpr int WN = C::kBN / 128;
+  constexpr int kBigBK = C::kBK;
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+  const int64_t nb = g.m_slots * g.n_tiles;
+  const int64_t L = xcd_remap(blockIdx.x, nb);
+  int64_t slot, nt;
+  if (g.tile_map) {
+    slot = L / g.n_tiles;
+    nt = L % g.n_tiles;
+  } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
+    constexpr int64_t GM = 8;
+    const int64_t per_group = GM * g.n_tiles;
+    const int64_t first = (L / per_group) * GM;
+    const int64_t gsize = g.m_slots - first < GM ? g.m_slots - first : GM;
+    const int64_t in = L % per_group;
+    slot = first + in % gsize;
+    nt = in / gsize;
+  }
+  const int64_t n0 = nt * C::kBN;
+  int e = 0, row0, row1;
+  if (g.tile_map) {
+    const int4 t = g.tile_map[slot];
+    if (t.x == -1) return;
+    row0 = t.y;
+    row1 = t.z;
+    if (t.x == -2) {
+      for (int idx = threadIdx.x; idx < (row1 - row0) * C::kBN; idx += C::kThreads) {
+        const int64_t r = row0 + idx / C::kBN, c = n0 + idx % C::kBN;
+        if (c < g.n) {
+          if constexpr (OUT == TAI_DT_INT32) static_cast<int32_t*>(g.out)[r * g.n + c] = 0;
+          else store_from_f32(g.out, OUT, r * g.n + c, 0.0f);
+        }
+      }
+      return;
+    }
+    e = t.x;
+  } else {
+    row0 = static_cast<int>(slot * C::kBM);
+    row1 = row0 + C::kBM < g.m ? row0 + C::kBM : static_cast<int>(g.m);
+  }
+  const int rows = row1 - row0;
+  const int8_t* bgrp = g.b + static_cast<int64_t>(e) * g.b_group_stride;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = w / WN, wn = w % WN;
+  const int act_m = max(0, min(2, (rows - wm * 64 + 31) / 32));
+  const int64_t ncols = g.n - n0 - wn * 128;
+  const int act_n = ncols <= 0 ? 0 : (ncols >= 128 ? 4 : static_cast<int>((ncols + 31) / 32));
+
+  v16i acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int64_t nk = g.k / kBigBK;
+#pragma unroll
+  for (int s = 0; s < C::kStages - 1; ++s)
+    if (s < nk) big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, s * kBigBK, smem + s * C::kStage, w, lane);
+
+  const int arow = wm * 64 + (lane & 31);            // + 32 i
+  const int brow = wn * 128 + (lane & 31);           // + 32 j (NK)
+  const int l16 = lane & 15;
+  const int bk_lane = (lane >> 5) * 16 + (l16 >> 1);  // KN: k row within the 32-row kk block (+ 8)
+  const int bc_lane = wn * 128 + ((lane >> 4) & 1) * 16 + (l16 & 1) * 8;  // KN: byte column (+ 32 j)
+
+  auto load_a = [&](const int8_t* st, int kk, int i) {
+    const int r = arow + 32 * i;
+    const int c = (2 * kk + (lane >> 5)) ^ ((r >> C::kRowShift) & (C::kCpr - 1));
+    return *reinterpret_cast<const v4i*>(st + r * kBigBK + 16 * c);
+  };
+  auto load_b = [&](const int8_t* bs, int kk, int j) -> v4i {
+    if constexpr (LAYOUT == TAI_LAYOUT_NK) {
+      const int r = brow + 32 * j;
+      const int c = (2 * kk + (lane >> 5)) ^ ((r >> C::kRowShift) & (C::kCpr - 1));
+      return *reinterpret_cast<const v4i*>(bs + r * kBigBK + 16 * c);
+    } else {
+      const int col = bc_lane + 32 * j;
+      const int k_lo = kk * 32 + bk_lane, k_hi = k_lo + 8;
+      const int8_t* plo = bs + k_lo * C::kBN + 16 * ((col >> 4) ^ (k_lo & 7)) + (col & 15);
+      const int8_t* phi = bs + k_hi * C::kBN + 16 * ((col >> 4) ^ (k_hi & 7)) + (col & 15);
+      return ds_read_tr8_pair(plo, phi);
+    }
+  };
+
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int64_t ahead = nk - 1 - kt;  // stages issued after this one (at most kStages - 2)
+    if constexpr (C::kStages == 2) {
+      wait_vmcnt<0>();  // the only loads in flight are this stage's
+    } else {
+      if (ahead >= C::kStages - 2) wait_vmcnt<C::kLoads * (C::kStages - 2)>();
+      else if (ahead == 2) wait_vmcnt<C::kLoads * 2>();
+      else if (ahead == 1) wait_vmcnt<C::kLoads>();
+      else wait_vmcnt<0>();
+    }
+    // Workgroup barrier that orders LDS only: the ring's later stages stay in flight across it
+    // (a fence here would drain every outstanding global->LDS load).
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + C::kStages - 1 < nk)
+      big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (kt + C::kStages - 1) * kBigBK,
+                                      smem + ((kt + C::kStages - 1) % C::kStages) * C::kStage, w, lane);
+    const int8_t* st = smem + (kt % C::kStages) * C::kStage;
+    const int8_t* bs = st + C::kBM * kBigBK;
+    if (act_m > 0) {  // waves whose 64 rows are all past the group end skip the stage
+#pragma unroll
+      for (int kk = 0; kk < kBigBK / 32; ++kk) {
+        v4i fa[2], fb[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) fa[i] = load_a(st, kk, i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[j] = load_b(bs, kk, j);
+        if constexpr (LAYOUT == TAI_LAYOUT_KN) lds_wait_frags(fb);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue, specialised on the output dtype so the accumulators stay in registers.
+  const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32)
+                              ? static_cast<const int32_t*>(g.bias) + e * g.bias_group_stride : nullptr;
+  const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32)
+                            ? static_cast<const float*>(g.bias) + e * g.bias_group_stride : nullptr;
+  const float* scl = g.scale ? g.scale + e * g.scale_group_stride : nullptr;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+    const bool colok = j < act_n && col < g.n;
+    const int64_t ccol = colok ? col : 0;
+    const int32_t bcol = bias_i ? bias_i[ccol] : 0;
+    const float sc = scl ? scl[g.scale_len == 1 ? 0 : ccol] : 1.0f;
+    const float bf = bias_f ? bias_f[ccol] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (colok && lr < rows) {
+          const int64_t idx = static_cast<int64_t>(row0 + lr) * g.n + col;
+          const int32_t v = acc[i][j][r] + bcol;
+          if constexpr (OUT == TAI_DT_INT32) {
+            static_cast<int32_t*>(g.out)[idx] = v;
+          } else {
+            float f = static_cast<float>(v);
+            if (scl) f = f * sc;
+            if (g.pts) f = f * g.pts[row0 + lr];
+            if (bias_f) f = f + bf;
+            if constexpr (OUT == TAI_DT_BF16) static_cast<uint16_t*>(g.out)[idx] = f32_to_bf16(f);
+            else if constexpr (OUT == TAI_DT_FP16) static_cast<uint16_t*>(g.out)[idx] = f32_to_f16(f);
+            else static_cast<float*>(g.out)[idx] = f;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Big-tile configuration used by the host: 4x2 waves (256 x 256 tile), 128-byte K stages, two
+// stages (128 KB of LDS, one workgroup of eight waves per CU).
+#ifndef TAI_BIG_CFG
+#define TAI_BIG_CFG 4, 2, 128, 2
+#endif
+using BigSel = BigCfg<TAI_BIG_CFG>;
+constexpr int kBigBK = BigSel::kBK;
+constexpr int kBigBM = BigSel::kBM, kBigBN = BigSel::kBN;
+constexpr size_t kBigLds = BigSel::kLds;
+
+template <int LAYOUT, int OUT>
+bool set_big_lds() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_big_kernel<LAYOUT, OUT, BigSel>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kBigLds)) == hipSuccess;
+}
+
+// True when the device lets one workgroup hold the big kernel's LDS.
+bool big_tile_available() {
+  static int cached = -1;
+  if (cached < 0) {
+    int dev = 0, lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      lds = 0;
+    }
+    bool ok = static_cast<size_t>(lds) >= kBigLds;
+    if (ok) {
+      ok = set_big_lds<TAI_LAYOUT_KN, TAI_DT_INT32>() && set_big_lds<TAI_LAYOUT_KN, TAI_DT_BF16>() &&
+           set_big_lds<TAI_LAYOUT_KN, TAI_DT_FP16>() && set_big_lds<TAI_LAYOUT_KN, TAI_DT_FP32>() &&
+           set_big_lds<TAI_LAYOUT_NK, TAI_DT_INT32>() && set_big_lds<TAI_LAYOUT_NK, TAI_DT_BF16>() &&
+           set_big_lds<TAI_LAYOUT_NK, TAI_DT_FP16>() && set_big_lds<TAI_LAYOUT_NK, TAI_DT_FP32>();
+      (void)hipGetLastError();
+    }
+    cached = ok ? 1 : 0;
+  }
+  return cached == 1;
+}
+
+template <int LAYOUT>
+void launch_big_layout(const GemmArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.m_slots * g.n_tiles));
+  constexpr int T = BigSel::kThreads;
+  switch (g.out_dt) {
+    case TAI_DT_INT32: gemm_i8_big_kernel<LAYOUT, TAI_DT_INT32, BigSel><<<grid, T, kBigLds, st>>>(g); break;
+    case TAI_DT_BF16: gemm_i8_big_kernel<LAYOUT, TAI_DT_BF16, BigSel><<<grid, T, kBigLds, st>>>(g); break;
+    case TAI_DT_FP16: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP16, BigSel><<<grid, T, kBigLds, st>>>(g); break;
+    default: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP32, BigSel><<<grid, T, kBigLds, st>>>(g); break;
+  }
+}
+
+void launch_big(const GemmArgs& g, int layout, hipStream_t st) {
+  if (layout == TAI_LAYOUT_NK) launch_big_layout<TAI_LAYOUT_NK>(g, st);
+  else launch_big_layout<TAI_LAYOUT_KN>(g, st);
+}
+
 constexpr int kGroupedBM = 128;
 constexpr int kMinBM = 32;  // workspace is sized for the smallest row tile any variant uses
 
@@ -376,6 +687,12 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (!fast_path_ok(g, x2_layout)) {
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, x2_layout, nullptr);
+    return launch_status("tai_quant_matmul");
+  }
+  if (m >= 256 && k % kBigBK == 0 && (x2_layout == TAI_LAYOUT_NK || n % 16 == 0) && big_tile_available()) {
+    g.m_slots = cdiv(m, kBigBM);
+    g.n_tiles = cdiv(n, kBigBN);
+    launch_big(g, x2_layout, st);
     return launch_status("tai_quant_matmul");
   }
   // Small M leaves most CUs idle with 128-wide tiles; use narrower N tiles there.
@@ -421,13 +738,14 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     return TAI_ERR_WORKSPACE;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int bm = kGroupedBM;
+  const bool big = k % kBigBK == 0 && (w_layout == TAI_LAYOUT_NK || n % 16 == 0) && big_tile_available();
+  const int bm = big ? kBigBM : kGroupedBM;
   const int64_t slots = static_cast<int64_t>(grouped_map_slots(m, num_groups, bm));
   int4* map = static_cast<int4*>(workspace);
   int32_t* row_group = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                   sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM));
   GemmArgs g{x, weight, m, k, n, k * n, scale, n, n, per_token_scale, bias, bias_dtype, n, out_dtype, out,
-             map, slots, cdiv(n, 128)};
+             map, slots, cdiv(n, big ? kBigBN : 128)};
   const bool fast = fast_path_ok(g, w_layout);
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type, m,
                                                                               bm, map, slots,
@@ -436,6 +754,7 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, w_layout, row_group);
     return launch_status("tai_grouped_matmul");
   }
-  launch_tile<128, 128>(g, w_layout, st);
+  if (big) launch_big(g, w_layout, st);
+  else launch_tile<128, 128>(g, w_layout, st);
   return launch_status("tai_grouped_matmul");
 }
