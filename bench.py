@@ -50,6 +50,7 @@ class MoeLayer:
         self.s_gu = torch.rand(E, 2 * I, generator=g, device=dev) * 9e-3 + 1e-3
         self.s_d = torch.rand(E, H, generator=g, device=dev) * 9e-3 + 1e-3
         self.gmm1_events = []
+        self.active_experts = None
 
     def step(self, record=False):
         torch = self.torch
@@ -61,6 +62,8 @@ class MoeLayer:
                                                         expert_tokens_num_type=1, expert_tokens_num_flag=True,
                                                         row_idx_type=0)
         q, s = npu.npu_dynamic_quant(ex)
+        if self.active_experts is None:
+            self.active_experts = int((counts > 0).sum().item())  # routing is fixed: same logits every step
         if record:
             e0, e1 = _events(torch)
             e0.record()
@@ -77,8 +80,9 @@ class MoeLayer:
         return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
 
     def gmm1_bytes(self):
-        T, H, E, K, I = self.T, self.H, self.E, self.K, self.I
-        return E * H * 2 * I + T * K * H + T * K * 2 * I * 4  # weights + int8 rows + int32 out
+        T, H, K, I = self.T, self.H, self.K, self.I
+        # weights of the experts that received rows + int8 rows + int32 out (an expert with no rows is never read)
+        return self.active_experts * H * 2 * I + T * K * H + T * K * 2 * I * 4
 
 
 def bench_moe(torch, dev, steps, warmup):
@@ -95,8 +99,8 @@ def bench_moe(torch, dev, steps, warmup):
     achieved = layer.gmm1_bytes() / (gmm_ms * 1e-3) / 1e9
     roof = {"kernel": "tai_grouped_matmul (gate_up, int32 out)", "bound": "hbm", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "avg_ms": round(gmm_ms, 4),
-            "algorithmic_bytes": layer.gmm1_bytes()}
+            "traffic": _measured_traffic(), "avg_ms": round(gmm_ms, 4),
+            "algorithmic_bytes": layer.gmm1_bytes(), "active_experts": layer.active_experts}
     return layer, dt, roof
 
 
@@ -334,13 +338,40 @@ def cpu_baseline(sample_experts=4):
                       f"({t_exp:.1f}s) scaled x{L.E // sample_experts}"}
 
 
+# ----------------------------------------------------------------------------- counter calibration
+def bench_copy(torch, dev, iters=3):
+    """1 GiB device-to-device copy: the known-size kernel that scales the HBM byte counters."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    return {"bytes": 2 << 30, "ms": round(ms, 4), "GB/s": round((2 << 30) / (ms * 1e-3) / 1e9, 1)}
+
+
+def _measured_traffic():
+    """HBM bytes per gate_up launch from the committed counter summary (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "gmm_gate_up_moe_cfg4_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of side benches to run (gemm,mlp,decode,prefill,mla)")
+    ap.add_argument("--only", default="",
+                    help="comma list of side benches to run (gemm,mlp,decode,prefill,mla; 'none' for the MoE layer "
+                         "alone; 'copy' adds the 1 GiB copy that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (no multi-GPU path is built)"}))
@@ -365,6 +396,8 @@ def main():
         extra["causal_prefill_cfg3"] = bench_prefill(torch, dev)
     if "mla" in only:
         extra["mla_decode_cfg5"] = bench_mla(torch, dev)
+    if "copy" in only:
+        extra["copy_1gib"] = bench_copy(torch, dev)
     torch.cuda.empty_cache()
     cpu = None if args.skip_cpu else cpu_baseline()
     line = {

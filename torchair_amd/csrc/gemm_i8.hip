@@ -600,24 +600,32 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   }
 }
 
-// Big-tile configuration used by the host: 4x2 waves (256 x 256 tile), 128-byte K stages, two
-// stages (128 KB of LDS, one workgroup of eight waves per CU).
+// Tile configurations used by the host.
+//   dense: 4x2 waves (256 x 256 tile), 128-byte K stages, two stages (128 KB of LDS, one workgroup
+//     of eight waves per CU);
+//   grouped: the same tile. Measured on the MoE gate_up shape (255 groups, ~128 rows mean),
+//     128 x 256 tiles with three- or four-stage rings are 13-80% slower: four-wave workgroups
+//     leave one wave per SIMD, which cannot hide the LDS fragment reads.
 #ifndef TAI_BIG_CFG
 #define TAI_BIG_CFG 4, 2, 128, 2
 #endif
+#ifndef TAI_GRP_CFG
+#define TAI_GRP_CFG 4, 2, 128, 2
+#endif
 using BigSel = BigCfg<TAI_BIG_CFG>;
+using GrpSel = BigCfg<TAI_GRP_CFG>;
 constexpr int kBigBK = BigSel::kBK;
 constexpr int kBigBM = BigSel::kBM, kBigBN = BigSel::kBN;
-constexpr size_t kBigLds = BigSel::kLds;
 
-template <int LAYOUT, int OUT>
-bool set_big_lds() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_big_kernel<LAYOUT, OUT, BigSel>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kBigLds)) == hipSuccess;
+template <class C, int LAYOUT, int OUT>
+bool set_cfg_lds() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_big_kernel<LAYOUT, OUT, C>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds) == hipSuccess;
 }
 
-// True when the device lets one workgroup hold the big kernel's LDS.
-bool big_tile_available() {
+// True when the device lets one workgroup hold configuration C's LDS (attributes set once).
+template <class C>
+bool cfg_available() {
   static int cached = -1;
   if (cached < 0) {
     int dev = 0, lds = 0;
@@ -626,12 +634,12 @@ bool big_tile_available() {
       (void)hipGetLastError();
       lds = 0;
     }
-    bool ok = static_cast<size_t>(lds) >= kBigLds;
+    bool ok = lds >= C::kLds;
     if (ok) {
-      ok = set_big_lds<TAI_LAYOUT_KN, TAI_DT_INT32>() && set_big_lds<TAI_LAYOUT_KN, TAI_DT_BF16>() &&
-           set_big_lds<TAI_LAYOUT_KN, TAI_DT_FP16>() && set_big_lds<TAI_LAYOUT_KN, TAI_DT_FP32>() &&
-           set_big_lds<TAI_LAYOUT_NK, TAI_DT_INT32>() && set_big_lds<TAI_LAYOUT_NK, TAI_DT_BF16>() &&
-           set_big_lds<TAI_LAYOUT_NK, TAI_DT_FP16>() && set_big_lds<TAI_LAYOUT_NK, TAI_DT_FP32>();
+      ok = set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_INT32>() && set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_BF16>() &&
+           set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_FP16>() && set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_FP32>() &&
+           set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_INT32>() && set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_BF16>() &&
+           set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP16>() && set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP32>();
       (void)hipGetLastError();
     }
     cached = ok ? 1 : 0;
@@ -639,21 +647,23 @@ bool big_tile_available() {
   return cached == 1;
 }
 
-template <int LAYOUT>
-void launch_big_layout(const GemmArgs& g, hipStream_t st) {
+template <class C, int LAYOUT>
+void launch_cfg_layout(const GemmArgs& g, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(g.m_slots * g.n_tiles));
-  constexpr int T = BigSel::kThreads;
+  constexpr int T = C::kThreads;
+  constexpr size_t L = C::kLds;
   switch (g.out_dt) {
-    case TAI_DT_INT32: gemm_i8_big_kernel<LAYOUT, TAI_DT_INT32, BigSel><<<grid, T, kBigLds, st>>>(g); break;
-    case TAI_DT_BF16: gemm_i8_big_kernel<LAYOUT, TAI_DT_BF16, BigSel><<<grid, T, kBigLds, st>>>(g); break;
-    case TAI_DT_FP16: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP16, BigSel><<<grid, T, kBigLds, st>>>(g); break;
-    default: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP32, BigSel><<<grid, T, kBigLds, st>>>(g); break;
+    case TAI_DT_INT32: gemm_i8_big_kernel<LAYOUT, TAI_DT_INT32, C><<<grid, T, L, st>>>(g); break;
+    case TAI_DT_BF16: gemm_i8_big_kernel<LAYOUT, TAI_DT_BF16, C><<<grid, T, L, st>>>(g); break;
+    case TAI_DT_FP16: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP16, C><<<grid, T, L, st>>>(g); break;
+    default: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP32, C><<<grid, T, L, st>>>(g); break;
   }
 }
 
-void launch_big(const GemmArgs& g, int layout, hipStream_t st) {
-  if (layout == TAI_LAYOUT_NK) launch_big_layout<TAI_LAYOUT_NK>(g, st);
-  else launch_big_layout<TAI_LAYOUT_KN>(g, st);
+template <class C>
+void launch_cfg(const GemmArgs& g, int layout, hipStream_t st) {
+  if (layout == TAI_LAYOUT_NK) launch_cfg_layout<C, TAI_LAYOUT_NK>(g, st);
+  else launch_cfg_layout<C, TAI_LAYOUT_KN>(g, st);
 }
 
 constexpr int kGroupedBM = 128;
@@ -689,10 +699,10 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, x2_layout, nullptr);
     return launch_status("tai_quant_matmul");
   }
-  if (m >= 256 && k % kBigBK == 0 && (x2_layout == TAI_LAYOUT_NK || n % 16 == 0) && big_tile_available()) {
+  if (m >= 256 && k % kBigBK == 0 && (x2_layout == TAI_LAYOUT_NK || n % 16 == 0) && cfg_available<BigSel>()) {
     g.m_slots = cdiv(m, kBigBM);
     g.n_tiles = cdiv(n, kBigBN);
-    launch_big(g, x2_layout, st);
+    launch_cfg<BigSel>(g, x2_layout, st);
     return launch_status("tai_quant_matmul");
   }
   // Small M leaves most CUs idle with 128-wide tiles; use narrower N tiles there.
@@ -738,14 +748,14 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     return TAI_ERR_WORKSPACE;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool big = k % kBigBK == 0 && (w_layout == TAI_LAYOUT_NK || n % 16 == 0) && big_tile_available();
-  const int bm = big ? kBigBM : kGroupedBM;
+  const bool big = k % GrpSel::kBK == 0 && (w_layout == TAI_LAYOUT_NK || n % 16 == 0) && cfg_available<GrpSel>();
+  const int bm = big ? GrpSel::kBM : kGroupedBM;
   const int64_t slots = static_cast<int64_t>(grouped_map_slots(m, num_groups, bm));
   int4* map = static_cast<int4*>(workspace);
   int32_t* row_group = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                   sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM));
   GemmArgs g{x, weight, m, k, n, k * n, scale, n, n, per_token_scale, bias, bias_dtype, n, out_dtype, out,
-             map, slots, cdiv(n, big ? kBigBN : 128)};
+             map, slots, cdiv(n, big ? GrpSel::kBN : 128)};
   const bool fast = fast_path_ok(g, w_layout);
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type, m,
                                                                               bm, map, slots,
@@ -754,7 +764,7 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, w_layout, row_group);
     return launch_status("tai_grouped_matmul");
   }
-  if (big) launch_big(g, w_layout, st);
+  if (big) launch_cfg<GrpSel>(g, w_layout, st);
   else launch_tile<128, 128>(g, w_layout, st);
   return launch_status("tai_grouped_matmul");
 }
