@@ -600,26 +600,34 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   }
 }
 
-// Tile configurations used by the host.
-//   dense: 4x2 waves (256 x 256 tile), 128-byte K stages, two stages (128 KB of LDS, one workgroup
-//     of eight waves per CU);
-//   grouped: the same tile. Measured on the MoE gate_up shape (255 groups, ~128 rows mean),
-//     128 x 256 tiles with three- or four-stage rings are 13-80% slower: four-wave workgroups
-//     leave one wave per SIMD, which cannot hide the LDS fragment reads.
-#ifndef TAI_BIG_CFG
-#define TAI_BIG_CFG 4, 2, 128, 2
+// Tile configurations used by the host (8 waves of 64 x 128, 256 x 256 tiles):
+//   dense: 128-byte K stages, two stages (128 KB of LDS): the 8192^3 GEMM is MFMA/LDS bound and
+//     fewer, larger stages halve the barriers;
+//   grouped: 64-byte K stages, four stages (128 KB): MoE expert GEMMs stream their weights from
+//     HBM, and three stages in flight instead of one cut the gate_up time by ~6%.
+// Measured and rejected on the MoE gate_up and 8192^3 shapes: 128 x 256 tiles (4 waves, 3-4
+// stages), and a 4-wave kernel with 128 x 128 wave tiles and software-pipelined fragment reads;
+// with one wave per SIMD the per-stage barrier and LDS reads cost more than the halved LDS
+// traffic saves.
+#ifndef TAI_BIG_SEL
+#define TAI_BIG_SEL BigCfg<4, 2, 128, 2>
 #endif
-#ifndef TAI_GRP_CFG
-#define TAI_GRP_CFG 4, 2, 128, 2
+#ifndef TAI_GRP_SEL
+#define TAI_GRP_SEL BigCfg<4, 2, 64, 4>
 #endif
-using BigSel = BigCfg<TAI_BIG_CFG>;
-using GrpSel = BigCfg<TAI_GRP_CFG>;
+using BigSel = TAI_BIG_SEL;
+using GrpSel = TAI_GRP_SEL;
 constexpr int kBigBK = BigSel::kBK;
 constexpr int kBigBM = BigSel::kBM, kBigBN = BigSel::kBN;
 
 template <class C, int LAYOUT, int OUT>
+constexpr auto cfg_kernel() {
+  return &gemm_i8_big_kernel<LAYOUT, OUT, C>;
+}
+
+template <class C, int LAYOUT, int OUT>
 bool set_cfg_lds() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_big_kernel<LAYOUT, OUT, C>),
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(cfg_kernel<C, LAYOUT, OUT>()),
                              hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds) == hipSuccess;
 }
 
@@ -653,10 +661,10 @@ void launch_cfg_layout(const GemmArgs& g, hipStream_t st) {
   constexpr int T = C::kThreads;
   constexpr size_t L = C::kLds;
   switch (g.out_dt) {
-    case TAI_DT_INT32: gemm_i8_big_kernel<LAYOUT, TAI_DT_INT32, C><<<grid, T, L, st>>>(g); break;
-    case TAI_DT_BF16: gemm_i8_big_kernel<LAYOUT, TAI_DT_BF16, C><<<grid, T, L, st>>>(g); break;
-    case TAI_DT_FP16: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP16, C><<<grid, T, L, st>>>(g); break;
-    default: gemm_i8_big_kernel<LAYOUT, TAI_DT_FP32, C><<<grid, T, L, st>>>(g); break;
+    case TAI_DT_INT32: cfg_kernel<C, LAYOUT, TAI_DT_INT32>()<<<grid, T, L, st>>>(g); break;
+    case TAI_DT_BF16: cfg_kernel<C, LAYOUT, TAI_DT_BF16>()<<<grid, T, L, st>>>(g); break;
+    case TAI_DT_FP16: cfg_kernel<C, LAYOUT, TAI_DT_FP16>()<<<grid, T, L, st>>>(g); break;
+    default: cfg_kernel<C, LAYOUT, TAI_DT_FP32>()<<<grid, T, L, st>>>(g); break;
   }
 }
 
