@@ -9,6 +9,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -229,6 +230,11 @@ size_t decode_ws(int64_t b, int hkv, int d, int nsplit) {
 // and used by all four waves. Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 puts one
 // query per lane (column), so the online-softmax rescale of O^T is a per-lane scalar and P^T
 // leaves the S^T registers already in the B-operand layout of O^T = V^T P^T.
+// K/V tiles are double buffered and filled with global_load_lds (16 bytes per lane, no register
+// round trip): the next tile is in flight while the current one is used. LDS rows are the
+// tile's token rows with 16-byte chunks XOR-swizzled by row, so the K fragment reads (32 rows,
+// same chunk) and the transposing V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes)
+// are free of bank conflicts.
 constexpr int kPQ = 32;    // query rows per wave
 constexpr int kPKV = 64;   // kv tokens per LDS tile
 
@@ -250,12 +256,32 @@ struct PrefillArgs {
   int blocks_per_bk;
 };
 
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void gbl_void_t;
+
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
+}
+
 template <int D>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-  constexpr int ROW = 2 * D + 16;  // LDS row bytes: 4 rows apart shift 16 banks
-  __shared__ __attribute__((aligned(16))) char s_k[kPKV * ROW];
-  __shared__ __attribute__((aligned(16))) char s_v[kPKV * ROW];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+struct PrefillTile {
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kCpr = kRowBytes / 16;          // 16-byte chunks per token row
+  static constexpr int kRsh = D == 128 ? 0 : 1;        // rows per 256-byte bank cycle = 1 << kRsh
+  static constexpr int kTile = kPKV * kRowBytes;       // bytes of one K (or V) tile
+  static constexpr int kRpi = 1024 / kRowBytes;        // token rows per 1 KB load instruction
+  static constexpr int kLoadsPerWave = kTile / 1024 / 4;
+  // LDS byte offset of (row, 16-byte chunk c) within a tile
+  __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ ((row >> kRsh) & (kCpr - 1))); }
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
+  using T = PrefillTile<D>;
+  __shared__ __attribute__((aligned(16))) char smem[4 * T::kTile];  // [stage][K, V]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, grp = lane >> 5;
   // heavy (late) query tiles first
   const int64_t blk = blockIdx.x;
@@ -281,6 +307,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   };
   const bool wave_live = unit_ok && q0 < Lq;
   const int64_t wave_kv = wave_live ? max<int64_t>(0, kv_limit(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
+  // tokens below this need no mask for any query of the wave
+  const int64_t wave_clean = wave_live ? max<int64_t>(0, kv_limit(q0)) - (a.causal ? 1 : 0) : 0;
   int64_t blk_kv = 0;
   {
     const int last_unit = min(jb * 4 + 3, a.units_per_bk - 1);
@@ -306,38 +334,58 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   float m_run = -INFINITY, l_run = 0.0f;
   const int64_t qlim = (a.causal == 1) ? myq + shift : (a.causal == 2 ? myq : INT64_MAX);
 
-  for (int64_t t0 = 0; t0 < blk_kv; t0 += kPKV) {
-    // ---- stage K and V tiles: 16 lanes per token row, 16 rows per pass
-    constexpr int LPR = D / 8;
-    constexpr int RPP = 256 / LPR;
+  // global_load_lds of tile [t0, t0 + 64) into stage s; rows past the end load the last row
+  // (finite values; their scores are masked, so they add nothing)
+  const uint16_t* kbase = a.k + b * a.ks[0] + kvh * a.ks[2];
+  const uint16_t* vbase = a.v + b * a.vs[0] + kvh * a.vs[2];
+  auto issue_tile = [&](int64_t t0, int s) {
+    char* kst = smem + s * 2 * T::kTile;
 #pragma unroll
-    for (int pass = 0; pass < kPKV / RPP; ++pass) {
-      const int tok = pass * RPP + tid / LPR;
-      const int dd = (tid % LPR) * 8;
-      const int64_t t = t0 + tok;
-      uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
-      if (t < Lkv) {
-        kv4 = *reinterpret_cast<const uint4*>(a.k + b * a.ks[0] + t * a.ks[1] + kvh * a.ks[2] + dd);
-        vv4 = *reinterpret_cast<const uint4*>(a.v + b * a.vs[0] + t * a.vs[1] + kvh * a.vs[2] + dd);
-      }
-      *reinterpret_cast<uint4*>(s_k + tok * ROW + dd * 2) = kv4;
-      *reinterpret_cast<uint4*>(s_v + tok * ROW + dd * 2) = vv4;
+    for (int i = 0; i < T::kLoadsPerWave; ++i) {
+      const int q = w * T::kLoadsPerWave + i;
+      const int row = q * T::kRpi + lane / T::kCpr;
+      const int c = (lane % T::kCpr) ^ ((row >> T::kRsh) & (T::kCpr - 1));
+      const int64_t tok = min<int64_t>(t0 + row, Lkv - 1);
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(kbase + tok * a.ks[1] + 8 * c), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(vbase + tok * a.vs[1] + 8 * c), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
     }
-    __syncthreads();
-    if (wave_live && t0 < wave_kv) {
-      f32x16 s[2];
-      float mx = -INFINITY;
+  };
+
+  const int64_t ntiles = cdiv(blk_kv, static_cast<int64_t>(kPKV));
+  if (ntiles > 0) issue_tile(0, 0);
+  const int h16 = lane >> 4, j16 = lane & 15;
+  for (int64_t it = 0; it < ntiles; ++it) {
+    const int64_t t0 = it * kPKV;
+    __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0): this wave's loads of tile it
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (it + 1 < ntiles) issue_tile(t0 + kPKV, static_cast<int>((it + 1) & 1));
+    if (!(wave_live && t0 < wave_kv)) continue;
+    const uint32_t kst = lds_u32(smem + (it & 1) * 2 * T::kTile);
+    const uint32_t vst = kst + T::kTile;
+    f32x16 s[2];
+    float mx = -INFINITY;
+    const bool need_mask = t0 + kPKV > wave_clean;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
+    for (int st = 0; st < 2; ++st) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
-        if (t0 + 32 * st < wave_kv) {
+      for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
+      if (t0 + 32 * st < wave_kv) {
+        const int row = 32 * st + col;
+        bf16x8 kf[D / 16];
 #pragma unroll
-          for (int kd = 0; kd < D / 16; ++kd) {
-            const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(s_k + (32 * st + col) * ROW + (16 * kd + 8 * grp) * 2));
-            s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kd], s[st], 0, 0, 0);
-          }
+        for (int kd = 0; kd < D / 16; ++kd) {
+          uint4 raw;
+          asm volatile("ds_read_b128 %0, %1" : "=v"(raw) : "v"(kst + T::off(row, 2 * kd + grp)));
+          kf[kd] = as_bf16x8(raw);
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the fragments pass through empty asm after the wait, so no use is scheduled before it
+#pragma unroll
+        for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+v"(kf[kd]));
+#pragma unroll
+        for (int kd = 0; kd < D / 16; ++kd) s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kd], qf[kd], s[st], 0, 0, 0);
+      }
+      if (need_mask) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t t = t0 + 32 * st + 8 * (r >> 2) + 4 * grp + (r & 3);
@@ -346,49 +394,61 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
           s[st][r] = v;
           mx = fmaxf(mx, v);
         }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      float rs = 0.0f;
-      bf16x8 pf[4];
+      } else {
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float e = exp2f(s[st][8 * kb2 + j] - m_use);
-            rs += e;
-            pf[2 * st + kb2][j] = static_cast<__bf16>(e);
-          }
-      rs += __shfl_xor(rs, 32, 64);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
-      // ---- O^T += V^T P^T: k-slots of lane group grp in k-block kb are tokens
-      //      16kb + 4grp + {0..3} and 16kb + 8 + 4grp + {0..3}
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if (t0 + 16 * kb >= wave_kv) break;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const int dcol = 32 * dt + col;
-          u16x8 vv;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int tok = 16 * kb + 8 * (j >> 2) + 4 * grp + (j & 3);
-            vv[j] = *reinterpret_cast<const uint16_t*>(s_v + tok * ROW + dcol * 2);
-          }
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pf[kb], acc[dt], 0, 0, 0);
+        for (int r = 0; r < 16; ++r) {
+          s[st][r] *= a.scale_log2;
+          mx = fmaxf(mx, s[st][r]);
         }
       }
     }
-    __syncthreads();
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+    float rs = 0.0f;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e = __builtin_amdgcn_exp2f(s[st][8 * kb2 + j] - m_use);
+          rs += e;
+          pf[2 * st + kb2][j] = static_cast<__bf16>(e);
+        }
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+    // ---- O^T += V^T P^T. The k slots of lane group grp in k-block kb are tokens
+    //      16kb + 4grp + {0..3} and 16kb + 8 + 4grp + {0..3} (the S^T row order); each half is
+    //      one ds_read_b64_tr_b16: source lane j16 addresses V[k0 + j16/4][nb + 4 (j16 & 3)] and
+    //      lane j16 receives V[k0 .. k0+3][nb + j16], nb = 32dt + 16 (h16 & 1).
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      if (t0 + 16 * kb >= wave_kv) break;
+      v2i_t lo[D / 32], hi[D / 32];
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int nb = 32 * dt + 16 * (h16 & 1) + 4 * (j16 & 3);
+        const int r_lo = 16 * kb + 4 * grp + (j16 >> 2), r_hi = r_lo + 8;
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo[dt]) : "v"(vst + T::off(r_lo, nb >> 3) + 2 * (nb & 7)));
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi[dt]) : "v"(vst + T::off(r_hi, nb >> 3) + 2 * (nb & 7)));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const v4i_t vv = v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]};
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pf[kb], acc[dt], 0, 0, 0);
+      }
+    }
   }
   if (!unit_ok || myq >= a.s_q) return;
   // ---- write O (lane = query col, d = 32dt + 8(r/4) + 4grp + r%4) and lse
