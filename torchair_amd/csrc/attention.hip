@@ -10,6 +10,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -20,14 +21,23 @@ __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); 
 
 // ============================================================================ paged GQA decode
 // Work unit = (sequence b, kv head, split of kChunk tokens), one wave each. Per 32-token step:
-//   S = Q K^T with v_mfma_f32_16x16x32_bf16 (rows = the G query heads of this kv head, padded to
-//   16; columns = 16 tokens; K fragments loaded straight from the paged cache, 64 contiguous
-//   bytes per token row and lane group), online softmax in the exp2 domain, P staged through
-//   LDS as bf16, V staged through LDS and read transposed, O += P V with the same MFMA.
+//   the step's K and V rows go global -> LDS (global_load_lds, whole 256-byte rows per 16 lanes)
+//   through a ring, one step ahead of their use; S^T = K Q^T with v_mfma_f32_16x16x32_bf16
+//   (rows = 16 tokens, columns = the G query heads of this kv head padded to 16). S^T leaves each
+//   lane with four tokens of one head, so the online softmax needs two cross-lane reductions,
+//   and P^T is already the B operand of O^T = V^T P^T; V is read transposed with
+//   ds_read_b64_tr_b16.
 // Each unit writes an unnormalised partial (O, running max, running sum); a second kernel
 // merges the splits of each (b, head) and writes bf16 output and the logsumexp.
-constexpr int kChunk = 256;  // tokens per split (multiple of the 32-token step)
+#ifndef TAI_DECODE_CHUNK
+#define TAI_DECODE_CHUNK 512
+#endif
+#ifndef TAI_DECODE_VSTAGES
+#define TAI_DECODE_VSTAGES 2
+#endif
+constexpr int kChunk = TAI_DECODE_CHUNK;  // tokens per split (multiple of the 32-token step)
 constexpr int kStep = 32;
+constexpr int kVStages = TAI_DECODE_VSTAGES;  // K/V ring stages of one step each
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -47,20 +57,33 @@ struct DecodeArgs {
 };
 
 template <int D>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
-  constexpr int VROW = 2 * D + 8;  // bytes per LDS V row (pad spreads the transposed reads over banks)
-  __shared__ __attribute__((aligned(16))) char s_v[kStep * VROW];
-  __shared__ __attribute__((aligned(16))) uint16_t s_p[16 * kStep];
+struct DecodeTile {
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kCpr = kRowBytes / 16;                 // 16-byte chunks per row
+  static constexpr int kRsh = kRowBytes >= 256 ? 0 : 1;       // rows per 256-byte bank cycle = 1 << kRsh
+  static constexpr int kXm = (kCpr < 16 ? kCpr : 16) - 1;     // swizzle mask
+  static constexpr int kStage = kStep * kRowBytes;            // bytes of one V step
+  static constexpr int kLoads = kStage / 1024;                // 1 KB global_load_lds per step
+  static constexpr int kRpi = 1024 / kRowBytes;               // rows per load instruction
+  __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ ((row >> kRsh) & kXm)); }
+};
+
+template <int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+void paged_decode_kernel(DecodeArgs a) {
+  using T = DecodeTile<D>;
+  __shared__ __attribute__((aligned(16))) char s_kv[kVStages * 2 * T::kStage];  // [stage][K, V]
   const int lane = threadIdx.x;
-  const int64_t unit = blockIdx.x;
-  const int split = static_cast<int>(unit % a.nsplit);
-  const int64_t bk = unit / a.nsplit;
-  const int kvh = static_cast<int>(bk % a.hkv);
-  const int64_t b = bk / a.hkv;
+  // Launch order (b, split, kv head): the kv heads of one token range run together, so the
+  // cache rows of a token (all heads adjacent in the BSH layout) are read at about the same time.
+  const int kvh = static_cast<int>(blockIdx.x % a.hkv);
+  const int split = static_cast<int>((blockIdx.x / a.hkv) % a.nsplit);
+  const int64_t b = blockIdx.x / (static_cast<int64_t>(a.hkv) * a.nsplit);
+  const int64_t unit = (b * a.hkv + kvh) * a.nsplit + split;  // partial index (merge kernel order)
   const int64_t L = a.lens[b];
   const int64_t t_begin = static_cast<int64_t>(split) * kChunk;
   const int64_t t_end = min<int64_t>(L, t_begin + kChunk);
-  const int row = lane & 15, grp = lane >> 4;
+  const int hcol = lane & 15, kg = lane >> 4;
 
   float* po = a.part_o + unit * 16 * D;
   float* pml = a.part_ml + unit * 32;
@@ -69,127 +92,154 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     return;
   }
 
-  // Q fragments: head row (padded to 16), d slots [(D/4)*grp + 8*m, +8) for MFMA m.
+  // Q^T fragments (B operand): head = hcol (padded to 16), d slots 32m + 8kg .. +8
   bf16x8 qf[D / 32];
   {
-    const bool valid = row < a.g;
-    const uint16_t* qh = a.q + (b * a.hq + kvh * a.g + (valid ? row : 0)) * D;
+    const bool valid = hcol < a.g;
+    const uint16_t* qh = a.q + (b * a.hq + kvh * a.g + (valid ? hcol : 0)) * D;
 #pragma unroll
-    for (int m = 0; m < D / 32; ++m) {
-      uint4 v = valid ? *reinterpret_cast<const uint4*>(qh + (D / 4) * grp + 8 * m) : make_uint4(0, 0, 0, 0);
-      qf[m] = as_bf16x8(v);
-    }
+    for (int m = 0; m < D / 32; ++m)
+      qf[m] = as_bf16x8(valid ? *reinterpret_cast<const uint4*>(qh + 32 * m + 8 * kg) : make_uint4(0, 0, 0, 0));
   }
   f32x4 acc[D / 16];
 #pragma unroll
   for (int t = 0; t < D / 16; ++t) acc[t] = f32x4{0, 0, 0, 0};
-  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  float l_run[4] = {0, 0, 0, 0};
+  float m_run = -INFINITY, l_run = 0.0f;
 
   const uint16_t* kbase = a.k + static_cast<int64_t>(kvh) * a.sh;
   const uint16_t* vbase = a.v + static_cast<int64_t>(kvh) * a.sh;
   const int32_t* btrow = a.bt + b * a.max_blocks;
+  // The split's block-table entries, one per lane, fetched once (a split spans at most
+  // kChunk / bs + 1 <= 9 pages, as the host requires bs % 32 == 0); pages are then broadcast with
+  // ds_bpermute. Offsets inside the split are 32-bit; a power-of-two bs divides by shifting.
+  const int bs = a.bs;
+  const int bs_shift = (bs & (bs - 1)) == 0 ? __builtin_ctz(bs) : -1;
+  const int64_t pg0 = t_begin / bs;
+  const int off0 = static_cast<int>(t_begin - pg0 * bs);  // slot of the split's first token
+  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);
+  const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
+  // A step never straddles a page (bs % 32 == 0 and steps start at multiples of 32), so one
+  // lookup per step gives the element offset of the step's first token.
+  auto step_base = [&](int s) -> int64_t {
+    const int x = s * kStep + off0;
+    const int pi = bs_shift >= 0 ? (x >> bs_shift) : x / bs;
+    const int slot = x - pi * bs;
+    return static_cast<int64_t>(__shfl(my_page, pi, 64)) * a.sb + static_cast<int64_t>(slot) * a.ss;
+  };
+  const int n_local = static_cast<int>(t_end - t_begin);
 
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += kStep) {
-    const int64_t page = btrow[t0 / a.bs];
-    const int64_t slot0 = t0 % a.bs;
-    const uint16_t* kp = kbase + page * a.sb + slot0 * a.ss;
-    const uint16_t* vp = vbase + page * a.sb + slot0 * a.ss;
-    // ---- V rows of this step into LDS (token = grp + 4*i, 8 dims per lane); zero past L.
-    constexpr int VL = (kStep * D) / (64 * 8);  // 16-byte loads per lane
-    uint4 vr[VL];
+  const int nsteps = static_cast<int>((t_end - t_begin + kStep - 1) / kStep);
+  // K and V rows of a step both go global -> LDS ([K tile][V tile] per ring stage).
+  auto issue_kv = [&](int s) __attribute__((always_inline)) {
+    char* st = s_kv + (s % kVStages) * 2 * T::kStage;
+    const int64_t sbase = step_base(s);
+    const int last = n_local - 1 - s * kStep;
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      constexpr int LPR = D / 8;  // lanes per token row
-      const int tok = (lane / LPR) + i * (64 / LPR);
-      const int dd = (lane % LPR) * 8;
-      vr[i] = (t0 + tok < t_end) ? *reinterpret_cast<const uint4*>(vp + tok * a.ss + dd) : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < T::kLoads; ++q) {
+      const int row = q * T::kRpi + lane / T::kCpr;
+      const int c = (lane % T::kCpr) ^ ((row >> T::kRsh) & T::kXm);
+      const int64_t o = sbase + static_cast<int64_t>(min(row, last)) * a.ss + 8 * c;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kbase + o),
+                                       (__attribute__((address_space(3))) void*)(st + q * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vbase + o),
+                                       (__attribute__((address_space(3))) void*)(st + T::kStage + q * 1024), 16, 0, 0);
     }
-    // ---- K fragments and S = Q K^T for two 16-token blocks.
-    f32x4 s[2];
+  };
+  constexpr int kAhead = kVStages - 1;
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (i < nsteps) issue_kv(i);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)s_kv));
+  for (int s = 0; s < nsteps; ++s) {
+    if (s + kAhead < nsteps) issue_kv(s + kAhead);
+    {
+      const int after = min(kAhead, nsteps - 1 - s);  // steps issued after this one
+      if (after >= 2) __builtin_amdgcn_s_waitcnt(((4 * T::kLoads) & 0xF) | (((4 * T::kLoads) >> 4) << 14) | 0x70 | 0xF00);
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(((2 * T::kLoads) & 0xF) | (((2 * T::kLoads) >> 4) << 14) | 0x70 | 0xF00);
+      else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
+    }
+    const int64_t t0 = t_begin + static_cast<int64_t>(s) * kStep;
+    const uint32_t kst = lds0 + (s % kVStages) * 2 * T::kStage;
+    const uint32_t vst = kst + T::kStage;
+    v4i_t kcur[2][D / 32];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int m = 0; m < D / 32; ++m)
+        asm volatile("ds_read_b128 %0, %1" : "=v"(kcur[tb][m]) : "v"(kst + T::off(16 * tb + hcol, 4 * m + kg)));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int m = 0; m < D / 32; ++m) asm volatile("" : "+v"(kcur[tb][m]));
+    // ---- S^T = K Q^T for two 16-token blocks: lane holds tokens 16tb + 4kg + r of head hcol
+    f32x4 sc[2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      s[tb] = f32x4{0, 0, 0, 0};
-      const int tok = tb * 16 + row;
-      const uint16_t* kr = kp + tok * a.ss + (D / 4) * grp;
+      sc[tb] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int m = 0; m < D / 32; ++m) {
-        uint4 kv = *reinterpret_cast<const uint4*>(kr + 8 * m);
-        s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[m], as_bf16x8(kv), s[tb], 0, 0, 0);
+      for (int m = 0; m < D / 32; ++m)
+        sc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kcur[tb][m]), qf[m], sc[tb], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = t0 + 16 * tb + 4 * kg + r < t_end;
+        const float v = ok ? sc[tb][r] * a.scale_log2 : -INFINITY;
+        sc[tb][r] = v;
+        mx = fmaxf(mx, v);
       }
-    }
-    // S layout: lane holds token (lane&15) of block tb, heads 4*grp + r.
-    float p[2][4];
-    float mx[4], alpha[4];
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);  // finite: every step holds at least one valid token
+    const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float rs = 0.0f;
+    bf16x8 pf;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v0 = (t0 + row < t_end) ? s[0][r] * a.scale_log2 : -INFINITY;
-      float v1 = (t0 + 16 + row < t_end) ? s[1][r] * a.scale_log2 : -INFINITY;
-      p[0][r] = v0;
-      p[1][r] = v1;
-      float mm = fmaxf(v0, v1);
+    for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int o = 8; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o, 64));
-      const float mnew = fmaxf(m_run[r], mm);
-      alpha[r] = (m_run[r] == -INFINITY) ? 0.0f : exp2f(m_run[r] - mnew);
-      mx[r] = mnew;
-      m_run[r] = mnew;
-    }
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f(sc[tb][r] - m_new);
+        rs += e;
+        pf[4 * tb + r] = static_cast<__bf16>(e);
+      }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float e0 = exp2f(p[0][r] - mx[r]);
-      const float e1 = exp2f(p[1][r] - mx[r]);
-      p[0][r] = e0;
-      p[1][r] = e1;
-      float sum = e0 + e1;
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-      l_run[r] = l_run[r] * alpha[r] + sum;
-    }
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] *= alpha[r];
-    // ---- stage P (bf16) and V in LDS.
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int head = 4 * grp + r;
-      s_p[head * kStep + row] = bf16_bits(p[0][r]);
-      s_p[head * kStep + 16 + row] = bf16_bits(p[1][r]);
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      constexpr int LPR = D / 8;
-      const int tok = (lane / LPR) + i * (64 / LPR);
-      const int dd = (lane % LPR) * 8;
-      uint2* dst = reinterpret_cast<uint2*>(s_v + tok * VROW + dd * 2);
-      dst[0] = make_uint2(vr[i].x, vr[i].y);
-      dst[1] = make_uint2(vr[i].z, vr[i].w);
-    }
-    __syncthreads();
-    // ---- O += P V: A = P (head rows, token slots 8*grp..+8), B = V^T read from LDS.
-    const bf16x8 pf = as_bf16x8(*reinterpret_cast<const uint4*>(s_p + row * kStep + 8 * grp));
+    for (int t = 0; t < D / 16; ++t) acc[t] *= alpha;
+    // ---- O^T += V^T P^T: k slots 8kg + e are tokens 4kg + e (e < 4) and 16 + 4kg + e - 4;
+    //      each half is one ds_read_b64_tr_b16 (source lane j reads V[k0 + j/4][nb + 4(j&3)],
+    //      lane j receives V[k0 .. k0+3][nb + j]).
+    const int j = lane & 15;
+    v2i_t lo[D / 16], hi[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
-      const int dcol = t * 16 + row;
-      u16x8 vv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vv[e] = *reinterpret_cast<const uint16_t*>(s_v + (8 * grp + e) * VROW + dcol * 2);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, __builtin_bit_cast(bf16x8, vv), acc[t], 0, 0, 0);
+      const int nb = 16 * t + 4 * (j & 3);
+      const int r_lo = 4 * kg + (j >> 2), r_hi = r_lo + 16;
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo[t]) : "v"(vst + T::off(r_lo, nb >> 3) + 2 * (nb & 7)));
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi[t]) : "v"(vst + T::off(r_hi, nb >> 3) + 2 * (nb & 7)));
     }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) asm volatile("" : "+v"(lo[t]), "+v"(hi[t]));
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const v4i_t vv = v4i_t{lo[t][0], lo[t][1], hi[t][0], hi[t][1]};
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pf, acc[t], 0, 0, 0);
+    }
   }
-  // ---- partial out: heads 4*grp + r, d = 16*t + row.
+  // ---- partial out: head hcol, d = 16t + 4kg + r
+  if (hcol < a.g) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int head = 4 * grp + r;
-    if (head < a.g) {
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t) po[head * D + t * 16 + row] = acc[t][r];
-      if (row == 0) {
-        pml[2 * head] = m_run[r];
-        pml[2 * head + 1] = l_run[r];
-      }
+    for (int t = 0; t < D / 16; ++t)
+      *reinterpret_cast<f32x4*>(po + hcol * D + 16 * t + 4 * kg) = acc[t];
+    if (kg == 0) {
+      pml[2 * hcol] = m_run;
+      pml[2 * hcol + 1] = l_run;
     }
   }
 }
@@ -256,7 +306,6 @@ struct PrefillArgs {
   int blocks_per_bk;
 };
 
-typedef int v2i_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef const __attribute__((address_space(1))) void gbl_void_t;
 
