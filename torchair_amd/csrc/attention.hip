@@ -2,6 +2,8 @@
 // MLA absorbed decode over an int8 latent cache.
 #include "common.h"
 
+#include <utility>
+
 namespace tai {
 namespace {
 
@@ -520,14 +522,46 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 // ============================================================================ MLA absorbed decode
-// Work: (sequence b, split of kMlaChunk tokens, group of 64 query heads); 4 waves x 16 heads.
-// Per 32-token step the int8 latent rows (exactly representable in bf16) and the bf16 rope keys
-// are staged once in LDS ([token][Dn + Dr]) and shared by the four waves. The per-token scale
-// c[t] = int8[t] * scale[t] is folded into the scores (S = (q_nope.int8 * scale + q_rope.k_rope))
-// and into P before O^T = C^T P'^T, so the MFMAs see unscaled integers.
-constexpr int kMlaChunk = 1024;
+// Work: (sequence b, split of kMlaChunk tokens, group of kMlaHeads query heads); kMlaWaves waves of
+// kMlaHB 16-head MFMA column blocks each. All heads of the group share one latent tile, so each
+// latent row is fetched and converted once per group. Per head a wave holds Q^T (576 bf16) and
+// O^T (512 fp32), 12.5 registers per lane; the rest of a step fits in the remaining registers
+// because fragment batches are small and every LDS address is one of a few per-lane bases plus an
+// immediate offset.
+// Per 32-token step s (one workgroup barrier):
+//   - raw rows (int8 latent 512 B, bf16 rope key 128 B, fp32 scale) go global -> LDS with
+//     global_load_lds through a four-stage ring, three steps ahead of their use;
+//   - the workgroup converts step s + 1's int8 latent to bf16 (exact) into the other half of a
+//     double-buffered tile while step s is computed from the first;
+//   - S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (rows = 16 tokens, columns = 16 heads); nope and
+//     rope parts stay apart so the per-token scale multiplies only the first:
+//     S = (q_nope . int8) * scale + q_rope . k_rope;
+//   - O^T += C^T P'^T with P' = P * scale, so the MFMAs see the unscaled integers; C^T comes
+//     from the tile with ds_read_b64_tr_b16 and P'^T straight from the S^T registers.
+// LDS reads are inline asm with explicit waits (the compiler would otherwise drain the ring's
+// outstanding loads before each read).
+#ifndef TAI_MLA_CHUNK
+#define TAI_MLA_CHUNK 2048
+#endif
+#ifndef TAI_MLA_WAVES
+#define TAI_MLA_WAVES 8
+#endif
+#ifndef TAI_MLA_KB
+#define TAI_MLA_KB 3
+#endif
+#ifndef TAI_MLA_VB
+#define TAI_MLA_VB 2
+#endif
+constexpr int kMlaChunk = TAI_MLA_CHUNK;
 constexpr int kMlaStep = 32;
-constexpr int kMlaHeads = 64;  // heads per workgroup
+constexpr int kMlaWaves = TAI_MLA_WAVES;        // 8 (two per SIMD, 16 heads each) or 4 (one per SIMD, 32 heads)
+constexpr int kMlaHB = 8 / kMlaWaves;           // 16-head column blocks per wave
+constexpr int kMlaHeads = 128;                  // heads per workgroup
+constexpr int kMlaRing = 4;
+constexpr int kMlaKB = TAI_MLA_KB;  // K fragments per pipelined batch
+constexpr int kMlaVB = TAI_MLA_VB;  // V d blocks per pipelined batch (2 reads each)
+constexpr float kMlaSlack = 8.0f;   // log2-domain headroom of the lazily raised softmax max
+static_assert(kMlaWaves == 4 || kMlaWaves == 8, "MLA waves");
 
 struct MlaArgs {
   const uint16_t* qn;
@@ -545,14 +579,59 @@ struct MlaArgs {
   float* part_ml;  // [b, nsplit, hq, 2]
 };
 
+// Raw ring stage: [latent 32 x 512 B][rope 32 x 128 B][4 x 256 B scale slots]; bf16 tiles 2 x 32 x 1 KB.
+// Tile chunk c of row r sits at chunk c ^ X(r), X(r) = ((r & 7) << 1) | ((r >> 3) & 1): 16 rows at
+// one chunk hit 16 distinct 16-byte bank groups, and so do 4 consecutive rows x 2 chunks (the
+// transposing reads). X only moves the low four bits, so chunk 16q + c' is 256 q bytes past
+// chunk c' ^ X(r). Rope chunk c of row r sits at c ^ ((r >> 1) & 7).
+constexpr int kMlaLatBytes = kMlaStep * 512;
+constexpr int kMlaRopeOff = kMlaLatBytes;
+constexpr int kMlaScaleOff = kMlaRopeOff + kMlaStep * 128;
+constexpr int kMlaRaw = kMlaScaleOff + 4 * 256;
+constexpr int kMlaTile = kMlaStep * 1024;
+constexpr int kMlaLds = kMlaRing * kMlaRaw + 2 * kMlaTile;
+
+__device__ __forceinline__ int mla_x(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int mla_tile_off(int row, int c) { return row * 1024 + 16 * (c ^ mla_x(row)); }
+
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, so i can feed immediates
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int IMM>
+__device__ __forceinline__ void lds_read_b128(v4i_t& d, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void lds_read_b64(v2i_t& d, uint32_t addr) {
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void lds_read_tr16(v2i_t& d, uint32_t addr) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+
 template <int DN, int DR>
-__global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
+__global__ __launch_bounds__(64 * kMlaWaves) __attribute__((amdgpu_waves_per_eu(kMlaWaves / 4, kMlaWaves / 4)))
+void mla_decode_kernel(MlaArgs a) {
+  static_assert(DN == 512 && DR == 64, "MLA shape");
   constexpr int DK = DN + DR;
-  constexpr int ROW = 2 * DK + 16;  // LDS bytes per token row
-  __shared__ __attribute__((aligned(16))) char s_lat[kMlaStep * ROW];
-  __shared__ float s_cs[kMlaStep];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int hcol = lane & 15, grp = lane >> 4;
+  constexpr int NM = DK / 32;  // 32-wide d blocks of S (16 nope + 2 rope)
+  constexpr int HB = kMlaHB;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hcol = lane & 15, kg = lane >> 4, j = lane & 15;
   const int64_t blk = blockIdx.x;
   const int hg = static_cast<int>(blk % a.hgroups);
   const int split = static_cast<int>((blk / a.hgroups) % a.nsplit);
@@ -560,139 +639,335 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   const int64_t L = a.lens[b];
   const int64_t t_begin = static_cast<int64_t>(split) * kMlaChunk;
   const int64_t t_end = min<int64_t>(L, t_begin + kMlaChunk);
-  const int head = hg * kMlaHeads + w * 16 + hcol;
-  const bool head_ok = head < a.hq;
+  int head[HB];
+  bool head_ok[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    head[hb] = hg * kMlaHeads + (w * HB + hb) * 16 + hcol;
+    head_ok[hb] = head[hb] < a.hq;
+  }
   const int64_t pbase = (b * a.nsplit + split) * a.hq;
   if (t_begin >= t_end) {
-    if (grp == 0 && head_ok) { a.part_ml[(pbase + head) * 2] = -INFINITY; a.part_ml[(pbase + head) * 2 + 1] = 0.0f; }
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+      if (kg == 0 && head_ok[hb]) { a.part_ml[(pbase + head[hb]) * 2] = -INFINITY; a.part_ml[(pbase + head[hb]) * 2 + 1] = 0.0f; }
     return;
   }
-  // Q^T fragments (B operand): head = hcol, d slots 32*m + 8*grp .. +8
-  bf16x8 qf[DK / 32];
-  {
-    const uint16_t* qnp = a.qn + (b * a.hq + (head_ok ? head : 0)) * DN;
-    const uint16_t* qrp = a.qr + (b * a.hq + (head_ok ? head : 0)) * DR;
+  // Q^T fragments (B operand): head = 16hb + hcol, d slots 32m + 8kg .. +8 (m < 16 nope, else rope)
+  bf16x8 qf[HB][NM];
 #pragma unroll
-    for (int m = 0; m < DK / 32; ++m) {
-      const int d = 32 * m + 8 * grp;
+  for (int hb = 0; hb < HB; ++hb) {
+    const int hh = head_ok[hb] ? head[hb] : 0;
+    const uint16_t* qnp = a.qn + (b * a.hq + hh) * DN;
+    const uint16_t* qrp = a.qr + (b * a.hq + hh) * DR;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const int d = 32 * m + 8 * kg;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (head_ok) v = d < DN ? *reinterpret_cast<const uint4*>(qnp + d) : *reinterpret_cast<const uint4*>(qrp + d - DN);
-      qf[m] = as_bf16x8(v);
+      if (head_ok[hb]) v = d < DN ? *reinterpret_cast<const uint4*>(qnp + d) : *reinterpret_cast<const uint4*>(qrp + d - DN);
+      qf[hb][m] = as_bf16x8(v);
     }
   }
-  f32x4 acc[DN / 16];
+  f32x4 acc[HB][DN / 16];
 #pragma unroll
-  for (int i = 0; i < DN / 16; ++i) acc[i] = f32x4{0, 0, 0, 0};
-  float m_run = -INFINITY, l_run = 0.0f;
-  const int32_t* btrow = a.bt + b * a.max_blocks;
+  for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+    for (int i = 0; i < DN / 16; ++i) acc[hb][i] = f32x4{0, 0, 0, 0};
+  float m_run[HB], l_run[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) { m_run[hb] = -INFINITY; l_run[hb] = 0.0f; }
 
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += kMlaStep) {
-    const int64_t page = btrow[t0 / a.bs];
-    const int64_t slot0 = t0 % a.bs;
-    // ---- stage: int8 latent -> bf16 (16 values per thread per pass), rope rows, scales
-    {
-      constexpr int LPR = DN / 16;          // threads per latent row
-      constexpr int RPP = 256 / LPR;        // rows per pass
+  // pages: a step lies inside one page (bs % 32 == 0, steps start at multiples of 32)
+  const int32_t* btrow = a.bt + b * a.max_blocks;
+  const int bs = a.bs;
+  const int64_t pg0 = t_begin / bs;
+  const int off0 = static_cast<int>(t_begin - pg0 * bs);
+  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);  // <= kMlaChunk / 32 + 1 <= 64
+  const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
+  const int n_local = static_cast<int>(t_end - t_begin);
+  const int nsteps = (n_local + kMlaStep - 1) / kMlaStep;
+
+  // Every wave issues the same number of global_load_lds per step (uniform vmcnt): 16 / kMlaWaves
+  // latent instructions (2 rows of 512 B each), and a rope instruction (8 rows of 128 B) and/or a
+  // scale instruction into its own 256 B slot (slot 0 is the one read): with 4 waves each wave
+  // issues both, with 8 waves waves 0-3 the rope and waves 4-7 the scale.
+  constexpr int kLatPerWave = 16 / kMlaWaves;
+  constexpr int kRawLoads = kLatPerWave + (kMlaWaves == 4 ? 2 : 1);
+  const bool do_rope = kMlaWaves == 4 || w < 4;
+  const bool do_scale = kMlaWaves == 4 || w >= 4;
+  auto issue_raw = [&](int s) __attribute__((always_inline)) {
+    char* st = smem + (s % kMlaRing) * kMlaRaw;
+    const int x = s * kMlaStep + off0;
+    const int pi = x / bs;
+    const int64_t tok0 = static_cast<int64_t>(__shfl(my_page, pi, 64)) * bs + (x - pi * bs);  // cache row
+    const int last = n_local - 1 - s * kMlaStep;
 #pragma unroll
-      for (int pass = 0; pass < kMlaStep / RPP; ++pass) {
-        const int tok = pass * RPP + tid / LPR;
-        const int dd = (tid % LPR) * 16;
-        uint4 raw = make_uint4(0, 0, 0, 0);
-        if (t0 + tok < t_end) raw = *reinterpret_cast<const uint4*>(a.ckv + ((page * a.bs + slot0 + tok) * DN + dd));
-        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-        uint32_t o[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float f0 = static_cast<float>(static_cast<int8_t>(wv[i] & 0xff));
-          const float f1 = static_cast<float>(static_cast<int8_t>((wv[i] >> 8) & 0xff));
-          const float f2 = static_cast<float>(static_cast<int8_t>((wv[i] >> 16) & 0xff));
-          const float f3 = static_cast<float>(static_cast<int8_t>(wv[i] >> 24));
-          o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-          o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
-        }
-        uint4* dst = reinterpret_cast<uint4*>(s_lat + tok * ROW + dd * 2);
-        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
-      }
-      constexpr int RL = DR / 8;  // threads per rope row
-      if (tid < kMlaStep * RL) {
-        const int tok = tid / RL, dd = (tid % RL) * 8;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (t0 + tok < t_end) v = *reinterpret_cast<const uint4*>(a.kr + (page * a.bs + slot0 + tok) * DR + dd);
-        *reinterpret_cast<uint4*>(s_lat + tok * ROW + (DN + dd) * 2) = v;
-      }
-      if (tid < kMlaStep) s_cs[tid] = (t0 + tid < t_end) ? a.cs[page * a.bs + slot0 + tid] : 0.0f;
+    for (int i = 0; i < kLatPerWave; ++i) {
+      const int q = kLatPerWave * w + i;
+      const int row = 2 * q + (lane >> 5);
+      const int8_t* src = a.ckv + (tok0 + min(row, last)) * DN + 16 * (lane & 31);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + q * 1024), 16, 0, 0);
     }
-    __syncthreads();
-    // ---- S^T = K Q^T, nope and rope parts kept apart (A = latent rows: token = 16tb + hcol)
-    f32x4 sn[2], sr[2];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      sn[tb] = f32x4{0, 0, 0, 0};
-      sr[tb] = f32x4{0, 0, 0, 0};
-      const char* rowp = s_lat + (16 * tb + hcol) * ROW;
-#pragma unroll
-      for (int m = 0; m < DK / 32; ++m) {
-        const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(rowp + (32 * m + 8 * grp) * 2));
-        if (32 * m < DN) sn[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], sn[tb], 0, 0, 0);
-        else sr[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], sr[tb], 0, 0, 0);
-      }
+    if (do_rope) {
+      const int row = 8 * (w & 3) + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const uint16_t* src = a.kr + (tok0 + min(row, last)) * DR + 8 * c;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + kMlaRopeOff + (w & 3) * 1024), 16, 0, 0);
     }
-    // S^T layout: lane holds head hcol, tokens 16tb + 4grp + r.
-    float sv[2][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * tb + 4 * grp + r;
-        const float v = (t0 + tok < t_end) ? (sn[tb][r] * s_cs[tok] + sr[tb][r]) * a.scale_log2 : -INFINITY;
-        sv[tb][r] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
-    float rs = 0.0f;
-    bf16x8 pf;
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * tb + 4 * grp + r;
-        const float e = exp2f(sv[tb][r] - m_new);
-        rs += e;
-        pf[4 * tb + r] = static_cast<__bf16>(e * s_cs[tok]);
-      }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-    // ---- O^T += C^T P'^T; k-slots of lane group grp: tokens 4grp + {0..3}, 16 + 4grp + {0..3}
-#pragma unroll
-    for (int dt = 0; dt < DN / 16; ++dt) {
-      const int dcol = 16 * dt + hcol;
-      u16x8 vv;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tok = 16 * (j >> 2) + 4 * grp + (j & 3);
-        vv[j] = *reinterpret_cast<const uint16_t*>(s_lat + tok * ROW + dcol * 2);
-      }
-      acc[dt] = acc[dt] * alpha;
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pf, acc[dt], 0, 0, 0);
+    if (do_scale) {
+      const float* src = a.cs + tok0 + min(lane & 31, last);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + kMlaScaleOff + (w & 3) * 256), 4, 0, 0);
     }
-    __syncthreads();
+  };
+
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)smem));
+  const uint32_t tiles = lds0 + kMlaRing * kMlaRaw;
+  char* tiles_p = smem + kMlaRing * kMlaRaw;
+  // int8 latent of raw step s -> bf16 tile t: a wave converts 32 / kMlaWaves rows in 8-byte units
+  // (16 lanes cover 128 contiguous source bytes and write 16 consecutive 16-byte chunks).
+  auto convert = [&](int s, int t) __attribute__((always_inline)) {
+    constexpr int RPW = kMlaStep / kMlaWaves, UPL = RPW * 64 / 64;  // 8-byte units per lane per row-set
+    const uint32_t raw = lds0 + (s % kMlaRing) * kMlaRaw;
+    char* tp = tiles_p + t * kMlaTile;
+    v2i_t r[UPL];
+    // unit u of a lane: row RPW w + (u / 4), source bytes 8 (16 (u % 4) + (lane & 15)) ...; lanes
+    // 16..63 take rows +1 .. +3 via the row offset below
+    const int rsub = lane >> 4;  // 0..3
+#pragma unroll
+    for (int u = 0; u < UPL; ++u) {
+      const int row = RPW * w + 4 * (u / 4) + rsub;
+      const int c = 16 * (u % 4) + (lane & 15);  // 8-byte source unit = bf16 chunk index
+      asm volatile("ds_read_b64 %0, %1" : "=v"(r[u]) : "v"(raw + row * 512 + 8 * c));
+    }
+    lds_wait<0>();
+#pragma unroll
+    for (int u = 0; u < UPL; ++u) asm volatile("" : "+v"(r[u]));
+#pragma unroll
+    for (int u = 0; u < UPL; ++u) {
+      const int row = RPW * w + 4 * (u / 4) + rsub;
+      const int c = 16 * (u % 4) + (lane & 15);
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t wv = static_cast<uint32_t>(r[u][q]);
+        const float f0 = static_cast<float>(static_cast<int8_t>(wv & 0xff));
+        const float f1 = static_cast<float>(static_cast<int8_t>((wv >> 8) & 0xff));
+        const float f2 = static_cast<float>(static_cast<int8_t>((wv >> 16) & 0xff));
+        const float f3 = static_cast<float>(static_cast<int8_t>(wv >> 24));
+        o[2 * q] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+        o[2 * q + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+      }
+      *reinterpret_cast<uint4*>(tp + mla_tile_off(row, c)) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  };
+  // Per-lane LDS bases (tile 0; tile 1 is kMlaTile further). K (nope) fragment (tb, m): row
+  //   16tb + hcol, chunk 4m + kg -> kb[m & 3] + 16384 tb + 256 (m >> 2). Rope fragment (tb, m'):
+  //   row 16tb + hcol -> raw + rb[m'] + 2048 tb. V^T halves for d block dt: rows 4kg + j/4 (+16),
+  //   columns 16dt + 4 (j & 3) .. +4 -> vb[dt & 7] + 256 (dt >> 3) (+ 16384).
+  uint32_t kb[4], rb[2], vb[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) kb[q] = tiles + hcol * 1024 + 16 * ((4 * q + kg) ^ mla_x(hcol));
+#pragma unroll
+  for (int q = 0; q < 2; ++q) rb[q] = kMlaRopeOff + hcol * 128 + 16 * ((4 * q + kg) ^ ((hcol >> 1) & 7));
+  {
+    const int r_lo = 4 * kg + (j >> 2), h = (j >> 1) & 1;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) vb[q] = tiles + r_lo * 1024 + 16 * ((2 * q + h) ^ mla_x(r_lo)) + 8 * (j & 1);
   }
-  if (!head_ok) return;
-  // ---- partial: O^T[d = 16dt + 4grp + r][head]
-  float* po = a.part_o + (pbase + head) * DN;
+
+  // ---- per-step pieces -------------------------------------------------------------------
+  f32x4 sn[2][HB], sr[2][HB];
+  float sv[HB][2][4];
+  f32x4 cs0, cs1;
+  float m_cand[HB];
+  uint32_t raw = 0, toff = 0;
+
+  // front: ring wait, the barrier, the next step's conversion, S^T and the step's maxima
+  auto front = [&](int s) __attribute__((always_inline)) {
+    // raw(s + 1) must have landed (for the conversion); raw(s + 2) may stay in flight
+    if (s + 2 < nsteps) __builtin_amdgcn_s_waitcnt(kRawLoads | 0x70 | 0xF00);
+    else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
+    // every wave's raw(s + 1) has landed, tile s & 1 is converted, and every wave is done with
+    // step s - 1 (its tile and raw slot are free)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (s + 3 < nsteps) issue_raw(s + 3);
+    if (s + 1 < nsteps) convert(s + 1, (s + 1) & 1);
+    raw = lds0 + (s % kMlaRing) * kMlaRaw;
+    toff = (s & 1) * kMlaTile;
+    // S^T: 36 fragments f = 18 tb + m in batches of kMlaKB, the next batch in flight
 #pragma unroll
-  for (int dt = 0; dt < DN / 16; ++dt)
-    *reinterpret_cast<float4*>(po + 16 * dt + 4 * grp) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
-  if (grp == 0) {
-    a.part_ml[(pbase + head) * 2] = m_run;
-    a.part_ml[(pbase + head) * 2 + 1] = l_run;
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) { sn[tb][hb] = f32x4{0, 0, 0, 0}; sr[tb][hb] = f32x4{0, 0, 0, 0}; }
+    constexpr int NKF = 2 * NM, NKB = (NKF + kMlaKB - 1) / kMlaKB;
+    v4i_t kf[2][kMlaKB];
+    auto kread = [&](auto f_c, v4i_t& d) __attribute__((always_inline)) {
+      constexpr int f = decltype(f_c)::value, tb = f / NM, m = f % NM;
+      if constexpr (m < DN / 32) lds_read_b128<16384 * tb + 256 * (m >> 2)>(d, kb[m & 3] + toff);
+      else lds_read_b128<2048 * tb>(d, raw + rb[m - DN / 32]);
+    };
+    static_for<kMlaKB>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      kread(std::integral_constant<int, i>{}, kf[0][i]);
+    });
+    static_for<NKB>([&](auto bi_c) {
+      constexpr int bi = decltype(bi_c)::value, cur = bi & 1;
+      constexpr int nnext = (bi + 1 < NKB) ? (NKF - (bi + 1) * kMlaKB < kMlaKB ? NKF - (bi + 1) * kMlaKB : kMlaKB) : 0;
+      if constexpr (nnext > 0) {
+        static_for<nnext>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          kread(std::integral_constant<int, (bi + 1) * kMlaKB + i>{}, kf[cur ^ 1][i]);
+        });
+      }
+      lds_wait<nnext>();
+      static_for<kMlaKB>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value, f = bi * kMlaKB + i;
+        if constexpr (f < NKF) {
+          asm volatile("" : "+v"(kf[cur][i]));
+          constexpr int tb = f / NM, m = f % NM;
+          const bf16x8 kv = __builtin_bit_cast(bf16x8, kf[cur][i]);
+#pragma unroll
+          for (int hb = 0; hb < HB; ++hb) {
+            if constexpr (m < DN / 32) sn[tb][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qf[hb][m], sn[tb][hb], 0, 0, 0);
+            else sr[tb][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qf[hb][m], sr[tb][hb], 0, 0, 0);
+          }
+        }
+      });
+    });
+    // per-token scales of this lane's tokens: 4kg + r and 16 + 4kg + r (slot 0)
+    lds_read_b128<0>(*reinterpret_cast<v4i_t*>(&cs0), raw + kMlaScaleOff + 16 * kg);
+    lds_read_b128<64>(*reinterpret_cast<v4i_t*>(&cs1), raw + kMlaScaleOff + 16 * kg);
+    lds_wait<0>();
+    asm volatile("" : "+v"(cs0), "+v"(cs1));
+    const int64_t t0 = t_begin + static_cast<int64_t>(s) * kMlaStep;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * tb + 4 * kg + r;
+          const float c = tb ? cs1[r] : cs0[r];
+          const float v = (t0 + tok < t_end) ? (sn[tb][hb][r] * c + sr[tb][hb][r]) * a.scale_log2 : -INFINITY;
+          sv[hb][tb][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      m_cand[hb] = mx;  // finite: every step holds a valid token
+    }
+  };
+  auto need_raise = [&]() __attribute__((always_inline)) {
+    bool r = false;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) r = r || m_cand[hb] > m_run[hb] + kMlaSlack;
+    return __any(r);  // wave-uniform
+  };
+  // rescale: raise the reference max to the step's and rescale O^T and l (rare)
+  auto rescale = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const float m_new = fmaxf(m_run[hb], m_cand[hb]);
+      const float alpha = (m_run[hb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[hb] - m_new);
+      l_run[hb] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DN / 16; ++dt) acc[hb][dt] *= alpha;
+      m_run[hb] = m_new;
+    }
+  };
+  // back: P' = exp2(S - m) * scale, l, and O^T += C^T P'^T (V batches of kMlaVB d blocks)
+  auto back = [&]() __attribute__((always_inline)) {
+    bf16x8 pf[HB];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      float rs = 0.0f;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = __builtin_amdgcn_exp2f(sv[hb][tb][r] - m_run[hb]);
+          rs += e;
+          pf[hb][4 * tb + r] = static_cast<__bf16>(e * (tb ? cs1[r] : cs0[r]));
+        }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l_run[hb] += rs;
+    }
+    constexpr int NVB = (DN / 16) / kMlaVB;
+    v2i_t vlo[2][kMlaVB], vhi[2][kMlaVB];
+    auto vread = [&](auto dt_c, v2i_t& lo, v2i_t& hi) __attribute__((always_inline)) {
+      constexpr int dt = decltype(dt_c)::value;
+      lds_read_tr16<256 * (dt >> 3)>(lo, vb[dt & 7] + toff);
+      lds_read_tr16<256 * (dt >> 3) + 16384>(hi, vb[dt & 7] + toff);
+    };
+    static_for<kMlaVB>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      vread(std::integral_constant<int, i>{}, vlo[0][i], vhi[0][i]);
+    });
+    static_for<NVB>([&](auto bi_c) {
+      constexpr int bi = decltype(bi_c)::value, cur = bi & 1;
+      if constexpr (bi + 1 < NVB) {
+        static_for<kMlaVB>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          vread(std::integral_constant<int, (bi + 1) * kMlaVB + i>{}, vlo[cur ^ 1][i], vhi[cur ^ 1][i]);
+        });
+        lds_wait<2 * kMlaVB>();
+      } else {
+        lds_wait<0>();
+      }
+      static_for<kMlaVB>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value, dt = bi * kMlaVB + i;
+        asm volatile("" : "+v"(vlo[cur][i]), "+v"(vhi[cur][i]));
+        const bf16x8 vv = __builtin_bit_cast(bf16x8, v4i_t{vlo[cur][i][0], vlo[cur][i][1], vhi[cur][i][0], vhi[cur][i][1]});
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) acc[hb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pf[hb], acc[hb][dt], 0, 0, 0);
+      });
+    });
+  };
+
+  // prologue: three raw steps in flight, step 0 converted into tile 0 (the loop's first barrier
+  // publishes it)
+  issue_raw(0);
+  if (nsteps > 1) issue_raw(1);
+  if (nsteps > 2) issue_raw(2);
+  if (nsteps > 2) __builtin_amdgcn_s_waitcnt((2 * kRawLoads) | 0x70 | 0xF00);
+  else if (nsteps > 1) __builtin_amdgcn_s_waitcnt(kRawLoads | 0x70 | 0xF00);
+  else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  convert(0, 0);
+  // Online softmax with a lazily raised reference max: m_run moves (and O^T is rescaled, which
+  // pulls the accumulators through VGPRs) only when the step's max exceeds it by more than
+  // kMlaSlack in the log2 domain, so P' <= 2^kMlaSlack * scale between raises; the result is the
+  // same. The rescale sits outside the steady-state loop: inside it, its join would make the
+  // register allocator move the accumulators on every step.
+  int s = 0;
+  while (true) {
+    for (; s < nsteps; ++s) {
+      front(s);
+      if (need_raise()) break;
+      back();
+    }
+    if (s >= nsteps) break;
+    rescale();
+    back();
+    ++s;
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    if (!head_ok[hb]) continue;
+    // ---- partial: O^T[d = 16dt + 4kg + r][head]
+    float* po = a.part_o + (pbase + head[hb]) * DN;
+#pragma unroll
+    for (int dt = 0; dt < DN / 16; ++dt)
+      *reinterpret_cast<float4*>(po + 16 * dt + 4 * kg) = make_float4(acc[hb][dt][0], acc[hb][dt][1], acc[hb][dt][2], acc[hb][dt][3]);
+    if (kg == 0) {
+      a.part_ml[(pbase + head[hb]) * 2] = m_run[hb];
+      a.part_ml[(pbase + head[hb]) * 2 + 1] = l_run[hb];
+    }
   }
 }
 
@@ -855,7 +1130,17 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + static_cast<size_t>(b) * nsplit * hq * dn;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  mla_decode_kernel<512, 64><<<dim3(static_cast<unsigned>(b * nsplit * a.hgroups)), 256, 0, st>>>(a);
+  static bool lds_set = false;
+  if (!lds_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) != hipSuccess) {
+      (void)hipGetLastError();
+      set_error("tai_fia_mla_decode: the device cannot give a workgroup %d bytes of LDS", kMlaLds);
+      return TAI_ERR_LAUNCH;
+    }
+    lds_set = true;
+  }
+  mla_decode_kernel<512, 64><<<dim3(static_cast<unsigned>(b * nsplit * a.hgroups)), 64 * kMlaWaves, kMlaLds, st>>>(a);
   mla_combine_kernel<512><<<dim3(static_cast<unsigned>(b * hq)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
   return launch_status("tai_fia_mla_decode");
 }
