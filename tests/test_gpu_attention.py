@@ -186,6 +186,11 @@ def test_mla_small():
     _check_mla([1, 40, 1100, 0, 2049], 128, 64, 120)
 
 
+def test_mla_small_pages_long_split():
+    # block_size 32: a full split spans 64 pages (one page id per lane)
+    _check_mla([4100, 2048, 31], 16, 32, 123)
+
+
 def test_mla_cfg5():
     g = torch.Generator().manual_seed(121)
     lens = torch.randint(2048, 8193, (128,), generator=g).tolist()

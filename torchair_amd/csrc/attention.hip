@@ -562,6 +562,7 @@ constexpr int kMlaKB = TAI_MLA_KB;  // K fragments per pipelined batch
 constexpr int kMlaVB = TAI_MLA_VB;  // V d blocks per pipelined batch (2 reads each)
 constexpr float kMlaSlack = 8.0f;   // log2-domain headroom of the lazily raised softmax max
 static_assert(kMlaWaves == 4 || kMlaWaves == 8, "MLA waves");
+static_assert(kMlaChunk % kMlaStep == 0 && kMlaChunk <= 2048, "a split must span at most 64 pages of 32+ tokens");
 
 struct MlaArgs {
   const uint16_t* qn;
@@ -682,7 +683,9 @@ void mla_decode_kernel(MlaArgs a) {
   const int bs = a.bs;
   const int64_t pg0 = t_begin / bs;
   const int off0 = static_cast<int>(t_begin - pg0 * bs);
-  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);  // <= kMlaChunk / 32 + 1 <= 64
+  // pages of the split, one per lane: bs is a multiple of 32 and splits start at multiples of
+  // kMlaChunk <= 2048, so a split spans at most 64 pages (bs = 32: exactly 2048 / 32)
+  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);
   const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
   const int n_local = static_cast<int>(t_end - t_begin);
   const int nsteps = (n_local + kMlaStep - 1) / kMlaStep;

@@ -567,6 +567,83 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32)
                             ? static_cast<const float*>(g.bias) + e * g.bias_group_stride : nullptr;
   const float* scl = g.scale ? g.scale + e * g.scale_group_stride : nullptr;
+  // value of accumulator (i, j, r) in the output type, as raw bits (pt: the row's per-token scale)
+  auto out_bits = [&](int32_t v, float sc, float bf, float pt) -> uint32_t {
+    if constexpr (OUT == TAI_DT_INT32) {
+      return static_cast<uint32_t>(v);
+    } else {
+      float f = static_cast<float>(v);
+      if (scl) f = f * sc;
+      if (g.pts) f = f * pt;
+      if (bias_f) f = f + bf;
+      if constexpr (OUT == TAI_DT_BF16) return f32_to_bf16(f);
+      else if constexpr (OUT == TAI_DT_FP16) return f32_to_f16(f);
+      else return __float_as_uint(f);
+    }
+  };
+  const int64_t wcol0 = n0 + wn * 128;
+  if (wcol0 + 128 <= g.n) {
+    // Full-width wave tile: 16-row slices go through a wave-private LDS region (the ring is free
+    // once every wave is past its last stage) and leave as 16-byte stores along the rows, instead
+    // of one 2- or 4-byte store per element.
+    constexpr int ES = (OUT == TAI_DT_BF16 || OUT == TAI_DT_FP16) ? 2 : 4;
+    constexpr int RB = 128 * ES + 16;  // LDS row bytes (padding moves the second lane half's row)
+    static_assert(8 * 16 * RB <= C::kLds, "epilogue staging must fit in the ring");
+    // per-token scales of this lane's 32 accumulator rows, loaded before any store (loads issued
+    // behind stores would wait for them: vmcnt retires in order)
+    float pt[2][2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+          const int lr = wm * 64 + i * 32 + 16 * h + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+          pt[i][h][rr] = (OUT != TAI_DT_INT32 && g.pts) ? g.pts[row0 + min(lr, rows - 1)] : 1.0f;
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    char* wreg = reinterpret_cast<char*>(smem) + w * (16 * RB);
+    int32_t bcol[4];
+    float sc[4], bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = wcol0 + j * 32 + (lane & 31);
+      bcol[j] = bias_i ? bias_i[col] : 0;
+      sc[j] = scl ? scl[g.scale_len == 1 ? 0 : col] : 1.0f;
+      bf[j] = bias_f ? bias_f[col] : 0.0f;
+    }
+    constexpr int LPR = 128 * ES / 16;  // lanes per row when reading 16 bytes each
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // accumulator rows of this slice: r = 8h .. 8h+7, local row 8((r&7)>>2) + 4(lane>>5) + (r&3)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int rr = 0; rr < 8; ++rr) {
+            const int r = 8 * h + rr;
+            const int sl = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+            const uint32_t bits = out_bits(acc[i][j][r] + bcol[j], sc[j], bf[j], pt[i][h][rr]);
+            char* dst = wreg + sl * RB + (j * 32 + (lane & 31)) * ES;
+            if constexpr (ES == 2) *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(bits);
+            else *reinterpret_cast<uint32_t*>(dst) = bits;
+          }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < 16 / (64 / LPR); ++q) {
+          const int sl = q * (64 / LPR) + lane / LPR;
+          const int lr = wm * 64 + i * 32 + 16 * h + sl;
+          const uint4 v = *reinterpret_cast<const uint4*>(wreg + sl * RB + 16 * (lane % LPR));
+          if (lr < rows)
+            *reinterpret_cast<uint4*>(static_cast<char*>(g.out) + (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
+                                      16 * (lane % LPR)) = v;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
@@ -582,18 +659,9 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
         const int lr = wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if (colok && lr < rows) {
           const int64_t idx = static_cast<int64_t>(row0 + lr) * g.n + col;
-          const int32_t v = acc[i][j][r] + bcol;
-          if constexpr (OUT == TAI_DT_INT32) {
-            static_cast<int32_t*>(g.out)[idx] = v;
-          } else {
-            float f = static_cast<float>(v);
-            if (scl) f = f * sc;
-            if (g.pts) f = f * g.pts[row0 + lr];
-            if (bias_f) f = f + bf;
-            if constexpr (OUT == TAI_DT_BF16) static_cast<uint16_t*>(g.out)[idx] = f32_to_bf16(f);
-            else if constexpr (OUT == TAI_DT_FP16) static_cast<uint16_t*>(g.out)[idx] = f32_to_f16(f);
-            else static_cast<float*>(g.out)[idx] = f;
-          }
+          const uint32_t bits = out_bits(acc[i][j][r] + bcol, sc, bf, g.pts ? g.pts[row0 + lr] : 1.0f);
+          if constexpr (OUT == TAI_DT_BF16 || OUT == TAI_DT_FP16) static_cast<uint16_t*>(g.out)[idx] = static_cast<uint16_t>(bits);
+          else static_cast<uint32_t*>(g.out)[idx] = bits;
         }
       }
     }
