@@ -357,15 +357,15 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     return Lkv;
   };
   const bool wave_live = unit_ok && q0 < Lq;
-  const int64_t wave_kv = wave_live ? max<int64_t>(0, kv_limit(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
+  const int64_t wave_kv = wave_live ? imax64(0, kv_limit(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
   // tokens below this need no mask for any query of the wave
-  const int64_t wave_clean = wave_live ? max<int64_t>(0, kv_limit(q0)) - (a.causal ? 1 : 0) : 0;
+  const int64_t wave_clean = wave_live ? imax64(0, kv_limit(q0)) - (a.causal ? 1 : 0) : 0;
   int64_t blk_kv = 0;
   {
     const int last_unit = min(jb * 4 + 3, a.units_per_bk - 1);
     const int qt_hi = last_unit / a.g;  // units are qtile-major, so the last unit has the largest tile
     const int64_t qlast = min<int64_t>(static_cast<int64_t>(qt_hi) * kPQ + kPQ, Lq) - 1;
-    blk_kv = qlast >= 0 ? max<int64_t>(0, kv_limit(qlast)) : 0;
+    blk_kv = qlast >= 0 ? imax64(0, kv_limit(qlast)) : 0;
   }
 
   // Q^T fragments (B operand): query = col, d slots 16*kd + 8*grp .. +8

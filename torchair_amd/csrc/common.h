@@ -99,6 +99,33 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
+// 64-bit integer max / min (HIP's max/min templates promote mixed int / int64 arguments to double).
+__host__ __device__ __forceinline__ int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
+__host__ __device__ __forceinline__ int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+// Inclusive scan over the block (blockDim.x a multiple of 64, at most 1024) of one value per
+// thread, combining with + (MAX = false) or max (MAX = true). `red` holds 16 values; every thread
+// of the block must call it.
+template <bool MAX, class T>
+__device__ __forceinline__ T block_incl_scan(T x, T* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const T u = __shfl_up(x, o, kWave);
+    if (lane >= o) x = MAX ? (u > x ? u : x) : x + u;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  if (w > 0) {
+    T pre = red[0];
+    for (int i = 1; i < w; ++i) pre = MAX ? (red[i] > pre ? red[i] : pre) : pre + red[i];
+    x = MAX ? (pre > x ? pre : x) : x + pre;
+  }
+  (void)nw;
+  return x;
+}
+
 __device__ __forceinline__ int64_t load_index(const void* p, int dtype, int64_t i) {
   return dtype == TAI_DT_INT64 ? static_cast<const int64_t*>(p)[i]
                                : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);

@@ -275,29 +275,44 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmArgs g, int la
 
 // ----------------------------------------------------------------------------- grouped prologue
 // Builds the tile table for row tiles of height bm, plus a row->group map for the generic path.
+// One workgroup of 1024 threads, groups 2t and 2t + 1 per thread (ng <= 2048): group ends are a
+// prefix sum of the counts (list type 1) or a running max of the cumulative ends (type 0), both
+// clamped to m; tile offsets are a prefix sum of the per-group tile counts.
 __global__ __launch_bounds__(1024) void group_tiles_kernel(const int64_t* __restrict__ gl, int64_t ng, int list_type,
                                                           int64_t m, int bm, int4* __restrict__ map, int64_t slots,
                                                           int32_t* __restrict__ row_group) {
   extern __shared__ int64_t sh[];  // begin[ng], end[ng], tile_prefix[ng + 1]
+  __shared__ int64_t red[16];
   int64_t* beg = sh;
   int64_t* end = sh + ng;
   int64_t* tp = sh + 2 * ng;
-  if (threadIdx.x == 0) {
-    int64_t run = 0, tiles = 0;
-    for (int64_t e = 0; e < ng; ++e) {
-      int64_t b = run, en;
-      if (list_type == 1) en = run + max<int64_t>(gl[e], 0);
-      else en = max<int64_t>(gl[e], run);
-      b = min<int64_t>(b, m);
-      en = min<int64_t>(en, m);
-      beg[e] = b;
-      end[e] = en;
-      tp[e] = tiles;
-      tiles += (en - b + bm - 1) / bm;
-      run = en;
-    }
-    tp[ng] = tiles;
+  const int64_t e0 = 2 * static_cast<int64_t>(threadIdx.x), e1 = e0 + 1;
+  const int64_t g0 = e0 < ng ? gl[e0] : 0, g1 = e1 < ng ? gl[e1] : 0;
+  int64_t end0, end1, beg0;
+  if (list_type == 1) {
+    const int64_t c0 = imax64(g0, 0), c1 = imax64(g1, 0);
+    const int64_t incl = block_incl_scan<false>(c0 + c1, red);
+    beg0 = incl - c0 - c1;
+    end0 = beg0 + c0;
+    end1 = incl;
+  } else {
+    __shared__ int64_t incl_sh[1024];
+    const int64_t incl = block_incl_scan<true>(imax64(imax64(g0, g1), 0), red);
+    incl_sh[threadIdx.x] = incl;
+    __syncthreads();
+    beg0 = threadIdx.x ? incl_sh[threadIdx.x - 1] : 0;  // running max before this thread's pair
+    end0 = max<int64_t>(beg0, g0);
+    end1 = max<int64_t>(end0, g1);
   }
+  beg0 = min<int64_t>(beg0, m);
+  end0 = min<int64_t>(end0, m);
+  end1 = min<int64_t>(end1, m);
+  const int64_t t0 = e0 < ng ? (end0 - beg0 + bm - 1) / bm : 0;
+  const int64_t t1 = e1 < ng ? (end1 - end0 + bm - 1) / bm : 0;
+  const int64_t tincl = block_incl_scan<false>(t0 + t1, red);
+  if (e0 < ng) { beg[e0] = beg0; end[e0] = end0; tp[e0] = tincl - t0 - t1; }
+  if (e1 < ng) { beg[e1] = end0; end[e1] = end1; tp[e1] = tincl - t1; }
+  if (threadIdx.x == blockDim.x - 1) tp[ng] = tincl;
   __syncthreads();
   const int64_t real = tp[ng];
   const int64_t covered = ng > 0 ? end[ng - 1] : 0;

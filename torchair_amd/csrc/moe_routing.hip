@@ -191,38 +191,46 @@ __global__ __launch_bounds__(kChunk) void route_hist_kernel(const int32_t* __res
   for (int b = threadIdx.x; b < bins; b += blockDim.x) hist[static_cast<int64_t>(b) * chunks + blockIdx.x] = h[b];
 }
 
-// K2: one workgroup. Turns counts into exclusive destination offsets (expert-major,
-// chunk-minor) and writes the per-expert token counts / cumsum.
+// K2: one workgroup of 1024 threads. Turns counts into exclusive destination offsets
+// (expert-major, chunk-minor) and writes the per-expert token counts / cumsum. One wave per
+// expert row of the histogram (lanes walk the chunks, coalesced); the per-expert totals are
+// scanned across the block (bins <= 1024: one per thread).
 __global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ hist, int64_t chunks, int bins,
                                                           int64_t* __restrict__ tokens, int tokens_cumsum,
                                                           int32_t* __restrict__ total) {
-  extern __shared__ int32_t tot[];  // [bins] then scan scratch
-  for (int b = threadIdx.x; b < bins; b += blockDim.x) {
-    int32_t s = 0;
-    int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
-    for (int64_t c = 0; c < chunks; ++c) s += hb[c];
-    tot[b] = s;
+  extern __shared__ int32_t tot[];  // [bins] totals, then [bins] exclusive bases
+  __shared__ int32_t red[16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int b = w; b < bins; b += nw) {
+    const int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
+    int32_t sum = 0;
+    for (int64_t c = lane; c < chunks; c += 64) sum += hb[c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) tot[b] = sum;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {  // bins <= 1024: a serial scan is a few microseconds at most
-    int32_t run = 0;
-    for (int b = 0; b < bins; ++b) {
-      int32_t c = tot[b];
-      tot[bins + b] = run;
-      run += c;
-    }
-    *total = run;
-  }
+  const int32_t mine = static_cast<int>(threadIdx.x) < bins ? tot[threadIdx.x] : 0;
+  const int32_t incl = block_incl_scan<false>(mine, red);
+  if (static_cast<int>(threadIdx.x) < bins) tot[bins + threadIdx.x] = incl - mine;
+  if (threadIdx.x == blockDim.x - 1) *total = incl;
   __syncthreads();
-  for (int b = threadIdx.x; b < bins; b += blockDim.x) {
-    int32_t run = tot[bins + b];
+  for (int b = w; b < bins; b += nw) {
     int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
-    for (int64_t c = 0; c < chunks; ++c) {
-      int32_t v = hb[c];
-      hb[c] = run;
-      run += v;
+    int32_t carry = tot[bins + b];
+    for (int64_t c0 = 0; c0 < chunks; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const int32_t v = c < chunks ? hb[c] : 0;
+      int32_t x = v;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t u = __shfl_up(x, o, 64);
+        if (lane >= o) x += u;
+      }
+      if (c < chunks) hb[c] = carry + x - v;
+      carry += __shfl(x, 63, 64);
     }
-    if (tokens) tokens[b] = tokens_cumsum ? static_cast<int64_t>(run) : static_cast<int64_t>(tot[b]);
+    if (tokens && lane == 0) tokens[b] = tokens_cumsum ? static_cast<int64_t>(carry) : static_cast<int64_t>(tot[b]);
   }
 }
 
