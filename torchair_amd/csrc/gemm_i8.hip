@@ -686,8 +686,10 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
 // Tile configurations used by the host (8 waves of 64 x 128, 256 x 256 tiles):
 //   dense: 128-byte K stages, two stages (128 KB of LDS): the 8192^3 GEMM is MFMA/LDS bound and
 //     fewer, larger stages halve the barriers;
-//   grouped: 64-byte K stages, four stages (128 KB): MoE expert GEMMs stream their weights from
-//     HBM, and three stages in flight instead of one cut the gate_up time by ~6%.
+//   grouped: 64-byte K stages, four stages: MoE expert GEMMs stream their weights from HBM, and
+//     three stages in flight instead of one cut the gate_up time by ~6%. [K, N] weights use
+//     128 x 512 tiles (2 x 4 waves, 160 KB): equal on gate_up, 9% faster on the down projection
+//     (N = 7168); [N, K] weights keep 256 x 256.
 // Measured and rejected on the MoE gate_up and 8192^3 shapes: 128 x 256 tiles (4 waves, 3-4
 // stages), and a 4-wave kernel with 128 x 128 wave tiles and software-pipelined fragment reads;
 // with one wave per SIMD the per-stage barrier and LDS reads cost more than the halved LDS
@@ -698,8 +700,12 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
 #ifndef TAI_GRP_SEL
 #define TAI_GRP_SEL BigCfg<4, 2, 64, 4>
 #endif
+#ifndef TAI_GRP_KN_SEL
+#define TAI_GRP_KN_SEL BigCfg<2, 4, 64, 4>
+#endif
 using BigSel = TAI_BIG_SEL;
-using GrpSel = TAI_GRP_SEL;
+using GrpSel = TAI_GRP_SEL;      // grouped, [N, K] weights
+using GrpKnSel = TAI_GRP_KN_SEL;  // grouped, [K, N] weights
 constexpr int kBigBK = BigSel::kBK;
 constexpr int kBigBM = BigSel::kBM, kBigBN = BigSel::kBN;
 
@@ -839,14 +845,17 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     return TAI_ERR_WORKSPACE;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool big = k % GrpSel::kBK == 0 && (w_layout == TAI_LAYOUT_NK || n % 16 == 0) && cfg_available<GrpSel>();
-  const int bm = big ? GrpSel::kBM : kGroupedBM;
+  const bool kn = w_layout == TAI_LAYOUT_KN;
+  const bool big = kn ? (k % GrpKnSel::kBK == 0 && n % 16 == 0 && cfg_available<GrpKnSel>())
+                      : (k % GrpSel::kBK == 0 && cfg_available<GrpSel>());
+  const int bm = big ? (kn ? GrpKnSel::kBM : GrpSel::kBM) : kGroupedBM;
+  const int bn = big ? (kn ? GrpKnSel::kBN : GrpSel::kBN) : 128;
   const int64_t slots = static_cast<int64_t>(grouped_map_slots(m, num_groups, bm));
   int4* map = static_cast<int4*>(workspace);
   int32_t* row_group = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                   sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM));
   GemmArgs g{x, weight, m, k, n, k * n, scale, n, n, per_token_scale, bias, bias_dtype, n, out_dtype, out,
-             map, slots, cdiv(n, big ? GrpSel::kBN : 128)};
+             map, slots, cdiv(n, bn)};
   const bool fast = fast_path_ok(g, w_layout);
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type, m,
                                                                               bm, map, slots,
@@ -855,7 +864,8 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, w_layout, row_group);
     return launch_status("tai_grouped_matmul");
   }
-  if (big) launch_cfg<GrpSel>(g, w_layout, st);
+  if (big && kn) launch_cfg<GrpKnSel>(g, w_layout, st);
+  else if (big) launch_cfg<GrpSel>(g, w_layout, st);
   else launch_tile<128, 128>(g, w_layout, st);
   return launch_status("tai_grouped_matmul");
 }
