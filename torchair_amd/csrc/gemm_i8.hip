@@ -41,15 +41,54 @@ struct GemmArgs {
   int64_t bias_group_stride;
   int out_dt;
   void* out;
-  const int4* tile_map;  // grouped: (group, row_begin, row_end, kind); kind -1 unused, -2 zero-fill
+  // grouped: per row-tile slot (group, group_row_begin, group_row_end, index of the slot within its
+  // group); group -1 marks an unused slot and -2 a zero-fill slot (then y, z are the slot's rows)
+  const int4* tile_map;
   int64_t m_slots;
   int64_t n_tiles;
+  const int64_t* live_slots;  // grouped: slots in use (real + zero-fill tiles), written by the prologue
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   const int64_t xcd = b % kXcds, idx = b / kXcds;
   const int64_t per = nb / kXcds, rem = nb % kXcds;
   return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// Linear tile id of workgroup b, or -1 when it has nothing to do. Grouped launches size the grid
+// for the worst case of the device-resident group list; only the first `live` tile ids carry work,
+// and each XCD takes an equal contiguous share of them (a plain remap of the whole grid would give
+// the XCDs holding the upper ids nothing but empty slots).
+__device__ __forceinline__ int64_t tile_id(const GemmArgs& g, int64_t b) {
+  const int64_t nb = g.m_slots * g.n_tiles;
+  if (!g.live_slots) return xcd_remap(b, nb);
+  const int64_t live = *g.live_slots * g.n_tiles;
+  const int64_t xcd = b % kXcds, idx = b / kXcds;
+  const int64_t per = live / kXcds, rem = live % kXcds;
+  if (idx >= per + (xcd < rem ? 1 : 0)) return -1;
+  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// Grouped launches: linear tile id L -> (group, rows, column tile). The row tiles of one group that
+// share a column tile are consecutive in L, so within an XCD they run together and read each weight
+// slice from HBM once (the slice is then served from that XCD's L2 to the group's other row tiles).
+// Returns the group, -1 (nothing to do) or -2 (zero-fill rows past the grouped total).
+__device__ __forceinline__ int grouped_tile(const GemmArgs& g, int64_t L, int bm, int& row0, int& row1, int64_t& nt) {
+  const int64_t s0 = L / g.n_tiles;
+  const int4 t = g.tile_map[s0];
+  if (t.x < 0) {
+    row0 = t.y;
+    row1 = t.z;
+    nt = L % g.n_tiles;
+    return t.x;
+  }
+  const int64_t first = s0 - t.w;
+  const int64_t rt = (static_cast<int64_t>(t.z) - t.y + bm - 1) / bm;
+  const int64_t off = L - first * g.n_tiles;
+  nt = off / rt;
+  row0 = t.y + static_cast<int>(off % rt) * bm;
+  row1 = row0 + bm < t.z ? row0 + bm : t.z;
+  return t.x;
 }
 
 // 4x4 byte transpose: in[r] holds bytes (r,0..3); out[c] holds bytes (0..3,c).
@@ -156,17 +195,17 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t s_b[2][BN * kLdk];
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
 
-  const int64_t nb = g.m_slots * g.n_tiles;
-  const int64_t L = xcd_remap(blockIdx.x, nb);
-  const int64_t slot = L / g.n_tiles, nt = L % g.n_tiles;
-  const int64_t n0 = nt * BN;
+  const int64_t L = tile_id(g, blockIdx.x);
+  if (L < 0) return;
+  int64_t nt = L % g.n_tiles;
   int e = 0, row0, row1;
   if (g.tile_map) {
-    const int4 t = g.tile_map[slot];
-    if (t.x == -1) return;
-    row0 = t.y;
-    row1 = t.z;
-    if (t.x == -2) {  // rows past the grouped total
+    e = grouped_tile(g, L, BM, row0, row1, nt);
+  }
+  const int64_t n0 = nt * BN;
+  if (g.tile_map) {
+    if (e == -1) return;
+    if (e == -2) {  // rows past the grouped total
       for (int idx = threadIdx.x; idx < (row1 - row0) * BN; idx += 256) {
         const int64_t r = row0 + idx / BN, c = n0 + idx % BN;
         if (c < g.n) {
@@ -176,8 +215,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs g) {
       }
       return;
     }
-    e = t.x;
   } else {
+    const int64_t slot = L / g.n_tiles;
     row0 = static_cast<int>(slot * BM);
     row1 = static_cast<int>(min<int64_t>(g.m, row0 + BM));
   }
@@ -280,7 +319,7 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmArgs g, int la
 // clamped to m; tile offsets are a prefix sum of the per-group tile counts.
 __global__ __launch_bounds__(1024) void group_tiles_kernel(const int64_t* __restrict__ gl, int64_t ng, int list_type,
                                                           int64_t m, int bm, int4* __restrict__ map, int64_t slots,
-                                                          int32_t* __restrict__ row_group) {
+                                                          int64_t* __restrict__ live, int32_t* __restrict__ row_group) {
   extern __shared__ int64_t sh[];  // begin[ng], end[ng], tile_prefix[ng + 1]
   __shared__ int64_t red[16];
   int64_t* beg = sh;
@@ -317,6 +356,7 @@ __global__ __launch_bounds__(1024) void group_tiles_kernel(const int64_t* __rest
   const int64_t real = tp[ng];
   const int64_t covered = ng > 0 ? end[ng - 1] : 0;
   const int64_t zero_tiles = (m - covered + bm - 1) / bm;
+  if (threadIdx.x == 0) *live = real + zero_tiles;
   for (int64_t s = threadIdx.x; s < slots; s += blockDim.x) {
     int4 t = make_int4(-1, 0, 0, 0);
     if (s < real) {
@@ -325,8 +365,8 @@ __global__ __launch_bounds__(1024) void group_tiles_kernel(const int64_t* __rest
         const int64_t mid = (lo + hi + 1) >> 1;
         if (tp[mid] <= s) lo = mid; else hi = mid - 1;
       }
-      const int64_t r0 = beg[lo] + (s - tp[lo]) * bm;
-      t = make_int4(static_cast<int>(lo), static_cast<int>(r0), static_cast<int>(min<int64_t>(r0 + bm, end[lo])), 0);
+      t = make_int4(static_cast<int>(lo), static_cast<int>(beg[lo]), static_cast<int>(end[lo]),
+                    static_cast<int>(s - tp[lo]));
     } else if (s < real + zero_tiles) {
       const int64_t r0 = covered + (s - real) * bm;
       t = make_int4(-2, static_cast<int>(r0), static_cast<int>(min<int64_t>(r0 + bm, m)), 0);
@@ -370,9 +410,11 @@ void launch_tile(const GemmArgs& g, int layout, hipStream_t st) {
 // LDS layouts (each 16-byte chunk placed by the lane that loads it, so swizzles cost nothing):
 //   A and an [N,K] weight: [rows][64 B]; chunk c of row r stored at chunk c ^ ((r >> 2) & 3)
 //     -> 16-byte fragment reads of 16 consecutive rows cover the 64 banks once.
-//   a [K,N] weight: [64 k rows][BN B]; chunk c of row r stored at chunk c ^ (r & 7); fragments
+//   a [K,N] weight: [64 k rows][BN B]; chunk c of row r stored at chunk c ^ 2(r & 7); fragments
 //     are read with ds_read_b64_tr_b8 (in each 16-lane group source lane L addresses
-//     B[k0 + L/2][n0 + 8*(L&1)] and output lane j receives B[k0..k0+7][n0 + j]).
+//     B[k0 + L/2][n0 + 8*(L&1)] and output lane j receives B[k0..k0+7][n0 + j]). The two 16-lane
+//     groups of a 32-lane LDS pass read chunks c and c + 1 of the same 8 rows; the even XOR keeps
+//     them on disjoint banks (an XOR by r & 7 maps both onto the same 32 banks).
 // Requires K % 64 == 0 (stage loads cannot zero-fill a K tail). Rows and columns past the end of
 // the tile are loaded from clamped addresses and never stored.
 template <int WM, int WN, int BK, int STAGES>
@@ -388,6 +430,7 @@ struct BigCfg {
   static constexpr int kBLoads = kBN * BK / 1024 / (WM * WN);
   static constexpr int kLoads = kALoads + kBLoads;
   static_assert(kALoads * WM * WN * 1024 == kBM * BK && kBLoads * WM * WN * 1024 == kBN * BK, "load split");
+  static_assert(kBN >= 256, "the [K,N] swizzle spans 16 chunks of a weight row");
 };
 
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -443,7 +486,7 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
     } else {
       constexpr int CPN = C::kBN / 16;  // chunks per k row
       const int kr = (1024 / C::kBN) * q + lane / CPN;
-      const int c = (lane % CPN) ^ (kr & 7);
+      const int c = (lane % CPN) ^ ((kr & 7) << 1);
       const int64_t nn = n0 + 16 * c < g.n ? n0 + 16 * c : g.n - 16;
       src = bgrp + (k0 + kr) * g.n + nn;
     }
@@ -457,12 +500,12 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   constexpr int kBigBK = C::kBK;
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
-  const int64_t nb = g.m_slots * g.n_tiles;
-  const int64_t L = xcd_remap(blockIdx.x, nb);
-  int64_t slot, nt;
+  const int64_t L = tile_id(g, blockIdx.x);
+  if (L < 0) return;
+  int64_t slot = 0, nt;
+  int e = 0, row0, row1;
   if (g.tile_map) {
-    slot = L / g.n_tiles;
-    nt = L % g.n_tiles;
+    e = grouped_tile(g, L, C::kBM, row0, row1, nt);
   } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
     constexpr int64_t GM = 8;
     const int64_t per_group = GM * g.n_tiles;
@@ -473,13 +516,9 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     nt = in / gsize;
   }
   const int64_t n0 = nt * C::kBN;
-  int e = 0, row0, row1;
   if (g.tile_map) {
-    const int4 t = g.tile_map[slot];
-    if (t.x == -1) return;
-    row0 = t.y;
-    row1 = t.z;
-    if (t.x == -2) {
+    if (e == -1) return;
+    if (e == -2) {
       for (int idx = threadIdx.x; idx < (row1 - row0) * C::kBN; idx += C::kThreads) {
         const int64_t r = row0 + idx / C::kBN, c = n0 + idx % C::kBN;
         if (c < g.n) {
@@ -489,7 +528,6 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
       }
       return;
     }
-    e = t.x;
   } else {
     row0 = static_cast<int>(slot * C::kBM);
     row1 = row0 + C::kBM < g.m ? row0 + C::kBM : static_cast<int>(g.m);
@@ -535,8 +573,8 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     } else {
       const int col = bc_lane + 32 * j;
       const int k_lo = kk * 32 + bk_lane, k_hi = k_lo + 8;
-      const int8_t* plo = bs + k_lo * C::kBN + 16 * ((col >> 4) ^ (k_lo & 7)) + (col & 15);
-      const int8_t* phi = bs + k_hi * C::kBN + 16 * ((col >> 4) ^ (k_hi & 7)) + (col & 15);
+      const int8_t* plo = bs + k_lo * C::kBN + 16 * ((col >> 4) ^ ((k_lo & 7) << 1)) + (col & 15);
+      const int8_t* phi = bs + k_hi * C::kBN + 16 * ((col >> 4) ^ ((k_hi & 7) << 1)) + (col & 15);
       return ds_read_tr8_pair(plo, phi);
     }
   };
@@ -818,7 +856,8 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
 
 extern "C" size_t tai_grouped_matmul_workspace_size(int64_t m, int64_t n, int64_t num_groups) {
   (void)n;
-  return sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM) + sizeof(int32_t) * static_cast<size_t>(m) + 256;
+  // [live slot count, padded to 256 B][tile map][row -> group map]
+  return 256 + sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM) + sizeof(int32_t) * static_cast<size_t>(m) + 256;
 }
 
 extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
@@ -851,14 +890,15 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
   const int bm = big ? (kn ? GrpKnSel::kBM : GrpSel::kBM) : kGroupedBM;
   const int bn = big ? (kn ? GrpKnSel::kBN : GrpSel::kBN) : 128;
   const int64_t slots = static_cast<int64_t>(grouped_map_slots(m, num_groups, bm));
-  int4* map = static_cast<int4*>(workspace);
-  int32_t* row_group = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+  int64_t* live = static_cast<int64_t*>(workspace);
+  int4* map = reinterpret_cast<int4*>(static_cast<char*>(workspace) + 256);
+  int32_t* row_group = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 256 +
                                                   sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM));
   GemmArgs g{x, weight, m, k, n, k * n, scale, n, n, per_token_scale, bias, bias_dtype, n, out_dtype, out,
-             map, slots, cdiv(n, bn)};
+             map, slots, cdiv(n, bn), live};
   const bool fast = fast_path_ok(g, w_layout);
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type, m,
-                                                                              bm, map, slots,
+                                                                              bm, map, slots, live,
                                                                               fast ? nullptr : row_group);
   if (!fast) {
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, w_layout, row_group);
