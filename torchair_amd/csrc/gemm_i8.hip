@@ -14,6 +14,8 @@
 // Linear workgroup ids are remapped so that each XCD (ids dispatched round-robin over 8
 // XCDs) receives a contiguous range of tiles: tiles that share activation rows and weight
 // columns meet in the same L2.
+#include <type_traits>
+
 #include "common.h"
 
 namespace tai {
@@ -445,7 +447,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Two ds_read_b64_tr_b8 into one 16-byte fragment (bytes 0-7 from `lo`, 8-15 from `hi`),
 // issued as inline asm: the builtin makes the compiler drain the in-flight global->LDS ring
-// before the read. The caller waits lgkmcnt(0) (lds_wait_frags) before using the result.
+// before the read. The caller waits with lgkm_wait before using the result.
 __device__ __forceinline__ v4i ds_read_tr8_pair(const int8_t* lo, const int8_t* hi) {
   v2i a, b;
   const uint32_t alo = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const int8_t*)lo));
@@ -455,9 +457,19 @@ __device__ __forceinline__ v4i ds_read_tr8_pair(const int8_t* lo, const int8_t* 
   return v4i{a[0], a[1], b[0], b[1]};
 }
 
-// Waits for outstanding LDS reads; the fragments are threaded through so their uses stay after it.
-__device__ __forceinline__ void lds_wait_frags(v4i (&f)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+// 16-byte LDS read as inline asm (counted by lgkm_wait like the transposing reads).
+__device__ __forceinline__ v4i ds_read_b128(const int8_t* p) {
+  v4i r;
+  const uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const int8_t*)p));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+
+// Waits until at most N LDS operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is four bits");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
 
 template <int LAYOUT, class C>
@@ -560,16 +572,18 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   const int bk_lane = (lane >> 5) * 16 + (l16 >> 1);  // KN: k row within the 32-row kk block (+ 8)
   const int bc_lane = wn * 128 + ((lane >> 4) & 1) * 16 + (l16 & 1) * 8;  // KN: byte column (+ 32 j)
 
+  // Fragment reads are inline asm so that the waits below count them exactly (LDS reads complete in
+  // issue order): the reads for step kk + 1 are issued before the MFMAs of step kk.
   auto load_a = [&](const int8_t* st, int kk, int i) {
     const int r = arow + 32 * i;
     const int c = (2 * kk + (lane >> 5)) ^ ((r >> C::kRowShift) & (C::kCpr - 1));
-    return *reinterpret_cast<const v4i*>(st + r * kBigBK + 16 * c);
+    return ds_read_b128(st + r * kBigBK + 16 * c);
   };
   auto load_b = [&](const int8_t* bs, int kk, int j) -> v4i {
     if constexpr (LAYOUT == TAI_LAYOUT_NK) {
       const int r = brow + 32 * j;
       const int c = (2 * kk + (lane >> 5)) ^ ((r >> C::kRowShift) & (C::kCpr - 1));
-      return *reinterpret_cast<const v4i*>(bs + r * kBigBK + 16 * c);
+      return ds_read_b128(bs + r * kBigBK + 16 * c);
     } else {
       const int col = bc_lane + 32 * j;
       const int k_lo = kk * 32 + bk_lane, k_hi = k_lo + 8;
@@ -578,41 +592,90 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
       return ds_read_tr8_pair(plo, phi);
     }
   };
-
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int64_t ahead = nk - 1 - kt;  // stages issued after this one (at most kStages - 2)
+  constexpr int KK = kBigBK / 32;  // MFMA steps per stage
+  static_assert(KK % 2 == 0, "fragment double buffer alternates within a stage");
+  // Stage kt has landed in this wave's view once only the stages issued after it remain in flight.
+  auto wait_stage = [&](int64_t kt) {
+    const int64_t after = nk - 1 - kt < C::kStages - 2 ? nk - 1 - kt : C::kStages - 2;
     if constexpr (C::kStages == 2) {
-      wait_vmcnt<0>();  // the only loads in flight are this stage's
+      wait_vmcnt<0>();
     } else {
-      if (ahead >= C::kStages - 2) wait_vmcnt<C::kLoads * (C::kStages - 2)>();
-      else if (ahead == 2) wait_vmcnt<C::kLoads * 2>();
-      else if (ahead == 1) wait_vmcnt<C::kLoads>();
+      if (after >= C::kStages - 2) wait_vmcnt<C::kLoads * (C::kStages - 2)>();
+      else if (after == 2) wait_vmcnt<C::kLoads * 2>();
+      else if (after == 1) wait_vmcnt<C::kLoads>();
       else wait_vmcnt<0>();
     }
-    // Workgroup barrier that orders LDS only: the ring's later stages stay in flight across it
-    // (a fence here would drain every outstanding global->LDS load).
+  };
+  // Main loop for waves with NI live 32-row halves (NI = 0: the wave only takes part in the ring).
+  // Per stage kt: steps 0 .. KK-2 prefetch the next step's fragments and multiply the current ones;
+  // the last step waits for stage kt + 1, passes the workgroup barrier (after it no wave reads slot
+  // kt, whose fragments are in registers), refills slot kt with stage kt + S, prefetches the first
+  // fragments of stage kt + 1, then multiplies.
+  auto main_loop = [&](auto ni) {
+    constexpr int NI = decltype(ni)::value;
+    constexpr int NF = NI == 0 ? 0 : NI + (LAYOUT == TAI_LAYOUT_KN ? 8 : 4);  // LDS reads per step
+    v4i fa[2][NI > 0 ? NI : 1], fb[2][4];
+    auto fetch = [&](int buf, const int8_t* st, int kk) {
+      if constexpr (NI > 0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) fa[buf][i] = load_a(st, kk, i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[buf][j] = load_b(st + C::kBM * kBigBK, kk, j);
+      }
+    };
+    auto ready = [&](int buf) {  // orders the uses of buffer buf after the preceding wait
+      if constexpr (NI > 0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) asm volatile("" : "+v"(fa[buf][i]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(fb[buf][j]));
+      }
+    };
+    auto mfma = [&](int buf) {
+      if constexpr (NI > 0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+      }
+    };
+    wait_stage(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + C::kStages - 1 < nk)
-      big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (kt + C::kStages - 1) * kBigBK,
-                                      smem + ((kt + C::kStages - 1) % C::kStages) * C::kStage, w, lane);
-    const int8_t* st = smem + (kt % C::kStages) * C::kStage;
-    const int8_t* bs = st + C::kBM * kBigBK;
-    if (act_m > 0) {  // waves whose 64 rows are all past the group end skip the stage
+    if (C::kStages - 1 < nk)
+      big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (C::kStages - 1) * kBigBK,
+                                 smem + (C::kStages - 1) * C::kStage, w, lane);
+    fetch(0, smem, 0);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int8_t* st = smem + (static_cast<int>(kt) % C::kStages) * C::kStage;
 #pragma unroll
-      for (int kk = 0; kk < kBigBK / 32; ++kk) {
-        v4i fa[2], fb[4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) fa[i] = load_a(st, kk, i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) fb[j] = load_b(bs, kk, j);
-        if constexpr (LAYOUT == TAI_LAYOUT_KN) lds_wait_frags(fb);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int kk = 0; kk < KK; ++kk) {
+        const int cur = kk & 1;
+        if (kk + 1 < KK) {
+          fetch(cur ^ 1, st, kk + 1);
+          lgkm_wait<NF>();
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (kt + 1 < nk) {
+            wait_stage(kt + 1);
+            asm volatile("s_barrier" ::: "memory");
+            if (kt + C::kStages < nk)
+              big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (kt + C::kStages) * kBigBK,
+                                         smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
+            fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
+          }
+        }
+        ready(cur);
+        mfma(cur);
+        __builtin_amdgcn_sched_barrier(0);  // the next step's waits stay behind these MFMAs
       }
     }
-  }
+  };
+  // Waves whose 64 rows are all past the group end skip the MFMAs; waves with at most 32 live rows
+  // skip those of the upper 32 (wave-uniform branches).
+  if (act_m > 1) main_loop(std::integral_constant<int, 2>());
+  else if (act_m == 1) main_loop(std::integral_constant<int, 1>());
+  else main_loop(std::integral_constant<int, 0>());
 
   // Epilogue, specialised on the output dtype so the accumulators stay in registers.
   const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32)
