@@ -48,6 +48,10 @@ extern "C" {
 #define TAI_LAYOUT_KN 0 /* row-major [K, N] (N contiguous) */
 #define TAI_LAYOUT_NK 1 /* row-major [N, K] (K contiguous): the transpose_x2 / weight.t() view */
 
+/* Cache layouts of npu_scatter_pa_kv_cache (cache_mode). */
+#define TAI_CACHE_NORM 0  /* [num_blocks, block_size, row]: a slot's row is contiguous */
+#define TAI_CACHE_PA_NZ 1 /* [num_blocks, row_bytes / 32, block_size, 32 bytes] (FRACTAL_NZ) */
+
 const char* tai_last_error(void);
 int tai_abi_version(void);
 
@@ -241,6 +245,70 @@ int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const int8_t* ckv
                        const int64_t* seq_lens_kv, int64_t b, int hq, int dn, int dr,
                        int block_size, float scale, void* out, float* lse, void* workspace,
                        size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_add_rms_norm: x = x1 + x2; y = x * rstd * gamma with rstd = 1/sqrt(mean(x^2) + eps).
+ * Replaces ge.AddRmsNorm emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_add_rms_norm.py:4-13 (prototype nn_norm.h:50-58).
+ * x1, x2, y, x_out: [rows, cols] of dtype (BF16/FP16/FP32); gamma: [cols] of dtype;
+ * rstd: NULL or [rows] fp32; x_out: NULL or x1 + x2 rounded to dtype.
+ * ------------------------------------------------------------------------------------- */
+int tai_add_rms_norm(const void* x1, const void* x2, const void* gamma, int dtype, int64_t rows,
+                     int64_t cols, float epsilon, void* y, float* rstd, void* x_out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_add_rms_norm_dynamic_quant: add_rms_norm (+ beta), then symmetric per-row int8
+ * quantisation of y (rounded to dtype) times smooth_scale1 (and, when y2 is given, times
+ * smooth_scale2). Replaces ge.AddRmsNormDynamicQuant emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_add_rms_norm_dynamic_quant.py:8-21
+ * and is the target of TorchAir's fusion pattern
+ *   python/torchair/patterns/add_rms_norm_dynamic_quant.py:67-80.
+ * beta, smooth_scale1/2: NULL or [cols]; y1/y2: [rows, cols] int8; scale1/2: [rows] fp32.
+ * ------------------------------------------------------------------------------------- */
+int tai_add_rms_norm_dynamic_quant(const void* x1, const void* x2, const void* gamma,
+                                   const void* beta, const float* smooth_scale1,
+                                   const float* smooth_scale2, int dtype, int64_t rows,
+                                   int64_t cols, float epsilon, int8_t* y1, int8_t* y2,
+                                   void* x_out, float* scale1, float* scale2, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_scatter_pa_kv_cache: writes token t's key / value rows into cache slot slot_mapping[t]
+ * (slot = block * block_size + offset; negative slots are skipped).
+ * Replaces ge.ScatterPaKvCache emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_scatter_pa_kv_cache.py:44-74
+ *   (prototype experiment_ops.h:3963-4002).
+ * key / value: [tokens, *] contiguous rows of key_row_bytes / value_row_bytes; caches in
+ * TAI_CACHE_NORM or TAI_CACHE_PA_NZ layout; slot_mapping: [tokens] INT32/INT64.
+ * ------------------------------------------------------------------------------------- */
+int tai_scatter_pa_kv_cache(const void* key, const void* value, void* key_cache,
+                            void* value_cache, const void* slot_mapping, int slot_dtype,
+                            int64_t tokens, int64_t key_row_bytes, int64_t value_row_bytes,
+                            int64_t num_blocks, int64_t block_size, int cache_mode, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_kv_rmsnorm_rope_cache: the MLA cache update. Per token: c_kv = rms_norm(kv[:dc]) *
+ * gamma; k_rope = interleaved RoPE of kv[dc:] with cos / sin; both written to their caches at
+ * the token's cache row. Replaces ge.KvRmsNormRopeCache emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_kv_rmsnorm_rope_cache.py:4-66
+ *   (prototype experiment_ops.h:3677-3697; meta auto_register_custom_torch_ops.py:82-110).
+ * kv: [tokens, dc + dr], cos / sin: [tokens, dr], gamma: [dc], all of dtype.
+ * index: [tokens] int64 cache row (PA layouts, norm_rows = 0) or position inside the token's
+ * batch (Norm layout: batch = token / seq, row = batch * norm_rows + index); negative skips.
+ * k_cache: rows of dr (dtype, or int8 quantised with k_rope_scale [dr] (+ offset)).
+ * ckv_cache: rows of dc (dtype, or int8): with c_kv_scale [dc] (+ offset) a static
+ * per-channel quantisation round(v * scale + offset); with c_kv_token_scale (a [cache_rows]
+ * fp32 cache) a per-token dynamic quantisation whose scale is stored there - the int8 latent
+ * format tai_fia_mla_decode reads.
+ * k_rope_out / c_kv_out: NULL or [tokens, dr] / [tokens, dc] of dtype.
+ * ------------------------------------------------------------------------------------- */
+int tai_kv_rmsnorm_rope_cache(const void* kv, const void* gamma, const void* cos, const void* sin,
+                              const int64_t* index, int dtype, int64_t tokens, int64_t seq, int dc,
+                              int dr, float epsilon, void* k_cache, int k_cache_dtype,
+                              void* ckv_cache, int ckv_cache_dtype, int64_t cache_rows,
+                              int64_t norm_rows, const float* k_rope_scale,
+                              const float* k_rope_offset, const float* c_kv_scale,
+                              const float* c_kv_offset, float* c_kv_token_scale, void* k_rope_out,
+                              void* c_kv_out, void* stream);
 
 #ifdef __cplusplus
 }

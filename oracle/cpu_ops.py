@@ -108,8 +108,78 @@ def register() -> None:
                                    0 if drop_pad_mode is None else drop_pad_mode, _NAMES[ex.dtype])
         return _t(y, ex.dtype)
 
+    def arn(x1, x2, gamma, epsilon=1e-6):
+        y, rstd, x = G.add_rms_norm(_np(x1), _np(x2), _np(gamma), epsilon, _NAMES[x1.dtype])
+        return _t(y, x1.dtype), _t(rstd), _t(x, x1.dtype)
+
+    def arnq(x1, x2, gamma, *, smooth_scale1=None, smooth_scale2=None, beta=None, epsilon=1e-6, output_mask=()):
+        mask = list(output_mask or [])
+        second = bool(mask[1]) if mask else smooth_scale2 is not None
+        y1, y2, x, s1, s2 = G.add_rms_norm_dynamic_quant(_np(x1), _np(x2), _np(gamma), _np(smooth_scale1),
+                                                         _np(smooth_scale2), _np(beta), epsilon, second,
+                                                         _NAMES[x1.dtype])
+        if not second:
+            y2, s2 = np.zeros_like(y1), np.zeros_like(s1)
+        return _t(y1), _t(y2), _t(x, x1.dtype), _t(s1), _t(s2)
+
+    def _cache_np(c):
+        return c.numpy() if c.dtype in (torch.int8, torch.int32, torch.int64, torch.float32) else _np(c)
+
+    def scatter_functional(key, value, key_cache, value_cache, slot_mapping, *, compress_lens=None,
+                           compress_seq_offsets=None, seq_lens=None, cache_mode="Norm"):
+        kc, vc = G.scatter_pa_kv_cache(_cache_np(key), _cache_np(value), _cache_np(key_cache),
+                                       _cache_np(value_cache), slot_mapping.numpy(), cache_mode)
+        return _t(kc, key_cache.dtype), _t(vc, value_cache.dtype)
+
+    def scatter_inplace(key, value, key_cache, value_cache, slot_mapping, *, compress_lens=None,
+                        compress_seq_offsets=None, seq_lens=None, cache_mode="Norm"):
+        kc, vc = scatter_functional(key, value, key_cache, value_cache, slot_mapping, cache_mode=cache_mode)
+        key_cache.copy_(kc)
+        value_cache.copy_(vc)
+
+    def _kv(kv, gamma, cos, sin, index, k_cache, ckv_cache, k_rope_scale, c_kv_scale, k_rope_offset, c_kv_offset,
+            epsilon, cache_mode):
+        per_token = ckv_cache.dtype == torch.int8 and c_kv_scale is not None and c_kv_scale.dim() >= 2
+        res = G.kv_rmsnorm_rope_cache(_np(kv), _np(gamma), _np(cos), _np(sin), index.numpy(), _cache_np(k_cache),
+                                      _cache_np(ckv_cache), epsilon, cache_mode, _np(k_rope_scale),
+                                      _np(k_rope_offset), None if per_token else _np(c_kv_scale), _np(c_kv_offset),
+                                      c_kv_scale.numpy() if per_token else None, _NAMES[kv.dtype])
+        kc, cc, kr, ckv = res[:4]
+        return (_t(kc, k_cache.dtype), _t(cc, ckv_cache.dtype), _t(kr, kv.dtype), _t(ckv, kv.dtype),
+                _t(res[4]) if per_token else None)
+
+    def kv_v2(kv, gamma, cos, sin, index, k_cache, ckv_cache, *, k_rope_scale=None, c_kv_scale=None,
+              k_rope_offset=None, c_kv_offset=None, v=None, epsilon=1e-5, cache_mode="Norm", is_output_kv=False):
+        kc, cc, kr, ckv, ts = _kv(kv, gamma, cos, sin, index, k_cache, ckv_cache, k_rope_scale, c_kv_scale,
+                                  k_rope_offset, c_kv_offset, epsilon, cache_mode)
+        k_cache.copy_(kc)
+        ckv_cache.copy_(cc)
+        if ts is not None:
+            c_kv_scale.copy_(ts)
+        return kr, ckv
+
+    def kv_v2f(kv, gamma, cos, sin, index, k_cache, ckv_cache, *, k_rope_scale=None, c_kv_scale=None,
+               k_rope_offset=None, c_kv_offset=None, v=None, epsilon=1e-5, cache_mode="Norm", is_output_kv=False):
+        kc, cc, kr, ckv, _ = _kv(kv, gamma, cos, sin, index, k_cache, ckv_cache, k_rope_scale, c_kv_scale,
+                                 k_rope_offset, c_kv_offset, epsilon, cache_mode)
+        return kr, ckv, kc, cc
+
+    def kv_legacy(kv, gamma, cos, sin, index, k_cache, ckv_cache, *, k_rope_scale=None, c_kv_scale=None,
+                  k_rope_offset=None, c_kv_offset=None, v=None, epsilon=1e-5, cache_mode="Norm", is_output_kv=False):
+        kc, cc, kr, ckv, _ = _kv(kv, gamma, cos, sin, index, k_cache, ckv_cache, k_rope_scale, c_kv_scale,
+                                 k_rope_offset, c_kv_offset, epsilon, cache_mode)
+        return kc, cc, kr, ckv
+
     for ns in ("npu",):
         lib = LIBS[ns]
+        lib.impl("npu_add_rms_norm", arn, "CPU")
+        lib.impl("npu_add_rms_norm_dynamic_quant", arnq, "CPU")
+        lib.impl("npu_scatter_pa_kv_cache", scatter_inplace, "CPU")
+        lib.impl("npu_scatter_pa_kv_cache_functional", scatter_functional, "CPU")
+        lib.impl("npu_kv_rmsnorm_rope_cache_v2", kv_v2, "CPU")
+        lib.impl("npu_kv_rmsnorm_rope_cache_v2_functional", kv_v2f, "CPU")
+        lib.impl("npu_kv_rmsnorm_rope_cache", kv_legacy, "CPU")
+        LIBS["npu_inference"].impl("npu_kv_rmsnorm_rope_cache", kv_legacy, "CPU")
         lib.impl("npu_dynamic_quant", dq, "CPU")
         lib.impl("npu_quant_matmul", qmm, "CPU")
         lib.impl("npu_grouped_matmul", gmm, "CPU")

@@ -470,3 +470,158 @@ def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq
         out[b] = o
         lse[b] = l
     return out, lse
+
+
+# ----------------------------------------------------------------------------- RMS norm family
+def _rms(x: np.ndarray, eps: float) -> np.ndarray:
+    """rstd per row of fp32 x: 1 / sqrt(mean(x^2) + eps); the sum in float64, rounded once."""
+    ms = (np.sum(x.astype(np.float64) ** 2, axis=-1) / x.shape[-1]).astype(F32)
+    return (F32(1.0) / np.sqrt((ms + F32(eps)).astype(F32))).astype(F32)
+
+
+def add_rms_norm(x1, x2, gamma, epsilon: float = 1e-6, dtype: str = "bf16"):
+    """npu_add_rms_norm -> (y, rstd, x).
+
+    Follows python/torchair/_ge_concrete_graph/ge_converter/custom/npu_add_rms_norm.py:4-13 and
+    the prototype third_party/ascend/include/ops/op_proto/inc/nn_norm.h:50-58 (y and x in the
+    input dtype, rstd fp32). x = x1 + x2 in fp32; the norm uses the unrounded fp32 x;
+    y = (x * rstd) * gamma rounded to dtype; rstd has shape x.shape[:-1] + [1].
+    """
+    x = (np.asarray(x1, F32) + np.asarray(x2, F32)).astype(F32)
+    g = np.asarray(gamma, F32)
+    rstd = _rms(x, epsilon)
+    y = round_to(((x * rstd[..., None]).astype(F32) * g).astype(F32), dtype)
+    return y, rstd[..., None], round_to(x, dtype)
+
+
+def add_rms_norm_dynamic_quant(x1, x2, gamma, smooth_scale1=None, smooth_scale2=None, beta=None,
+                               epsilon: float = 1e-6, second: bool = False, dtype: str = "bf16"):
+    """npu_add_rms_norm_dynamic_quant -> (y1, y2, x, scale1, scale2); y2 / scale2 are None unless
+    `second`.
+
+    Follows .../custom/npu_add_rms_norm_dynamic_quant.py:8-21 and the fusion pattern
+    python/torchair/patterns/add_rms_norm_dynamic_quant.py:67-80, which replaces
+    npu_add_rms_norm + npu_dynamic_quant(y, smooth_scales) by this op: y (+ beta) is rounded
+    to the input dtype before it is quantised, so the fused op equals that composition.
+    """
+    x = (np.asarray(x1, F32) + np.asarray(x2, F32)).astype(F32)
+    rstd = _rms(x, epsilon)
+    y = ((x * rstd[..., None]).astype(F32) * np.asarray(gamma, F32)).astype(F32)
+    if beta is not None:
+        y = (y + np.asarray(beta, F32)).astype(F32)
+    y = round_to(y, dtype)
+    y1, s1 = dynamic_quant(y, smooth_scale1)
+    y2 = s2 = None
+    if second:
+        y2, s2 = dynamic_quant(y, smooth_scale2)
+    return y1, y2, round_to(x, dtype), s1, s2
+
+
+# ----------------------------------------------------------------------------- KV-cache writers
+def nz_index(slot: int, block_size: int, row_bytes: int):
+    """PA_NZ cache position of a slot's row: (block, offset); 32-byte piece p of the row sits at
+    cache[block, p, offset] of the [num_blocks, row_bytes / 32, block_size, 32 B] layout."""
+    return slot // block_size, slot % block_size
+
+
+def scatter_pa_kv_cache(key, value, key_cache, value_cache, slot_mapping, cache_mode: str = "Norm"):
+    """npu_scatter_pa_kv_cache: returns updated copies of (key_cache, value_cache).
+
+    Follows .../custom/npu_scatter_pa_kv_cache.py:44-74 (ge.ScatterPaKvCache, prototype
+    experiment_ops.h:3963-4002). Token t's row (all heads) goes to slot slot_mapping[t]; negative
+    slots are skipped. 'Norm': cache [blocks, block_size, ...] with the slot's row contiguous;
+    'PA_NZ': cache [blocks, row / last, block_size, last] (last = 32 bytes of elements), the
+    layout of the reference's smoke test tests/smoke/ge_test.py:253-287.
+    """
+    out = []
+    for src, cache in ((key, key_cache), (value, value_cache)):
+        c = np.array(cache, copy=True)
+        s = np.asarray(src)
+        t = s.shape[0]
+        rows = s.reshape(t, -1)
+        if cache_mode == "Norm":
+            flat = c.reshape(-1, rows.shape[1])
+            for i in range(t):
+                slot = int(slot_mapping[i])
+                if slot >= 0:
+                    flat[slot] = rows[i]
+        else:
+            nb, pieces, bs, last = c.shape
+            for i in range(t):
+                slot = int(slot_mapping[i])
+                if slot >= 0:
+                    blk, off = nz_index(slot, bs, 0)
+                    c[blk, :, off, :] = rows[i].reshape(pieces, last)
+        out.append(c)
+    return out[0], out[1]
+
+
+def interleave_rope(x, cos, sin):
+    """RoPE of interleaved pairs: xd = (x[..., 0::2], x[..., 1::2]) concatenated, then
+    xd * cos + rotate_half(xd) * sin with rotate_half(u) = (-u[h:], u[:h]) (fp32)."""
+    x = np.asarray(x, F32)
+    xd = np.concatenate([x[..., 0::2], x[..., 1::2]], axis=-1)
+    h = xd.shape[-1] // 2
+    rh = np.concatenate([-xd[..., h:], xd[..., :h]], axis=-1)
+    return ((xd * np.asarray(cos, F32)).astype(F32) + (rh * np.asarray(sin, F32)).astype(F32)).astype(F32)
+
+
+def kv_rmsnorm_rope_cache(kv, gamma, cos, sin, index, k_cache, ckv_cache, epsilon: float = 1e-5,
+                          cache_mode: str = "PA", k_rope_scale=None, k_rope_offset=None, c_kv_scale=None,
+                          c_kv_offset=None, c_kv_token_scale=None, dtype: str = "bf16"):
+    """npu_kv_rmsnorm_rope_cache (MLA cache update) -> (k_cache, ckv_cache, k_rope, c_kv[, token scales]).
+
+    Follows .../custom/npu_kv_rmsnorm_rope_cache.py:4-66 (ge.KvRmsNormRopeCache, prototype
+    experiment_ops.h:3677-3697) and the meta rule
+    python/torchair/_contrib/custom_torch_ops/auto_register_custom_torch_ops.py:82-110:
+    kv [B, 1, S, dc + dr] splits into the latent (RMS norm with gamma, eps) and the rope key
+    (interleaved RoPE with cos / sin [B, 1, S, dr]); both are rounded to the kv dtype and written
+    at the token's cache row: PA layouts (cache [blocks, block_size, 1, d]) take index as the
+    slot; 'Norm' (cache [B, 1, S_cache, d]) as the position in the token's batch. Negative
+    index skips the write. int8 caches: static per-channel round(v * scale + offset) clamped to
+    [-128, 127]; for the latent, c_kv_token_scale ([blocks, block_size] fp32) selects per-token
+    dynamic quantisation (npu_dynamic_quant arithmetic), its scale stored at the row.
+    """
+    kv = np.asarray(kv, F32)
+    b, n, s, w = kv.shape
+    dr = np.asarray(cos).shape[-1]
+    dc = w - dr
+    flat = kv.reshape(b * s, w)
+    lat = flat[:, :dc]
+    rstd = _rms(lat, epsilon)
+    c_kv = round_to(((lat * rstd[:, None]).astype(F32) * np.asarray(gamma, F32)).astype(F32), dtype)
+    k_rope = round_to(interleave_rope(flat[:, dc:], np.asarray(cos, F32).reshape(b * s, dr),
+                                      np.asarray(sin, F32).reshape(b * s, dr)), dtype)
+    kc = np.array(k_cache, copy=True)
+    cc = np.array(ckv_cache, copy=True)
+    ts = None if c_kv_token_scale is None else np.array(c_kv_token_scale, F32, copy=True).reshape(-1)
+    kflat = kc.reshape(-1, dr)
+    cflat = cc.reshape(-1, dc)
+    idx = np.asarray(index, np.int64).reshape(-1)
+    norm_rows = kc.shape[2] if cache_mode == "Norm" else 0
+
+    def q_static(v, scale, offset):
+        o = np.zeros_like(v) if offset is None else np.asarray(offset, F32)
+        return np.clip(np.rint((v * np.asarray(scale, F32)).astype(F32) + o), -128, 127).astype(np.int8)
+
+    for t in range(b * s):
+        if idx[t] < 0:
+            continue
+        row = (t // s) * norm_rows + idx[t] if norm_rows else idx[t]
+        if kflat.dtype == np.int8:
+            kflat[row] = q_static(k_rope[t], k_rope_scale, k_rope_offset)
+        else:
+            kflat[row] = k_rope[t]
+        if cflat.dtype == np.int8:
+            if ts is not None:
+                q, sc = _quant_rows(c_kv[t][None, :])
+                cflat[row] = q[0]
+                ts[row] = sc[0]
+            else:
+                cflat[row] = q_static(c_kv[t], c_kv_scale, c_kv_offset)
+        else:
+            cflat[row] = c_kv[t]
+    out = (kc, cc, k_rope.reshape(b, n, s, dr), c_kv.reshape(b, n, s, dc))
+    if ts is not None:
+        out = out + (ts.reshape(np.asarray(c_kv_token_scale).shape),)
+    return out

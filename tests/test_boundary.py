@@ -164,3 +164,41 @@ def test_compiler_config_validation():
         cfg.debug.aclgraph.static_capture_size_limit = 0
     assert CompilerConfig() != cfg and CompilerConfig() == CompilerConfig()
     assert torchair_amd.get_compiler(cfg).config is cfg
+
+
+def test_pattern_pass_fuses_add_rms_norm_dynamic_quant_on_cpu():
+    """add_rms_norm + dynamic_quant becomes the fused op (python/torchair/patterns/add_rms_norm_dynamic_quant.py)
+    and the compiled result equals the eager composition, bit for bit."""
+    from oracle import cpu_ops
+    from torchair_amd.patterns import fuse_add_rms_norm_dynamic_quant
+    cpu_ops.register()
+    g = torch.Generator().manual_seed(3)
+    x1, x2 = torch.randn(8, 64, generator=g).to(torch.bfloat16), torch.randn(8, 64, generator=g).to(torch.bfloat16)
+    gamma = (torch.rand(64, generator=g) + 0.5).to(torch.bfloat16)
+    sm = torch.rand(64, generator=g) + 0.5
+
+    def block(x1, x2):
+        y, _, x = torch.ops.npu.npu_add_rms_norm(x1, x2, gamma, 1e-5)
+        q, s = torch.ops.npu.npu_dynamic_quant(y, smooth_scales=sm)
+        return q, s, x
+
+    gm = torch.fx.symbolic_trace(block)
+    assert fuse_add_rms_norm_dynamic_quant(gm) == 1
+    targets = {n.target for n in gm.graph.nodes if n.op == "call_function"}
+    assert torch.ops.npu.npu_add_rms_norm_dynamic_quant.default in targets
+    assert torch.ops.npu.npu_dynamic_quant.default not in targets
+    for a, b in zip(gm(x1, x2), block(x1, x2)):
+        assert torch.equal(a, b)
+    fn = torch.compile(block, backend=get_npu_backend(), fullgraph=True)
+    for a, b in zip(fn(x1, x2), block(x1, x2)):
+        assert torch.equal(a, b)
+    # rstd in use: no fusion of that call; a second call that only feeds a quant is fused
+    def two(a, b):
+        rstd = torch.ops.npu.npu_add_rms_norm(a, b, gamma)[1]
+        q, s = torch.ops.npu.npu_dynamic_quant(torch.ops.npu.npu_add_rms_norm(a, b, gamma)[0])
+        return rstd, q, s
+
+    gm2 = torch.fx.symbolic_trace(two)
+    assert fuse_add_rms_norm_dynamic_quant(gm2) == 1
+    for a, b in zip(gm2(x1, x2), two(x1, x2)):
+        assert torch.equal(a, b)

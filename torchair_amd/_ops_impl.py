@@ -585,3 +585,5 @@ _define("air", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
     seq="Tensor?", bt_first="", bt_second=_BT,
     tail="int key_antiquant_mode=0, int value_antiquant_mode=0, bool softmax_lse_flag=False"),
     _fia.fia_fake, _fia.fia_cuda)
+
+from . import _norm_cache  # noqa: E402,F401  (RMS-norm family and KV-cache writers)

@@ -102,6 +102,8 @@ class _AclGraphConfig(NpuBaseConfig):
 class _ExperimentalConfig(NpuBaseConfig):
     def __init__(self):
         self.frozen_parameter = OptionValue(False, [True, False])
+        # FX fusion passes before lowering (python/torchair/configs/experimental_config.py:29)
+        self.pattern_fusion_pass = OptionValue(True, [True, False])
 
 
 class _Opaque(NpuBaseConfig):

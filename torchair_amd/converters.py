@@ -55,3 +55,16 @@ register_fx_node_ge_converter(npu.npu_fused_infer_attention_score.default)(
     _identity(npu.npu_fused_infer_attention_score.default))
 register_fx_node_ge_converter(air.npu_fused_infer_attention_score.default)(
     _identity(air.npu_fused_infer_attention_score.default))
+# .../custom/npu_add_rms_norm.py:4-13, npu_add_rms_norm_dynamic_quant.py:8-21
+register_fx_node_ge_converter(npu.npu_add_rms_norm.default)(_identity(npu.npu_add_rms_norm.default))
+register_fx_node_ge_converter(npu.npu_add_rms_norm_dynamic_quant.default)(
+    _identity(npu.npu_add_rms_norm_dynamic_quant.default))
+# .../custom/npu_scatter_pa_kv_cache.py:44-74
+register_fx_node_ge_converter(npu.npu_scatter_pa_kv_cache_functional.default)(
+    _identity(npu.npu_scatter_pa_kv_cache_functional.default))
+# .../custom/npu_kv_rmsnorm_rope_cache.py:4-66 and python/torchair/_contrib/custom_torch_ops/npu_kv_rmsnorm_rope_cache.py:17
+register_fx_node_ge_converter(npu.npu_kv_rmsnorm_rope_cache.default)(_identity(npu.npu_kv_rmsnorm_rope_cache.default))
+register_fx_node_ge_converter(npu.npu_kv_rmsnorm_rope_cache_v2_functional.default)(
+    _identity(npu.npu_kv_rmsnorm_rope_cache_v2_functional.default))
+register_fx_node_ge_converter(npu_inference.npu_kv_rmsnorm_rope_cache.default)(
+    _identity(npu_inference.npu_kv_rmsnorm_rope_cache.default))

@@ -21,6 +21,7 @@ from . import converters as _converters  # noqa: F401  (registers the hot-path c
 from .configs import CompilerConfig, check_config_support
 from .converter import _get_converter
 from .graph import HipGraphRunner
+from .patterns import apply_pattern_passes
 
 logger = logging.getLogger("torchair_amd")
 
@@ -52,6 +53,9 @@ class _NpuFxCompiler:
         self.config = compiler_config
 
     def __call__(self, gm: torch.fx.GraphModule, example_inputs: List[Any]):
+        # pattern passes run on the aten/npu graph, as in python/torchair/npu_fx_compiler.py:337-338
+        if self.config.experimental_config.pattern_fusion_pass.value:
+            apply_pattern_passes(gm)
         lowered = lower_graph(gm)
         if self.config.debug.run_eagerly.value:
             return lowered

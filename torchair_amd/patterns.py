@@ -1,0 +1,94 @@
+"""FX fusion passes applied before lowering (CompilerConfig.experimental_config.pattern_fusion_pass).
+
+add_rms_norm + dynamic_quant -> add_rms_norm_dynamic_quant, the rewrite of
+python/torchair/patterns/add_rms_norm_dynamic_quant.py:67-80 (and its epsilon / no-x-out
+variants): npu_add_rms_norm(x1, x2, gamma[, eps]) whose normalised output feeds only
+npu_dynamic_quant(y, smooth_scales=s) becomes npu_add_rms_norm_dynamic_quant(x1, x2, gamma,
+smooth_scale1=s, epsilon=eps, output_mask=[True, False]); the fused kernel quantises y rounded to
+the input dtype, so the rewrite changes no value. A match whose rstd output is used, or whose
+quant has other arguments than smooth_scales, is left alone.
+"""
+from __future__ import annotations
+
+import logging
+import operator
+
+import torch
+import torch.fx
+
+logger = logging.getLogger("torchair_amd")
+
+
+def _getitems(node: torch.fx.Node):
+    """index -> list of getitem users of a multi-output node; None if another kind of use exists."""
+    out = {}
+    for u in node.users:
+        if u.op != "call_function" or u.target is not operator.getitem:
+            return None
+        out.setdefault(u.args[1], []).append(u)
+    return out
+
+
+def _calls(node: torch.fx.Node, packet) -> bool:
+    """True for a call of the op (its packet, as symbolic tracing records it, or its default overload)."""
+    return node.op == "call_function" and node.target in (packet, packet.default)
+
+
+def fuse_add_rms_norm_dynamic_quant(gm: torch.fx.GraphModule) -> int:
+    npu = torch.ops.npu
+    if not hasattr(npu, "npu_add_rms_norm_dynamic_quant"):
+        return 0
+    fused = 0
+    for norm in list(gm.graph.nodes):
+        if not _calls(norm, npu.npu_add_rms_norm):
+            continue
+        outs = _getitems(norm)
+        if outs is None:
+            continue
+        dead = [u for us in outs.values() for u in us if not u.users]
+        outs = {i: [u for u in us if u.users] for i, us in outs.items()}
+        if outs.get(1) or len(outs.get(0, [])) != 1:
+            continue
+        y = outs[0][0]
+        if len(y.users) != 1:
+            continue
+        quant = next(iter(y.users))
+        if not _calls(quant, npu.npu_dynamic_quant):
+            continue
+        if quant.args[0] is not y or len(quant.args) != 1 or set(quant.kwargs) - {"smooth_scales"}:
+            continue
+        qouts = _getitems(quant)
+        if qouts is None:
+            continue
+        for us in qouts.values():
+            for u in [u for u in us if not u.users]:
+                us.remove(u)
+                gm.graph.erase_node(u)
+        x1, x2, gamma = norm.args[:3]
+        eps = norm.args[3] if len(norm.args) > 3 else norm.kwargs.get("epsilon", 1e-6)
+        with gm.graph.inserting_after(quant):
+            node = gm.graph.call_function(
+                npu.npu_add_rms_norm_dynamic_quant.default, (x1, x2, gamma),
+                {"smooth_scale1": quant.kwargs.get("smooth_scales"), "epsilon": eps, "output_mask": [True, False]})
+        for src_idx, users, dst_idx in ((0, qouts.get(0, []), 0), (1, qouts.get(1, []), 3), (2, outs.get(2, []), 2)):
+            for u in users:
+                with gm.graph.inserting_after(node):
+                    new = gm.graph.call_function(operator.getitem, (node, dst_idx))
+                u.replace_all_uses_with(new)
+                gm.graph.erase_node(u)
+        gm.graph.erase_node(quant)
+        gm.graph.erase_node(y)
+        for u in dead:
+            gm.graph.erase_node(u)
+        gm.graph.erase_node(norm)
+        fused += 1
+    if fused:
+        gm.graph.lint()
+        gm.recompile()
+        logger.debug("fused %d add_rms_norm + dynamic_quant pair(s)", fused)
+    return fused
+
+
+def apply_pattern_passes(gm: torch.fx.GraphModule) -> torch.fx.GraphModule:
+    fuse_add_rms_norm_dynamic_quant(gm)
+    return gm
