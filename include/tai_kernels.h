@@ -126,6 +126,52 @@ int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t m, int64_t
                        void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * npu_grouped_matmul_swiglu_quant_v2 (dequant_mode 0, quant_mode 0, int8 out): the grouped
+ * W8A8 GEMM of the MoE gate_up projection fused with dequant_swiglu_quant. For expert e's rows:
+ * d = (float(x @ weight[e]) * weight_scale[e, col]) * x_scale[row]; h = silu(d[:, :n/2]) *
+ * d[:, n/2:]; y = per-row symmetric int8 of h, y_scale = max|h| / 127.
+ * Replaces ge.GroupedMatmulSwigluQuantV2 emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/grouped_matmul_swiglu_quant_v2.py:86-166
+ *   (prototype fusion_ops.h:769-789).
+ * x: [m, k] int8; weight: [num_groups, k, n] (_KN) or [num_groups, n, k] (_NK) int8;
+ * weight_scale: [num_groups, n] fp32; x_scale: [m] fp32; y: [m, n/2] int8; y_scale: [m] fp32.
+ * Needs k % 64 == 0 and (n / 2) % 256 (_KN) or % 128 (_NK) == 0; TAI_ERR_UNSUPPORTED otherwise.
+ * ------------------------------------------------------------------------------------- */
+size_t tai_grouped_matmul_swiglu_quant_workspace_size(int64_t m, int64_t n, int64_t num_groups);
+int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, int64_t m, int64_t k,
+                                    int64_t n, int64_t num_groups, int w_layout,
+                                    const int64_t* group_list, int group_list_type,
+                                    const float* weight_scale, const float* x_scale, int8_t* y,
+                                    float* y_scale, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_grouped_matmul_finalize_routing (int8 x / w, fp32 out): the grouped W8A8 GEMM of the MoE
+ * down projection fused with the weighted combine. Row r's dequantised product
+ * v = float(x[r] @ w[e]) * scale[e] * pertoken_scale[r] (+ bias[e]) is added, times logit[r],
+ * into y[row_index[r]]; rows of a token are summed in ascending r; shared_input rows (times
+ * shared_input_weight) are added at rows [shared_input_offset, + shared_rows).
+ * Replaces ge.GroupedMatmulFinalizeRouting emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/grouped_matmul_finalize_routing.py:32-133
+ *   (prototype fusion_ops.h:640-725).
+ * scale: [num_groups, n] fp32; pertoken_scale, logit: NULL or [m] fp32; bias: NULL or
+ * [num_groups, n] fp32; row_index: NULL (row r -> token r) or [m] INT32/INT64;
+ * shared_input: NULL or [shared_rows, n] bf16; y: [output_bs, n] fp32 (every row written).
+ * A token may gather at most 1024 rows (beyond that its row is NaN).
+ * ------------------------------------------------------------------------------------- */
+size_t tai_grouped_matmul_finalize_routing_workspace_size(int64_t m, int64_t n, int64_t num_groups,
+                                                         int64_t output_bs);
+int tai_grouped_matmul_finalize_routing(const int8_t* x, const int8_t* weight, int64_t m,
+                                        int64_t k, int64_t n, int64_t num_groups, int w_layout,
+                                        const int64_t* group_list, int group_list_type,
+                                        const float* scale, const float* pertoken_scale,
+                                        const float* bias, const float* logit,
+                                        const void* row_index, int row_index_dtype,
+                                        const void* shared_input, int64_t shared_rows,
+                                        float shared_input_weight, int64_t shared_input_offset,
+                                        int64_t output_bs, float* y, void* workspace,
+                                        size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * npu_moe_gating_top_k: grouped top-k expert selection (DeepSeek-V3 "noaux_tc").
  * Replaces ge.MoeGatingTopK emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_moe_gating_top_k.py:4-22

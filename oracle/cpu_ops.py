@@ -170,8 +170,28 @@ def register() -> None:
                                  k_rope_offset, c_kv_offset, epsilon, cache_mode)
         return kc, cc, kr, ckv
 
+    def gsq(x, weight, weight_scale, x_scale, group_list, *, smooth_scale=None, weight_assist_matrix=None,
+            bias=None, dequant_mode=0, dequant_dtype=0, quant_mode=0, quant_dtype=1, group_list_type=0,
+            tuning_config=None, x_dtype=None, weight_dtype=None, weight_scale_dtype=None, x_scale_dtype=None):
+        y, s = G.grouped_matmul_swiglu_quant(x.numpy(), weight[0].numpy(), _np(weight_scale[0]), _np(x_scale),
+                                             group_list.numpy(), group_list_type)
+        return _t(y), _t(s)
+
+    def gfr(x, w, group_list, *, scale=None, bias=None, offset=None, pertoken_scale=None, shared_input=None,
+            logit=None, row_index=None, dtype=None, shared_input_weight=1.0, shared_input_offset=0, output_bs=0,
+            group_list_type=1, tuning_config=()):
+        y = G.grouped_matmul_finalize_routing(x.numpy(), w.numpy(), group_list.numpy(),
+                                              1 if group_list_type is None else group_list_type, _np(scale),
+                                              _np(pertoken_scale), _np(bias), _np(logit),
+                                              None if row_index is None else row_index.numpy(), _np(shared_input),
+                                              1.0 if shared_input_weight is None else shared_input_weight,
+                                              shared_input_offset or 0, output_bs or 0)
+        return _t(y)
+
     for ns in ("npu",):
         lib = LIBS[ns]
+        lib.impl("npu_grouped_matmul_swiglu_quant_v2", gsq, "CPU")
+        lib.impl("npu_grouped_matmul_finalize_routing", gfr, "CPU")
         lib.impl("npu_add_rms_norm", arn, "CPU")
         lib.impl("npu_add_rms_norm_dynamic_quant", arnq, "CPU")
         lib.impl("npu_scatter_pa_kv_cache", scatter_inplace, "CPU")

@@ -625,3 +625,51 @@ def kv_rmsnorm_rope_cache(kv, gamma, cos, sin, index, k_cache, ckv_cache, epsilo
     if ts is not None:
         out = out + (ts.reshape(np.asarray(c_kv_token_scale).shape),)
     return out
+
+
+# ----------------------------------------------------------------------------- fused MoE grouped GEMMs
+def grouped_matmul_swiglu_quant(x, w, weight_scale, x_scale, group_list, group_list_type: int = 0):
+    """npu_grouped_matmul_swiglu_quant_v2 (dequant_mode 0, per-token int8) -> (y int8 [m, n/2], scale [m]).
+
+    Follows .../custom/grouped_matmul_swiglu_quant_v2.py:86-166 (ge.GroupedMatmulSwigluQuantV2,
+    prototype fusion_ops.h:769-789): the int32 grouped product of npu_grouped_matmul, then
+    npu_dequant_swiglu_quant's arithmetic with activate_left (silu of the first half times the second
+    half), per-group weight scales and the per-token x_scale; rows past the grouped total give 0.
+    """
+    x = np.asarray(x)
+    m = x.shape[0]
+    acc = grouped_matmul(x, w, group_list, group_list_type, out_dtype="int32")
+    b, en = group_offsets(group_list, group_list_type, m)
+    counts = (en - b).astype(np.int64)
+    return dequant_swiglu_quant(acc, np.asarray(weight_scale, F32), np.asarray(x_scale, F32), None, None, counts,
+                                activate_left=True)
+
+
+def grouped_matmul_finalize_routing(x, w, group_list, group_list_type: int = 1, scale=None, pertoken_scale=None,
+                                    bias=None, logit=None, row_index=None, shared_input=None,
+                                    shared_input_weight: float = 1.0, shared_input_offset: int = 0,
+                                    output_bs: int = 0) -> np.ndarray:
+    """npu_grouped_matmul_finalize_routing -> y fp32 [output_bs, n].
+
+    Follows .../custom/grouped_matmul_finalize_routing.py:32-133 (ge.GroupedMatmulFinalizeRouting,
+    prototype fusion_ops.h:640-725): v[r] = the fp32 dequantised grouped product of row r;
+    y[row_index[r]] += logit[r] * v[r], summed over a token's rows in ascending r; shared_input
+    rows times shared_input_weight are added at rows [shared_input_offset, + rows).
+    """
+    x = np.asarray(x)
+    m = x.shape[0]
+    v = grouped_matmul(x, w, group_list, group_list_type, scale, pertoken_scale, bias, out_dtype="fp32")
+    n = v.shape[1]
+    bs = output_bs or m
+    y = np.zeros((bs, n), F32)
+    ri = np.arange(m) if row_index is None else np.asarray(row_index, np.int64)
+    lg = np.ones(m, F32) if logit is None else np.asarray(logit, F32)
+    for r in range(m):
+        t = int(ri[r])
+        if 0 <= t < bs:
+            y[t] = (y[t] + (lg[r] * v[r]).astype(F32)).astype(F32)
+    if shared_input is not None:
+        s = np.asarray(shared_input, F32)
+        y[shared_input_offset:shared_input_offset + s.shape[0]] = (
+            y[shared_input_offset:shared_input_offset + s.shape[0]] + (F32(shared_input_weight) * s).astype(F32))
+    return y

@@ -1,0 +1,116 @@
+"""GPU parity: npu_grouped_matmul_swiglu_quant_v2 and npu_grouped_matmul_finalize_routing against the
+CPU oracle and against the unfused GPU compositions they replace."""
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_close, assert_int8_close, f32np, gen, rand_i8, uniform
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+npu = torch.ops.npu
+
+
+def _case(g, counts, k, n, m=None):
+    e = len(counts)
+    m = int(sum(counts)) if m is None else m
+    x = rand_i8((m, k), g)
+    w = rand_i8((e, k, n), g)
+    ws = uniform((e, n), g, 1e-3, 1e-2)
+    xs = uniform((m,), g, 1e-3, 1e-2)
+    return x, w, ws, xs, torch.tensor(counts, dtype=torch.int64)
+
+
+@pytest.mark.parametrize("layout", ["KN", "NK"])
+@pytest.mark.parametrize("counts,k,n,extra", [([5, 0, 300, 17], 256, 512, 3), ([1, 1], 64, 1024, 0),
+                                              ([128] * 6, 512, 1536, 0)])
+def test_swiglu_quant_v2_vs_oracle(layout, counts, k, n, extra):
+    g = gen(11)
+    x, w, ws, xs, cnt = _case(g, counts, k, n, int(sum(counts)) + extra)
+    wd = w.to(DEV) if layout == "KN" else w.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    if layout == "NK" and (n // 2) % 128:
+        pytest.skip("the [N, K] tiles cover 128 output columns")
+    y, s = npu.npu_grouped_matmul_swiglu_quant_v2(x.to(DEV), [wd], [ws.to(DEV)], xs.to(DEV), cnt.to(DEV),
+                                                  group_list_type=1)
+    wy, wsc = G.grouped_matmul_swiglu_quant(x.numpy(), w.numpy(), ws.numpy(), xs.numpy(), cnt.numpy(), 1)
+    assert y.shape == (x.shape[0], n // 2) and s.shape == (x.shape[0],)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)
+
+
+def test_swiglu_quant_v2_equals_unfused_gpu_path_cfg4_slice():
+    # 16 experts of the config-4 gate_up shape: fused == grouped_matmul(int32) + dequant_swiglu_quant, bit for bit
+    g = gen(12)
+    counts = torch.randint(0, 300, (16,), generator=g).tolist()
+    x, w, ws, xs, cnt = _case(g, counts, 7168, 4096)
+    xd, wd, wsd, xsd, cd = x.to(DEV), w.to(DEV), ws.to(DEV), xs.to(DEV), cnt.to(DEV)
+    y, s = npu.npu_grouped_matmul_swiglu_quant_v2(xd, [wd], [wsd], xsd, cd, group_list_type=1)
+    acc = npu.npu_grouped_matmul([xd], [wd], group_list=cd, split_item=3, group_type=0, group_list_type=1,
+                                 output_dtype=torch.int32)[0]
+    y2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=wsd, activation_scale=xsd, group_index=cd,
+                                          activate_left=True, quant_mode=1)
+    assert torch.equal(y, y2) and torch.equal(s, s2)
+
+
+@pytest.mark.parametrize("layout", ["KN", "NK"])
+def test_finalize_routing_vs_oracle(layout):
+    g = gen(13)
+    t, kk, e, k, n = 96, 4, 6, 256, 384
+    idx = torch.stack([torch.randperm(e, generator=g)[:kk] for _ in range(t)]).to(torch.int32)
+    order = torch.argsort(idx.reshape(-1).to(torch.int64), stable=True)
+    row_index = (order // kk).to(torch.int64)  # expanded row -> token
+    counts = torch.bincount(idx.reshape(-1).to(torch.int64), minlength=e)
+    x, w, sc, pts, _ = _case(g, counts.tolist(), k, n)
+    logit = uniform((t * kk,), g, 0.0, 1.0)
+    shared = torch.randn(10, n, generator=g).to(torch.bfloat16)
+    wd = w.to(DEV) if layout == "KN" else w.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    y = npu.npu_grouped_matmul_finalize_routing(x.to(DEV), wd, counts.to(DEV), scale=sc.to(DEV),
+                                                pertoken_scale=pts.to(DEV), shared_input=shared.to(DEV),
+                                                logit=logit.to(DEV), row_index=row_index.to(DEV),
+                                                shared_input_weight=0.5, shared_input_offset=7, output_bs=t,
+                                                group_list_type=1)
+    want = G.grouped_matmul_finalize_routing(x.numpy(), w.numpy(), counts.numpy(), 1, sc.numpy(), pts.numpy(), None,
+                                             logit.numpy(), row_index.numpy(), f32np(shared), 0.5, 7, t)
+    assert y.dtype == torch.float32 and y.shape == (t, n)
+    assert_close(y.cpu().numpy(), want)
+    # deterministic: a second call gives identical bits
+    y2 = npu.npu_grouped_matmul_finalize_routing(x.to(DEV), wd, counts.to(DEV), scale=sc.to(DEV),
+                                                 pertoken_scale=pts.to(DEV), shared_input=shared.to(DEV),
+                                                 logit=logit.to(DEV), row_index=row_index.to(DEV),
+                                                 shared_input_weight=0.5, shared_input_offset=7, output_bs=t,
+                                                 group_list_type=1)
+    assert torch.equal(y, y2)
+
+
+def test_finalize_routing_on_the_moe_routing_path():
+    # routing from the GPU gating / init_routing ops; the fused op against the fp32 oracle, and the
+    # unfused grouped_matmul(bf16) + moe_finalize_routing tail as a wiring check at bf16 precision
+    g = gen(14)
+    t, kk, e, k, n = 256, 8, 32, 512, 1024
+    logits = torch.randn(t, e, generator=g)
+    y_w, idx, _ = npu.npu_moe_gating_top_k(logits.to(DEV), kk, k_group=1, group_count=1, norm_type=1)
+    xs = torch.randn(t, k, generator=g).to(torch.bfloat16).to(DEV)
+    ex, ri, counts, _ = npu.npu_moe_init_routing_v2(xs, idx, active_num=t * kk, expert_num=e,
+                                                    expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                    row_idx_type=0)
+    q, s = npu.npu_dynamic_quant(ex)
+    w = rand_i8((e, k, n), g).to(DEV)
+    sc = uniform((e, n), g, 1e-3, 1e-2).to(DEV)
+    # expanded row i holds routing slot p with ri[p] = i: token p // k, weight y_w[p]
+    inv = torch.empty_like(ri)
+    inv[ri.to(torch.int64)] = torch.arange(ri.numel(), device=DEV, dtype=ri.dtype)
+    slot = inv.to(torch.int64)
+    logit = y_w.reshape(-1)[slot].float()
+    fused = npu.npu_grouped_matmul_finalize_routing(q, w, counts, scale=sc, pertoken_scale=s, logit=logit,
+                                                    row_index=slot // kk, output_bs=t, group_list_type=1)
+    want = G.grouped_matmul_finalize_routing(q.cpu().numpy(), w.cpu().numpy(), counts.cpu().numpy(), 1,
+                                             sc.cpu().numpy(), s.cpu().numpy(), None, logit.cpu().numpy(),
+                                             (slot // kk).cpu().numpy(), None, 1.0, 0, t)
+    assert_close(fused.cpu().numpy(), want)
+    out = npu.npu_grouped_matmul([q], [w], scale=[sc], per_token_scale=[s], group_list=counts, split_item=3,
+                                 group_type=0, group_list_type=1, output_dtype=torch.bfloat16)[0]
+    ref = npu.npu_moe_finalize_routing(out, None, None, None, y_w, ri, idx, drop_pad_mode=2)
+    # bf16 rounding of the 8 rows and of the output: errors scale with the terms, not their sum
+    np.testing.assert_allclose(ref.float().cpu().numpy(), want, rtol=3e-2, atol=0.15)

@@ -161,3 +161,54 @@ def test_kv_rmsnorm_rope_cache_int8_latent_modes():
                                               c_kv_offset=off)
     want = np.clip(np.rint(ckv2.reshape(b * s, dc) * 20.0 + 1.0), -128, 127)
     np.testing.assert_array_equal(co2.reshape(-1, dc)[idx], want)
+
+
+# ----------------------------------------------------------------------------- fused MoE grouped GEMMs
+def _silu64(a):
+    return a / (1.0 + np.exp(-a))
+
+
+def test_grouped_matmul_swiglu_quant_brute_force():
+    e, k, n = 3, 32, 8
+    counts = np.array([2, 0, 3])
+    m = 6  # one row past the grouped total
+    x = RNG.integers(-127, 128, (m, k)).astype(np.int8)
+    w = RNG.integers(-127, 128, (e, k, n)).astype(np.int8)
+    ws = RNG.uniform(1e-3, 1e-2, (e, n)).astype(np.float32)
+    xs = RNG.uniform(1e-3, 1e-2, m).astype(np.float32)
+    y, s = G.grouped_matmul_swiglu_quant(x, w, ws, xs, counts, 1)
+    ends = np.cumsum(counts)
+    for r in range(m):
+        g = int(np.searchsorted(ends, r, side="right"))
+        if g >= e:
+            assert s[r] == 0 and (y[r] == 0).all()
+            continue
+        d = (x[r].astype(np.int64) @ w[g].astype(np.int64)) * ws[g].astype(np.float64) * float(xs[r])
+        h = _silu64(d[: n // 2]) * d[n // 2:]
+        sc = np.abs(h).max() / 127
+        assert abs(s[r] - sc) <= 1e-5 * sc
+        assert np.abs(y[r].astype(int) - np.clip(np.rint(h / sc), -128, 127)).max() <= 1
+    # cumulative group_list gives the same result
+    y2, s2 = G.grouped_matmul_swiglu_quant(x, w, ws, xs, ends, 0)
+    assert (y2 == y).all() and (s2 == s).all()
+
+
+def test_grouped_matmul_finalize_routing_brute_force():
+    e, k, n, t = 3, 16, 8, 4
+    counts = np.array([3, 2, 3])
+    m = int(counts.sum())
+    x = RNG.integers(-127, 128, (m, k)).astype(np.int8)
+    w = RNG.integers(-127, 128, (e, k, n)).astype(np.int8)
+    sc = RNG.uniform(1e-3, 1e-2, (e, n)).astype(np.float32)
+    pts = RNG.uniform(1e-3, 1e-2, m).astype(np.float32)
+    logit = RNG.uniform(0, 1, m).astype(np.float32)
+    row_index = np.array([2, 0, 3, 1, 0, 2, 3, 1])
+    shared = RNG.standard_normal((2, n)).astype(np.float32)
+    y = G.grouped_matmul_finalize_routing(x, w, counts, 1, sc, pts, None, logit, row_index, shared, 0.5, 1, t)
+    want = np.zeros((t, n))
+    g = np.repeat(np.arange(e), counts)
+    for r in range(m):
+        v = (x[r].astype(np.int64) @ w[g[r]].astype(np.int64)) * sc[g[r]].astype(np.float64) * float(pts[r])
+        want[row_index[r]] += float(logit[r]) * v
+    want[1:3] += 0.5 * shared
+    np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5)

@@ -30,6 +30,13 @@ _SIGS = {
     "tai_grouped_matmul": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P,
                 _P, c_size_t, _P]),
+    "tai_grouped_matmul_swiglu_quant_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "tai_grouped_matmul_swiglu_quant": (
+        c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, _P, _P, c_size_t, _P]),
+    "tai_grouped_matmul_finalize_routing_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),
+    "tai_grouped_matmul_finalize_routing": (
+        c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, _P, c_int64,
+                c_float, c_int64, c_int64, _P, _P, c_size_t, _P]),
     "tai_moe_gating_top_k": (
         c_int, [_P, c_int, c_int64, c_int64, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                 c_float, c_float, _P, _P, _P, _P]),

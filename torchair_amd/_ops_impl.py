@@ -587,3 +587,5 @@ _define("air", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
     _fia.fia_fake, _fia.fia_cuda)
 
 from . import _norm_cache  # noqa: E402,F401  (RMS-norm family and KV-cache writers)
+
+from . import _gmm_fused  # noqa: E402,F401  (fused MoE grouped GEMMs)

@@ -68,3 +68,8 @@ register_fx_node_ge_converter(npu.npu_kv_rmsnorm_rope_cache_v2_functional.defaul
     _identity(npu.npu_kv_rmsnorm_rope_cache_v2_functional.default))
 register_fx_node_ge_converter(npu_inference.npu_kv_rmsnorm_rope_cache.default)(
     _identity(npu_inference.npu_kv_rmsnorm_rope_cache.default))
+# .../custom/grouped_matmul_swiglu_quant_v2.py:86-166, grouped_matmul_finalize_routing.py:32-133
+register_fx_node_ge_converter(npu.npu_grouped_matmul_swiglu_quant_v2.default)(
+    _identity(npu.npu_grouped_matmul_swiglu_quant_v2.default))
+register_fx_node_ge_converter(npu.npu_grouped_matmul_finalize_routing.default)(
+    _identity(npu.npu_grouped_matmul_finalize_routing.default))

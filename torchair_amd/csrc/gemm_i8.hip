@@ -49,7 +49,26 @@ struct GemmArgs {
   int64_t m_slots;
   int64_t n_tiles;
   const int64_t* live_slots;  // grouped: slots in use (real + zero-fill tiles), written by the prologue
+  float* h;          // SwiGLU epilogue: silu(gate) * up, fp32 [m, n / 2]
+  float* amax_part;  // SwiGLU epilogue: per-row max |h| of each column tile, [m, n_tiles]
 };
+
+// Output code of the fused SwiGLU epilogue (npu_grouped_matmul_swiglu_quant_v2).
+constexpr int kOutSwiglu = 100;
+
+// Weight column of tile column tc in a tile starting at n0. With the SwiGLU epilogue each
+// 128-column slab of the tile holds 64 gate columns and the 64 up columns (+ n / 2) that pair
+// with them, so every lane holds gate and up of the same output element in registers; the
+// tile's n0 / 2 is its first output column.
+template <bool SWI>
+__device__ __forceinline__ int64_t weight_col(const GemmArgs& g, int64_t n0, int tc) {
+  if constexpr (!SWI) {
+    return n0 + tc;
+  } else {
+    const int w = tc & 127;
+    return (w < 64 ? 0 : g.n / 2) + n0 / 2 + 64 * (tc >> 7) + (w & 63);
+  }
+}
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   const int64_t xcd = b % kXcds, idx = b / kXcds;
@@ -472,7 +491,7 @@ __device__ __forceinline__ void lgkm_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
 
-template <int LAYOUT, class C>
+template <int LAYOUT, class C, bool SWI = false>
 __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, int row0, int rows,
                                                 int64_t n0, int64_t k0, int8_t* stage, int w, int lane) {
   constexpr int BK = C::kBK, CPR = C::kCpr, RPI = 1024 / BK;  // rows per 1 KB instruction
@@ -493,16 +512,88 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
     if constexpr (LAYOUT == TAI_LAYOUT_NK) {
       const int row = RPI * q + lane / CPR;
       const int c = (lane % CPR) ^ ((row >> C::kRowShift) & (CPR - 1));
-      const int64_t nn = n0 + row < g.n ? n0 + row : g.n - 1;
+      const int64_t wc = weight_col<SWI>(g, n0, row);
+      const int64_t nn = wc < g.n ? wc : g.n - 1;
       src = bgrp + nn * g.k + k0 + 16 * c;
     } else {
       constexpr int CPN = C::kBN / 16;  // chunks per k row
       const int kr = (1024 / C::kBN) * q + lane / CPN;
       const int c = (lane % CPN) ^ ((kr & 7) << 1);
-      const int64_t nn = n0 + 16 * c < g.n ? n0 + 16 * c : g.n - 16;
+      const int64_t wc = weight_col<SWI>(g, n0, 16 * c);
+      const int64_t nn = wc < g.n ? wc : g.n - 16;
       src = bgrp + (k0 + kr) * g.n + nn;
     }
     __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(bst + q * 1024), 16, 0, 0);
+  }
+}
+
+// SwiGLU epilogue of npu_grouped_matmul_swiglu_quant_v2 (the arithmetic of npu_dequant_swiglu_quant
+// with activate_left): d = (float(acc) * weight_scale[col]) * x_scale[row]; h = silu(d_gate) * d_up
+// with silu(a) = a / (1 + exp(-a)). Writes h (fp32) and, per row, the max |h| over this tile's
+// output columns; a second kernel turns them into the per-row int8 quantisation.
+// Accumulator blocks j = 0, 1 hold gate columns and j = 2, 3 the matching up columns (weight_col).
+template <class C>
+__device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&acc)[2][4], int e, int row0, int rows,
+                                                int64_t n0, int64_t nt, int w, int lane, int8_t* smem) {
+#pragma clang fp contract(off)
+  constexpr int WN = C::kBN / 128;
+  const int wm = w / WN, wn = w % WN;
+  const int64_t n2 = g.n / 2;
+  const float* ws = g.scale + e * g.scale_group_stride;
+  float wg[2], wu[2];  // weight scales of this lane's gate / up columns
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t oc = n0 / 2 + 64 * wn + 32 * j + (lane & 31);
+    wg[j] = ws[oc];
+    wu[j] = ws[oc + n2];
+  }
+  float rmax[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const bool live = lr < rows;
+      const float xs = live ? g.pts[row0 + lr] : 0.0f;
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t oc = n0 / 2 + 64 * wn + 32 * j + (lane & 31);
+        const float dg = (static_cast<float>(acc[i][j][r]) * wg[j]) * xs;
+        const float du = (static_cast<float>(acc[i][j + 2][r]) * wu[j]) * xs;
+        const float hv = (dg / (1.0f + expf(-dg))) * du;
+        if (live) g.h[static_cast<int64_t>(row0 + lr) * n2 + oc] = hv;
+        m = fmaxf(m, fabsf(hv));
+      }
+      rmax[i][r] = m;
+    }
+  // max over the 32 lanes that share a row, then over the waves that share the row (LDS)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float m = rmax[i][r];
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      rmax[i][r] = m;
+    }
+  float* red = reinterpret_cast<float*>(smem);  // [WN][kBM]
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        red[wn * C::kBM + lr] = rmax[i][r];
+      }
+  }
+  __syncthreads();
+  for (int lr = threadIdx.x; lr < rows && lr < C::kBM; lr += C::kThreads) {
+    float m = red[lr];
+#pragma unroll
+    for (int q = 1; q < WN; ++q) m = fmaxf(m, red[q * C::kBM + lr]);
+    g.amax_part[static_cast<int64_t>(row0 + lr) * g.n_tiles + nt] = m;
   }
 }
 
@@ -531,11 +622,20 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   if (g.tile_map) {
     if (e == -1) return;
     if (e == -2) {
-      for (int idx = threadIdx.x; idx < (row1 - row0) * C::kBN; idx += C::kThreads) {
-        const int64_t r = row0 + idx / C::kBN, c = n0 + idx % C::kBN;
-        if (c < g.n) {
-          if constexpr (OUT == TAI_DT_INT32) static_cast<int32_t*>(g.out)[r * g.n + c] = 0;
-          else store_from_f32(g.out, OUT, r * g.n + c, 0.0f);
+      if constexpr (OUT == kOutSwiglu) {  // rows past the grouped total: h = 0, partial max 0
+        const int64_t n2 = g.n / 2, o0 = n0 / 2;
+        for (int idx = threadIdx.x; idx < (row1 - row0) * (C::kBN / 2); idx += C::kThreads) {
+          const int64_t r = row0 + idx / (C::kBN / 2), c = o0 + idx % (C::kBN / 2);
+          if (c < n2) g.h[r * n2 + c] = 0.0f;
+        }
+        for (int r = row0 + threadIdx.x; r < row1; r += C::kThreads) g.amax_part[r * g.n_tiles + nt] = 0.0f;
+      } else {
+        for (int idx = threadIdx.x; idx < (row1 - row0) * C::kBN; idx += C::kThreads) {
+          const int64_t r = row0 + idx / C::kBN, c = n0 + idx % C::kBN;
+          if (c < g.n) {
+            if constexpr (OUT == TAI_DT_INT32) static_cast<int32_t*>(g.out)[r * g.n + c] = 0;
+            else store_from_f32(g.out, OUT, r * g.n + c, 0.0f);
+          }
         }
       }
       return;
@@ -564,7 +664,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   const int64_t nk = g.k / kBigBK;
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s)
-    if (s < nk) big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, s * kBigBK, smem + s * C::kStage, w, lane);
+    if (s < nk) big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, s * kBigBK, smem + s * C::kStage, w, lane);
 
   const int arow = wm * 64 + (lane & 31);            // + 32 i
   const int brow = wn * 128 + (lane & 31);           // + 32 j (NK)
@@ -643,7 +743,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     wait_stage(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (C::kStages - 1 < nk)
-      big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (C::kStages - 1) * kBigBK,
+      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, (C::kStages - 1) * kBigBK,
                                  smem + (C::kStages - 1) * C::kStage, w, lane);
     fetch(0, smem, 0);
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -660,7 +760,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
             wait_stage(kt + 1);
             asm volatile("s_barrier" ::: "memory");
             if (kt + C::kStages < nk)
-              big_issue_stage<LAYOUT, C>(g, bgrp, row0, rows, n0, (kt + C::kStages) * kBigBK,
+              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, (kt + C::kStages) * kBigBK,
                                          smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
             fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
           }
@@ -677,6 +777,10 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   else if (act_m == 1) main_loop(std::integral_constant<int, 1>());
   else main_loop(std::integral_constant<int, 0>());
 
+  if constexpr (OUT == kOutSwiglu) {
+    swiglu_epilogue<C>(g, acc, e, row0, rows, n0, nt, w, lane, smem);
+    return;
+  }
   // Epilogue, specialised on the output dtype so the accumulators stay in registers.
   const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32)
                               ? static_cast<const int32_t*>(g.bias) + e * g.bias_group_stride : nullptr;
@@ -837,7 +941,8 @@ bool cfg_available() {
       ok = set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_INT32>() && set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_BF16>() &&
            set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_FP16>() && set_cfg_lds<C, TAI_LAYOUT_KN, TAI_DT_FP32>() &&
            set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_INT32>() && set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_BF16>() &&
-           set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP16>() && set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP32>();
+           set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP16>() && set_cfg_lds<C, TAI_LAYOUT_NK, TAI_DT_FP32>() &&
+           set_cfg_lds<C, TAI_LAYOUT_KN, kOutSwiglu>() && set_cfg_lds<C, TAI_LAYOUT_NK, kOutSwiglu>();
       (void)hipGetLastError();
     }
     cached = ok ? 1 : 0;
@@ -854,6 +959,7 @@ void launch_cfg_layout(const GemmArgs& g, hipStream_t st) {
     case TAI_DT_INT32: cfg_kernel<C, LAYOUT, TAI_DT_INT32>()<<<grid, T, L, st>>>(g); break;
     case TAI_DT_BF16: cfg_kernel<C, LAYOUT, TAI_DT_BF16>()<<<grid, T, L, st>>>(g); break;
     case TAI_DT_FP16: cfg_kernel<C, LAYOUT, TAI_DT_FP16>()<<<grid, T, L, st>>>(g); break;
+    case kOutSwiglu: cfg_kernel<C, LAYOUT, kOutSwiglu>()<<<grid, T, L, st>>>(g); break;
     default: cfg_kernel<C, LAYOUT, TAI_DT_FP32>()<<<grid, T, L, st>>>(g); break;
   }
 }
@@ -868,6 +974,33 @@ constexpr int kGroupedBM = 128;
 constexpr int kMinBM = 32;  // workspace is sized for the smallest row tile any variant uses
 
 size_t grouped_map_slots(int64_t m, int64_t ng, int bm) { return static_cast<size_t>(2 * cdiv(m, bm) + ng); }
+
+// Second half of npu_grouped_matmul_swiglu_quant_v2: one wave per row; the row's scale is
+// max|h| / 127 from the column tiles' partial maxima, y = clamp(rint(h / scale), -128, 127)
+// (npu_dynamic_quant arithmetic; a zero row gives scale 0 and y 0).
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ h, const float* __restrict__ part,
+                                                           int64_t nparts, int64_t m, int64_t n2, int8_t* __restrict__ y,
+                                                           float* __restrict__ scale) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (row >= m) return;
+  float amax = 0.0f;
+  for (int64_t p = lane; p < nparts; p += 64) amax = fmaxf(amax, part[row * nparts + p]);
+  amax = wave_max(amax);
+  const float sc = amax / 127.0f;
+  for (int64_t c = 4 * lane; c < n2; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(h + row * n2 + c);
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t word = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(vv[q] / sc), -128.0f), 127.0f);
+      word |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(r)))) << (8 * q);
+    }
+    *reinterpret_cast<uint32_t*>(y + row * n2 + c) = word;
+  }
+  if (lane == 0) scale[row] = sc;
+}
 
 }  // namespace
 }  // namespace tai
@@ -971,4 +1104,65 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
   else if (big) launch_cfg<GrpSel>(g, w_layout, st);
   else launch_tile<128, 128>(g, w_layout, st);
   return launch_status("tai_grouped_matmul");
+}
+
+// Workspace of the fused op: the grouped tile table, then h [m, n / 2] fp32 and the per-tile row maxima.
+static size_t swiglu_ws_parts(int64_t m, int64_t n, int64_t num_groups, size_t* h_off, size_t* part_off) {
+  const size_t base = (tai_grouped_matmul_workspace_size(m, n, num_groups) + 255) / 256 * 256;
+  const size_t hb = (static_cast<size_t>(m) * static_cast<size_t>(n / 2) * sizeof(float) + 255) / 256 * 256;
+  const int64_t max_tiles = cdiv(n / 2, 64);  // the narrowest tile covers 64 output columns
+  if (h_off) *h_off = base;
+  if (part_off) *part_off = base + hb;
+  return base + hb + static_cast<size_t>(m) * static_cast<size_t>(max_tiles) * sizeof(float) + 256;
+}
+
+extern "C" size_t tai_grouped_matmul_swiglu_quant_workspace_size(int64_t m, int64_t n, int64_t num_groups) {
+  return swiglu_ws_parts(m, n, num_groups, nullptr, nullptr);
+}
+
+extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                                               int64_t num_groups, int w_layout, const int64_t* group_list,
+                                               int group_list_type, const float* weight_scale, const float* x_scale,
+                                               int8_t* y, float* y_scale, void* workspace, size_t ws_bytes,
+                                               void* stream) {
+  TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 2 && num_groups >= 1, "tai_grouped_matmul_swiglu_quant: bad sizes");
+  TAI_CHECK_ARG(num_groups <= 2048, "tai_grouped_matmul_swiglu_quant: at most 2048 groups");
+  TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK, "tai_grouped_matmul_swiglu_quant: w_layout");
+  TAI_CHECK_ARG(group_list_type == 0 || group_list_type == 1, "tai_grouped_matmul_swiglu_quant: group_list_type");
+  TAI_CHECK_ARG(group_list && weight_scale && x_scale, "tai_grouped_matmul_swiglu_quant: group_list, weight_scale and "
+                "x_scale are required");
+  if (m == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && weight && y && y_scale, "tai_grouped_matmul_swiglu_quant: null pointer");
+  TAI_CHECK_ARG(m < (1ll << 31), "tai_grouped_matmul_swiglu_quant: m must be < 2^31");
+  const bool kn = w_layout == TAI_LAYOUT_KN;
+  const int bk = kn ? GrpKnSel::kBK : GrpSel::kBK;
+  const int bn = kn ? GrpKnSel::kBN : GrpSel::kBN;
+  const bool avail = kn ? cfg_available<GrpKnSel>() : cfg_available<GrpSel>();
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
+  TAI_UNSUPPORTED(!avail || k % bk != 0 || (n / 2) % (bn / 2) != 0 || !al(x) || !al(weight),
+                  "tai_grouped_matmul_swiglu_quant: needs k %% %d == 0, (n / 2) %% %d == 0 and 16-byte aligned "
+                  "operands", bk, bn / 2);
+  size_t h_off = 0, part_off = 0;
+  const size_t need = swiglu_ws_parts(m, n, num_groups, &h_off, &part_off);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_grouped_matmul_swiglu_quant: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int bm = kn ? GrpKnSel::kBM : GrpSel::kBM;
+  const int64_t slots = static_cast<int64_t>(grouped_map_slots(m, num_groups, bm));
+  char* wsp = static_cast<char*>(workspace);
+  int64_t* live = reinterpret_cast<int64_t*>(wsp);
+  int4* map = reinterpret_cast<int4*>(wsp + 256);
+  float* h = reinterpret_cast<float*>(wsp + h_off);
+  float* part = reinterpret_cast<float*>(wsp + part_off);
+  const int64_t n_tiles = (n / 2) / (bn / 2);
+  GemmArgs g{x, weight, m, k, n, k * n, weight_scale, n, n, x_scale, nullptr, 0, n, kOutSwiglu, nullptr,
+             map, slots, n_tiles, live, h, part};
+  group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type,
+                                                                              m, bm, map, slots, live, nullptr);
+  if (kn) launch_cfg<GrpKnSel>(g, w_layout, st);
+  else launch_cfg<GrpSel>(g, w_layout, st);
+  swiglu_quant_kernel<<<dim3(static_cast<unsigned>(cdiv(m, 4))), 256, 0, st>>>(h, part, n_tiles, m, n / 2, y, y_scale);
+  return launch_status("tai_grouped_matmul_swiglu_quant");
 }

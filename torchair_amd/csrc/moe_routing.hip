@@ -521,3 +521,185 @@ extern "C" int tai_moe_finalize_routing(const void* expanded, int dtype, int64_t
     finalize_generic_kernel<<<dim3(static_cast<unsigned>(t)), 256, 0, st>>>(a);
   return launch_status("tai_moe_finalize_routing");
 }
+
+// ============================================================================ grouped_matmul_finalize_routing
+// The W8A8 grouped GEMM writes its dequantised rows (fp32, so the combine adds no rounding of its
+// own) to a scratch buffer; each output token
+// then gathers the rows r with row_index[r] == token, in ascending r, as
+//   y[token] = sum_r logit[r] * row[r]  (+ shared_input_weight * shared_input[token - offset]).
+// The token -> rows lists come from a histogram, a scan and an atomic placement; the gather
+// sorts each list, so the fp32 sum has a fixed order and the result is reproducible.
+namespace tai {
+namespace {
+
+constexpr int kGfrMaxRows = 1024;  // rows one token may gather
+
+__global__ __launch_bounds__(256) void gfr_fill_kernel(int32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void gfr_hist_kernel(const void* __restrict__ row_index, int idx_dt, int64_t m,
+                                                       int64_t bs, int32_t* __restrict__ counts) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= m) return;
+  const int64_t t = row_index ? load_index(row_index, idx_dt, r) : r;
+  if (t >= 0 && t < bs) atomicAdd(&counts[t], 1);
+}
+
+// One workgroup: exclusive offsets of the per-token counts, 1024 tokens per pass.
+__global__ __launch_bounds__(1024) void gfr_scan_kernel(const int32_t* __restrict__ counts, int64_t bs,
+                                                        int32_t* __restrict__ offs) {
+  __shared__ int32_t red[16];
+  __shared__ int32_t carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int64_t b0 = 0; b0 < bs; b0 += 1024) {
+    const int64_t i = b0 + threadIdx.x;
+    const int32_t v = i < bs ? counts[i] : 0;
+    const int32_t incl = block_incl_scan<false>(v, red);
+    const int32_t base = carry;
+    if (i < bs) offs[i] = base + incl - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = base + incl;
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void gfr_place_kernel(const void* __restrict__ row_index, int idx_dt, int64_t m,
+                                                        int64_t bs, const int32_t* __restrict__ offs,
+                                                        int32_t* __restrict__ cursor, int32_t* __restrict__ list) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= m) return;
+  const int64_t t = row_index ? load_index(row_index, idx_dt, r) : r;
+  if (t >= 0 && t < bs) list[offs[t] + atomicAdd(&cursor[t], 1)] = static_cast<int32_t>(r);
+}
+
+struct GfrArgs {
+  const float* rows;     // [m, n] fp32 dequantised GEMM rows
+  const float* logit;    // [m] or null (1)
+  const int32_t* counts;
+  const int32_t* offs;
+  const int32_t* list;
+  const uint16_t* shared;  // [shared_rows, n] bf16 or null
+  int64_t shared_rows, shared_offset;
+  float shared_weight;
+  int64_t n;
+  float* y;  // [bs, n] fp32
+};
+
+// One workgroup per output token.
+__global__ __launch_bounds__(256) void gfr_gather_kernel(GfrArgs a) {
+  __shared__ int32_t s_in[kGfrMaxRows];
+  __shared__ int32_t s_sorted[kGfrMaxRows];
+  __shared__ float s_w[kGfrMaxRows];
+  const int64_t t = blockIdx.x;
+  const int cnt = a.counts[t];
+  float* yrow = a.y + t * a.n;
+  if (cnt > kGfrMaxRows) {  // outside the supported range: make it loud
+    for (int64_t c = threadIdx.x; c < a.n; c += 256) yrow[c] = __builtin_nanf("");
+    return;
+  }
+  const int32_t* lst = a.list + a.offs[t];
+  for (int i = threadIdx.x; i < cnt; i += 256) s_in[i] = lst[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < cnt; i += 256) {  // rank sort: rows are distinct
+    const int32_t v = s_in[i];
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) rank += s_in[j] < v;
+    s_sorted[rank] = v;
+    s_w[rank] = a.logit ? a.logit[v] : 1.0f;
+  }
+  __syncthreads();
+  const bool sh = a.shared && t >= a.shared_offset && t < a.shared_offset + a.shared_rows;
+  const int64_t n8 = a.n / 8;
+  for (int64_t c = threadIdx.x; c < n8; c += 256) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < cnt; ++i) {
+      const float4* src = reinterpret_cast<const float4*>(a.rows + static_cast<int64_t>(s_sorted[i]) * a.n + 8 * c);
+      const float4 lo = src[0], hi = src[1];
+      const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const float wgt = s_w[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + wgt * v[e];
+    }
+    if (sh) {
+      float v[8];
+      load8_bf16(a.shared, (t - a.shared_offset) * a.n + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + a.shared_weight * v[e];
+    }
+    float4* dst = reinterpret_cast<float4*>(yrow + 8 * c);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+}  // namespace
+}  // namespace tai
+
+static size_t gfr_parts(int64_t m, int64_t n, int64_t num_groups, int64_t bs, size_t* rows_off, size_t* idx_off) {
+  const size_t base = align256(tai_grouped_matmul_workspace_size(m, n, num_groups));
+  const size_t rows = align256(static_cast<size_t>(m) * static_cast<size_t>(n) * sizeof(float));
+  if (rows_off) *rows_off = base;
+  if (idx_off) *idx_off = base + rows;
+  return base + rows + align256(sizeof(int32_t) * (3 * static_cast<size_t>(bs) + static_cast<size_t>(m))) + 256;
+}
+
+extern "C" size_t tai_grouped_matmul_finalize_routing_workspace_size(int64_t m, int64_t n, int64_t num_groups,
+                                                                     int64_t output_bs) {
+  return gfr_parts(m, n, num_groups, output_bs, nullptr, nullptr);
+}
+
+extern "C" int tai_grouped_matmul_finalize_routing(const int8_t* x, const int8_t* weight, int64_t m, int64_t k,
+                                                   int64_t n, int64_t num_groups, int w_layout,
+                                                   const int64_t* group_list, int group_list_type, const float* scale,
+                                                   const float* pertoken_scale, const float* bias, const float* logit,
+                                                   const void* row_index, int row_index_dtype, const void* shared_input,
+                                                   int64_t shared_rows, float shared_input_weight,
+                                                   int64_t shared_input_offset, int64_t output_bs, float* y,
+                                                   void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(m >= 0 && n >= 1 && output_bs >= 0 && shared_rows >= 0, "tai_grouped_matmul_finalize_routing: bad sizes");
+  TAI_CHECK_ARG(n % 8 == 0, "tai_grouped_matmul_finalize_routing: n must be a multiple of 8");
+  TAI_CHECK_ARG(scale != nullptr, "tai_grouped_matmul_finalize_routing: scale is required");
+  TAI_CHECK_ARG(row_index == nullptr || row_index_dtype == TAI_DT_INT32 || row_index_dtype == TAI_DT_INT64,
+                "tai_grouped_matmul_finalize_routing: row_index must be int32 or int64");
+  TAI_CHECK_ARG(shared_input == nullptr || (shared_input_offset >= 0 && shared_input_offset + shared_rows <= output_bs),
+                "tai_grouped_matmul_finalize_routing: shared_input rows must lie inside the output");
+  TAI_CHECK_ARG(m < (1ll << 31), "tai_grouped_matmul_finalize_routing: m must be < 2^31");
+  if (output_bs == 0) return TAI_OK;
+  TAI_CHECK_ARG(y != nullptr, "tai_grouped_matmul_finalize_routing: null output");
+  size_t rows_off = 0, idx_off = 0;
+  const size_t need = gfr_parts(m, n, num_groups, output_bs, &rows_off, &idx_off);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_grouped_matmul_finalize_routing: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* wsp = static_cast<char*>(workspace);
+  float* rows = reinterpret_cast<float*>(wsp + rows_off);
+  int32_t* counts = reinterpret_cast<int32_t*>(wsp + idx_off);
+  int32_t* cursor = counts + output_bs;
+  int32_t* offs = cursor + output_bs;
+  int32_t* list = offs + output_bs;
+  if (m > 0) {
+    const int rc = tai_grouped_matmul(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, scale,
+                                      pertoken_scale, bias, bias ? TAI_DT_FP32 : TAI_DT_NONE, TAI_DT_FP32, rows,
+                                      workspace, rows_off, stream);
+    if (rc != TAI_OK) return rc;
+  }
+  gfr_fill_kernel<<<dim3(static_cast<unsigned>(cdiv(2 * output_bs, 256) < 1024 ? cdiv(2 * output_bs, 256) : 1024)), 256, 0,
+                    st>>>(counts, 2 * output_bs);
+  if (m > 0) {
+    const dim3 grid(static_cast<unsigned>(cdiv(m, 256)));
+    gfr_hist_kernel<<<grid, 256, 0, st>>>(row_index, row_index_dtype, m, output_bs, counts);
+    gfr_scan_kernel<<<1, 1024, 0, st>>>(counts, output_bs, offs);
+    gfr_place_kernel<<<grid, 256, 0, st>>>(row_index, row_index_dtype, m, output_bs, offs, cursor, list);
+  } else {
+    gfr_scan_kernel<<<1, 1024, 0, st>>>(counts, output_bs, offs);
+  }
+  GfrArgs a{rows, logit, counts, offs, list, static_cast<const uint16_t*>(shared_input), shared_rows,
+            shared_input_offset, shared_input_weight, n, y};
+  gfr_gather_kernel<<<dim3(static_cast<unsigned>(output_bs)), 256, 0, st>>>(a);
+  return launch_status("tai_grouped_matmul_finalize_routing");
+}
