@@ -79,6 +79,24 @@ class MoeLayer:
                                      output_dtype=torch.bfloat16)[0]
         return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
 
+    def step_fused(self):
+        """The same layer with gate_up + dequant_swiglu_quant as one op (npu_grouped_matmul_swiglu_quant_v2),
+        whose result is bit-identical to the two-op composition."""
+        torch = self.torch
+        npu = torch.ops.npu
+        y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
+                                             group_select_mode=1, renorm=0, norm_type=1,
+                                             routed_scaling_factor=1.0, eps=1e-20)
+        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
+                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                        row_idx_type=0)
+        q, s = npu.npu_dynamic_quant(ex)
+        q2, s2 = npu.npu_grouped_matmul_swiglu_quant_v2(q, [self.w_gu], [self.s_gu], s, counts, group_list_type=1)
+        out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
+                                     split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.bfloat16)[0]
+        return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
+
     def gmm1_bytes(self):
         T, H, K, I = self.T, self.H, self.K, self.I
         # weights of the experts that received rows + int8 rows + int32 out (an expert with no rows is never read)
@@ -102,6 +120,89 @@ def bench_moe(torch, dev, steps, warmup):
             "traffic": _measured_traffic(), "avg_ms": round(gmm_ms, 4),
             "algorithmic_bytes": layer.gmm1_bytes(), "active_experts": layer.active_experts}
     return layer, dt, roof
+
+
+def bench_moe_variants(torch, layer, iters=10):
+    """ms per step of the config-4 layer with the fused gate_up op, and of the prescribed composition
+    replayed from a hipGraph (launch gaps removed)."""
+    from torchair_amd.graph import HipGraphRunner
+    out = {}
+    # the runner captures per input signature; the router logits are passed as a static input (no copy)
+    runner = HipGraphRunner(lambda logits: layer.step(), clone_input=False)
+    for _ in range(2):
+        layer.step_fused()
+        runner(layer.logits)
+    torch.cuda.synchronize()
+    for name, fn in (("fused_gate_up_ms", layer.step_fused), ("hipgraph_ms", lambda: runner(layer.logits))):
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / iters, 4)
+    out["fused_gate_up_tokens_per_s"] = round(MoeLayer.T / (out["fused_gate_up_ms"] * 1e-3), 1)
+    out["hipgraph_tokens_per_s"] = round(MoeLayer.T / (out["hipgraph_ms"] * 1e-3), 1)
+    return out
+
+
+# ----------------------------------------------------------------------------- norm / cache writers
+def bench_norm_cache(torch, dev, iters=40):
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    npu = torch.ops.npu
+    res = {}
+
+    from torchair_amd.graph import HipGraphRunner
+
+    def timed(fn, per_graph=20):
+        """GPU ms per call: per_graph calls are captured into one hipGraph and replayed, so neither the
+        host launch cost nor the replay overhead is counted."""
+        key = torch.zeros(1, device=dev)  # a device input, so the runner captures (static: never copied)
+        runner = HipGraphRunner(lambda k: [fn() for _ in range(per_graph)], clone_input=False)
+        for _ in range(3):
+            runner(key)
+        torch.cuda.synchronize()
+        reps = max(1, iters // per_graph * 4)
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            runner(key)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * per_graph)
+
+    # add_rms_norm_dynamic_quant on the config-4 activations [4096, 7168]
+    T, H = 4096, 7168
+    x1 = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    x2 = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    gamma = (torch.rand(H, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    sm = torch.rand(H, generator=g, device=dev) + 0.5
+    ms = timed(lambda: npu.npu_add_rms_norm_dynamic_quant(x1, x2, gamma, smooth_scale1=sm, output_mask=[True, False]))
+    byts = T * H * 2 * 3 + T * H + T * 4 + H * 6
+    res["add_rms_norm_dynamic_quant_4096x7168"] = {"us": round(ms * 1e3, 2), "GB/s": round(byts / ms / 1e6, 1),
+                                                   "frac_hbm": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    # MLA cache update for one decode step of config 5 (128 tokens) into an int8 latent cache
+    B, nb, bs = 128, 128 * 64, 128
+    kv = torch.randn(B, 1, 1, 576, generator=g, device=dev).to(torch.bfloat16)
+    cos = torch.randn(B, 1, 1, 64, generator=g, device=dev).to(torch.bfloat16)
+    sin = torch.randn(B, 1, 1, 64, generator=g, device=dev).to(torch.bfloat16)
+    gam = (torch.rand(512, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    slots = torch.randperm(nb * bs, generator=g, device=dev)[:B]
+    kcache = torch.zeros(nb, bs, 1, 64, dtype=torch.bfloat16, device=dev)
+    ccache = torch.zeros(nb, bs, 1, 512, dtype=torch.int8, device=dev)
+    tok = torch.zeros(nb, bs, dtype=torch.float32, device=dev)
+    ms = timed(lambda: npu.npu_kv_rmsnorm_rope_cache_v2(kv, gam, cos, sin, slots, kcache, ccache, c_kv_scale=tok,
+                                                        cache_mode="PA"))
+    res["kv_rmsnorm_rope_cache_cfg5_step_us"] = round(ms * 1e3, 2)
+    # paged KV write for one decode step of config 2 (64 tokens, 8 kv heads, d 128)
+    key = torch.randn(64, 8, 128, generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.zeros(1152, 128, 8, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    sl = torch.randperm(1152 * 128, generator=g, device=dev)[:64]
+    ms = timed(lambda: npu.npu_scatter_pa_kv_cache(key, key, kc, vc, sl))
+    res["scatter_pa_kv_cache_cfg2_step_us"] = round(ms * 1e3, 2)
+    return res
 
 
 # ----------------------------------------------------------------------------- W8A8 GEMM 8192^3
@@ -370,7 +471,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of side benches to run (gemm,mlp,decode,prefill,mla; 'none' for the MoE layer "
+                    help="comma list of side benches to run (moe,norm,gemm,mlp,decode,prefill,mla; 'none' for the MoE layer "
                          "alone; 'copy' adds the 1 GiB copy that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -382,10 +483,14 @@ def main():
     dev = "cuda:0"
     torch.cuda.synchronize()
     layer, dt, roof = bench_moe(torch, dev, args.steps, args.warmup)
+    extra = {}
+    only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode", "prefill", "mla", "moe", "norm"}
+    if "moe" in only:
+        extra["moe_layer_variants"] = bench_moe_variants(torch, layer)
     del layer
     torch.cuda.empty_cache()
-    extra = {}
-    only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode", "prefill", "mla"}
+    if "norm" in only:
+        extra["norm_cache_writers"] = bench_norm_cache(torch, dev)
     if "gemm" in only:
         extra["w8a8_gemm_8192"] = bench_gemm(torch, dev)
     if "mlp" in only:

@@ -266,8 +266,10 @@ def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
         return out
     if k == 0:
         return out.zero_()
+    ws_bytes = _lib.query("tai_quant_matmul_workspace_size", m, k, n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x1.device) if ws_bytes else None
     _lib.call("tai_quant_matmul", _p(a), _p(w), m, k, n, layout, _p(sc), sc.numel() if sc is not None else 0,
-              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _stream(a))
+              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _p(ws), ws_bytes, _stream(a))
     return out
 
 

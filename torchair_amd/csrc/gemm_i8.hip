@@ -51,6 +51,10 @@ struct GemmArgs {
   const int64_t* live_slots;  // grouped: slots in use (real + zero-fill tiles), written by the prologue
   float* h;          // SwiGLU epilogue: silu(gate) * up, fp32 [m, n / 2]
   float* amax_part;  // SwiGLU epilogue: per-row max |h| of each column tile, [m, n_tiles]
+  // split-K (dense, int32 partials): k_split slices of k_per K stages each; slice s writes its raw
+  // accumulators to out + s * m * n
+  int64_t k_split;
+  int64_t k_per;
 };
 
 // Output code of the fused SwiGLU epilogue (npu_grouped_matmul_swiglu_quant_v2).
@@ -81,8 +85,8 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
 // and each XCD takes an equal contiguous share of them (a plain remap of the whole grid would give
 // the XCDs holding the upper ids nothing but empty slots).
 __device__ __forceinline__ int64_t tile_id(const GemmArgs& g, int64_t b) {
-  const int64_t nb = g.m_slots * g.n_tiles;
-  if (!g.live_slots) return xcd_remap(b, nb);
+  const int64_t nb = g.m_slots * g.n_tiles * (g.k_split > 1 ? g.k_split : 1);  // the launch's grid
+  if (!g.live_slots) return b < nb ? xcd_remap(b, nb) : -1;
   const int64_t live = *g.live_slots * g.n_tiles;
   const int64_t xcd = b % kXcds, idx = b / kXcds;
   const int64_t per = live / kXcds, rem = live % kXcds;
@@ -612,9 +616,10 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
     constexpr int64_t GM = 8;
     const int64_t per_group = GM * g.n_tiles;
-    const int64_t first = (L / per_group) * GM;
+    const int64_t Lt = g.k_split > 1 ? L % (g.m_slots * g.n_tiles) : L;  // split-K: slice = L / tiles
+    const int64_t first = (Lt / per_group) * GM;
     const int64_t gsize = g.m_slots - first < GM ? g.m_slots - first : GM;
-    const int64_t in = L % per_group;
+    const int64_t in = Lt % per_group;
     slot = first + in % gsize;
     nt = in / gsize;
   }
@@ -661,10 +666,20 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int64_t nk = g.k / kBigBK;
+  // K range of this workgroup (split-K slices a dense launch; otherwise the whole of K)
+  int64_t kbeg = 0, nk = g.k / kBigBK;
+  void* gout = g.out;
+  if (g.k_split > 1) {
+    const int64_t ks = L / (g.m_slots * g.n_tiles);
+    if (ks >= g.k_split) return;
+    kbeg = ks * g.k_per;
+    nk = nk - kbeg < g.k_per ? nk - kbeg : g.k_per;
+    gout = static_cast<int32_t*>(g.out) + ks * g.m * g.n;
+  }
+  const int64_t kb0 = kbeg * kBigBK;
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s)
-    if (s < nk) big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, s * kBigBK, smem + s * C::kStage, w, lane);
+    if (s < nk) big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + s * kBigBK, smem + s * C::kStage, w, lane);
 
   const int arow = wm * 64 + (lane & 31);            // + 32 i
   const int brow = wn * 128 + (lane & 31);           // + 32 j (NK)
@@ -743,7 +758,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     wait_stage(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (C::kStages - 1 < nk)
-      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, (C::kStages - 1) * kBigBK,
+      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + (C::kStages - 1) * kBigBK,
                                  smem + (C::kStages - 1) * C::kStage, w, lane);
     fetch(0, smem, 0);
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -760,7 +775,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
             wait_stage(kt + 1);
             asm volatile("s_barrier" ::: "memory");
             if (kt + C::kStages < nk)
-              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, (kt + C::kStages) * kBigBK,
+              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + (kt + C::kStages) * kBigBK,
                                          smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
             fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
           }
@@ -856,7 +871,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
           const int lr = wm * 64 + i * 32 + 16 * h + sl;
           const uint4 v = *reinterpret_cast<const uint4*>(wreg + sl * RB + 16 * (lane % LPR));
           if (lr < rows)
-            *reinterpret_cast<uint4*>(static_cast<char*>(g.out) + (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
+            *reinterpret_cast<uint4*>(static_cast<char*>(gout) + (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
                                       16 * (lane % LPR)) = v;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
@@ -880,8 +895,8 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
         if (colok && lr < rows) {
           const int64_t idx = static_cast<int64_t>(row0 + lr) * g.n + col;
           const uint32_t bits = out_bits(acc[i][j][r] + bcol, sc, bf, g.pts ? g.pts[row0 + lr] : 1.0f);
-          if constexpr (OUT == TAI_DT_BF16 || OUT == TAI_DT_FP16) static_cast<uint16_t*>(g.out)[idx] = static_cast<uint16_t>(bits);
-          else static_cast<uint32_t*>(g.out)[idx] = bits;
+          if constexpr (OUT == TAI_DT_BF16 || OUT == TAI_DT_FP16) static_cast<uint16_t*>(gout)[idx] = static_cast<uint16_t>(bits);
+          else static_cast<uint32_t*>(gout)[idx] = bits;
         }
       }
     }
@@ -975,6 +990,55 @@ constexpr int kMinBM = 32;  // workspace is sized for the smallest row tile any 
 
 size_t grouped_map_slots(int64_t m, int64_t ng, int bm) { return static_cast<size_t>(2 * cdiv(m, bm) + ng); }
 
+// Skinny dense GEMMs (m < 256, e.g. a decode-sized MLP): 128 x 256 tiles leave most CUs idle, so K
+// is split into slices whose int32 partials are summed (exactly) by splitk_reduce_kernel, which also
+// applies the epilogue. The partials are small enough to stay in the last-level cache.
+using SkinnyCfg = BigCfg<2, 2, 64, 4>;
+constexpr int64_t kSkinnyTargetWgs = 512;
+
+struct SplitPlan {
+  int64_t m_slots, n_tiles, split, per;
+};
+
+SplitPlan skinny_plan(int64_t m, int64_t k, int64_t n) {
+  SplitPlan p{cdiv(m, SkinnyCfg::kBM), cdiv(n, SkinnyCfg::kBN), 1, k / SkinnyCfg::kBK};
+  const int64_t tiles = p.m_slots * p.n_tiles;
+  const int64_t nk = k / SkinnyCfg::kBK;
+  int64_t want = cdiv(kSkinnyTargetWgs, tiles);
+  want = want < 1 ? 1 : (want > nk ? nk : want);
+  p.per = cdiv(nk, want);
+  p.split = cdiv(nk, p.per);
+  return p;
+}
+
+bool skinny_ok(int64_t m, int64_t k, int64_t n, int layout) {
+  return m < 256 && k % SkinnyCfg::kBK == 0 && k >= SkinnyCfg::kBK && (layout == TAI_LAYOUT_NK || n % 16 == 0) &&
+         n % 4 == 0;
+}
+
+// out = epilogue(sum of the split partials); 4 consecutive elements per thread (n % 4 == 0).
+template <int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __restrict__ part, int64_t split, GemmArgs g) {
+  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  const int64_t mn = g.m * g.n;
+  if (i4 >= mn) return;
+  int4 acc = *reinterpret_cast<const int4*>(part + i4);
+  for (int64_t sidx = 1; sidx < split; ++sidx) {
+    const int4 v = *reinterpret_cast<const int4*>(part + sidx * mn + i4);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  const int64_t row = i4 / g.n, col = i4 % g.n;
+  const int32_t a4[4] = {acc.x, acc.y, acc.z, acc.w};
+  const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(g.bias) : nullptr;
+  const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(g.bias) : nullptr;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int32_t v = a4[q] + (bias_i ? bias_i[col + q] : 0);
+    if constexpr (OUT == TAI_DT_INT32) static_cast<int32_t*>(g.out)[i4 + q] = v;
+    else store_from_f32(g.out, OUT, i4 + q, epilogue_value(g, 0, row, col + q, v, bias_f));
+  }
+}
+
 // Second half of npu_grouped_matmul_swiglu_quant_v2: one wave per row; the row's scale is
 // max|h| / 127 from the column tiles' partial maxima, y = clamp(rint(h / scale), -128, 127)
 // (npu_dynamic_quant arithmetic; a zero row gives scale 0 and y 0).
@@ -1007,9 +1071,16 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
 
 using namespace tai;
 
+extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n) {
+  if (m <= 0 || n <= 0 || !skinny_ok(m, k, n, TAI_LAYOUT_NK)) return 0;
+  const SplitPlan p = skinny_plan(m, k, n);
+  return p.split > 1 ? static_cast<size_t>(p.split) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4 + 256 : 0;
+}
+
 extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
                                 const float* scale, int64_t scale_len, const float* pertoken_scale, const void* bias,
-                                int bias_dtype, int out_dtype, void* out, void* stream) {
+                                int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes,
+                                void* stream) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 0, "tai_quant_matmul: negative size");
   TAI_CHECK_ARG(x2_layout == TAI_LAYOUT_KN || x2_layout == TAI_LAYOUT_NK, "tai_quant_matmul: x2_layout");
   TAI_CHECK_ARG(out_dtype == TAI_DT_INT32 || out_dtype == TAI_DT_BF16 || out_dtype == TAI_DT_FP16 ||
@@ -1028,6 +1099,42 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (!fast_path_ok(g, x2_layout)) {
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, x2_layout, nullptr);
+    return launch_status("tai_quant_matmul");
+  }
+  if (skinny_ok(m, k, n, x2_layout) && cfg_available<SkinnyCfg>()) {
+    const SplitPlan p = skinny_plan(m, k, n);
+    g.m_slots = p.m_slots;
+    g.n_tiles = p.n_tiles;
+    if (p.split == 1) {
+      launch_cfg<SkinnyCfg>(g, x2_layout, st);
+      return launch_status("tai_quant_matmul");
+    }
+    const size_t need = tai_quant_matmul_workspace_size(m, k, n);
+    if (workspace == nullptr || ws_bytes < need) {
+      set_error("tai_quant_matmul: workspace of %zu bytes, need %zu", ws_bytes, need);
+      return TAI_ERR_WORKSPACE;
+    }
+    GemmArgs gp = g;  // partial pass: raw int32 slices into the workspace
+    gp.scale = nullptr;
+    gp.pts = nullptr;
+    gp.bias = nullptr;
+    gp.out_dt = TAI_DT_INT32;
+    gp.out = workspace;
+    gp.k_split = p.split;
+    gp.k_per = p.per;
+    const dim3 grid(static_cast<unsigned>(p.m_slots * p.n_tiles * p.split));
+    if (x2_layout == TAI_LAYOUT_NK)
+      cfg_kernel<SkinnyCfg, TAI_LAYOUT_NK, TAI_DT_INT32>()<<<grid, SkinnyCfg::kThreads, SkinnyCfg::kLds, st>>>(gp);
+    else
+      cfg_kernel<SkinnyCfg, TAI_LAYOUT_KN, TAI_DT_INT32>()<<<grid, SkinnyCfg::kThreads, SkinnyCfg::kLds, st>>>(gp);
+    const dim3 rgrid(static_cast<unsigned>(cdiv(m * n, 1024)));
+    const int32_t* part = static_cast<const int32_t*>(workspace);
+    switch (out_dtype) {
+      case TAI_DT_INT32: splitk_reduce_kernel<TAI_DT_INT32><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      case TAI_DT_BF16: splitk_reduce_kernel<TAI_DT_BF16><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      case TAI_DT_FP16: splitk_reduce_kernel<TAI_DT_FP16><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      default: splitk_reduce_kernel<TAI_DT_FP32><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+    }
     return launch_status("tai_quant_matmul");
   }
   if (m >= 256 && k % kBigBK == 0 && (x2_layout == TAI_LAYOUT_NK || n % 16 == 0) && cfg_available<BigSel>()) {

@@ -62,6 +62,17 @@ __device__ __forceinline__ void store8(void* base, int64_t idx, const float (&v)
   }
 }
 
+// 8 consecutive fp32 values (16-byte aligned), or 1.0 when p is null.
+__device__ __forceinline__ void load8_f32_or_one(const float* p, int64_t idx, float (&v)[kVec]) {
+  if (!p) {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) v[j] = 1.0f;
+    return;
+  }
+  const float4 a = reinterpret_cast<const float4*>(p + idx)[0], b = reinterpret_cast<const float4*>(p + idx)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 __device__ __forceinline__ int8_t quant1(float v, float scale) {
   if (scale == 0.0f) return 0;
   const float q = fminf(fmaxf(rintf(v / scale), -128.0f), 127.0f);
@@ -172,11 +183,14 @@ __global__ __launch_bounds__(TPR) void add_rms_norm_kernel(NormArgs a) {
       if constexpr (!QUANT) {
         store8<DT>(a.y, base + vi * kVec, x[i]);
       } else {
+        float sm[kVec];
+        load8_f32_or_one(a.smooth1, vi * kVec, sm);
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-          const float s1 = a.smooth1 ? x[i][j] * a.smooth1[vi * kVec + j] : x[i][j];
-          amax1 = fmaxf(amax1, fabsf(s1));
-          if (a.y2) amax2 = fmaxf(amax2, fabsf(a.smooth2 ? x[i][j] * a.smooth2[vi * kVec + j] : x[i][j]));
+        for (int j = 0; j < kVec; ++j) amax1 = fmaxf(amax1, fabsf(x[i][j] * sm[j]));
+        if (a.y2) {
+          load8_f32_or_one(a.smooth2, vi * kVec, sm);
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) amax2 = fmaxf(amax2, fabsf(x[i][j] * sm[j]));
         }
       }
     }
@@ -191,13 +205,15 @@ __global__ __launch_bounds__(TPR) void add_rms_norm_kernel(NormArgs a) {
     for (int i = 0; i < NV; ++i) {
       const int64_t vi = lane + static_cast<int64_t>(i) * TPR;
       if (vi < nvec) {
-        float q[kVec];
+        float sm[kVec], q[kVec];
+        load8_f32_or_one(a.smooth1, vi * kVec, sm);
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) q[j] = a.smooth1 ? x[i][j] * a.smooth1[vi * kVec + j] : x[i][j];
+        for (int j = 0; j < kVec; ++j) q[j] = x[i][j] * sm[j];
         *reinterpret_cast<uint2*>(a.y1 + base + vi * kVec) = pack8(q, sc1);
         if (a.y2) {
+          load8_f32_or_one(a.smooth2, vi * kVec, sm);
 #pragma unroll
-          for (int j = 0; j < kVec; ++j) q[j] = a.smooth2 ? x[i][j] * a.smooth2[vi * kVec + j] : x[i][j];
+          for (int j = 0; j < kVec; ++j) q[j] = x[i][j] * sm[j];
           *reinterpret_cast<uint2*>(a.y2 + base + vi * kVec) = pack8(q, sc2);
         }
       }
@@ -272,7 +288,8 @@ int run_norm(const NormArgs& a, int dt, hipStream_t st, const char* what) {
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
   const bool vec = a.cols % kVec == 0 && a.cols / kVec <= 256 * 4 && al(a.x1) && al(a.x2) && al(a.gamma) &&
                    (!a.beta || al(a.beta)) && (!a.x_out || al(a.x_out)) && (QUANT || al(a.y)) &&
-                   (!QUANT || (al(a.y1) && (!a.y2 || al(a.y2))));
+                   (!QUANT || (al(a.y1) && (!a.y2 || al(a.y2)) && (!a.smooth1 || al(a.smooth1)) &&
+                               (!a.smooth2 || al(a.smooth2))));
   if (!vec) {
     add_rms_norm_generic_kernel<QUANT><<<dim3(static_cast<unsigned>(a.rows)), 256, 0, st>>>(a, dt);
   } else if (dt == TAI_DT_BF16) {
