@@ -17,3 +17,10 @@ npu_moe_gating_top_k = torch.ops.npu.npu_moe_gating_top_k
 npu_moe_init_routing = torch.ops.npu.npu_moe_init_routing
 npu_moe_init_routing_v2 = torch.ops.npu.npu_moe_init_routing_v2
 npu_moe_finalize_routing = torch.ops.npu.npu_moe_finalize_routing
+npu_add_rms_norm = torch.ops.npu.npu_add_rms_norm
+npu_add_rms_norm_dynamic_quant = torch.ops.npu.npu_add_rms_norm_dynamic_quant
+npu_scatter_pa_kv_cache = torch.ops.npu.npu_scatter_pa_kv_cache
+npu_kv_rmsnorm_rope_cache = torch.ops.npu.npu_kv_rmsnorm_rope_cache
+npu_kv_rmsnorm_rope_cache_v2 = torch.ops.npu.npu_kv_rmsnorm_rope_cache_v2
+npu_grouped_matmul_swiglu_quant_v2 = torch.ops.npu.npu_grouped_matmul_swiglu_quant_v2
+npu_grouped_matmul_finalize_routing = torch.ops.npu.npu_grouped_matmul_finalize_routing
