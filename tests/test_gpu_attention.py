@@ -195,3 +195,25 @@ def test_mla_cfg5():
     g = torch.Generator().manual_seed(121)
     lens = torch.randint(2048, 8193, (128,), generator=g).tolist()
     _check_mla(lens, 128, 128, 122)
+
+
+def test_mla_rising_logits_take_the_rescaling_pass():
+    # Rope keys of sequence 0 jump by ~100 (log2 units) after its first two pages: the fast pass
+    # flags those splits and the rescaling pass redoes them; the other sequences stay on the fast pass.
+    lens, h, bs = [3000, 500, 2100], 128, 64
+    qn, qr, ckv, cs, kr, bt = _mla_case(lens, h, bs, 124)
+    qr = torch.ones_like(qr)
+    for j in range(2, (lens[0] + bs - 1) // bs):
+        kr[bt[0, j]] = 16.0
+    scale = 1.0 / math.sqrt(192)
+    out, lse = torch.ops.air.npu_fused_infer_attention_score(
+        qn.to(DEV), ckv.to(DEV), ckv.to(DEV), query_rope=qr.to(DEV), key_rope=kr.to(DEV),
+        key_antiquant_scale=cs.to(DEV), key_antiquant_mode=1, block_table=bt.to(DEV),
+        actual_seq_lengths_kv=torch.tensor(lens, device=DEV), num_heads=h, num_key_value_heads=1,
+        input_layout="BSND", block_size=bs, scale=scale, softmax_lse_flag=True)
+    want, wl = G.mla_decode_attention(f32np(qn[:, 0]), f32np(qr[:, 0]), ckv[:, :, 0].numpy(), cs.numpy(),
+                                      f32np(kr[:, :, 0]), bt.numpy(), lens, scale)
+    assert np.isfinite(f32np(out)).all()
+    assert_close(f32np(out[:, 0]), want)
+    got = lse.reshape(len(lens), h).cpu().numpy()
+    np.testing.assert_allclose(got, wl, rtol=1e-3, atol=1e-3)

@@ -246,7 +246,9 @@ void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Merge the splits of one (b, q head): one workgroup of D threads.
+// Merge the splits of one (b, q head): one workgroup of D threads. Every wave reduces the split
+// maxima and sums itself (lane s holds split s, s + 64, ...), so no workgroup barrier is needed;
+// the numerator loop has no data-dependent branch, so its loads are issued back to back.
 template <int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint16_t* out, float* lse) {
   const int64_t bh = blockIdx.x;
@@ -256,18 +258,29 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
   const int64_t base = (b * a.hkv + kvh) * a.nsplit;
   const int64_t L = a.lens[b];
   const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kChunk - 1) / kChunk));
+  const float* ml = a.part_ml + base * 32 + 2 * hi;  // split s: ml[32 s], ml[32 s + 1]
+  const int lane = threadIdx.x & 63;
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base + s) * 32 + 2 * hi]);
-  float den = 0.0f, num = 0.0f;
-  const int d = threadIdx.x;
-  for (int s = 0; s < ns; ++s) {
-    const float m = a.part_ml[(base + s) * 32 + 2 * hi];
-    if (m == -INFINITY) continue;
-    const float w = exp2f(m - M);
-    den += w * a.part_ml[(base + s) * 32 + 2 * hi + 1];
-    if (d < D) num += w * a.part_o[((base + s) * 16 + hi) * D + d];
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, ml[32 * s]);
+  M = wave_max(M);
+  float den = 0.0f;
+  for (int s = lane; s < ns; s += 64) {
+    const float m = ml[32 * s];
+    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[32 * s + 1];
   }
-  if (d < D) out[(b * a.hq + h) * D + d] = f32_to_bf16(den > 0.0f ? num / den : 0.0f);
+  den = wave_sum(den);
+  const int d = threadIdx.x;
+  if (d < D) {
+    const float* po = a.part_o + (base * 16 + hi) * D + d;  // split s: po[16 D s]
+    float num = 0.0f;
+#pragma unroll 4
+    for (int s = 0; s < ns; ++s) {
+      const float m = ml[32 * s];
+      const float o = po[static_cast<int64_t>(16 * D) * s];
+      num += m == -INFINITY ? 0.0f : exp2f(m - M) * o;
+    }
+    out[(b * a.hq + h) * D + d] = f32_to_bf16(den > 0.0f ? num / den : 0.0f);
+  }
   if (lse && d == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
 
@@ -522,46 +535,39 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 // ============================================================================ MLA absorbed decode
-// Work: (sequence b, split of kMlaChunk tokens, group of kMlaHeads query heads); kMlaWaves waves of
-// kMlaHB 16-head MFMA column blocks each. All heads of the group share one latent tile, so each
-// latent row is fetched and converted once per group. Per head a wave holds Q^T (576 bf16) and
-// O^T (512 fp32), 12.5 registers per lane; the rest of a step fits in the remaining registers
-// because fragment batches are small and every LDS address is one of a few per-lane bases plus an
-// immediate offset.
+// Work: (sequence b, split of kMlaChunk tokens, group of 128 query heads) -> one workgroup of four
+// waves, one per SIMD; wave w owns heads 32w .. 32w + 31 of the group. All heads of the group share
+// one latent tile, so each latent row is fetched and converted once per group. A lane holds Q^T of
+// its head (576 bf16, the B operand of S^T: 144 VGPRs) and that head's O^T (512 fp32: 256
+// accumulators, which the allocator places in AGPRs).
 // Per 32-token step s (one workgroup barrier):
 //   - raw rows (int8 latent 512 B, bf16 rope key 128 B, fp32 scale) go global -> LDS with
 //     global_load_lds through a four-stage ring, three steps ahead of their use;
-//   - the workgroup converts step s + 1's int8 latent to bf16 (exact) into the other half of a
-//     double-buffered tile while step s is computed from the first;
-//   - S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (rows = 16 tokens, columns = 16 heads); nope and
-//     rope parts stay apart so the per-token scale multiplies only the first:
+//   - the workgroup converts step s + 1 into the other half of a double-buffered bf16 tile (the
+//     int8 latent -> bf16 conversion is exact; rope rows and scales are copied alongside) while
+//     step s is computed from the first;
+//   - S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (rows = 32 tokens, columns = 32 heads); nope and
+//     rope parts accumulate apart so the per-token scale multiplies only the first:
 //     S = (q_nope . int8) * scale + q_rope . k_rope;
-//   - O^T += C^T P'^T with P' = P * scale, so the MFMAs see the unscaled integers; C^T comes
-//     from the tile with ds_read_b64_tr_b16 and P'^T straight from the S^T registers.
-// LDS reads are inline asm with explicit waits (the compiler would otherwise drain the ring's
-// outstanding loads before each read).
+//   - O^T += C^T P'^T with P' = P * scale, so the MFMAs see the unscaled integers. A lane's S^T
+//     values are the tokens 8i + 4h + r (h = lane / 32) of its head; the PV MFMAs order their k
+//     slots the same way, so P'^T comes straight from the S^T registers and C^T is read in that
+//     order with ds_read_b64_tr_b16.
+// LDS accesses are inline asm with explicit waits (the compiler would otherwise drain the ring's
+// outstanding global -> LDS loads before each access). The step loop is unrolled twice so that
+// the tile of a step is an immediate offset.
 #ifndef TAI_MLA_CHUNK
 #define TAI_MLA_CHUNK 2048
 #endif
-#ifndef TAI_MLA_WAVES
-#define TAI_MLA_WAVES 8
-#endif
-#ifndef TAI_MLA_KB
-#define TAI_MLA_KB 3
-#endif
-#ifndef TAI_MLA_VB
-#define TAI_MLA_VB 2
-#endif
 constexpr int kMlaChunk = TAI_MLA_CHUNK;
 constexpr int kMlaStep = 32;
-constexpr int kMlaWaves = TAI_MLA_WAVES;        // 8 (two per SIMD, 16 heads each) or 4 (one per SIMD, 32 heads)
-constexpr int kMlaHB = 8 / kMlaWaves;           // 16-head column blocks per wave
-constexpr int kMlaHeads = 128;                  // heads per workgroup
+constexpr int kMlaWaves = 4;
+constexpr int kMlaHeads = 128;  // heads per workgroup (32 per wave)
 constexpr int kMlaRing = 4;
-constexpr int kMlaKB = TAI_MLA_KB;  // K fragments per pipelined batch
-constexpr int kMlaVB = TAI_MLA_VB;  // V d blocks per pipelined batch (2 reads each)
+constexpr int kMlaKB = 2;           // K fragments per pipelined batch
+constexpr int kMlaVB = 4;           // V fragments per pipelined batch (two reads each)
 constexpr float kMlaSlack = 8.0f;   // log2-domain headroom of the lazily raised softmax max
-static_assert(kMlaWaves == 4 || kMlaWaves == 8, "MLA waves");
+constexpr float kMlaHeadroom = 64.0f;  // log2-domain headroom of the fast pass's fixed reference
 static_assert(kMlaChunk % kMlaStep == 0 && kMlaChunk <= 2048, "a split must span at most 64 pages of 32+ tokens");
 
 struct MlaArgs {
@@ -578,22 +584,26 @@ struct MlaArgs {
   float scale_log2;
   float* part_o;   // [b, nsplit, hq, DN]
   float* part_ml;  // [b, nsplit, hq, 2]
+  int32_t* flags;  // per workgroup of the fast pass: 1 = its split needs the rescaling pass
 };
 
-// Raw ring stage: [latent 32 x 512 B][rope 32 x 128 B][4 x 256 B scale slots]; bf16 tiles 2 x 32 x 1 KB.
-// Tile chunk c of row r sits at chunk c ^ X(r), X(r) = ((r & 7) << 1) | ((r >> 3) & 1): 16 rows at
-// one chunk hit 16 distinct 16-byte bank groups, and so do 4 consecutive rows x 2 chunks (the
-// transposing reads). X only moves the low four bits, so chunk 16q + c' is 256 q bytes past
-// chunk c' ^ X(r). Rope chunk c of row r sits at c ^ ((r >> 1) & 7).
+// Raw ring stage: [latent 32 x 512 B][rope 32 x 128 B][one 256 B scale slot per wave].
+// bf16 tile: [latent 32 x 1 KB][rope 32 x 128 B][scale 32 x 4 B].
+// Latent chunk c of tile row r sits at chunk c ^ X(r), X(r) = ((r & 7) << 1) | ((r >> 3) & 1): 16
+// rows at one chunk hit 16 distinct 16-byte bank groups, and so do 4 consecutive rows x 2 chunks
+// (the transposing reads). X only moves the low four bits, so chunk 16q + c' is 256 q bytes past
+// chunk c' ^ X(r), and X(r + 16) = X(r). Rope chunk c of row r (raw and tile) sits at c ^ ((r >> 1) & 7).
 constexpr int kMlaLatBytes = kMlaStep * 512;
 constexpr int kMlaRopeOff = kMlaLatBytes;
 constexpr int kMlaScaleOff = kMlaRopeOff + kMlaStep * 128;
-constexpr int kMlaRaw = kMlaScaleOff + 4 * 256;
-constexpr int kMlaTile = kMlaStep * 1024;
+constexpr int kMlaRaw = kMlaScaleOff + kMlaWaves * 256;
+constexpr int kMlaTRope = kMlaStep * 1024;
+constexpr int kMlaTScale = kMlaTRope + kMlaStep * 128;
+constexpr int kMlaTile = kMlaTScale + kMlaStep * 4;
 constexpr int kMlaLds = kMlaRing * kMlaRaw + 2 * kMlaTile;
+static_assert(kMlaLds <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ int mla_x(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
-__device__ __forceinline__ int mla_tile_off(int row, int c) { return row * 1024 + 16 * (c ^ mla_x(row)); }
 
 template <class F, int... I>
 __device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
@@ -617,22 +627,32 @@ template <int IMM>
 __device__ __forceinline__ void lds_read_tr16(v2i_t& d, uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
 }
+template <int IMM>
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, const v4i_t& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(v), "n"(IMM) : "memory");
+}
+// O^T += A B with the accumulator pinned to AGPRs. The compiler does not see the MFMA's latency:
+// code that reads the accumulator with VALU ops must first wait it out (mfma_drain).
+__device__ __forceinline__ void mfma_agpr(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Longer than the worst-case latency of one 32x32x16 MFMA (16 passes).
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
 template <int N>
 __device__ __forceinline__ void lds_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int DN, int DR>
-__global__ __launch_bounds__(64 * kMlaWaves) __attribute__((amdgpu_waves_per_eu(kMlaWaves / 4, kMlaWaves / 4)))
+template <int DN, int DR, bool RESCALE>
+__global__ __launch_bounds__(64 * kMlaWaves) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void mla_decode_kernel(MlaArgs a) {
   static_assert(DN == 512 && DR == 64, "MLA shape");
-  constexpr int DK = DN + DR;
-  constexpr int NM = DK / 32;  // 32-wide d blocks of S (16 nope + 2 rope)
-  constexpr int HB = kMlaHB;
+  constexpr int NQ = (DN + DR) / 16;  // Q^T fragments: 32 nope + 4 rope
+  constexpr int NN = DN / 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hcol = lane & 15, kg = lane >> 4, j = lane & 15;
+  const int col = lane & 31, h = lane >> 5;
   const int64_t blk = blockIdx.x;
   const int hg = static_cast<int>(blk % a.hgroups);
   const int split = static_cast<int>((blk / a.hgroups) % a.nsplit);
@@ -640,64 +660,55 @@ void mla_decode_kernel(MlaArgs a) {
   const int64_t L = a.lens[b];
   const int64_t t_begin = static_cast<int64_t>(split) * kMlaChunk;
   const int64_t t_end = min<int64_t>(L, t_begin + kMlaChunk);
-  int head[HB];
-  bool head_ok[HB];
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    head[hb] = hg * kMlaHeads + (w * HB + hb) * 16 + hcol;
-    head_ok[hb] = head[hb] < a.hq;
-  }
+  const int head = hg * kMlaHeads + 32 * w + col;
+  const bool head_ok = head < a.hq;
   const int64_t pbase = (b * a.nsplit + split) * a.hq;
+  if constexpr (RESCALE) {
+    if (a.flags[blk] == 0) return;  // the fast pass finished this workgroup's split
+  }
   if (t_begin >= t_end) {
-#pragma unroll
-    for (int hb = 0; hb < HB; ++hb)
-      if (kg == 0 && head_ok[hb]) { a.part_ml[(pbase + head[hb]) * 2] = -INFINITY; a.part_ml[(pbase + head[hb]) * 2 + 1] = 0.0f; }
+    if (h == 0 && head_ok) { a.part_ml[(pbase + head) * 2] = -INFINITY; a.part_ml[(pbase + head) * 2 + 1] = 0.0f; }
+    if (!RESCALE && tid == 0) a.flags[blk] = 0;
     return;
   }
-  // Q^T fragments (B operand): head = 16hb + hcol, d slots 32m + 8kg .. +8 (m < 16 nope, else rope)
-  bf16x8 qf[HB][NM];
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    const int hh = head_ok[hb] ? head[hb] : 0;
+  // Q^T fragments (B operand): column = this lane's head, k slots = d 16m + 8h .. +8
+  bf16x8 qf[NQ];
+  {
+    const int hh = head_ok ? head : 0;
     const uint16_t* qnp = a.qn + (b * a.hq + hh) * DN;
     const uint16_t* qrp = a.qr + (b * a.hq + hh) * DR;
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const int d = 32 * m + 8 * kg;
+    for (int m = 0; m < NQ; ++m) {
+      const int d = 16 * m + 8 * h;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (head_ok[hb]) v = d < DN ? *reinterpret_cast<const uint4*>(qnp + d) : *reinterpret_cast<const uint4*>(qrp + d - DN);
-      qf[hb][m] = as_bf16x8(v);
+      if (head_ok) v = m < NN ? *reinterpret_cast<const uint4*>(qnp + d) : *reinterpret_cast<const uint4*>(qrp + d - DN);
+      qf[m] = as_bf16x8(v);
     }
   }
-  f32x4 acc[HB][DN / 16];
+  // O^T accumulators, defined (as zeros) by an MFMA so that they live in AGPRs from the start
+  f32x16 acc[DN / 32];
+  {
+    const bf16x8 z = as_bf16x8(make_uint4(0, 0, 0, 0));
 #pragma unroll
-  for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-    for (int i = 0; i < DN / 16; ++i) acc[hb][i] = f32x4{0, 0, 0, 0};
-  float m_run[HB], l_run[HB];
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) { m_run[hb] = -INFINITY; l_run[hb] = 0.0f; }
+    for (int dt = 0; dt < DN / 32; ++dt) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc[dt]) : "v"(z));
+  }
+  float m_run = -INFINITY, l_run = 0.0f;
 
-  // pages: a step lies inside one page (bs % 32 == 0, steps start at multiples of 32)
+  // pages of the split, one per lane: bs is a multiple of 32 and splits start at multiples of
+  // kMlaChunk <= 2048, so a split spans at most 64 pages; a step lies inside one page
   const int32_t* btrow = a.bt + b * a.max_blocks;
   const int bs = a.bs;
   const int64_t pg0 = t_begin / bs;
   const int off0 = static_cast<int>(t_begin - pg0 * bs);
-  // pages of the split, one per lane: bs is a multiple of 32 and splits start at multiples of
-  // kMlaChunk <= 2048, so a split spans at most 64 pages (bs = 32: exactly 2048 / 32)
   const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);
   const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
   const int n_local = static_cast<int>(t_end - t_begin);
   const int nsteps = (n_local + kMlaStep - 1) / kMlaStep;
 
-  // Every wave issues the same number of global_load_lds per step (uniform vmcnt): 16 / kMlaWaves
-  // latent instructions (2 rows of 512 B each), and a rope instruction (8 rows of 128 B) and/or a
-  // scale instruction into its own 256 B slot (slot 0 is the one read): with 4 waves each wave
-  // issues both, with 8 waves waves 0-3 the rope and waves 4-7 the scale.
-  constexpr int kLatPerWave = 16 / kMlaWaves;
-  constexpr int kRawLoads = kLatPerWave + (kMlaWaves == 4 ? 2 : 1);
-  const bool do_rope = kMlaWaves == 4 || w < 4;
-  const bool do_scale = kMlaWaves == 4 || w >= 4;
+  // Every wave issues the same number of global_load_lds per step, so one vmcnt fits all: four
+  // latent instructions (2 rows of 512 B each), one rope instruction (8 rows of 128 B) and one
+  // scale instruction into the wave's own 256 B slot (slot 0 is the one read).
+  constexpr int kRawLoads = 6;
   auto issue_raw = [&](int s) __attribute__((always_inline)) {
     char* st = smem + (s % kMlaRing) * kMlaRaw;
     const int x = s * kMlaStep + off0;
@@ -705,52 +716,53 @@ void mla_decode_kernel(MlaArgs a) {
     const int64_t tok0 = static_cast<int64_t>(__shfl(my_page, pi, 64)) * bs + (x - pi * bs);  // cache row
     const int last = n_local - 1 - s * kMlaStep;
 #pragma unroll
-    for (int i = 0; i < kLatPerWave; ++i) {
-      const int q = kLatPerWave * w + i;
+    for (int i = 0; i < 4; ++i) {
+      const int q = 4 * w + i;
       const int row = 2 * q + (lane >> 5);
       const int8_t* src = a.ckv + (tok0 + min(row, last)) * DN + 16 * (lane & 31);
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(st + q * 1024), 16, 0, 0);
     }
-    if (do_rope) {
-      const int row = 8 * (w & 3) + (lane >> 3);
+    {
+      const int row = 8 * w + (lane >> 3);
       const int c = (lane & 7) ^ ((row >> 1) & 7);
       const uint16_t* src = a.kr + (tok0 + min(row, last)) * DR + 8 * c;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(st + kMlaRopeOff + (w & 3) * 1024), 16, 0, 0);
+                                       (__attribute__((address_space(3))) void*)(st + kMlaRopeOff + w * 1024), 16, 0, 0);
     }
-    if (do_scale) {
+    {
       const float* src = a.cs + tok0 + min(lane & 31, last);
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(st + kMlaScaleOff + (w & 3) * 256), 4, 0, 0);
+                                       (__attribute__((address_space(3))) void*)(st + kMlaScaleOff + w * 256), 4, 0, 0);
     }
   };
 
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)smem));
   const uint32_t tiles = lds0 + kMlaRing * kMlaRaw;
-  char* tiles_p = smem + kMlaRing * kMlaRaw;
-  // int8 latent of raw step s -> bf16 tile t: a wave converts 32 / kMlaWaves rows in 8-byte units
-  // (16 lanes cover 128 contiguous source bytes and write 16 consecutive 16-byte chunks).
-  auto convert = [&](int s, int t) __attribute__((always_inline)) {
-    constexpr int RPW = kMlaStep / kMlaWaves, UPL = RPW * 64 / 64;  // 8-byte units per lane per row-set
+  // Raw step s -> bf16 tile t. Latent: 2048 units of 8 bytes, eight per thread: unit u is row
+  // 8w + 4(u / 4) + lane / 16, 8-byte source unit (= bf16 chunk) 16(u % 4) + lane % 16. Rope rows
+  // and scales are copied as they are (16 bytes per thread; scales by threads 0-7).
+  auto convert = [&](int s, auto t_c) __attribute__((always_inline)) {
+    constexpr int T = decltype(t_c)::value * kMlaTile;
     const uint32_t raw = lds0 + (s % kMlaRing) * kMlaRaw;
-    char* tp = tiles_p + t * kMlaTile;
-    v2i_t r[UPL];
-    // unit u of a lane: row RPW w + (u / 4), source bytes 8 (16 (u % 4) + (lane & 15)) ...; lanes
-    // 16..63 take rows +1 .. +3 via the row offset below
-    const int rsub = lane >> 4;  // 0..3
+    const int rsub = lane >> 4;
+    v2i_t r[8];
+    v4i_t rope, scl;
 #pragma unroll
-    for (int u = 0; u < UPL; ++u) {
-      const int row = RPW * w + 4 * (u / 4) + rsub;
-      const int c = 16 * (u % 4) + (lane & 15);  // 8-byte source unit = bf16 chunk index
+    for (int u = 0; u < 8; ++u) {
+      const int row = 8 * w + 4 * (u / 4) + rsub;
+      const int c = 16 * (u % 4) + (lane & 15);
       asm volatile("ds_read_b64 %0, %1" : "=v"(r[u]) : "v"(raw + row * 512 + 8 * c));
     }
+    lds_read_b128<kMlaRopeOff>(rope, raw + 16 * tid);
+    lds_read_b128<kMlaScaleOff>(scl, raw + 16 * (tid & 7));
     lds_wait<0>();
 #pragma unroll
-    for (int u = 0; u < UPL; ++u) asm volatile("" : "+v"(r[u]));
+    for (int u = 0; u < 8; ++u) asm volatile("" : "+v"(r[u]));
+    asm volatile("" : "+v"(rope), "+v"(scl));
 #pragma unroll
-    for (int u = 0; u < UPL; ++u) {
-      const int row = RPW * w + 4 * (u / 4) + rsub;
+    for (int u = 0; u < 8; ++u) {
+      const int row = 8 * w + 4 * (u / 4) + rsub;
       const int c = 16 * (u % 4) + (lane & 15);
       uint32_t o[4];
 #pragma unroll
@@ -763,54 +775,68 @@ void mla_decode_kernel(MlaArgs a) {
         o[2 * q] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
         o[2 * q + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
       }
-      *reinterpret_cast<uint4*>(tp + mla_tile_off(row, c)) = make_uint4(o[0], o[1], o[2], o[3]);
+      lds_write_b128<T>(tiles + row * 1024 + 16 * (c ^ mla_x(row)),
+                        v4i_t{static_cast<int>(o[0]), static_cast<int>(o[1]), static_cast<int>(o[2]), static_cast<int>(o[3])});
     }
+    lds_write_b128<T>(tiles + kMlaTRope + 16 * tid, rope);
+    if (tid < 8) lds_write_b128<T>(tiles + kMlaTScale + 16 * tid, scl);
   };
-  // Per-lane LDS bases (tile 0; tile 1 is kMlaTile further). K (nope) fragment (tb, m): row
-  //   16tb + hcol, chunk 4m + kg -> kb[m & 3] + 16384 tb + 256 (m >> 2). Rope fragment (tb, m'):
-  //   row 16tb + hcol -> raw + rb[m'] + 2048 tb. V^T halves for d block dt: rows 4kg + j/4 (+16),
-  //   columns 16dt + 4 (j & 3) .. +4 -> vb[dt & 7] + 256 (dt >> 3) (+ 16384).
-  uint32_t kb[4], rb[2], vb[8];
+
+  // Per-lane LDS bases (tile 0; tile 1 is kMlaTile further, an immediate).
+  //   K (nope) fragment m: row col, chunk 2m + h -> kb[m & 7] + 256 (m >> 3).
+  //   Rope fragment q: row col, chunk 2q + h of the 128-byte rope row -> rb[q].
+  //   C^T fragment (dt, kk): lane group g = lane / 16, j = lane % 16; the two transposing reads
+  //   address rows 16kk + 4h + j / 4 (+ 8) at bf16 column 32dt + 16(g & 1) + 4(j & 3)
+  //   -> vb[half][dt & 3] + 256 (dt >> 2) + 16384 kk.
+  uint32_t kb[8], rb[4], vb[2][4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) kb[q] = tiles + hcol * 1024 + 16 * ((4 * q + kg) ^ mla_x(hcol));
+  for (int q = 0; q < 8; ++q) kb[q] = tiles + col * 1024 + 16 * ((2 * q + h) ^ mla_x(col));
 #pragma unroll
-  for (int q = 0; q < 2; ++q) rb[q] = kMlaRopeOff + hcol * 128 + 16 * ((4 * q + kg) ^ ((hcol >> 1) & 7));
+  for (int q = 0; q < 4; ++q) rb[q] = tiles + kMlaTRope + col * 128 + 16 * ((2 * q + h) ^ ((col >> 1) & 7));
   {
-    const int r_lo = 4 * kg + (j >> 2), h = (j >> 1) & 1;
+    const int g = lane >> 4, j = lane & 15;
+    const int cp = 2 * (g & 1) + ((j >> 1) & 1);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) vb[q] = tiles + r_lo * 1024 + 16 * ((2 * q + h) ^ mla_x(r_lo)) + 8 * (j & 1);
+    for (int half = 0; half < 2; ++half) {
+      const int row = 4 * h + (j >> 2) + 8 * half;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) vb[half][q] = tiles + row * 1024 + 16 * ((4 * q + cp) ^ mla_x(row)) + 8 * (j & 1);
+    }
   }
 
-  // ---- per-step pieces -------------------------------------------------------------------
-  f32x4 sn[2][HB], sr[2][HB];
-  float sv[HB][2][4];
-  f32x4 cs0, cs1;
-  float m_cand[HB];
-  uint32_t raw = 0, toff = 0;
-
-  // front: ring wait, the barrier, the next step's conversion, S^T and the step's maxima
-  auto front = [&](int s) __attribute__((always_inline)) {
+  f32x16 sn;      // S^T of the current step (then the log2-domain logits)
+  f32x4 cs[4];    // per-token scales of the lane's tokens
+  float mx = 0.0f;
+  // front: ring wait, the barrier, the next step's conversion, S^T and the step's max
+  auto front = [&](int s, auto t_c) __attribute__((always_inline)) {
+    constexpr int T = decltype(t_c)::value * kMlaTile;
     // raw(s + 1) must have landed (for the conversion); raw(s + 2) may stay in flight
     if (s + 2 < nsteps) __builtin_amdgcn_s_waitcnt(kRawLoads | 0x70 | 0xF00);
     else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
-    // every wave's raw(s + 1) has landed, tile s & 1 is converted, and every wave is done with
-    // step s - 1 (its tile and raw slot are free)
+    // every wave's raw(s + 1) has landed, tile s is converted, and every wave is done with step
+    // s - 1 (its tile and raw slot are free)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (s + 3 < nsteps) issue_raw(s + 3);
-    if (s + 1 < nsteps) convert(s + 1, (s + 1) & 1);
-    raw = lds0 + (s % kMlaRing) * kMlaRaw;
-    toff = (s & 1) * kMlaTile;
-    // S^T: 36 fragments f = 18 tb + m in batches of kMlaKB, the next batch in flight
+    if (s + 1 < nsteps) convert(s + 1, std::integral_constant<int, 1 - decltype(t_c)::value>{});
+    // ---- per-token scales of this lane's tokens 8i + 4h + r
+    static_for<4>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      lds_read_b128<T + 32 * i>(*reinterpret_cast<v4i_t*>(&cs[i]), tiles + kMlaTScale + 16 * h);
+    });
+    lds_wait<0>();
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(cs[i]));
+    // ---- S^T: 36 fragments in batches of kMlaKB, the next batch in flight; S^T = (K_nope Q_nope^T)
+    //      * scale + K_rope Q_rope^T, the rope MFMAs accumulating onto the scaled nope part
 #pragma unroll
-      for (int hb = 0; hb < HB; ++hb) { sn[tb][hb] = f32x4{0, 0, 0, 0}; sr[tb][hb] = f32x4{0, 0, 0, 0}; }
-    constexpr int NKF = 2 * NM, NKB = (NKF + kMlaKB - 1) / kMlaKB;
+    for (int r = 0; r < 16; ++r) sn[r] = 0.0f;
+    constexpr int NKB = NQ / kMlaKB;
+    static_assert(NQ % kMlaKB == 0, "K batches");
     v4i_t kf[2][kMlaKB];
     auto kread = [&](auto f_c, v4i_t& d) __attribute__((always_inline)) {
-      constexpr int f = decltype(f_c)::value, tb = f / NM, m = f % NM;
-      if constexpr (m < DN / 32) lds_read_b128<16384 * tb + 256 * (m >> 2)>(d, kb[m & 3] + toff);
-      else lds_read_b128<2048 * tb>(d, raw + rb[m - DN / 32]);
+      constexpr int m = decltype(f_c)::value;
+      if constexpr (m < NN) lds_read_b128<T + 256 * (m >> 3)>(d, kb[m & 7]);
+      else lds_read_b128<T>(d, rb[m - NN]);
     };
     static_for<kMlaKB>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -818,94 +844,74 @@ void mla_decode_kernel(MlaArgs a) {
     });
     static_for<NKB>([&](auto bi_c) {
       constexpr int bi = decltype(bi_c)::value, cur = bi & 1;
-      constexpr int nnext = (bi + 1 < NKB) ? (NKF - (bi + 1) * kMlaKB < kMlaKB ? NKF - (bi + 1) * kMlaKB : kMlaKB) : 0;
-      if constexpr (nnext > 0) {
-        static_for<nnext>([&](auto i_c) {
+      if constexpr (bi + 1 < NKB) {
+        static_for<kMlaKB>([&](auto i_c) {
           constexpr int i = decltype(i_c)::value;
           kread(std::integral_constant<int, (bi + 1) * kMlaKB + i>{}, kf[cur ^ 1][i]);
         });
+        lds_wait<kMlaKB>();
+      } else {
+        lds_wait<0>();
       }
-      lds_wait<nnext>();
       static_for<kMlaKB>([&](auto i_c) {
-        constexpr int i = decltype(i_c)::value, f = bi * kMlaKB + i;
-        if constexpr (f < NKF) {
-          asm volatile("" : "+v"(kf[cur][i]));
-          constexpr int tb = f / NM, m = f % NM;
-          const bf16x8 kv = __builtin_bit_cast(bf16x8, kf[cur][i]);
+        constexpr int i = decltype(i_c)::value, m = bi * kMlaKB + i;
+        asm volatile("" : "+v"(kf[cur][i]));
+        const bf16x8 kv = __builtin_bit_cast(bf16x8, kf[cur][i]);
+        if constexpr (m == NN) {  // nope part complete: scale it, then add the rope part
 #pragma unroll
-          for (int hb = 0; hb < HB; ++hb) {
-            if constexpr (m < DN / 32) sn[tb][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qf[hb][m], sn[tb][hb], 0, 0, 0);
-            else sr[tb][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qf[hb][m], sr[tb][hb], 0, 0, 0);
-          }
+          for (int e = 0; e < 16; ++e) sn[e] *= cs[e >> 2][e & 3];
         }
+        sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[m], sn, 0, 0, 0);
       });
     });
-    // per-token scales of this lane's tokens: 4kg + r and 16 + 4kg + r (slot 0)
-    lds_read_b128<0>(*reinterpret_cast<v4i_t*>(&cs0), raw + kMlaScaleOff + 16 * kg);
-    lds_read_b128<64>(*reinterpret_cast<v4i_t*>(&cs1), raw + kMlaScaleOff + 16 * kg);
-    lds_wait<0>();
-    asm volatile("" : "+v"(cs0), "+v"(cs1));
+    // ---- logits
     const int64_t t0 = t_begin + static_cast<int64_t>(s) * kMlaStep;
+    mx = -INFINITY;
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      float mx = -INFINITY;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = 16 * tb + 4 * kg + r;
-          const float c = tb ? cs1[r] : cs0[r];
-          const float v = (t0 + tok < t_end) ? (sn[tb][hb][r] * c + sr[tb][hb][r]) * a.scale_log2 : -INFINITY;
-          sv[hb][tb][r] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      m_cand[hb] = mx;  // finite: every step holds a valid token
-    }
+      for (int r = 0; r < 4; ++r) {
+        const float v = (t0 + 8 * i + 4 * h + r < t_end) ? sn[4 * i + r] * a.scale_log2 : -INFINITY;
+        sn[4 * i + r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // finite: every step holds a valid token
   };
-  auto need_raise = [&]() __attribute__((always_inline)) {
-    bool r = false;
-#pragma unroll
-    for (int hb = 0; hb < HB; ++hb) r = r || m_cand[hb] > m_run[hb] + kMlaSlack;
-    return __any(r);  // wave-uniform
-  };
-  // rescale: raise the reference max to the step's and rescale O^T and l (rare)
+  // Online softmax with a lazily raised reference max: m_run moves (and O^T is rescaled) only
+  // when the step's max exceeds it by more than kMlaSlack in the log2 domain, so
+  // P' <= 2^kMlaSlack * scale between raises; the result is the same. Code that rescales O^T in
+  // place makes the register allocator spill (it moves the AGPR accumulators through VGPRs), so
+  // only the rescaling pass carries it.
+  auto need_raise = [&]() __attribute__((always_inline)) { return __any(mx > m_run + kMlaSlack); };
   auto rescale = [&]() __attribute__((always_inline)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+    mfma_drain();
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      const float m_new = fmaxf(m_run[hb], m_cand[hb]);
-      const float alpha = (m_run[hb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[hb] - m_new);
-      l_run[hb] *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DN / 16; ++dt) acc[hb][dt] *= alpha;
-      m_run[hb] = m_new;
-    }
+    for (int dt = 0; dt < DN / 32; ++dt) acc[dt] *= alpha;
+    m_run = m_new;
   };
-  // back: P' = exp2(S - m) * scale, l, and O^T += C^T P'^T (V batches of kMlaVB d blocks)
-  auto back = [&]() __attribute__((always_inline)) {
-    bf16x8 pf[HB];
+  // back: P' = exp2(S - m) * scale, l, and O^T += C^T P'^T
+  auto back = [&](auto t_c) __attribute__((always_inline)) {
+    constexpr int T = decltype(t_c)::value * kMlaTile;
+    bf16x8 pf[2];
+    float rs = 0.0f;
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      float rs = 0.0f;
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = __builtin_amdgcn_exp2f(sv[hb][tb][r] - m_run[hb]);
-          rs += e;
-          pf[hb][4 * tb + r] = static_cast<__bf16>(e * (tb ? cs1[r] : cs0[r]));
-        }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l_run[hb] += rs;
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sn[e] - m_run);
+      rs += p;
+      pf[e >> 3][e & 7] = static_cast<__bf16>(p * cs[e >> 2][e & 3]);
     }
-    constexpr int NVB = (DN / 16) / kMlaVB;
+    rs += __shfl_xor(rs, 32, 64);
+    l_run += rs;
+    // ---- O^T += C^T P'^T: fragment f = 16 kk + dt, batches of kMlaVB
+    constexpr int NVF = 2 * (DN / 32), NVB = NVF / kMlaVB;
     v2i_t vlo[2][kMlaVB], vhi[2][kMlaVB];
-    auto vread = [&](auto dt_c, v2i_t& lo, v2i_t& hi) __attribute__((always_inline)) {
-      constexpr int dt = decltype(dt_c)::value;
-      lds_read_tr16<256 * (dt >> 3)>(lo, vb[dt & 7] + toff);
-      lds_read_tr16<256 * (dt >> 3) + 16384>(hi, vb[dt & 7] + toff);
+    auto vread = [&](auto f_c, v2i_t& lo, v2i_t& hi) __attribute__((always_inline)) {
+      constexpr int f = decltype(f_c)::value, kk = f / (DN / 32), dt = f % (DN / 32);
+      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(lo, vb[0][dt & 3]);
+      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(hi, vb[1][dt & 3]);
     };
     static_for<kMlaVB>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -923,16 +929,15 @@ void mla_decode_kernel(MlaArgs a) {
         lds_wait<0>();
       }
       static_for<kMlaVB>([&](auto i_c) {
-        constexpr int i = decltype(i_c)::value, dt = bi * kMlaVB + i;
+        constexpr int i = decltype(i_c)::value, f = bi * kMlaVB + i, kk = f / (DN / 32), dt = f % (DN / 32);
         asm volatile("" : "+v"(vlo[cur][i]), "+v"(vhi[cur][i]));
         const bf16x8 vv = __builtin_bit_cast(bf16x8, v4i_t{vlo[cur][i][0], vlo[cur][i][1], vhi[cur][i][0], vhi[cur][i][1]});
-#pragma unroll
-        for (int hb = 0; hb < HB; ++hb) acc[hb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pf[hb], acc[hb][dt], 0, 0, 0);
+        mfma_agpr(acc[dt], vv, pf[kk]);
       });
     });
   };
 
-  // prologue: three raw steps in flight, step 0 converted into tile 0 (the loop's first barrier
+  // prologue: three raw steps in flight, step 0 converted into tile 0 (the first step's barrier
   // publishes it)
   issue_raw(0);
   if (nsteps > 1) issue_raw(1);
@@ -940,40 +945,55 @@ void mla_decode_kernel(MlaArgs a) {
   if (nsteps > 2) __builtin_amdgcn_s_waitcnt((2 * kRawLoads) | 0x70 | 0xF00);
   else if (nsteps > 1) __builtin_amdgcn_s_waitcnt(kRawLoads | 0x70 | 0xF00);
   else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
+  if (!RESCALE && tid == 0) a.flags[blk] = 0;  // ordered before any wave's 1 by the barriers
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  convert(0, 0);
-  // Online softmax with a lazily raised reference max: m_run moves (and O^T is rescaled, which
-  // pulls the accumulators through VGPRs) only when the step's max exceeds it by more than
-  // kMlaSlack in the log2 domain, so P' <= 2^kMlaSlack * scale between raises; the result is the
-  // same. The rescale sits outside the steady-state loop: inside it, its join would make the
-  // register allocator move the accumulators on every step.
-  int s = 0;
-  while (true) {
-    for (; s < nsteps; ++s) {
-      front(s);
-      if (need_raise()) break;
-      back();
+  convert(0, std::integral_constant<int, 0>{});
+  const std::integral_constant<int, 0> t0c;
+  const std::integral_constant<int, 1> t1c;
+  // The fast pass (RESCALE = false) keeps the first step's max as the reference for the whole
+  // split and never touches O^T in between: P' <= 2^kMlaHeadroom * scale keeps O^T and l far from
+  // fp32 overflow (2048 tokens x 127 x 2^64). A split whose logits rise further is flagged and
+  // redone by the rescaling pass, which raises the reference as above.
+  bool overflow = false;
+  auto settle = [&]() __attribute__((always_inline)) {
+    if constexpr (RESCALE) {
+      if (need_raise()) rescale();
+    } else {
+      if (m_run == -INFINITY) m_run = mx;  // first step: O^T and l are still zero
+      else overflow = overflow || (mx > m_run + kMlaHeadroom);
     }
-    if (s >= nsteps) break;
-    rescale();
-    back();
-    ++s;
+  };
+  for (int s = 0; s < nsteps; s += 2) {
+    front(s, t0c);
+    settle();
+    back(t0c);
+    if (s + 1 < nsteps) {
+      front(s + 1, t1c);
+      settle();
+      back(t1c);
+    }
   }
+  if constexpr (!RESCALE) {
+    if (__any(overflow) && lane == 0) a.flags[blk] = 1;
+  }
+  if (!head_ok) return;
+  mfma_drain();
+  // ---- partial: O^T[d = 32dt + 8i + 4h + r][head]
+  float* po = a.part_o + (pbase + head) * DN;
 #pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    if (!head_ok[hb]) continue;
-    // ---- partial: O^T[d = 16dt + 4kg + r][head]
-    float* po = a.part_o + (pbase + head[hb]) * DN;
+  for (int dt = 0; dt < DN / 32; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DN / 16; ++dt)
-      *reinterpret_cast<float4*>(po + 16 * dt + 4 * kg) = make_float4(acc[hb][dt][0], acc[hb][dt][1], acc[hb][dt][2], acc[hb][dt][3]);
-    if (kg == 0) {
-      a.part_ml[(pbase + head[hb]) * 2] = m_run[hb];
-      a.part_ml[(pbase + head[hb]) * 2 + 1] = l_run[hb];
-    }
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<float4*>(po + 32 * dt + 8 * i + 4 * h) =
+          make_float4(acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]);
+  if (h == 0) {
+    a.part_ml[(pbase + head) * 2] = m_run;
+    a.part_ml[(pbase + head) * 2 + 1] = l_run;
   }
 }
 
+// Merge the splits of one (b, head): 256 threads, DN / 256 outputs each. As in the GQA merge,
+// each wave reduces the split statistics itself and the numerator loop is branch free.
 template <int DN>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* out, float* lse) {
   const int64_t bh = blockIdx.x;
@@ -981,20 +1001,33 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   const int64_t b = bh / a.hq;
   const int64_t L = a.lens[b];
   const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kMlaChunk - 1) / kMlaChunk));
+  const int64_t pi0 = b * a.nsplit * a.hq + h;  // split s: pi0 + s * hq
+  const float* ml = a.part_ml + pi0 * 2;
+  const int64_t mls = 2 * static_cast<int64_t>(a.hq);
+  const int lane = threadIdx.x & 63;
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((b * a.nsplit + s) * a.hq + h) * 2]);
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, ml[mls * s]);
+  M = wave_max(M);
   float den = 0.0f;
+  for (int s = lane; s < ns; s += 64) {
+    const float m = ml[mls * s];
+    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[mls * s + 1];
+  }
+  den = wave_sum(den);
   float num[DN / 256];
 #pragma unroll
   for (int i = 0; i < DN / 256; ++i) num[i] = 0.0f;
+  const float* po = a.part_o + pi0 * DN + threadIdx.x;
+  const int64_t pos = static_cast<int64_t>(a.hq) * DN;
+#pragma unroll 4
   for (int s = 0; s < ns; ++s) {
-    const int64_t pi = (b * a.nsplit + s) * a.hq + h;
-    const float m = a.part_ml[pi * 2];
-    if (m == -INFINITY) continue;
-    const float wgt = exp2f(m - M);
-    den += wgt * a.part_ml[pi * 2 + 1];
+    const float m = ml[mls * s];
+    const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
 #pragma unroll
-    for (int i = 0; i < DN / 256; ++i) num[i] += wgt * a.part_o[pi * DN + threadIdx.x + 256 * i];
+    for (int i = 0; i < DN / 256; ++i) {
+      const float o = po[pos * s + 256 * i];
+      num[i] += m == -INFINITY ? 0.0f : wgt * o;
+    }
   }
 #pragma unroll
   for (int i = 0; i < DN / 256; ++i)
@@ -1002,8 +1035,10 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   if (lse && threadIdx.x == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
 
+// [part_o fp32 b x nsplit x hq x dn][part_ml fp32 b x nsplit x hq x 2][flags int32, one per workgroup]
 size_t mla_ws(int64_t b, int hq, int dn, int nsplit) {
-  return static_cast<size_t>(b) * nsplit * hq * (dn + 2) * sizeof(float);
+  const int64_t wgs = b * nsplit * ((hq + kMlaHeads - 1) / kMlaHeads);
+  return static_cast<size_t>(b) * nsplit * hq * (dn + 2) * sizeof(float) + static_cast<size_t>(wgs) * sizeof(int32_t);
 }
 }  // namespace
 }  // namespace tai
@@ -1132,10 +1167,13 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.nsplit = nsplit; a.hgroups = static_cast<int>(cdiv(hq, kMlaHeads)); a.scale_log2 = scale * kLog2e;
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + static_cast<size_t>(b) * nsplit * hq * dn;
+  a.flags = reinterpret_cast<int32_t*>(a.part_ml + static_cast<size_t>(b) * nsplit * hq * 2);
   hipStream_t st = static_cast<hipStream_t>(stream);
   static bool lds_set = false;
   if (!lds_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) != hipSuccess) {
       (void)hipGetLastError();
       set_error("tai_fia_mla_decode: the device cannot give a workgroup %d bytes of LDS", kMlaLds);
@@ -1143,7 +1181,11 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
     }
     lds_set = true;
   }
-  mla_decode_kernel<512, 64><<<dim3(static_cast<unsigned>(b * nsplit * a.hgroups)), 64 * kMlaWaves, kMlaLds, st>>>(a);
+  // fast pass over every split, then the rescaling pass over the splits it flagged (its other
+  // workgroups exit at once)
+  const dim3 grid(static_cast<unsigned>(b * nsplit * a.hgroups));
+  mla_decode_kernel<512, 64, false><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
+  mla_decode_kernel<512, 64, true><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
   mla_combine_kernel<512><<<dim3(static_cast<unsigned>(b * hq)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
   return launch_status("tai_fia_mla_decode");
 }
