@@ -633,9 +633,21 @@ __device__ __forceinline__ void lds_write_b128(uint32_t addr, const v4i_t& v) {
 }
 // O^T += A B with the accumulator pinned to AGPRs. The compiler does not see the MFMA's latency:
 // code that reads the accumulator with VALU ops must first wait it out (mfma_drain).
+// The leading s_nop covers a VALU write of an operand just before (the compiler does not track
+// hazards into inline asm).
 __device__ __forceinline__ void mfma_agpr(f32x16& acc, const bf16x8& a, const bf16x8& b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+// The same with the accumulator pinned to VGPRs (S^T, which VALU code reads): before a VALU read of
+// the result, mfma_vgpr_wait() covers the latency of the last MFMA (16 passes).
+__device__ __forceinline__ void mfma_vgpr(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_vgpr_zero(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_vgpr_wait() { asm volatile("s_nop 15\n\ts_nop 7" ::: "memory"); }
+
 // Longer than the worst-case latency of one 32x32x16 MFMA (16 passes).
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
 template <int N>
@@ -686,8 +698,13 @@ void mla_decode_kernel(MlaArgs a) {
     }
   }
   // O^T accumulators, defined (as zeros) by an MFMA so that they live in AGPRs from the start
+  // (The rescaling pass uses compiler-scheduled MFMAs throughout: it spills, and the compiler
+  // cannot see the hazards of inline-asm MFMAs around its spill code.)
   f32x16 acc[DN / 32];
-  {
+  if constexpr (RESCALE) {
+#pragma unroll
+    for (int dt = 0; dt < DN / 32; ++dt) acc[dt] = f32x16{};
+  } else {
     const bf16x8 z = as_bf16x8(make_uint4(0, 0, 0, 0));
 #pragma unroll
     for (int dt = 0; dt < DN / 32; ++dt) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc[dt]) : "v"(z));
@@ -709,29 +726,36 @@ void mla_decode_kernel(MlaArgs a) {
   // latent instructions (2 rows of 512 B each), one rope instruction (8 rows of 128 B) and one
   // scale instruction into the wave's own 256 B slot (slot 0 is the one read).
   constexpr int kRawLoads = 6;
+  // The step's cache row base is wave-uniform (scalar); per lane only a 32-bit offset is formed.
+  // The lane-dependent row numbers are recomputed from an opaque copy of the lane id at every
+  // step: hoisted out of the loop they would be spilled, and a scratch reload waits on vmcnt,
+  // which would drain the ring.
   auto issue_raw = [&](int s) __attribute__((always_inline)) {
     char* st = smem + (s % kMlaRing) * kMlaRaw;
     const int x = s * kMlaStep + off0;
     const int pi = x / bs;
-    const int64_t tok0 = static_cast<int64_t>(__shfl(my_page, pi, 64)) * bs + (x - pi * bs);  // cache row
+    const int page = __builtin_amdgcn_readfirstlane(__shfl(my_page, pi, 64));
+    const int64_t tok0 = static_cast<int64_t>(page) * bs + (x - pi * bs);  // cache row of the step
     const int last = n_local - 1 - s * kMlaStep;
+    int ln;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+    const int8_t* lat = a.ckv + tok0 * DN;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = 4 * w + i;
-      const int row = 2 * q + (lane >> 5);
-      const int8_t* src = a.ckv + (tok0 + min(row, last)) * DN + 16 * (lane & 31);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+      const int row = 2 * q + (ln >> 5);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(lat + min(row, last) * DN + 16 * (ln & 31)),
                                        (__attribute__((address_space(3))) void*)(st + q * 1024), 16, 0, 0);
     }
     {
-      const int row = 8 * w + (lane >> 3);
-      const int c = (lane & 7) ^ ((row >> 1) & 7);
-      const uint16_t* src = a.kr + (tok0 + min(row, last)) * DR + 8 * c;
+      const int row = 8 * w + (ln >> 3);
+      const int c = (ln & 7) ^ ((row >> 1) & 7);
+      const uint16_t* src = a.kr + tok0 * DR + min(row, last) * DR + 8 * c;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(st + kMlaRopeOff + w * 1024), 16, 0, 0);
     }
     {
-      const float* src = a.cs + tok0 + min(lane & 31, last);
+      const float* src = a.cs + tok0 + min(ln & 31, last);
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(st + kMlaScaleOff + w * 256), 4, 0, 0);
     }
@@ -783,26 +807,29 @@ void mla_decode_kernel(MlaArgs a) {
   };
 
   // Per-lane LDS bases (tile 0; tile 1 is kMlaTile further, an immediate).
-  //   K (nope) fragment m: row col, chunk 2m + h -> kb[m & 7] + 256 (m >> 3).
-  //   Rope fragment q: row col, chunk 2q + h of the 128-byte rope row -> rb[q].
+  //   K (nope) fragment m: row col, chunk 2m + h -> kb(m & 7) + 256 (m >> 3).
+  //   Rope fragment q: row col, chunk 2q + h of the 128-byte rope row -> rb(q).
   //   C^T fragment (dt, kk): lane group g = lane / 16, j = lane % 16; the two transposing reads
   //   address rows 16kk + 4h + j / 4 (+ 8) at bf16 column 32dt + 16(g & 1) + 4(j & 3)
-  //   -> vb[half][dt & 3] + 256 (dt >> 2) + 16384 kk.
-  uint32_t kb[8], rb[4], vb[2][4];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) kb[q] = tiles + col * 1024 + 16 * ((2 * q + h) ^ mla_x(col));
-#pragma unroll
-  for (int q = 0; q < 4; ++q) rb[q] = tiles + kMlaTRope + col * 128 + 16 * ((2 * q + h) ^ ((col >> 1) & 7));
+  //   -> vb(half, dt & 3) + 256 (dt >> 2) + 16384 kk.
+  // Each family of bases is one row base plus a per-lane XOR pattern: chunk (2q + h) ^ X equals
+  // 2q ^ (h ^ X), so the address of fragment q is base + (pattern ^ 32q) (one v_xad per read).
+  const uint32_t k_row = tiles + col * 1024, k_pat = 16 * (h ^ mla_x(col));
+  const uint32_t r_row = tiles + kMlaTRope + col * 128, r_pat = 16 * (h ^ ((col >> 1) & 7));
+  uint32_t v_row[2], v_pat[2];
   {
     const int g = lane >> 4, j = lane & 15;
     const int cp = 2 * (g & 1) + ((j >> 1) & 1);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int row = 4 * h + (j >> 2) + 8 * half;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) vb[half][q] = tiles + row * 1024 + 16 * ((4 * q + cp) ^ mla_x(row)) + 8 * (j & 1);
+      v_row[half] = tiles + row * 1024 + 8 * (j & 1);
+      v_pat[half] = 16 * (cp ^ mla_x(row));
     }
   }
+  auto kb = [&](int q) -> uint32_t { return k_row + (k_pat ^ (32u * q)); };
+  auto rb = [&](int q) -> uint32_t { return r_row + (r_pat ^ (32u * q)); };
+  auto vb = [&](int half, int q) -> uint32_t { return v_row[half] + (v_pat[half] ^ (64u * q)); };
 
   f32x16 sn;      // S^T of the current step (then the log2-domain logits)
   f32x4 cs[4];    // per-token scales of the lane's tokens
@@ -828,15 +855,13 @@ void mla_decode_kernel(MlaArgs a) {
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(cs[i]));
     // ---- S^T: 36 fragments in batches of kMlaKB, the next batch in flight; S^T = (K_nope Q_nope^T)
     //      * scale + K_rope Q_rope^T, the rope MFMAs accumulating onto the scaled nope part
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sn[r] = 0.0f;
     constexpr int NKB = NQ / kMlaKB;
     static_assert(NQ % kMlaKB == 0, "K batches");
     v4i_t kf[2][kMlaKB];
     auto kread = [&](auto f_c, v4i_t& d) __attribute__((always_inline)) {
       constexpr int m = decltype(f_c)::value;
-      if constexpr (m < NN) lds_read_b128<T + 256 * (m >> 3)>(d, kb[m & 7]);
-      else lds_read_b128<T>(d, rb[m - NN]);
+      if constexpr (m < NN) lds_read_b128<T + 256 * (m >> 3)>(d, kb(m & 7));
+      else lds_read_b128<T>(d, rb(m - NN));
     };
     static_for<kMlaKB>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -858,13 +883,20 @@ void mla_decode_kernel(MlaArgs a) {
         asm volatile("" : "+v"(kf[cur][i]));
         const bf16x8 kv = __builtin_bit_cast(bf16x8, kf[cur][i]);
         if constexpr (m == NN) {  // nope part complete: scale it, then add the rope part
+          if constexpr (!RESCALE) mfma_vgpr_wait();
 #pragma unroll
           for (int e = 0; e < 16; ++e) sn[e] *= cs[e >> 2][e & 3];
         }
-        sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[m], sn, 0, 0, 0);
+        if constexpr (RESCALE) {
+          sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[m], m == 0 ? f32x16{} : sn, 0, 0, 0);
+        } else {
+          if constexpr (m == 0) mfma_vgpr_zero(sn, kv, qf[m]);
+          else mfma_vgpr(sn, kv, qf[m]);
+        }
       });
     });
     // ---- logits
+    if constexpr (!RESCALE) mfma_vgpr_wait();
     const int64_t t0 = t_begin + static_cast<int64_t>(s) * kMlaStep;
     mx = -INFINITY;
 #pragma unroll
@@ -910,8 +942,8 @@ void mla_decode_kernel(MlaArgs a) {
     v2i_t vlo[2][kMlaVB], vhi[2][kMlaVB];
     auto vread = [&](auto f_c, v2i_t& lo, v2i_t& hi) __attribute__((always_inline)) {
       constexpr int f = decltype(f_c)::value, kk = f / (DN / 32), dt = f % (DN / 32);
-      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(lo, vb[0][dt & 3]);
-      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(hi, vb[1][dt & 3]);
+      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(lo, vb(0, dt & 3));
+      lds_read_tr16<T + 256 * (dt >> 2) + 16384 * kk>(hi, vb(1, dt & 3));
     };
     static_for<kMlaVB>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -932,7 +964,8 @@ void mla_decode_kernel(MlaArgs a) {
         constexpr int i = decltype(i_c)::value, f = bi * kMlaVB + i, kk = f / (DN / 32), dt = f % (DN / 32);
         asm volatile("" : "+v"(vlo[cur][i]), "+v"(vhi[cur][i]));
         const bf16x8 vv = __builtin_bit_cast(bf16x8, v4i_t{vlo[cur][i][0], vlo[cur][i][1], vhi[cur][i][0], vhi[cur][i][1]});
-        mfma_agpr(acc[dt], vv, pf[kk]);
+        if constexpr (RESCALE) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, pf[kk], acc[dt], 0, 0, 0);
+        else mfma_agpr(acc[dt], vv, pf[kk]);
       });
     });
   };
@@ -977,7 +1010,7 @@ void mla_decode_kernel(MlaArgs a) {
     if (__any(overflow) && lane == 0) a.flags[blk] = 1;
   }
   if (!head_ok) return;
-  mfma_drain();
+  if constexpr (!RESCALE) mfma_drain();
   // ---- partial: O^T[d = 32dt + 8i + 4h + r][head]
   float* po = a.part_o + (pbase + head) * DN;
 #pragma unroll
