@@ -198,13 +198,15 @@ def test_mla_cfg5():
 
 
 def test_mla_rising_logits_take_the_rescaling_pass():
-    # Rope keys of sequence 0 jump by ~100 (log2 units) after its first two pages: the fast pass
-    # flags those splits and the rescaling pass redoes them; the other sequences stay on the fast pass.
-    lens, h, bs = [3000, 500, 2100], 128, 64
+    # Every third page of sequence 0 has rope keys whose logits exceed the others by ~200 (log2
+    # units): past the fast pass's headroom, so P' would overflow bf16. The fast pass flags the
+    # segments where such a page follows a low one and the rescaling pass redoes them; the other
+    # segments and sequences stay on the fast pass.
+    lens, h, bs = [30000, 500, 2100], 128, 64
     qn, qr, ckv, cs, kr, bt = _mla_case(lens, h, bs, 124)
     qr = torch.ones_like(qr)
-    for j in range(2, (lens[0] + bs - 1) // bs):
-        kr[bt[0, j]] = 16.0
+    for j in range(2, (lens[0] + bs - 1) // bs, 3):
+        kr[bt[0, j]] = 32.0
     scale = 1.0 / math.sqrt(192)
     out, lse = torch.ops.air.npu_fused_infer_attention_score(
         qn.to(DEV), ckv.to(DEV), ckv.to(DEV), query_rope=qr.to(DEV), key_rope=kr.to(DEV),

@@ -556,10 +556,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 // LDS accesses are inline asm with explicit waits (the compiler would otherwise drain the ring's
 // outstanding global -> LDS loads before each access). The step loop is unrolled twice so that
 // the tile of a step is an immediate offset.
-#ifndef TAI_MLA_CHUNK
-#define TAI_MLA_CHUNK 2048
-#endif
-constexpr int kMlaChunk = TAI_MLA_CHUNK;
 constexpr int kMlaStep = 32;
 constexpr int kMlaWaves = 4;
 constexpr int kMlaHeads = 128;  // heads per workgroup (32 per wave)
@@ -568,7 +564,7 @@ constexpr int kMlaKB = 2;           // K fragments per pipelined batch
 constexpr int kMlaVB = 4;           // V fragments per pipelined batch (two reads each)
 constexpr float kMlaSlack = 8.0f;   // log2-domain headroom of the lazily raised softmax max
 constexpr float kMlaHeadroom = 64.0f;  // log2-domain headroom of the fast pass's fixed reference
-static_assert(kMlaChunk % kMlaStep == 0 && kMlaChunk <= 2048, "a split must span at most 64 pages of 32+ tokens");
+constexpr int kMlaWgs = 256;         // workgroups of a launch (one per CU of an MI355X)
 
 struct MlaArgs {
   const uint16_t* qn;
@@ -580,11 +576,15 @@ struct MlaArgs {
   int64_t max_blocks;
   const int64_t* lens;
   int64_t b;
-  int hq, bs, nsplit, hgroups;
+  int hq, bs, hgroups;
   float scale_log2;
-  float* part_o;   // [b, nsplit, hq, DN]
-  float* part_ml;  // [b, nsplit, hq, 2]
-  int32_t* flags;  // per workgroup of the fast pass: 1 = its split needs the rescaling pass
+  // Partials: slot hg * (kMlaWgs + b_count) + w + b holds workgroup w's part of sequence b for head
+  // group hg (w + b is unique: the workgroups covering one sequence are consecutive, and so are
+  // the sequences one workgroup covers).
+  float* part_o;   // [slots, kMlaHeads, DN]
+  float* part_ml;  // [slots, kMlaHeads, 2]
+  int32_t* flags;  // [slots, kMlaWaves]: 1 = that wave's heads need the rescaling pass
+  int64_t* steps;  // [0] = 32-token steps of all sequences S, [1 + b] = steps before sequence b
 };
 
 // Raw ring stage: [latent 32 x 512 B][rope 32 x 128 B][one 256 B scale slot per wave].
@@ -655,34 +655,21 @@ __device__ __forceinline__ void lds_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// One segment: tokens [t_begin, t_end) of sequence b for head group hg, partial written to slot
+// `slot` (rows of kMlaHeads heads). Every wave of the workgroup runs it with the same arguments.
 template <int DN, int DR, bool RESCALE>
-__global__ __launch_bounds__(64 * kMlaWaves) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void mla_decode_kernel(MlaArgs a) {
+__device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg, int64_t b, int64_t t_begin,
+                                            int64_t t_end, int64_t slot) {
   static_assert(DN == 512 && DR == 64, "MLA shape");
   constexpr int NQ = (DN + DR) / 16;  // Q^T fragments: 32 nope + 4 rope
   constexpr int NN = DN / 16;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
-  const int64_t blk = blockIdx.x;
-  const int hg = static_cast<int>(blk % a.hgroups);
-  const int split = static_cast<int>((blk / a.hgroups) % a.nsplit);
-  const int64_t b = blk / (static_cast<int64_t>(a.hgroups) * a.nsplit);
-  const int64_t L = a.lens[b];
-  const int64_t t_begin = static_cast<int64_t>(split) * kMlaChunk;
-  const int64_t t_end = min<int64_t>(L, t_begin + kMlaChunk);
-  const int head = hg * kMlaHeads + 32 * w + col;
+  const int hl = 32 * w + col;  // head within the group
+  const int head = hg * kMlaHeads + hl;
   const bool head_ok = head < a.hq;
-  const int64_t pbase = (b * a.nsplit + split) * a.hq;
-  if constexpr (RESCALE) {
-    if (a.flags[blk] == 0) return;  // the fast pass finished this workgroup's split
-  }
-  if (t_begin >= t_end) {
-    if (h == 0 && head_ok) { a.part_ml[(pbase + head) * 2] = -INFINITY; a.part_ml[(pbase + head) * 2 + 1] = 0.0f; }
-    if (!RESCALE && tid == 0) a.flags[blk] = 0;
-    return;
-  }
+  const int64_t pbase = slot * kMlaHeads;
   // Q^T fragments (B operand): column = this lane's head, k slots = d 16m + 8h .. +8
   bf16x8 qf[NQ];
   {
@@ -711,14 +698,10 @@ void mla_decode_kernel(MlaArgs a) {
   }
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // pages of the split, one per lane: bs is a multiple of 32 and splits start at multiples of
-  // kMlaChunk <= 2048, so a split spans at most 64 pages; a step lies inside one page
+  // A step lies inside one page (bs % 32 == 0, segments start at multiples of 32 tokens): its page
+  // id is one scalar load, issued with the step's loads three steps ahead of use.
   const int32_t* btrow = a.bt + b * a.max_blocks;
   const int bs = a.bs;
-  const int64_t pg0 = t_begin / bs;
-  const int off0 = static_cast<int>(t_begin - pg0 * bs);
-  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);
-  const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
   const int n_local = static_cast<int>(t_end - t_begin);
   const int nsteps = (n_local + kMlaStep - 1) / kMlaStep;
 
@@ -732,9 +715,9 @@ void mla_decode_kernel(MlaArgs a) {
   // which would drain the ring.
   auto issue_raw = [&](int s) __attribute__((always_inline)) {
     char* st = smem + (s % kMlaRing) * kMlaRaw;
-    const int x = s * kMlaStep + off0;
-    const int pi = x / bs;
-    const int page = __builtin_amdgcn_readfirstlane(__shfl(my_page, pi, 64));
+    const int64_t x = t_begin + static_cast<int64_t>(s) * kMlaStep;
+    const int64_t pi = x / bs;
+    const int page = __builtin_amdgcn_readfirstlane(btrow[pi]);
     const int64_t tok0 = static_cast<int64_t>(page) * bs + (x - pi * bs);  // cache row of the step
     const int last = n_local - 1 - s * kMlaStep;
     int ln;
@@ -972,13 +955,14 @@ void mla_decode_kernel(MlaArgs a) {
 
   // prologue: three raw steps in flight, step 0 converted into tile 0 (the first step's barrier
   // publishes it)
+  // every wave is done with the previous segment's ring and tiles
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   issue_raw(0);
   if (nsteps > 1) issue_raw(1);
   if (nsteps > 2) issue_raw(2);
   if (nsteps > 2) __builtin_amdgcn_s_waitcnt((2 * kRawLoads) | 0x70 | 0xF00);
   else if (nsteps > 1) __builtin_amdgcn_s_waitcnt(kRawLoads | 0x70 | 0xF00);
   else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
-  if (!RESCALE && tid == 0) a.flags[blk] = 0;  // ordered before any wave's 1 by the barriers
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   convert(0, std::integral_constant<int, 0>{});
   const std::integral_constant<int, 0> t0c;
@@ -1007,12 +991,13 @@ void mla_decode_kernel(MlaArgs a) {
     }
   }
   if constexpr (!RESCALE) {
-    if (__any(overflow) && lane == 0) a.flags[blk] = 1;
+    const bool any_ov = __any(overflow);
+    if (lane == 0) a.flags[slot * kMlaWaves + w] = any_ov ? 1 : 0;
   }
   if (!head_ok) return;
   if constexpr (!RESCALE) mfma_drain();
   // ---- partial: O^T[d = 32dt + 8i + 4h + r][head]
-  float* po = a.part_o + (pbase + head) * DN;
+  float* po = a.part_o + (pbase + hl) * DN;
 #pragma unroll
   for (int dt = 0; dt < DN / 32; ++dt)
 #pragma unroll
@@ -1020,45 +1005,153 @@ void mla_decode_kernel(MlaArgs a) {
       *reinterpret_cast<float4*>(po + 32 * dt + 8 * i + 4 * h) =
           make_float4(acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]);
   if (h == 0) {
-    a.part_ml[(pbase + head) * 2] = m_run;
-    a.part_ml[(pbase + head) * 2 + 1] = l_run;
+    a.part_ml[(pbase + hl) * 2] = m_run;
+    a.part_ml[(pbase + hl) * 2 + 1] = l_run;
   }
 }
 
-// Merge the splits of one (b, head): 256 threads, DN / 256 outputs each. As in the GQA merge,
-// each wave reduces the split statistics itself and the numerator loop is branch free.
+__device__ __forceinline__ int64_t mla_steps(int64_t len) { return len > 0 ? (len + kMlaStep - 1) / kMlaStep : 0; }
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The kMlaWgs workgroups of a launch split all 32-token steps (head group major, then sequence)
+// into equal contiguous ranges, so every CU gets the same work whatever the lengths; a workgroup
+// runs one segment per sequence its range touches. Workgroup 0 of the fast pass also records the
+// step prefix the merge uses to find a sequence's partials.
+template <int DN, int DR, bool RESCALE>
+__global__ __launch_bounds__(64 * kMlaWaves) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void mla_decode_kernel(MlaArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = a.b;
+  int64_t mine = 0;
+  for (int64_t c = lane; c < nb; c += 64) mine += mla_steps(a.lens[c]);
+  const int64_t S = uniform64(wave_sum64(mine));
+  const int64_t W = S * a.hgroups;
+  const int64_t wg = blockIdx.x;
+  if (!RESCALE && wg == 0 && threadIdx.x < 64) {
+    int64_t carry = 0;
+    for (int64_t c = 0; c < nb; c += 64) {
+      const int64_t i = c + lane;
+      const int64_t n = i < nb ? mla_steps(a.lens[i]) : 0;
+      const int64_t incl = wave_incl_scan64(n, lane) + carry;
+      if (i < nb) a.steps[1 + i] = incl - n;
+      carry = __shfl(incl, 63, 64);
+    }
+    if (lane == 0) a.steps[0] = S;
+  }
+  const int64_t g0 = wg * W / kMlaWgs, g1 = (wg + 1) * W / kMlaWgs;
+  if (g0 >= g1) return;
+  // the range's first sequence: head group g0 / S, step x = g0 % S inside it
+  int hg = static_cast<int>(g0 / S);
+  int64_t x = g0 % S, b = 0, pb = 0;
+  {
+    int64_t carry = 0;
+    for (int64_t c = 0; c < nb; c += 64) {
+      const int64_t i = c + lane;
+      const int64_t n = i < nb ? mla_steps(a.lens[i]) : 0;
+      const int64_t incl = wave_incl_scan64(n, lane) + carry;
+      const uint64_t hit = __ballot(i < nb && n > 0 && incl - n <= x && x < incl);
+      if (hit) {
+        const int j = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+        b = c + j;
+        pb = __shfl(incl - n, j, 64);
+        break;
+      }
+      carry = __shfl(incl, 63, 64);
+    }
+  }
+  b = uniform64(b);
+  pb = uniform64(pb);
+  for (int64_t g = g0; g < g1;) {
+    const int64_t len = a.lens[b];
+    const int64_t n = mla_steps(len);
+    const int64_t seg = min(g1 - g, pb + n - x);
+    const int64_t t_begin = (x - pb) * kMlaStep;
+    const int64_t slot = hg * (kMlaWgs + nb) + wg + b;
+    bool run = true;
+    if constexpr (RESCALE) {
+      const int32_t* f = a.flags + slot * kMlaWaves;
+      run = (f[0] | f[1] | f[2] | f[3]) != 0;
+    }
+    if (run) mla_segment<DN, DR, RESCALE>(a, smem, hg, b, t_begin, min(len, t_begin + seg * kMlaStep), slot);
+    g += seg;
+    x += seg;
+    if (x == pb + n) {  // on to the next non-empty sequence (the next head group after the last)
+      pb += n;
+      do {
+        if (++b == nb) { b = 0; pb = 0; x = 0; ++hg; }
+      } while (g < g1 && mla_steps(a.lens[b]) == 0);
+    }
+  }
+}
+
+// Merge the partials of one (b, head): 256 threads, DN / 256 outputs each. The partials are those of
+// the workgroups whose step ranges cover the sequence. Each wave reduces the partial statistics
+// itself and the numerator loop is branch free.
 template <int DN>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* out, float* lse) {
   const int64_t bh = blockIdx.x;
   const int h = static_cast<int>(bh % a.hq);
   const int64_t b = bh / a.hq;
-  const int64_t L = a.lens[b];
-  const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kMlaChunk - 1) / kMlaChunk));
-  const int64_t pi0 = b * a.nsplit * a.hq + h;  // split s: pi0 + s * hq
-  const float* ml = a.part_ml + pi0 * 2;
-  const int64_t mls = 2 * static_cast<int64_t>(a.hq);
+  const int64_t n = mla_steps(a.lens[b]);
+  if (n == 0) {
+#pragma unroll
+    for (int i = 0; i < DN / 256; ++i) out[(b * a.hq + h) * DN + threadIdx.x + 256 * i] = 0;
+    if (lse && threadIdx.x == 0) lse[b * a.hq + h] = -INFINITY;
+    return;
+  }
+  const int64_t S = a.steps[0], W = S * a.hgroups;
+  const int hg = h / kMlaHeads, hl = h % kMlaHeads;
+  const int64_t x0 = hg * S + a.steps[1 + b], x1 = x0 + n;
+  const int64_t w_first = ((x0 + 1) * kMlaWgs - 1) / W, w_last = (x1 * kMlaWgs - 1) / W;
+  const int ns = static_cast<int>(w_last - w_first + 1);
+  const int64_t row0 = (hg * (kMlaWgs + a.b) + w_first + b) * kMlaHeads + hl;  // partial s: row0 + s * kMlaHeads
+  const float* ml = a.part_ml + row0 * 2;
+  // With fewer steps than workgroups some ranges are empty; those workgroups wrote nothing.
+  auto stat_m = [&](int s) {
+    const int64_t w = w_first + s;
+    return (w + 1) * W / kMlaWgs > w * W / kMlaWgs ? ml[2 * kMlaHeads * s] : -INFINITY;
+  };
   const int lane = threadIdx.x & 63;
   float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, ml[mls * s]);
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, stat_m(s));
   M = wave_max(M);
   float den = 0.0f;
   for (int s = lane; s < ns; s += 64) {
-    const float m = ml[mls * s];
-    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[mls * s + 1];
+    const float m = stat_m(s);
+    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[2 * kMlaHeads * s + 1];
   }
   den = wave_sum(den);
   float num[DN / 256];
 #pragma unroll
   for (int i = 0; i < DN / 256; ++i) num[i] = 0.0f;
-  const float* po = a.part_o + pi0 * DN + threadIdx.x;
-  const int64_t pos = static_cast<int64_t>(a.hq) * DN;
+  const float* po = a.part_o + row0 * DN + threadIdx.x;
 #pragma unroll 4
   for (int s = 0; s < ns; ++s) {
-    const float m = ml[mls * s];
+    const float m = stat_m(s);
     const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
 #pragma unroll
     for (int i = 0; i < DN / 256; ++i) {
-      const float o = po[pos * s + 256 * i];
+      const float o = po[static_cast<int64_t>(kMlaHeads) * DN * s + 256 * i];
       num[i] += m == -INFINITY ? 0.0f : wgt * o;
     }
   }
@@ -1068,10 +1161,19 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   if (lse && threadIdx.x == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
 
-// [part_o fp32 b x nsplit x hq x dn][part_ml fp32 b x nsplit x hq x 2][flags int32, one per workgroup]
-size_t mla_ws(int64_t b, int hq, int dn, int nsplit) {
-  const int64_t wgs = b * nsplit * ((hq + kMlaHeads - 1) / kMlaHeads);
-  return static_cast<size_t>(b) * nsplit * hq * (dn + 2) * sizeof(float) + static_cast<size_t>(wgs) * sizeof(int32_t);
+// Workspace: [step prefix int64 x (b + 1), padded to 256 B][part_o][part_ml][flags]
+struct MlaWs {
+  size_t steps, part_o, part_ml, flags, total;
+};
+MlaWs mla_ws(int64_t b, int hq, int dn) {
+  const int64_t slots = ((hq + kMlaHeads - 1) / kMlaHeads) * (kMlaWgs + b);
+  MlaWs w;
+  w.steps = 0;
+  w.part_o = (static_cast<size_t>(b + 1) * sizeof(int64_t) + 255) / 256 * 256;
+  w.part_ml = w.part_o + static_cast<size_t>(slots) * kMlaHeads * dn * sizeof(float);
+  w.flags = w.part_ml + static_cast<size_t>(slots) * kMlaHeads * 2 * sizeof(float);
+  w.total = w.flags + static_cast<size_t>(slots) * kMlaWaves * sizeof(int32_t);
+  return w;
 }
 }  // namespace
 }  // namespace tai
@@ -1171,8 +1273,9 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
 }
 
 extern "C" size_t tai_fia_mla_decode_workspace_size(int64_t b, int hq, int dn, int64_t max_blocks, int block_size) {
-  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kMlaChunk));
-  return mla_ws(b, hq, dn, nsplit) + 256;
+  (void)max_blocks;
+  (void)block_size;
+  return mla_ws(b, hq, dn).total + 256;
 }
 
 extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const int8_t* ckv_cache, const float* ckv_scale,
@@ -1186,8 +1289,8 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   if (b == 0) return TAI_OK;
   TAI_CHECK_ARG(q_nope && q_rope && ckv_cache && ckv_scale && krope_cache && block_table && seq_lens_kv && out,
                 "tai_fia_mla_decode: null pointer");
-  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kMlaChunk));
-  const size_t need = mla_ws(b, hq, dn, nsplit);
+  const MlaWs lay = mla_ws(b, hq, dn);
+  const size_t need = lay.total;
   if (workspace == nullptr || ws_bytes < need) {
     set_error("tai_fia_mla_decode: workspace of %zu bytes, need %zu", ws_bytes, need);
     return TAI_ERR_WORKSPACE;
@@ -1197,10 +1300,12 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.qr = static_cast<const uint16_t*>(q_rope);
   a.ckv = ckv_cache; a.cs = ckv_scale; a.kr = static_cast<const uint16_t*>(krope_cache);
   a.bt = block_table; a.max_blocks = max_blocks; a.lens = seq_lens_kv; a.b = b; a.hq = hq; a.bs = block_size;
-  a.nsplit = nsplit; a.hgroups = static_cast<int>(cdiv(hq, kMlaHeads)); a.scale_log2 = scale * kLog2e;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + static_cast<size_t>(b) * nsplit * hq * dn;
-  a.flags = reinterpret_cast<int32_t*>(a.part_ml + static_cast<size_t>(b) * nsplit * hq * 2);
+  a.hgroups = static_cast<int>(cdiv(hq, kMlaHeads)); a.scale_log2 = scale * kLog2e;
+  char* ws = static_cast<char*>(workspace);
+  a.steps = reinterpret_cast<int64_t*>(ws + lay.steps);
+  a.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  a.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+  a.flags = reinterpret_cast<int32_t*>(ws + lay.flags);
   hipStream_t st = static_cast<hipStream_t>(stream);
   static bool lds_set = false;
   if (!lds_set) {
@@ -1214,9 +1319,8 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
     }
     lds_set = true;
   }
-  // fast pass over every split, then the rescaling pass over the splits it flagged (its other
-  // workgroups exit at once)
-  const dim3 grid(static_cast<unsigned>(b * nsplit * a.hgroups));
+  // fast pass, then the rescaling pass over the segments the fast pass flagged (it skips the others)
+  const dim3 grid(kMlaWgs);
   mla_decode_kernel<512, 64, false><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
   mla_decode_kernel<512, 64, true><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
   mla_combine_kernel<512><<<dim3(static_cast<unsigned>(b * hq)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
