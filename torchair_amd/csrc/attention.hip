@@ -698,12 +698,19 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
   }
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // A step lies inside one page (bs % 32 == 0, segments start at multiples of 32 tokens): its page
-  // id is one scalar load, issued with the step's loads three steps ahead of use.
+  // A step lies inside one page (bs % 32 == 0, segments start at multiples of 32 tokens). The page
+  // ids of the segment are held one per lane, 64 at a time (a window is reloaded when a step leaves
+  // it); a step's id is a lane broadcast.
   const int32_t* btrow = a.bt + b * a.max_blocks;
   const int bs = a.bs;
   const int n_local = static_cast<int>(t_end - t_begin);
   const int nsteps = (n_local + kMlaStep - 1) / kMlaStep;
+  const int64_t pg_first = t_begin / bs, pg_last = (t_end - 1) / bs;
+  int64_t win = pg_first;  // first page of the window
+  int my_page = lane <= pg_last - win ? btrow[win + lane] : 0;
+  // issue cursor: page (relative to the window) and slot of the next step to load; the steps are
+  // issued in order, so the cursor advances by one step per issue (no division per step)
+  int cur_pg = 0, cur_slot = static_cast<int>(t_begin - pg_first * bs);
 
   // Every wave issues the same number of global_load_lds per step, so one vmcnt fits all: four
   // latent instructions (2 rows of 512 B each), one rope instruction (8 rows of 128 B) and one
@@ -715,10 +722,16 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
   // which would drain the ring.
   auto issue_raw = [&](int s) __attribute__((always_inline)) {
     char* st = smem + (s % kMlaRing) * kMlaRaw;
-    const int64_t x = t_begin + static_cast<int64_t>(s) * kMlaStep;
-    const int64_t pi = x / bs;
-    const int page = __builtin_amdgcn_readfirstlane(btrow[pi]);
-    const int64_t tok0 = static_cast<int64_t>(page) * bs + (x - pi * bs);  // cache row of the step
+    if (cur_pg == 64) {  // rare: segments longer than 64 pages
+      win += 64;
+      cur_pg = 0;
+      my_page = lane <= pg_last - win ? btrow[win + lane] : 0;
+      __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // here, so that the common path waits for nothing
+    }
+    const int page = __builtin_amdgcn_readfirstlane(__shfl(my_page, cur_pg, 64));
+    const int64_t tok0 = static_cast<int64_t>(page) * bs + cur_slot;  // cache row of the step
+    cur_slot += kMlaStep;
+    if (cur_slot == bs) { cur_slot = 0; ++cur_pg; }
     const int last = n_local - 1 - s * kMlaStep;
     int ln;
     asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
