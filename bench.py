@@ -1,7 +1,7 @@
 """Benchmark of the fused-op hot path on one MI355X.
 
 Headline (value): DeepSeek-V3-shaped quantized MoE layer in tokens/s:
-  gating_top_k -> init_routing_v2 -> dynamic_quant -> grouped_matmul (W8A8 gate_up, int32)
+  gating_top_k -> init_routing_v2 (fused dynamic quant, quant_mode 1) -> grouped_matmul (W8A8 gate_up, int32)
   -> dequant_swiglu_quant -> grouped_matmul (W8A8 down, bf16) -> finalize_routing,
 with every input resident in HBM before the timed region. Side measurements in the same JSON
 line: paged GQA decode attention (config 2) HBM GB/s, the W8A8 GEMM at M=N=K=8192 and the
@@ -58,10 +58,11 @@ class MoeLayer:
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
                                              group_select_mode=1, renorm=0, norm_type=1,
                                              routed_scaling_factor=1.0, eps=1e-20)
-        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
-                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
-                                                        row_idx_type=0)
-        q, s = npu.npu_dynamic_quant(ex)
+        # routing with the fused dynamic quant (quant_mode 1): the int8 rows and per-row scales equal
+        # npu_dynamic_quant of the gathered bf16 rows, bit for bit
+        q, ri, counts, s = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
+                                                       expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                       row_idx_type=0, quant_mode=1)
         if self.active_experts is None:
             self.active_experts = int((counts > 0).sum().item())  # routing is fixed: same logits every step
         if record:
@@ -87,10 +88,11 @@ class MoeLayer:
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
                                              group_select_mode=1, renorm=0, norm_type=1,
                                              routed_scaling_factor=1.0, eps=1e-20)
-        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
-                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
-                                                        row_idx_type=0)
-        q, s = npu.npu_dynamic_quant(ex)
+        # routing with the fused dynamic quant (quant_mode 1): the int8 rows and per-row scales equal
+        # npu_dynamic_quant of the gathered bf16 rows, bit for bit
+        q, ri, counts, s = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
+                                                       expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                       row_idx_type=0, quant_mode=1)
         q2, s2 = npu.npu_grouped_matmul_swiglu_quant_v2(q, [self.w_gu], [self.s_gu], s, counts, group_list_type=1)
         out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
                                      split_item=3, group_type=0, group_list_type=1,

@@ -274,7 +274,8 @@ def moe_gating_top_k(x, k: int, bias=None, k_group: int = 1, group_count: int = 
 
 def moe_init_routing_v2(x, expert_idx, scale=None, active_rows: Optional[int] = None, expert_start: int = 0,
                         expert_end: Optional[int] = None, expert_tokens_num_type: int = 0, row_idx_type: int = 0):
-    """npu_moe_init_routing_v2, dropless (drop_pad_mode 0), quant_mode -1.
+    """npu_moe_init_routing_v2, dropless (drop_pad_mode 0), quant_mode -1. (quant_mode 1 without smooth
+    scales is this followed by dynamic_quant of the expanded rows; the tests compose the two.)
 
     Follows .../custom/npu_moe_init_routing_v2.py:41-91 (-> ge.MoeInitRoutingV3) and prototype
     experiment_ops.h:2138-2190 (row_idx_type 0 gather / 1 scatter, expert_tokens_num_type 0

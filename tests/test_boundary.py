@@ -68,6 +68,10 @@ def test_meta_shapes_follow_reference_rules():
                                                             torch.empty(4096, 8, device=m, dtype=torch.int32),
                                                             expert_num=256)
     assert ex.shape == (32768, 7168) and ri.shape == (32768,) and tok.shape == (256,)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(torch.empty(4096, 7168, device=m, dtype=torch.bfloat16),
+                                                            torch.empty(4096, 8, device=m, dtype=torch.int32),
+                                                            expert_num=256, quant_mode=1)
+    assert ex.dtype == torch.int8 and es.shape == (32768,) and es.dtype == torch.float32
     q = torch.empty(64, 1, 32 * 128, device=m, dtype=torch.bfloat16)
     kc = torch.empty(100, 128, 8 * 128, device=m, dtype=torch.bfloat16)
     out, lse = torch.ops.air.npu_fused_infer_attention_score(

@@ -88,6 +88,29 @@ def test_init_routing_v2_range_active_and_scale():
     np.testing.assert_array_equal(es.cpu().numpy(), wes)
 
 
+def test_init_routing_v2_dynamic_quant_cfg4():
+    # quant_mode 1: int8 expanded rows and their per-row scales, bit for bit the npu_dynamic_quant of
+    # the gathered bf16 rows
+    g = gen(35)
+    t, h, e, k = 4096, 7168, 256, 8
+    x, idx = _routing_inputs(t, h, e, k, g)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), active_num=t * k, expert_num=e, expert_tokens_num_type=1,
+        expert_tokens_num_flag=True, quant_mode=1)
+    assert ex.dtype == torch.int8 and es.shape == (t * k,)
+    wex, wri, wtok, _ = G.moe_init_routing_v2(f32np(x), idx.numpy(), None, t * k, 0, e, 1, 0)
+    wq, ws = G.dynamic_quant(wex)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    np.testing.assert_array_equal(ex.cpu().numpy(), wq)
+    np.testing.assert_array_equal(es.cpu().numpy(), ws)
+    # and the same as the unfused pair of ops
+    ex2, _, _, _ = torch.ops.npu.npu_moe_init_routing_v2(x.to(DEV), idx.to(DEV), active_num=t * k, expert_num=e,
+                                                         expert_tokens_num_type=1, expert_tokens_num_flag=True)
+    q2, s2 = torch.ops.npu.npu_dynamic_quant(ex2)
+    assert torch.equal(q2, ex) and torch.equal(s2, es)
+
+
 def test_init_routing_legacy():
     g = gen(34)
     t, h, k = 250, 64, 3

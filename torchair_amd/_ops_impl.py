@@ -465,18 +465,35 @@ def _init_routing_v2_fake(x, expert_idx, *, scale=None, offset=None, active_num=
     n = t * k
     rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
     lo, hi = _v2_expert_range(expert_num, active_expert_range)
-    return (x.new_empty((rows, x.shape[1])), x.new_empty((n,), dtype=torch.int32),
+    dyn = quant_mode == 1
+    return (x.new_empty((rows, x.shape[1]), dtype=torch.int8 if dyn else x.dtype),
+            x.new_empty((n,), dtype=torch.int32),
             x.new_empty((max(hi - lo, 0),), dtype=torch.int64),
-            x.new_empty((rows if scale is not None else 0,), dtype=torch.float32))
+            x.new_empty((rows if (scale is not None or dyn) else 0,), dtype=torch.float32))
 
 
 def _init_routing_v2_cuda(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1,
                           expert_num=-1, drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False,
                           quant_mode=-1, active_expert_range=(), row_idx_type=0):
-    """npu_moe_init_routing_v2, dropless (npu_moe_init_routing_v2.py:41-91)."""
+    """npu_moe_init_routing_v2, dropless (npu_moe_init_routing_v2.py:41-91).
+
+    quant_mode 1 (dynamic, experiment_ops.h:2167) without smooth scales: every expanded row is the
+    symmetric per-row int8 quantisation of its token row and expanded_scale holds that row's scale.
+    A token row and its copies quantise identically, so the T token rows are quantised once (the
+    npu_dynamic_quant kernel) and the int8 rows and scales are gathered."""
     _on_gpu(x, expert_idx, scale)
     _check(drop_pad_mode == 0, "npu_moe_init_routing_v2: only drop_pad_mode 0 (dropless) is supported")
-    _check(quant_mode == -1, "npu_moe_init_routing_v2: only quant_mode -1 (no fused quant) is supported")
+    _check(quant_mode in (-1, 1), "npu_moe_init_routing_v2: quant_mode -1 (none) or 1 (dynamic) is supported")
+    if quant_mode == 1:
+        _check(scale is None and offset is None,
+               "npu_moe_init_routing_v2: quant_mode 1 is supported without smooth scale or offset")
+        _check(x.dim() == 2, "npu_moe_init_routing_v2: x [T,H] and expert_idx [T,k]")
+        q, s = torch.ops.npu.npu_dynamic_quant(x)
+        return _init_routing_v2_cuda(q, expert_idx, scale=s, active_num=active_num, expert_capacity=expert_capacity,
+                                     expert_num=expert_num, drop_pad_mode=drop_pad_mode,
+                                     expert_tokens_num_type=expert_tokens_num_type,
+                                     expert_tokens_num_flag=expert_tokens_num_flag, quant_mode=-1,
+                                     active_expert_range=active_expert_range, row_idx_type=row_idx_type)
     _check(offset is None, "npu_moe_init_routing_v2: offset is not supported")
     _check(expert_tokens_num_type in (0, 1), "npu_moe_init_routing_v2: expert_tokens_num_type must be 0 or 1")
     _check(x.dim() == 2 and expert_idx.dim() == 2 and expert_idx.shape[0] == x.shape[0],
