@@ -1,7 +1,7 @@
 """Benchmark of the fused-op hot path on one MI355X.
 
 Headline (value): DeepSeek-V3-shaped quantized MoE layer in tokens/s:
-  gating_top_k -> init_routing_v2 (fused dynamic quant, quant_mode 1) -> grouped_matmul (W8A8 gate_up, int32)
+  gating_top_k -> init_routing_v2 -> dynamic_quant -> grouped_matmul (W8A8 gate_up, int32)
   -> dequant_swiglu_quant -> grouped_matmul (W8A8 down, bf16) -> finalize_routing,
 with every input resident in HBM before the timed region. Side measurements in the same JSON
 line: paged GQA decode attention (config 2) HBM GB/s, the W8A8 GEMM at M=N=K=8192 and the
@@ -52,17 +52,23 @@ class MoeLayer:
         self.gmm1_events = []
         self.active_experts = None
 
-    def step(self, record=False):
+    def step(self, record=False, fused_quant=False):
         torch = self.torch
         npu = torch.ops.npu
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
                                              group_select_mode=1, renorm=0, norm_type=1,
                                              routed_scaling_factor=1.0, eps=1e-20)
-        # routing with the fused dynamic quant (quant_mode 1): the int8 rows and per-row scales equal
-        # npu_dynamic_quant of the gathered bf16 rows, bit for bit
-        q, ri, counts, s = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
-                                                       expert_tokens_num_type=1, expert_tokens_num_flag=True,
-                                                       row_idx_type=0, quant_mode=1)
+        if fused_quant:
+            # routing with the fused dynamic quant (quant_mode 1): the int8 rows and per-row scales
+            # equal npu_dynamic_quant of the gathered bf16 rows, bit for bit
+            q, ri, counts, s = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K,
+                                                           expert_num=self.E, expert_tokens_num_type=1,
+                                                           expert_tokens_num_flag=True, row_idx_type=0, quant_mode=1)
+        else:  # the composition config 4 prescribes: init_routing permute, then npu_dynamic_quant
+            ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K,
+                                                            expert_num=self.E, expert_tokens_num_type=1,
+                                                            expert_tokens_num_flag=True, row_idx_type=0)
+            q, s = npu.npu_dynamic_quant(ex)
         if self.active_experts is None:
             self.active_experts = int((counts > 0).sum().item())  # routing is fixed: same logits every step
         if record:
@@ -88,11 +94,10 @@ class MoeLayer:
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
                                              group_select_mode=1, renorm=0, norm_type=1,
                                              routed_scaling_factor=1.0, eps=1e-20)
-        # routing with the fused dynamic quant (quant_mode 1): the int8 rows and per-row scales equal
-        # npu_dynamic_quant of the gathered bf16 rows, bit for bit
-        q, ri, counts, s = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
-                                                       expert_tokens_num_type=1, expert_tokens_num_flag=True,
-                                                       row_idx_type=0, quant_mode=1)
+        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(self.x, idx, active_num=self.T * self.K, expert_num=self.E,
+                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                        row_idx_type=0)
+        q, s = npu.npu_dynamic_quant(ex)
         q2, s2 = npu.npu_grouped_matmul_swiglu_quant_v2(q, [self.w_gu], [self.s_gu], s, counts, group_list_type=1)
         out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
                                      split_item=3, group_type=0, group_list_type=1,
@@ -125,7 +130,8 @@ def bench_moe(torch, dev, steps, warmup):
 
 
 def bench_moe_variants(torch, layer, iters=10):
-    """ms per step of the config-4 layer with the fused gate_up op, and of the prescribed composition
+    """ms per step of the config-4 layer with the fused gate_up op, with the routing's fused dynamic
+    quant (npu_moe_init_routing_v2 quant_mode 1, bit-identical), and of the prescribed composition
     replayed from a hipGraph (launch gaps removed)."""
     from torchair_amd.graph import HipGraphRunner
     out = {}
@@ -135,7 +141,8 @@ def bench_moe_variants(torch, layer, iters=10):
         layer.step_fused()
         runner(layer.logits)
     torch.cuda.synchronize()
-    for name, fn in (("fused_gate_up_ms", layer.step_fused), ("hipgraph_ms", lambda: runner(layer.logits))):
+    for name, fn in (("fused_gate_up_ms", layer.step_fused), ("fused_routing_quant_ms", lambda: layer.step(fused_quant=True)),
+                     ("hipgraph_ms", lambda: runner(layer.logits))):
         e0, e1 = _events(torch)
         e0.record()
         for _ in range(iters):
@@ -144,6 +151,7 @@ def bench_moe_variants(torch, layer, iters=10):
         torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / iters, 4)
     out["fused_gate_up_tokens_per_s"] = round(MoeLayer.T / (out["fused_gate_up_ms"] * 1e-3), 1)
+    out["fused_routing_quant_tokens_per_s"] = round(MoeLayer.T / (out["fused_routing_quant_ms"] * 1e-3), 1)
     out["hipgraph_tokens_per_s"] = round(MoeLayer.T / (out["hipgraph_ms"] * 1e-3), 1)
     return out
 
