@@ -219,3 +219,10 @@ def test_mla_rising_logits_take_the_rescaling_pass():
     assert_close(f32np(out[:, 0]), want)
     got = lse.reshape(len(lens), h).cpu().numpy()
     np.testing.assert_allclose(got, wl, rtol=1e-3, atol=1e-3)
+
+
+def test_mla_segments_longer_than_a_page_window():
+    # block_size 32 and ~16.9K steps over 256 workgroups: ~66 steps (= pages) per workgroup range, so
+    # segments cross the 64-page window of page ids the kernel holds and reload it
+    lens, h, bs = [140000, 140000, 140000, 120000], 16, 32
+    _check_mla(lens, h, bs, 125)
