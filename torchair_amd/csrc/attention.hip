@@ -376,9 +376,12 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   int64_t blk_kv = 0;
   {
     const int last_unit = min(jb * 4 + 3, a.units_per_bk - 1);
-    const int qt_hi = last_unit / a.g;  // units are qtile-major, so the last unit has the largest tile
+    const int qt_lo = (jb * 4) / a.g;   // units are qtile-major: the first unit has the smallest tile
+    const int qt_hi = last_unit / a.g;  // and the last unit the largest
     const int64_t qlast = min<int64_t>(static_cast<int64_t>(qt_hi) * kPQ + kPQ, Lq) - 1;
-    blk_kv = qlast >= 0 ? imax64(0, kv_limit(qlast)) : 0;
+    // a workgroup whose query tiles all lie past this sequence's length has no live wave: it loads
+    // nothing (its tiles exist because the grid is sized for the longest sequence)
+    blk_kv = (qlast >= 0 && static_cast<int64_t>(qt_lo) * kPQ < Lq) ? imax64(0, kv_limit(qlast)) : 0;
   }
 
   // Q^T fragments (B operand): query = col, d slots 16*kd + 8*grp .. +8
