@@ -302,6 +302,7 @@ size_t decode_ws(int64_t b, int hkv, int d, int nsplit) {
 // are free of bank conflicts.
 constexpr int kPQ = 32;    // query rows per wave
 constexpr int kPKV = 64;   // kv tokens per LDS tile
+constexpr float kPfSlack = 8.0f;  // log2-domain headroom of the lazily raised softmax max
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -470,9 +471,20 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+    // Online softmax with a lazily raised reference max (as in the MLA kernel): m_run moves, and O^T
+    // and l are rescaled, only when a query's tile max exceeds it by more than kPfSlack (log2 units),
+    // so P <= 2^kPfSlack between raises; the result is the same.
+    if (__any(mx > m_run + kPfSlack)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
     float rs = 0.0f;
     bf16x8 pf[4];
 #pragma unroll
@@ -486,12 +498,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
           pf[2 * st + kb2][j] = static_cast<__bf16>(e);
         }
     rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+    l_run += rs;
     // ---- O^T += V^T P^T. The k slots of lane group grp in k-block kb are tokens
     //      16kb + 4grp + {0..3} and 16kb + 8 + 4grp + {0..3} (the S^T row order); each half is
     //      one ds_read_b64_tr_b16: source lane j16 addresses V[k0 + j16/4][nb + 4 (j16 & 3)] and
