@@ -656,10 +656,18 @@ __device__ __forceinline__ void mfma_vgpr(f32x16& acc, const bf16x8& a, const bf
 __device__ __forceinline__ void mfma_vgpr_zero(f32x16& acc, const bf16x8& a, const bf16x8& b) {
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(a), "v"(b));
 }
-__device__ __forceinline__ void mfma_vgpr_wait() { asm volatile("s_nop 15\n\ts_nop 7" ::: "memory"); }
+// The nops are tied to the accumulator (a read-write operand), so no instruction that reads it can
+// be scheduled above them.
+__device__ __forceinline__ void mfma_vgpr_wait(f32x16& acc) { asm volatile("s_nop 15\n\ts_nop 7" : "+v"(acc)::"memory"); }
 
-// Longer than the worst-case latency of one 32x32x16 MFMA (16 passes).
-__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
+// Longer than the worst-case latency of one 32x32x16 MFMA (16 passes). Every accumulator passes
+// through an empty asm after the nops, so no read of one can be scheduled above them.
+template <int N>
+__device__ __forceinline__ void mfma_drain(f32x16 (&acc)[N]) {
+  asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+}
 template <int N>
 __device__ __forceinline__ void lds_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
@@ -889,7 +897,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
         asm volatile("" : "+v"(kf[cur][i]));
         const bf16x8 kv = __builtin_bit_cast(bf16x8, kf[cur][i]);
         if constexpr (m == NN) {  // nope part complete: scale it, then add the rope part
-          if constexpr (!RESCALE) mfma_vgpr_wait();
+          if constexpr (!RESCALE) mfma_vgpr_wait(sn);
 #pragma unroll
           for (int e = 0; e < 16; ++e) sn[e] *= cs[e >> 2][e & 3];
         }
@@ -902,7 +910,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
       });
     });
     // ---- logits
-    if constexpr (!RESCALE) mfma_vgpr_wait();
+    if constexpr (!RESCALE) mfma_vgpr_wait(sn);
     const int64_t t0 = t_begin + static_cast<int64_t>(s) * kMlaStep;
     mx = -INFINITY;
 #pragma unroll
@@ -925,7 +933,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
     const float m_new = fmaxf(m_run, mx);
     const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     l_run *= alpha;
-    mfma_drain();
+    mfma_drain(acc);
 #pragma unroll
     for (int dt = 0; dt < DN / 32; ++dt) acc[dt] *= alpha;
     m_run = m_new;
@@ -1018,7 +1026,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
     if (lane == 0) a.flags[slot * kMlaWaves + w] = any_ov ? 1 : 0;
   }
   if (!head_ok) return;
-  if constexpr (!RESCALE) mfma_drain();
+  if constexpr (!RESCALE) mfma_drain(acc);
   // ---- partial: O^T[d = 32dt + 8i + 4h + r][head]
   float* po = a.part_o + (pbase + hl) * DN;
 #pragma unroll
