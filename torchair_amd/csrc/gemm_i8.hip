@@ -458,6 +458,9 @@ struct BigCfg {
   static_assert(kBN >= 256, "the [K,N] swizzle spans 16 chunks of a weight row");
 };
 
+#ifndef TAI_SPLIT_ISSUE
+#define TAI_SPLIT_ISSUE 1
+#endif
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
@@ -495,12 +498,18 @@ __device__ __forceinline__ void lgkm_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 }
 
-template <int LAYOUT, class C, bool SWI = false>
+// The loads of one stage: PART 0 issues all of them, PART 1 the first half and PART 2 the rest (a
+// stage's loads are split so that the workgroup's waves do not all queue in the address unit at
+// the same moment after a barrier).
+template <int LAYOUT, class C, bool SWI = false, int PART = 0>
 __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, int row0, int rows,
                                                 int64_t n0, int64_t k0, int8_t* stage, int w, int lane) {
   constexpr int BK = C::kBK, CPR = C::kCpr, RPI = 1024 / BK;  // rows per 1 KB instruction
+  constexpr int kFirst = (C::kLoads + 1) / 2;
+  constexpr int j0 = PART == 2 ? kFirst : 0, j1 = PART == 1 ? kFirst : C::kLoads;
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) {
+    if (i < j0 || i >= j1) continue;
     const int q = C::kALoads * w + i;
     const int row = RPI * q + lane / CPR;
     const int c = (lane % CPR) ^ ((row >> C::kRowShift) & (CPR - 1));
@@ -511,6 +520,7 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
   int8_t* bst = stage + C::kBM * BK;
 #pragma unroll
   for (int i = 0; i < C::kBLoads; ++i) {
+    if (C::kALoads + i < j0 || C::kALoads + i >= j1) continue;
     const int q = C::kBLoads * w + i;
     const int8_t* src;
     if constexpr (LAYOUT == TAI_LAYOUT_NK) {
@@ -726,6 +736,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   // the last step waits for stage kt + 1, passes the workgroup barrier (after it no wave reads slot
   // kt, whose fragments are in registers), refills slot kt with stage kt + S, prefetches the first
   // fragments of stage kt + 1, then multiplies.
+  constexpr bool kSplit = TAI_SPLIT_ISSUE != 0 && C::kStages > 2;  // needs two stages in flight
   auto main_loop = [&](auto ni) {
     constexpr int NI = decltype(ni)::value;
     constexpr int NF = NI == 0 ? 0 : NI + (LAYOUT == TAI_LAYOUT_KN ? 8 : 4);  // LDS reads per step
@@ -774,14 +785,23 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
           if (kt + 1 < nk) {
             wait_stage(kt + 1);
             asm volatile("s_barrier" ::: "memory");
+            // stage kt + S into the slot just freed: its first half now, the rest after the next
+            // stage's first MFMA step (every load is still issued before the next stage wait)
             if (kt + C::kStages < nk)
-              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + (kt + C::kStages) * kBigBK,
-                                         smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
+              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, kSplit ? 1 : 0>(
+                  g, bgrp, row0, rows, n0, kb0 + (kt + C::kStages) * kBigBK,
+                  smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
             fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
           }
         }
         ready(cur);
         mfma(cur);
+        if constexpr (kSplit) {
+          if (kk == 0 && kt >= 1 && kt - 1 + C::kStages < nk)
+            big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 2>(g, bgrp, row0, rows, n0, kb0 + (kt - 1 + C::kStages) * kBigBK,
+                                                           smem + ((static_cast<int>(kt) - 1) % C::kStages) * C::kStage,
+                                                           w, lane);
+        }
         __builtin_amdgcn_sched_barrier(0);  // the next step's waits stay behind these MFMAs
       }
     }
