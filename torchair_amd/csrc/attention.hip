@@ -1135,61 +1135,84 @@ void mla_decode_kernel(MlaArgs a) {
   }
 }
 
-// Merge the partials of one (b, head): 256 threads, DN / 256 outputs each. The partials are those of
-// the workgroups whose step ranges cover the sequence. Each wave reduces the partial statistics
-// itself and the numerator loop is branch free.
+// Merge the partials of a sequence's heads: one wave per pair of heads (each lane owns 8
+// consecutive d of both), four waves per workgroup. The partials are those of the workgroups whose
+// step ranges cover the sequence. The statistics of both heads of a partial are one 16-byte load
+// (uniform across the wave), and every partial's O values are loaded before the weights that
+// scale them are known, so a wave waits on few dependent round trips.
+constexpr int kMlaCombineHeads = 8;  // heads per combine workgroup (2 per wave)
 template <int DN>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* out, float* lse) {
-  const int64_t bh = blockIdx.x;
-  const int h = static_cast<int>(bh % a.hq);
-  const int64_t b = bh / a.hq;
+  static_assert(DN == 512, "one lane holds 8 of the 512 latent dims");
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t per_b = (a.hq + kMlaCombineHeads - 1) / kMlaCombineHeads;
+  const int64_t b = blockIdx.x / per_b;
+  const int h0 = static_cast<int>(blockIdx.x % per_b) * kMlaCombineHeads + 2 * wv;
+  if (h0 >= a.hq) return;
+  const bool two = h0 + 1 < a.hq;
   const int64_t n = mla_steps(a.lens[b]);
+  uint4* o0 = reinterpret_cast<uint4*>(out + (b * a.hq + h0) * DN) + lane;
+  uint4* o1 = reinterpret_cast<uint4*>(out + (b * a.hq + h0 + 1) * DN) + lane;
   if (n == 0) {
-#pragma unroll
-    for (int i = 0; i < DN / 256; ++i) out[(b * a.hq + h) * DN + threadIdx.x + 256 * i] = 0;
-    if (lse && threadIdx.x == 0) lse[b * a.hq + h] = -INFINITY;
+    *o0 = make_uint4(0, 0, 0, 0);
+    if (two) *o1 = make_uint4(0, 0, 0, 0);
+    if (lse && lane < (two ? 2 : 1)) lse[b * a.hq + h0 + lane] = -INFINITY;
     return;
   }
   const int64_t S = a.steps[0], W = S * a.hgroups;
-  const int hg = h / kMlaHeads, hl = h % kMlaHeads;
+  const int hg = h0 / kMlaHeads, hl = h0 % kMlaHeads;  // h0 is even, so both heads share hg
   const int64_t x0 = hg * S + a.steps[1 + b], x1 = x0 + n;
   const int64_t w_first = ((x0 + 1) * kMlaWgs - 1) / W, w_last = (x1 * kMlaWgs - 1) / W;
   const int ns = static_cast<int>(w_last - w_first + 1);
   const int64_t row0 = (hg * (kMlaWgs + a.b) + w_first + b) * kMlaHeads + hl;  // partial s: row0 + s * kMlaHeads
   const float* ml = a.part_ml + row0 * 2;
+  const float* po = a.part_o + row0 * DN + 8 * lane;
   // With fewer steps than workgroups some ranges are empty; those workgroups wrote nothing.
-  auto stat_m = [&](int s) {
+  auto live = [&](int s) {
     const int64_t w = w_first + s;
-    return (w + 1) * W / kMlaWgs > w * W / kMlaWgs ? ml[2 * kMlaHeads * s] : -INFINITY;
+    return (w + 1) * W / kMlaWgs > w * W / kMlaWgs;
   };
-  const int lane = threadIdx.x & 63;
-  float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, stat_m(s));
-  M = wave_max(M);
-  float den = 0.0f;
-  for (int s = lane; s < ns; s += 64) {
-    const float m = stat_m(s);
-    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[2 * kMlaHeads * s + 1];
-  }
-  den = wave_sum(den);
-  float num[DN / 256];
-#pragma unroll
-  for (int i = 0; i < DN / 256; ++i) num[i] = 0.0f;
-  const float* po = a.part_o + row0 * DN + threadIdx.x;
-#pragma unroll 4
+  float M0 = -INFINITY, M1 = -INFINITY;
   for (int s = 0; s < ns; ++s) {
-    const float m = stat_m(s);
-    const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
+    if (!live(s)) continue;
+    const float4 st = *reinterpret_cast<const float4*>(ml + 2 * kMlaHeads * s);
+    M0 = fmaxf(M0, st.x);
+    M1 = fmaxf(M1, st.z);
+  }
+  float den0 = 0.0f, den1 = 0.0f, num0[8], num1[8];
 #pragma unroll
-    for (int i = 0; i < DN / 256; ++i) {
-      const float o = po[static_cast<int64_t>(kMlaHeads) * DN * s + 256 * i];
-      num[i] += m == -INFINITY ? 0.0f : wgt * o;
+  for (int i = 0; i < 8; ++i) num0[i] = num1[i] = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float* p = po + static_cast<int64_t>(kMlaHeads) * DN * s;
+    const float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(p + DN), b1 = *reinterpret_cast<const float4*>(p + DN + 4);
+    if (!live(s)) continue;
+    const float4 st = *reinterpret_cast<const float4*>(ml + 2 * kMlaHeads * s);
+    const float w0 = exp2f(st.x - M0), w1 = exp2f(st.z - M1);
+    den0 += w0 * st.y;
+    den1 += w1 * st.w;
+    const float v0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float v1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      num0[i] += w0 * v0[i];
+      num1[i] += w1 * v1[i];
     }
   }
+  auto pack = [](const float (&v)[8], float den) {
+    uint32_t r[4];
 #pragma unroll
-  for (int i = 0; i < DN / 256; ++i)
-    out[(b * a.hq + h) * DN + threadIdx.x + 256 * i] = f32_to_bf16(den > 0.0f ? num[i] / den : 0.0f);
-  if (lse && threadIdx.x == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
+    for (int i = 0; i < 4; ++i)
+      r[i] = static_cast<uint32_t>(f32_to_bf16(den > 0.0f ? v[2 * i] / den : 0.0f)) |
+             (static_cast<uint32_t>(f32_to_bf16(den > 0.0f ? v[2 * i + 1] / den : 0.0f)) << 16);
+    return make_uint4(r[0], r[1], r[2], r[3]);
+  };
+  *o0 = pack(num0, den0);
+  if (two) *o1 = pack(num1, den1);
+  if (lse && lane == 0) {
+    lse[b * a.hq + h0] = den0 > 0.0f ? (M0 + log2f(den0)) * kLn2 : -INFINITY;
+    if (two) lse[b * a.hq + h0 + 1] = den1 > 0.0f ? (M1 + log2f(den1)) * kLn2 : -INFINITY;
+  }
 }
 
 // Workspace: [step prefix int64 x (b + 1), padded to 256 B][part_o][part_ml][flags]
@@ -1354,6 +1377,7 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   const dim3 grid(kMlaWgs);
   mla_decode_kernel<512, 64, false><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
   mla_decode_kernel<512, 64, true><<<grid, 64 * kMlaWaves, kMlaLds, st>>>(a);
-  mla_combine_kernel<512><<<dim3(static_cast<unsigned>(b * hq)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
+  const int64_t combine_wgs = b * ((hq + kMlaCombineHeads - 1) / kMlaCombineHeads);
+  mla_combine_kernel<512><<<dim3(static_cast<unsigned>(combine_wgs)), 256, 0, st>>>(a, static_cast<uint16_t*>(out), lse);
   return launch_status("tai_fia_mla_decode");
 }

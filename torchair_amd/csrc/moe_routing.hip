@@ -154,6 +154,7 @@ struct RouteWs {
   int32_t* hist;      // [bins][chunks]: counts, then exclusive destination offsets
   int32_t* dst2src;   // [n] source slot of each destination row
   int32_t* total;     // [1] rows that fall in the expert range
+  int32_t* bintot;    // [bins] rows per expert
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -167,12 +168,15 @@ inline RouteWs carve_route_ws(void* ws, int64_t n, int64_t bins) {
   r.dst2src = reinterpret_cast<int32_t*>(p);
   p += align256(sizeof(int32_t) * n);
   r.total = reinterpret_cast<int32_t*>(p);
+  p += 256;
+  r.bintot = reinterpret_cast<int32_t*>(p);
   return r;
 }
 
 inline size_t route_ws_bytes(int64_t n, int64_t bins) {
   const int64_t chunks = cdiv(n, kChunk);
-  return align256(sizeof(int32_t) * bins * chunks) + align256(sizeof(int32_t) * n) + 256;
+  return align256(sizeof(int32_t) * bins * chunks) + align256(sizeof(int32_t) * n) + 256 +
+         align256(sizeof(int32_t) * bins);
 }
 
 // K1: per-chunk histogram over experts in [e0, e0 + bins).
@@ -191,47 +195,36 @@ __global__ __launch_bounds__(kChunk) void route_hist_kernel(const int32_t* __res
   for (int b = threadIdx.x; b < bins; b += blockDim.x) hist[static_cast<int64_t>(b) * chunks + blockIdx.x] = h[b];
 }
 
-// K2: one workgroup of 1024 threads. Turns counts into exclusive destination offsets
-// (expert-major, chunk-minor) and writes the per-expert token counts / cumsum. One wave per
-// expert row of the histogram (lanes walk the chunks, coalesced); the per-expert totals are
-// scanned across the block (bins <= 1024: one per thread).
-__global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ hist, int64_t chunks, int bins,
-                                                          int64_t* __restrict__ tokens, int tokens_cumsum,
-                                                          int32_t* __restrict__ total) {
-  extern __shared__ int32_t tot[];  // [bins] totals, then [bins] exclusive bases
-  __shared__ int32_t red[16];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  for (int b = w; b < bins; b += nw) {
-    const int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
-    int32_t sum = 0;
-    for (int64_t c = lane; c < chunks; c += 64) sum += hb[c];
+// K2: one wave per expert. Turns the expert's row of chunk counts into exclusive in-expert offsets
+// (lanes walk the chunks, 64 at a time, all loads of a row issued before the scan) and writes the
+// expert's total. The cross-expert base is added by K3, so no single-workgroup pass sits on the
+// critical path.
+__global__ __launch_bounds__(64) void route_bin_scan_kernel(int32_t* __restrict__ hist, int64_t chunks,
+                                                            int32_t* __restrict__ bintot) {
+  const int lane = threadIdx.x;
+  int32_t* hb = hist + static_cast<int64_t>(blockIdx.x) * chunks;
+  int32_t carry = 0;
+  for (int64_t c0 = 0; c0 < chunks; c0 += 256) {
+    int32_t v[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if (lane == 0) tot[b] = sum;
-  }
-  __syncthreads();
-  const int32_t mine = static_cast<int>(threadIdx.x) < bins ? tot[threadIdx.x] : 0;
-  const int32_t incl = block_incl_scan<false>(mine, red);
-  if (static_cast<int>(threadIdx.x) < bins) tot[bins + threadIdx.x] = incl - mine;
-  if (threadIdx.x == blockDim.x - 1) *total = incl;
-  __syncthreads();
-  for (int b = w; b < bins; b += nw) {
-    int32_t* hb = hist + static_cast<int64_t>(b) * chunks;
-    int32_t carry = tot[bins + b];
-    for (int64_t c0 = 0; c0 < chunks; c0 += 64) {
-      const int64_t c = c0 + lane;
-      const int32_t v = c < chunks ? hb[c] : 0;
-      int32_t x = v;
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + 64 * j + lane;
+      v[j] = c < chunks ? hb[c] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + 64 * j + lane;
+      int32_t x = v[j];
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int32_t u = __shfl_up(x, o, 64);
         if (lane >= o) x += u;
       }
-      if (c < chunks) hb[c] = carry + x - v;
+      if (c < chunks) hb[c] = carry + x - v[j];
       carry += __shfl(x, 63, 64);
     }
-    if (tokens && lane == 0) tokens[b] = tokens_cumsum ? static_cast<int64_t>(carry) : static_cast<int64_t>(tot[b]);
   }
+  if (lane == 0) bintot[blockIdx.x] = carry;
 }
 
 // K3: stable in-chunk rank -> destination row of every slot.
@@ -240,11 +233,16 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ 
 // mode 2 (legacy): row_idx[legacy_row[p]] = dst; eout[dst] = expert.
 __global__ __launch_bounds__(kChunk) void route_place_kernel(const int32_t* __restrict__ eidx, int64_t n, int e0,
                                                              int bins, const int32_t* __restrict__ hist,
+                                                             const int32_t* __restrict__ bintot,
+                                                             int64_t* __restrict__ tokens, int tokens_cumsum,
+                                                             int32_t* __restrict__ total,
                                                              int32_t* __restrict__ dst2src, int mode,
                                                              int32_t* __restrict__ row_idx,
                                                              const int32_t* __restrict__ legacy_row,
                                                              int32_t* __restrict__ eout) {
-  __shared__ int32_t se[kChunk];
+  __shared__ __align__(16) int32_t se[kChunk];
+  __shared__ int32_t base[1024];
+  __shared__ int32_t red[kChunk / 64];
   const int64_t chunks = gridDim.x;
   const int64_t p = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
   int e = -1;
@@ -253,15 +251,42 @@ __global__ __launch_bounds__(kChunk) void route_place_kernel(const int32_t* __re
     if (e < 0 || e >= bins) e = -1;
   }
   se[threadIdx.x] = e;
+  // Exclusive scan of the per-expert totals (bins <= 1024: four per thread, in expert order).
+  int32_t t4[4], s4 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = 4 * static_cast<int>(threadIdx.x) + j;
+    t4[j] = b < bins ? bintot[b] : 0;
+    s4 += t4[j];
+  }
+  const int32_t incl = block_incl_scan<false>(s4, red);
+  int32_t run = incl - s4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = 4 * static_cast<int>(threadIdx.x) + j;
+    if (b < bins) {
+      base[b] = run;
+      if (blockIdx.x == 0 && tokens) tokens[b] = tokens_cumsum ? static_cast<int64_t>(run + t4[j]) : t4[j];
+    }
+    run += t4[j];
+  }
+  if (blockIdx.x == 0 && threadIdx.x == kChunk - 1) *total = incl;
   __syncthreads();
   if (p >= n) return;
   if (e < 0) {
     if (mode == 0) row_idx[p] = -1;
     return;
   }
+  // Stable rank among the chunk's earlier slots of the same expert.
   int rank = 0;
-  for (int i = 0; i < static_cast<int>(threadIdx.x); ++i) rank += (se[i] == e);
-  const int32_t dst = hist[static_cast<int64_t>(e) * chunks + blockIdx.x] + rank;
+  const int me = static_cast<int>(threadIdx.x);
+  int i = 0;
+  for (; i + 4 <= me; i += 4) {
+    const int4 q = *reinterpret_cast<const int4*>(se + i);
+    rank += (q.x == e) + (q.y == e) + (q.z == e) + (q.w == e);
+  }
+  for (; i < me; ++i) rank += (se[i] == e);
+  const int32_t dst = base[e] + hist[static_cast<int64_t>(e) * chunks + blockIdx.x] + rank;
   dst2src[dst] = static_cast<int32_t>(p);
   if (mode == 0) row_idx[p] = dst;
   else if (mode == 1) row_idx[dst] = static_cast<int32_t>(p);
@@ -298,8 +323,16 @@ __global__ __launch_bounds__(256) void route_gather_kernel(const void* __restric
   const int64_t src_row = legacy_row ? static_cast<int64_t>(legacy_row[p]) % t : p / k;
   const char* src = static_cast<const char*>(x) + src_row * row_bytes;
   if ((row_bytes & 15) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ex)) & 15) == 0) {
-    for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
-      *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
+    // Four 16-byte loads in flight per lane before their stores.
+    for (int64_t o = lane * 16; o < row_bytes; o += 4 * 64 * 16) {
+      uint4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (o + j * 1024 < row_bytes) v[j] = *reinterpret_cast<const uint4*>(src + o + j * 1024);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (o + j * 1024 < row_bytes) *reinterpret_cast<uint4*>(dst + o + j * 1024) = v[j];
+    }
   } else {
     for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src[o];
   }
@@ -452,8 +485,9 @@ static int run_routing(const void* x, int elem_bytes, int64_t t, int64_t h, cons
   TAI_CHECK_ARG(chunks < (1ll << 31), "%s: too many slots", name);
   if (n == 0) return TAI_OK;
   route_hist_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, sizeof(int32_t) * bins, st>>>(eidx, n, e0, bins, w.hist);
-  route_scan_kernel<<<1, 1024, sizeof(int32_t) * 2 * bins, st>>>(w.hist, chunks, bins, tokens, tokens_cumsum, w.total);
-  route_place_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, 0, st>>>(eidx, n, e0, bins, w.hist, w.dst2src,
+  route_bin_scan_kernel<<<dim3(static_cast<unsigned>(bins)), 64, 0, st>>>(w.hist, chunks, w.bintot);
+  route_place_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, 0, st>>>(eidx, n, e0, bins, w.hist, w.bintot,
+                                                                          tokens, tokens_cumsum, w.total, w.dst2src,
                                                                           mode, row_idx, legacy_row, eout);
   const int tail_mode = (mode == 1) ? 1 : 0;
   route_gather_kernel<<<dim3(static_cast<unsigned>(cdiv(n, 4))), 256, 0, st>>>(
