@@ -199,32 +199,23 @@ struct DsqArgs {
 
 __device__ __forceinline__ float silu(float a) { return a / (1.0f + expf(-a)); }
 
-// Finds the group of `row` from per-group row counts with a workgroup-wide scan.
-// Returns -1 when the row is past the total.
-__device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, int64_t row, int64_t* sh) {
-  __shared__ int64_t carry;
+// Finds the group of `row` from per-group row counts with a workgroup-wide scan (one count per
+// thread per pass, wave scans joined through LDS). Returns -1 when the row is past the total.
+// Every thread of the workgroup must call it.
+__device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, int64_t row) {
+  __shared__ int64_t red[16];
   __shared__ int64_t found;
-  if (threadIdx.x == 0) { carry = 0; found = -1; }
-  __syncthreads();
+  if (threadIdx.x == 0) found = -1;
+  const int nw = static_cast<int>(blockDim.x >> 6);
+  int64_t carry = 0;
   for (int64_t base = 0; base < ng; base += blockDim.x) {
     const int64_t g = base + threadIdx.x;
-    int64_t c = g < ng ? load_index(counts, dt, g) : 0;
-    sh[threadIdx.x] = c;
+    const int64_t c = g < ng ? load_index(counts, dt, g) : 0;
+    const int64_t end = carry + block_incl_scan<false>(c, red);
+    if (g < ng && row >= end - c && row < end) found = g;
+    for (int i = 0; i < nw; ++i) carry += red[i];
     __syncthreads();
-    // Hillis-Steele inclusive scan over blockDim.x entries.
-    for (int o = 1; o < static_cast<int>(blockDim.x); o <<= 1) {
-      int64_t add = threadIdx.x >= static_cast<unsigned>(o) ? sh[threadIdx.x - o] : 0;
-      __syncthreads();
-      sh[threadIdx.x] += add;
-      __syncthreads();
-    }
-    const int64_t end = carry + sh[threadIdx.x];
-    const int64_t begin = end - c;
-    if (g < ng && row >= begin && row < end) found = g;
-    __syncthreads();
-    if (threadIdx.x == blockDim.x - 1) carry = end;
-    __syncthreads();
-    if (found >= 0) break;
+    if (found >= 0 || carry > row) break;
   }
   return found;
 }
@@ -232,14 +223,24 @@ __device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, i
 // One workgroup of 256 threads per row; each thread owns NV groups of 4 output columns.
 template <int NV>
 __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
-  __shared__ int64_t scan[256];
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t n = a.n, n2 = 2 * a.n;
-  int64_t g = 0;
-  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row, scan);
   const int64_t ng4 = n / 4;
+  const int32_t* xr = a.x + row * n2;
+  // The row's int32 values do not depend on its group: their loads go out before the lookup.
+  int4 xa[NV], xb[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    if (c < ng4) {
+      xa[i] = *reinterpret_cast<const int4*>(xr + 4 * c);
+      xb[i] = *reinterpret_cast<const int4*>(xr + n + 4 * c);
+    }
+  }
+  int64_t g = 0;
+  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row);
   if (g < 0) {  // row beyond the grouped rows
     for (int64_t c = tid; c < ng4; c += 256)
       *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = 0u;
@@ -251,7 +252,6 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
   const float act = a.as ? a.as[row] : 1.0f;
   const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
   const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
-  const int32_t* xr = a.x + row * n2;
 
   float v[NV][4];
   float amax = 0.0f;
@@ -260,9 +260,7 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
     const int64_t c = tid + static_cast<int64_t>(i) * 256;
     if (c < ng4) {
       const int64_t j = 4 * c;
-      int4 xa = *reinterpret_cast<const int4*>(xr + j);
-      int4 xb = *reinterpret_cast<const int4*>(xr + n + j);
-      int ia[4] = {xa.x, xa.y, xa.z, xa.w}, ib[4] = {xb.x, xb.y, xb.z, xb.w};
+      int ia[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w}, ib[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
       if (bi) {
         int4 ba = *reinterpret_cast<const int4*>(bi + j), bb = *reinterpret_cast<const int4*>(bi + n + j);
         ia[0] += ba.x; ia[1] += ba.y; ia[2] += ba.z; ia[3] += ba.w;
@@ -307,12 +305,11 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
 
 // Any n: two passes over global memory.
 __global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
-  __shared__ int64_t scan[256];
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int64_t n = a.n, n2 = 2 * a.n;
   int64_t g = 0;
-  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row, scan);
+  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row);
   if (g < 0) {
     for (int64_t c = threadIdx.x; c < n; c += blockDim.x) a.y[row * n + c] = 0;
     if (threadIdx.x == 0) a.scale[row] = 0.0f;
