@@ -20,6 +20,8 @@
 
 namespace tai {
 namespace {
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -686,6 +688,30 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     nk = nk - kbeg < g.k_per ? nk - kbeg : g.k_per;
     gout = static_cast<int32_t*>(g.out) + ks * g.m * g.n;
   }
+  // Epilogue operands of a full-width wave tile are loaded before the main loop, and ahead of the
+  // ring's first stages (whose waits count loads in issue order), so their latency is hidden: the
+  // per-column scales and biases, and one per-token scale per lane (the wave's row wm * 64 + lane),
+  // handed to the lanes that need it by a cross-lane read.
+  const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32)
+                              ? static_cast<const int32_t*>(g.bias) + e * g.bias_group_stride : nullptr;
+  const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32)
+                            ? static_cast<const float*>(g.bias) + e * g.bias_group_stride : nullptr;
+  const float* scl = g.scale ? g.scale + e * g.scale_group_stride : nullptr;
+  const int64_t wcol0 = n0 + wn * 128;
+  const bool full_width = wcol0 + 128 <= g.n;
+  float my_pt = 1.0f;
+  int32_t bcol[4];
+  float sc[4], bf[4];
+  if constexpr (OUT != kOutSwiglu) {
+    if (OUT != TAI_DT_INT32 && g.pts && full_width) my_pt = g.pts[row0 + min(wm * 64 + lane, rows - 1)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = wcol0 + j * 32 + (lane & 31);
+      bcol[j] = (bias_i && full_width) ? bias_i[col] : 0;
+      sc[j] = (scl && full_width) ? scl[g.scale_len == 1 ? 0 : col] : 1.0f;
+      bf[j] = (bias_f && full_width) ? bias_f[col] : -0.0f;
+    }
+  }
   const int64_t kb0 = kbeg * kBigBK;
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s)
@@ -817,73 +843,75 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     return;
   }
   // Epilogue, specialised on the output dtype so the accumulators stay in registers.
-  const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32)
-                              ? static_cast<const int32_t*>(g.bias) + e * g.bias_group_stride : nullptr;
-  const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32)
-                            ? static_cast<const float*>(g.bias) + e * g.bias_group_stride : nullptr;
-  const float* scl = g.scale ? g.scale + e * g.scale_group_stride : nullptr;
+  // value of accumulator (i, j, r) as fp32 after the scales and fp32 bias; absent operands hold
+  // their neutral values (1.0, 1.0, -0.0: x * 1 and x + (-0) are x for every x, signed zeros
+  // included), so no per-element selects are needed
+  auto out_f32 = [&](int32_t v, float sc, float bf, float pt) -> float {
+    return (static_cast<float>(v) * sc) * pt + bf;
+  };
   // value of accumulator (i, j, r) in the output type, as raw bits (pt: the row's per-token scale)
   auto out_bits = [&](int32_t v, float sc, float bf, float pt) -> uint32_t {
     if constexpr (OUT == TAI_DT_INT32) {
       return static_cast<uint32_t>(v);
     } else {
-      float f = static_cast<float>(v);
-      if (scl) f = f * sc;
-      if (g.pts) f = f * pt;
-      if (bias_f) f = f + bf;
+      const float f = out_f32(v, sc, bf, pt);
       if constexpr (OUT == TAI_DT_BF16) return f32_to_bf16(f);
       else if constexpr (OUT == TAI_DT_FP16) return f32_to_f16(f);
       else return __float_as_uint(f);
     }
   };
-  const int64_t wcol0 = n0 + wn * 128;
-  if (wcol0 + 128 <= g.n) {
+  if (full_width) {
     // Full-width wave tile: 16-row slices go through a wave-private LDS region (the ring is free
     // once every wave is past its last stage) and leave as 16-byte stores along the rows, instead
     // of one 2- or 4-byte store per element.
     constexpr int ES = (OUT == TAI_DT_BF16 || OUT == TAI_DT_FP16) ? 2 : 4;
     constexpr int RB = 128 * ES + 16;  // LDS row bytes (padding moves the second lane half's row)
     static_assert(8 * 16 * RB <= C::kLds, "epilogue staging must fit in the ring");
-    // per-token scales of this lane's 32 accumulator rows, loaded before any store (loads issued
-    // behind stores would wait for them: vmcnt retires in order)
-    float pt[2][2][8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-          const int lr = wm * 64 + i * 32 + 16 * h + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
-          pt[i][h][rr] = (OUT != TAI_DT_INT32 && g.pts) ? g.pts[row0 + min(lr, rows - 1)] : 1.0f;
-        }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     char* wreg = reinterpret_cast<char*>(smem) + w * (16 * RB);
-    int32_t bcol[4];
-    float sc[4], bf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = wcol0 + j * 32 + (lane & 31);
-      bcol[j] = bias_i ? bias_i[col] : 0;
-      sc[j] = scl ? scl[g.scale_len == 1 ? 0 : col] : 1.0f;
-      bf[j] = bias_f ? bias_f[col] : 0.0f;
-    }
     constexpr int LPR = 128 * ES / 16;  // lanes per row when reading 16 bytes each
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // accumulator rows of this slice: r = 8h .. 8h+7, local row 8((r&7)>>2) + 4(lane>>5) + (r&3)
+        float pt[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int rr = 0; rr < 8; ++rr)
+          pt[rr] = __shfl(my_pt, i * 32 + 16 * h + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3), 64);
+        if constexpr (OUT == TAI_DT_BF16) {
+          // Two rows of a lane pair (columns c, c + 1) become one bf16x2 word per lane: the even
+          // lane takes row r's pair, the odd lane row r + 1's; one DPP swap, one
+          // v_cvt_pk_bf16_f32 (round to nearest even) and one 4-byte LDS write per two outputs.
+          const bool odd = lane & 1;
 #pragma unroll
-          for (int rr = 0; rr < 8; ++rr) {
-            const int r = 8 * h + rr;
-            const int sl = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
-            const uint32_t bits = out_bits(acc[i][j][r] + bcol[j], sc[j], bf[j], pt[i][h][rr]);
-            char* dst = wreg + sl * RB + (j * 32 + (lane & 31)) * ES;
-            if constexpr (ES == 2) *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(bits);
-            else *reinterpret_cast<uint32_t*>(dst) = bits;
-          }
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 8; rr += 2) {
+              const int r = 8 * h + rr;
+              const float f0 = out_f32(acc[i][j][r] + bcol[j], sc[j], bf[j], pt[rr]);
+              const float f1 = out_f32(acc[i][j][r + 1] + bcol[j], sc[j], bf[j], pt[rr + 1]);
+              const float send = odd ? f0 : f1;
+              const float recv =
+                  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));
+              bf16x2_t pk = __builtin_convertvector((f32x2_t){odd ? recv : f0, odd ? f1 : recv}, bf16x2_t);
+              const int sl = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3) + (odd ? 1 : 0);
+              char* dst = wreg + sl * RB + (j * 32 + (lane & 30)) * ES;
+              *reinterpret_cast<uint32_t*>(dst) = __builtin_bit_cast(uint32_t, pk);
+            }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+              const int r = 8 * h + rr;
+              const int sl = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+              const uint32_t bits = out_bits(acc[i][j][r] + bcol[j], sc[j], bf[j], pt[rr]);
+              char* dst = wreg + sl * RB + (j * 32 + (lane & 31)) * ES;
+              if constexpr (ES == 2) *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(bits);
+              else *reinterpret_cast<uint32_t*>(dst) = bits;
+            }
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int q = 0; q < 16 / (64 / LPR); ++q) {
@@ -906,7 +934,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     const int64_t ccol = colok ? col : 0;
     const int32_t bcol = bias_i ? bias_i[ccol] : 0;
     const float sc = scl ? scl[g.scale_len == 1 ? 0 : ccol] : 1.0f;
-    const float bf = bias_f ? bias_f[ccol] : 0.0f;
+    const float bf = bias_f ? bias_f[ccol] : -0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
