@@ -79,7 +79,9 @@ __global__ __launch_bounds__(256) void dynamic_quant_kernel(
   __shared__ float red[RPB][TPR / 64];
   const int sub = threadIdx.x / TPR;
   const int lane = threadIdx.x % TPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + sub;
+  // Rows are taken last to first: an input just written front to back by the previous kernel (the
+  // routing gather) has its last rows still in the memory-side cache, so they are read first.
+  const int64_t row = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * RPB + sub;
   const bool active = row < rows;
   const int64_t nvec = cols / kVec;
 
