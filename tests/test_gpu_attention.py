@@ -70,6 +70,12 @@ def test_paged_decode_shapes(hq, hkv, d):
     _check_decode([1, 33, 300, 0, 257], hq, hkv, d, 64, 102)
 
 
+def test_paged_decode_segments_longer_than_a_page_window():
+    # 128 kv heads leave 8 step ranges, so a range covers ~74 pages of 32 tokens: the per-lane
+    # block-table window (64 pages) has to move inside a segment
+    _check_decode([12000, 7000, 0, 1], 128, 128, 64, 32, 104)
+
+
 def test_paged_decode_bnsd_cache_and_list_lengths():
     _check_decode([77, 130, 512], 8, 2, 128, 32, 103, cache_layout="BNSD", api="npu", lse=True)
 

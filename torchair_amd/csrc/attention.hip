@@ -2,6 +2,7 @@
 // MLA absorbed decode over an int8 latent cache.
 #include "common.h"
 
+#include <algorithm>
 #include <utility>
 
 namespace tai {
@@ -22,22 +23,19 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
 // ============================================================================ paged GQA decode
-// Work unit = (sequence b, kv head, split of kChunk tokens), one wave each. Per 32-token step:
+// Work: the batch's 32-token steps are cut into equal contiguous ranges; each (range, kv head) is
+// one wave, which runs a segment per sequence its range touches. Per 32-token step:
 //   the step's K and V rows go global -> LDS (global_load_lds, whole 256-byte rows per 16 lanes)
 //   through a ring, one step ahead of their use; S^T = K Q^T with v_mfma_f32_16x16x32_bf16
 //   (rows = 16 tokens, columns = the G query heads of this kv head padded to 16). S^T leaves each
 //   lane with four tokens of one head, so the online softmax needs two cross-lane reductions,
 //   and P^T is already the B operand of O^T = V^T P^T; V is read transposed with
 //   ds_read_b64_tr_b16.
-// Each unit writes an unnormalised partial (O, running max, running sum); a second kernel
-// merges the splits of each (b, head) and writes bf16 output and the logsumexp.
-#ifndef TAI_DECODE_CHUNK
-#define TAI_DECODE_CHUNK 512
-#endif
+// Each segment writes an unnormalised partial (O, running max, running sum); a second kernel
+// merges the partials of each (b, head) and writes bf16 output and the logsumexp.
 #ifndef TAI_DECODE_VSTAGES
 #define TAI_DECODE_VSTAGES 2
 #endif
-constexpr int kChunk = TAI_DECODE_CHUNK;  // tokens per split (multiple of the 32-token step)
 constexpr int kStep = 32;
 constexpr int kVStages = TAI_DECODE_VSTAGES;  // K/V ring stages of one step each
 
@@ -53,10 +51,31 @@ struct DecodeArgs {
   int hq, hkv, g;
   int bs;
   float scale_log2;  // softmax scale * log2(e)
-  int nsplit;
-  float* part_o;  // [b, hkv, nsplit, 16, D]
-  float* part_ml; // [b, hkv, nsplit, 16, 2]
+  int nranges;     // step ranges of a launch (one wave per range and kv head)
+  int64_t* steps;  // [0] = all steps of the batch, [1 + b] = steps before sequence b
+  float* part_o;   // [slot, hkv, 16, D], slot = range + sequence
+  float* part_ml;  // [slot, hkv, 16, 2]
 };
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 template <int D>
 struct DecodeTile {
@@ -70,29 +89,21 @@ struct DecodeTile {
   __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ ((row >> kRsh) & kXm)); }
 };
 
-template <int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
-void paged_decode_kernel(DecodeArgs a) {
-  using T = DecodeTile<D>;
-  __shared__ __attribute__((aligned(16))) char s_kv[kVStages * 2 * T::kStage];  // [stage][K, V]
-  const int lane = threadIdx.x;
-  // Launch order (b, split, kv head): the kv heads of one token range run together, so the
-  // cache rows of a token (all heads adjacent in the BSH layout) are read at about the same time.
-  const int kvh = static_cast<int>(blockIdx.x % a.hkv);
-  const int split = static_cast<int>((blockIdx.x / a.hkv) % a.nsplit);
-  const int64_t b = blockIdx.x / (static_cast<int64_t>(a.hkv) * a.nsplit);
-  const int64_t unit = (b * a.hkv + kvh) * a.nsplit + split;  // partial index (merge kernel order)
-  const int64_t L = a.lens[b];
-  const int64_t t_begin = static_cast<int64_t>(split) * kChunk;
-  const int64_t t_end = min<int64_t>(L, t_begin + kChunk);
-  const int hcol = lane & 15, kg = lane >> 4;
+typedef __attribute__((address_space(3))) char lds_char_t;
 
+__device__ __forceinline__ int64_t dec_steps(int64_t len) { return len > 0 ? (len + kStep - 1) / kStep : 0; }
+
+// One segment: tokens [t_begin, t_end) of sequence b for kv head kvh, written as the partial of
+// the given slot.
+template <int D>
+__device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* s_kv, int64_t b, int kvh, int64_t t_begin,
+                                               int64_t t_end, int64_t slot) {
+  using T = DecodeTile<D>;
+  const int lane = threadIdx.x;
+  const int hcol = lane & 15, kg = lane >> 4;
+  const int64_t unit = slot * a.hkv + kvh;
   float* po = a.part_o + unit * 16 * D;
   float* pml = a.part_ml + unit * 32;
-  if (t_begin >= t_end) {  // empty split: a neutral partial
-    if (lane < 16) { pml[2 * lane] = -INFINITY; pml[2 * lane + 1] = 0.0f; }
-    return;
-  }
 
   // Q^T fragments (B operand): head = hcol (padded to 16), d slots 32m + 8kg .. +8
   bf16x8 qf[D / 32];
@@ -111,29 +122,37 @@ void paged_decode_kernel(DecodeArgs a) {
   const uint16_t* kbase = a.k + static_cast<int64_t>(kvh) * a.sh;
   const uint16_t* vbase = a.v + static_cast<int64_t>(kvh) * a.sh;
   const int32_t* btrow = a.bt + b * a.max_blocks;
-  // The split's block-table entries, one per lane, fetched once (a split spans at most
-  // kChunk / bs + 1 <= 9 pages, as the host requires bs % 32 == 0); pages are then broadcast with
-  // ds_bpermute. Offsets inside the split are 32-bit; a power-of-two bs divides by shifting.
+  // A window of 64 block-table entries, one per lane, broadcast with ds_bpermute; it moves on (a
+  // rare, draining load) when a step lies past it. Offsets inside the segment are 32-bit; a
+  // power-of-two bs divides by shifting.
   const int bs = a.bs;
   const int bs_shift = (bs & (bs - 1)) == 0 ? __builtin_ctz(bs) : -1;
   const int64_t pg0 = t_begin / bs;
-  const int off0 = static_cast<int>(t_begin - pg0 * bs);  // slot of the split's first token
-  const int npg = static_cast<int>((t_end - 1) / bs - pg0 + 1);
-  const int my_page = lane < npg ? btrow[pg0 + lane] : 0;
+  const int off0 = static_cast<int>(t_begin - pg0 * bs);  // slot of the segment's first token
+  int wb = 0;                                              // window base (pages after pg0)
+  auto load_window = [&]() {
+    const int64_t pg = pg0 + wb + lane;
+    return pg < a.max_blocks ? btrow[pg] : 0;
+  };
+  int my_page = load_window();
   // A step never straddles a page (bs % 32 == 0 and steps start at multiples of 32), so one
   // lookup per step gives the element offset of the step's first token.
   auto step_base = [&](int s) -> int64_t {
     const int x = s * kStep + off0;
     const int pi = bs_shift >= 0 ? (x >> bs_shift) : x / bs;
-    const int slot = x - pi * bs;
-    return static_cast<int64_t>(__shfl(my_page, pi, 64)) * a.sb + static_cast<int64_t>(slot) * a.ss;
+    if (pi - wb >= 64) {
+      wb = pi;
+      my_page = load_window();
+    }
+    const int slot_in_page = x - pi * bs;
+    return static_cast<int64_t>(__shfl(my_page, pi - wb, 64)) * a.sb + static_cast<int64_t>(slot_in_page) * a.ss;
   };
   const int n_local = static_cast<int>(t_end - t_begin);
 
   const int nsteps = static_cast<int>((t_end - t_begin + kStep - 1) / kStep);
   // K and V rows of a step both go global -> LDS ([K tile][V tile] per ring stage).
   auto issue_kv = [&](int s) __attribute__((always_inline)) {
-    char* st = s_kv + (s % kVStages) * 2 * T::kStage;
+    lds_char_t* st = s_kv + (s % kVStages) * 2 * T::kStage;
     const int64_t sbase = step_base(s);
     const int last = n_local - 1 - s * kStep;
 #pragma unroll
@@ -151,7 +170,7 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < kAhead; ++i)
     if (i < nsteps) issue_kv(i);
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)s_kv));
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_kv));
   for (int s = 0; s < nsteps; ++s) {
     if (s + kAhead < nsteps) issue_kv(s + kAhead);
     {
@@ -246,47 +265,144 @@ void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Merge the splits of one (b, q head): one workgroup of D threads. Every wave reduces the split
-// maxima and sums itself (lane s holds split s, s + 64, ...), so no workgroup barrier is needed;
-// the numerator loop has no data-dependent branch, so its loads are issued back to back.
+
+// Balanced launch: the batch's 32-token steps (sequence major) are cut into a.nranges equal
+// contiguous ranges, and each range is run by hkv single-wave workgroups, one per kv head, launched
+// next to each other (the cache rows of a token hold all its kv heads, so they are read at about
+// the same time). A wave runs one segment per sequence its range touches. The first wave also
+// records the step prefix the merge uses to find a sequence's partials.
+template <int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+void paged_decode_kernel(DecodeArgs a) {
+  using T = DecodeTile<D>;
+  __shared__ __attribute__((aligned(16))) char s_kv[kVStages * 2 * T::kStage];  // [stage][K, V]
+  const int lane = threadIdx.x;
+  const int kvh = static_cast<int>(blockIdx.x % a.hkv);
+  const int64_t r = blockIdx.x / a.hkv;
+  const int64_t nb = a.b, R = a.nranges;
+  int64_t mine = 0;
+  for (int64_t c = lane; c < nb; c += 64) mine += dec_steps(a.lens[c]);
+  const int64_t S = uniform64(wave_sum64(mine));
+  if (blockIdx.x == 0) {
+    int64_t carry = 0;
+    for (int64_t c = 0; c < nb; c += 64) {
+      const int64_t i = c + lane;
+      const int64_t n = i < nb ? dec_steps(a.lens[i]) : 0;
+      const int64_t incl = wave_incl_scan64(n, lane) + carry;
+      if (i < nb) a.steps[1 + i] = incl - n;
+      carry = __shfl(incl, 63, 64);
+    }
+    if (lane == 0) a.steps[0] = S;
+  }
+  const int64_t g0 = r * S / R, g1 = (r + 1) * S / R;
+  if (g0 >= g1) return;
+  // the range's first sequence b (steps before it: pb) and step x = g0 inside the batch
+  int64_t x = g0, b = 0, pb = 0;
+  {
+    int64_t carry = 0;
+    for (int64_t c = 0; c < nb; c += 64) {
+      const int64_t i = c + lane;
+      const int64_t n = i < nb ? dec_steps(a.lens[i]) : 0;
+      const int64_t incl = wave_incl_scan64(n, lane) + carry;
+      const uint64_t hit = __ballot(i < nb && n > 0 && incl - n <= x && x < incl);
+      if (hit) {
+        const int j = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+        b = c + j;
+        pb = __shfl(incl - n, j, 64);
+        break;
+      }
+      carry = __shfl(incl, 63, 64);
+    }
+  }
+  b = uniform64(b);
+  pb = uniform64(pb);
+  for (int64_t g = g0; g < g1;) {
+    const int64_t len = a.lens[b];
+    const int64_t n = dec_steps(len);
+    const int64_t seg = min(g1 - g, pb + n - x);
+    const int64_t t_begin = (x - pb) * kStep;
+    decode_segment<D>(a, (lds_char_t*)s_kv, b, kvh, t_begin, min(len, t_begin + seg * kStep), r + b);
+    g += seg;
+    x += seg;
+    if (x == pb + n) {  // on to the next non-empty sequence
+      pb += n;
+      do {
+        ++b;
+      } while (g < g1 && b < nb && dec_steps(a.lens[b]) == 0);
+    }
+  }
+}
+
+// Merge the partials of (b, q head) pairs: one wave per head, four per workgroup, each lane owning
+// D / 64 consecutive d. The partials are those of the ranges that cover the sequence's steps
+// (ranges with no steps wrote nothing). A partial's statistics are wave-uniform loads and its O
+// values do not depend on them, so all loads of a partial go out together.
 template <int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint16_t* out, float* lse) {
-  const int64_t bh = blockIdx.x;
+  constexpr int E = D / 64;  // outputs per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t bh = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (bh >= a.b * a.hq) return;
   const int h = static_cast<int>(bh % a.hq);
   const int64_t b = bh / a.hq;
   const int kvh = h / a.g, hi = h % a.g;
-  const int64_t base = (b * a.hkv + kvh) * a.nsplit;
-  const int64_t L = a.lens[b];
-  const int ns = static_cast<int>(min<int64_t>(a.nsplit, (L + kChunk - 1) / kChunk));
-  const float* ml = a.part_ml + base * 32 + 2 * hi;  // split s: ml[32 s], ml[32 s + 1]
-  const int lane = threadIdx.x & 63;
+  const int64_t n = dec_steps(a.lens[b]);
+  uint16_t* o = out + (b * a.hq + h) * D + E * lane;
+  if (n == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0;
+    if (lse && lane == 0) lse[b * a.hq + h] = -INFINITY;
+    return;
+  }
+  const int64_t S = a.steps[0], R = a.nranges;
+  const int64_t x0 = a.steps[1 + b], x1 = x0 + n;
+  const int64_t r_first = ((x0 + 1) * R - 1) / S, r_last = (x1 * R - 1) / S;
+  const int ns = static_cast<int>(r_last - r_first + 1);
+  const int64_t row0 = ((r_first + b) * a.hkv + kvh) * 16 + hi;  // partial s: row0 + s * hkv * 16
+  const int64_t rstep = static_cast<int64_t>(a.hkv) * 16;
+  auto live = [&](int s) {
+    const int64_t r = r_first + s;
+    return (r + 1) * S / R > r * S / R;
+  };
   float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, ml[32 * s]);
-  M = wave_max(M);
-  float den = 0.0f;
-  for (int s = lane; s < ns; s += 64) {
-    const float m = ml[32 * s];
-    den += m == -INFINITY ? 0.0f : exp2f(m - M) * ml[32 * s + 1];
+  for (int s = 0; s < ns; ++s)
+    if (live(s)) M = fmaxf(M, a.part_ml[(row0 + rstep * s) * 2]);
+  float den = 0.0f, num[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) num[e] = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const int64_t row = row0 + rstep * s;
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = a.part_o[row * D + E * lane + e];
+    if (!live(s)) continue;
+    const float w = exp2f(a.part_ml[row * 2] - M);
+    den += w * a.part_ml[row * 2 + 1];
+#pragma unroll
+    for (int e = 0; e < E; ++e) num[e] += w * v[e];
   }
-  den = wave_sum(den);
-  const int d = threadIdx.x;
-  if (d < D) {
-    const float* po = a.part_o + (base * 16 + hi) * D + d;  // split s: po[16 D s]
-    float num = 0.0f;
-#pragma unroll 4
-    for (int s = 0; s < ns; ++s) {
-      const float m = ml[32 * s];
-      const float o = po[static_cast<int64_t>(16 * D) * s];
-      num += m == -INFINITY ? 0.0f : exp2f(m - M) * o;
-    }
-    out[(b * a.hq + h) * D + d] = f32_to_bf16(den > 0.0f ? num / den : 0.0f);
-  }
-  if (lse && d == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[e] = f32_to_bf16(den > 0.0f ? num[e] / den : 0.0f);
+  if (lse && lane == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
 
-size_t decode_ws(int64_t b, int hkv, int d, int nsplit) {
-  return static_cast<size_t>(b) * hkv * nsplit * (16 * d + 32) * sizeof(float);
+// Ranges per launch: about 1024 single-wave workgroups (four per CU: the 32 KB ring puts two in
+// each 80 KB half of a CU's LDS).
+inline int decode_ranges(int hkv) { return static_cast<int>(cdiv(1024, hkv)); }
+
+// Workspace: [step prefix int64 x (b + 1), padded to 256 B][part_o][part_ml]
+struct DecWs {
+  size_t part_o, part_ml, total;
+};
+DecWs dec_ws(int64_t b, int hkv, int d) {
+  const int64_t slots = decode_ranges(hkv) + b;
+  DecWs w;
+  w.part_o = (static_cast<size_t>(b + 1) * sizeof(int64_t) + 255) / 256 * 256;
+  w.part_ml = w.part_o + static_cast<size_t>(slots) * hkv * 16 * d * sizeof(float);
+  w.total = w.part_ml + static_cast<size_t>(slots) * hkv * 32 * sizeof(float);
+  return w;
 }
+
 
 
 // ============================================================================ dense prefill
@@ -1043,26 +1159,6 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
 
 __device__ __forceinline__ int64_t mla_steps(int64_t len) { return len > 0 ? (len + kMlaStep - 1) / kMlaStep : 0; }
 
-__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ int64_t wave_incl_scan64(int64_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
-__device__ __forceinline__ int64_t uniform64(int64_t v) {
-  const uint64_t u = static_cast<uint64_t>(v);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
 // The kMlaWgs workgroups of a launch split all 32-token steps (head group major, then sequence)
 // into equal contiguous ranges, so every CU gets the same work whatever the lengths; a workgroup
 // runs one segment per sequence its range touches. Workgroup 0 of the fast pass also records the
@@ -1235,10 +1331,13 @@ MlaWs mla_ws(int64_t b, int hq, int dn) {
 using namespace tai;
 
 extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, int64_t max_blocks, int block_size) {
-  (void)hq;
-  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kChunk));
-  // sized for hkv == hq (the largest the kernel can be asked for)
-  return decode_ws(b, hq, d, nsplit) + 256;
+  (void)max_blocks;
+  (void)block_size;
+  // the largest over the kv head counts hq allows
+  size_t need = 0;
+  for (int hkv = 1; hkv <= hq; ++hkv)
+    if (hq % hkv == 0) need = std::max(need, dec_ws(b, hkv, d).total);
+  return need;
 }
 
 extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block,
@@ -1254,10 +1353,9 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
                 "tai_fia_paged_decode: cache strides must keep 16-byte alignment");
   if (b == 0) return TAI_OK;
   TAI_CHECK_ARG(q && k_cache && v_cache && block_table && seq_lens_kv && out, "tai_fia_paged_decode: null pointer");
-  const int nsplit = static_cast<int>(cdiv(max_blocks * block_size, kChunk));
-  const size_t need = decode_ws(b, hkv, d, nsplit);
-  if (workspace == nullptr || ws_bytes < need) {
-    set_error("tai_fia_paged_decode: workspace of %zu bytes, need %zu", ws_bytes, need);
+  const DecWs wl = dec_ws(b, hkv, d);
+  if (workspace == nullptr || ws_bytes < wl.total) {
+    set_error("tai_fia_paged_decode: workspace of %zu bytes, need %zu", ws_bytes, wl.total);
     return TAI_ERR_WORKSPACE;
   }
   DecodeArgs a;
@@ -1268,21 +1366,22 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
   a.bt = block_table; a.max_blocks = max_blocks; a.lens = seq_lens_kv;
   a.b = b; a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.bs = block_size;
   a.scale_log2 = scale * kLog2e;
-  a.nsplit = nsplit;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + static_cast<size_t>(b) * hkv * nsplit * 16 * d;
+  a.nranges = decode_ranges(hkv);
+  a.steps = static_cast<int64_t*>(workspace);
+  a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_o);
+  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_ml);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(b * hkv * nsplit));
-  const dim3 cgrid(static_cast<unsigned>(b * hq));
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nranges) * hkv));
+  const dim3 cgrid(static_cast<unsigned>(cdiv(b * hq, 4)));
   uint16_t* o = static_cast<uint16_t*>(out);
   switch (d) {
     case 64:
       paged_decode_kernel<64><<<grid, 64, 0, st>>>(a);
-      decode_combine_kernel<64><<<cgrid, 64, 0, st>>>(a, o, lse);
+      decode_combine_kernel<64><<<cgrid, 256, 0, st>>>(a, o, lse);
       break;
     case 128:
       paged_decode_kernel<128><<<grid, 64, 0, st>>>(a);
-      decode_combine_kernel<128><<<cgrid, 128, 0, st>>>(a, o, lse);
+      decode_combine_kernel<128><<<cgrid, 256, 0, st>>>(a, o, lse);
       break;
     default:
       paged_decode_kernel<256><<<grid, 64, 0, st>>>(a);
