@@ -710,6 +710,7 @@ struct MlaArgs {
   float* part_o;   // [slots, kMlaHeads, DN]
   float* part_ml;  // [slots, kMlaHeads, 2]
   int32_t* flags;  // [slots, kMlaWaves]: 1 = that wave's heads need the rescaling pass
+  int32_t* wgflags;  // [kMlaWgs, kMlaWaves]: 1 = some segment of that workgroup's wave was flagged
   int64_t* steps;  // [0] = 32-token steps of all sequences S, [1 + b] = steps before sequence b
 };
 
@@ -792,7 +793,7 @@ __device__ __forceinline__ void lds_wait() {
 // One segment: tokens [t_begin, t_end) of sequence b for head group hg, partial written to slot
 // `slot` (rows of kMlaHeads heads). Every wave of the workgroup runs it with the same arguments.
 template <int DN, int DR, bool RESCALE>
-__device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg, int64_t b, int64_t t_begin,
+__device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, bool& ov_seen, int hg, int64_t b, int64_t t_begin,
                                             int64_t t_end, int64_t slot) {
   static_assert(DN == 512 && DR == 64, "MLA shape");
   constexpr int NQ = (DN + DR) / 16;  // Q^T fragments: 32 nope + 4 rope
@@ -1140,6 +1141,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, int hg
   if constexpr (!RESCALE) {
     const bool any_ov = __any(overflow);
     if (lane == 0) a.flags[slot * kMlaWaves + w] = any_ov ? 1 : 0;
+    ov_seen = ov_seen || any_ov;
   }
   if (!head_ok) return;
   if constexpr (!RESCALE) mfma_drain(acc);
@@ -1169,11 +1171,17 @@ void mla_decode_kernel(MlaArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int lane = threadIdx.x & 63;
   const int64_t nb = a.b;
+  const int64_t wg = blockIdx.x;
+  int32_t* wgflag = a.wgflags + wg * kMlaWaves + (threadIdx.x >> 6);
+  if constexpr (RESCALE) {  // nothing flagged in this workgroup's range: done
+    const int4 f = *reinterpret_cast<const int4*>(a.wgflags + wg * kMlaWaves);
+    if ((f.x | f.y | f.z | f.w) == 0) return;
+  }
+  bool ov_seen = false;
   int64_t mine = 0;
   for (int64_t c = lane; c < nb; c += 64) mine += mla_steps(a.lens[c]);
   const int64_t S = uniform64(wave_sum64(mine));
   const int64_t W = S * a.hgroups;
-  const int64_t wg = blockIdx.x;
   if (!RESCALE && wg == 0 && threadIdx.x < 64) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
@@ -1186,7 +1194,10 @@ void mla_decode_kernel(MlaArgs a) {
     if (lane == 0) a.steps[0] = S;
   }
   const int64_t g0 = wg * W / kMlaWgs, g1 = (wg + 1) * W / kMlaWgs;
-  if (g0 >= g1) return;
+  if (g0 >= g1) {
+    if (!RESCALE && lane == 0) *wgflag = 0;
+    return;
+  }
   // the range's first sequence: head group g0 / S, step x = g0 % S inside it
   int hg = static_cast<int>(g0 / S);
   int64_t x = g0 % S, b = 0, pb = 0;
@@ -1219,7 +1230,7 @@ void mla_decode_kernel(MlaArgs a) {
       const int32_t* f = a.flags + slot * kMlaWaves;
       run = (f[0] | f[1] | f[2] | f[3]) != 0;
     }
-    if (run) mla_segment<DN, DR, RESCALE>(a, smem, hg, b, t_begin, min(len, t_begin + seg * kMlaStep), slot);
+    if (run) mla_segment<DN, DR, RESCALE>(a, smem, ov_seen, hg, b, t_begin, min(len, t_begin + seg * kMlaStep), slot);
     g += seg;
     x += seg;
     if (x == pb + n) {  // on to the next non-empty sequence (the next head group after the last)
@@ -1229,6 +1240,7 @@ void mla_decode_kernel(MlaArgs a) {
       } while (g < g1 && mla_steps(a.lens[b]) == 0);
     }
   }
+  if (!RESCALE && lane == 0) *wgflag = ov_seen ? 1 : 0;
 }
 
 // Merge the partials of a sequence's heads: one wave per pair of heads (each lane owns 8
@@ -1311,9 +1323,9 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   }
 }
 
-// Workspace: [step prefix int64 x (b + 1), padded to 256 B][part_o][part_ml][flags]
+// Workspace: [step prefix int64 x (b + 1), padded to 256 B][part_o][part_ml][flags][workgroup flags]
 struct MlaWs {
-  size_t steps, part_o, part_ml, flags, total;
+  size_t steps, part_o, part_ml, flags, wgflags, total;
 };
 MlaWs mla_ws(int64_t b, int hq, int dn) {
   const int64_t slots = ((hq + kMlaHeads - 1) / kMlaHeads) * (kMlaWgs + b);
@@ -1322,7 +1334,8 @@ MlaWs mla_ws(int64_t b, int hq, int dn) {
   w.part_o = (static_cast<size_t>(b + 1) * sizeof(int64_t) + 255) / 256 * 256;
   w.part_ml = w.part_o + static_cast<size_t>(slots) * kMlaHeads * dn * sizeof(float);
   w.flags = w.part_ml + static_cast<size_t>(slots) * kMlaHeads * 2 * sizeof(float);
-  w.total = w.flags + static_cast<size_t>(slots) * kMlaWaves * sizeof(int32_t);
+  w.wgflags = (w.flags + static_cast<size_t>(slots) * kMlaWaves * sizeof(int32_t) + 15) / 16 * 16;
+  w.total = w.wgflags + static_cast<size_t>(kMlaWgs) * kMlaWaves * sizeof(int32_t);
   return w;
 }
 }  // namespace
@@ -1459,6 +1472,7 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.part_o = reinterpret_cast<float*>(ws + lay.part_o);
   a.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   a.flags = reinterpret_cast<int32_t*>(ws + lay.flags);
+  a.wgflags = reinterpret_cast<int32_t*>(ws + lay.wgflags);
   hipStream_t st = static_cast<hipStream_t>(stream);
   static bool lds_set = false;
   if (!lds_set) {
