@@ -14,6 +14,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -707,7 +709,7 @@ struct MlaArgs {
   // Partials: slot hg * (kMlaWgs + b_count) + w + b holds workgroup w's part of sequence b for head
   // group hg (w + b is unique: the workgroups covering one sequence are consecutive, and so are
   // the sequences one workgroup covers).
-  float* part_o;   // [slots, kMlaHeads, DN]
+  uint16_t* part_o;  // [slots, kMlaHeads, DN] bf16, each partial divided by its own running sum
   float* part_ml;  // [slots, kMlaHeads, 2]
   int32_t* flags;  // [slots, kMlaWaves]: 1 = that wave's heads need the rescaling pass
   int32_t* wgflags;  // [kMlaWgs, kMlaWaves]: 1 = some segment of that workgroup's wave was flagged
@@ -1145,14 +1147,20 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, bool& 
   }
   if (!head_ok) return;
   if constexpr (!RESCALE) mfma_drain(acc);
-  // ---- partial: O^T[d = 32dt + 8i + 4h + r][head]
-  float* po = a.part_o + (pbase + hl) * DN;
+  // ---- partial: O^T[d = 32dt + 8i + 4h + r][head] / l, as bf16 (the merge weighs it by l again); half
+  //      the bytes of fp32 for the partial's write and the merge's read, at most one bf16 rounding
+  //      of a convex combination's terms
+  uint16_t* po = a.part_o + (pbase + hl) * DN;
+  const float inv_l = 1.0f / l_run;
 #pragma unroll
   for (int dt = 0; dt < DN / 32; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<float4*>(po + 32 * dt + 8 * i + 4 * h) =
-          make_float4(acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]);
+    for (int i = 0; i < 4; ++i) {
+      const bf16x2_t p0 = __builtin_convertvector((f32x2_t){acc[dt][4 * i] * inv_l, acc[dt][4 * i + 1] * inv_l}, bf16x2_t);
+      const bf16x2_t p1 = __builtin_convertvector((f32x2_t){acc[dt][4 * i + 2] * inv_l, acc[dt][4 * i + 3] * inv_l}, bf16x2_t);
+      *reinterpret_cast<uint2*>(po + 32 * dt + 8 * i + 4 * h) =
+          make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+    }
   if (h == 0) {
     a.part_ml[(pbase + hl) * 2] = m_run;
     a.part_ml[(pbase + hl) * 2 + 1] = l_run;
@@ -1274,7 +1282,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   const int ns = static_cast<int>(w_last - w_first + 1);
   const int64_t row0 = (hg * (kMlaWgs + a.b) + w_first + b) * kMlaHeads + hl;  // partial s: row0 + s * kMlaHeads
   const float* ml = a.part_ml + row0 * 2;
-  const float* po = a.part_o + row0 * DN + 8 * lane;
+  const uint16_t* po = a.part_o + row0 * DN + 8 * lane;
   // With fewer steps than workgroups some ranges are empty; those workgroups wrote nothing.
   auto live = [&](int s) {
     const int64_t w = w_first + s;
@@ -1291,16 +1299,22 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
 #pragma unroll
   for (int i = 0; i < 8; ++i) num0[i] = num1[i] = 0.0f;
   for (int s = 0; s < ns; ++s) {
-    const float* p = po + static_cast<int64_t>(kMlaHeads) * DN * s;
-    const float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
-    const float4 b0 = *reinterpret_cast<const float4*>(p + DN), b1 = *reinterpret_cast<const float4*>(p + DN + 4);
+    const uint16_t* p = po + static_cast<int64_t>(kMlaHeads) * DN * s;
+    const uint4 a8 = *reinterpret_cast<const uint4*>(p), b8 = *reinterpret_cast<const uint4*>(p + DN);
     if (!live(s)) continue;
     const float4 st = *reinterpret_cast<const float4*>(ml + 2 * kMlaHeads * s);
-    const float w0 = exp2f(st.x - M0), w1 = exp2f(st.z - M1);
-    den0 += w0 * st.y;
-    den1 += w1 * st.w;
-    const float v0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float v1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float w0 = exp2f(st.x - M0) * st.y, w1 = exp2f(st.z - M1) * st.w;  // weight x running sum
+    den0 += w0;
+    den1 += w1;
+    float v0[8], v1[8];
+    const uint32_t aw[4] = {a8.x, a8.y, a8.z, a8.w}, bw[4] = {b8.x, b8.y, b8.z, b8.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v0[2 * i] = __uint_as_float(aw[i] << 16);
+      v0[2 * i + 1] = __uint_as_float(aw[i] & 0xffff0000u);
+      v1[2 * i] = __uint_as_float(bw[i] << 16);
+      v1[2 * i + 1] = __uint_as_float(bw[i] & 0xffff0000u);
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       num0[i] += w0 * v0[i];
@@ -1332,7 +1346,7 @@ MlaWs mla_ws(int64_t b, int hq, int dn) {
   MlaWs w;
   w.steps = 0;
   w.part_o = (static_cast<size_t>(b + 1) * sizeof(int64_t) + 255) / 256 * 256;
-  w.part_ml = w.part_o + static_cast<size_t>(slots) * kMlaHeads * dn * sizeof(float);
+  w.part_ml = w.part_o + (static_cast<size_t>(slots) * kMlaHeads * dn * sizeof(uint16_t) + 255) / 256 * 256;
   w.flags = w.part_ml + static_cast<size_t>(slots) * kMlaHeads * 2 * sizeof(float);
   w.wgflags = (w.flags + static_cast<size_t>(slots) * kMlaWaves * sizeof(int32_t) + 15) / 16 * 16;
   w.total = w.wgflags + static_cast<size_t>(kMlaWgs) * kMlaWaves * sizeof(int32_t);
@@ -1469,7 +1483,7 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.hgroups = static_cast<int>(cdiv(hq, kMlaHeads)); a.scale_log2 = scale * kLog2e;
   char* ws = static_cast<char*>(workspace);
   a.steps = reinterpret_cast<int64_t*>(ws + lay.steps);
-  a.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  a.part_o = reinterpret_cast<uint16_t*>(ws + lay.part_o);
   a.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   a.flags = reinterpret_cast<int32_t*>(ws + lay.flags);
   a.wgflags = reinterpret_cast<int32_t*>(ws + lay.wgflags);
