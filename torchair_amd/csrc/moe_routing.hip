@@ -356,8 +356,10 @@ struct FinArgs {
   void* y;
 };
 
+template <bool NT = false>
 __device__ __forceinline__ void load8_bf16(const void* base, int64_t off, float (&v)[8]) {
-  uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+  const uint16_t* p = static_cast<const uint16_t*>(base) + off;
+  uint4 r = NT ? load_nt_u4(p) : *reinterpret_cast<const uint4*>(p);
   uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(256) void finalize_bf16_kernel(FinArgs a) {
     for (int j = 0; j < a.k; ++j) {
       const int32_t d = s_dst[j];
       if (d < 0) continue;
-      load8_bf16(a.ex, static_cast<int64_t>(d) * a.h + 8 * c, v);
+      load8_bf16<true>(a.ex, static_cast<int64_t>(d) * a.h + 8 * c, v);  // each expanded row is read once
       if (a.bias) {
         float b[8];
         load8_bf16(a.bias, static_cast<int64_t>(s_exp[j]) * a.h + 8 * c, b);

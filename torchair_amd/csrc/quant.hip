@@ -16,15 +16,15 @@ namespace {
 constexpr int kVec = 8;  // elements per vector load
 
 template <int DT>
-struct Vec8 {
+struct Vec8 {  // loads 8 elements as fp32 (non-temporal: the quantiser reads its input once)
   static __device__ __forceinline__ void load(const void* base, int64_t idx, float (&v)[kVec]) {
     if constexpr (DT == TAI_DT_FP32) {
-      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
-      float4 a = p[0], b = p[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      const float* p = static_cast<const float*>(base) + idx;
+      const uint4 a = load_nt_u4(p), b = load_nt_u4(p + 4);
+      v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+      v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
     } else {
-      uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+      uint4 r = load_nt_u4(static_cast<const uint16_t*>(base) + idx);
       uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
