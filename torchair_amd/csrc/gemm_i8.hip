@@ -100,9 +100,11 @@ __device__ __forceinline__ int64_t tile_id(const GemmArgs& g, int64_t b) {
 // share a column tile are consecutive in L, so within an XCD they run together and read each weight
 // slice from HBM once (the slice is then served from that XCD's L2 to the group's other row tiles).
 // Returns the group, -1 (nothing to do) or -2 (zero-fill rows past the grouped total).
-__device__ __forceinline__ int grouped_tile(const GemmArgs& g, int64_t L, int bm, int& row0, int& row1, int64_t& nt) {
+__device__ __forceinline__ int grouped_tile(const GemmArgs& g, int64_t L, int bm, int& row0, int& row1, int64_t& nt,
+                                            int64_t& rt_out) {
   const int64_t s0 = L / g.n_tiles;
   const int4 t = g.tile_map[s0];
+  rt_out = 1;
   if (t.x < 0) {
     row0 = t.y;
     row1 = t.z;
@@ -111,6 +113,7 @@ __device__ __forceinline__ int grouped_tile(const GemmArgs& g, int64_t L, int bm
   }
   const int64_t first = s0 - t.w;
   const int64_t rt = (static_cast<int64_t>(t.z) - t.y + bm - 1) / bm;
+  rt_out = rt;
   const int64_t off = L - first * g.n_tiles;
   nt = off / rt;
   row0 = t.y + static_cast<int>(off % rt) * bm;
@@ -227,7 +230,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs g) {
   int64_t nt = L % g.n_tiles;
   int e = 0, row0, row1;
   if (g.tile_map) {
-    e = grouped_tile(g, L, BM, row0, row1, nt);
+    int64_t rt;
+    e = grouped_tile(g, L, BM, row0, row1, nt, rt);
   }
   const int64_t n0 = nt * BN;
   if (g.tile_map) {
@@ -460,6 +464,9 @@ struct BigCfg {
   static_assert(kBN >= 256, "the [K,N] swizzle spans 16 chunks of a weight row");
 };
 
+#ifndef TAI_GEMM_B_NT
+#define TAI_GEMM_B_NT 1
+#endif
 #ifndef TAI_SPLIT_ISSUE
 #define TAI_SPLIT_ISSUE 1
 #endif
@@ -503,7 +510,7 @@ __device__ __forceinline__ void lgkm_wait() {
 // The loads of one stage: PART 0 issues all of them, PART 1 the first half and PART 2 the rest (a
 // stage's loads are split so that the workgroup's waves do not all queue in the address unit at
 // the same moment after a barrier).
-template <int LAYOUT, class C, bool SWI = false, int PART = 0>
+template <int LAYOUT, class C, bool SWI = false, int PART = 0, int BPOL = 0>
 __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, int row0, int rows,
                                                 int64_t n0, int64_t k0, int8_t* stage, int w, int lane) {
   constexpr int BK = C::kBK, CPR = C::kCpr, RPI = 1024 / BK;  // rows per 1 KB instruction
@@ -539,7 +546,7 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
       const int64_t nn = wc < g.n ? wc : g.n - 16;
       src = bgrp + (k0 + kr) * g.n + nn;
     }
-    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(bst + q * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(bst + q * 1024), 16, 0, BPOL);
   }
 }
 
@@ -621,10 +628,10 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
 
   const int64_t L = tile_id(g, blockIdx.x);
   if (L < 0) return;
-  int64_t slot = 0, nt;
+  int64_t slot = 0, nt, row_tiles = 0;
   int e = 0, row0, row1;
   if (g.tile_map) {
-    e = grouped_tile(g, L, C::kBM, row0, row1, nt);
+    e = grouped_tile(g, L, C::kBM, row0, row1, nt, row_tiles);
   } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
     constexpr int64_t GM = 8;
     const int64_t per_group = GM * g.n_tiles;
@@ -713,9 +720,6 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     }
   }
   const int64_t kb0 = kbeg * kBigBK;
-#pragma unroll
-  for (int s = 0; s < C::kStages - 1; ++s)
-    if (s < nk) big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + s * kBigBK, smem + s * C::kStage, w, lane);
 
   const int arow = wm * 64 + (lane & 31);            // + 32 i
   const int brow = wn * 128 + (lane & 31);           // + 32 j (NK)
@@ -763,8 +767,14 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   // kt, whose fragments are in registers), refills slot kt with stage kt + S, prefetches the first
   // fragments of stage kt + 1, then multiplies.
   constexpr bool kSplit = TAI_SPLIT_ISSUE != 0 && C::kStages > 2;  // needs two stages in flight
-  auto main_loop = [&](auto ni) {
+  auto main_loop = [&](auto ni, auto bpol) {
     constexpr int NI = decltype(ni)::value;
+    constexpr int BP = decltype(bpol)::value;
+#pragma unroll
+    for (int s = 0; s < C::kStages - 1; ++s)
+      if (s < nk)
+        big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, row0, rows, n0, kb0 + s * kBigBK, smem + s * C::kStage,
+                                                             w, lane);
     constexpr int NF = NI == 0 ? 0 : NI + (LAYOUT == TAI_LAYOUT_KN ? 8 : 4);  // LDS reads per step
     v4i fa[2][NI > 0 ? NI : 1], fb[2][4];
     auto fetch = [&](int buf, const int8_t* st, int kk) {
@@ -795,7 +805,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     wait_stage(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (C::kStages - 1 < nk)
-      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu>(g, bgrp, row0, rows, n0, kb0 + (C::kStages - 1) * kBigBK,
+      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, row0, rows, n0, kb0 + (C::kStages - 1) * kBigBK,
                                  smem + (C::kStages - 1) * C::kStage, w, lane);
     fetch(0, smem, 0);
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -814,7 +824,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
             // stage kt + S into the slot just freed: its first half now, the rest after the next
             // stage's first MFMA step (every load is still issued before the next stage wait)
             if (kt + C::kStages < nk)
-              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, kSplit ? 1 : 0>(
+              big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, kSplit ? 1 : 0, BP>(
                   g, bgrp, row0, rows, n0, kb0 + (kt + C::kStages) * kBigBK,
                   smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
             fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
@@ -824,7 +834,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
         mfma(cur);
         if constexpr (kSplit) {
           if (kk == 0 && kt >= 1 && kt - 1 + C::kStages < nk)
-            big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 2>(g, bgrp, row0, rows, n0, kb0 + (kt - 1 + C::kStages) * kBigBK,
+            big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 2, BP>(g, bgrp, row0, rows, n0, kb0 + (kt - 1 + C::kStages) * kBigBK,
                                                            smem + ((static_cast<int>(kt) - 1) % C::kStages) * C::kStage,
                                                            w, lane);
         }
@@ -834,9 +844,15 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
   };
   // Waves whose 64 rows are all past the group end skip the MFMAs; waves with at most 32 live rows
   // skip those of the upper 32 (wave-uniform branches).
-  if (act_m > 1) main_loop(std::integral_constant<int, 2>());
-  else if (act_m == 1) main_loop(std::integral_constant<int, 1>());
-  else main_loop(std::integral_constant<int, 0>());
+  // A group with a single row tile reads each weight byte once: its weight loads stream with the
+  // non-temporal policy. Groups with several row tiles share their weight slices through L2.
+  auto dispatch = [&](auto bpol) {
+    if (act_m > 1) main_loop(std::integral_constant<int, 2>(), bpol);
+    else if (act_m == 1) main_loop(std::integral_constant<int, 1>(), bpol);
+    else main_loop(std::integral_constant<int, 0>(), bpol);
+  };
+  if (TAI_GEMM_B_NT && row_tiles == 1) dispatch(std::integral_constant<int, 2>());
+  else dispatch(std::integral_constant<int, 0>());
 
   if constexpr (OUT == kOutSwiglu) {
     swiglu_epilogue<C>(g, acc, e, row0, rows, n0, nt, w, lane, smem);
