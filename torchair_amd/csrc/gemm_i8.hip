@@ -935,8 +935,11 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
           const int lr = wm * 64 + i * 32 + 16 * h + sl;
           const uint4 v = *reinterpret_cast<const uint4*>(wreg + sl * RB + 16 * (lane % LPR));
           if (lr < rows)
-            *reinterpret_cast<uint4*>(static_cast<char*>(gout) + (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
-                                      16 * (lane % LPR)) = v;
+            // output rows are written once: non-temporal stores (the down projection gains 2%)
+            __builtin_nontemporal_store(tai_u32x4_t{v.x, v.y, v.z, v.w},
+                                        reinterpret_cast<tai_u32x4_t*>(static_cast<char*>(gout) +
+                                                                       (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
+                                                                       16 * (lane % LPR)));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
       }
