@@ -885,6 +885,7 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
     static_assert(8 * 16 * RB <= C::kLds, "epilogue staging must fit in the ring");
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     char* wreg = reinterpret_cast<char*>(smem) + w * (16 * RB);
+    const bool nt_out = g.tile_map != nullptr;
     constexpr int LPR = 128 * ES / 16;  // lanes per row when reading 16 bytes each
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -934,12 +935,16 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
           const int sl = q * (64 / LPR) + lane / LPR;
           const int lr = wm * 64 + i * 32 + 16 * h + sl;
           const uint4 v = *reinterpret_cast<const uint4*>(wreg + sl * RB + 16 * (lane % LPR));
-          if (lr < rows)
-            // output rows are written once: non-temporal stores (the down projection gains 2%)
-            __builtin_nontemporal_store(tai_u32x4_t{v.x, v.y, v.z, v.w},
-                                        reinterpret_cast<tai_u32x4_t*>(static_cast<char*>(gout) +
-                                                                       (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
-                                                                       16 * (lane % LPR)));
+          if (lr < rows) {
+            tai_u32x4_t* dst = reinterpret_cast<tai_u32x4_t*>(static_cast<char*>(gout) +
+                                                              (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
+                                                              16 * (lane % LPR));
+            // grouped launches write rows that the next op streams once: non-temporal stores (down
+            // projection -2%); split-K partials, re-read at once by the reduction, and dense outputs
+            // keep the default policy
+            if (nt_out) __builtin_nontemporal_store(tai_u32x4_t{v.x, v.y, v.z, v.w}, dst);
+            else *dst = tai_u32x4_t{v.x, v.y, v.z, v.w};
+          }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
       }
