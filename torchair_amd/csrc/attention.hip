@@ -59,7 +59,7 @@ struct DecodeArgs {
   int bs;
   float scale_log2;  // softmax scale * log2(e)
   int nranges;     // step ranges of a launch (one wave per range and kv head)
-  int64_t* steps;  // [0] = all steps of the batch, [1 + b] = steps before sequence b
+  int64_t* steps;  // [0] = balance units of the batch, [1 + b] = units before sequence b
   float* part_o;   // [slot, hkv, 16, D], slot = range + sequence
   float* part_ml;  // [slot, hkv, 16, 2]
 };
@@ -99,6 +99,13 @@ struct DecodeTile {
 typedef __attribute__((address_space(3))) char lds_char_t;
 
 __device__ __forceinline__ int64_t dec_steps(int64_t len) { return len > 0 ? (len + kStep - 1) / kStep : 0; }
+// Balance units of a sequence: its steps plus kDecSegCost for the start of a segment (Q load, ring
+// fill, partial store), so a range that starts a sequence gets that much less streaming.
+#ifndef TAI_DEC_SEG_COST
+#define TAI_DEC_SEG_COST 2
+#endif
+constexpr int kDecSegCost = TAI_DEC_SEG_COST;
+__device__ __forceinline__ int64_t dec_units(int64_t len) { return len > 0 ? dec_steps(len) + kDecSegCost : 0; }
 
 // One segment: tokens [t_begin, t_end) of sequence b for kv head kvh, written as the partial of
 // the given slot.
@@ -288,13 +295,13 @@ void paged_decode_kernel(DecodeArgs a) {
   const int64_t r = blockIdx.x / a.hkv;
   const int64_t nb = a.b, R = a.nranges;
   int64_t mine = 0;
-  for (int64_t c = lane; c < nb; c += 64) mine += dec_steps(a.lens[c]);
+  for (int64_t c = lane; c < nb; c += 64) mine += dec_units(a.lens[c]);
   const int64_t S = uniform64(wave_sum64(mine));
   if (blockIdx.x == 0) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? dec_steps(a.lens[i]) : 0;
+      const int64_t n = i < nb ? dec_units(a.lens[i]) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       if (i < nb) a.steps[1 + i] = incl - n;
       carry = __shfl(incl, 63, 64);
@@ -309,7 +316,7 @@ void paged_decode_kernel(DecodeArgs a) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? dec_steps(a.lens[i]) : 0;
+      const int64_t n = i < nb ? dec_units(a.lens[i]) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       const uint64_t hit = __ballot(i < nb && n > 0 && incl - n <= x && x < incl);
       if (hit) {
@@ -325,17 +332,20 @@ void paged_decode_kernel(DecodeArgs a) {
   pb = uniform64(pb);
   for (int64_t g = g0; g < g1;) {
     const int64_t len = a.lens[b];
-    const int64_t n = dec_steps(len);
+    const int64_t n = dec_units(len);
     const int64_t seg = min(g1 - g, pb + n - x);
-    const int64_t t_begin = (x - pb) * kStep;
-    decode_segment<D>(a, (lds_char_t*)s_kv, b, kvh, t_begin, min(len, t_begin + seg * kStep), r + b);
+    // units [u0, u1) of this sequence; the first kDecSegCost carry no tokens
+    const int64_t u0 = x - pb, u1 = u0 + seg;
+    const int64_t s0 = max<int64_t>(u0, kDecSegCost) - kDecSegCost, s1 = max<int64_t>(u1, kDecSegCost) - kDecSegCost;
+    if (s1 > s0)
+      decode_segment<D>(a, (lds_char_t*)s_kv, b, kvh, s0 * kStep, min(len, s1 * kStep), r + b);
     g += seg;
     x += seg;
     if (x == pb + n) {  // on to the next non-empty sequence
       pb += n;
       do {
         ++b;
-      } while (g < g1 && b < nb && dec_steps(a.lens[b]) == 0);
+      } while (g < g1 && b < nb && dec_units(a.lens[b]) == 0);
     }
   }
 }
@@ -363,8 +373,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
     if (lse && lane == 0) lse[b * a.hq + h] = -INFINITY;
     return;
   }
-  const int64_t x1 = x0 + n;
-  const int64_t r_first = ((x0 + 1) * R - 1) / S, r_last = (x1 * R - 1) / S;
+  // the sequence's units are [x0, x1); its tokens start kDecSegCost units in
+  const int64_t xs = x0 + kDecSegCost, x1 = xs + n;
+  const int64_t r_first = ((xs + 1) * R - 1) / S, r_last = (x1 * R - 1) / S;
   const int ns = static_cast<int>(r_last - r_first + 1);
   const int64_t row0 = ((r_first + b) * a.hkv + kvh) * 16 + hi;  // partial s: row0 + s * hkv * 16
   const int64_t rstep = static_cast<int64_t>(a.hkv) * 16;
