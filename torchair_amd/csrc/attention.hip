@@ -1319,7 +1319,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   for (int i = 0; i < 8; ++i) num0[i] = num1[i] = 0.0f;
   for (int s = 0; s < ns; ++s) {
     const uint16_t* p = po + static_cast<int64_t>(kMlaHeads) * DN * s;
-    const uint4 a8 = *reinterpret_cast<const uint4*>(p), b8 = *reinterpret_cast<const uint4*>(p + DN);
+    const uint4 a8 = load_nt_u4(p), b8 = load_nt_u4(p + DN);  // each partial is read once
     if (!live(s)) continue;
     const float4 st = *reinterpret_cast<const float4*>(ml + 2 * kMlaHeads * s);
     const float w0 = exp2f(st.x - M0) * st.y, w1 = exp2f(st.z - M1) * st.w;  // weight x running sum
