@@ -38,17 +38,23 @@ class MoeLayer:
     T, H, E, K, I = 4096, 7168, 256, 8, 2048
 
     def __init__(self, torch, dev):
+        """Activations, router logits, bias and scales come from one CPU torch.Generator seeded with 0
+        and are copied to the device, so the CPU leg sees the same routing. The 11.3 GB of int8
+        weights are drawn on the device (seed 0): drawing them on the host would take minutes, and
+        the CPU leg reads the experts it times back from HBM."""
         self.torch = torch
-        g = torch.Generator(device=dev)
+        g = torch.Generator()
         g.manual_seed(0)
         T, H, E, I = self.T, self.H, self.E, self.I
-        self.x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
-        self.logits = torch.randn(T, E, generator=g, device=dev)
-        self.bias = torch.randn(E, generator=g, device=dev) * 0.1
-        self.w_gu = torch.randint(-127, 128, (E, H, 2 * I), generator=g, device=dev, dtype=torch.int8)
-        self.w_d = torch.randint(-127, 128, (E, I, H), generator=g, device=dev, dtype=torch.int8)
-        self.s_gu = torch.rand(E, 2 * I, generator=g, device=dev) * 9e-3 + 1e-3
-        self.s_d = torch.rand(E, H, generator=g, device=dev) * 9e-3 + 1e-3
+        self.x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        self.logits = torch.randn(T, E, generator=g).to(dev)
+        self.bias = (torch.randn(E, generator=g) * 0.1).to(dev)
+        self.s_gu = (torch.rand(E, 2 * I, generator=g) * 9e-3 + 1e-3).to(dev)
+        self.s_d = (torch.rand(E, H, generator=g) * 9e-3 + 1e-3).to(dev)
+        gd = torch.Generator(device=dev)
+        gd.manual_seed(0)
+        self.w_gu = torch.randint(-127, 128, (E, H, 2 * I), generator=gd, device=dev, dtype=torch.int8)
+        self.w_d = torch.randint(-127, 128, (E, I, H), generator=gd, device=dev, dtype=torch.int8)
         self.gmm1_events = []
         self.active_experts = None
 

@@ -54,6 +54,9 @@ extern "C" {
 
 const char* tai_last_error(void);
 int tai_abi_version(void);
+/* Hash of the sources and build flags the library was compiled from. The Python loader refuses a
+ * library whose id differs from the hash of the sources beside it (a stale build). */
+const char* tai_build_id(void);
 
 /* ---------------------------------------------------------------------------------------
  * npu_dynamic_quant: symmetric per-row int8 quantisation.

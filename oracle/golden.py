@@ -7,7 +7,7 @@ The reference ships no arithmetic for these ops: its converters emit opaque GE n
 kernels live in closed CANN packages (python/torchair/_ge_concrete_graph/ge_converter/custom/*.py),
 so this module restates each op from its prototype, converter arguments and meta rules
 (file:line cited per function). Where those leave a choice open the choice is written here
-and frozen by tests/golden fixtures:
+and frozen by the fixtures in tests/golden/ (written by tests/golden/make_fixtures.py):
   * quantisation: scale = amax/127 (fp32 divide), y = clamp(rint(xs/scale), -128, 127),
     rint = round half to even; an all-zero row gives scale 0 and y 0;
   * dequant_swiglu_quant: d = (float(x [+ int32 bias]) * weight_scale) * activation_scale
@@ -97,7 +97,8 @@ def dynamic_quant(x: np.ndarray, smooth_scales: Optional[np.ndarray] = None,
 
 def silu(a: np.ndarray) -> np.ndarray:
     a = np.asarray(a, F32)
-    return (a / (F32(1.0) + np.exp(-a))).astype(F32)
+    with np.errstate(over="ignore"):  # exp(-a) overflows to inf for a < -88.7, giving silu = -0 as it should
+        return (a / (F32(1.0) + np.exp(-a))).astype(F32)
 
 
 def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None, bias=None, quant_scale=None,

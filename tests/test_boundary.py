@@ -30,6 +30,19 @@ def test_library_exports_every_header_symbol():
     assert lib.tai_abi_version() == 1
 
 
+def test_library_build_id_matches_sources_and_stale_library_is_refused():
+    from torchair_amd import _build
+    lib = _lib.load()
+    assert lib.tai_build_id().decode() == _build.source_id()
+
+    class _Stale:
+        @staticmethod
+        def tai_build_id():
+            return b"0000"
+    with pytest.raises(RuntimeError, match="stale"):
+        _lib._check_fresh(_Stale())
+
+
 def test_library_rejects_bad_arguments_without_gpu():
     with pytest.raises(RuntimeError, match="dtype"):
         _lib.call("tai_dynamic_quant", 1, 99, 4, 4, None, None, -1, 0, 1, 1, None)
@@ -205,4 +218,38 @@ def test_pattern_pass_fuses_add_rms_norm_dynamic_quant_on_cpu():
     gm2 = torch.fx.symbolic_trace(two)
     assert fuse_add_rms_norm_dynamic_quant(gm2) == 1
     for a, b in zip(gm2(x1, x2), two(x1, x2)):
+        assert torch.equal(a, b)
+
+
+def test_pattern_pass_keeps_graph_order_when_x_out_is_used_before_the_quant():
+    """A user of the norm's x output placed between the norm and the quant must still see a node
+    defined before it (the fused node goes where the norm was)."""
+    from oracle import cpu_ops
+    from torchair_amd.patterns import fuse_add_rms_norm_dynamic_quant
+    cpu_ops.register()
+    g = torch.Generator().manual_seed(4)
+    x1, x2 = torch.randn(4, 64, generator=g).to(torch.bfloat16), torch.randn(4, 64, generator=g).to(torch.bfloat16)
+    gamma = (torch.rand(64, generator=g) + 0.5).to(torch.bfloat16)
+
+    def block(x1, x2, sm):
+        y, _, x = torch.ops.npu.npu_add_rms_norm(x1, x2, gamma)
+        r = torch.relu(x)
+        q, s = torch.ops.npu.npu_dynamic_quant(y, smooth_scales=sm * 2)  # smooth scale defined after the norm
+        return q, s, r
+
+    sm = torch.rand(64, generator=g) + 0.5
+    gm = torch.fx.symbolic_trace(block)
+    assert fuse_add_rms_norm_dynamic_quant(gm) == 0  # relu(x) precedes the smooth scale: left alone
+    gm.graph.lint()
+
+    def block2(x1, x2, sm):
+        y, _, x = torch.ops.npu.npu_add_rms_norm(x1, x2, gamma)
+        r = torch.relu(x)
+        q, s = torch.ops.npu.npu_dynamic_quant(y, smooth_scales=sm)
+        return q, s, r
+
+    gm2 = torch.fx.symbolic_trace(block2)
+    assert fuse_add_rms_norm_dynamic_quant(gm2) == 1
+    gm2.graph.lint()
+    for a, b in zip(gm2(x1, x2, sm), block2(x1, x2, sm)):
         assert torch.equal(a, b)

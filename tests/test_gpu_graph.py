@@ -1,0 +1,206 @@
+"""GPU: torch.compile(backend=get_npu_backend(mode="reduce-overhead")) lowers onto the HIP ops and
+captures a hipGraph; replays with new device values (activations, sequence lengths, block tables,
+group lists, cache slots) are checked against eager and the oracle on every replay, with eager
+work and synchronisations in between. This is the role of the reference's graph_task_update
+(python/torchair/_acl_concrete_graph/acl_graph.py:542-577): data-dependent sizes are read on the
+device, so a replay with new values needs no re-capture."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd
+from oracle import golden as G
+from tests.helpers import assert_close, f32np
+from torchair_amd import graph as tai_graph
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _backend():
+    cfg = torchair_amd.CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    return torchair_amd.get_npu_backend(compiler_config=cfg)
+
+
+def _churn():
+    """Unrelated eager work and a host synchronisation between replays."""
+    a = torch.randn(1 << 20, device=DEV)
+    (a * 3).sum().item()
+    torch.cuda.synchronize()
+
+
+class _Mlp(torch.nn.Module):
+    """Config-1 W8A8 SwiGLU MLP; the weights are parameters, so the graph uses them in place."""
+
+    def __init__(self, h, inter, g):
+        super().__init__()
+        p = lambda t: torch.nn.Parameter(t.to(DEV), requires_grad=False)  # noqa: E731
+        self.wgu = p(torch.randint(-127, 128, (h, 2 * inter), generator=g, dtype=torch.int8))
+        self.sgu = p(torch.rand(2 * inter, generator=g) * 9e-3 + 1e-3)
+        self.wd = p(torch.randint(-127, 128, (inter, h), generator=g, dtype=torch.int8))
+        self.sd = p(torch.rand(h, generator=g) * 9e-3 + 1e-3)
+        self.one = p(torch.ones(1))
+
+    def forward(self, x):
+        npu = torch.ops.npu
+        q, s = npu.npu_dynamic_quant(x)
+        h = npu.npu_quant_matmul(q, self.wgu, self.one, output_dtype=torch.int32)
+        q2, s2 = npu.npu_dequant_swiglu_quant(h, weight_scale=self.sgu, activation_scale=s, quant_mode=1,
+                                              activate_left=True)
+        return npu.npu_quant_matmul(q2, self.wd, self.sd, pertoken_scale=s2, output_dtype=torch.bfloat16)
+
+
+def test_compiled_mlp_cfg1_captures_and_replays():
+    g = torch.Generator().manual_seed(50)
+    t, h, inter = 128, 2048, 5632
+    mod = _Mlp(h, inter, g)
+    fn = torch.compile(mod, backend=_backend(), fullgraph=True)
+    caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+    for i in range(4):
+        x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+        got = fn(x.to(DEV)).clone()
+        want = mod(x.to(DEV))
+        assert torch.equal(got, want), f"call {i}: graph differs from eager"
+        if i in (0, 3):  # the oracle on the first and the last replay
+            wq, ws = G.dynamic_quant(f32np(x))
+            acc = G.quant_matmul(wq, mod.wgu.cpu().numpy(), out_dtype="int32")
+            q2, s2 = G.dequant_swiglu_quant(acc, mod.sgu.cpu().numpy(), ws, activate_left=True)
+            ref = G.quant_matmul(q2, mod.wd.cpu().numpy(), mod.sd.cpu().numpy(), s2, None, "bf16")
+            assert_close(f32np(got), ref, rtol=2e-2, atol=2e-2)
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+    assert tai_graph.stats["eager_fallbacks"] == falls
+
+
+def _paged(g, lens, nb_total, width, bs, hkv, d):
+    perm = torch.randperm(nb_total, generator=g).to(torch.int32)
+    bt = torch.zeros(len(lens), width, dtype=torch.int32)
+    off = 0
+    for b, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        bt[b, :n] = perm[off:off + n]
+        off += n
+    return bt
+
+
+def test_compiled_decode_replays_with_new_lengths_and_block_table():
+    g = torch.Generator().manual_seed(51)
+    b, hq, hkv, d, bs, width = 8, 32, 8, 128, 128, 16
+    nblk = b * width
+    kc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16)
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+
+    def step(q, lens, bt):
+        return torch.ops.air.npu_fused_infer_attention_score(
+            q, kcd, vcd, actual_seq_lengths_kv=lens, block_table=bt, num_heads=hq, num_key_value_heads=hkv,
+            input_layout="BSH", block_size=bs, scale=1.0 / math.sqrt(d))[0]
+
+    fn = torch.compile(step, backend=_backend(), fullgraph=True)
+    caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+    for i in range(4):
+        lens = torch.randint(1, width * bs + 1, (b,), generator=g)
+        if i == 2:
+            lens[3] = 0  # an empty sequence
+        bt = _paged(g, lens.tolist(), nblk, width, bs, hkv, d)
+        q = torch.randn(b, 1, hq * d, generator=g).to(torch.bfloat16)
+        got = fn(q.to(DEV), lens.to(DEV), bt.to(DEV)).clone()
+        want = step(q.to(DEV), lens.to(DEV), bt.to(DEV))
+        assert torch.equal(got, want), f"replay {i} differs from eager"
+        ref, _ = G.paged_decode_attention(f32np(q).reshape(b, hq, d), f32np(kc).reshape(nblk, bs, hkv, d),
+                                          f32np(vc).reshape(nblk, bs, hkv, d), bt.numpy(), lens.numpy(),
+                                          1.0 / math.sqrt(d))
+        assert_close(f32np(got).reshape(b, hq, d), ref)
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+    assert tai_graph.stats["eager_fallbacks"] == falls
+
+
+def test_compiled_fia_with_list_lengths_is_captured():
+    """npu:: FIA with int-list lengths: the lengths are constants of the captured graph."""
+    g = torch.Generator().manual_seed(52)
+    b, hq, hkv, d, bs, width = 4, 8, 2, 128, 64, 8
+    lens = [100, 1, 512, 300]
+    nblk = b * width
+    kc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    bt = _paged(g, lens, nblk, width, bs, hkv, d).to(DEV)
+
+    def step(q):
+        return torch.ops.npu.npu_fused_infer_attention_score(
+            q, kc, vc, actual_seq_lengths_kv=lens, block_table=bt, num_heads=hq, num_key_value_heads=hkv,
+            input_layout="BSH", block_size=bs, scale=1.0 / math.sqrt(d))[0]
+
+    fn = torch.compile(step, backend=_backend(), fullgraph=True)
+    caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+    for i in range(3):
+        q = torch.randn(b, 1, hq * d, generator=g).to(torch.bfloat16).to(DEV)
+        got = fn(q).clone()
+        assert torch.equal(got, step(q)), f"replay {i}"
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+    assert tai_graph.stats["eager_fallbacks"] == falls
+
+
+def test_compiled_grouped_matmul_replays_with_new_group_list():
+    g = torch.Generator().manual_seed(53)
+    e, k, n, m = 16, 512, 768, 2000
+    w = torch.nn.Parameter(torch.randint(-127, 128, (e, k, n), generator=g, dtype=torch.int8).to(DEV),
+                           requires_grad=False)
+
+    def step(x, gl):
+        return torch.ops.npu.npu_grouped_matmul([x], [w], group_list=gl, split_item=3, group_type=0,
+                                                group_list_type=1, output_dtype=torch.int32)[0]
+
+    fn = torch.compile(step, backend=_backend(), fullgraph=True)
+    caps = tai_graph.stats["captures"]
+    for i in range(4):
+        x = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+        hi = e if i % 2 else e // 4  # alternately all experts live, then a quarter of them with long groups
+        counts = torch.bincount(torch.randint(0, hi, (m - 50,), generator=g), minlength=e).to(torch.int64)
+        got = fn(x.to(DEV), counts.to(DEV)).clone()
+        want = G.grouped_matmul(x.numpy(), w.cpu().numpy(), counts.numpy(), 1, out_dtype="int32")
+        rows = int(counts.sum())
+        np.testing.assert_array_equal(got.cpu().numpy()[:rows], want[:rows], err_msg=f"replay {i}")
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+
+
+def test_compiled_cache_write_updates_the_callers_cache():
+    """A compiled decode step that scatters into the KV cache: the cache is written in place (not a
+    clone), on the capture call and on every replay, exactly as eager writes it."""
+    g = torch.Generator().manual_seed(54)
+    t, hkv, d, nblk, bs = 16, 8, 128, 64, 32
+    kc = torch.zeros(nblk, bs, hkv, d, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+
+    def step(key, value, kcache, vcache, slots):
+        torch.ops.npu.npu_scatter_pa_kv_cache(key, value, kcache, vcache, slots)
+        return key.float().sum()
+
+    fn = torch.compile(step, backend=_backend(), fullgraph=True)
+    caps = tai_graph.stats["captures"]
+    perm = torch.randperm(nblk * bs, generator=g)
+    for i in range(4):
+        key = torch.randn(t, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+        val = torch.randn(t, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+        slots = perm[i * t:(i + 1) * t].to(DEV)
+        fn(key, val, kc, vc, slots)
+        step(key, val, kc_ref, vc_ref, slots)
+        torch.cuda.synchronize()
+        assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), f"call {i}: cache differs from eager"
+        s = slots.cpu()
+        assert torch.equal(kc.view(-1, hkv, d)[s.to(DEV)], key)
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+    # a cache at another address is captured anew (it is part of the graph by pointer)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    key = torch.randn(t, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    fn(key, key, kc2, vc2, perm[:t].to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(kc2.view(-1, hkv, d)[perm[:t].to(DEV)], key)
+    assert tai_graph.stats["captures"] == caps + 2

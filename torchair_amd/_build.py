@@ -6,6 +6,7 @@ linked into ``torchair_amd/libtai_kernels.so``, which travels with the source tr
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import subprocess
 import sys
@@ -31,9 +32,26 @@ COMMON_FLAGS = [
 NO_CONTRACT = {"quant.hip", "moe_routing.hip", "norm_cache.hip"}
 
 
-def _compile(src: Path) -> Path:
+INCLUDE = PKG.parent / "include"
+
+
+def source_id() -> str:
+    """Hash of every source and flag the library is built from. It is compiled into the library
+    (``tai_build_id``) and compared at load time, so a library built from other sources is refused."""
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + sorted(INCLUDE.glob("*.h"))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    h.update(" ".join(COMMON_FLAGS + sorted(NO_CONTRACT)).encode())
+    return h.hexdigest()[:20]
+
+
+def _compile(src: Path, build_id: str) -> Path:
     obj = BUILD / (src.stem + ".o")
     flags = list(COMMON_FLAGS)
+    if src.name == "runtime.hip":
+        flags.append(f'-DTAI_BUILD_ID="{build_id}"')
     if src.name in NO_CONTRACT:
         flags.append("-ffp-contract=off")
     cmd = [HIPCC, *flags, "-c", str(src), "-o", str(obj)]
@@ -48,7 +66,8 @@ def build(verbose: bool = True) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(jobs, 1)) as ex:
-        objs = list(ex.map(_compile, sources))
+        bid = source_id()
+        objs = list(ex.map(lambda src: _compile(src, bid), sources))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -143,7 +143,22 @@ def _lens_tensor(v, device) -> Optional[torch.Tensor]:
         return None
     if isinstance(v, torch.Tensor):
         return v.to(device=device, dtype=torch.int64).contiguous()
-    return torch.tensor([int(x) for x in v], dtype=torch.int64, device=device)
+    vals = tuple(int(x) for x in v)
+    if torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing():
+        # A blocking host-to-device copy cannot be captured. The list is a constant of the captured
+        # graph (a graph input signature with other values captures anew), so the lengths are copied
+        # from a pinned host buffer that is kept for the life of the process: every replay re-reads it.
+        host = _PINNED_LENS.get(vals)
+        if host is None:
+            host = torch.tensor(vals, dtype=torch.int64).pin_memory()
+            _PINNED_LENS[vals] = host
+        out = torch.empty(len(vals), dtype=torch.int64, device=device)
+        out.copy_(host, non_blocking=True)
+        return out
+    return torch.tensor(vals, dtype=torch.int64, device=device)
+
+
+_PINNED_LENS: dict = {}
 
 
 def _check(cond, msg):

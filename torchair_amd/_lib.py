@@ -21,6 +21,7 @@ _P = c_void_p
 _SIGS = {
     "tai_last_error": (c_char_p, []),
     "tai_abi_version": (c_int, []),
+    "tai_build_id": (c_char_p, []),
     "tai_dynamic_quant": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P]),
     "tai_dequant_swiglu_quant": (
         c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, c_int, c_int64, c_int, _P, _P, _P]),
@@ -94,8 +95,22 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            _check_fresh(lib)
             _lib = lib
     return _lib
+
+
+def _check_fresh(lib: ctypes.CDLL) -> None:
+    """Refuses a library built from other sources than the ones beside it."""
+    from . import _build
+    if not _build.CSRC.is_dir():  # an installed copy without sources: nothing to compare against
+        return
+    want = _build.source_id()
+    got = lib.tai_build_id().decode(errors="replace")
+    if got != want:
+        raise RuntimeError(
+            f"{LIB_PATH} is stale: built from sources {got}, the sources beside it hash to {want}; rebuild "
+            "with `python -c 'import __graft_entry__ as g; g.build()'`")
 
 
 class KernelError(RuntimeError):

@@ -1507,17 +1507,19 @@ extern "C" int tai_fia_mla_decode(const void* q_nope, const void* q_rope, const 
   a.flags = reinterpret_cast<int32_t*>(ws + lay.flags);
   a.wgflags = reinterpret_cast<int32_t*>(ws + lay.wgflags);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  static bool lds_set = false;
-  if (!lds_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) != hipSuccess ||
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) != hipSuccess) {
-      (void)hipGetLastError();
-      set_error("tai_fia_mla_decode: the device cannot give a workgroup %d bytes of LDS", kMlaLds);
-      return TAI_ERR_LAUNCH;
-    }
-    lds_set = true;
+  // the LDS attribute is set once per process; a function-local static initialiser runs exactly
+  // once even when several host threads reach it together
+  static const bool lds_ok = [] {
+    const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_decode_kernel<512, 64, true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMlaLds) == hipSuccess;
+    (void)hipGetLastError();
+    return ok;
+  }();
+  if (!lds_ok) {
+    set_error("tai_fia_mla_decode: the device cannot give a workgroup %d bytes of LDS", kMlaLds);
+    return TAI_ERR_LAUNCH;
   }
   // fast pass, then the rescaling pass over the segments the fast pass flagged (it skips the others)
   const dim3 grid(kMlaWgs);

@@ -1015,8 +1015,8 @@ bool set_cfg_lds() {
 // True when the device lets one workgroup hold configuration C's LDS (attributes set once).
 template <class C>
 bool cfg_available() {
-  static int cached = -1;
-  if (cached < 0) {
+  // evaluated once (a function-local static initialiser is thread-safe)
+  static const bool cached = [] {
     int dev = 0, lds = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
@@ -1032,9 +1032,9 @@ bool cfg_available() {
            set_cfg_lds<C, TAI_LAYOUT_KN, kOutSwiglu>() && set_cfg_lds<C, TAI_LAYOUT_NK, kOutSwiglu>();
       (void)hipGetLastError();
     }
-    cached = ok ? 1 : 0;
-  }
-  return cached == 1;
+    return ok;
+  }();
+  return cached;
 }
 
 template <class C, int LAYOUT>

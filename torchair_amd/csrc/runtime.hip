@@ -27,3 +27,9 @@ int launch_status(const char* what) {
 
 extern "C" const char* tai_last_error(void) { return tai::g_last_error; }
 extern "C" int tai_abi_version(void) { return 1; }
+
+#ifndef TAI_BUILD_ID
+#define TAI_BUILD_ID "unversioned"
+#endif
+// Hash of the sources and flags this library was compiled from (set by the in-tree build).
+extern "C" const char* tai_build_id(void) { return TAI_BUILD_ID; }

@@ -4,7 +4,7 @@ Plays the role of the reference's graph executors (GE session run,
 torchair/npu_graph_executor/*, and the ACL graph capture of
 python/torchair/_acl_concrete_graph/acl_graph.py:825-848, 1174-1288, 1290-1402):
 one graph per input signature, inputs copied into graph-owned buffers before a replay,
-parameters used in place. Sequence lengths, block tables and group lists are device
+parameters and inputs the graph writes in place (KV caches) used by pointer. Sequence lengths, block tables and group lists are device
 tensors read by the kernels, so a replay with new values needs no re-capture.
 """
 from __future__ import annotations
@@ -16,81 +16,98 @@ import torch
 
 logger = logging.getLogger("torchair_amd")
 
+# process-wide counts, for diagnostics and tests: graphs captured, and calls that ran eagerly
+# because a graph could not be captured or the capture limit was reached
+stats = {"captures": 0, "eager_fallbacks": 0}
 
-def _signature(args: Sequence[Any]) -> Tuple:
+
+def _signature(args: Sequence[Any], by_pointer: Sequence[bool]) -> Tuple:
     sig = []
-    for a in args:
+    for a, ptr in zip(args, by_pointer):
         if isinstance(a, torch.Tensor):
-            sig.append(("T", tuple(a.shape), tuple(a.stride()), a.dtype, str(a.device)))
+            # an input used in place is part of the captured graph by its address: another address
+            # captures anew, as the reference re-captures when a mutated input moves
+            # (acl_graph.py:1195, 1368-1372)
+            sig.append(("T", tuple(a.shape), tuple(a.stride()), a.dtype, str(a.device), a.data_ptr() if ptr else None))
         else:
             sig.append(("V", a))
     return tuple(sig)
 
 
 class _Captured:
-    def __init__(self, fn: Callable, args: Sequence[Any], clone_input: bool):
-        self.static_idx: List[int] = []
+    """One captured graph. Inputs passed by pointer (parameters, inputs the graph writes in place,
+    or every tensor when ``clone_input`` is off) are used as they are; the others are copied into
+    graph-owned buffers before each replay."""
+
+    def __init__(self, fn: Callable, args: Sequence[Any], by_pointer: Sequence[bool]):
+        self.copy_idx: List[int] = []
         self.inputs: List[Any] = []
-        for i, a in enumerate(args):
-            if isinstance(a, torch.Tensor) and (isinstance(a, torch.nn.Parameter) or not clone_input):
-                self.static_idx.append(i)
-                self.inputs.append(a)
-            elif isinstance(a, torch.Tensor):
+        for i, (a, ptr) in enumerate(zip(args, by_pointer)):
+            if isinstance(a, torch.Tensor) and not ptr:
+                self.copy_idx.append(i)
                 self.inputs.append(a.clone())
             else:
                 self.inputs.append(a)
-        self.static_ptrs = {i: args[i].data_ptr() for i in self.static_idx}
         dev = next((a.device for a in args if isinstance(a, torch.Tensor)), torch.device("cuda"))
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            fn(*self.inputs)  # warm-up: allocator state and lazy library loading outside capture
+            # warm-up outside capture (allocator state, lazy library loading); its result is the
+            # result of this first call, so side effects on inputs happen exactly once per call
+            self.first_outputs = fn(*self.inputs)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             out = fn(*self.inputs)
         self.outputs = out
+        stats["captures"] += 1
 
     def run(self, args: Sequence[Any]):
-        for i, a in enumerate(args):
-            if not isinstance(a, torch.Tensor):
-                continue
-            if i in self.static_ptrs:
-                if a.data_ptr() != self.static_ptrs[i]:
-                    raise RuntimeError("a static (parameter) input changed its storage after capture; "
-                                       "recompile or set debug.aclgraph.clone_input=True")
-                continue
-            self.inputs[i].copy_(a)
+        for i in self.copy_idx:
+            self.inputs[i].copy_(args[i])
         self.graph.replay()
         return self.outputs
 
 
 class HipGraphRunner:
-    """Callable that captures ``fn`` per input signature and replays it."""
+    """Callable that captures ``fn`` per input signature and replays it.
+
+    ``mutated_inputs``: positions of the inputs ``fn`` writes in place (KV caches); they are never
+    copied, so the caller's tensors see the writes."""
 
     def __init__(self, fn: Callable, capture_limit: int = 64, clone_output: bool = False,
-                 clone_input: bool = True):
+                 clone_input: bool = True, mutated_inputs: Sequence[int] = ()):
         self.fn = fn
         self.capture_limit = capture_limit
         self.clone_output = clone_output
         self.clone_input = clone_input
+        self.mutated_inputs = frozenset(mutated_inputs)
         self.graphs: Dict[Tuple, _Captured] = {}
         self._warned = False
+
+    def _by_pointer(self, args) -> List[bool]:
+        return [isinstance(a, torch.Tensor) and (not self.clone_input or isinstance(a, torch.nn.Parameter)
+                                                 or i in self.mutated_inputs) for i, a in enumerate(args)]
 
     def __call__(self, *args):
         if not any(isinstance(a, torch.Tensor) and a.is_cuda for a in args):
             return self.fn(*args)
-        key = _signature(args)
+        by_ptr = self._by_pointer(args)
+        key = _signature(args, by_ptr)
         entry = self.graphs.get(key)
         if entry is None:
             if len(self.graphs) >= self.capture_limit:
                 if not self._warned:
                     logger.warning("static_capture_size_limit (%d) reached; running eagerly", self.capture_limit)
                     self._warned = True
+                stats["eager_fallbacks"] += 1
                 return self.fn(*args)
-            entry = _Captured(self.fn, args, self.clone_input)
+            entry = _Captured(self.fn, args, by_ptr)
             self.graphs[key] = entry
-        out = entry.run(args)
+            out = entry.first_outputs
+            entry.first_outputs = None
+        else:
+            out = entry.run(args)
         if self.clone_output:
             out = _map_tensors(out, lambda t: t.clone())
         return out

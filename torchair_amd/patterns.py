@@ -60,13 +60,20 @@ def fuse_add_rms_norm_dynamic_quant(gm: torch.fx.GraphModule) -> int:
         qouts = _getitems(quant)
         if qouts is None:
             continue
+        # the fused node takes the norm's place, or the smooth scale's when that is defined later;
+        # users of the norm's x output must all come after that point
+        order = {n: i for i, n in enumerate(gm.graph.nodes)}
+        smooth = quant.kwargs.get("smooth_scales")
+        anchor = smooth if isinstance(smooth, torch.fx.Node) and order[smooth] > order[norm] else norm
+        if any(order[u] <= order[anchor] for xu in outs.get(2, []) for u in xu.users):
+            continue
         for us in qouts.values():
             for u in [u for u in us if not u.users]:
                 us.remove(u)
                 gm.graph.erase_node(u)
         x1, x2, gamma = norm.args[:3]
         eps = norm.args[3] if len(norm.args) > 3 else norm.kwargs.get("epsilon", 1e-6)
-        with gm.graph.inserting_after(quant):
+        with gm.graph.inserting_after(anchor):
             node = gm.graph.call_function(
                 npu.npu_add_rms_norm_dynamic_quant.default, (x1, x2, gamma),
                 {"smooth_scale1": quant.kwargs.get("smooth_scales"), "epsilon": eps, "output_mask": [True, False]})
