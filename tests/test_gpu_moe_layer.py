@@ -1,5 +1,5 @@
 """GPU parity of the config-4 MoE layer exactly as bench.py runs it: bench.MoeLayer's inputs
-(seed 0), its gating-derived, skewed group list (0 to ~1600 rows per expert, so up to 13 row
+(seed 0), its gating-derived, skewed group list (0 to ~940 rows per expert, so up to 8 row
 tiles share one weight slice) and its op sequence, checked stage by stage:
   gating ids and the routing permutation / counts bit-exact against the oracle; the quantised
   rows against the oracle (+-1 LSB); the gate_up int32 accumulators exact against a float64 GPU
@@ -54,7 +54,7 @@ def test_cfg4_routing_and_quant_as_benched(layer):
     np.testing.assert_array_equal(ri.cpu().numpy(), wri)
     np.testing.assert_array_equal(counts.cpu().numpy(), wcounts)
     c = counts.cpu()
-    assert int(c.max()) > 12 * 128, "the benched routing should give some expert >= 13 row tiles"
+    assert int(c.max()) > 6 * 128, "the benched routing should give some expert >= 7 row tiles of 128"
     # expanded rows: row i holds token sorted_slot(i) // k (the gather form of row_idx_type 0 is inverted)
     inv = torch.empty_like(ri)
     inv[ri.long()] = torch.arange(ri.numel(), device=DEV, dtype=ri.dtype)

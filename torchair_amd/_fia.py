@@ -144,17 +144,23 @@ def _lens_tensor(v, device) -> Optional[torch.Tensor]:
     if isinstance(v, torch.Tensor):
         return v.to(device=device, dtype=torch.int64).contiguous()
     vals = tuple(int(x) for x in v)
-    if torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing():
-        # A blocking host-to-device copy cannot be captured. The list is a constant of the captured
-        # graph (a graph input signature with other values captures anew), so the lengths are copied
-        # from a pinned host buffer that is kept for the life of the process: every replay re-reads it.
-        host = _PINNED_LENS.get(vals)
-        if host is None:
-            host = torch.tensor(vals, dtype=torch.int64).pin_memory()
-            _PINNED_LENS[vals] = host
-        out = torch.empty(len(vals), dtype=torch.int64, device=device)
-        out.copy_(host, non_blocking=True)
-        return out
+    if torch.device(device).type == "cuda":
+        from .graph import preparing_capture
+        if preparing_capture() and vals not in _PINNED_LENS:
+            # The list is a constant of the graph about to be captured (other values capture anew).
+            # A blocking host-to-device copy cannot be captured, so the captured graph copies the
+            # lengths from a pinned host buffer kept for the life of the process, which every replay
+            # re-reads. It is allocated here, in the warm-up run before the capture: pinned memory
+            # cannot be allocated while a stream is captured.
+            _PINNED_LENS[vals] = torch.tensor(vals, dtype=torch.int64).pin_memory()
+        if torch.cuda.is_current_stream_capturing():
+            host = _PINNED_LENS.get(vals)
+            if host is None:
+                raise RuntimeError("npu_fused_infer_attention_score: list-valued sequence lengths under hipGraph "
+                                   "capture need a warm-up run first (or pass them as a device tensor)")
+            out = torch.empty(len(vals), dtype=torch.int64, device=device)
+            out.copy_(host, non_blocking=True)
+            return out
     return torch.tensor(vals, dtype=torch.int64, device=device)
 
 

@@ -10,6 +10,7 @@ tensors read by the kernels, so a replay with new values needs no re-capture.
 from __future__ import annotations
 
 import logging
+import threading
 from typing import Any, Callable, Dict, List, Sequence, Tuple
 
 import torch
@@ -19,6 +20,15 @@ logger = logging.getLogger("torchair_amd")
 # process-wide counts, for diagnostics and tests: graphs captured, and calls that ran eagerly
 # because a graph could not be captured or the capture limit was reached
 stats = {"captures": 0, "eager_fallbacks": 0}
+
+_state = threading.local()
+
+
+def preparing_capture() -> bool:
+    """True while the eager warm-up run that precedes a capture is executing (on this thread). Ops
+    that need host-side resources inside the captured graph (pinned buffers) create them then:
+    nothing may allocate pinned memory while a stream is being captured."""
+    return getattr(_state, "warmup", False)
 
 
 def _signature(args: Sequence[Any], by_pointer: Sequence[bool]) -> Tuple:
@@ -54,7 +64,11 @@ class _Captured:
         with torch.cuda.stream(side):
             # warm-up outside capture (allocator state, lazy library loading); its result is the
             # result of this first call, so side effects on inputs happen exactly once per call
-            self.first_outputs = fn(*self.inputs)
+            _state.warmup = True
+            try:
+                self.first_outputs = fn(*self.inputs)
+            finally:
+                _state.warmup = False
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
