@@ -130,6 +130,18 @@ int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t m, int64_t
                        const void* bias, int bias_dtype, int out_dtype, void* out,
                        void* workspace, size_t ws_bytes, void* stream);
 
+/* No counterpart in the reference. tai_grouped_matmul without a workspace argument and without
+ * any allocation, for callers that cannot allocate device memory (code under hipGraph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Its scratch is a static device array of
+ * tai_grouped_matmul_noalloc_max_scratch() bytes (1 MiB) per device, held until the process ends;
+ * calls whose tai_grouped_matmul_workspace_size exceeds it fail with TAI_ERR_INVALID. Calls that
+ * overlap on one device share that array and race. Same arguments and results otherwise. */
+size_t tai_grouped_matmul_noalloc_max_scratch(void);
+int tai_grouped_matmul_noalloc(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                               int64_t num_groups, int w_layout, const int64_t* group_list,
+                               int group_list_type, const float* scale, const float* per_token_scale,
+                               const void* bias, int bias_dtype, int out_dtype, void* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * npu_grouped_matmul_swiglu_quant_v2 (dequant_mode 0, quant_mode 0, int8 out): the grouped
  * W8A8 GEMM of the MoE gate_up projection fused with dequant_swiglu_quant. For expert e's rows:

@@ -32,6 +32,9 @@ _SIGS = {
     "tai_grouped_matmul": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P,
                 _P, c_size_t, _P]),
+    "tai_grouped_matmul_noalloc_max_scratch": (c_size_t, []),
+    "tai_grouped_matmul_noalloc": (
+        c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P, _P]),
     "tai_grouped_matmul_swiglu_quant_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "tai_grouped_matmul_swiglu_quant": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, _P, _P, c_size_t, _P]),

@@ -14,6 +14,7 @@
 // Linear workgroup ids are remapped so that each XCD (ids dispatched round-robin over 8
 // XCDs) receives a contiguous range of tiles: tiles that share activation rows and weight
 // columns meet in the same L2.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1229,6 +1230,11 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
   return launch_status("tai_quant_matmul");
 }
 
+static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                               int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
+                               const float* scale, const float* per_token_scale, const void* bias, int bias_dtype,
+                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream);
+
 extern "C" size_t tai_grouped_matmul_workspace_size(int64_t m, int64_t n, int64_t num_groups) {
   (void)n;
   // [live slot count, padded to 256 B][tile map][row -> group map]
@@ -1239,6 +1245,73 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
                                   int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
                                   const float* scale, const float* per_token_scale, const void* bias, int bias_dtype,
                                   int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream) {
+  return grouped_matmul_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, scale,
+                             per_token_scale, bias, bias_dtype, out_dtype, out, workspace, ws_bytes, stream);
+}
+
+// ----------------------------------------------------------------------------- no-allocation variant
+// The grouped GEMM's scratch (tile table, live count, row -> group map) lives in a file-scope device
+// array instead of a caller workspace. Each device holds its own copy; its address is looked up once
+// per device with hipGetSymbolAddress and only that address reaches the kernels. Calls on one device
+// share the array, so calls that overlap on one device race; every call rewrites what it reads (the
+// prologue writes the whole table and count), so nothing has to start at zero.
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Address of this device's copy of `scratch` (looked up on the device's first call).
+void* device_scratch(int* err_dev) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    *err_dev = dev;
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (g_scratch_err[dev] != hipSuccess) (void)hipGetLastError();
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  *err_dev = dev;
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" size_t tai_grouped_matmul_noalloc_max_scratch(void) { return kNoAllocScratchBytes; }
+
+extern "C" int tai_grouped_matmul_noalloc(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                                          int64_t num_groups, int w_layout, const int64_t* group_list,
+                                          int group_list_type, const float* scale, const float* per_token_scale,
+                                          const void* bias, int bias_dtype, int out_dtype, void* out, void* stream) {
+  TAI_CHECK_ARG(m >= 0 && n >= 0 && num_groups >= 1 && num_groups <= 2048, "tai_grouped_matmul_noalloc: bad sizes");
+  const size_t need = tai_grouped_matmul_workspace_size(m, n, num_groups);
+  if (need > kNoAllocScratchBytes) {
+    set_error("tai_grouped_matmul_noalloc: %lld rows and %lld groups need %zu bytes of scratch; the no-allocation "
+              "entry point holds %zu (use tai_grouped_matmul with a workspace)",
+              static_cast<long long>(m), static_cast<long long>(num_groups), need, kNoAllocScratchBytes);
+    return TAI_ERR_INVALID;
+  }
+  int dev = -1;
+  void* ws = device_scratch(&dev);
+  if (ws == nullptr) {
+    set_error("tai_grouped_matmul_noalloc: no scratch address for device %d (%s)", dev,
+              (dev >= 0 && dev < kMaxDevices) ? hipGetErrorString(g_scratch_err[dev]) : "no current device");
+    return TAI_ERR_LAUNCH;
+  }
+  return grouped_matmul_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, scale,
+                             per_token_scale, bias, bias_dtype, out_dtype, out, ws, kNoAllocScratchBytes, stream);
+}
+
+static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                               int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
+                               const float* scale, const float* per_token_scale, const void* bias, int bias_dtype,
+                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 0 && num_groups >= 1, "tai_grouped_matmul: bad sizes");
   TAI_CHECK_ARG(num_groups <= 2048, "tai_grouped_matmul: at most 2048 groups");
   TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK, "tai_grouped_matmul: w_layout");
