@@ -290,7 +290,10 @@ int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int6
                     const int64_t* k_strides, const int64_t* v_strides,
                     const int64_t* out_strides, const int64_t* seq_lens_q,
                     const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
-                    void* stream);
+                    void* workspace, size_t ws_bytes, void* stream);
+/* Bytes of the prefill workspace: work-queue counters and the rescaling pass's item list, which the
+ * call clears itself. */
+size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv);
 
 /* ---------------------------------------------------------------------------------------
  * npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache

@@ -232,3 +232,28 @@ def test_mla_segments_longer_than_a_page_window():
     # segments cross the 64-page window of page ids the kernel holds and reload it
     lens, h, bs = [140000, 140000, 140000, 120000], 16, 32
     _check_mla(lens, h, bs, 125)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_prefill_rising_logits_take_the_rescaling_loop(d):
+    # Keys grow along the sequence, so a query's logits rise by far more than the fast loop's 2^64
+    # headroom (log2 units) above the max of the first tile it sees: those waves switch to the
+    # rescaling loop mid-sequence. Batch 1 keeps random keys (fast loop only).
+    gen = torch.Generator().manual_seed(112)
+    b, s, hq, hkv = 2, 333, 4, 2
+    q = torch.randn(b, s, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    q[0] = 1.0
+    k[0] = (torch.arange(s, dtype=torch.float32) * (12.0 / s)).view(s, 1, 1).expand(s, hkv, d).to(torch.bfloat16)
+    lens = torch.tensor([s, 250])
+    for sparse_mode, causal in ((3, 1), (0, 0)):
+        out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lens, lens, hq, hkv, "BSND", sparse_mode, lse=True)
+        want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lens.numpy(), lens.numpy(), causal,
+                                       1.0 / math.sqrt(d))
+        assert np.isfinite(f32np(out)).all()
+        assert_close(f32np(out), want)
+        got = lse.cpu().numpy().reshape(b, hq, s)
+        fin = np.isfinite(wl)
+        np.testing.assert_array_equal(np.isfinite(got), fin)
+        np.testing.assert_allclose(got[fin], wl[fin], rtol=1e-3, atol=1e-3)

@@ -276,10 +276,12 @@ def fia_cuda(query, key, value, **kw):
     os_ = _strides_bshd(out, ol, hq)
     _check(hq % n_kv == 0, "npu_fused_infer_attention_score: num_heads must be a multiple of num_key_value_heads")
     arr = [(_ctypes_i64(qs)), _ctypes_i64(ks), _ctypes_i64(vs), _ctypes_i64(os_)]
+    ws_bytes = _lib.query("tai_fia_prefill_workspace_size", b, s_q, hq, n_kv)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
     _lib.call("tai_fia_prefill", query.data_ptr(), key.data_ptr(), value.data_ptr(), b, s_q, s_kv, hq, n_kv, d,
               arr[0], arr[1], arr[2], arr[3], seq_q.data_ptr() if seq_q is not None else None,
               seq_kv.data_ptr() if seq_kv is not None else None, causal, scale, out.data_ptr(),
-              lse.data_ptr() if want_lse else None, stream)
+              lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
     return out, lse
 
 

@@ -427,19 +427,26 @@ DecWs dec_ws(int64_t b, int hkv, int d) {
 
 
 // ============================================================================ dense prefill
-// Work: (batch b, kv head, group of 4 "wave units"); a wave unit is (query head, 32 query rows).
-// Units of one workgroup share the kv head, so K/V tiles of 64 tokens are staged once in LDS
-// and used by all four waves. Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 puts one
-// query per lane (column), so the online-softmax rescale of O^T is a per-lane scalar and P^T
-// leaves the S^T registers already in the B-operand layout of O^T = V^T P^T.
-// K/V tiles are double buffered and filled with global_load_lds (16 bytes per lane, no register
-// round trip): the next tile is in flight while the current one is used. LDS rows are the
-// tile's token rows with 16-byte chunks XOR-swizzled by row, so the K fragment reads (32 rows,
-// same chunk) and the transposing V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes)
-// are free of bank conflicts.
-constexpr int kPQ = 32;    // query rows per wave
+// Work: (batch b, kv head, group of 4 "wave units"); a wave unit is (query head, 64 query rows).
+// Units of one workgroup share the kv head, so K/V tiles of 64 tokens are staged once in LDS and
+// used by all four waves (one per SIMD). Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 for
+// two 32-query column blocks: each K fragment read from LDS feeds two MFMAs, so the LDS traffic
+// per MFMA is half that of 32-query waves. A lane owns one query of each block, so the online-
+// softmax rescale of O^T is a per-lane scalar and P^T leaves the S^T registers already in the
+// B-operand layout of O^T = V^T P^T.
+// K/V tiles go through a three-stage ring filled with global_load_lds (16 bytes per lane, no
+// register round trip): two tiles are in flight while one is used. LDS rows are the tile's token
+// rows with 16-byte chunks XOR-swizzled by row, so the K fragment reads (32 rows, same chunk) and
+// the transposing V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes) are free of bank
+// conflicts.
+// Workgroups are ordered heaviest first over the whole launch: launch index i takes query tile
+// (last - i / (B * Hkv)) of (b, kv head) = i % (B * Hkv). The tiles of one (b, kv head) then share
+// an XCD (B * Hkv is usually a multiple of 8), whose L2 serves their common K/V.
+constexpr int kPQ = 64;    // query rows per wave (two 32-query MFMA column blocks)
 constexpr int kPKV = 64;   // kv tokens per LDS tile
-constexpr float kPfSlack = 8.0f;  // log2-domain headroom of the lazily raised softmax max
+constexpr int kPStages = 3;
+constexpr int kPfQueues = 8;  // one work queue per XCD
+constexpr float kPfSlack = 64.0f;  // log2-domain headroom of the softmax reference max
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -450,13 +457,20 @@ struct PrefillArgs {
   int64_t qs[3], ks[3], vs[3], os[3];  // element strides (batch, pos, head)
   const int64_t* lq;
   const int64_t* lkv;
+  int64_t b;
   int64_t s_q, s_kv;
   int hq, hkv, g;
   int causal;
-  float scale_log2;
+  float scale_log2;    // |scale| * log2(e), > 0
+  int neg_scale;       // the scale is negative: Q is negated on load
   int n_qt;            // query tiles per sequence
   int units_per_bk;    // n_qt * g
   int blocks_per_bk;
+  int64_t n_items;     // B * Hkv * blocks_per_bk work items
+  int n_queues;        // work queues (one per XCD)
+  int* queue;          // [kPfQueues] next-item counters, then the rescaling list's length and cursor
+  int* flags;          // [n_items]: 1 = on the rescaling list
+  int32_t* redo;       // [n_items] rescaling list
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -474,21 +488,101 @@ struct PrefillTile {
   static constexpr int kTile = kPKV * kRowBytes;       // bytes of one K (or V) tile
   static constexpr int kRpi = 1024 / kRowBytes;        // token rows per 1 KB load instruction
   static constexpr int kLoadsPerWave = kTile / 1024 / 4;
+  static constexpr int kLoadsPerTile = 2 * kLoadsPerWave;  // K and V instructions per wave per tile
+  static constexpr int kLds = kPStages * 2 * kTile;
   // LDS byte offset of (row, 16-byte chunk c) within a tile
   __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ ((row >> kRsh) & (kCpr - 1))); }
 };
 
-template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
-  using T = PrefillTile<D>;
-  __shared__ __attribute__((aligned(16))) char smem[4 * T::kTile];  // [stage][K, V]
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, so i can feed immediates
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// S^T = K Q^T step with Q^T held in AGPRs (the B operand of gfx950 MFMAs may be an AGPR), so the 64
+// registers of Q^T do not compete with the softmax for VGPRs. The compiler does not see the latency
+// of these inline-asm MFMAs: before a VALU read of S^T, prefill_s_wait() covers it. Consecutive
+// MFMAs into the same accumulator need no wait, and the operands come from LDS loads (no VALU write
+// just before), so no nop precedes them. The zeroing form takes 0 as its accumulator input; its
+// output is early-clobber, so it never shares registers with an operand.
+__device__ __forceinline__ void prefill_s_first(f32x16& acc, const bf16x8& k, const bf16x8& q) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(k), "a"(q));
+}
+__device__ __forceinline__ void prefill_s_next(f32x16& acc, const bf16x8& k, const bf16x8& q) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(k), "a"(q));
+}
+// Longer than the latency of one 32x32x16 MFMA (16 passes). The nops are tied to the accumulators,
+// so no instruction that reads one can be scheduled above them.
+__device__ __forceinline__ void prefill_s_wait(f32x16 (&s)[2][2]) {
+  asm volatile("s_nop 15\n\ts_nop 7" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1])::"memory");
+}
+// LDS fragment reads with an immediate offset (inline asm, so the explicit waits count them exactly)
+template <int IMM>
+__device__ __forceinline__ void pf_read_b128(uint4& d, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void pf_read_tr16(v2i_t& d, uint32_t addr) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(IMM));
+}
+
+// Counters and flags start at zero: a fill kernel clears them before the passes (a memset node
+// in a captured graph is avoided on purpose).
+__global__ void prefill_queue_reset(int* queue, int* flags, int64_t n_items) {
+  if (blockIdx.x == 0 && threadIdx.x < kPfQueues + 2) queue[threadIdx.x] = 0;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n_items; i += gridDim.x * 256) flags[i] = 0;
+}
+
+template <int D, bool RESCALE>
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int tid, int lane,
+                                             int w, int col, int grp);
+
+// The fast pass (RESCALE = false) takes every item; the rescaling pass takes the items the fast
+// pass put on its list (none, on ordinary data: its workgroups read an empty list and exit).
+template <int D, bool RESCALE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, grp = lane >> 5;
-  // heavy (late) query tiles first
-  const int64_t blk = blockIdx.x;
-  const int jb = a.blocks_per_bk - 1 - static_cast<int>(blk % a.blocks_per_bk);
-  const int64_t bk = blk / a.blocks_per_bk;
+  const int64_t nbk = a.b * a.hkv;
+  // Persistent workgroups (one per CU) take work items from per-XCD queues: item i of queue x is
+  // item 8 i + x of the whole list, which runs heaviest first. Taking items as CUs free up keeps
+  // the CUs busy to the end (with one workgroup per CU the hardware dispatcher's fixed order leaves
+  // a CU idle behind a long workgroup of another CU). When B * Hkv is a multiple of 8, one queue
+  // holds the items of the (b, kv head) pairs that share an XCD's L2.
+  __shared__ int64_t s_item;
+  const int q_id = static_cast<int>(blockIdx.x % a.n_queues);
+  for (;;) {
+    if (tid == 0) {
+      if constexpr (RESCALE) {
+        const int i = atomicAdd(a.queue + kPfQueues + 1, 1);
+        s_item = i < *reinterpret_cast<volatile int*>(a.queue + kPfQueues) ? a.redo[i] : a.n_items;
+      } else {
+        s_item = static_cast<int64_t>(atomicAdd(a.queue + q_id, 1)) * a.n_queues + q_id;
+      }
+    }
+    __syncthreads();  // also: every wave is done with the previous item's LDS tiles
+    const uint64_t it_u = static_cast<uint64_t>(s_item);
+    const int64_t blk = static_cast<int64_t>((static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it_u >> 32))) << 32) |
+                                             __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it_u)));
+    __syncthreads();
+    if (blk >= a.n_items) break;
+    prefill_item<D, RESCALE>(a, blk, smem, nbk, tid, lane, w, col, grp);
+  }
+}
+
+template <int D, bool RESCALE>
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int tid, int lane,
+                                             int w, int col, int grp) {
+  using T = PrefillTile<D>;
+  const int jb = a.blocks_per_bk - 1 - static_cast<int>(blk / nbk);  // heaviest query tiles first
+  const int64_t bk = blk % nbk;
   const int kvh = static_cast<int>(bk % a.hkv);
   const int64_t b = bk / a.hkv;
   const int unit = jb * 4 + w;
@@ -499,7 +593,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   const int64_t Lkv = a.lkv ? a.lkv[b] : a.s_kv;
   const int64_t shift = Lkv - Lq;  // right-down causal offset
   const int64_t q0 = static_cast<int64_t>(qt) * kPQ;
-  const int64_t myq = q0 + col;
 
   // kv extent of this wave and of the whole workgroup (uniform across the workgroup)
   auto kv_limit = [&](int64_t qlast) -> int64_t {
@@ -522,22 +615,66 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     blk_kv = (qlast >= 0 && static_cast<int64_t>(qt_lo) * kPQ < Lq) ? imax64(0, kv_limit(qlast)) : 0;
   }
 
-  // Q^T fragments (B operand): query = col, d slots 16*kd + 8*grp .. +8
-  bf16x8 qf[D / 16];
-  {
+  // Q^T fragments (B operand) of the two query blocks: query q0 + 32 qb + col, d slots 16 kd + 8 grp
+  // .. +8. With a negative scale Q is negated (exact in bf16), so the kernel always works with a
+  // positive scale and can take the row maximum of the raw scores.
+  const uint32_t qsign = a.neg_scale ? 0x80008000u : 0u;
+  bf16x8 qf[2][D / 16];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int64_t myq = q0 + 32 * qb + col;
     const bool ok = wave_live && myq < Lq;
     const uint16_t* qp = a.q + b * a.qs[0] + (ok ? myq : 0) * a.qs[1] + head * a.qs[2];
 #pragma unroll
-    for (int kd = 0; kd < D / 16; ++kd)
-      qf[kd] = as_bf16x8(ok ? *reinterpret_cast<const uint4*>(qp + 16 * kd + 8 * grp) : make_uint4(0, 0, 0, 0));
+    for (int kd = 0; kd < D / 16; ++kd) {
+      uint4 u = ok ? *reinterpret_cast<const uint4*>(qp + 16 * kd + 8 * grp) : make_uint4(0, 0, 0, 0);
+      u.x ^= qsign; u.y ^= qsign; u.z ^= qsign; u.w ^= qsign;
+      qf[qb][kd] = as_bf16x8(u);
+    }
   }
-  f32x16 acc[D / 32];
+  // pin Q^T to AGPRs; the nops cover the AGPR writes before the first MFMA reads them
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i)
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
-  const int64_t qlim = (a.causal == 1) ? myq + shift : (a.causal == 2 ? myq : INT64_MAX);
+    for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+a"(qf[qb][kd]));
+  asm volatile("s_nop 7" ::: "memory");
+
+  f32x16 acc[2][D / 32];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[qb][i][r] = 0.0f;
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  // last kv token + 1 that each of the lane's two queries sees
+  int64_t qend[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int64_t myq = q0 + 32 * qb + col;
+    qend[qb] = (a.causal == 1) ? min<int64_t>(Lkv, myq + shift + 1) : (a.causal == 2 ? min<int64_t>(Lkv, myq + 1) : Lkv);
+  }
+
+  // LDS byte offsets (within a stage) of this lane's fragment reads. Rows 32 further (the second
+  // 32-token half of K) or 16 further (the next 16-token block of V) keep the row's swizzle, so
+  // they are immediate offsets.
+  const int h16 = lane >> 4, j16 = lane & 15;
+  uint32_t koff[D / 16];
+#pragma unroll
+  for (int kd = 0; kd < D / 16; ++kd) koff[kd] = T::off(col, 2 * kd + grp);
+  // V: k slots of lane group grp in 16-token block kb are tokens 16kb + 4grp + {0..3} (lo read) and
+  // 16kb + 8 + 4grp + {0..3} (hi read): in each ds_read_b64_tr_b16 source lane j16 addresses
+  // V[k0 + j16/4][nb + 4 (j16 & 3)] and lane j16 receives V[k0 .. k0+3][nb + j16], nb = 32dt + 16 (h16 & 1)
+  uint32_t voff[2][D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+    const int nb = 32 * dt + 16 * (h16 & 1) + 4 * (j16 & 3);
+    const int r_lo = 4 * grp + (j16 >> 2);
+    voff[0][dt] = T::kTile + T::off(r_lo, nb >> 3) + 2 * (nb & 7);
+    voff[1][dt] = T::kTile + T::off(r_lo + 8, nb >> 3) + 2 * (nb & 7);
+  }
+  static_assert(((32 >> T::kRsh) % T::kCpr) == 0 && ((16 >> T::kRsh) % T::kCpr) == 0, "row steps keep the swizzle");
+  const uint32_t smem_base = lds_u32(smem);
 
   // global_load_lds of tile [t0, t0 + 64) into stage s; rows past the end load the last row
   // (finite values; their scores are masked, so they add nothing)
@@ -557,128 +694,208 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   };
 
   const int64_t ntiles = cdiv(blk_kv, static_cast<int64_t>(kPKV));
-  if (ntiles > 0) issue_tile(0, 0);
-  const int h16 = lane >> 4, j16 = lane & 15;
-  for (int64_t it = 0; it < ntiles; ++it) {
+#pragma unroll
+  for (int s = 0; s < kPStages - 1; ++s)
+    if (s < ntiles) issue_tile(s * kPKV, s);
+
+  // Phase A of tile it: ring wait, barrier, refill, S^T = K Q^T and the masked row maxima (log2
+  // domain); returns false when this wave has nothing to do in the tile (the ring steps are still
+  // taken). Scores stay raw (unscaled); masked ones become -inf.
+  f32x16 s[2][2];  // [32-token half][query block]
+  float mx[2];
+  auto phase_a = [&](int64_t it) -> bool {
     const int64_t t0 = it * kPKV;
-    __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0): this wave's loads of tile it
+    // tile it has landed once only the tiles issued after it remain in flight (loads complete in order)
+    static_assert(kPStages == 3, "the wait below counts one tile in flight behind the current one");
+    if (it + 1 < ntiles) __builtin_amdgcn_s_waitcnt((T::kLoadsPerTile & 0xF) | ((T::kLoadsPerTile >> 4) << 14) | 0x70 | 0xF00);
+    else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + 1 < ntiles) issue_tile(t0 + kPKV, static_cast<int>((it + 1) & 1));
-    if (!(wave_live && t0 < wave_kv)) continue;
-    const uint32_t kst = lds_u32(smem + (it & 1) * 2 * T::kTile);
-    const uint32_t vst = kst + T::kTile;
-    f32x16 s[2];
-    float mx = -INFINITY;
-    const bool need_mask = t0 + kPKV > wave_clean;
+    if (it + kPStages - 1 < ntiles) issue_tile(t0 + (kPStages - 1) * kPKV, static_cast<int>((it + kPStages - 1) % kPStages));
+    if (!(wave_live && t0 < wave_kv)) return false;
+    const uint32_t sb = smem_base + static_cast<uint32_t>(it % kPStages) * 2 * T::kTile;
+    uint32_t ka[D / 16];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int kd = 0; kd < D / 16; ++kd) ka[kd] = sb + koff[kd];
+    static_for<2>([&](auto stc) {
+      constexpr int st = decltype(stc)::value;
+      if (t0 + 32 * st >= wave_kv) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
-      if (t0 + 32 * st < wave_kv) {
-        const int row = 32 * st + col;
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[st][qb][r] = -INFINITY;
+      } else {
         bf16x8 kf[D / 16];
-#pragma unroll
-        for (int kd = 0; kd < D / 16; ++kd) {
+        static_for<D / 16>([&](auto kdc) {
+          constexpr int kd = decltype(kdc)::value;
           uint4 raw;
-          asm volatile("ds_read_b128 %0, %1" : "=v"(raw) : "v"(kst + T::off(row, 2 * kd + grp)));
+          pf_read_b128<st * 32 * T::kRowBytes>(raw, ka[kd]);
           kf[kd] = as_bf16x8(raw);
-        }
+        });
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         // the fragments pass through empty asm after the wait, so no use is scheduled before it
 #pragma unroll
         for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+v"(kf[kd]));
 #pragma unroll
-        for (int kd = 0; kd < D / 16; ++kd) s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kd], qf[kd], s[st], 0, 0, 0);
-      }
-      if (need_mask) {
+        for (int qb = 0; qb < 2; ++qb) prefill_s_first(s[st][qb], kf[0], qf[qb][0]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t t = t0 + 32 * st + 8 * (r >> 2) + 4 * grp + (r & 3);
-          const bool ok = t < Lkv && t <= qlim;
-          const float v = ok ? s[st][r] * a.scale_log2 : -INFINITY;
-          s[st][r] = v;
-          mx = fmaxf(mx, v);
+        for (int kd = 1; kd < D / 16; ++kd)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) prefill_s_next(s[st][qb], kf[kd], qf[qb][kd]);
+      }
+    });
+    prefill_s_wait(s);
+    float m[2];
+    if (t0 + kPKV > wave_clean) {  // a tile on the causal diagonal or past a sequence end: mask
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        // the query's limit relative to the tile start, as a 32-bit value in [0, 64]
+        const int lim = static_cast<int>(imin64(kPKV, imax64(0, qend[qb] - t0)));
+        m[qb] = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int t = 32 * st + 8 * (r >> 2) + 4 * grp + (r & 3);
+            const float v = t < lim ? s[st][qb][r] : -INFINITY;
+            s[st][qb][r] = v;
+            m[qb] = fmaxf(m[qb], v);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        m[qb] = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) m[qb] = fmaxf(m[qb], s[st][qb][r]);
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) mx[qb] = fmaxf(m[qb], __shfl_xor(m[qb], 32, 64)) * a.scale_log2;
+    return true;
+  };
+  // Phase B: P = exp2(scale * S - m_run), l += rowsum(P), O^T += V^T P^T. With RESCALE the reference
+  // max is raised (and O^T, l rescaled) when a query's tile max exceeds it by more than kPfSlack;
+  // without, the caller has checked that no query needs that. Keeping the rescale out of the fast
+  // loop keeps the O^T accumulators in place (rescaling code in the loop makes the compiler move all
+  // of them through VGPRs on every tile). l sums the bf16-rounded P that the PV MFMAs use.
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  auto phase_b = [&](int64_t it, auto rescale_tag) {
+    constexpr bool RAISE = decltype(rescale_tag)::value;
+    const int64_t t0 = it * kPKV;
+    const uint32_t sb = smem_base + static_cast<uint32_t>(it % kPStages) * 2 * T::kTile;
+    bf16x8 pf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if constexpr (RAISE) {
+        if (__any(mx[qb] > m_run[qb] + kPfSlack)) {
+          const float m_new = fmaxf(m_run[qb], mx[qb]);
+          const float alpha = (m_run[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[qb][i][r] *= alpha;
+          m_run[qb] = m_new;
         }
       } else {
+        // a query that has seen nothing so far (m_run = -inf: O^T and l are zero) takes this tile's max
+        if (m_run[qb] == -INFINITY) m_run[qb] = mx[qb];
+      }
+      const float neg_m = (m_run[qb] == -INFINITY) ? 0.0f : -m_run[qb];
+      float rs[2] = {0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[st][r] *= a.scale_log2;
-          mx = fmaxf(mx, s[st][r]);
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][qb][8 * kb2 + j], a.scale_log2, neg_m));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][qb][8 * kb2 + j + 1], a.scale_log2, neg_m));
+            const bf16x2_t pk = __builtin_convertvector((f32x2_t){e0, e1}, bf16x2_t);
+            pf[qb][2 * st + kb2][j] = pk[0];
+            pf[qb][2 * st + kb2][j + 1] = pk[1];
+            rs[j >> 2 & 1] = __builtin_amdgcn_fdot2_f32_bf16(pk, ones, rs[j >> 2 & 1], false);
+          }
+      float r = rs[0] + rs[1];
+      r += __shfl_xor(r, 32, 64);
+      l_run[qb] += r;
+    }
+    // ---- O^T += V^T P^T; each V fragment feeds both query blocks
+    uint32_t va[2][D / 32];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) va[h][dt] = sb + voff[h][dt];
+    static_for<4>([&](auto kbc) {
+      constexpr int kb = decltype(kbc)::value;
+      if (t0 + 16 * kb < wave_kv) {
+        v2i_t lo[D / 32], hi[D / 32];
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          pf_read_tr16<kb * 16 * T::kRowBytes>(lo[dt], va[0][dt]);
+          pf_read_tr16<kb * 16 * T::kRowBytes>(hi[dt], va[1][dt]);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const bf16x8 vv = __builtin_bit_cast(bf16x8, (v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]}));
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            acc[qb][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, pf[qb][kb], acc[qb][dt], 0, 0, 0);
         }
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // Online softmax with a lazily raised reference max (as in the MLA kernel): m_run moves, and O^T
-    // and l are rescaled, only when a query's tile max exceeds it by more than kPfSlack (log2 units),
-    // so P <= 2^kPfSlack between raises; the result is the same.
-    if (__any(mx > m_run + kPfSlack)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+    });
+  };
+  if constexpr (!RESCALE) {
+    // Fast pass: the reference max of each query is the max of the first tile it sees, and stays. A
+    // wave whose tile max rises above it by more than kPfSlack (2^64 of headroom in P, l and O^T)
+    // puts the item on the rescaling pass's list and stops computing (it still takes its part in the
+    // ring); the rescaling pass redoes the whole item.
+    bool dead = false;
+    for (int64_t it = 0; it < ntiles; ++it) {
+      if (!phase_a(it) || dead) continue;
+      bool rise = false;
 #pragma unroll
-      for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
-      m_run = m_new;
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
-    float rs = 0.0f;
-    bf16x8 pf[4];
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e = __builtin_amdgcn_exp2f(s[st][8 * kb2 + j] - m_use);
-          rs += e;
-          pf[2 * st + kb2][j] = static_cast<__bf16>(e);
-        }
-    rs += __shfl_xor(rs, 32, 64);
-    l_run += rs;
-    // ---- O^T += V^T P^T. The k slots of lane group grp in k-block kb are tokens
-    //      16kb + 4grp + {0..3} and 16kb + 8 + 4grp + {0..3} (the S^T row order); each half is
-    //      one ds_read_b64_tr_b16: source lane j16 addresses V[k0 + j16/4][nb + 4 (j16 & 3)] and
-    //      lane j16 receives V[k0 .. k0+3][nb + j16], nb = 32dt + 16 (h16 & 1).
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      if (t0 + 16 * kb >= wave_kv) break;
-      v2i_t lo[D / 32], hi[D / 32];
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const int nb = 32 * dt + 16 * (h16 & 1) + 4 * (j16 & 3);
-        const int r_lo = 16 * kb + 4 * grp + (j16 >> 2), r_hi = r_lo + 8;
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo[dt]) : "v"(vst + T::off(r_lo, nb >> 3) + 2 * (nb & 7)));
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi[dt]) : "v"(vst + T::off(r_hi, nb >> 3) + 2 * (nb & 7)));
+      for (int qb = 0; qb < 2; ++qb) rise |= m_run[qb] != -INFINITY && mx[qb] > m_run[qb] + kPfSlack;
+      if (__any(rise)) {
+        dead = true;
+        if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
+        continue;
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const v4i_t vv = v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]};
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pf[kb], acc[dt], 0, 0, 0);
-      }
+      phase_b(it, std::false_type());
     }
+    if (dead) return;
+  } else {
+    for (int64_t it = 0; it < ntiles; ++it)
+      if (phase_a(it)) phase_b(it, std::true_type());
   }
-  if (!unit_ok || myq >= a.s_q) return;
+  if (!unit_ok) return;
   // ---- write O (lane = query col, d = 32dt + 8(r/4) + 4grp + r%4) and lse
-  const bool live = wave_live && myq < Lq && l_run > 0.0f;
-  const float inv = live ? 1.0f / l_run : 0.0f;
-  uint16_t* op = a.out + b * a.os[0] + myq * a.os[1] + head * a.os[2];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int qb = 0; qb < 2; ++qb) {
+    const int64_t myq = q0 + 32 * qb + col;
+    if (myq >= a.s_q) continue;
+    const bool live = wave_live && myq < Lq && l_run[qb] > 0.0f;
+    const float inv = live ? 1.0f / l_run[qb] : 0.0f;
+    uint16_t* op = a.out + b * a.os[0] + myq * a.os[1] + head * a.os[2];
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int d = 32 * dt + 8 * r4 + 4 * grp;
-      uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4] * inv)) |
-                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 1] * inv)) << 16);
-      uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 2] * inv)) |
-                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 3] * inv)) << 16);
-      *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
-    }
-  if (a.lse && grp == 0)
-    a.lse[(b * a.hq + head) * a.s_q + myq] = live ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = 32 * dt + 8 * r4 + 4 * grp;
+        uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4] * inv)) |
+                      (static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 1] * inv)) << 16);
+        uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 2] * inv)) |
+                      (static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
+      }
+    if (a.lse && grp == 0)
+      a.lse[(b * a.hq + head) * a.s_q + myq] = live ? (m_run[qb] + log2f(l_run[qb])) * kLn2 : -INFINITY;
+  }
 }
 
 // ============================================================================ MLA absorbed decode
@@ -753,15 +970,6 @@ static_assert(kMlaLds <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ int mla_x(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-template <class F, int... I>
-__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-// f(std::integral_constant<int, i>) for i = 0 .. N-1, so i can feed immediates
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 template <int IMM>
 __device__ __forceinline__ void lds_read_b128(v4i_t& d, uint32_t addr) {
@@ -792,7 +1000,7 @@ __device__ __forceinline__ void mfma_vgpr(f32x16& acc, const bf16x8& a, const bf
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void mfma_vgpr_zero(f32x16& acc, const bf16x8& a, const bf16x8& b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(a), "v"(b));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
 }
 // The nops are tied to the accumulator (a read-write operand), so no instruction that reads it can
 // be scheduled above them.
@@ -1437,11 +1645,17 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
   return launch_status("tai_fia_paged_decode");
 }
 
+extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv) {
+  if (b <= 0 || s_q <= 0 || hq <= 0 || hkv <= 0) return 256;
+  const int64_t n_items = b * hkv * cdiv(cdiv(s_q, kPQ) * (hq / hkv), 4);
+  return static_cast<size_t>(256 + 8 * n_items + 256);
+}
+
 extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q, int64_t s_kv, int hq,
                                int hkv, int d, const int64_t* q_strides, const int64_t* k_strides,
                                const int64_t* v_strides, const int64_t* out_strides, const int64_t* seq_lens_q,
                                const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
-                               void* stream) {
+                               void* workspace, size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(b >= 0 && s_q >= 0 && s_kv >= 0, "tai_fia_prefill: negative size");
   TAI_CHECK_ARG(hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_prefill: heads must be a multiple of kv heads");
   TAI_CHECK_ARG(causal >= 0 && causal <= 2, "tai_fia_prefill: causal must be 0, 1 (right-down) or 2 (left-up)");
@@ -1459,15 +1673,60 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.out = static_cast<uint16_t*>(out);
   a.lse = lse;
   for (int i = 0; i < 3; ++i) { a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = out_strides[i]; }
-  a.lq = seq_lens_q; a.lkv = seq_lens_kv; a.s_q = s_q; a.s_kv = s_kv;
-  a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.causal = causal; a.scale_log2 = scale * kLog2e;
+  a.lq = seq_lens_q; a.lkv = seq_lens_kv; a.b = b; a.s_q = s_q; a.s_kv = s_kv;
+  a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.causal = causal;
+  // the kernel works with a positive scale (a negative one negates Q); a zero scale makes every score
+  // zero, which the smallest normal scale reproduces up to rounding far below bf16 resolution
+  a.neg_scale = scale < 0.0f;
+  a.scale_log2 = fmaxf(fabsf(scale) * kLog2e, 1.17549435e-38f);
   a.n_qt = static_cast<int>(cdiv(s_q, kPQ));
   a.units_per_bk = a.n_qt * a.g;
   a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, 4));
-  const dim3 grid(static_cast<unsigned>(b * hkv * a.blocks_per_bk));
+  // the three-stage ring needs more LDS than a workgroup gets by default (set once per process)
+  static const bool lds_ok = [] {
+    const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<64, false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<64>::kLds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<64, true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<64>::kLds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<128>::kLds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<128>::kLds) == hipSuccess;
+    (void)hipGetLastError();
+    return ok;
+  }();
+  if (!lds_ok) {
+    set_error("tai_fia_prefill: the device cannot give a workgroup %d bytes of LDS", PrefillTile<128>::kLds);
+    return TAI_ERR_LAUNCH;
+  }
+  a.n_items = b * hkv * a.blocks_per_bk;
+  const size_t need = tai_fia_prefill_workspace_size(b, s_q, hq, hkv);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_fia_prefill: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  static const int n_cu = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    return n > 0 ? n : 256;
+  }();
+  a.n_queues = n_cu < kPfQueues ? n_cu : kPfQueues;
+  a.queue = static_cast<int*>(workspace);
+  a.flags = a.queue + 64;
+  a.redo = a.flags + a.n_items;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (d == 64) prefill_kernel<64><<<grid, 256, 0, st>>>(a);
-  else prefill_kernel<128><<<grid, 256, 0, st>>>(a);
+  prefill_queue_reset<<<static_cast<unsigned>(std::min<int64_t>(64, cdiv(a.n_items, 256))), 256, 0, st>>>(a.queue, a.flags, a.n_items);
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(n_cu, a.n_items)));
+  if (d == 64) {
+    prefill_kernel<64, false><<<grid, 256, PrefillTile<64>::kLds, st>>>(a);
+    prefill_kernel<64, true><<<grid, 256, PrefillTile<64>::kLds, st>>>(a);
+  } else {
+    prefill_kernel<128, false><<<grid, 256, PrefillTile<128>::kLds, st>>>(a);
+    prefill_kernel<128, true><<<grid, 256, PrefillTile<128>::kLds, st>>>(a);
+  }
   return launch_status("tai_fia_prefill");
 }
 
