@@ -427,24 +427,24 @@ DecWs dec_ws(int64_t b, int hkv, int d) {
 
 
 // ============================================================================ dense prefill
-// Work: (batch b, kv head, group of 4 "wave units"); a wave unit is (query head, 64 query rows).
-// Units of one workgroup share the kv head, so K/V tiles of 64 tokens are staged once in LDS and
-// used by all four waves (one per SIMD). Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 for
-// two 32-query column blocks: each K fragment read from LDS feeds two MFMAs, so the LDS traffic
-// per MFMA is half that of 32-query waves. A lane owns one query of each block, so the online-
-// softmax rescale of O^T is a per-lane scalar and P^T leaves the S^T registers already in the
-// B-operand layout of O^T = V^T P^T.
+// Work item: (batch b, kv head, 8 "wave units"); a wave unit is (query head, 32 query rows), and the
+// units of (b, kv head) run query-tile major, so an item is two 32-query tiles of 4 heads when
+// Hq / Hkv = 4. The 8 waves of an item share the kv head: K/V tiles of 64 tokens are staged once in
+// LDS and used by all of them. Two waves per SIMD: one wave's softmax (VALU) runs while the other's
+// MFMAs do (a lone wave issues a VALU instruction only every ~8 cycles).
+// Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 puts one query per lane (column), so the
+// online-softmax rescale of O^T is a per-lane scalar and P^T leaves the S^T registers already in
+// the B-operand layout of O^T = V^T P^T.
 // K/V tiles go through a three-stage ring filled with global_load_lds (16 bytes per lane, no
 // register round trip): two tiles are in flight while one is used. LDS rows are the tile's token
 // rows with 16-byte chunks XOR-swizzled by row, so the K fragment reads (32 rows, same chunk) and
 // the transposing V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes) are free of bank
 // conflicts.
-// Workgroups are ordered heaviest first over the whole launch: launch index i takes query tile
-// (last - i / (B * Hkv)) of (b, kv head) = i % (B * Hkv). The tiles of one (b, kv head) then share
-// an XCD (B * Hkv is usually a multiple of 8), whose L2 serves their common K/V.
-constexpr int kPQ = 64;    // query rows per wave (two 32-query MFMA column blocks)
-constexpr int kPKV = 64;   // kv tokens per LDS tile
-constexpr int kPStages = 3;
+// Persistent workgroups (one per CU) take items from per-XCD work queues, heaviest items first.
+constexpr int kPQ = 32;       // query rows per wave
+constexpr int kPWaves = 8;    // waves (units) per item
+constexpr int kPKV = 64;      // kv tokens per LDS tile
+constexpr int kPStages = 4;
 constexpr int kPfQueues = 8;  // one work queue per XCD
 constexpr float kPfSlack = 64.0f;  // log2-domain headroom of the softmax reference max
 
@@ -465,7 +465,7 @@ struct PrefillArgs {
   int neg_scale;       // the scale is negative: Q is negated on load
   int n_qt;            // query tiles per sequence
   int units_per_bk;    // n_qt * g
-  int blocks_per_bk;
+  int blocks_per_bk;   // items per (b, kv head)
   int64_t n_items;     // B * Hkv * blocks_per_bk work items
   int n_queues;        // work queues (one per XCD)
   int* queue;          // [kPfQueues] next-item counters, then the rescaling list's length and cursor
@@ -487,11 +487,19 @@ struct PrefillTile {
   static constexpr int kRsh = D == 128 ? 0 : 1;        // rows per 256-byte bank cycle = 1 << kRsh
   static constexpr int kTile = kPKV * kRowBytes;       // bytes of one K (or V) tile
   static constexpr int kRpi = 1024 / kRowBytes;        // token rows per 1 KB load instruction
-  static constexpr int kLoadsPerWave = kTile / 1024 / 4;
+  static constexpr int kLoadsPerWave = kTile / 1024 / kPWaves;
   static constexpr int kLoadsPerTile = 2 * kLoadsPerWave;  // K and V instructions per wave per tile
   static constexpr int kLds = kPStages * 2 * kTile;
+  static_assert(kLoadsPerWave * kPWaves * 1024 == kTile, "load split");
+  // XOR key of a row's 16-byte chunks. Over any 16 aligned rows it is a permutation (the K fragment
+  // reads: 16 rows at one chunk hit 16 distinct 16-byte bank groups), and over 4 aligned rows of
+  // one 256-byte bank line it takes 4 values that differ above the low two bits (the transposing V
+  // reads: 4 rows x 4 consecutive chunks hit 16 distinct bank groups). Rows 16 apart share the key.
+  __device__ static __forceinline__ int swz(int row) {
+    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+  }
   // LDS byte offset of (row, 16-byte chunk c) within a tile
-  __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ ((row >> kRsh) & (kCpr - 1))); }
+  __device__ static __forceinline__ int off(int row, int c) { return row * kRowBytes + 16 * (c ^ swz(row)); }
 };
 
 template <class F, int... I>
@@ -504,23 +512,8 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// S^T = K Q^T step with Q^T held in AGPRs (the B operand of gfx950 MFMAs may be an AGPR), so the 64
-// registers of Q^T do not compete with the softmax for VGPRs. The compiler does not see the latency
-// of these inline-asm MFMAs: before a VALU read of S^T, prefill_s_wait() covers it. Consecutive
-// MFMAs into the same accumulator need no wait, and the operands come from LDS loads (no VALU write
-// just before), so no nop precedes them. The zeroing form takes 0 as its accumulator input; its
-// output is early-clobber, so it never shares registers with an operand.
-__device__ __forceinline__ void prefill_s_first(f32x16& acc, const bf16x8& k, const bf16x8& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(k), "a"(q));
-}
-__device__ __forceinline__ void prefill_s_next(f32x16& acc, const bf16x8& k, const bf16x8& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(k), "a"(q));
-}
-// Longer than the latency of one 32x32x16 MFMA (16 passes). The nops are tied to the accumulators,
-// so no instruction that reads one can be scheduled above them.
-__device__ __forceinline__ void prefill_s_wait(f32x16 (&s)[2][2]) {
-  asm volatile("s_nop 15\n\ts_nop 7" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1])::"memory");
-}
+// With two waves per SIMD a wave has 256 registers; keeping every operand and accumulator in VGPRs
+// (no AGPR use in the kernel) lets the compiler use all 256 of them as VGPRs.
 // LDS fragment reads with an immediate offset (inline asm, so the explicit waits count them exactly)
 template <int IMM>
 __device__ __forceinline__ void pf_read_b128(uint4& d, uint32_t addr) {
@@ -539,23 +532,23 @@ __global__ void prefill_queue_reset(int* queue, int* flags, int64_t n_items) {
 }
 
 template <int D, bool RESCALE>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int tid, int lane,
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int lane,
                                              int w, int col, int grp);
 
 // The fast pass (RESCALE = false) takes every item; the rescaling pass takes the items the fast
 // pass put on its list (none, on ordinary data: its workgroups read an empty list and exit).
+// Queue x hands out items x, x + 8, x + 16, ... of the heaviest-first list (item i: query tiles
+// blocks_per_bk - 1 - i / (B * Hkv) of (b, kv head) = i % (B * Hkv)). Taking items as CUs free up
+// keeps the CUs busy to the end (with one workgroup per CU, the hardware dispatcher's fixed order
+// leaves a CU idle behind another CU's long workgroup). When B * Hkv is a multiple of 8 a queue
+// holds the items of the (b, kv head) pairs whose K/V then stays in one XCD's L2.
 template <int D, bool RESCALE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, grp = lane >> 5;
   const int64_t nbk = a.b * a.hkv;
-  // Persistent workgroups (one per CU) take work items from per-XCD queues: item i of queue x is
-  // item 8 i + x of the whole list, which runs heaviest first. Taking items as CUs free up keeps
-  // the CUs busy to the end (with one workgroup per CU the hardware dispatcher's fixed order leaves
-  // a CU idle behind a long workgroup of another CU). When B * Hkv is a multiple of 8, one queue
-  // holds the items of the (b, kv head) pairs that share an XCD's L2.
   __shared__ int64_t s_item;
   const int q_id = static_cast<int>(blockIdx.x % a.n_queues);
   for (;;) {
@@ -573,19 +566,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                                              __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it_u)));
     __syncthreads();
     if (blk >= a.n_items) break;
-    prefill_item<D, RESCALE>(a, blk, smem, nbk, tid, lane, w, col, grp);
+    prefill_item<D, RESCALE>(a, blk, smem, nbk, lane, w, col, grp);
   }
 }
 
 template <int D, bool RESCALE>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int tid, int lane,
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int lane,
                                              int w, int col, int grp) {
   using T = PrefillTile<D>;
   const int jb = a.blocks_per_bk - 1 - static_cast<int>(blk / nbk);  // heaviest query tiles first
   const int64_t bk = blk % nbk;
   const int kvh = static_cast<int>(bk % a.hkv);
   const int64_t b = bk / a.hkv;
-  const int unit = jb * 4 + w;
+  const int unit = jb * kPWaves + w;
   const bool unit_ok = unit < a.units_per_bk;
   const int qt = unit_ok ? unit / a.g : 0;
   const int head = kvh * a.g + (unit_ok ? unit % a.g : 0);
@@ -593,8 +586,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   const int64_t Lkv = a.lkv ? a.lkv[b] : a.s_kv;
   const int64_t shift = Lkv - Lq;  // right-down causal offset
   const int64_t q0 = static_cast<int64_t>(qt) * kPQ;
+  const int64_t myq = q0 + col;
 
-  // kv extent of this wave and of the whole workgroup (uniform across the workgroup)
+  // kv extent of this wave and of the whole item (uniform across the workgroup)
   auto kv_limit = [&](int64_t qlast) -> int64_t {
     if (a.causal == 1) return min<int64_t>(Lkv, qlast + shift + 1);
     if (a.causal == 2) return min<int64_t>(Lkv, qlast + 1);
@@ -606,54 +600,38 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   const int64_t wave_clean = wave_live ? imax64(0, kv_limit(q0)) - (a.causal ? 1 : 0) : 0;
   int64_t blk_kv = 0;
   {
-    const int last_unit = min(jb * 4 + 3, a.units_per_bk - 1);
-    const int qt_lo = (jb * 4) / a.g;   // units are qtile-major: the first unit has the smallest tile
-    const int qt_hi = last_unit / a.g;  // and the last unit the largest
+    const int last_unit = min(jb * kPWaves + kPWaves - 1, a.units_per_bk - 1);
+    const int qt_lo = (jb * kPWaves) / a.g;   // units are qtile-major: the first unit has the smallest tile
+    const int qt_hi = last_unit / a.g;        // and the last unit the largest
     const int64_t qlast = min<int64_t>(static_cast<int64_t>(qt_hi) * kPQ + kPQ, Lq) - 1;
-    // a workgroup whose query tiles all lie past this sequence's length has no live wave: it loads
-    // nothing (its tiles exist because the grid is sized for the longest sequence)
+    // an item whose query tiles all lie past this sequence's length has no live wave: it loads
+    // nothing (its tiles exist because the item list is sized for the longest sequence)
     blk_kv = (qlast >= 0 && static_cast<int64_t>(qt_lo) * kPQ < Lq) ? imax64(0, kv_limit(qlast)) : 0;
   }
 
-  // Q^T fragments (B operand) of the two query blocks: query q0 + 32 qb + col, d slots 16 kd + 8 grp
-  // .. +8. With a negative scale Q is negated (exact in bf16), so the kernel always works with a
-  // positive scale and can take the row maximum of the raw scores.
-  const uint32_t qsign = a.neg_scale ? 0x80008000u : 0u;
-  bf16x8 qf[2][D / 16];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int64_t myq = q0 + 32 * qb + col;
+  // Q^T fragments (B operand): query myq, d slots 16 kd + 8 grp .. +8. With a negative scale Q is
+  // negated (exact in bf16), so the kernel always works with a positive scale and takes the row
+  // maximum of the raw scores.
+  bf16x8 qf[D / 16];
+  {
+    const uint32_t qsign = a.neg_scale ? 0x80008000u : 0u;
     const bool ok = wave_live && myq < Lq;
     const uint16_t* qp = a.q + b * a.qs[0] + (ok ? myq : 0) * a.qs[1] + head * a.qs[2];
 #pragma unroll
     for (int kd = 0; kd < D / 16; ++kd) {
       uint4 u = ok ? *reinterpret_cast<const uint4*>(qp + 16 * kd + 8 * grp) : make_uint4(0, 0, 0, 0);
       u.x ^= qsign; u.y ^= qsign; u.z ^= qsign; u.w ^= qsign;
-      qf[qb][kd] = as_bf16x8(u);
+      qf[kd] = as_bf16x8(u);
     }
   }
-  // pin Q^T to AGPRs; the nops cover the AGPR writes before the first MFMA reads them
+  f32x16 acc[D / 32];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-    for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+a"(qf[qb][kd]));
-  asm volatile("s_nop 7" ::: "memory");
-
-  f32x16 acc[2][D / 32];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[qb][i][r] = 0.0f;
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
-  // last kv token + 1 that each of the lane's two queries sees
-  int64_t qend[2];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int64_t myq = q0 + 32 * qb + col;
-    qend[qb] = (a.causal == 1) ? min<int64_t>(Lkv, myq + shift + 1) : (a.causal == 2 ? min<int64_t>(Lkv, myq + 1) : Lkv);
-  }
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  // last kv token + 1 that the lane's query sees
+  const int64_t qend = (a.causal == 1) ? min<int64_t>(Lkv, myq + shift + 1) : (a.causal == 2 ? min<int64_t>(Lkv, myq + 1) : Lkv);
 
   // LDS byte offsets (within a stage) of this lane's fragment reads. Rows 32 further (the second
   // 32-token half of K) or 16 further (the next 16-token block of V) keep the row's swizzle, so
@@ -663,8 +641,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 #pragma unroll
   for (int kd = 0; kd < D / 16; ++kd) koff[kd] = T::off(col, 2 * kd + grp);
   // V: k slots of lane group grp in 16-token block kb are tokens 16kb + 4grp + {0..3} (lo read) and
-  // 16kb + 8 + 4grp + {0..3} (hi read): in each ds_read_b64_tr_b16 source lane j16 addresses
-  // V[k0 + j16/4][nb + 4 (j16 & 3)] and lane j16 receives V[k0 .. k0+3][nb + j16], nb = 32dt + 16 (h16 & 1)
+  // 16kb + 8 + 4grp + {0..3} (hi read), the S^T row order: in each ds_read_b64_tr_b16 source lane
+  // j16 addresses V[k0 + j16/4][nb + 4 (j16 & 3)] and lane j16 receives V[k0 .. k0+3][nb + j16],
+  // nb = 32dt + 16 (h16 & 1)
   uint32_t voff[2][D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) {
@@ -673,7 +652,6 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
     voff[0][dt] = T::kTile + T::off(r_lo, nb >> 3) + 2 * (nb & 7);
     voff[1][dt] = T::kTile + T::off(r_lo + 8, nb >> 3) + 2 * (nb & 7);
   }
-  static_assert(((32 >> T::kRsh) % T::kCpr) == 0 && ((16 >> T::kRsh) % T::kCpr) == 0, "row steps keep the swizzle");
   const uint32_t smem_base = lds_u32(smem);
 
   // global_load_lds of tile [t0, t0 + 64) into stage s; rows past the end load the last row
@@ -686,216 +664,183 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
     for (int i = 0; i < T::kLoadsPerWave; ++i) {
       const int q = w * T::kLoadsPerWave + i;
       const int row = q * T::kRpi + lane / T::kCpr;
-      const int c = (lane % T::kCpr) ^ ((row >> T::kRsh) & (T::kCpr - 1));
+      const int c = (lane % T::kCpr) ^ T::swz(row);
       const int64_t tok = min<int64_t>(t0 + row, Lkv - 1);
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(kbase + tok * a.ks[1] + 8 * c), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(vbase + tok * a.vs[1] + 8 * c), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
     }
   };
 
-  const int64_t ntiles = cdiv(blk_kv, static_cast<int64_t>(kPKV));
-#pragma unroll
-  for (int s = 0; s < kPStages - 1; ++s)
-    if (s < ntiles) issue_tile(s * kPKV, s);
-
-  // Phase A of tile it: ring wait, barrier, refill, S^T = K Q^T and the masked row maxima (log2
-  // domain); returns false when this wave has nothing to do in the tile (the ring steps are still
-  // taken). Scores stay raw (unscaled); masked ones become -inf.
-  f32x16 s[2][2];  // [32-token half][query block]
-  float mx[2];
-  auto phase_a = [&](int64_t it) -> bool {
-    const int64_t t0 = it * kPKV;
-    // tile it has landed once only the tiles issued after it remain in flight (loads complete in order)
-    static_assert(kPStages == 3, "the wait below counts one tile in flight behind the current one");
-    if (it + 1 < ntiles) __builtin_amdgcn_s_waitcnt((T::kLoadsPerTile & 0xF) | ((T::kLoadsPerTile >> 4) << 14) | 0x70 | 0xF00);
+  const int ntiles = static_cast<int>(cdiv(blk_kv, static_cast<int64_t>(kPKV)));
+  // Ring of kPStages = 4 slots, tile u in slot u % 4. publish(u) waits for this wave's loads of tile
+  // u and passes the workgroup barrier, after which every wave's part of tile u is in LDS; the tile
+  // issued next goes into the slot of tile u - 2 (u - 1 in the rescaling pass), whose last reads
+  // every wave has passed by then.
+  int issued = 0;
+  auto issue_next = [&] {
+    if (issued < ntiles) issue_tile(static_cast<int64_t>(issued) * kPKV, issued % kPStages);
+    ++issued;
+  };
+  auto publish = [&](int u) {
+    const int after = min(issued, ntiles) - 1 - u;  // tiles issued after u (loads complete in order)
+    if (after >= 2) __builtin_amdgcn_s_waitcnt(((2 * T::kLoadsPerTile) & 0xF) | (((2 * T::kLoadsPerTile) >> 4) << 14) | 0x70 | 0xF00);
+    else if (after == 1) __builtin_amdgcn_s_waitcnt((T::kLoadsPerTile & 0xF) | ((T::kLoadsPerTile >> 4) << 14) | 0x70 | 0xF00);
     else __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + kPStages - 1 < ntiles) issue_tile(t0 + (kPStages - 1) * kPKV, static_cast<int>((it + kPStages - 1) % kPStages));
-    if (!(wave_live && t0 < wave_kv)) return false;
-    const uint32_t sb = smem_base + static_cast<uint32_t>(it % kPStages) * 2 * T::kTile;
-    uint32_t ka[D / 16];
-#pragma unroll
-    for (int kd = 0; kd < D / 16; ++kd) ka[kd] = sb + koff[kd];
-    static_for<2>([&](auto stc) {
-      constexpr int st = decltype(stc)::value;
-      if (t0 + 32 * st >= wave_kv) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[st][qb][r] = -INFINITY;
-      } else {
-        bf16x8 kf[D / 16];
-        static_for<D / 16>([&](auto kdc) {
-          constexpr int kd = decltype(kdc)::value;
-          uint4 raw;
-          pf_read_b128<st * 32 * T::kRowBytes>(raw, ka[kd]);
-          kf[kd] = as_bf16x8(raw);
-        });
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        // the fragments pass through empty asm after the wait, so no use is scheduled before it
-#pragma unroll
-        for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+v"(kf[kd]));
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) prefill_s_first(s[st][qb], kf[0], qf[qb][0]);
-#pragma unroll
-        for (int kd = 1; kd < D / 16; ++kd)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) prefill_s_next(s[st][qb], kf[kd], qf[qb][kd]);
-      }
+  };
+  static_assert(kPStages == 4, "the ring protocol below assumes four slots");
+  static_assert(2 * T::kLoadsPerTile < 64, "vmcnt range");
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+
+  // S^T of 32-token step n (tokens 32n .. 32n + 31) from the slot of its tile, raw (unscaled).
+  auto s_mfma = [&](int n, f32x16& sd) {
+    const uint32_t kb0 = smem_base + static_cast<uint32_t>((n >> 1) % kPStages) * 2 * T::kTile +
+                         static_cast<uint32_t>(n & 1) * 32 * T::kRowBytes;
+    bf16x8 kf[D / 16];
+    static_for<D / 16>([&](auto kdc) {
+      constexpr int kd = decltype(kdc)::value;
+      uint4 raw;
+      pf_read_b128<0>(raw, kb0 + koff[kd]);
+      kf[kd] = as_bf16x8(raw);
     });
-    prefill_s_wait(s);
-    float m[2];
-    if (t0 + kPKV > wave_clean) {  // a tile on the causal diagonal or past a sequence end: mask
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // the fragments pass through empty asm after the wait, so no use is scheduled before it
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        // the query's limit relative to the tile start, as a 32-bit value in [0, 64]
-        const int lim = static_cast<int>(imin64(kPKV, imax64(0, qend[qb] - t0)));
-        m[qb] = -INFINITY;
+    for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+v"(kf[kd]));
+    sd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], f32x16{}, 0, 0, 0);
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+    for (int kd = 1; kd < D / 16; ++kd) sd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kd], qf[kd], sd, 0, 0, 0);
+  };
+  // masked maximum (log2 domain) of step n's raw scores; masked scores become -inf (branch-free:
+  // the compares run in the shadow of MFMAs)
+  auto mask_max = [&](int n, f32x16& sd) -> float {
+    const int lim = static_cast<int>(imin64(32, imax64(0, qend - 32 * static_cast<int64_t>(n))));
+    float m = -INFINITY;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int t = 32 * st + 8 * (r >> 2) + 4 * grp + (r & 3);
-            const float v = t < lim ? s[st][qb][r] : -INFINITY;
-            s[st][qb][r] = v;
-            m[qb] = fmaxf(m[qb], v);
-          }
+    for (int r = 0; r < 16; ++r) {
+      const int t = 8 * (r >> 2) + 4 * grp + (r & 3);
+      sd[r] = t < lim ? sd[r] : -INFINITY;
+      m = fmaxf(m, sd[r]);
+    }
+    return fmaxf(m, __shfl_xor(m, 32, 64)) * a.scale_log2;
+  };
+  // P of a step (16 scores of this lane's query) into two bf16 B fragments; returns the row sum
+  auto softmax = [&](const f32x16& sc, bf16x8 (&pf)[2]) -> float {
+    const float neg_m = (m_run == -INFINITY) ? 0.0f : -m_run;
+    float rs[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * kb2 + j], a.scale_log2, neg_m));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * kb2 + j + 1], a.scale_log2, neg_m));
+        const bf16x2_t pk = __builtin_convertvector((f32x2_t){e0, e1}, bf16x2_t);
+        pf[kb2][j] = pk[0];
+        pf[kb2][j + 1] = pk[1];
+        rs[kb2] = __builtin_amdgcn_fdot2_f32_bf16(pk, ones, rs[kb2], false);
+      }
+    const float r = rs[0] + rs[1];
+    return r + __shfl_xor(r, 32, 64);
+  };
+  // V^T fragments of 16-token block kb (0..3) of the tile in slot `slot`
+  auto v_read = [&](int slot, auto kbc, v2i_t (&lo)[D / 32], v2i_t (&hi)[D / 32]) {
+    constexpr int kb = decltype(kbc)::value;
+    const uint32_t vb = smem_base + static_cast<uint32_t>(slot) * 2 * T::kTile;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      pf_read_tr16<kb * 16 * T::kRowBytes>(lo[dt], vb + voff[0][dt]);
+      pf_read_tr16<kb * 16 * T::kRowBytes>(hi[dt], vb + voff[1][dt]);
+    }
+  };
+  auto pv_mfma = [&](v2i_t (&lo)[D / 32], v2i_t (&hi)[D / 32], const bf16x8& p) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      const bf16x8 vv = __builtin_bit_cast(bf16x8, (v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]}));
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p, acc[dt], 0, 0, 0);
+    }
+  };
+
+  // One 64-token tile at a time. The fast pass (RESCALE = false) keeps the reference max of each
+  // query at the max of the first tile it sees: a wave whose tile max rises above it by more than
+  // kPfSlack (2^64 of headroom in P, l and O^T) puts the item on the rescaling pass's list and stops
+  // computing (it still takes its part in the ring); the rescaling pass redoes the whole item,
+  // raising the reference max (and rescaling O^T and l) whenever a tile's max exceeds it by more
+  // than kPfSlack. Keeping the rescale out of the fast pass keeps the O^T accumulators in place.
+  bool dead = false;
+  const int wave_steps = static_cast<int>(cdiv(wave_kv, 32));
+  for (int i = 0; i < kPStages - 1; ++i) issue_next();
+  for (int it = 0; it < ntiles; ++it) {
+    publish(it);
+    issue_next();
+    if (2 * it >= wave_steps || dead) continue;
+    const int slot = it % kPStages;
+    const bool second = 2 * it + 1 < wave_steps;
+    f32x16 s0, s1;
+    s_mfma(2 * it, s0);
+    float mx = mask_max(2 * it, s0);
+    if (second) {
+      s_mfma(2 * it + 1, s1);
+      mx = fmaxf(mx, mask_max(2 * it + 1, s1));
+    }
+    if constexpr (RESCALE) {
+      if (__any(mx > m_run + kPfSlack)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+        m_run = m_new;
       }
     } else {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        m[qb] = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) m[qb] = fmaxf(m[qb], s[st][qb][r]);
-      }
-    }
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) mx[qb] = fmaxf(m[qb], __shfl_xor(m[qb], 32, 64)) * a.scale_log2;
-    return true;
-  };
-  // Phase B: P = exp2(scale * S - m_run), l += rowsum(P), O^T += V^T P^T. With RESCALE the reference
-  // max is raised (and O^T, l rescaled) when a query's tile max exceeds it by more than kPfSlack;
-  // without, the caller has checked that no query needs that. Keeping the rescale out of the fast
-  // loop keeps the O^T accumulators in place (rescaling code in the loop makes the compiler move all
-  // of them through VGPRs on every tile). l sums the bf16-rounded P that the PV MFMAs use.
-  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-  auto phase_b = [&](int64_t it, auto rescale_tag) {
-    constexpr bool RAISE = decltype(rescale_tag)::value;
-    const int64_t t0 = it * kPKV;
-    const uint32_t sb = smem_base + static_cast<uint32_t>(it % kPStages) * 2 * T::kTile;
-    bf16x8 pf[2][4];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      if constexpr (RAISE) {
-        if (__any(mx[qb] > m_run[qb] + kPfSlack)) {
-          const float m_new = fmaxf(m_run[qb], mx[qb]);
-          const float alpha = (m_run[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-          l_run[qb] *= alpha;
-#pragma unroll
-          for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[qb][i][r] *= alpha;
-          m_run[qb] = m_new;
-        }
-      } else {
-        // a query that has seen nothing so far (m_run = -inf: O^T and l are zero) takes this tile's max
-        if (m_run[qb] == -INFINITY) m_run[qb] = mx[qb];
-      }
-      const float neg_m = (m_run[qb] == -INFINITY) ? 0.0f : -m_run[qb];
-      float rs[2] = {0.0f, 0.0f};
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][qb][8 * kb2 + j], a.scale_log2, neg_m));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][qb][8 * kb2 + j + 1], a.scale_log2, neg_m));
-            const bf16x2_t pk = __builtin_convertvector((f32x2_t){e0, e1}, bf16x2_t);
-            pf[qb][2 * st + kb2][j] = pk[0];
-            pf[qb][2 * st + kb2][j + 1] = pk[1];
-            rs[j >> 2 & 1] = __builtin_amdgcn_fdot2_f32_bf16(pk, ones, rs[j >> 2 & 1], false);
-          }
-      float r = rs[0] + rs[1];
-      r += __shfl_xor(r, 32, 64);
-      l_run[qb] += r;
-    }
-    // ---- O^T += V^T P^T; each V fragment feeds both query blocks
-    uint32_t va[2][D / 32];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) va[h][dt] = sb + voff[h][dt];
-    static_for<4>([&](auto kbc) {
-      constexpr int kb = decltype(kbc)::value;
-      if (t0 + 16 * kb < wave_kv) {
-        v2i_t lo[D / 32], hi[D / 32];
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          pf_read_tr16<kb * 16 * T::kRowBytes>(lo[dt], va[0][dt]);
-          pf_read_tr16<kb * 16 * T::kRowBytes>(hi[dt], va[1][dt]);
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const bf16x8 vv = __builtin_bit_cast(bf16x8, (v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]}));
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-            acc[qb][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, pf[qb][kb], acc[qb][dt], 0, 0, 0);
-        }
-      }
-    });
-  };
-  if constexpr (!RESCALE) {
-    // Fast pass: the reference max of each query is the max of the first tile it sees, and stays. A
-    // wave whose tile max rises above it by more than kPfSlack (2^64 of headroom in P, l and O^T)
-    // puts the item on the rescaling pass's list and stops computing (it still takes its part in the
-    // ring); the rescaling pass redoes the whole item.
-    bool dead = false;
-    for (int64_t it = 0; it < ntiles; ++it) {
-      if (!phase_a(it) || dead) continue;
-      bool rise = false;
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) rise |= m_run[qb] != -INFINITY && mx[qb] > m_run[qb] + kPfSlack;
-      if (__any(rise)) {
+      if (__any(m_run != -INFINITY && mx > m_run + kPfSlack)) {
         dead = true;
         if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
         continue;
       }
-      phase_b(it, std::false_type());
+      if (m_run == -INFINITY) m_run = mx;  // a query that has seen nothing so far: O^T and l are zero
     }
-    if (dead) return;
-  } else {
-    for (int64_t it = 0; it < ntiles; ++it)
-      if (phase_a(it)) phase_b(it, std::true_type());
+    bf16x8 pf[2];
+    v2i_t lo[D / 32], hi[D / 32];
+    l_run += softmax(s0, pf);
+    v_read(slot, std::integral_constant<int, 0>(), lo, hi);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pv_mfma(lo, hi, pf[0]);
+    v_read(slot, std::integral_constant<int, 1>(), lo, hi);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pv_mfma(lo, hi, pf[1]);
+    if (second) {
+      l_run += softmax(s1, pf);
+      v_read(slot, std::integral_constant<int, 2>(), lo, hi);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      pv_mfma(lo, hi, pf[0]);
+      v_read(slot, std::integral_constant<int, 3>(), lo, hi);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      pv_mfma(lo, hi, pf[1]);
+    }
   }
-  if (!unit_ok) return;
+  if (dead) return;
+  if (!unit_ok || myq >= a.s_q) return;
   // ---- write O (lane = query col, d = 32dt + 8(r/4) + 4grp + r%4) and lse
+  const bool live = wave_live && myq < Lq && l_run > 0.0f;
+  const float inv = live ? 1.0f / l_run : 0.0f;
+  uint16_t* op = a.out + b * a.os[0] + myq * a.os[1] + head * a.os[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int64_t myq = q0 + 32 * qb + col;
-    if (myq >= a.s_q) continue;
-    const bool live = wave_live && myq < Lq && l_run[qb] > 0.0f;
-    const float inv = live ? 1.0f / l_run[qb] : 0.0f;
-    uint16_t* op = a.out + b * a.os[0] + myq * a.os[1] + head * a.os[2];
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = 32 * dt + 8 * r4 + 4 * grp;
-        uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4] * inv)) |
-                      (static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 1] * inv)) << 16);
-        uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 2] * inv)) |
-                      (static_cast<uint32_t>(f32_to_bf16(acc[qb][dt][4 * r4 + 3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
-      }
-    if (a.lse && grp == 0)
-      a.lse[(b * a.hq + head) * a.s_q + myq] = live ? (m_run[qb] + log2f(l_run[qb])) * kLn2 : -INFINITY;
-  }
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d = 32 * dt + 8 * r4 + 4 * grp;
+      uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4] * inv)) |
+                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 1] * inv)) << 16);
+      uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 2] * inv)) |
+                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 3] * inv)) << 16);
+      *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
+    }
+  if (a.lse && grp == 0)
+    a.lse[(b * a.hq + head) * a.s_q + myq] = live ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
 }
 
 // ============================================================================ MLA absorbed decode
@@ -1647,7 +1592,7 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
 
 extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv) {
   if (b <= 0 || s_q <= 0 || hq <= 0 || hkv <= 0) return 256;
-  const int64_t n_items = b * hkv * cdiv(cdiv(s_q, kPQ) * (hq / hkv), 4);
+  const int64_t n_items = b * hkv * cdiv(cdiv(s_q, kPQ) * (hq / hkv), kPWaves);
   return static_cast<size_t>(256 + 8 * n_items + 256);
 }
 
@@ -1681,7 +1626,7 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.scale_log2 = fmaxf(fabsf(scale) * kLog2e, 1.17549435e-38f);
   a.n_qt = static_cast<int>(cdiv(s_q, kPQ));
   a.units_per_bk = a.n_qt * a.g;
-  a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, 4));
+  a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, kPWaves));
   // the three-stage ring needs more LDS than a workgroup gets by default (set once per process)
   static const bool lds_ok = [] {
     const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<64, false>),
@@ -1721,11 +1666,11 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   prefill_queue_reset<<<static_cast<unsigned>(std::min<int64_t>(64, cdiv(a.n_items, 256))), 256, 0, st>>>(a.queue, a.flags, a.n_items);
   const dim3 grid(static_cast<unsigned>(std::min<int64_t>(n_cu, a.n_items)));
   if (d == 64) {
-    prefill_kernel<64, false><<<grid, 256, PrefillTile<64>::kLds, st>>>(a);
-    prefill_kernel<64, true><<<grid, 256, PrefillTile<64>::kLds, st>>>(a);
+    prefill_kernel<64, false><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
+    prefill_kernel<64, true><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
   } else {
-    prefill_kernel<128, false><<<grid, 256, PrefillTile<128>::kLds, st>>>(a);
-    prefill_kernel<128, true><<<grid, 256, PrefillTile<128>::kLds, st>>>(a);
+    prefill_kernel<128, false><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
+    prefill_kernel<128, true><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
   }
   return launch_status("tai_fia_prefill");
 }
