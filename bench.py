@@ -15,6 +15,8 @@ from __future__ import annotations
 
 import argparse
 import json
+
+import numpy as np
 import os
 import sys
 import time
@@ -242,19 +244,58 @@ def bench_gemm(torch, dev, iters=20):
         ms = e0.elapsed_time(e1) / iters
         tops = 2 * n ** 3 / (ms * 1e-3) / 1e12
         res[name] = {"ms": round(ms, 4), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        # the vendor library on the same operands (torch._int_mm -> hipBLASLt), as the reachable-rate reference
+        try:
+            for _ in range(3):
+                torch._int_mm(a, bb)
+            e0, e1 = _events(torch)
+            e0.record()
+            for _ in range(iters):
+                torch._int_mm(a, bb)
+            e1.record()
+            torch.cuda.synchronize()
+            ms_v = e0.elapsed_time(e1) / iters
+            res[name]["hipblaslt_TOPS"] = round(2 * n ** 3 / (ms_v * 1e-3) / 1e12, 1)
+        except RuntimeError as e:  # pragma: no cover
+            res[name]["hipblaslt_TOPS"] = f"unavailable: {str(e)[:80]}"
     return res
 
 
 # ----------------------------------------------------------------------------- config-1 MLP
-def bench_mlp(torch, dev, iters=50):
-    g = torch.Generator(device=dev)
-    g.manual_seed(2)
+def _cpu_gen(torch, seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _cpu_time(fn, warmup=1, runs=3):
+    """Median wall time (s) of `runs` calls after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        return os.cpu_count()
+
+
+def bench_mlp(torch, dev, iters=50, cpu=False):
+    g = _cpu_gen(torch, 1)
     T, H, I = 128, 2048, 5632
-    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
-    wgu = torch.randint(-127, 128, (H, 2 * I), generator=g, device=dev, dtype=torch.int8)
-    sgu = torch.rand(2 * I, generator=g, device=dev) * 9e-3 + 1e-3
-    wd = torch.randint(-127, 128, (I, H), generator=g, device=dev, dtype=torch.int8)
-    sd = torch.rand(H, generator=g, device=dev) * 9e-3 + 1e-3
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    wgu = torch.randint(-127, 128, (H, 2 * I), generator=g, dtype=torch.int8).to(dev)
+    sgu = (torch.rand(2 * I, generator=g) * 9e-3 + 1e-3).to(dev)
+    wd = torch.randint(-127, 128, (I, H), generator=g, dtype=torch.int8).to(dev)
+    sd = (torch.rand(H, generator=g) * 9e-3 + 1e-3).to(dev)
     one = torch.ones(1, device=dev)
     npu = torch.ops.npu
 
@@ -283,30 +324,43 @@ def bench_mlp(torch, dev, iters=50):
     algo = T * H * 2 + H * 2 * I + T * 2 * I * 4 * 2 + I * H + T * I + T * H * 2
     out["algorithmic_MB"] = round(algo / 1e6, 2)
     out["hbm_frac_hipgraph"] = round(algo / (out["hipgraph_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    if cpu:
+        from oracle import golden as G
+        xs, wg, sg, wdn, sdn = (x.float().cpu().numpy(), wgu.cpu().numpy(), sgu.cpu().numpy(), wd.cpu().numpy(),
+                                sd.cpu().numpy())
+
+        def mlp_cpu():
+            q, s = G.dynamic_quant(xs)
+            h = G.quant_matmul(q, wg, out_dtype="int32")
+            q2, s2 = G.dequant_swiglu_quant(h, sg, s, activate_left=True)
+            return G.quant_matmul(q2, wdn, sdn, s2, None, "bf16")
+        t = _cpu_time(mlp_cpu)
+        out["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us per MLP call", "cores": _cpu_threads(),
+                               "kind": "port", "sample": "numpy oracle, the whole config-1 MLP on the same inputs; "
+                                                         "1 warm-up, median of 3"}
     return out
 
 
 # ----------------------------------------------------------------------------- paged decode (config 2)
-def make_decode_case(torch, dev, seed=3, B=64, HQ=32, HKV=8, D=128, BS=128):
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
-    lens = torch.randint(512, 4097, (B,), generator=g, device=dev)
+def make_decode_case(torch, dev, seed=2, B=64, HQ=32, HKV=8, D=128, BS=128):
+    g = _cpu_gen(torch, seed)
+    lens = torch.randint(512, 4097, (B,), generator=g)
     nb = ((lens + BS - 1) // BS)
     total = int(nb.sum())
     width = int(nb.max())
-    perm = torch.randperm(total, generator=g, device=dev).to(torch.int32)
-    bt = torch.zeros(B, width, dtype=torch.int32, device=dev)
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    bt = torch.zeros(B, width, dtype=torch.int32)
     off = 0
     for b, n in enumerate(nb.tolist()):
         bt[b, :n] = perm[off:off + n]
         off += n
-    kc = torch.randn(total, BS, HKV * D, generator=g, device=dev).to(torch.bfloat16)
-    vc = torch.randn(total, BS, HKV * D, generator=g, device=dev).to(torch.bfloat16)
-    q = torch.randn(B, 1, HQ * D, generator=g, device=dev).to(torch.bfloat16)
-    return q, kc, vc, bt, lens
+    kc = torch.randn(total, BS, HKV * D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(total, BS, HKV * D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, 1, HQ * D, generator=g).to(torch.bfloat16)
+    return q.to(dev), kc.to(dev), vc.to(dev), bt.to(dev), lens.to(dev)
 
 
-def bench_decode(torch, dev, iters=50):
+def bench_decode(torch, dev, iters=50, cpu=False):
     q, kc, vc, bt, lens = make_decode_case(torch, dev)
     B, HQ, HKV, D, BS = 64, 32, 8, 128, 128
 
@@ -330,18 +384,39 @@ def bench_decode(torch, dev, iters=50):
     ms = e0.elapsed_time(e1) / iters
     kv_bytes = int(lens.sum()) * HKV * D * 2 * 2 + 2 * B * HQ * D * 2 + bt.numel() * 4
     gbs = kv_bytes / (ms * 1e-3) / 1e9
-    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": kv_bytes}
+    res = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes": kv_bytes}
+    if cpu:
+        from oracle import golden as G
+        ns = 8  # sequences 0..7 of the batch
+        ls = lens[:ns].cpu().numpy()
+        btc = bt[:ns].cpu().numpy()
+        used = sorted(set(btc[i, j] for i in range(ns) for j in range((int(ls[i]) + BS - 1) // BS)))
+        remap = {blk: i for i, blk in enumerate(used)}
+        idx = torch.tensor(used, device=kc.device, dtype=torch.long)
+        kcs = kc.index_select(0, idx).float().cpu().numpy().reshape(len(used), BS, HKV, D)
+        vcs = vc.index_select(0, idx).float().cpu().numpy().reshape(len(used), BS, HKV, D)
+        btl = btc.copy()
+        for i in range(ns):
+            for j in range((int(ls[i]) + BS - 1) // BS):
+                btl[i, j] = remap[btc[i, j]]
+        qs = q[:ns].float().cpu().numpy().reshape(ns, HQ, D)
+        t = _cpu_time(lambda: G.paged_decode_attention(qs, kcs, vcs, btl, ls, 1.0 / D ** 0.5))
+        frac = float(ls.sum()) / float(lens.sum())
+        res["cpu_baseline"] = {"value": round(kv_bytes * frac / t / 1e9, 3), "unit": "GB/s", "cores": _cpu_threads(),
+                               "kind": "port", "sample": f"numpy oracle on sequences 0-{ns - 1} of the batch "
+                                                         f"({frac:.1%} of the KV tokens); 1 warm-up, median of 3",
+                               "ms_whole_batch_est": round(t / frac * 1e3, 1)}
+    return res
 
 
 # ----------------------------------------------------------------------------- causal prefill (config 3)
-def bench_prefill(torch, dev, iters=10):
-    g = torch.Generator(device=dev)
-    g.manual_seed(4)
+def bench_prefill(torch, dev, iters=10, cpu=False):
+    g = _cpu_gen(torch, 3)
     B, S, HQ, HKV, D = 4, 4096, 32, 8, 128
-    q = torch.randn(B, S, HQ * D, generator=g, device=dev).to(torch.bfloat16)
-    k = torch.randn(B, S, HKV * D, generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn(B, S, HKV * D, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, S, HQ * D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(B, S, HKV * D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, S, HKV * D, generator=g).to(torch.bfloat16).to(dev)
     lens = torch.tensor([4096, 3072, 2048, 1024], device=dev)
 
     def run():
@@ -360,29 +435,43 @@ def bench_prefill(torch, dev, iters=10):
     ms = e0.elapsed_time(e1) / iters
     flops = sum(8192 * L * (L + 1) for L in (4096, 3072, 2048, 1024))
     tf = flops / (ms * 1e-3) / 1e12
-    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-            "algorithmic_flops": flops}
+    res = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+           "algorithmic_flops": flops}
+    if cpu:
+        from oracle import golden as G
+        L = 1024  # batch 3 (the 1024-token sequence), all heads
+        qs = q[3:4, :L].float().cpu().numpy().reshape(1, L, HQ, D)
+        ks = k[3:4, :L].float().cpu().numpy().reshape(1, L, HKV, D)
+        vs = v[3:4, :L].float().cpu().numpy().reshape(1, L, HKV, D)
+        ln = np.array([L])
+        t = _cpu_time(lambda: G.prefill_attention(qs, ks, vs, ln, ln, 1, 1.0 / D ** 0.5), warmup=0, runs=1)
+        sflops = 8192 * L * (L + 1)
+        res["cpu_baseline"] = {"value": round(sflops / t / 1e12, 4), "unit": "TFLOP/s", "cores": _cpu_threads(),
+                               "kind": "port", "sample": f"numpy oracle on sequence 3 (L = {L}, "
+                                                         f"{sflops / flops:.1%} of the causal flops); 1 timed run",
+                               "ms_whole_batch_est": round(t * flops / sflops * 1e3, 1)}
+    return res
 
 
 # ----------------------------------------------------------------------------- MLA decode (config 5)
-def bench_mla(torch, dev, iters=20):
-    g = torch.Generator(device=dev)
-    g.manual_seed(5)
+def bench_mla(torch, dev, iters=20, cpu=False):
+    g = _cpu_gen(torch, 4)
     B, H, DN, DR, BS = 128, 128, 512, 64, 128
-    lens = torch.randint(2048, 8193, (B,), generator=g, device=dev)
+    lens = torch.randint(2048, 8193, (B,), generator=g)
     nb = (lens + BS - 1) // BS
     total = int(nb.sum())
-    perm = torch.randperm(total, generator=g, device=dev).to(torch.int32)
-    bt = torch.zeros(B, int(nb.max()), dtype=torch.int32, device=dev)
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    bt = torch.zeros(B, int(nb.max()), dtype=torch.int32)
     off = 0
     for b, n in enumerate(nb.tolist()):
         bt[b, :n] = perm[off:off + n]
         off += n
-    qn = torch.randn(B, 1, H, DN, generator=g, device=dev).to(torch.bfloat16)
-    qr = torch.randn(B, 1, H, DR, generator=g, device=dev).to(torch.bfloat16)
-    ckv = torch.randint(-127, 128, (total, BS, 1, DN), generator=g, device=dev, dtype=torch.int8)
-    cs = torch.rand(total, BS, generator=g, device=dev) * 9e-3 + 1e-3
-    kr = torch.randn(total, BS, 1, DR, generator=g, device=dev).to(torch.bfloat16)
+    qn = torch.randn(B, 1, H, DN, generator=g).to(torch.bfloat16).to(dev)
+    qr = torch.randn(B, 1, H, DR, generator=g).to(torch.bfloat16).to(dev)
+    ckv = torch.randint(-127, 128, (total, BS, 1, DN), generator=g, dtype=torch.int8).to(dev)
+    cs = (torch.rand(total, BS, generator=g) * 9e-3 + 1e-3).to(dev)
+    kr = torch.randn(total, BS, 1, DR, generator=g).to(torch.bfloat16).to(dev)
+    lens, bt = lens.to(dev), bt.to(dev)
 
     def run():
         return torch.ops.air.npu_fused_infer_attention_score(
@@ -404,55 +493,116 @@ def bench_mla(torch, dev, iters=20):
     byts = ltot * (DN + 2 * DR + 4) + B * H * (DN + DR) * 2 + B * H * DN * 2
     tf = flops / (ms * 1e-3) / 1e12
     gbs = byts / (ms * 1e-3) / 1e9
-    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-            "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    res = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+           "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    if cpu:
+        from oracle import golden as G
+        ns = 2  # sequences 0 and 1 of the batch
+        ls = lens[:ns].cpu().numpy()
+        btc = bt[:ns].cpu().numpy()
+        used = sorted(set(int(btc[i, j]) for i in range(ns) for j in range((int(ls[i]) + BS - 1) // BS)))
+        remap = {blk: i for i, blk in enumerate(used)}
+        idx = torch.tensor(used, device=ckv.device, dtype=torch.long)
+        ck = ckv.index_select(0, idx)[:, :, 0].cpu().numpy()
+        csc = cs.index_select(0, idx).cpu().numpy()
+        krs = kr.index_select(0, idx)[:, :, 0].float().cpu().numpy()
+        btl = btc.copy()
+        for i in range(ns):
+            for j in range((int(ls[i]) + BS - 1) // BS):
+                btl[i, j] = remap[int(btc[i, j])]
+        qns, qrs = qn[:ns, 0].float().cpu().numpy(), qr[:ns, 0].float().cpu().numpy()
+        t = _cpu_time(lambda: G.mla_decode_attention(qns, qrs, ck, csc, krs, btl, ls, 1.0 / 192 ** 0.5), warmup=0,
+                      runs=1)
+        frac = float(ls.sum()) / ltot
+        res["cpu_baseline"] = {"value": round(flops * frac / t / 1e12, 4), "unit": "TFLOP/s", "cores": _cpu_threads(),
+                               "kind": "port", "sample": f"numpy oracle on sequences 0-{ns - 1} ({frac:.1%} of the "
+                                                         f"latent tokens); 1 timed run",
+                               "ms_whole_batch_est": round(t / frac * 1e3, 1)}
+    return res
 
 
 # ----------------------------------------------------------------------------- CPU baseline (oracle)
-def cpu_baseline(sample_experts=4):
-    """Oracle MoE layer on the host: full gating/routing/quant for all T tokens plus the expert
-    GEMMs of `sample_experts` of the 256 experts, scaled to the whole layer."""
-    import numpy as np
-    from oracle import golden as G
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count()
-    L = MoeLayer
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((L.T, L.H), dtype=np.float32)
-    x = G.round_bf16(x)
-    logits = rng.standard_normal((L.T, L.E), dtype=np.float32)
-    bias = (rng.standard_normal(L.E) * 0.1).astype(np.float32)
+def cpu_baseline(layer, sample_experts=8):
+    """The MoE layer on the host through the CPU debug path: the oracle registered as the npu ops' CPU
+    kernels, gating -> init_routing -> dynamic_quant and finalize compiled with
+    torch.compile(backend=get_npu_backend()), on the very inputs of the GPU run (copied back from HBM).
+    All 4096 tokens are routed, quantised and finalized (one timed run after a warm-up compile run).
+    The expert chain (gate_up int32 -> dequant_swiglu_quant -> down bf16) runs for a sample of
+    experts spread over the row-count distribution (smallest, largest and evenly spaced ranks), each
+    timed once after one untimed call; a least-squares fit time = a + b * rows over the sample gives
+    every live expert's time."""
+    import torch
+    from oracle import cpu_ops
+    from torchair_amd import get_npu_backend
+    cpu_ops.register()
+    torch.set_num_threads(os.cpu_count())
+    npu = torch.ops.npu
+    L = layer
+    x, logits, bias = L.x.cpu(), L.logits.cpu(), L.bias.cpu()
+
+    def route(x, logits, bias):
+        y, idx, _ = npu.npu_moe_gating_top_k(logits, L.K, bias=bias, k_group=4, group_count=8, group_select_mode=1,
+                                             renorm=0, norm_type=1, routed_scaling_factor=1.0, eps=1e-20)
+        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(x, idx, active_num=L.T * L.K, expert_num=L.E,
+                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                        row_idx_type=0)
+        q, s = npu.npu_dynamic_quant(ex)
+        return y, idx, ri, counts, q, s
+
+    def fin(out, y, ri, idx):
+        return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
+
+    route_c = torch.compile(route, backend=get_npu_backend(), fullgraph=True)
+    fin_c = torch.compile(fin, backend=get_npu_backend(), fullgraph=True)
+    route_c(x, logits, bias)  # compile + warm-up
     t0 = time.perf_counter()
-    y, idx, _ = G.moe_gating_top_k(logits, L.K, bias, 4, 8, 1, 0, 1, False, 1.0, 1e-20)
-    ex, ri, counts, _ = G.moe_init_routing_v2(x, idx, None, L.T * L.K, 0, L.E, 1, 0)
-    q, s = G.dynamic_quant(ex)
+    y, idx, ri, counts, q, s = route_c(x, logits, bias)
     t_route = time.perf_counter() - t0
-    ends = np.cumsum(counts)
-    t1 = time.perf_counter()
-    outs = []
-    for e in range(sample_experts):
-        b0 = 0 if e == 0 else int(ends[e - 1])
-        b1 = int(ends[e])
-        w_gu = rng.integers(-127, 128, (L.H, 2 * L.I), dtype=np.int8)
-        w_d = rng.integers(-127, 128, (L.I, L.H), dtype=np.int8)
-        s_gu = rng.uniform(1e-3, 1e-2, 2 * L.I).astype(np.float32)
-        s_d = rng.uniform(1e-3, 1e-2, L.H).astype(np.float32)
-        acc = G.quant_matmul(q[b0:b1], w_gu, out_dtype="int32")
-        q2, s2 = G.dequant_swiglu_quant(acc, s_gu, s[b0:b1], activate_left=True)
-        outs.append(G.quant_matmul(q2, w_d, s_d, s2, None, "bf16"))
-    t_exp = time.perf_counter() - t1
-    t2 = time.perf_counter()
-    out = np.zeros((L.T * L.K, L.H), np.float32)
-    G.moe_finalize_routing(out, None, None, None, y, ri, idx, 2, "bf16")
-    t_fin = time.perf_counter() - t2
-    total = t_route + t_fin + t_exp * (L.E / sample_experts)
-    return {"value": round(L.T / total, 2), "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": f"numpy oracle: gating+routing+quant+finalize for all {L.T} tokens "
-                      f"({t_route + t_fin:.1f}s) + expert GEMMs of {sample_experts}/{L.E} experts "
-                      f"({t_exp:.1f}s) scaled x{L.E // sample_experts}"}
+    down = torch.zeros(L.T * L.K, L.H, dtype=torch.bfloat16)
+    fin_c(down, y, ri, idx)
+    t0 = time.perf_counter()
+    fin_c(down, y, ri, idx)
+    t_fin = time.perf_counter() - t0
+    cnt = counts.numpy()
+    ends = np.cumsum(cnt)
+    live = [e for e in range(L.E) if cnt[e] > 0]
+    order = sorted(live, key=lambda e: cnt[e])
+    picks = sorted({order[round(i * (len(order) - 1) / (sample_experts - 1))] for i in range(sample_experts)})
+    one = torch.ones(1)
+
+    def expert(e):
+        b0, b1 = int(ends[e] - cnt[e]), int(ends[e])
+        w_gu, w_d = L.w_gu[e].cpu(), L.w_d[e].cpu()
+        s_gu, s_d = L.s_gu[e].cpu(), L.s_d[e].cpu()
+
+        def run():
+            acc = npu.npu_quant_matmul(q[b0:b1], w_gu, one, output_dtype=torch.int32)
+            q2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=s_gu, activation_scale=s[b0:b1], quant_mode=1,
+                                                  activate_left=True)
+            return npu.npu_quant_matmul(q2, w_d, s_d, pertoken_scale=s2, output_dtype=torch.bfloat16)
+        return run
+
+    expert(picks[0])()  # warm-up
+    rows, secs = [], []
+    for e in picks:
+        run = expert(e)
+        t0 = time.perf_counter()
+        run()
+        secs.append(time.perf_counter() - t0)
+        rows.append(int(cnt[e]))
+    if len(set(rows)) >= 2:
+        b_fit, a_fit = np.polyfit(np.array(rows, np.float64), np.array(secs), 1)
+    else:
+        a_fit, b_fit = float(np.mean(secs)), 0.0
+    t_exp = float(sum(a_fit + b_fit * cnt[e] for e in live))
+    total = t_route + t_fin + t_exp
+    return {"value": round(L.T / total, 2), "unit": "tokens/s", "cores": _cpu_threads(), "kind": "port",
+            "sample": f"numpy oracle as the npu ops' CPU kernels under torch.compile(backend=get_npu_backend()), on "
+                      f"the GPU run's inputs: routing + quant ({t_route:.1f} s) and finalize ({t_fin:.1f} s) for all "
+                      f"{L.T} tokens, one timed run each after a warm-up; expert chains of {len(picks)} of "
+                      f"{len(live)} live experts (rows {min(rows)}-{max(rows)}, {sum(secs):.1f} s), each timed once "
+                      f"after a warm-up call, fitted as {a_fit * 1e3:.0f} ms + {b_fit * 1e3:.3f} ms/row and summed "
+                      f"over all live experts ({t_exp:.1f} s)"}
 
 
 # ----------------------------------------------------------------------------- counter calibration
@@ -503,24 +653,25 @@ def main():
     only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode", "prefill", "mla", "moe", "norm"}
     if "moe" in only:
         extra["moe_layer_variants"] = bench_moe_variants(torch, layer)
+    cpu_moe = None if args.skip_cpu else cpu_baseline(layer)
     del layer
     torch.cuda.empty_cache()
     if "norm" in only:
         extra["norm_cache_writers"] = bench_norm_cache(torch, dev)
+    cpu = not args.skip_cpu
     if "gemm" in only:
         extra["w8a8_gemm_8192"] = bench_gemm(torch, dev)
     if "mlp" in only:
-        extra["mlp_cfg1"] = bench_mlp(torch, dev)
+        extra["mlp_cfg1"] = bench_mlp(torch, dev, cpu=cpu)
     if "decode" in only:
-        extra["paged_decode_cfg2"] = bench_decode(torch, dev)
+        extra["paged_decode_cfg2"] = bench_decode(torch, dev, cpu=cpu)
     if "prefill" in only:
-        extra["causal_prefill_cfg3"] = bench_prefill(torch, dev)
+        extra["causal_prefill_cfg3"] = bench_prefill(torch, dev, cpu=cpu)
     if "mla" in only:
-        extra["mla_decode_cfg5"] = bench_mla(torch, dev)
+        extra["mla_decode_cfg5"] = bench_mla(torch, dev, cpu=cpu)
     if "copy" in only:
         extra["copy_1gib"] = bench_copy(torch, dev)
     torch.cuda.empty_cache()
-    cpu = None if args.skip_cpu else cpu_baseline()
     line = {
         "metric": METRIC, "value": round(MoeLayer.T / dt, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
@@ -529,7 +680,7 @@ def main():
         "config": {"workload": "DeepSeek-V3-shaped quantized MoE layer, T=4096 H=7168 E=256 top-8 I=2048 "
                                "(BASELINE config 4), all experts on one GPU", "global_batch": MoeLayer.T,
                    "seq_len": 1, "parallelism": "single GPU"},
-        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+        "roofline": roof, "cpu_baseline": cpu_moe, "extra": extra,
     }
     print(json.dumps(line))
 
