@@ -65,14 +65,14 @@ class Converter:
     def supported_cases(self, cases):
         for c in cases:
             if not isinstance(c, Support):
-                raise AssertionError("The testcase must be instance of Support")
+                raise AssertionError(f"declared cases must be Support objects, got {type(c).__name__}")
         self._supported_cases = cases
 
 
 def declare_supported(supported_cases: List[Support]):
     def add(converter):
         if not isinstance(converter, Converter):
-            raise AssertionError("The converter must be instance of Converter")
+            raise AssertionError("declare_supported decorates what register_fx_node_ge_converter returned")
         converter.supported_cases = supported_cases
         _DECLARED_SUPPORTED_CONVERTERS[converter._aten_op] = converter
         return converter

@@ -43,13 +43,30 @@ register_fx_node_ge_converter(npu_inference.npu_moe_gating_top_k.default)(
     _identity(npu_inference.npu_moe_gating_top_k.default))
 # .../custom/moe_init_routing.py:4-10
 declare_supported([
-    Support(torch.empty(3, 4), torch.empty(3, 2, dtype=torch.int32), torch.empty(3, 2, dtype=torch.int32),
-            active_num=3),
+    Support(torch.empty(3, 4), torch.tensor([[0, 3], [1, 4], [2, 5]], dtype=torch.int32),
+            torch.tensor([[1, 0], [2, 1], [0, 2]], dtype=torch.int32), active_num=3),
 ])(register_fx_node_ge_converter(npu.npu_moe_init_routing.default)(_identity(npu.npu_moe_init_routing.default)))
 # .../custom/npu_moe_init_routing_v2.py:41
 register_fx_node_ge_converter(npu.npu_moe_init_routing_v2.default)(_identity(npu.npu_moe_init_routing_v2.default))
-# .../custom/npu_moe_finalize_routing.py:4-21
-register_fx_node_ge_converter(npu.npu_moe_finalize_routing.default)(_identity(npu.npu_moe_finalize_routing.default))
+# .../custom/npu_moe_finalize_routing.py:4-21 (the declared cases: 12 tokens, k = 2, 3 experts, hidden 7)
+def _fin_cases():
+    rows = torch.arange(24, dtype=torch.int32)
+    experts = torch.tensor([[0, 1], [2, 0], [1, 1], [2, 2], [0, 2], [1, 0], [0, 0], [2, 1], [1, 2], [0, 1],
+                            [2, 0], [1, 2]], dtype=torch.int32)
+    f16, f32 = torch.float16, torch.float32
+    e = torch.empty
+    return [
+        Support(e(24, 7, dtype=f16), e(12, 7, dtype=f16), e(12, 7, dtype=f16), e(3, 7, dtype=f16), e(12, 2, dtype=f16),
+                rows, experts),
+        Support(e(24, 7, dtype=f16), e(12, 7, dtype=f16), None, e(3, 7, dtype=f16), e(12, 2, dtype=f16), rows, experts),
+        Support(e(24, 7, dtype=f32), e(12, 7, dtype=f32), None, e(3, 7, dtype=f32), e(12, 2, dtype=f32), rows, experts),
+        Support(e(24, 7, dtype=f32), None, None, e(3, 7, dtype=f32), e(12, 2, dtype=f32), rows, experts),
+        Support(e(24, 7, dtype=f32), None, None, None, e(12, 2, dtype=f32), rows, experts),
+    ]
+
+
+declare_supported(_fin_cases())(
+    register_fx_node_ge_converter(npu.npu_moe_finalize_routing.default)(_identity(npu.npu_moe_finalize_routing.default)))
 # .../custom/fused_infer_attention_score.py:4 and python/torchair/ops/_npu_fused_infer_attention_score.py:46-58
 register_fx_node_ge_converter(npu.npu_fused_infer_attention_score.default)(
     _identity(npu.npu_fused_infer_attention_score.default))
@@ -57,8 +74,15 @@ register_fx_node_ge_converter(air.npu_fused_infer_attention_score.default)(
     _identity(air.npu_fused_infer_attention_score.default))
 # .../custom/npu_add_rms_norm.py:4-13, npu_add_rms_norm_dynamic_quant.py:8-21
 register_fx_node_ge_converter(npu.npu_add_rms_norm.default)(_identity(npu.npu_add_rms_norm.default))
-register_fx_node_ge_converter(npu.npu_add_rms_norm_dynamic_quant.default)(
-    _identity(npu.npu_add_rms_norm_dynamic_quant.default))
+# .../custom/npu_add_rms_norm_dynamic_quant.py:4-7
+declare_supported([
+    Support(torch.empty(1, 2, 3, dtype=torch.float16), torch.empty(1, 2, 3, dtype=torch.float16),
+            torch.empty(3, dtype=torch.float16), output_mask=[True, True]),
+    Support(torch.empty(1, 2, 3, dtype=torch.float16), torch.empty(1, 2, 3, dtype=torch.float16),
+            torch.empty(3, dtype=torch.float16), smooth_scale1=torch.empty(3, dtype=torch.float16),
+            output_mask=[True, True]),
+])(register_fx_node_ge_converter(npu.npu_add_rms_norm_dynamic_quant.default)(
+    _identity(npu.npu_add_rms_norm_dynamic_quant.default)))
 # .../custom/npu_scatter_pa_kv_cache.py:44-74
 register_fx_node_ge_converter(npu.npu_scatter_pa_kv_cache_functional.default)(
     _identity(npu.npu_scatter_pa_kv_cache_functional.default))
