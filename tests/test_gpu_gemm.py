@@ -58,6 +58,39 @@ def test_quant_matmul_bias():
     assert_close(f32np(out), G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), None, bf.numpy(), "bf16"))
 
 
+# Skinny path (m <= 128, k % 64 == 0, n % 16 == 0): row fragments of 1, 2 and 4 x 32 rows, 32- and
+# 64-column slabs, K split over workgroups or not, slabs cut by the end of N, waves left without a stage.
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 11264), (31, 640, 4112), (33, 5632, 2048), (64, 64, 80),
+                                   (65, 128, 176), (100, 4096, 8192), (128, 192, 16), (128, 2048, 11264),
+                                   (5, 8192, 256), (64, 12288, 512)])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_quant_matmul_skinny_exact(m, k, n, layout):
+    g = gen(14)
+    x1 = rand_i8((m, k), g)
+    w = rand_i8((k, n), g)
+    x2 = w if layout == "kn" else w.t().contiguous().t()
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), x2.to(DEV), torch.ones(1, device=DEV),
+                                         output_dtype=torch.int32)
+    np.testing.assert_array_equal(out.cpu().numpy(), G.quant_matmul(x1.numpy(), w.numpy(), out_dtype="int32"))
+
+
+@pytest.mark.parametrize("m,k,n", [(7, 1024, 11264), (128, 5632, 2048), (64, 12288, 512)])
+@pytest.mark.parametrize("out_dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")])
+def test_quant_matmul_skinny_epilogue(m, k, n, out_dtype, name):
+    g = gen(15)
+    x1, w = rand_i8((m, k), g), rand_i8((k, n), g)
+    scale, pts = uniform((n,), g, 1e-3, 1e-2), uniform((m,), g, 1e-3, 1e-2)
+    bf = uniform((n,), g, -1, 1)
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), scale.to(DEV), pertoken_scale=pts.to(DEV),
+                                         bias=bf.to(DEV), output_dtype=out_dtype)
+    assert_close(f32np(out), G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), pts.numpy(), bf.numpy(), name))
+    bi = torch.randint(-5000, 5000, (n,), generator=g, dtype=torch.int32)
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), torch.ones(1, device=DEV), bias=bi.to(DEV),
+                                         output_dtype=torch.int32)
+    np.testing.assert_array_equal(out.cpu().numpy(), G.quant_matmul(x1.numpy(), w.numpy(), bias=bi.numpy(),
+                                                                     out_dtype="int32"))
+
+
 def test_quant_matmul_large_exact_vs_f64():
     """8192^3 demonstrator shape: exact against a float64 GPU product."""
     g = torch.Generator(device=DEV)

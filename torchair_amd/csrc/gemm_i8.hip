@@ -1112,6 +1112,292 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
   }
 }
 
+// ----------------------------------------------------------------------------- skinny kernel
+// Dense GEMMs with at most 128 rows (decode-sized MLPs) use each weight byte for at most 128 rows,
+// so they are bound by the weight stream. One workgroup of 4 waves (one per SIMD) owns a BN-column
+// slab of the output and a contiguous range of 64-byte K stages, which its waves take round-robin:
+// every wave streams its own weight and activation stages through a private 2-slot LDS ring
+// (global_load_lds, so no workgroup barrier in the loop; the activations are read by every slab and
+// come from L2). After the loop the four partial tiles are summed through LDS. With k_split > 1 each slab's K is also split over workgroups, whose raw int32
+// partials splitk_reduce_kernel sums (it also applies the epilogue).
+template <int MI, int BN>
+struct SkinnyShape {
+  static constexpr int kD = 2;                    // ring slots per wave (3 and 4 measured slower)
+  static constexpr int kSlotB = 64 * BN;          // bytes of one weight stage
+  static constexpr int kSlotA = MI * 32 * 64;     // bytes of one activation stage
+  static constexpr int kSlot = kSlotB + kSlotA;
+  static constexpr int kNB = kSlotB / 1024;       // 1 KB weight loads per stage
+  static constexpr int kNL = kNB + 2 * MI;        // vector memory instructions per stage (weights + activations)
+  static constexpr int kRowWords = BN + 8;        // partial-sum row in LDS: rows r and r + 4 land 32 banks apart
+  static constexpr int kRing = 4 * kD * kSlot;
+  static constexpr int kRed = 4 * MI * 32 * kRowWords * 4;
+  static constexpr int kLds = kRing > kRed ? kRing : kRed;
+  static_assert(kNL * (kD - 1) < 64, "vmcnt holds 6 bits");
+  static_assert(BN == 32 || BN == 64, "slab width");
+  static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+template <int LAYOUT, int MI, int BN>
+__global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
+#pragma clang fp contract(off)
+  using Sh = SkinnyShape<MI, BN>;
+  constexpr int D = Sh::kD, NJ = BN / 32, NL = Sh::kNL;
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const int64_t L = xcd_remap(blockIdx.x, g.n_tiles * g.k_split);  // consecutive slabs share an XCD's L2
+  const int64_t slab = L / g.k_split, ks = L % g.k_split;
+  const int64_t n0 = slab * BN;
+  const int64_t nk = g.k / 64;
+  const int64_t kb = ks * g.k_per;
+  const int64_t ke = kb + g.k_per < nk ? kb + g.k_per : nk;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ns = kb + w < ke ? static_cast<int>((ke - kb - w + 3) / 4) : 0;  // stages kb + w + 4t of this wave
+  int8_t* ring = smem + w * D * Sh::kSlot;
+  const int m = static_cast<int>(g.m);
+
+  // weight source of load q relative to the stage's first K row, and the LDS placement: lane L of a
+  // load fills bytes 16L .. 16L + 15 of its 1 KB
+  //   [K, N] weights: slot = [64 k][BN B]; chunk c of k row r stored at c ^ 2((r >> 2) & 1) (BN = 64)
+  //   [N, K] weights: slot = [BN n][64 B]; chunk c of row r stored at c ^ ((r >> 2) & 3)
+  int64_t boff[Sh::kNB];
+#pragma unroll
+  for (int q = 0; q < Sh::kNB; ++q) {
+    if constexpr (LAYOUT == TAI_LAYOUT_KN) {
+      constexpr int CPR = BN / 16, RPL = 1024 / BN;
+      const int kr = RPL * q + lane / CPR;
+      const int c = (lane % CPR) ^ (BN == 64 ? ((kr >> 2) & 1) << 1 : 0);
+      int64_t nn = n0 + 16 * c;
+      nn = nn + 16 <= g.n ? nn : g.n - 16;
+      boff[q] = kr * g.n + nn;
+    } else {
+      const int r = 16 * q + lane / 4;
+      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      const int64_t nn = n0 + r < g.n ? n0 + r : g.n - 1;
+      boff[q] = nn * g.k + 16 * c;
+    }
+  }
+  auto stage_k = [&](int t) -> int64_t { return (kb + w + 4 * static_cast<int64_t>(t)) * 64; };
+  auto issue_b = [&](int t, int slot) {
+    const int64_t k0 = stage_k(t);
+    const int8_t* base = LAYOUT == TAI_LAYOUT_KN ? g.b + k0 * g.n : g.b + k0;
+#pragma unroll
+    for (int q = 0; q < Sh::kNB; ++q)
+      __builtin_amdgcn_global_load_lds((gbl_void*)(base + boff[q]), (lds_void*)(ring + slot * Sh::kSlot + q * 1024), 16,
+                                       0, 0);
+  };
+  // activation stage: [MI * 32 rows][64 B] after the weight stage, chunk c of row r stored at
+  // c ^ ((r >> 2) & 3); rows past m re-read row m - 1 (their sums are never stored). Loaded through LDS
+  // (16 rows of 64 contiguous bytes per instruction): loading the fragments straight into registers
+  // (32 rows of 32 bytes per instruction) made the config-1 gate_up 17.5 instead of 12 us.
+  const int8_t* asrc[2 * MI];
+#pragma unroll
+  for (int q = 0; q < 2 * MI; ++q) {
+    const int r = 16 * q + lane / 4;
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    asrc[q] = g.a + static_cast<int64_t>(r < m ? r : m - 1) * g.k + 16 * c;
+  }
+  auto issue_a = [&](int t, int slot) {
+    const int64_t k0 = stage_k(t);
+#pragma unroll
+    for (int q = 0; q < 2 * MI; ++q)
+      __builtin_amdgcn_global_load_lds((gbl_void*)(asrc[q] + k0),
+                                       (lds_void*)(ring + slot * Sh::kSlot + Sh::kSlotB + q * 1024), 16, 0, 0);
+  };
+  auto read_a = [&](int slot, int h, int i) -> v4i {
+    const int r = 32 * i + (lane & 31);
+    const int c = (2 * h + (lane >> 5)) ^ ((r >> 2) & 3);
+    return ds_read_b128(ring + slot * Sh::kSlot + Sh::kSlotB + r * 64 + 16 * c);
+  };
+  // weight fragment (K step h, column block j) of this lane from ring slot `slot`
+  const int l16 = lane & 15;
+  auto read_b = [&](int slot, int h, int j) -> v4i {
+    const int8_t* st = ring + slot * Sh::kSlot;
+    if constexpr (LAYOUT == TAI_LAYOUT_KN) {
+      const int col = 32 * j + ((lane >> 4) & 1) * 16 + (l16 & 1) * 8;
+      const int k_lo = 32 * h + (lane >> 5) * 16 + (l16 >> 1), k_hi = k_lo + 8;
+      auto swz = [](int k) { return BN == 64 ? ((k >> 2) & 1) << 1 : 0; };
+      return ds_read_tr8_pair(st + k_lo * BN + 16 * ((col >> 4) ^ swz(k_lo)) + (col & 15),
+                              st + k_hi * BN + 16 * ((col >> 4) ^ swz(k_hi)) + (col & 15));
+    } else {
+      const int r = 32 * j + (lane & 31);
+      const int c = (2 * h + (lane >> 5)) ^ ((r >> 2) & 3);
+      return ds_read_b128(st + r * 64 + 16 * c);
+    }
+  };
+
+  v16i acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  // Per stage: its weight loads, then its activation loads, all global -> LDS. Loads complete in
+  // issue order, so stage t has landed once only the D - 1 stages issued after it are outstanding.
+  // Every iteration issues one stage (past the wave's last stage it re-reads that stage and nothing
+  // consumes it), so the waits are the same constant in every iteration.
+  if (ns > 0) {
+    auto clamp = [&](int t) { return t < ns ? t : ns - 1; };
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      issue_b(clamp(d), d);
+      issue_a(clamp(d), d);
+    }
+    for (int t0 = 0; t0 < ns; t0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int t = t0 + d;
+        wait_vmcnt<(D - 1) * NL>();
+        v4i fb[2][NJ], fa[2][MI];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) fb[h][j] = read_b(d, h, j);
+#pragma unroll
+          for (int i = 0; i < MI; ++i) fa[h][i] = read_a(d, h, i);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the reads are asm the compiler takes as complete at issue: route their results through the
+        // wait so no use is scheduled above it
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(fb[h][j]));
+#pragma unroll
+          for (int i = 0; i < MI; ++i) asm volatile("" : "+v"(fa[h][i]));
+        }
+        issue_b(clamp(t + D), d);  // the slot's fragments are in registers: refill it
+        issue_a(clamp(t + D), d);
+        if (t < ns) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+              for (int j = 0; j < NJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[h][i], fb[h][j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    wait_vmcnt<0>();  // the trailing re-reads land before the ring is reused below
+  }
+
+  // Sum the four waves' partial tiles through LDS (the ring is free once every wave is past its loop).
+  __syncthreads();
+  int32_t* red = reinterpret_cast<int32_t*>(smem);
+  constexpr int kTileWords = MI * 32 * Sh::kRowWords;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        red[w * kTileWords + row * Sh::kRowWords + 32 * j + (lane & 31)] = acc[i][j][r];
+      }
+  __syncthreads();
+  const bool partial = g.k_split > 1;
+  const int32_t* bias_i = (g.bias && g.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(g.bias) : nullptr;
+  const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(g.bias) : nullptr;
+  constexpr int G4 = BN / 4;
+  for (int idx = threadIdx.x; idx < MI * 32 * G4; idx += 256) {
+    const int row = idx / G4, c4 = 4 * (idx % G4);
+    const int64_t col = n0 + c4;
+    if (row >= m || col >= g.n) continue;
+    int4 s = *reinterpret_cast<const int4*>(red + row * Sh::kRowWords + c4);
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const int4 v = *reinterpret_cast<const int4*>(red + q * kTileWords + row * Sh::kRowWords + c4);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    const int64_t o = static_cast<int64_t>(row) * g.n + col;
+    if (partial) {
+      *reinterpret_cast<int4*>(static_cast<int32_t*>(g.out) + ks * g.m * g.n + o) = s;
+      continue;
+    }
+    int32_t v[4] = {s.x, s.y, s.z, s.w};
+    if (bias_i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] += bias_i[col + q];
+    }
+    if (g.out_dt == TAI_DT_INT32) {
+      *reinterpret_cast<int4*>(static_cast<int32_t*>(g.out) + o) = make_int4(v[0], v[1], v[2], v[3]);
+      continue;
+    }
+    const float pt = g.pts ? g.pts[row] : 1.0f;
+    float f[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float sc = g.scale_len == 1 ? g.scale[0] : g.scale[col + q];
+      f[q] = (static_cast<float>(v[q]) * sc) * pt + (bias_f ? bias_f[col + q] : -0.0f);
+    }
+    if (g.out_dt == TAI_DT_FP32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(g.out) + o) = make_float4(f[0], f[1], f[2], f[3]);
+    } else {
+      uint16_t hv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hv[q] = g.out_dt == TAI_DT_BF16 ? f32_to_bf16(f[q]) : f32_to_f16(f[q]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.out) + o) =
+          make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
+    }
+  }
+}
+
+// Plan of the skinny kernel: 64-column slabs when there are enough of them to fill the chip, else
+// 32; K split over workgroups toward one workgroup per CU, keeping at least one stage per wave (on
+// the config-1 down projection the split plus its reduction takes 15 us, one workgroup per slab 21 us).
+struct SkinnyPlan {
+  int bn, mi;
+  int64_t slabs, split, per;
+};
+
+bool skinny_fit(int64_t m, int64_t k, int64_t n) {
+  return m >= 1 && m <= 128 && k >= 64 && k % 64 == 0 && n >= 16 && n % 16 == 0 && n < (1ll << 31);
+}
+
+SkinnyPlan skinny_fit_plan(int64_t m, int64_t k, int64_t n) {
+  SkinnyPlan p{};
+  p.mi = m <= 32 ? 1 : (m <= 64 ? 2 : 4);
+  p.bn = cdiv(n, 64) >= 128 ? 64 : 32;
+  p.slabs = cdiv(n, p.bn);
+  const int64_t nk = k / 64;
+  int64_t want = (256 + p.slabs / 2) / p.slabs;
+  const int64_t cap = nk / 4 > 1 ? nk / 4 : 1;
+  want = want < 1 ? 1 : (want > cap ? cap : want);
+  p.per = cdiv(nk, want);
+  p.split = cdiv(nk, p.per);
+  return p;
+}
+
+template <int LAYOUT, int MI, int BN>
+bool skinny_launch_one(const GemmArgs& g, hipStream_t st) {
+  using Sh = SkinnyShape<MI, BN>;
+  static const bool ready = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_skinny_kernel<LAYOUT, MI, BN>),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, Sh::kLds) == hipSuccess;
+  if (!ready) return false;
+  gemm_i8_skinny_kernel<LAYOUT, MI, BN>
+      <<<dim3(static_cast<unsigned>(g.n_tiles * g.k_split)), 256, Sh::kLds, st>>>(g);
+  return true;
+}
+
+template <int LAYOUT>
+bool skinny_launch_layout(const GemmArgs& g, const SkinnyPlan& p, hipStream_t st) {
+  if (p.bn == 64) {
+    if (p.mi == 1) return skinny_launch_one<LAYOUT, 1, 64>(g, st);
+    if (p.mi == 2) return skinny_launch_one<LAYOUT, 2, 64>(g, st);
+    return skinny_launch_one<LAYOUT, 4, 64>(g, st);
+  }
+  if (p.mi == 1) return skinny_launch_one<LAYOUT, 1, 32>(g, st);
+  if (p.mi == 2) return skinny_launch_one<LAYOUT, 2, 32>(g, st);
+  return skinny_launch_one<LAYOUT, 4, 32>(g, st);
+}
+
+bool skinny_launch(const GemmArgs& g, int layout, const SkinnyPlan& p, hipStream_t st) {
+  return layout == TAI_LAYOUT_NK ? skinny_launch_layout<TAI_LAYOUT_NK>(g, p, st)
+                                 : skinny_launch_layout<TAI_LAYOUT_KN>(g, p, st);
+}
+
 // Second half of npu_grouped_matmul_swiglu_quant_v2: one wave per row; the row's scale is
 // max|h| / 127 from the column tiles' partial maxima, y = clamp(rint(h / scale), -128, 127)
 // (npu_dynamic_quant arithmetic; a zero row gives scale 0 and y 0).
@@ -1145,7 +1431,12 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
 using namespace tai;
 
 extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n) {
-  if (m <= 0 || n <= 0 || !skinny_ok(m, k, n, TAI_LAYOUT_NK)) return 0;
+  if (m <= 0 || n <= 0) return 0;
+  if (skinny_fit(m, k, n)) {
+    const SkinnyPlan p = skinny_fit_plan(m, k, n);
+    return p.split > 1 ? static_cast<size_t>(p.split) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4 + 256 : 0;
+  }
+  if (!skinny_ok(m, k, n, TAI_LAYOUT_NK)) return 0;
   const SplitPlan p = skinny_plan(m, k, n);
   return p.split > 1 ? static_cast<size_t>(p.split) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4 + 256 : 0;
 }
@@ -1172,6 +1463,33 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (!fast_path_ok(g, x2_layout)) {
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, x2_layout, nullptr);
+    return launch_status("tai_quant_matmul");
+  }
+  if (skinny_fit(m, k, n)) {
+    const SkinnyPlan p = skinny_fit_plan(m, k, n);
+    g.n_tiles = p.slabs;
+    g.k_split = p.split;
+    g.k_per = p.per;
+    if (p.split == 1) {
+      if (!skinny_launch(g, x2_layout, p, st)) return launch_status("tai_quant_matmul (skinny LDS attribute)");
+      return launch_status("tai_quant_matmul");
+    }
+    const size_t need = tai_quant_matmul_workspace_size(m, k, n);
+    if (workspace == nullptr || ws_bytes < need) {
+      set_error("tai_quant_matmul: workspace of %zu bytes, need %zu", ws_bytes, need);
+      return TAI_ERR_WORKSPACE;
+    }
+    GemmArgs gp = g;  // partial pass: raw int32 slices into the workspace
+    gp.out = workspace;
+    if (!skinny_launch(gp, x2_layout, p, st)) return launch_status("tai_quant_matmul (skinny LDS attribute)");
+    const dim3 rgrid(static_cast<unsigned>(cdiv(m * n, 1024)));
+    const int32_t* part = static_cast<const int32_t*>(workspace);
+    switch (out_dtype) {
+      case TAI_DT_INT32: splitk_reduce_kernel<TAI_DT_INT32><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      case TAI_DT_BF16: splitk_reduce_kernel<TAI_DT_BF16><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      case TAI_DT_FP16: splitk_reduce_kernel<TAI_DT_FP16><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+      default: splitk_reduce_kernel<TAI_DT_FP32><<<rgrid, 256, 0, st>>>(part, p.split, g); break;
+    }
     return launch_status("tai_quant_matmul");
   }
   if (skinny_ok(m, k, n, x2_layout) && cfg_available<SkinnyCfg>()) {

@@ -161,7 +161,9 @@ int launch_dynamic_quant(const void* x, int64_t rows, int64_t cols, const float*
                        (reinterpret_cast<uintptr_t>(y) % 8) == 0 &&
                        (smooth == nullptr || (reinterpret_cast<uintptr_t>(smooth) % 16) == 0);
   const int64_t nvec = cols / kVec;
-  if (aligned && nvec <= 64 * 8) {
+  // Few rows (decode-sized batches) leave most CUs idle at one wave per row: give each row 256 threads.
+  const bool few_rows = rows <= 1024 && nvec > 64;
+  if (aligned && nvec <= 64 * 8 && !few_rows) {
     dim3 grid(static_cast<unsigned>(cdiv(rows, 4)));
     if (nvec <= 64 * 2)
       dynamic_quant_kernel<DT, 64, 2><<<grid, 256, 0, st>>>(x, rows, cols, smooth, gidx, gidx_dt, ng, y, scale);
@@ -222,10 +224,10 @@ __device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, i
   return found;
 }
 
-// One workgroup of 256 threads per row; each thread owns NV groups of 4 output columns.
-template <int NV>
-__global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
-  __shared__ float red[4];
+// One workgroup of TPB threads per row; each thread owns NV groups of 4 output columns.
+template <int NV, int TPB = 256>
+__global__ __launch_bounds__(TPB) void dsq_kernel(DsqArgs a) {
+  __shared__ float red[TPB / 64];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t n = a.n, n2 = 2 * a.n;
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
   int4 xa[NV], xb[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
     if (c < ng4) {
       xa[i] = *reinterpret_cast<const int4*>(xr + 4 * c);
       xb[i] = *reinterpret_cast<const int4*>(xr + n + 4 * c);
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
   int64_t g = 0;
   if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row);
   if (g < 0) {  // row beyond the grouped rows
-    for (int64_t c = tid; c < ng4; c += 256)
+    for (int64_t c = tid; c < ng4; c += TPB)
       *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = 0u;
     if (tid == 0) a.scale[row] = 0.0f;
     return;
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
     if (c < ng4) {
       const int64_t j = 4 * c;
       int ia[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w}, ib[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
@@ -290,11 +292,13 @@ __global__ __launch_bounds__(256) void dsq_kernel(DsqArgs a) {
   amax = wave_max(amax);
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  amax = red[0];
+#pragma unroll
+  for (int q = 1; q < TPB / 64; ++q) amax = fmaxf(amax, red[q]);
   const float scale = amax / 127.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * 256;
+    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
     if (c < ng4) {
       uint32_t w = 0;
 #pragma unroll
@@ -390,7 +394,11 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
   const bool aligned = n % 4 == 0 && al(x) && al(weight_scale) && al(bias) && (reinterpret_cast<uintptr_t>(y) % 4) == 0;
   const int64_t ng4 = n / 4;
   dim3 grid(static_cast<unsigned>(rows));
-  if (aligned && ng4 <= 256 * 2) dsq_kernel<2><<<grid, 256, 0, st>>>(a);
+  // Few rows (decode-sized batches): 1024 threads per row spread the SwiGLU arithmetic over more SIMDs.
+  if (aligned && rows <= 512 && ng4 > 512 && ng4 <= 1024 * 2) {
+    if (ng4 <= 1024) dsq_kernel<1, 1024><<<grid, 1024, 0, st>>>(a);
+    else dsq_kernel<2, 1024><<<grid, 1024, 0, st>>>(a);
+  } else if (aligned && ng4 <= 256 * 2) dsq_kernel<2><<<grid, 256, 0, st>>>(a);
   else if (aligned && ng4 <= 256 * 4) dsq_kernel<4><<<grid, 256, 0, st>>>(a);
   else if (aligned && ng4 <= 256 * 8) dsq_kernel<8><<<grid, 256, 0, st>>>(a);
   else dsq_generic_kernel<<<grid, 256, 0, st>>>(a);
