@@ -277,11 +277,22 @@ int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache
                          size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * npu_fused_infer_attention_score, dense prefill (GQA, optional causal mask).
- * q / k / v / out: bf16 with element (batch, pos, head, dim) at
- *   batch*sb + pos*ss + head*sh + dim (per-tensor strides, elements).
- * seq_lens_q / seq_lens_kv: NULL (full length) or [b] int64 on the device.
- * causal: 0 none, 1 = query i sees kv j <= i + (len_kv - len_q) (sparse_mode 2/3).
+ * npu_fused_infer_attention_score with query sequences (GQA prefill, chunked prefill over a paged
+ * cache, multi-token decode). Replaces ge.FusedInferAttentionScore for S_q > 1, emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/fused_infer_attention_score.py:4-109
+ *   (pre_tokens / next_tokens / sparse_mode / block_table: prototype experiment_ops.h:3878-3965).
+ * q / out: bf16 with element (batch, pos, head, dim) at batch*sb + pos*ss + head*sh + dim
+ *   (per-tensor strides, elements).
+ * k / v, dense (block_table NULL): like q. Paged (block_table [b, max_blocks] int32 on the device):
+ *   caches whose element (block, slot, kv_head, dim) sits at block*k_block_stride + slot*k_strides[1]
+ *   + kv_head*k_strides[2] + dim (v likewise); token t of sequence b is at block
+ *   block_table[b, t / block_size], slot t % block_size; block_size a multiple of 32; k_strides[0]
+ *   is not used.
+ * seq_lens_q / seq_lens_kv: NULL (full length) or [b] int64 on the device (required when paged).
+ * Mask: query i (of len_q) sees kv j (of len_kv) when -pre_tokens <= j - i - off <= next_tokens,
+ *   off = len_kv - len_q for mask_origin 1 (bottom-right: sparse_mode 3 causal is next_tokens 0,
+ *   sparse_mode 4 band) and 0 for mask_origin 0 (top-left: sparse_mode 2 causal, sparse_mode 0
+ *   band). pre / next of 2^31 - 1 or more are no bound. A query that sees nothing gets 0 and lse -inf.
  * Query rows at or past seq_lens_q[b] are written as zero.
  * lse: NULL or [b, hq, s_q] fp32.
  * ------------------------------------------------------------------------------------- */
@@ -289,8 +300,10 @@ int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int6
                     int64_t s_kv, int hq, int hkv, int d, const int64_t* q_strides,
                     const int64_t* k_strides, const int64_t* v_strides,
                     const int64_t* out_strides, const int64_t* seq_lens_q,
-                    const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
-                    void* workspace, size_t ws_bytes, void* stream);
+                    const int64_t* seq_lens_kv, int mask_origin, int64_t pre_tokens,
+                    int64_t next_tokens, const int32_t* block_table, int64_t max_blocks,
+                    int block_size, int64_t k_block_stride, int64_t v_block_stride, float scale,
+                    void* out, float* lse, void* workspace, size_t ws_bytes, void* stream);
 /* Bytes of the prefill workspace: work-queue counters and the rescaling pass's item list, which the
  * call clears itself. */
 size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv);

@@ -412,11 +412,31 @@ def paged_decode_attention(q, k_cache, v_cache, block_table, seq_lens, scale: fl
     return out, lse
 
 
-def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float):
+def band_mask(lq: int, lk: int, origin: int, pre: int, nxt: int) -> np.ndarray:
+    """Visibility of kv j (of lk) to query i (of lq): -pre <= j - i - off <= nxt, with off = lk - lq for
+    origin 1 (bottom-right) and 0 for origin 0 (top-left); pre / nxt >= 2**31 - 1 are no bound.
+
+    The sparse_mode / pre_tokens / next_tokens attributes of FusedInferAttentionScore (prototype
+    experiment_ops.h:3878-3965; converter .../custom/fused_infer_attention_score.py:36-40, 105-106):
+    mode 2 = (0, inf, 0), mode 3 = (1, inf, 0), mode 0 = (0, pre, next), mode 4 = (1, pre, next).
+    """
+    big = 2147483647
+    off = (lk - lq) if origin == 1 else 0
+    rel = np.arange(lk)[None, :] - np.arange(lq)[:, None] - off
+    ok = np.ones((lq, lk), bool)
+    if pre < big:
+        ok &= rel >= -pre
+    if nxt < big:
+        ok &= rel <= nxt
+    return ok
+
+
+def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None):
     """npu_fused_infer_attention_score, dense prefill. q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D].
 
     causal 1 (sparse_mode 3, right-down): query i sees kv j <= i + (Lkv - Lq); causal 2
-    (sparse_mode 2, left-up): j <= i; 0: no mask. Rows at or past Lq are zero.
+    (sparse_mode 2, left-up): j <= i; 0: no mask. band = (origin, pre, next) replaces causal with
+    band_mask's rule. Rows at or past Lq are zero.
     Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
     """
     q = np.asarray(q, F32)
@@ -431,7 +451,9 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float):
         ii = np.arange(lq)[:, None]
         jj = np.arange(lk)[None, :]
         mask = None
-        if causal == 1:
+        if band is not None:
+            mask = band_mask(lq, lk, *band)
+        elif causal == 1:
             mask = jj <= ii + (lk - lq)
         elif causal == 2:
             mask = jj <= ii
@@ -441,6 +463,25 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float):
             out[b, :lq, h] = o
             lse[b, h, :lq] = l
     return out, lse
+
+
+def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float):
+    """npu_fused_infer_attention_score with a block table and several query tokens per sequence
+    (chunked prefill / multi-token decode). q [B,Sq,Hq,D]; caches [blocks, bs, Hkv, D]; token t of
+    sequence b at cache[block_table[b, t // bs], t % bs] (the paged rule of paged_decode_attention);
+    band = (origin, pre, next) as in band_mask. Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
+    """
+    b_cnt = q.shape[0]
+    bs, hkv, d = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    lmax = max(int(x) for x in seq_kv) if b_cnt else 0
+    k = np.zeros((b_cnt, lmax, hkv, d), F32)
+    v = np.zeros((b_cnt, lmax, hkv, d), F32)
+    for b in range(b_cnt):
+        L = int(seq_kv[b])
+        pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
+        k[b, :L] = np.asarray(k_cache[pages], F32).reshape(-1, hkv, d)[:L]
+        v[b, :L] = np.asarray(v_cache[pages], F32).reshape(-1, hkv, d)[:L]
+    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band)
 
 
 def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_lens, scale: float):

@@ -99,7 +99,7 @@ def _prefill_ref_torch(q, k, v, lq, lkv, causal, scale):
     return out
 
 
-def _prefill(q, k, v, lq, lkv, hq, hkv, layout, sparse_mode, lse=False):
+def _prefill(q, k, v, lq, lkv, hq, hkv, layout, sparse_mode, lse=False, **mask_kw):
     b, s = q.shape[0], q.shape[1]
     d = q.shape[3]
     if layout == "BSH":
@@ -111,7 +111,7 @@ def _prefill(q, k, v, lq, lkv, hq, hkv, layout, sparse_mode, lse=False):
     out, l = torch.ops.air.npu_fused_infer_attention_score(
         qa, ka, va, actual_seq_lengths=lq.to(DEV), actual_seq_lengths_kv=lkv.to(DEV), num_heads=hq,
         num_key_value_heads=hkv, input_layout=layout, scale=1.0 / math.sqrt(d), sparse_mode=sparse_mode,
-        softmax_lse_flag=lse)
+        softmax_lse_flag=lse, **mask_kw)
     if layout == "BSH":
         out = out.reshape(b, s, hq, d)
     elif layout == "BNSD":
@@ -257,3 +257,108 @@ def test_prefill_rising_logits_take_the_rescaling_loop(d):
         fin = np.isfinite(wl)
         np.testing.assert_array_equal(np.isfinite(got), fin)
         np.testing.assert_allclose(got[fin], wl[fin], rtol=1e-3, atol=1e-3)
+
+
+def _assert_lse(got, wl):
+    """lse: -inf exactly where the oracle's is, elsewhere the fp32-output bar (rtol = atol = 1e-2). The
+    kernel's row sums add the bf16-rounded P that also feeds P V, so a row of a few visible tokens can
+    differ by ~2^-9 relative per term."""
+    fin = np.isfinite(wl)
+    np.testing.assert_array_equal(np.isfinite(got), fin)
+    np.testing.assert_allclose(got[fin], wl[fin], rtol=1e-2, atol=1e-2)
+
+
+# Band masks (sparse_mode 0: pre/next tokens from the top-left; 4: from the bottom-right), including a
+# band that leaves the first queries nothing (next_tokens < 0) and one narrower than a 32-token step.
+@pytest.mark.parametrize("sparse_mode,pre,nxt", [(0, 50, 7), (0, 2147483647, -10), (0, 5, 0), (4, 20, 0),
+                                                 (4, 100, 30), (4, 0, 0)])
+def test_prefill_band_masks(sparse_mode, pre, nxt):
+    gen = torch.Generator().manual_seed(113)
+    b, s, hq, hkv, d = 2, 230, 8, 2, 128
+    q = torch.randn(b, s, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    lq, lkv = torch.tensor([230, 101]), torch.tensor([230, 199])
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lq, lkv, hq, hkv, "BSND", sparse_mode, lse=True,
+                        pre_tokens=pre, next_tokens=nxt)
+    band = (1 if sparse_mode == 4 else 0, pre, nxt)
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lq.numpy(), lkv.numpy(), 0, 1.0 / math.sqrt(d),
+                                   band=band)
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)
+
+
+def _paged_seq_case(lq, lkv, hq, hkv, d, bs, seed):
+    g = torch.Generator().manual_seed(seed)
+    b = len(lkv)
+    nb = [(L + bs - 1) // bs for L in lkv]
+    total = sum(nb) + 3
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(b, max(nb), dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    k4 = torch.randn(total, bs, hkv, d, generator=g).to(torch.bfloat16)
+    v4 = torch.randn(total, bs, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b, max(lq), hq, d, generator=g).to(torch.bfloat16)
+    return q, k4, v4, bt
+
+
+def _paged_seq(q, k4, v4, bt, lq, lkv, hq, hkv, bs, q_layout, cache_layout, **mask_kw):
+    b, s, _, d = q.shape
+    if cache_layout == "BSH":
+        kc = k4.reshape(k4.shape[0], bs, hkv * d).to(DEV)
+        vc = v4.reshape(v4.shape[0], bs, hkv * d).to(DEV)
+    else:  # [blocks, Hkv, bs, D]
+        kc = k4.permute(0, 2, 1, 3).contiguous().to(DEV)
+        vc = v4.permute(0, 2, 1, 3).contiguous().to(DEV)
+    if q_layout == "BSH":
+        qa = q.reshape(b, s, hq * d)
+    elif q_layout == "BNSD":
+        qa = q.transpose(1, 2)
+    else:
+        qa = q
+    out, l = torch.ops.air.npu_fused_infer_attention_score(
+        qa.to(DEV), kc, vc, block_table=bt.to(DEV), actual_seq_lengths=torch.tensor(lq, device=DEV),
+        actual_seq_lengths_kv=torch.tensor(lkv, device=DEV), num_heads=hq, num_key_value_heads=hkv,
+        input_layout=q_layout, block_size=bs, scale=1.0 / math.sqrt(d), softmax_lse_flag=True, **mask_kw)
+    if q_layout == "BSH":
+        out = out.reshape(b, s, hq, d)
+    elif q_layout == "BNSD":
+        out = out.transpose(1, 2)
+    return out, l
+
+
+# Chunked prefill over a paged cache: each sequence's new query tokens are the last len_q of its len_kv
+# tokens (bottom-right causal, sparse_mode 3); block sizes 32 / 64 / 128 / 96 (a 64-token tile across
+# two blocks), both cache layouts, the three query layouts.
+@pytest.mark.parametrize("bs,cache_layout,q_layout", [(128, "BSH", "BSH"), (64, "BNSD", "BSND"), (32, "BSH", "BNSD"),
+                                                      (96, "BNSD", "BSH")])
+def test_paged_chunked_prefill(bs, cache_layout, q_layout):
+    lq, lkv = [37, 64, 1, 100], [300, 64, 77, 229]
+    hq, hkv, d = 8, 2, 128
+    q, k4, v4, bt = _paged_seq_case(lq, lkv, hq, hkv, d, bs, 114)
+    out, lse = _paged_seq(q, k4, v4, bt, lq, lkv, hq, hkv, bs, q_layout, cache_layout, sparse_mode=3)
+    want, wl = G.paged_prefill_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lq, lkv, (1, 2147483647, 0),
+                                         1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(len(lq), hq, max(lq)), wl)
+
+
+# Multi-token decode (speculative / MTP: 2-4 new tokens per sequence) and a sliding window over the
+# paged cache (sparse_mode 4, including one query token, which then takes the query-sequence kernel).
+@pytest.mark.parametrize("lq,mask_kw,band", [
+    ([3, 2, 4], dict(sparse_mode=3), (1, 2147483647, 0)),
+    ([4, 4, 4], dict(sparse_mode=4, pre_tokens=40, next_tokens=0), (1, 40, 0)),
+    ([1, 1, 1], dict(sparse_mode=4, pre_tokens=70, next_tokens=0), (1, 70, 0)),
+])
+def test_paged_multi_token_decode_and_window(lq, mask_kw, band):
+    lkv = [517, 130, 64]
+    hq, hkv, d, bs = 32, 8, 128, 128
+    q, k4, v4, bt = _paged_seq_case(lq, lkv, hq, hkv, d, bs, 115)
+    out, lse = _paged_seq(q, k4, v4, bt, lq, lkv, hq, hkv, bs, "BSH", "BSH", **mask_kw)
+    want, wl = G.paged_prefill_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lq, lkv, band,
+                                         1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(len(lq), hq, max(lq)), wl)

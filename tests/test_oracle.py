@@ -276,6 +276,57 @@ def test_prefill_causal_prefix_property():
     assert (out3[0, 3:] == 0).all() and np.isneginf(lse3[0, :, 3:]).all()
 
 
+def test_band_mask_rules():
+    big = 2147483647
+    # the causal modes
+    for lq, lk in ((5, 5), (3, 7), (6, 6)):
+        ii, jj = np.arange(lq)[:, None], np.arange(lk)[None, :]
+        np.testing.assert_array_equal(G.band_mask(lq, lk, 1, big, 0), jj <= ii + (lk - lq))
+        np.testing.assert_array_equal(G.band_mask(lq, lk, 0, big, 0), jj <= ii)
+        assert G.band_mask(lq, lk, 0, big, big).all() and G.band_mask(lq, lk, 1, big, big).all()
+    # visible count per row against the closed form clamp(min(i+off+nxt, lk-1) - max(i+off-pre, 0) + 1, 0)
+    for lq, lk, origin, pre, nxt in ((7, 12, 1, 3, 2), (9, 9, 0, 0, 0), (4, 10, 0, 2, -1), (6, 3, 1, 1, 5)):
+        m = G.band_mask(lq, lk, origin, pre, nxt)
+        off = lk - lq if origin else 0
+        for i in range(lq):
+            hi, lo = min(i + off + nxt, lk - 1), max(i + off - pre, 0)
+            assert m[i].sum() == max(hi - lo + 1, 0)
+            vis = [j for j in range(lk) if lo <= j <= hi]
+            assert list(np.nonzero(m[i])[0]) == vis
+
+
+def test_band_diagonal_returns_value_rows():
+    q = RNG.standard_normal((1, 6, 2, 4)).astype(np.float32)
+    k = RNG.standard_normal((1, 6, 1, 4)).astype(np.float32)
+    v = RNG.standard_normal((1, 6, 1, 4)).astype(np.float32)
+    out, lse = G.prefill_attention(q, k, v, None, None, 0, 0.5, band=(0, 0, 0))
+    np.testing.assert_allclose(out[0, :, 0], v[0, :, 0], rtol=1e-6)
+    np.testing.assert_allclose(lse[0, 0], (q[0, :, 0] * k[0, :, 0]).sum(-1) * 0.5, rtol=1e-5)
+    # a band that leaves a query nothing gives zero output and lse -inf
+    out, lse = G.prefill_attention(q, k, v, None, None, 0, 0.5, band=(0, 2147483647, -2))
+    assert (out[0, :2] == 0).all() and np.isneginf(lse[0, :, :2]).all() and np.isfinite(lse[0, :, 2:]).all()
+
+
+def test_paged_prefill_gather_and_decode_case():
+    L, lq = [9, 14], [3, 5]
+    bs, hkv, hq, d = 4, 2, 4, 8
+    k, v, bt = _paged(L, hkv, d, bs, RNG)
+    q = RNG.standard_normal((2, 5, hq, d)).astype(np.float32)
+    out, lse = G.paged_prefill_attention(q, k, v, bt, lq, L, (1, 2147483647, 0), 0.3)
+    for b in range(2):
+        kk = k[bt[b]].reshape(-1, hkv, d)[None, :L[b]]
+        vv = v[bt[b]].reshape(-1, hkv, d)[None, :L[b]]
+        o2, l2 = G.prefill_attention(q[b:b + 1, :lq[b]], kk, vv, None, None, 1, 0.3)
+        np.testing.assert_allclose(out[b, :lq[b]], o2[0], rtol=1e-6)
+        np.testing.assert_allclose(lse[b, :, :lq[b]], l2[0], rtol=1e-6)
+        assert (out[b, lq[b]:] == 0).all()
+    # one query token with the bottom-right causal mask is the decode case
+    o1, l1 = G.paged_prefill_attention(q[:, :1], k, v, bt, [1, 1], L, (1, 2147483647, 0), 0.3)
+    od, ld = G.paged_decode_attention(q[:, 0], k, v, bt, L, 0.3)
+    np.testing.assert_allclose(o1[:, 0], od, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(l1[:, :, 0], ld, rtol=1e-5)
+
+
 def test_mla_equals_gqa_on_dequantised_latent():
     L = [7, 20]
     bs, dn, dr, h = 4, 16, 4, 3

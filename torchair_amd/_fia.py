@@ -2,11 +2,16 @@
 
 Output shapes follow python/torchair/ops/_npu_fused_infer_attention_score.py:160-374
 (layout table, value head dim, attention_out and softmax_lse shapes). The ROCm
-implementation serves three cases:
-  * paged GQA decode   - block_table given, one query token per sequence;
+implementation serves four cases:
+  * paged GQA decode    - block_table given, one query token per sequence that sees the whole cached
+                          prefix;
+  * paged query sequences - block_table given, several query tokens (chunked prefill, multi-token
+                          decode) or a band mask: the prefill kernel reading K/V through the block table;
   * MLA absorbed decode - block_table + query_rope/key_rope, int8 latent cache with a
                           per-token fp32 scale (key_antiquant_mode 1);
-  * dense prefill       - no block_table; optional causal mask (sparse_mode 2 / 3).
+  * dense prefill       - no block_table.
+Masks: sparse_mode 2 / 3 (causal from the top-left / bottom-right), 0 and 4 (a band of pre_tokens /
+next_tokens from the top-left / bottom-right).
 Sequence lengths stay on the device (tensor arguments of air::npu_fused_infer_attention_score),
 so a captured graph replays correctly with new lengths.
 """
@@ -205,23 +210,23 @@ def fia_cuda(query, key, value, **kw):
     seq_kv = _lens_tensor(kw.get("actual_seq_lengths_kv"), query.device)
     seq_q = _lens_tensor(kw.get("actual_seq_lengths"), query.device)
 
+    mask_origin, pre, nxt = _mask_params(kw)
+
     if block_table is not None:
         _check(ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql,
                "npu_fused_infer_attention_score: paged attention supports BSH/BSND/BNSD/TND without layout change")
         b = query.size(0)
         s = 1 if ql == "TND" else _bsnd(query, ql, num_heads)[1]
-        _check(s == 1, "npu_fused_infer_attention_score: paged attention serves one query token per sequence")
         _check(seq_kv is not None and seq_kv.numel() == b,
                "npu_fused_infer_attention_score: actual_seq_lengths_kv is required with block_table")
         bt = block_table.to(torch.int32).contiguous()
         _check(bt.dim() == 2 and bt.size(0) == b, "npu_fused_infer_attention_score: block_table must be [B, max_blocks]")
         if kw.get("query_rope") is not None:
+            _check(s == 1, "npu_fused_infer_attention_score: MLA serves one query token per sequence")
             return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
         _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
-               "npu_fused_infer_attention_score: paged decode takes bf16 query/key/value")
-        _check(kw.get("atten_mask") is None, "npu_fused_infer_attention_score: atten_mask is not used in decode")
-        q = query.contiguous()
-        d = q.numel() // (b * num_heads)
+               "npu_fused_infer_attention_score: paged attention takes bf16 query/key/value")
+        d = _value_d(block_table, value, query, ql, n_kv)
         if key.dim() == 3:
             bs = key.size(1)
             _check(key.size(2) == n_kv * d, "npu_fused_infer_attention_score: key cache must be [blocks, bs, Hkv*D]")
@@ -235,53 +240,79 @@ def fia_cuda(query, key, value, **kw):
                "npu_fused_infer_attention_score: key/value caches must share shape and a dense head dim")
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
-        ws_bytes = _lib.query("tai_fia_paged_decode_workspace_size", b, num_heads, d, bt.size(1), bs)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
-        _lib.call("tai_fia_paged_decode", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh, bt.data_ptr(),
-                  bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, bs, scale, out.data_ptr(),
-                  lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
-        return out, lse
+        # one query token that the mask leaves the whole prefix: the decode kernel
+        if s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0)):
+            q = query.contiguous()
+            ws_bytes = _lib.query("tai_fia_paged_decode_workspace_size", b, num_heads, d, bt.size(1), bs)
+            ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+            _lib.call("tai_fia_paged_decode", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh,
+                      bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, bs, scale, out.data_ptr(),
+                      lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+            return out, lse
+        # query sequences over the paged cache (chunked prefill, multi-token decode)
+        _check(ql != "TND", "npu_fused_infer_attention_score: paged attention with several query tokens takes "
+                            "BSH/BSND/BNSD queries")
+        b, s_q, hq, d = _bsnd(query, ql, num_heads)
+        qs = _strides_bshd(query, ql, hq)
+        os_ = _strides_bshd(out, ol, hq)
+        kstr = [0, ss, sh]
+        return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, bt.size(1) * bs, hq, n_kv, d, qs, kstr,
+                             kstr, os_, seq_q, seq_kv, mask_origin, pre, nxt, bt, bs, sb, sb, scale, stream)
 
     # ---------------------------------------------------------------- dense prefill
     _check(ql in ("BSH", "BSND", "BNSD") and ol == ql,
            "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
     _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
            "npu_fused_infer_attention_score: prefill takes bf16 query/key/value")
-    sparse_mode = int(kw.get("sparse_mode", 0))
-    mask = kw.get("atten_mask")
-    if sparse_mode in (2, 3):
-        causal = 1 if sparse_mode == 3 else 2
-    elif sparse_mode == 0:
-        _check(mask is None, "npu_fused_infer_attention_score: explicit atten_mask with sparse_mode 0 is not supported;"
-                             " use sparse_mode 2/3 for causal masks")
-        pre, nxt = int(kw.get("pre_tokens", 2147483647)), int(kw.get("next_tokens", 2147483647))
-        if nxt == 0 and pre >= 2147483647 // 2:
-            causal = 2
-        else:
-            _check(pre >= 2147483647 // 2 and nxt >= 2147483647 // 2,
-                   "npu_fused_infer_attention_score: band masks (pre/next tokens) are not supported")
-            causal = 0
-    else:
-        raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported")
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
-    if ql == "BSH":
-        s_kv = key.size(1)
-    elif ql == "BSND":
-        s_kv = key.size(1)
-    else:
-        s_kv = key.size(2)
+    s_kv = key.size(2) if ql == "BNSD" else key.size(1)
     qs = _strides_bshd(query, ql, hq)
     ks = _strides_bshd(key, ql, n_kv)
     vs = _strides_bshd(value, ql, n_kv)
     os_ = _strides_bshd(out, ol, hq)
+    return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, qs, ks, vs, os_, seq_q,
+                         seq_kv, mask_origin, pre, nxt, None, 0, 0, 0, scale, stream)
+
+
+# pre_tokens / next_tokens at or above this are no bound (the default 2147483647)
+_NO_BOUND = 2147483647
+
+
+def _mask_params(kw):
+    """(origin, pre_tokens, next_tokens) of the attention mask: query i of len_q sees kv j of len_kv when
+    -pre <= j - i - off <= next, off = len_kv - len_q (origin 1, bottom-right) or 0 (origin 0, top-left).
+    sparse_mode 0: band of pre/next tokens from the top-left (no bound by default); 2: top-left causal;
+    3: bottom-right causal; 4: band of pre/next tokens from the bottom-right. Modes 2-4 take the fixed
+    compressed triangle as atten_mask (torch_npu's 2048 x 2048 convention); its contents are implied by
+    the mode and not read. An explicit mask (mode 0 or 1) is not supported."""
+    sparse_mode = int(kw.get("sparse_mode", 0))
+    pre = int(kw.get("pre_tokens", _NO_BOUND))
+    nxt = int(kw.get("next_tokens", _NO_BOUND))
+    if sparse_mode == 0:
+        _check(kw.get("atten_mask") is None,
+               "npu_fused_infer_attention_score: explicit atten_mask with sparse_mode 0 is not supported; use "
+               "sparse_mode 2/3 for causal masks or pre_tokens/next_tokens for a band")
+        return 0, pre, nxt
+    if sparse_mode == 2:
+        return 0, _NO_BOUND, 0
+    if sparse_mode == 3:
+        return 1, _NO_BOUND, 0
+    if sparse_mode == 4:
+        return 1, pre, nxt
+    raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported (0, 2, 3, 4)")
+
+
+def _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, qs, ks, vs, os_, seq_q, seq_kv,
+                  mask_origin, pre, nxt, bt, bs, kblk, vblk, scale, stream):
     _check(hq % n_kv == 0, "npu_fused_infer_attention_score: num_heads must be a multiple of num_key_value_heads")
-    arr = [(_ctypes_i64(qs)), _ctypes_i64(ks), _ctypes_i64(vs), _ctypes_i64(os_)]
+    arr = [_ctypes_i64(qs), _ctypes_i64(ks), _ctypes_i64(vs), _ctypes_i64(os_)]
     ws_bytes = _lib.query("tai_fia_prefill_workspace_size", b, s_q, hq, n_kv)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
     _lib.call("tai_fia_prefill", query.data_ptr(), key.data_ptr(), value.data_ptr(), b, s_q, s_kv, hq, n_kv, d,
               arr[0], arr[1], arr[2], arr[3], seq_q.data_ptr() if seq_q is not None else None,
-              seq_kv.data_ptr() if seq_kv is not None else None, causal, scale, out.data_ptr(),
-              lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+              seq_kv.data_ptr() if seq_kv is not None else None, mask_origin, pre, nxt,
+              bt.data_ptr() if bt is not None else None, bt.size(1) if bt is not None else 0, bs, kblk, vblk, scale,
+              out.data_ptr(), lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
     return out, lse
 
 

@@ -460,7 +460,16 @@ struct PrefillArgs {
   int64_t b;
   int64_t s_q, s_kv;
   int hq, hkv, g;
-  int causal;
+  // Visible kv positions of query i (both clamped to [0, len_kv)): -pre <= j - i - off <= next, with
+  // off = len_kv - len_q (bottom-right origin) or 0 (top-left origin). A causal mask is next = 0.
+  int origin_rd;
+  int64_t pre, next;
+  // Paged K/V (bt != null): token t of sequence b at block bt[b * bt_stride + t / bs], slot t % bs;
+  // element (block, slot, head) at block * kblk (vblk) + slot * ks[1] (vs[1]) + head * ks[2] (vs[2]).
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bs;
+  int64_t kblk, vblk;
   float scale_log2;    // |scale| * log2(e), > 0
   int neg_scale;       // the scale is negative: Q is negated on load
   int n_qt;            // query tiles per sequence
@@ -475,6 +484,16 @@ struct PrefillArgs {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef const __attribute__((address_space(1))) void gbl_void_t;
+
+// 4-byte load of a wave-uniform address through the scalar cache (counted by lgkmcnt, waited for here).
+__device__ __forceinline__ int64_t sload_i32(const int32_t* p) {
+  // uniform64 widens each 32-bit half unsigned: the builtin returns int, and OR-ing that into a 64-bit
+  // value directly would sign-extend the low half
+  const uint64_t u = static_cast<uint64_t>(uniform64(static_cast<int64_t>(reinterpret_cast<uint64_t>(p))));
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(u) : "memory");
+  return v;
+}
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
@@ -562,8 +581,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
     }
     __syncthreads();  // also: every wave is done with the previous item's LDS tiles
     const uint64_t it_u = static_cast<uint64_t>(s_item);
-    const int64_t blk = static_cast<int64_t>((static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it_u >> 32))) << 32) |
-                                             __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it_u)));
+    const int64_t blk = uniform64(static_cast<int64_t>(it_u));
     __syncthreads();
     if (blk >= a.n_items) break;
     prefill_item<D, RESCALE>(a, blk, smem, nbk, lane, w, col, grp);
@@ -584,21 +602,18 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   const int head = kvh * a.g + (unit_ok ? unit % a.g : 0);
   const int64_t Lq = a.lq ? a.lq[b] : a.s_q;
   const int64_t Lkv = a.lkv ? a.lkv[b] : a.s_kv;
-  const int64_t shift = Lkv - Lq;  // right-down causal offset
+  const int64_t off = a.origin_rd ? Lkv - Lq : 0;
   const int64_t q0 = static_cast<int64_t>(qt) * kPQ;
   const int64_t myq = q0 + col;
+  // kv range [lo_of(q), hi_of(q)) that query q sees (empty when lo >= hi)
+  auto hi_of = [&](int64_t q) -> int64_t { return imin64(Lkv, q + off + a.next + 1); };
+  auto lo_of = [&](int64_t q) -> int64_t { return imax64(0, q + off - a.pre); };
 
   // kv extent of this wave and of the whole item (uniform across the workgroup)
-  auto kv_limit = [&](int64_t qlast) -> int64_t {
-    if (a.causal == 1) return min<int64_t>(Lkv, qlast + shift + 1);
-    if (a.causal == 2) return min<int64_t>(Lkv, qlast + 1);
-    return Lkv;
-  };
   const bool wave_live = unit_ok && q0 < Lq;
-  const int64_t wave_kv = wave_live ? imax64(0, kv_limit(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
-  // tokens below this need no mask for any query of the wave
-  const int64_t wave_clean = wave_live ? imax64(0, kv_limit(q0)) - (a.causal ? 1 : 0) : 0;
-  int64_t blk_kv = 0;
+  const int64_t wave_kv = wave_live ? imax64(0, hi_of(min<int64_t>(q0 + kPQ, Lq) - 1)) : 0;
+  const int64_t wave_lo = wave_live ? imin64(lo_of(q0), wave_kv) : 0;
+  int64_t blk_kv = 0, blk_lo = 0;
   {
     const int last_unit = min(jb * kPWaves + kPWaves - 1, a.units_per_bk - 1);
     const int qt_lo = (jb * kPWaves) / a.g;   // units are qtile-major: the first unit has the smallest tile
@@ -606,8 +621,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
     const int64_t qlast = min<int64_t>(static_cast<int64_t>(qt_hi) * kPQ + kPQ, Lq) - 1;
     // an item whose query tiles all lie past this sequence's length has no live wave: it loads
     // nothing (its tiles exist because the item list is sized for the longest sequence)
-    blk_kv = (qlast >= 0 && static_cast<int64_t>(qt_lo) * kPQ < Lq) ? imax64(0, kv_limit(qlast)) : 0;
+    const bool live = qlast >= 0 && static_cast<int64_t>(qt_lo) * kPQ < Lq;
+    blk_kv = live ? imax64(0, hi_of(qlast)) : 0;
+    blk_lo = live ? imin64(lo_of(static_cast<int64_t>(qt_lo) * kPQ), blk_kv) : 0;
   }
+  // the item streams whole 64-token tiles from the one holding blk_lo
+  const int64_t kv0 = (blk_lo / kPKV) * kPKV;
 
   // Q^T fragments (B operand): query myq, d slots 16 kd + 8 grp .. +8. With a negative scale Q is
   // negated (exact in bf16), so the kernel always works with a positive scale and takes the row
@@ -630,8 +649,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  // last kv token + 1 that the lane's query sees
-  const int64_t qend = (a.causal == 1) ? min<int64_t>(Lkv, myq + shift + 1) : (a.causal == 2 ? min<int64_t>(Lkv, myq + 1) : Lkv);
+  // kv tokens the lane's query sees, relative to the item's first tile
+  const int64_t qend = hi_of(myq) - kv0, qbeg = lo_of(myq) - kv0;
 
   // LDS byte offsets (within a stage) of this lane's fragment reads. Rows 32 further (the second
   // 32-token half of K) or 16 further (the next 16-token block of V) keep the row's swizzle, so
@@ -656,29 +675,46 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 
   // global_load_lds of tile [t0, t0 + 64) into stage s; rows past the end load the last row
   // (finite values; their scores are masked, so they add nothing)
-  const uint16_t* kbase = a.k + b * a.ks[0] + kvh * a.ks[2];
-  const uint16_t* vbase = a.v + b * a.vs[0] + kvh * a.vs[2];
+  const uint16_t* kbase = a.k + (a.bt ? 0 : b * a.ks[0]) + kvh * a.ks[2];
+  const uint16_t* vbase = a.v + (a.bt ? 0 : b * a.vs[0]) + kvh * a.vs[2];
+  const int32_t* btrow = a.bt ? a.bt + b * a.bt_stride : nullptr;
   auto issue_tile = [&](int64_t t0, int s) {
     char* kst = smem + s * 2 * T::kTile;
+    // paged: a 64-token tile spans at most two blocks (bs >= 32); their ids come through the scalar
+    // cache, so the wait for them does not drain the ring's outstanding vector loads
+    int64_t first_blk = 0, pid0 = 0, pid1 = 0;
+    if (btrow) {
+      first_blk = t0 / a.bs;
+      const int64_t last_blk = min<int64_t>(t0 + kPKV - 1, Lkv - 1) / a.bs;
+      pid0 = sload_i32(btrow + first_blk);
+      pid1 = last_blk > first_blk ? sload_i32(btrow + last_blk) : pid0;
+    }
 #pragma unroll
     for (int i = 0; i < T::kLoadsPerWave; ++i) {
       const int q = w * T::kLoadsPerWave + i;
       const int row = q * T::kRpi + lane / T::kCpr;
       const int c = (lane % T::kCpr) ^ T::swz(row);
       const int64_t tok = min<int64_t>(t0 + row, Lkv - 1);
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(kbase + tok * a.ks[1] + 8 * c), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(vbase + tok * a.vs[1] + 8 * c), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
+      int64_t koff = tok * a.ks[1], voff = tok * a.vs[1];
+      if (btrow) {
+        const int64_t blkn = tok / a.bs, slot = tok - blkn * a.bs;
+        const int64_t pid = blkn == first_blk ? pid0 : pid1;
+        koff = pid * a.kblk + slot * a.ks[1];
+        voff = pid * a.vblk + slot * a.vs[1];
+      }
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(kbase + koff + 8 * c), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(vbase + voff + 8 * c), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
     }
   };
 
-  const int ntiles = static_cast<int>(cdiv(blk_kv, static_cast<int64_t>(kPKV)));
+  const int ntiles = static_cast<int>(cdiv(blk_kv - kv0, static_cast<int64_t>(kPKV)));
   // Ring of kPStages = 4 slots, tile u in slot u % 4. publish(u) waits for this wave's loads of tile
   // u and passes the workgroup barrier, after which every wave's part of tile u is in LDS; the tile
   // issued next goes into the slot of tile u - 2 (u - 1 in the rescaling pass), whose last reads
   // every wave has passed by then.
   int issued = 0;
   auto issue_next = [&] {
-    if (issued < ntiles) issue_tile(static_cast<int64_t>(issued) * kPKV, issued % kPStages);
+    if (issued < ntiles) issue_tile(kv0 + static_cast<int64_t>(issued) * kPKV, issued % kPStages);
     ++issued;
   };
   auto publish = [&](int u) {
@@ -715,11 +751,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   // the compares run in the shadow of MFMAs)
   auto mask_max = [&](int n, f32x16& sd) -> float {
     const int lim = static_cast<int>(imin64(32, imax64(0, qend - 32 * static_cast<int64_t>(n))));
+    const int beg = static_cast<int>(imin64(32, imax64(0, qbeg - 32 * static_cast<int64_t>(n))));
     float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 8 * (r >> 2) + 4 * grp + (r & 3);
-      sd[r] = t < lim ? sd[r] : -INFINITY;
+      sd[r] = (t < lim && t >= beg) ? sd[r] : -INFINITY;
       m = fmaxf(m, sd[r]);
     }
     return fmaxf(m, __shfl_xor(m, 32, 64)) * a.scale_log2;
@@ -769,14 +806,17 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   // raising the reference max (and rescaling O^T and l) whenever a tile's max exceeds it by more
   // than kPfSlack. Keeping the rescale out of the fast pass keeps the O^T accumulators in place.
   bool dead = false;
-  const int wave_steps = static_cast<int>(cdiv(wave_kv, 32));
+  // this wave's 32-token steps (relative to kv0): [step_lo, step_hi)
+  const int step_hi = static_cast<int>(cdiv(imax64(0, wave_kv - kv0), 32));
+  const int step_lo = static_cast<int>(imax64(0, wave_lo - kv0) / 32);
   for (int i = 0; i < kPStages - 1; ++i) issue_next();
   for (int it = 0; it < ntiles; ++it) {
     publish(it);
     issue_next();
-    if (2 * it >= wave_steps || dead) continue;
+    // a tile's first step runs (masked) whenever its second one is live
+    if (2 * it >= step_hi || 2 * it + 1 < step_lo || dead) continue;
     const int slot = it % kPStages;
-    const bool second = 2 * it + 1 < wave_steps;
+    const bool second = 2 * it + 1 < step_hi;
     f32x16 s0, s1;
     s_mfma(2 * it, s0);
     float mx = mask_max(2 * it, s0);
@@ -1599,16 +1639,27 @@ extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq,
 extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q, int64_t s_kv, int hq,
                                int hkv, int d, const int64_t* q_strides, const int64_t* k_strides,
                                const int64_t* v_strides, const int64_t* out_strides, const int64_t* seq_lens_q,
-                               const int64_t* seq_lens_kv, int causal, float scale, void* out, float* lse,
-                               void* workspace, size_t ws_bytes, void* stream) {
+                               const int64_t* seq_lens_kv, int mask_origin, int64_t pre_tokens, int64_t next_tokens,
+                               const int32_t* block_table, int64_t max_blocks, int block_size, int64_t k_block_stride,
+                               int64_t v_block_stride, float scale, void* out, float* lse, void* workspace,
+                               size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(b >= 0 && s_q >= 0 && s_kv >= 0, "tai_fia_prefill: negative size");
   TAI_CHECK_ARG(hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_prefill: heads must be a multiple of kv heads");
-  TAI_CHECK_ARG(causal >= 0 && causal <= 2, "tai_fia_prefill: causal must be 0, 1 (right-down) or 2 (left-up)");
+  TAI_CHECK_ARG(mask_origin == 0 || mask_origin == 1, "tai_fia_prefill: mask_origin must be 0 (top-left) or 1 "
+                "(bottom-right)");
   TAI_UNSUPPORTED(d != 64 && d != 128, "tai_fia_prefill: head_dim %d not supported (64, 128)", d);
   TAI_CHECK_ARG(q_strides && k_strides && v_strides && out_strides, "tai_fia_prefill: null strides");
   for (int i = 0; i < 3; ++i)
     TAI_CHECK_ARG(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && out_strides[i] % 4 == 0,
                   "tai_fia_prefill: strides must keep 16-byte rows");
+  if (block_table) {
+    TAI_CHECK_ARG(seq_lens_kv != nullptr && max_blocks > 0, "tai_fia_prefill: paged K/V need seq_lens_kv and "
+                  "max_blocks > 0");
+    TAI_UNSUPPORTED(block_size < 32 || block_size % 32 != 0, "tai_fia_prefill: paged block_size %d must be a "
+                    "multiple of 32", block_size);
+    TAI_CHECK_ARG(k_block_stride % 8 == 0 && v_block_stride % 8 == 0, "tai_fia_prefill: block strides must keep "
+                  "16-byte rows");
+  }
   if (b == 0 || s_q == 0) return TAI_OK;
   TAI_CHECK_ARG(q && k && v && out, "tai_fia_prefill: null pointer");
   PrefillArgs a;
@@ -1619,7 +1670,19 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.lse = lse;
   for (int i = 0; i < 3; ++i) { a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = out_strides[i]; }
   a.lq = seq_lens_q; a.lkv = seq_lens_kv; a.b = b; a.s_q = s_q; a.s_kv = s_kv;
-  a.hq = hq; a.hkv = hkv; a.g = hq / hkv; a.causal = causal;
+  a.hq = hq; a.hkv = hkv; a.g = hq / hkv;
+  // pre / next beyond 2^40 tokens are no bound (keeps the kernel's position arithmetic in range)
+  constexpr int64_t kNoBound = int64_t(1) << 40;
+  a.origin_rd = mask_origin;
+  a.pre = pre_tokens < kNoBound ? pre_tokens : kNoBound;
+  a.next = next_tokens < kNoBound ? next_tokens : kNoBound;
+  a.pre = a.pre > -kNoBound ? a.pre : -kNoBound;
+  a.next = a.next > -kNoBound ? a.next : -kNoBound;
+  a.bt = block_table;
+  a.bt_stride = max_blocks;
+  a.bs = block_size;
+  a.kblk = k_block_stride;
+  a.vblk = v_block_stride;
   // the kernel works with a positive scale (a negative one negates Q); a zero scale makes every score
   // zero, which the smallest normal scale reproduces up to rounding far below bf16 resolution
   a.neg_scale = scale < 0.0f;
