@@ -261,18 +261,18 @@ int tai_moe_finalize_routing(const void* expanded, int dtype, int64_t t, int64_t
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/fused_infer_attention_score.py:4-109
  *   and python/torchair/ops/_npu_fused_infer_attention_score.py:14-34 (prototype
  *   experiment_ops.h:3878-3965; output shape rules :160-374 of the latter file).
- * q: [b, hq, d] bf16 (BSH with S=1 and BNSD with S=1 share this memory order).
- * k_cache / v_cache: bf16, element (block, slot, kv_head, dim) at
+ * q: [b, hq, d] of dtype (TAI_DT_BF16 or TAI_DT_FP16; BSH with S=1 and BNSD with S=1 share this
+ *   memory order). k_cache / v_cache / out: dtype, element (block, slot, kv_head, dim) at
  *   block*stride_block + slot*stride_slot + kv_head*stride_head + dim (elements).
  * block_table: [b, max_blocks] int32; seq_lens_kv: [b] int64 (device).
- * out: [b, hq, d] bf16; lse: NULL or [b, hq] fp32 (natural-log logsumexp of scaled scores).
+ * out: [b, hq, d]; lse: NULL or [b, hq] fp32 (natural-log logsumexp of scaled scores).
  * ------------------------------------------------------------------------------------- */
 size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, int64_t max_blocks,
                                            int block_size);
 int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                          int64_t stride_block, int64_t stride_slot, int64_t stride_head,
                          const int32_t* block_table, int64_t max_blocks,
-                         const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
+                         const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d, int dtype,
                          int block_size, float scale, void* out, float* lse, void* workspace,
                          size_t ws_bytes, void* stream);
 
@@ -281,8 +281,8 @@ int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache
  * cache, multi-token decode). Replaces ge.FusedInferAttentionScore for S_q > 1, emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/fused_infer_attention_score.py:4-109
  *   (pre_tokens / next_tokens / sparse_mode / block_table: prototype experiment_ops.h:3878-3965).
- * q / out: bf16 with element (batch, pos, head, dim) at batch*sb + pos*ss + head*sh + dim
- *   (per-tensor strides, elements).
+ * q / k / v / out: dtype (TAI_DT_BF16 or TAI_DT_FP16) with element (batch, pos, head, dim) at
+ *   batch*sb + pos*ss + head*sh + dim (per-tensor strides, elements).
  * k / v, dense (block_table NULL): like q. Paged (block_table [b, max_blocks] int32 on the device):
  *   caches whose element (block, slot, kv_head, dim) sits at block*k_block_stride + slot*k_strides[1]
  *   + kv_head*k_strides[2] + dim (v likewise); token t of sequence b is at block
@@ -297,7 +297,7 @@ int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache
  * lse: NULL or [b, hq, s_q] fp32.
  * ------------------------------------------------------------------------------------- */
 int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q,
-                    int64_t s_kv, int hq, int hkv, int d, const int64_t* q_strides,
+                    int64_t s_kv, int hq, int hkv, int d, int dtype, const int64_t* q_strides,
                     const int64_t* k_strides, const int64_t* v_strides,
                     const int64_t* out_strides, const int64_t* seq_lens_q,
                     const int64_t* seq_lens_kv, int mask_origin, int64_t pre_tokens,

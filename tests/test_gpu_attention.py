@@ -362,3 +362,48 @@ def test_paged_multi_token_decode_and_window(lq, mask_kw, band):
                                          1.0 / math.sqrt(d))
     assert_close(f32np(out), want)
     _assert_lse(lse.cpu().numpy().reshape(len(lq), hq, max(lq)), wl)
+
+
+# fp16 query / key / value: the MFMAs take fp16 on both operands (P rounded to fp16), the fast
+# prefill pass keeps P within 2^8 of its reference max.
+def test_paged_decode_fp16():
+    lens, hq, hkv, d, bs = [700, 33, 1, 129], 32, 8, 128, 128
+    q, k4, v4, bt, L = _paged_case(lens, hq, hkv, d, bs, 116)
+    q, k4, v4 = q.half(), k4.half(), v4.half()
+    out, lse = _decode(q, k4, v4, bt, L, hq, hkv, d, bs)
+    assert out.dtype == torch.float16
+    want, wl = G.paged_decode_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lens, 1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.reshape(len(lens), hq).cpu().numpy(), wl)
+
+
+@pytest.mark.parametrize("sparse_mode,band", [(3, (1, 2147483647, 0)), (4, (1, 40, 3))])
+def test_prefill_fp16(sparse_mode, band):
+    gen = torch.Generator().manual_seed(117)
+    b, s, hq, hkv, d = 2, 190, 8, 2, 128
+    q = torch.randn(b, s, hq, d, generator=gen).half()
+    k = torch.randn(b, s, hkv, d, generator=gen).half()
+    v = torch.randn(b, s, hkv, d, generator=gen).half()
+    lq, lkv = torch.tensor([190, 77]), torch.tensor([190, 120])
+    kw = dict(pre_tokens=band[1], next_tokens=band[2]) if sparse_mode == 4 else {}
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lq, lkv, hq, hkv, "BSND", sparse_mode, lse=True, **kw)
+    assert out.dtype == torch.float16
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lq.numpy(), lkv.numpy(), 0, 1.0 / math.sqrt(d),
+                                   band=band)
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)
+
+
+def test_prefill_fp16_rising_logits_take_the_rescaling_pass():
+    # logits rising far beyond the fp16 fast pass's 2^8 headroom: its items are redone by the rescaling pass
+    gen = torch.Generator().manual_seed(118)
+    b, s, hq, hkv, d = 1, 300, 4, 2, 64
+    q = torch.ones(b, s, hq, d).half()
+    k = (torch.arange(s, dtype=torch.float32) * (6.0 / s)).view(1, s, 1, 1).expand(b, s, hkv, d).half()
+    v = torch.randn(b, s, hkv, d, generator=gen).half()
+    lens = torch.tensor([s])
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lens, lens, hq, hkv, "BSND", 3, lse=True)
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lens.numpy(), lens.numpy(), 1, 1.0 / math.sqrt(d))
+    assert np.isfinite(f32np(out)).all()
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)

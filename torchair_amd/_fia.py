@@ -22,7 +22,7 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import DT_NONE
+from ._lib import DT_BF16, DT_FP16, DT_NONE
 
 # input_layout -> (query layout, output layout, query rank)
 _LAYOUTS: Dict[str, Tuple[str, str, int]] = {
@@ -224,8 +224,7 @@ def fia_cuda(query, key, value, **kw):
         if kw.get("query_rope") is not None:
             _check(s == 1, "npu_fused_infer_attention_score: MLA serves one query token per sequence")
             return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
-        _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
-               "npu_fused_infer_attention_score: paged attention takes bf16 query/key/value")
+        dt = _half_code(query, key, value)
         d = _value_d(block_table, value, query, ql, n_kv)
         if key.dim() == 3:
             bs = key.size(1)
@@ -246,7 +245,7 @@ def fia_cuda(query, key, value, **kw):
             ws_bytes = _lib.query("tai_fia_paged_decode_workspace_size", b, num_heads, d, bt.size(1), bs)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
             _lib.call("tai_fia_paged_decode", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh,
-                      bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, bs, scale, out.data_ptr(),
+                      bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, dt, bs, scale, out.data_ptr(),
                       lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
             return out, lse
         # query sequences over the paged cache (chunked prefill, multi-token decode)
@@ -256,21 +255,20 @@ def fia_cuda(query, key, value, **kw):
         qs = _strides_bshd(query, ql, hq)
         os_ = _strides_bshd(out, ol, hq)
         kstr = [0, ss, sh]
-        return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, bt.size(1) * bs, hq, n_kv, d, qs, kstr,
+        return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, bt.size(1) * bs, hq, n_kv, d, dt, qs, kstr,
                              kstr, os_, seq_q, seq_kv, mask_origin, pre, nxt, bt, bs, sb, sb, scale, stream)
 
     # ---------------------------------------------------------------- dense prefill
     _check(ql in ("BSH", "BSND", "BNSD") and ol == ql,
            "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
-    _check(query.dtype == torch.bfloat16 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16,
-           "npu_fused_infer_attention_score: prefill takes bf16 query/key/value")
+    dt = _half_code(query, key, value)
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
     s_kv = key.size(2) if ql == "BNSD" else key.size(1)
     qs = _strides_bshd(query, ql, hq)
     ks = _strides_bshd(key, ql, n_kv)
     vs = _strides_bshd(value, ql, n_kv)
     os_ = _strides_bshd(out, ol, hq)
-    return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, qs, ks, vs, os_, seq_q,
+    return _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, dt, qs, ks, vs, os_, seq_q,
                          seq_kv, mask_origin, pre, nxt, None, 0, 0, 0, scale, stream)
 
 
@@ -302,13 +300,20 @@ def _mask_params(kw):
     raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported (0, 2, 3, 4)")
 
 
-def _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, qs, ks, vs, os_, seq_q, seq_kv,
-                  mask_origin, pre, nxt, bt, bs, kblk, vblk, scale, stream):
+def _half_code(query, key, value) -> int:
+    """ScalarType code of the attention element type: bf16 or fp16, the same for query, key and value."""
+    _check(query.dtype in (torch.bfloat16, torch.float16) and key.dtype == query.dtype and value.dtype == query.dtype,
+           "npu_fused_infer_attention_score: query/key/value must all be bf16 or all fp16")
+    return DT_BF16 if query.dtype == torch.bfloat16 else DT_FP16
+
+
+def _prefill_call(query, key, value, out, lse, want_lse, b, s_q, s_kv, hq, n_kv, d, dt, qs, ks, vs, os_, seq_q,
+                  seq_kv, mask_origin, pre, nxt, bt, bs, kblk, vblk, scale, stream):
     _check(hq % n_kv == 0, "npu_fused_infer_attention_score: num_heads must be a multiple of num_key_value_heads")
     arr = [_ctypes_i64(qs), _ctypes_i64(ks), _ctypes_i64(vs), _ctypes_i64(os_)]
     ws_bytes = _lib.query("tai_fia_prefill_workspace_size", b, s_q, hq, n_kv)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
-    _lib.call("tai_fia_prefill", query.data_ptr(), key.data_ptr(), value.data_ptr(), b, s_q, s_kv, hq, n_kv, d,
+    _lib.call("tai_fia_prefill", query.data_ptr(), key.data_ptr(), value.data_ptr(), b, s_q, s_kv, hq, n_kv, d, dt,
               arr[0], arr[1], arr[2], arr[3], seq_q.data_ptr() if seq_q is not None else None,
               seq_kv.data_ptr() if seq_kv is not None else None, mask_origin, pre, nxt,
               bt.data_ptr() if bt is not None else None, bt.size(1) if bt is not None else 0, bs, kblk, vblk, scale,

@@ -55,11 +55,11 @@ _SIGS = {
         c_int, [_P, c_int, c_int64, c_int64, c_int, _P, _P, _P, _P, c_int, _P, _P, c_int, _P, _P]),
     "tai_fia_paged_decode_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int]),
     "tai_fia_paged_decode": (
-        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int,
+        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
                 c_float, _P, _P, _P, c_size_t, _P]),
     "tai_fia_prefill_workspace_size": (c_size_t, [c_int64, c_int64, c_int, c_int]),
     "tai_fia_prefill": (
-        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int,
+        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int,
                 c_int64, c_int64, _P, c_int64, c_int, c_int64, c_int64, c_float, _P, _P, _P, c_size_t, _P]),
     "tai_add_rms_norm": (c_int, [_P, _P, _P, c_int, c_int64, c_int64, c_float, _P, _P, _P, _P]),
     "tai_add_rms_norm_dynamic_quant": (

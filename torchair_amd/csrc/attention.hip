@@ -22,6 +22,44 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// The 16-bit element of query, key, value and output: bf16 (F16 = false) or fp16 (F16 = true). The
+// score and P.V MFMAs take that type on both operands, so P is rounded to it too.
+template <bool F16>
+struct Half;
+template <>
+struct Half<false> {
+  using v8 = bf16x8;
+  using v2 = bf16x2_t;
+  static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) { return f32_to_bf16(f); }
+  static __device__ __forceinline__ v2 pack(float a, float b) { return __builtin_convertvector((f32x2_t){a, b}, v2); }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
+  static constexpr float kSlack = 64.0f;  // log2 headroom of P above the fast pass's reference max
+};
+template <>
+struct Half<true> {
+  using v8 = f16x8;
+  using v2 = f16x2_t;
+  static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) { return f32_to_f16(f); }
+  static __device__ __forceinline__ v2 pack(float a, float b) { return __builtin_convertvector((f32x2_t){a, b}, v2); }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+  static constexpr float kSlack = 8.0f;  // P <= 2^8 keeps it well inside fp16's 65504
+};
+
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
 // ============================================================================ paged GQA decode
@@ -109,10 +147,12 @@ __device__ __forceinline__ int64_t dec_units(int64_t len) { return len > 0 ? dec
 
 // One segment: tokens [t_begin, t_end) of sequence b for kv head kvh, written as the partial of
 // the given slot.
-template <int D>
+template <int D, bool F16>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* s_kv, int64_t b, int kvh, int64_t t_begin,
                                                int64_t t_end, int64_t slot) {
   using T = DecodeTile<D>;
+  using H = Half<F16>;
+  using hv8 = typename H::v8;
   const int lane = threadIdx.x;
   const int hcol = lane & 15, kg = lane >> 4;
   const int64_t unit = slot * a.hkv + kvh;
@@ -120,13 +160,13 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* 
   float* pml = a.part_ml + unit * 32;
 
   // Q^T fragments (B operand): head = hcol (padded to 16), d slots 32m + 8kg .. +8
-  bf16x8 qf[D / 32];
+  hv8 qf[D / 32];
   {
     const bool valid = hcol < a.g;
     const uint16_t* qh = a.q + (b * a.hq + kvh * a.g + (valid ? hcol : 0)) * D;
 #pragma unroll
     for (int m = 0; m < D / 32; ++m)
-      qf[m] = as_bf16x8(valid ? *reinterpret_cast<const uint4*>(qh + 32 * m + 8 * kg) : make_uint4(0, 0, 0, 0));
+      qf[m] = __builtin_bit_cast(hv8, valid ? *reinterpret_cast<const uint4*>(qh + 32 * m + 8 * kg) : make_uint4(0, 0, 0, 0));
   }
   f32x4 acc[D / 16];
 #pragma unroll
@@ -214,7 +254,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* 
       sc[tb] = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int m = 0; m < D / 32; ++m)
-        sc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kcur[tb][m]), qf[m], sc[tb], 0, 0, 0);
+        sc[tb] = H::mfma16(__builtin_bit_cast(hv8, kcur[tb][m]), qf[m], sc[tb]);
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -231,14 +271,17 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* 
     const float m_new = fmaxf(m_run, mx);  // finite: every step holds at least one valid token
     const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     float rs = 0.0f;
-    bf16x8 pf;
+    hv8 pf;
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(sc[tb][r] - m_new);
-        rs += e;
-        pf[4 * tb + r] = static_cast<__bf16>(e);
+      for (int r = 0; r < 4; r += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(sc[tb][r] - m_new);
+        const float e1 = __builtin_amdgcn_exp2f(sc[tb][r + 1] - m_new);
+        rs += e0 + e1;
+        const typename H::v2 pk = H::pack(e0, e1);
+        pf[4 * tb + r] = pk[0];
+        pf[4 * tb + r + 1] = pk[1];
       }
     rs += __shfl_xor(rs, 16, 64);
     rs += __shfl_xor(rs, 32, 64);
@@ -264,7 +307,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* 
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
       const v4i_t vv = v4i_t{lo[t][0], lo[t][1], hi[t][0], hi[t][1]};
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pf, acc[t], 0, 0, 0);
+      acc[t] = H::mfma16(__builtin_bit_cast(hv8, vv), pf, acc[t]);
     }
   }
   // ---- partial out: head hcol, d = 16t + 4kg + r
@@ -285,7 +328,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, lds_char_t* 
 // next to each other (the cache rows of a token hold all its kv heads, so they are read at about
 // the same time). A wave runs one segment per sequence its range touches. The first wave also
 // records the step prefix the merge uses to find a sequence's partials.
-template <int D>
+template <int D, bool F16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
 void paged_decode_kernel(DecodeArgs a) {
   using T = DecodeTile<D>;
@@ -338,7 +381,7 @@ void paged_decode_kernel(DecodeArgs a) {
     const int64_t u0 = x - pb, u1 = u0 + seg;
     const int64_t s0 = max<int64_t>(u0, kDecSegCost) - kDecSegCost, s1 = max<int64_t>(u1, kDecSegCost) - kDecSegCost;
     if (s1 > s0)
-      decode_segment<D>(a, (lds_char_t*)s_kv, b, kvh, s0 * kStep, min(len, s1 * kStep), r + b);
+      decode_segment<D, F16>(a, (lds_char_t*)s_kv, b, kvh, s0 * kStep, min(len, s1 * kStep), r + b);
     g += seg;
     x += seg;
     if (x == pb + n) {  // on to the next non-empty sequence
@@ -354,7 +397,7 @@ void paged_decode_kernel(DecodeArgs a) {
 // D / 64 consecutive d. The partials are those of the ranges that cover the sequence's steps
 // (ranges with no steps wrote nothing). A partial's statistics are wave-uniform loads and its O
 // values do not depend on them, so all loads of a partial go out together.
-template <int D>
+template <int D, bool F16>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint16_t* out, float* lse) {
   constexpr int E = D / 64;  // outputs per lane
   const int lane = threadIdx.x & 63;
@@ -403,7 +446,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
     M = m_new;
   }
 #pragma unroll
-  for (int e = 0; e < E; ++e) o[e] = f32_to_bf16(den > 0.0f ? num[e] / den : 0.0f);
+  for (int e = 0; e < E; ++e) o[e] = Half<F16>::bits(den > 0.0f ? num[e] / den : 0.0f);
   if (lse && lane == 0) lse[b * a.hq + h] = den > 0.0f ? (M + log2f(den)) * kLn2 : -INFINITY;
 }
 
@@ -446,7 +489,6 @@ constexpr int kPWaves = 8;    // waves (units) per item
 constexpr int kPKV = 64;      // kv tokens per LDS tile
 constexpr int kPStages = 4;
 constexpr int kPfQueues = 8;  // one work queue per XCD
-constexpr float kPfSlack = 64.0f;  // log2-domain headroom of the softmax reference max
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -550,7 +592,7 @@ __global__ void prefill_queue_reset(int* queue, int* flags, int64_t n_items) {
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n_items; i += gridDim.x * 256) flags[i] = 0;
 }
 
-template <int D, bool RESCALE>
+template <int D, bool RESCALE, bool F16>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int lane,
                                              int w, int col, int grp);
 
@@ -561,7 +603,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 // keeps the CUs busy to the end (with one workgroup per CU, the hardware dispatcher's fixed order
 // leaves a CU idle behind another CU's long workgroup). When B * Hkv is a multiple of 8 a queue
 // holds the items of the (b, kv head) pairs whose K/V then stays in one XCD's L2.
-template <int D, bool RESCALE>
+template <int D, bool RESCALE, bool F16>
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63;
@@ -584,14 +626,17 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
     const int64_t blk = uniform64(static_cast<int64_t>(it_u));
     __syncthreads();
     if (blk >= a.n_items) break;
-    prefill_item<D, RESCALE>(a, blk, smem, nbk, lane, w, col, grp);
+    prefill_item<D, RESCALE, F16>(a, blk, smem, nbk, lane, w, col, grp);
   }
 }
 
-template <int D, bool RESCALE>
+template <int D, bool RESCALE, bool F16>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, char* smem, int64_t nbk, int lane,
                                              int w, int col, int grp) {
   using T = PrefillTile<D>;
+  using H = Half<F16>;
+  using hv8 = typename H::v8;
+  constexpr float kSlack = H::kSlack;
   const int jb = a.blocks_per_bk - 1 - static_cast<int>(blk / nbk);  // heaviest query tiles first
   const int64_t bk = blk % nbk;
   const int kvh = static_cast<int>(bk % a.hkv);
@@ -631,7 +676,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   // Q^T fragments (B operand): query myq, d slots 16 kd + 8 grp .. +8. With a negative scale Q is
   // negated (exact in bf16), so the kernel always works with a positive scale and takes the row
   // maximum of the raw scores.
-  bf16x8 qf[D / 16];
+  hv8 qf[D / 16];
   {
     const uint32_t qsign = a.neg_scale ? 0x80008000u : 0u;
     const bool ok = wave_live && myq < Lq;
@@ -640,7 +685,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
     for (int kd = 0; kd < D / 16; ++kd) {
       uint4 u = ok ? *reinterpret_cast<const uint4*>(qp + 16 * kd + 8 * grp) : make_uint4(0, 0, 0, 0);
       u.x ^= qsign; u.y ^= qsign; u.z ^= qsign; u.w ^= qsign;
-      qf[kd] = as_bf16x8(u);
+      qf[kd] = __builtin_bit_cast(hv8, u);
     }
   }
   f32x16 acc[D / 32];
@@ -726,43 +771,44 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   };
   static_assert(kPStages == 4, "the ring protocol below assumes four slots");
   static_assert(2 * T::kLoadsPerTile < 64, "vmcnt range");
-  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  const typename H::v2 ones = H::pack(1.0f, 1.0f);
 
   // S^T of 32-token step n (tokens 32n .. 32n + 31) from the slot of its tile, raw (unscaled).
   auto s_mfma = [&](int n, f32x16& sd) {
     const uint32_t kb0 = smem_base + static_cast<uint32_t>((n >> 1) % kPStages) * 2 * T::kTile +
                          static_cast<uint32_t>(n & 1) * 32 * T::kRowBytes;
-    bf16x8 kf[D / 16];
+    hv8 kf[D / 16];
     static_for<D / 16>([&](auto kdc) {
       constexpr int kd = decltype(kdc)::value;
       uint4 raw;
       pf_read_b128<0>(raw, kb0 + koff[kd]);
-      kf[kd] = as_bf16x8(raw);
+      kf[kd] = __builtin_bit_cast(hv8, raw);
     });
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // the fragments pass through empty asm after the wait, so no use is scheduled before it
 #pragma unroll
     for (int kd = 0; kd < D / 16; ++kd) asm volatile("" : "+v"(kf[kd]));
-    sd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], f32x16{}, 0, 0, 0);
+    sd = H::mfma32(kf[0], qf[0], f32x16{});
 #pragma unroll
-    for (int kd = 1; kd < D / 16; ++kd) sd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kd], qf[kd], sd, 0, 0, 0);
+    for (int kd = 1; kd < D / 16; ++kd) sd = H::mfma32(kf[kd], qf[kd], sd);
   };
   // masked maximum (log2 domain) of step n's raw scores; masked scores become -inf (branch-free:
   // the compares run in the shadow of MFMAs)
   auto mask_max = [&](int n, f32x16& sd) -> float {
-    const int lim = static_cast<int>(imin64(32, imax64(0, qend - 32 * static_cast<int64_t>(n))));
     const int beg = static_cast<int>(imin64(32, imax64(0, qbeg - 32 * static_cast<int64_t>(n))));
+    const int lim = static_cast<int>(imin64(32, imax64(beg, qend - 32 * static_cast<int64_t>(n))));
+    const uint32_t span = static_cast<uint32_t>(lim - beg);  // token t is visible when t - beg < span (unsigned)
     float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 8 * (r >> 2) + 4 * grp + (r & 3);
-      sd[r] = (t < lim && t >= beg) ? sd[r] : -INFINITY;
+      sd[r] = static_cast<uint32_t>(t - beg) < span ? sd[r] : -INFINITY;
       m = fmaxf(m, sd[r]);
     }
     return fmaxf(m, __shfl_xor(m, 32, 64)) * a.scale_log2;
   };
   // P of a step (16 scores of this lane's query) into two bf16 B fragments; returns the row sum
-  auto softmax = [&](const f32x16& sc, bf16x8 (&pf)[2]) -> float {
+  auto softmax = [&](const f32x16& sc, hv8 (&pf)[2]) -> float {
     const float neg_m = (m_run == -INFINITY) ? 0.0f : -m_run;
     float rs[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -771,10 +817,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
       for (int j = 0; j < 8; j += 2) {
         const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * kb2 + j], a.scale_log2, neg_m));
         const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * kb2 + j + 1], a.scale_log2, neg_m));
-        const bf16x2_t pk = __builtin_convertvector((f32x2_t){e0, e1}, bf16x2_t);
+        const typename H::v2 pk = H::pack(e0, e1);
         pf[kb2][j] = pk[0];
         pf[kb2][j + 1] = pk[1];
-        rs[kb2] = __builtin_amdgcn_fdot2_f32_bf16(pk, ones, rs[kb2], false);
+        rs[kb2] = H::dot2(pk, ones, rs[kb2]);
       }
     const float r = rs[0] + rs[1];
     return r + __shfl_xor(r, 32, 64);
@@ -789,22 +835,22 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
       pf_read_tr16<kb * 16 * T::kRowBytes>(hi[dt], vb + voff[1][dt]);
     }
   };
-  auto pv_mfma = [&](v2i_t (&lo)[D / 32], v2i_t (&hi)[D / 32], const bf16x8& p) {
+  auto pv_mfma = [&](v2i_t (&lo)[D / 32], v2i_t (&hi)[D / 32], const hv8& p) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) asm volatile("" : "+v"(lo[dt]), "+v"(hi[dt]));
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
-      const bf16x8 vv = __builtin_bit_cast(bf16x8, (v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]}));
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p, acc[dt], 0, 0, 0);
+      const hv8 vv = __builtin_bit_cast(hv8, (v4i_t{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]}));
+      acc[dt] = H::mfma32(vv, p, acc[dt]);
     }
   };
 
   // One 64-token tile at a time. The fast pass (RESCALE = false) keeps the reference max of each
   // query at the max of the first tile it sees: a wave whose tile max rises above it by more than
-  // kPfSlack (2^64 of headroom in P, l and O^T) puts the item on the rescaling pass's list and stops
+  // kSlack (2^64 of headroom in P, l and O^T for bf16, 2^8 for fp16) puts the item on the rescaling pass's list and stops
   // computing (it still takes its part in the ring); the rescaling pass redoes the whole item,
   // raising the reference max (and rescaling O^T and l) whenever a tile's max exceeds it by more
-  // than kPfSlack. Keeping the rescale out of the fast pass keeps the O^T accumulators in place.
+  // than kSlack. Keeping the rescale out of the fast pass keeps the O^T accumulators in place.
   bool dead = false;
   // this wave's 32-token steps (relative to kv0): [step_lo, step_hi)
   const int step_hi = static_cast<int>(cdiv(imax64(0, wave_kv - kv0), 32));
@@ -825,7 +871,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
       mx = fmaxf(mx, mask_max(2 * it + 1, s1));
     }
     if constexpr (RESCALE) {
-      if (__any(mx > m_run + kPfSlack)) {
+      if (__any(mx > m_run + kSlack)) {
         const float m_new = fmaxf(m_run, mx);
         const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
@@ -836,14 +882,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
         m_run = m_new;
       }
     } else {
-      if (__any(m_run != -INFINITY && mx > m_run + kPfSlack)) {
+      if (__any(m_run != -INFINITY && mx > m_run + kSlack)) {
         dead = true;
         if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
         continue;
       }
       if (m_run == -INFINITY) m_run = mx;  // a query that has seen nothing so far: O^T and l are zero
     }
-    bf16x8 pf[2];
+    hv8 pf[2];
     v2i_t lo[D / 32], hi[D / 32];
     l_run += softmax(s0, pf);
     v_read(slot, std::integral_constant<int, 0>(), lo, hi);
@@ -873,10 +919,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int d = 32 * dt + 8 * r4 + 4 * grp;
-      uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4] * inv)) |
-                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 1] * inv)) << 16);
-      uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 2] * inv)) |
-                    (static_cast<uint32_t>(f32_to_bf16(acc[dt][4 * r4 + 3] * inv)) << 16);
+      uint32_t lo = static_cast<uint32_t>(H::bits(acc[dt][4 * r4] * inv)) |
+                    (static_cast<uint32_t>(H::bits(acc[dt][4 * r4 + 1] * inv)) << 16);
+      uint32_t hi = static_cast<uint32_t>(H::bits(acc[dt][4 * r4 + 2] * inv)) |
+                    (static_cast<uint32_t>(H::bits(acc[dt][4 * r4 + 3] * inv)) << 16);
       *reinterpret_cast<uint2*>(op + d) = make_uint2(lo, hi);
     }
   if (a.lse && grp == 0)
@@ -1582,9 +1628,11 @@ extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, 
 extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block,
                                     int64_t stride_slot, int64_t stride_head, const int32_t* block_table,
                                     int64_t max_blocks, const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
-                                    int block_size, float scale, void* out, float* lse, void* workspace,
+                                    int dtype, int block_size, float scale, void* out, float* lse, void* workspace,
                                     size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(b >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_paged_decode: heads must be a multiple of kv heads");
+  TAI_UNSUPPORTED(dtype != TAI_DT_BF16 && dtype != TAI_DT_FP16, "tai_fia_paged_decode: dtype %d not supported (bf16, "
+                  "fp16)", dtype);
   TAI_UNSUPPORTED(hq / hkv > 16, "tai_fia_paged_decode: at most 16 query heads per kv head (got %d)", hq / hkv);
   TAI_UNSUPPORTED(d != 64 && d != 128 && d != 256, "tai_fia_paged_decode: head_dim %d not supported (64/128/256)", d);
   TAI_UNSUPPORTED(block_size <= 0 || block_size % kStep != 0, "tai_fia_paged_decode: block_size must be a multiple of %d", kStep);
@@ -1613,20 +1661,25 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nranges) * hkv));
   const dim3 cgrid(static_cast<unsigned>(cdiv(b * hq, 4)));
   uint16_t* o = static_cast<uint16_t*>(out);
-  switch (d) {
-    case 64:
-      paged_decode_kernel<64><<<grid, 64, 0, st>>>(a);
-      decode_combine_kernel<64><<<cgrid, 256, 0, st>>>(a, o, lse);
-      break;
-    case 128:
-      paged_decode_kernel<128><<<grid, 64, 0, st>>>(a);
-      decode_combine_kernel<128><<<cgrid, 256, 0, st>>>(a, o, lse);
-      break;
-    default:
-      paged_decode_kernel<256><<<grid, 64, 0, st>>>(a);
-      decode_combine_kernel<256><<<cgrid, 256, 0, st>>>(a, o, lse);
-      break;
-  }
+  auto launch = [&](auto f16c) {
+    constexpr bool F16 = decltype(f16c)::value;
+    switch (d) {
+      case 64:
+        paged_decode_kernel<64, F16><<<grid, 64, 0, st>>>(a);
+        decode_combine_kernel<64, F16><<<cgrid, 256, 0, st>>>(a, o, lse);
+        break;
+      case 128:
+        paged_decode_kernel<128, F16><<<grid, 64, 0, st>>>(a);
+        decode_combine_kernel<128, F16><<<cgrid, 256, 0, st>>>(a, o, lse);
+        break;
+      default:
+        paged_decode_kernel<256, F16><<<grid, 64, 0, st>>>(a);
+        decode_combine_kernel<256, F16><<<cgrid, 256, 0, st>>>(a, o, lse);
+        break;
+    }
+  };
+  if (dtype == TAI_DT_FP16) launch(std::true_type());
+  else launch(std::false_type());
   return launch_status("tai_fia_paged_decode");
 }
 
@@ -1637,7 +1690,7 @@ extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq,
 }
 
 extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int64_t s_q, int64_t s_kv, int hq,
-                               int hkv, int d, const int64_t* q_strides, const int64_t* k_strides,
+                               int hkv, int d, int dtype, const int64_t* q_strides, const int64_t* k_strides,
                                const int64_t* v_strides, const int64_t* out_strides, const int64_t* seq_lens_q,
                                const int64_t* seq_lens_kv, int mask_origin, int64_t pre_tokens, int64_t next_tokens,
                                const int32_t* block_table, int64_t max_blocks, int block_size, int64_t k_block_stride,
@@ -1648,6 +1701,8 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   TAI_CHECK_ARG(mask_origin == 0 || mask_origin == 1, "tai_fia_prefill: mask_origin must be 0 (top-left) or 1 "
                 "(bottom-right)");
   TAI_UNSUPPORTED(d != 64 && d != 128, "tai_fia_prefill: head_dim %d not supported (64, 128)", d);
+  TAI_UNSUPPORTED(dtype != TAI_DT_BF16 && dtype != TAI_DT_FP16, "tai_fia_prefill: dtype %d not supported (bf16, fp16)",
+                  dtype);
   TAI_CHECK_ARG(q_strides && k_strides && v_strides && out_strides, "tai_fia_prefill: null strides");
   for (int i = 0; i < 3; ++i)
     TAI_CHECK_ARG(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && out_strides[i] % 4 == 0,
@@ -1692,14 +1747,17 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, kPWaves));
   // the three-stage ring needs more LDS than a workgroup gets by default (set once per process)
   static const bool lds_ok = [] {
-    const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<64, false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<64>::kLds) == hipSuccess &&
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<64, true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<64>::kLds) == hipSuccess &&
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<128>::kLds) == hipSuccess &&
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, PrefillTile<128>::kLds) == hipSuccess;
+    auto set = [](const void* f, int bytes) {
+      return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+    };
+    const bool ok = set(reinterpret_cast<const void*>(&prefill_kernel<64, false, false>), PrefillTile<64>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<64, true, false>), PrefillTile<64>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<128, false, false>), PrefillTile<128>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<128, true, false>), PrefillTile<128>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<64, false, true>), PrefillTile<64>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<64, true, true>), PrefillTile<64>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<128, false, true>), PrefillTile<128>::kLds) &&
+                    set(reinterpret_cast<const void*>(&prefill_kernel<128, true, true>), PrefillTile<128>::kLds);
     (void)hipGetLastError();
     return ok;
   }();
@@ -1728,13 +1786,18 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   hipStream_t st = static_cast<hipStream_t>(stream);
   prefill_queue_reset<<<static_cast<unsigned>(std::min<int64_t>(64, cdiv(a.n_items, 256))), 256, 0, st>>>(a.queue, a.flags, a.n_items);
   const dim3 grid(static_cast<unsigned>(std::min<int64_t>(n_cu, a.n_items)));
-  if (d == 64) {
-    prefill_kernel<64, false><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
-    prefill_kernel<64, true><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
-  } else {
-    prefill_kernel<128, false><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
-    prefill_kernel<128, true><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
-  }
+  auto launch = [&](auto f16c) {
+    constexpr bool F16 = decltype(f16c)::value;
+    if (d == 64) {
+      prefill_kernel<64, false, F16><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
+      prefill_kernel<64, true, F16><<<grid, 64 * kPWaves, PrefillTile<64>::kLds, st>>>(a);
+    } else {
+      prefill_kernel<128, false, F16><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
+      prefill_kernel<128, true, F16><<<grid, 64 * kPWaves, PrefillTile<128>::kLds, st>>>(a);
+    }
+  };
+  if (dtype == TAI_DT_FP16) launch(std::true_type());
+  else launch(std::false_type());
   return launch_status("tai_fia_prefill");
 }
 
