@@ -792,19 +792,27 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
 #pragma unroll
     for (int kd = 1; kd < D / 16; ++kd) sd = H::mfma32(kf[kd], qf[kd], sd);
   };
-  // masked maximum (log2 domain) of step n's raw scores; masked scores become -inf (branch-free:
-  // the compares run in the shadow of MFMAs)
-  auto mask_max = [&](int n, f32x16& sd) -> float {
+  // Steps whose every token every query of the wave sees need no mask: tokens (relative to kv0) in
+  // [clean_lo, clean_hi), bounded by the last live query's first token and the first query's end.
+  const int64_t clean_lo = wave_live ? lo_of(min<int64_t>(q0 + kPQ, Lq) - 1) - kv0 : 0;
+  const int64_t clean_hi = wave_live ? hi_of(q0) - kv0 : 0;
+  auto clean = [&](int n) { return 32 * static_cast<int64_t>(n) >= clean_lo && 32 * static_cast<int64_t>(n) + 32 <= clean_hi; };
+  // masked scores of step n become -inf (branch-free: the compares run in the shadow of MFMAs)
+  auto mask = [&](int n, f32x16& sd) {
     const int beg = static_cast<int>(imin64(32, imax64(0, qbeg - 32 * static_cast<int64_t>(n))));
     const int lim = static_cast<int>(imin64(32, imax64(beg, qend - 32 * static_cast<int64_t>(n))));
     const uint32_t span = static_cast<uint32_t>(lim - beg);  // token t is visible when t - beg < span (unsigned)
-    float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 8 * (r >> 2) + 4 * grp + (r & 3);
       sd[r] = static_cast<uint32_t>(t - beg) < span ? sd[r] : -INFINITY;
-      m = fmaxf(m, sd[r]);
     }
+  };
+  // maximum (log2 domain) of a step's scores for this lane's query
+  auto row_max = [&](const f32x16& sd) -> float {
+    float m = sd[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) m = fmaxf(m, sd[r]);
     return fmaxf(m, __shfl_xor(m, 32, 64)) * a.scale_log2;
   };
   // P of a step (16 scores of this lane's query) into two bf16 B fragments; returns the row sum
@@ -863,49 +871,73 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
     if (2 * it >= step_hi || 2 * it + 1 < step_lo || dead) continue;
     const int slot = it % kPStages;
     const bool second = 2 * it + 1 < step_hi;
+    // both steps' score MFMAs go out before the first mask, so the second step's K reads and MFMAs
+    // overlap the wait for the first step's scores
     f32x16 s0, s1;
     s_mfma(2 * it, s0);
-    float mx = mask_max(2 * it, s0);
-    if (second) {
-      s_mfma(2 * it + 1, s1);
-      mx = fmaxf(mx, mask_max(2 * it + 1, s1));
-    }
-    if constexpr (RESCALE) {
-      if (__any(mx > m_run + kSlack)) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
+    if (second) s_mfma(2 * it + 1, s1);
+    if (!clean(2 * it)) mask(2 * it, s0);
+    if (second && !clean(2 * it + 1)) mask(2 * it + 1, s1);
+    // The fast pass takes a step's maximum only while some query of the wave has no reference max
+    // yet; afterwards a row sum above 2^kSlack (which any score more than kSlack above the reference
+    // max produces) sends the item to the rescaling pass before the step's P V.
+    const bool need_max = RESCALE || __any(m_run == -INFINITY);
+    if (need_max) {
+      float mx = row_max(s0);
+      if (second) mx = fmaxf(mx, row_max(s1));
+      if constexpr (RESCALE) {
+        if (__any(mx > m_run + kSlack)) {
+          const float m_new = fmaxf(m_run, mx);
+          const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+          l_run *= alpha;
 #pragma unroll
-        for (int i = 0; i < D / 32; ++i)
+          for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
-        m_run = m_new;
+            for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+          m_run = m_new;
+        }
+      } else {
+        if (__any(m_run != -INFINITY && mx > m_run + kSlack)) {
+          dead = true;
+          if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
+          continue;
+        }
+        if (m_run == -INFINITY) m_run = mx;  // a query that has seen nothing so far: O^T and l are zero
       }
-    } else {
-      if (__any(m_run != -INFINITY && mx > m_run + kSlack)) {
-        dead = true;
-        if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
-        continue;
-      }
-      if (m_run == -INFINITY) m_run = mx;  // a query that has seen nothing so far: O^T and l are zero
     }
+    constexpr float kSlackLin = F16 ? 256.0f : 18446744073709551616.0f;  // 2^kSlack
+    static_assert(kSlack == (F16 ? 8.0f : 64.0f), "kSlackLin follows kSlack");
+    auto overflow = [&](float rs) {  // fast pass, reference max fixed: does P leave its headroom?
+      if (RESCALE || need_max || !__any(rs > kSlackLin)) return false;
+      dead = true;
+      if (lane == 0 && atomicExch(a.flags + blk, 1) == 0) a.redo[atomicAdd(a.queue + kPfQueues, 1)] = static_cast<int32_t>(blk);
+      return true;
+    };
+    // V^T fragments of a step's two 16-token blocks are read before its softmax, which hides their LDS
+    // latency; the reads of the first block are complete once only the second block's remain
+    // (LDS reads complete in order)
+    constexpr int kVReads = 2 * (D / 32);  // ds_read_b64_tr_b16 per 16-token block
     hv8 pf[2];
-    v2i_t lo[D / 32], hi[D / 32];
-    l_run += softmax(s0, pf);
-    v_read(slot, std::integral_constant<int, 0>(), lo, hi);
+    v2i_t lo[2][D / 32], hi[2][D / 32];
+    v_read(slot, std::integral_constant<int, 0>(), lo[0], hi[0]);
+    v_read(slot, std::integral_constant<int, 1>(), lo[1], hi[1]);
+    const float rs0 = softmax(s0, pf);
+    if (overflow(rs0)) continue;  // the next publish waits for the outstanding reads
+    l_run += rs0;
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(kVReads) : "memory");
+    pv_mfma(lo[0], hi[0], pf[0]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    pv_mfma(lo, hi, pf[0]);
-    v_read(slot, std::integral_constant<int, 1>(), lo, hi);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    pv_mfma(lo, hi, pf[1]);
+    pv_mfma(lo[1], hi[1], pf[1]);
     if (second) {
-      l_run += softmax(s1, pf);
-      v_read(slot, std::integral_constant<int, 2>(), lo, hi);
+      v_read(slot, std::integral_constant<int, 2>(), lo[0], hi[0]);
+      v_read(slot, std::integral_constant<int, 3>(), lo[1], hi[1]);
+      const float rs1 = softmax(s1, pf);
+      if (overflow(rs1)) continue;
+      l_run += rs1;
+      asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(kVReads) : "memory");
+      pv_mfma(lo[0], hi[0], pf[0]);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      pv_mfma(lo, hi, pf[0]);
-      v_read(slot, std::integral_constant<int, 3>(), lo, hi);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      pv_mfma(lo, hi, pf[1]);
+      pv_mfma(lo[1], hi[1], pf[1]);
     }
   }
   if (dead) return;
