@@ -723,14 +723,39 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   const uint16_t* kbase = a.k + (a.bt ? 0 : b * a.ks[0]) + kvh * a.ks[2];
   const uint16_t* vbase = a.v + (a.bt ? 0 : b * a.vs[0]) + kvh * a.vs[2];
   const int32_t* btrow = a.bt ? a.bt + b * a.bt_stride : nullptr;
+  // Each lane's rows of a tile and their chunk offsets do not change from tile to tile: a dense tile
+  // that lies wholly before len_kv costs one scalar product and one add per load.
+  // (the host keeps 64 rows of either stride below 2^31 elements)
+  uint32_t lk_off[T::kLoadsPerWave], lv_off[T::kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < T::kLoadsPerWave; ++i) {
+    const int q = w * T::kLoadsPerWave + i;
+    const int row = q * T::kRpi + lane / T::kCpr;
+    const int c = (lane % T::kCpr) ^ T::swz(row);
+    lk_off[i] = static_cast<uint32_t>(row * a.ks[1] + 8 * c);
+    lv_off[i] = static_cast<uint32_t>(row * a.vs[1] + 8 * c);
+  }
   auto issue_tile = [&](int64_t t0, int s) {
     char* kst = smem + s * 2 * T::kTile;
+    if (!btrow && t0 + kPKV <= Lkv) {
+      const uint16_t* kt = kbase + t0 * a.ks[1];
+      const uint16_t* vt = vbase + t0 * a.vs[1];
+#pragma unroll
+      for (int i = 0; i < T::kLoadsPerWave; ++i) {
+        const int q = w * T::kLoadsPerWave + i;
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(kt + lk_off[i]), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(vt + lv_off[i]), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
+      }
+      return;
+    }
     // paged: a 64-token tile spans at most two blocks (bs >= 32); their ids come through the scalar
-    // cache, so the wait for them does not drain the ring's outstanding vector loads
-    int64_t first_blk = 0, pid0 = 0, pid1 = 0;
+    // cache, so the wait for them does not drain the ring's outstanding vector loads. Token positions
+    // stay below 2^31, so block arithmetic is 32-bit.
+    int first_blk = 0;
+    int64_t pid0 = 0, pid1 = 0;
     if (btrow) {
-      first_blk = t0 / a.bs;
-      const int64_t last_blk = min<int64_t>(t0 + kPKV - 1, Lkv - 1) / a.bs;
+      first_blk = static_cast<int>(t0) / a.bs;
+      const int last_blk = static_cast<int>(min<int64_t>(t0 + kPKV - 1, Lkv - 1)) / a.bs;
       pid0 = sload_i32(btrow + first_blk);
       pid1 = last_blk > first_blk ? sload_i32(btrow + last_blk) : pid0;
     }
@@ -739,13 +764,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
       const int q = w * T::kLoadsPerWave + i;
       const int row = q * T::kRpi + lane / T::kCpr;
       const int c = (lane % T::kCpr) ^ T::swz(row);
-      const int64_t tok = min<int64_t>(t0 + row, Lkv - 1);
-      int64_t koff = tok * a.ks[1], voff = tok * a.vs[1];
+      const int tok = static_cast<int>(min<int64_t>(t0 + row, Lkv - 1));  // rows past the end load the last row
+      int64_t koff = static_cast<int64_t>(tok) * a.ks[1], voff = static_cast<int64_t>(tok) * a.vs[1];
       if (btrow) {
-        const int64_t blkn = tok / a.bs, slot = tok - blkn * a.bs;
+        const int blkn = tok / a.bs, slot = tok - blkn * a.bs;
         const int64_t pid = blkn == first_blk ? pid0 : pid1;
-        koff = pid * a.kblk + slot * a.ks[1];
-        voff = pid * a.vblk + slot * a.vs[1];
+        koff = pid * a.kblk + static_cast<int64_t>(slot) * a.ks[1];
+        voff = pid * a.vblk + static_cast<int64_t>(slot) * a.vs[1];
       }
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(kbase + koff + 8 * c), (lds_void_t*)(kst + q * 1024), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(vbase + voff + 8 * c), (lds_void_t*)(kst + T::kTile + q * 1024), 16, 0, 0);
@@ -1739,6 +1764,9 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   for (int i = 0; i < 3; ++i)
     TAI_CHECK_ARG(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && out_strides[i] % 4 == 0,
                   "tai_fia_prefill: strides must keep 16-byte rows");
+  TAI_UNSUPPORTED(64 * std::max(std::abs(k_strides[1]), std::abs(v_strides[1])) >= (int64_t(1) << 31) ||
+                      s_kv >= (int64_t(1) << 31),
+                  "tai_fia_prefill: kv positions and 64 token rows of K/V must stay below 2^31 elements");
   if (block_table) {
     TAI_CHECK_ARG(seq_lens_kv != nullptr && max_blocks > 0, "tai_fia_prefill: paged K/V need seq_lens_kv and "
                   "max_blocks > 0");
