@@ -101,8 +101,10 @@ int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t n2,
  * x1: [M, K] int8 row-major; x2: int8, layout x2_layout (TAI_LAYOUT_KN / _NK).
  * scale: [N] or [1] fp32 (scale_len 1 or N), may be NULL for INT32 output.
  * pertoken_scale: NULL or [M] fp32. bias: NULL or [N] of bias_dtype (INT32 or FP32).
- * out: [M, N] of out_dtype. workspace: tai_quant_matmul_workspace_size(M, K, N) bytes (0 unless
- * M < 256, where K is split across workgroups and the int32 partials are summed exactly).
+ * out: [M, N] of out_dtype. workspace: tai_quant_matmul_workspace_size(M, K, N) bytes, 16-byte
+ * aligned: for M <= 128 the int32 partials of a K split (summed exactly), for M >= 4096 (K a
+ * multiple of 64, N of 256) room for an [N, K] copy of a [K, N] x2, which the call transposes into and
+ * multiplies from (without that room the [K, N] kernel runs); 0 otherwise.
  * ------------------------------------------------------------------------------------- */
 size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n);
 int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n,

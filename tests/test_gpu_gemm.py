@@ -91,6 +91,22 @@ def test_quant_matmul_skinny_epilogue(m, k, n, out_dtype, name):
                                                                      out_dtype="int32"))
 
 
+# Tall dense GEMMs with a [K, N] weight transpose it into the workspace first (M >= 4096, N % 256 == 0).
+@pytest.mark.parametrize("m,k,n,out_dtype", [(4096, 320, 768, torch.int32), (4100, 1024, 512, torch.bfloat16),
+                                             (4096, 256, 300, torch.int32)])
+def test_quant_matmul_tall_kn(m, k, n, out_dtype):
+    g = gen(16)
+    x1, w = rand_i8((m, k), g), rand_i8((k, n), g)
+    scale, pts = uniform((n,), g, 1e-3, 1e-2), uniform((m,), g, 1e-3, 1e-2)
+    if out_dtype == torch.int32:
+        out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), torch.ones(1, device=DEV), output_dtype=torch.int32)
+        np.testing.assert_array_equal(out.cpu().numpy(), G.quant_matmul(x1.numpy(), w.numpy(), out_dtype="int32"))
+    else:
+        out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), w.to(DEV), scale.to(DEV), pertoken_scale=pts.to(DEV),
+                                             output_dtype=out_dtype)
+        assert_close(f32np(out), G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), pts.numpy(), None, "bf16"))
+
+
 def test_quant_matmul_large_exact_vs_f64():
     """8192^3 demonstrator shape: exact against a float64 GPU product."""
     g = torch.Generator(device=DEV)

@@ -1398,6 +1398,46 @@ bool skinny_launch(const GemmArgs& g, int layout, const SkinnyPlan& p, hipStream
                                  : skinny_launch_layout<TAI_LAYOUT_KN>(g, p, st);
 }
 
+// [K, N] -> [N, K] byte transpose through LDS, 64 x 256 tiles (K % 64 == 0, N % 256 == 0). Large dense
+// GEMMs with a [K, N] weight run on the transposed copy: the [N, K] kernel reads its B fragments with
+// plain 16-byte LDS reads instead of transposing ones and holds a higher clock (8192^3: the transpose
+// moves 128 MB, ~25 us, and the GEMM gains more than that).
+__global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ b, int64_t k, int64_t n,
+                                                          int8_t* __restrict__ bt) {
+  __shared__ uint32_t tile[64][65];  // 64 k rows of 256 bytes (64 words), one word of padding
+  const int64_t tiles_n = n / 256;
+  const int64_t k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 256;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // 16-byte chunks, 16 per k row
+    const int c = t + 256 * i, r = c >> 4, c16 = c & 15;
+    const uint4 v = *reinterpret_cast<const uint4*>(b + (k0 + r) * n + n0 + 16 * c16);
+    tile[r][4 * c16] = v.x; tile[r][4 * c16 + 1] = v.y; tile[r][4 * c16 + 2] = v.z; tile[r][4 * c16 + 3] = v.w;
+  }
+  __syncthreads();
+  // lane: columns 4 ng .. 4 ng + 3; wave: k rows 16 kc .. 16 kc + 15; four 4 x 4 byte transposes give
+  // 16 bytes of each of the four output rows
+  const int ng = t & 63, kc = t >> 6;
+  uint32_t out[4][4];  // [column][k word]
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t in[4] = {tile[16 * kc + 4 * q][ng], tile[16 * kc + 4 * q + 1][ng], tile[16 * kc + 4 * q + 2][ng],
+                            tile[16 * kc + 4 * q + 3][ng]};
+    uint32_t tr[4];
+    transpose4x4(in, tr);  // tr[c] = bytes (k 4q .. 4q + 3) of column c
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[c][q] = tr[c];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    *reinterpret_cast<uint4*>(bt + (n0 + 4 * ng + c) * k + k0 + 16 * kc) = make_uint4(out[c][0], out[c][1], out[c][2], out[c][3]);
+}
+
+// Dense [K, N]-weight GEMMs at least this tall take the transpose above (its cost is below the
+// [N, K] kernel's gain from M = 4096 on).
+constexpr int64_t kTransposeMinM = 4096;
+bool transpose_ok(int64_t m, int64_t k, int64_t n) { return m >= kTransposeMinM && k % 64 == 0 && n % 256 == 0; }
+
 // Second half of npu_grouped_matmul_swiglu_quant_v2: one wave per row; the row's scale is
 // max|h| / 127 from the column tiles' partial maxima, y = clamp(rint(h / scale), -128, 127)
 // (npu_dynamic_quant arithmetic; a zero row gives scale 0 and y 0).
@@ -1432,6 +1472,7 @@ using namespace tai;
 
 extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n) {
   if (m <= 0 || n <= 0) return 0;
+  if (transpose_ok(m, k, n)) return static_cast<size_t>(k) * static_cast<size_t>(n) + 256;  // [N, K] copy of x2
   if (skinny_fit(m, k, n)) {
     const SkinnyPlan p = skinny_fit_plan(m, k, n);
     return p.split > 1 ? static_cast<size_t>(p.split) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4 + 256 : 0;
@@ -1531,6 +1572,15 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
   if (m >= 256 && k % kBigBK == 0 && (x2_layout == TAI_LAYOUT_NK || n % 16 == 0) && cfg_available<BigSel>()) {
     g.m_slots = cdiv(m, kBigBM);
     g.n_tiles = cdiv(n, kBigBN);
+    if (x2_layout == TAI_LAYOUT_KN && transpose_ok(m, k, n) && workspace != nullptr &&
+        ws_bytes >= static_cast<size_t>(k) * static_cast<size_t>(n) &&
+        (reinterpret_cast<uintptr_t>(workspace) % 16) == 0) {
+      int8_t* bt = static_cast<int8_t*>(workspace);
+      transpose_i8_kernel<<<dim3(static_cast<unsigned>((k / 64) * (n / 256))), 256, 0, st>>>(x2, k, n, bt);
+      g.b = bt;
+      launch_cfg<BigSel>(g, TAI_LAYOUT_NK, st);
+      return launch_status("tai_quant_matmul");
+    }
     launch_cfg<BigSel>(g, x2_layout, st);
     return launch_status("tai_quant_matmul");
   }
