@@ -73,6 +73,27 @@ int tai_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t cols,
                       int64_t num_groups, int8_t* y, float* scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * npu_dynamic_quant with quant_mode "pertensor" or dst_type_max != 0 (symmetric) and
+ * npu_dynamic_quant_asymmetric: ge.DynamicQuantV2 emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dynamic_quant.py:21-25, 47-61
+ *   (prototype third_party/ascend/include/ops/op_proto/inc/nn_quantize.h:77-85).
+ * x, smooth_scales, group_index as for tai_dynamic_quant. Per row (per_tensor 0) or over the whole
+ * input (per_tensor 1), of the smoothed values xs with maximum mx and minimum mn:
+ *   symmetric:  scale = max(|mx|, |mn|) / q (q = dst_type_max, 127 when 0),
+ *               y = clamp(rint(xs / scale), -128, 127);
+ *   asymmetric: hi = max(mx, 0), lo = min(mn, 0), scale = (hi - lo) / 255,
+ *               offset = -128 - lo / scale, y = clamp(rint(xs / scale + offset), -128, 127).
+ * A zero range gives scale 0 (offset 0) and y 0. y: [rows, cols] int8; scale (and offset for the
+ * asymmetric mode): [rows] fp32, or [1] per tensor. workspace: tai_dynamic_quant_v2_workspace_size.
+ * ------------------------------------------------------------------------------------- */
+size_t tai_dynamic_quant_v2_workspace_size(int64_t rows);
+int tai_dynamic_quant_v2(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                         const float* smooth_scales, const void* group_index,
+                         int group_index_dtype, int64_t num_groups, int symmetric, int per_tensor,
+                         float dst_type_max, int8_t* y, float* scale, float* offset,
+                         void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * npu_dequant_swiglu_quant (quant_mode=1 dynamic, swiglu_mode=0, round_mode=0 rint).
  * Replaces ge.DequantSwigluQuant emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dequant_swiglu_quant.py:5-47

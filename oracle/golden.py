@@ -95,6 +95,52 @@ def dynamic_quant(x: np.ndarray, smooth_scales: Optional[np.ndarray] = None,
     return q.reshape(x.shape), s.reshape(x.shape[:-1])
 
 
+def dynamic_quant_v2(x: np.ndarray, smooth_scales: Optional[np.ndarray] = None,
+                     group_index: Optional[np.ndarray] = None, symmetric: bool = True, per_tensor: bool = False,
+                     dst_type_max: float = 0.0):
+    """ge.DynamicQuantV2: npu_dynamic_quant with quant_mode "pertensor" or dst_type_max != 0
+    (is_symmetrical=True, .../custom/npu_dynamic_quant.py:21-25) and npu_dynamic_quant_asymmetric
+    (is_symmetrical=False, :47-61; prototype nn_quantize.h:77-85). The arithmetic is frozen by this build
+    (the reference holds only the prototype): over each row (or the whole input) of the smoothed xs,
+    symmetric: scale = max(|max|, |min|) / q (q = dst_type_max or 127), y = clamp(rint(xs / scale));
+    asymmetric: hi = max(max, 0), lo = min(min, 0), scale = (hi - lo) / 255, offset = -128 - lo / scale,
+    y = clamp(rint(xs / scale + offset)); a zero range gives scale 0, offset 0, y 0. fp32 throughout.
+    Returns (y, scale, offset) with offset None when symmetric.
+    """
+    x = np.asarray(x, F32)
+    h = x.shape[-1]
+    xr = x.reshape(-1, h)
+    if smooth_scales is not None:
+        sm = np.asarray(smooth_scales, F32)
+        if group_index is None:
+            xr = (xr * sm.reshape(1, h)).astype(F32)
+        else:
+            ends = np.asarray(group_index, np.int64)
+            g = np.minimum(np.searchsorted(ends, np.arange(xr.shape[0]), side="right"), len(ends) - 1)
+            xr = (xr * sm.reshape(-1, h)[g]).astype(F32)
+    stats = xr.reshape(1, -1) if per_tensor else xr
+    mx = stats.max(axis=1) if stats.shape[1] else np.zeros(stats.shape[0], F32)
+    mn = stats.min(axis=1) if stats.shape[1] else np.zeros(stats.shape[0], F32)
+    q = F32(dst_type_max if dst_type_max > 0 else 127.0)
+    if symmetric:
+        scale = (np.maximum(np.abs(mx), np.abs(mn)).astype(F32) / q).astype(F32)
+        offset = np.zeros_like(scale)
+    else:
+        hi, lo = np.maximum(mx, F32(0)).astype(F32), np.minimum(mn, F32(0)).astype(F32)
+        scale = ((hi - lo).astype(F32) / F32(255.0)).astype(F32)
+        safe = np.where(scale == 0, F32(1), scale).astype(F32)
+        offset = np.where(scale == 0, F32(0), (F32(-128.0) - (lo / safe).astype(F32)).astype(F32)).astype(F32)
+    sc_rows = np.broadcast_to(scale, (xr.shape[0],)) if per_tensor else scale
+    off_rows = np.broadcast_to(offset, (xr.shape[0],)) if per_tensor else offset
+    safe = np.where(sc_rows == 0, F32(1), sc_rows).astype(F32)
+    v = (xr / safe[:, None]).astype(F32)
+    if not symmetric:
+        v = (v + off_rows[:, None]).astype(F32)
+    yq = np.where(sc_rows[:, None] == 0, 0, np.clip(np.rint(v), -128, 127)).astype(np.int8)
+    shape = (1,) if per_tensor else x.shape[:-1]
+    return yq.reshape(x.shape), scale.reshape(shape), (None if symmetric else offset.reshape(shape))
+
+
 def silu(a: np.ndarray) -> np.ndarray:
     a = np.asarray(a, F32)
     with np.errstate(over="ignore"):  # exp(-a) overflows to inf for a < -88.7, giving silu = -0 as it should

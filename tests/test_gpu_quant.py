@@ -91,3 +91,30 @@ def test_dsq_bias_quant_scale_and_odd_n():
     _dsq_check(x, ws, None, True, bias=uniform((200,), g, -1, 1), qs=uniform((100,), g, 0.5, 2))
     x2, ws2, act2 = _dsq_inputs(9, 7, g)  # n not a multiple of 4 -> generic kernel
     _dsq_check(x2, ws2, act2, True)
+
+
+# DynamicQuantV2: symmetric per tensor or with a custom range, and the asymmetric op; smooth scales with
+# group_index; a zero row and an all-positive row.
+@pytest.mark.parametrize("asym,quant_mode,qmax", [(False, "pertensor", 0.0), (False, "pertoken", 63.0),
+                                                  (False, "pertensor", 100.0), (True, "pertoken", 0.0),
+                                                  (True, "pertensor", 0.0)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dynamic_quant_v2(asym, quant_mode, qmax, dtype):
+    g = gen(5)
+    x = randn((300, 1000), g, dtype)
+    x[7] = 0
+    x[9] = x[9].abs() + 0.25
+    sm = uniform((3, 1000), g, 0.5, 2.0)
+    gidx = torch.tensor([100, 250, 300], dtype=torch.int64)
+    kw = dict(smooth_scales=sm.to(DEV), group_index=gidx.to(DEV), quant_mode=quant_mode, dst_type_max=qmax)
+    if asym:
+        y, s, off = torch.ops.npu.npu_dynamic_quant_asymmetric(x.to(DEV), **kw)
+    else:
+        y, s = torch.ops.npu.npu_dynamic_quant(x.to(DEV), **kw)
+    wy, ws, woff = G.dynamic_quant_v2(f32np(x), f32np(sm), gidx.numpy(), symmetric=not asym,
+                                      per_tensor=quant_mode == "pertensor", dst_type_max=qmax)
+    assert tuple(s.shape) == ws.shape
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), ws, rtol=1e-6, atol=0)
+    if asym:
+        np.testing.assert_allclose(off.cpu().numpy(), woff, rtol=1e-5, atol=1e-5)

@@ -344,3 +344,34 @@ def test_mla_equals_gqa_on_dequantised_latent():
     o2, l2 = G.paged_decode_attention(np.concatenate([qn, qr], -1), kfull, vfull, bt, L, 0.2)
     np.testing.assert_allclose(out, o2[..., :dn], rtol=1e-4, atol=1e-6)
     np.testing.assert_allclose(lse, l2, rtol=1e-5)
+
+
+def test_dynamic_quant_v2_pinned():
+    x = RNG.standard_normal((6, 40)).astype(np.float32) * 3
+    x[2] = 0.0
+    x[3] = np.abs(x[3]) + 0.5  # all positive: lo = 0
+    # symmetric per token with q = 127 is the DynamicQuant rule
+    y, s, off = G.dynamic_quant_v2(x)
+    y0, s0 = G.dynamic_quant(x)
+    np.testing.assert_array_equal(y, y0)
+    np.testing.assert_array_equal(s, s0)
+    assert off is None
+    # a narrower symmetric range: max |y| = q, scale = amax / q
+    y, s, _ = G.dynamic_quant_v2(x, dst_type_max=63.0)
+    assert np.abs(y).max() == 63 and s[0] == pytest.approx(np.abs(x[0]).max() / 63, rel=1e-6)
+    # per tensor = per token on the flattened input
+    y, s, _ = G.dynamic_quant_v2(x, per_tensor=True)
+    yf, sf = G.dynamic_quant(x.reshape(1, -1))
+    np.testing.assert_array_equal(y, yf.reshape(x.shape))
+    assert s.shape == (1,) and s[0] == sf[0]
+    # asymmetric: the row extremes (range widened to 0) land on -128 / 127, reconstruction within half a step
+    y, s, off = G.dynamic_quant_v2(x, symmetric=False)
+    for r in (0, 1, 4, 5):
+        assert y[r, np.argmin(x[r])] == -128 and y[r, np.argmax(x[r])] == 127
+        rec = (y[r].astype(np.float64) - off[r]) * s[r]
+        assert np.abs(rec - x[r]).max() <= s[r] * 0.5 * (1 + 1e-5)
+    assert off[3] == pytest.approx(-128.0)  # lo = 0: offset -128
+    assert s[2] == 0 and off[2] == 0 and (y[2] == 0).all()
+    # asymmetric per tensor
+    y, s, off = G.dynamic_quant_v2(x, symmetric=False, per_tensor=True)
+    assert s.shape == (1,) and y.min() == -128 and y.max() == 127

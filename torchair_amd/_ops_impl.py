@@ -85,40 +85,73 @@ def _define(ns: str, schema: str, fake, cuda, name: Optional[str] = None):
 
 
 # ============================================================================ npu_dynamic_quant
+def _dq_scale_shape(input, quant_mode):
+    return [1] if quant_mode == "pertensor" else list(input.shape[:-1])
+
+
 def _dynamic_quant_fake(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
                         dst_type_max=0.0):
     return (torch.empty(input.shape, dtype=torch.int8, device=input.device),
-            torch.empty(input.shape[:-1], dtype=torch.float32, device=input.device))
+            torch.empty(_dq_scale_shape(input, quant_mode), dtype=torch.float32, device=input.device))
 
 
-def _dynamic_quant_cuda(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
-                        dst_type_max=0.0):
-    """npu_dynamic_quant: symmetric per-token int8 (npu_dynamic_quant.py:8-42)."""
+def _dq_prepare(name, input, smooth_scales, group_index, dst_type, quant_mode):
     _on_gpu(input, smooth_scales, group_index)
     code = scalar_type_code(dst_type)
-    _check(code in (None, DT_INT8), f"npu_dynamic_quant: dst_type {dst_type} not supported (int8 only)")
-    _check(quant_mode in (None, "pertoken") and math.isclose(dst_type_max or 0.0, 0.0, abs_tol=1e-12),
-           "npu_dynamic_quant: only quant_mode='pertoken' with dst_type_max=0 is supported")
-    _check(input.dtype in (torch.bfloat16, torch.float16, torch.float32),
-           "npu_dynamic_quant: input must be bf16, fp16 or fp32")
-    _check(input.dim() >= 1, "npu_dynamic_quant: input must have at least one dim")
+    _check(code in (None, DT_INT8), f"{name}: dst_type {dst_type} not supported (int8 only)")
+    _check(quant_mode in (None, "pertoken", "pertensor"), f"{name}: quant_mode must be 'pertoken' or 'pertensor'")
+    _check(input.dtype in (torch.bfloat16, torch.float16, torch.float32), f"{name}: input must be bf16, fp16 or fp32")
+    _check(input.dim() >= 1, f"{name}: input must have at least one dim")
     x = input.contiguous()
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
-    y = torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
     sm = _f32(smooth_scales)
     ng = 0
     gi = None
     if sm is not None:
         if group_index is not None:
-            _check(sm.dim() == 2 and sm.shape[1] == cols, "npu_dynamic_quant: smooth_scales must be [G, H] with group_index")
+            _check(sm.dim() == 2 and sm.shape[1] == cols, f"{name}: smooth_scales must be [G, H] with group_index")
             gi = group_index.contiguous()
             _check(gi.dtype in (torch.int32, torch.int64) and gi.numel() == sm.shape[0],
-                   "npu_dynamic_quant: group_index must be int32/int64 with G entries")
+                   f"{name}: group_index must be int32/int64 with G entries")
             ng = gi.numel()
         else:
-            _check(sm.numel() == cols, "npu_dynamic_quant: smooth_scales must have H entries")
+            _check(sm.numel() == cols, f"{name}: smooth_scales must have H entries")
+    return x, rows, cols, sm, gi, ng
+
+
+def _dq_v2(name, x, rows, cols, sm, gi, ng, symmetric, quant_mode, dst_type_max):
+    """ge.DynamicQuantV2 (npu_dynamic_quant.py:21-25 symmetric, :47-61 asymmetric)."""
+    per_tensor = quant_mode == "pertensor"
+    y = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    sshape = [1] if per_tensor else list(x.shape[:-1])
+    scale = torch.empty(sshape, dtype=torch.float32, device=x.device)
+    offset = None if symmetric else torch.empty(sshape, dtype=torch.float32, device=x.device)
+    if rows == 0:
+        if per_tensor:
+            scale.zero_()
+            if offset is not None:
+                offset.zero_()
+        return y, scale, offset
+    ws_bytes = _lib.query("tai_dynamic_quant_v2_workspace_size", rows)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    _lib.call("tai_dynamic_quant_v2", _p(x), _DT[x.dtype], rows, cols, _p(sm), _p(gi),
+              _DT[gi.dtype] if gi is not None else DT_NONE, ng, 1 if symmetric else 0, 1 if per_tensor else 0,
+              float(dst_type_max or 0.0), _p(y), _p(scale), _p(offset), _p(ws), ws_bytes, _stream(x))
+    return y, scale, offset
+
+
+def _dynamic_quant_cuda(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                        dst_type_max=0.0):
+    """npu_dynamic_quant: symmetric int8 (npu_dynamic_quant.py:8-42). Per token with dst_type_max 0 is
+    ge.DynamicQuant; per tensor, or a custom range, is ge.DynamicQuantV2 (is_symmetrical=True)."""
+    x, rows, cols, sm, gi, ng = _dq_prepare("npu_dynamic_quant", input, smooth_scales, group_index, dst_type,
+                                            quant_mode)
+    if quant_mode == "pertensor" or not math.isclose(dst_type_max or 0.0, 0.0, abs_tol=1e-12):
+        y, scale, _ = _dq_v2("npu_dynamic_quant", x, rows, cols, sm, gi, ng, True, quant_mode, dst_type_max)
+        return y, scale
+    y = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
     if rows == 0:
         return y, scale
     _lib.call("tai_dynamic_quant", _p(x), _DT[x.dtype], rows, cols, _p(sm), _p(gi),
@@ -129,6 +162,30 @@ def _dynamic_quant_cuda(input, *, smooth_scales=None, group_index=None, dst_type
 _define("npu", "npu_dynamic_quant(Tensor input, *, Tensor? smooth_scales=None, Tensor? group_index=None, "
                "ScalarType? dst_type=None, str? quant_mode=\"pertoken\", float dst_type_max=0.0) -> (Tensor, Tensor)",
         _dynamic_quant_fake, _dynamic_quant_cuda)
+
+
+def _dynamic_quant_asym_fake(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                             dst_type_max=0.0):
+    sshape = _dq_scale_shape(input, quant_mode)
+    return (torch.empty(input.shape, dtype=torch.int8, device=input.device),
+            torch.empty(sshape, dtype=torch.float32, device=input.device),
+            torch.empty(sshape, dtype=torch.float32, device=input.device))
+
+
+def _dynamic_quant_asym_cuda(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                             dst_type_max=0.0):
+    """npu_dynamic_quant_asymmetric: ge.DynamicQuantV2 with is_symmetrical=False (npu_dynamic_quant.py:47-61)."""
+    x, rows, cols, sm, gi, ng = _dq_prepare("npu_dynamic_quant_asymmetric", input, smooth_scales, group_index,
+                                            dst_type, quant_mode)
+    _check(math.isclose(dst_type_max or 0.0, 0.0, abs_tol=1e-12),
+           "npu_dynamic_quant_asymmetric: dst_type_max is not supported (the range is the full int8 range)")
+    return _dq_v2("npu_dynamic_quant_asymmetric", x, rows, cols, sm, gi, ng, False, quant_mode, 0.0)
+
+
+_define("npu", "npu_dynamic_quant_asymmetric(Tensor input, *, Tensor? smooth_scales=None, Tensor? group_index=None, "
+               "ScalarType? dst_type=None, str? quant_mode=\"pertoken\", float dst_type_max=0.0) "
+               "-> (Tensor, Tensor, Tensor)",
+        _dynamic_quant_asym_fake, _dynamic_quant_asym_cuda)
 
 
 # ============================================================================ npu_dequant_swiglu_quant

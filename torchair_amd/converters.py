@@ -28,6 +28,12 @@ declare_supported([
     Support(torch.empty(64, 16384, dtype=torch.float16)),
     Support(torch.empty(64, 16384, dtype=torch.bfloat16)),
 ])(register_fx_node_ge_converter(npu.npu_dynamic_quant.default)(_identity(npu.npu_dynamic_quant.default)))
+# .../custom/npu_dynamic_quant.py:44-48 (declared cases as for npu_dynamic_quant)
+declare_supported([
+    Support(torch.empty(64, 16384, dtype=torch.float16)),
+    Support(torch.empty(64, 16384, dtype=torch.bfloat16)),
+])(register_fx_node_ge_converter(npu.npu_dynamic_quant_asymmetric.default)(
+    _identity(npu.npu_dynamic_quant_asymmetric.default)))
 # .../custom/npu_dequant_swiglu_quant.py:5
 register_fx_node_ge_converter(npu.npu_dequant_swiglu_quant.default)(_identity(npu.npu_dequant_swiglu_quant.default))
 register_fx_node_ge_converter(npu_inference.npu_dequant_swiglu_quant.default)(

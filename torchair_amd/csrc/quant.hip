@@ -345,6 +345,110 @@ __global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
   if (threadIdx.x == 0) a.scale[row] = scale;
 }
 
+// ----------------------------------------------------------------------------- dynamic quant v2
+// Symmetric with a custom range (dst_type_max), per-tensor, and asymmetric quantisation. Three
+// passes: each row's max and min of the smoothed input -> (per-tensor) one workgroup folds the row
+// statistics -> each row is quantised with its own or the tensor's scale and offset:
+//   symmetric:  scale = max(|max|, |min|) / q,      y = clamp(rint(xs / scale), -128, 127), offset 0
+//   asymmetric: hi = max(max, 0), lo = min(min, 0), scale = (hi - lo) / 255,
+//               offset = -128 - lo / scale,         y = clamp(rint(xs / scale + offset), -128, 127)
+// (q = dst_type_max, or 127 when it is 0; fp32 arithmetic in that order; a zero range gives scale 0,
+// offset 0 and y 0).
+struct Dq2Args {
+  const void* x;
+  int dt;
+  int64_t rows, cols;
+  const float* smooth;
+  const void* gidx;
+  int gidx_dt;
+  int64_t ngroups;
+  int symmetric, per_tensor;
+  float qmax;
+  float* smax;  // [rows] row maxima (then the tensor's at [0] when per_tensor)
+  float* smin;  // [rows] row minima
+  int8_t* y;
+  float* scale;
+  float* offset;  // asymmetric only
+};
+
+__device__ __forceinline__ float dq2_value(const Dq2Args& a, const float* sm, int64_t row, int64_t c) {
+  const float v = load_as_f32(a.x, a.dt, row * a.cols + c);
+  return sm ? v * sm[c] : v;
+}
+
+__device__ __forceinline__ const float* dq2_smooth(const Dq2Args& a, int64_t row) {
+  if (a.smooth == nullptr) return nullptr;
+  const int64_t g = a.gidx != nullptr ? group_of_row_cumsum(a.gidx, a.gidx_dt, a.ngroups, row) : 0;
+  return a.smooth + g * a.cols;
+}
+
+__global__ __launch_bounds__(256) void dq2_stats_kernel(Dq2Args a) {
+  __shared__ float red[2][4];
+  const int64_t row = blockIdx.x;
+  const float* sm = dq2_smooth(a, row);
+  float mx = -INFINITY, mn = INFINITY;
+  for (int64_t c = threadIdx.x; c < a.cols; c += 256) {
+    const float v = dq2_value(a, sm, row, c);
+    mx = fmaxf(mx, v);
+    mn = fminf(mn, v);
+  }
+  mx = wave_max(mx);
+  mn = -wave_max(-mn);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[0][w] = mx; red[1][w] = mn; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    a.smax[row] = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    a.smin[row] = fminf(fminf(red[1][0], red[1][1]), fminf(red[1][2], red[1][3]));
+  }
+}
+
+__global__ __launch_bounds__(1024) void dq2_fold_kernel(Dq2Args a) {
+  __shared__ float red[2][16];
+  float mx = -INFINITY, mn = INFINITY;
+  for (int64_t r = threadIdx.x; r < a.rows; r += 1024) {
+    mx = fmaxf(mx, a.smax[r]);
+    mn = fminf(mn, a.smin[r]);
+  }
+  mx = wave_max(mx);
+  mn = -wave_max(-mn);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[0][w] = mx; red[1][w] = mn; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 16; ++i) { mx = fmaxf(mx, red[0][i]); mn = fminf(mn, red[1][i]); }
+    mx = fmaxf(mx, red[0][0]);
+    mn = fminf(mn, red[1][0]);
+    a.smax[0] = mx;
+    a.smin[0] = mn;
+  }
+}
+
+__global__ __launch_bounds__(256) void dq2_apply_kernel(Dq2Args a) {
+  const int64_t row = blockIdx.x;
+  const int64_t srow = a.per_tensor ? 0 : row;
+  const float mx = a.smax[srow], mn = a.smin[srow];
+  float sc, off = 0.0f;
+  if (a.symmetric) {
+    sc = fmaxf(fabsf(mx), fabsf(mn)) / a.qmax;
+  } else {
+    const float hi = fmaxf(mx, 0.0f), lo = fminf(mn, 0.0f);
+    sc = (hi - lo) / 255.0f;
+    off = sc == 0.0f ? 0.0f : -128.0f - lo / sc;
+  }
+  const float* sm = dq2_smooth(a, row);
+  for (int64_t c = threadIdx.x; c < a.cols; c += 256) {
+    const float v = dq2_value(a, sm, row, c);
+    float q = 0.0f;
+    if (sc != 0.0f) q = fminf(fmaxf(rintf(a.symmetric ? v / sc : v / sc + off), -128.0f), 127.0f);
+    a.y[row * a.cols + c] = static_cast<int8_t>(static_cast<int>(q));
+  }
+  if (threadIdx.x == 0 && (!a.per_tensor || row == 0)) {
+    a.scale[a.per_tensor ? 0 : row] = sc;
+    if (a.offset) a.offset[a.per_tensor ? 0 : row] = off;
+  }
+}
+
 }  // namespace
 }  // namespace tai
 
@@ -403,4 +507,41 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
   else if (aligned && ng4 <= 256 * 8) dsq_kernel<8><<<grid, 256, 0, st>>>(a);
   else dsq_generic_kernel<<<grid, 256, 0, st>>>(a);
   return launch_status("tai_dequant_swiglu_quant");
+}
+
+extern "C" size_t tai_dynamic_quant_v2_workspace_size(int64_t rows) {
+  return rows > 0 ? static_cast<size_t>(2 * rows) * sizeof(float) + 256 : 256;
+}
+
+extern "C" int tai_dynamic_quant_v2(const void* x, int x_dtype, int64_t rows, int64_t cols, const float* smooth_scales,
+                                    const void* group_index, int group_index_dtype, int64_t num_groups, int symmetric,
+                                    int per_tensor, float dst_type_max, int8_t* y, float* scale, float* offset,
+                                    void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(rows >= 0 && cols >= 0, "tai_dynamic_quant_v2: negative size");
+  TAI_CHECK_ARG(x_dtype == TAI_DT_BF16 || x_dtype == TAI_DT_FP16 || x_dtype == TAI_DT_FP32,
+                "tai_dynamic_quant_v2: x dtype %d not supported (bf16, fp16, fp32)", x_dtype);
+  TAI_CHECK_ARG(dst_type_max >= 0.0f && dst_type_max <= 127.0f, "tai_dynamic_quant_v2: dst_type_max must be in [0, 127]");
+  TAI_UNSUPPORTED(!symmetric && dst_type_max != 0.0f, "tai_dynamic_quant_v2: dst_type_max applies to the symmetric mode only");
+  TAI_CHECK_ARG(group_index == nullptr || (smooth_scales != nullptr && num_groups > 0),
+                "tai_dynamic_quant_v2: group_index needs smooth_scales with num_groups > 0");
+  TAI_CHECK_ARG(group_index == nullptr || group_index_dtype == TAI_DT_INT32 || group_index_dtype == TAI_DT_INT64,
+                "tai_dynamic_quant_v2: group_index must be int32 or int64");
+  if (rows == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && y && scale && (symmetric || offset), "tai_dynamic_quant_v2: null pointer");
+  TAI_CHECK_ARG(rows < (1ll << 31), "tai_dynamic_quant_v2: rows must be < 2^31");
+  const size_t need = tai_dynamic_quant_v2_workspace_size(rows);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_dynamic_quant_v2: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  float* smax = static_cast<float*>(workspace);
+  Dq2Args a{x, x_dtype, rows, cols, smooth_scales, group_index, group_index_dtype, group_index ? num_groups : 1,
+            symmetric ? 1 : 0, per_tensor ? 1 : 0, dst_type_max > 0.0f ? dst_type_max : 127.0f, smax, smax + rows, y,
+            scale, symmetric ? nullptr : offset};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows));
+  dq2_stats_kernel<<<grid, 256, 0, st>>>(a);
+  if (per_tensor) dq2_fold_kernel<<<1, 1024, 0, st>>>(a);
+  dq2_apply_kernel<<<grid, 256, 0, st>>>(a);
+  return launch_status("tai_dynamic_quant_v2");
 }
