@@ -116,21 +116,25 @@ int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t n2,
  * npu_quant_matmul (W8A8): acc = x1 @ x2 with exact int32 accumulation, then
  *   out_dtype INT32: acc (+ int32 bias)
  *   out_dtype BF16/FP16/FP32: (acc [+ int32 bias]) * scale[n] * pertoken_scale[m] [+ fp32 bias]
+ *   out_dtype INT8 (the converter's default, quantmatmul.py:91-92, 244-254): clamp(rint(
+ *     (acc [+ int32 bias]) * scale[n] [+ offset[n]]), -128, 127), fp32 arithmetic in that order
+ *     (scale as fp32 values; the fp32 result is held in the workspace)
  * Replaces ge.QuantBatchMatmulV3 emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/quantmatmul.py:63-255
  *   (prototype third_party/ascend/include/ops/op_proto/inc/fusion_ops.h:440-451).
  * x1: [M, K] int8 row-major; x2: int8, layout x2_layout (TAI_LAYOUT_KN / _NK).
  * scale: [N] or [1] fp32 (scale_len 1 or N), may be NULL for INT32 output.
+ * offset: NULL or [N] / [1] fp32 (offset_len), INT8 output only.
  * pertoken_scale: NULL or [M] fp32. bias: NULL or [N] of bias_dtype (INT32 or FP32).
- * out: [M, N] of out_dtype. workspace: tai_quant_matmul_workspace_size(M, K, N) bytes, 16-byte
- * aligned: for M <= 128 the int32 partials of a K split (summed exactly), for M >= 4096 (K a
+ * out: [M, N] of out_dtype. workspace: tai_quant_matmul_workspace_size(M, K, N, out_dtype) bytes,
+ * 16-byte aligned: for M <= 128 the int32 partials of a K split (summed exactly), for M >= 4096 (K a
  * multiple of 64, N of 256) room for an [N, K] copy of a [K, N] x2, which the call transposes into and
- * multiplies from (without that room the [K, N] kernel runs); 0 otherwise.
+ * multiplies from (without that room the [K, N] kernel runs), for INT8 output the fp32 result.
  * ------------------------------------------------------------------------------------- */
-size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n);
+size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n, int out_dtype);
 int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n,
-                     int x2_layout, const float* scale, int64_t scale_len,
-                     const float* pertoken_scale, const void* bias, int bias_dtype,
+                     int x2_layout, const float* scale, int64_t scale_len, const float* offset,
+                     int64_t offset_len, const float* pertoken_scale, const void* bias, int bias_dtype,
                      int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------

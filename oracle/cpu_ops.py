@@ -41,8 +41,18 @@ def register() -> None:
     from torchair_amd._ops_impl import LIBS, dtype_of_code
 
     def dq(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken", dst_type_max=0.0):
+        if quant_mode == "pertensor" or (dst_type_max or 0.0) != 0.0:
+            y, s, _ = G.dynamic_quant_v2(_np(input), _np(smooth_scales), _np(group_index), True,
+                                         quant_mode == "pertensor", dst_type_max or 0.0)
+            return _t(y), _t(s)
         y, s = G.dynamic_quant(_np(input), _np(smooth_scales), _np(group_index))
         return _t(y), _t(s)
+
+    def dq_asym(input, *, smooth_scales=None, group_index=None, dst_type=None, quant_mode="pertoken",
+                dst_type_max=0.0):
+        y, s, o = G.dynamic_quant_v2(_np(input), _np(smooth_scales), _np(group_index), False,
+                                     quant_mode == "pertensor", 0.0)
+        return _t(y), _t(s), _t(o)
 
     def dsq(x, *, weight_scale=None, activation_scale=None, bias=None, quant_scale=None, quant_offset=None,
             group_index=None, activate_left=False, quant_mode=0, dst_type=None, round_mode=None, activate_dim=None,
@@ -54,12 +64,14 @@ def register() -> None:
 
     def qmm(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None, x1_dtype=None,
             x2_dtype=None, pertoken_scale_dtype=None, scale_dtype=None, group_sizes=None):
-        od = dtype_of_code(_code(output_dtype))
-        name = "int32" if od == torch.int32 else _NAMES[od]
+        code = _code(output_dtype)
+        od = torch.int8 if code is None else dtype_of_code(code)
+        name = {torch.int32: "int32", torch.int8: "int8"}.get(od) or _NAMES[od]
         b = None if bias is None else (bias.numpy() if bias.dtype == torch.int32 else _np(bias))
         k = x1.shape[-1]
         out = G.quant_matmul(x1.reshape(-1, k).numpy(), x2.numpy(), _np(scale).reshape(-1) if scale is not None
-                             else None, _np(pertoken_scale), b, name)
+                             else None, _np(pertoken_scale), b, name,
+                             offset=None if offset is None else _np(offset).reshape(-1))
         return _t(out, od).reshape(list(x1.shape[:-1]) + [x2.shape[-1]])
 
     def gmm(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
@@ -201,6 +213,7 @@ def register() -> None:
         lib.impl("npu_kv_rmsnorm_rope_cache", kv_legacy, "CPU")
         LIBS["npu_inference"].impl("npu_kv_rmsnorm_rope_cache", kv_legacy, "CPU")
         lib.impl("npu_dynamic_quant", dq, "CPU")
+        lib.impl("npu_dynamic_quant_asymmetric", dq_asym, "CPU")
         lib.impl("npu_quant_matmul", qmm, "CPU")
         lib.impl("npu_grouped_matmul", gmm, "CPU")
         lib.impl("npu_moe_init_routing_v2", init_v2, "CPU")

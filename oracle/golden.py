@@ -224,7 +224,8 @@ def _epilogue(acc: np.ndarray, scale, pts, bias, out_dtype: str, col_scale_rows=
     return round_to(v, out_dtype)
 
 
-def quant_matmul(x1, x2, scale=None, pertoken_scale=None, bias=None, out_dtype: str = "bf16") -> np.ndarray:
+def quant_matmul(x1, x2, scale=None, pertoken_scale=None, bias=None, out_dtype: str = "bf16",
+                 offset=None) -> np.ndarray:
     """npu_quant_matmul W8A8: exact int32 accumulation, then (acc [+int32 bias]) * scale[n] * pertoken[m]
     [+ fp32 bias], rounded to out_dtype.
 
@@ -234,6 +235,13 @@ def quant_matmul(x1, x2, scale=None, pertoken_scale=None, bias=None, out_dtype: 
     """
     acc = int_matmul(x1, x2)
     sc = None if scale is None else np.asarray(scale, F32).reshape(1, -1)
+    if out_dtype == "int8":
+        # the converter's default output (output_dtype None -> 1, quantmatmul.py:91-92): fp32
+        # (acc [+ int32 bias]) * scale [* pertoken] [+ offset], then round half to even and saturate
+        v = _epilogue(acc, sc, pertoken_scale, bias, "fp32")
+        if offset is not None:
+            v = (v + np.asarray(offset, F32).reshape(1, -1)).astype(F32)
+        return np.clip(np.rint(v), -128, 127).astype(np.int8)
     return _epilogue(acc, sc, pertoken_scale, bias, out_dtype)
 
 

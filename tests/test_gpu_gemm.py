@@ -5,7 +5,7 @@ import torch
 
 import torchair_amd  # noqa: F401
 from oracle import golden as G
-from tests.helpers import assert_close, f32np, gen, rand_i8, uniform
+from tests.helpers import assert_close, assert_int8_close, f32np, gen, rand_i8, uniform
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -172,3 +172,21 @@ def test_grouped_matmul_cfg4_gate_up_exact_vs_f64():
             ref = _exact_f64(x[b0:b1], w[ei])
             assert torch.equal(out[b0:b1].to(torch.int64), ref), f"expert {ei}"
     del begin
+
+
+# int8 output (the converter's default when output_dtype is None): fp32 dequant, + offset, rint, saturate.
+@pytest.mark.parametrize("m,k,n,layout", [(64, 2048, 1024, "kn"), (512, 1024, 512, "nk"), (4096, 256, 512, "kn"),
+                                          (5, 48, 100, "kn")])
+def test_quant_matmul_int8_output(m, k, n, layout):
+    g = gen(17)
+    x1, w = rand_i8((m, k), g), rand_i8((k, n), g)
+    scale = uniform((n,), g, 1e-4, 4e-4)  # keeps most outputs inside int8, some saturate
+    off = uniform((n,), g, -3.0, 3.0)
+    bi = torch.randint(-5000, 5000, (n,), generator=g, dtype=torch.int32)
+    x2 = w if layout == "kn" else w.t().contiguous().t()
+    out = torch.ops.npu.npu_quant_matmul(x1.to(DEV), x2.to(DEV), scale.to(DEV), offset=off.to(DEV), bias=bi.to(DEV))
+    assert out.dtype == torch.int8
+    want = G.quant_matmul(x1.numpy(), w.numpy(), scale.numpy(), None, bi.numpy(), "int8", offset=off.numpy())
+    assert_int8_close(out.cpu().numpy(), want)
+    if k >= 256:
+        assert (want == 127).any() and (want == -128).any()  # saturation is exercised

@@ -375,3 +375,15 @@ def test_dynamic_quant_v2_pinned():
     # asymmetric per tensor
     y, s, off = G.dynamic_quant_v2(x, symmetric=False, per_tensor=True)
     assert s.shape == (1,) and y.min() == -128 and y.max() == 127
+
+
+def test_quant_matmul_int8_output_rule():
+    x1 = RNG.integers(-127, 128, (9, 40), dtype=np.int8)
+    x2 = RNG.integers(-127, 128, (40, 6), dtype=np.int8)
+    acc = x1.astype(np.int64) @ x2.astype(np.int64)
+    scale = np.full(6, 0.0625, np.float32)  # a power of two: acc * scale is exact
+    off = np.array([0.0, 0.5, -0.5, 1.25, -3.0, 100.0], np.float32)
+    got = G.quant_matmul(x1, x2, scale, None, None, "int8", offset=off)
+    v = acc * 0.0625 + off.astype(np.float64)
+    want = np.clip(np.round(v), -128, 127)  # numpy rounds half to even, like rint
+    np.testing.assert_array_equal(got, want.astype(np.int8))

@@ -294,11 +294,11 @@ def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
     _on_gpu(x1, x2, scale, pertoken_scale, bias)
     _check(x1.dtype == torch.int8 and x2.dtype == torch.int8, "npu_quant_matmul: x1 and x2 must be int8")
     _check(x2.dim() == 2, "npu_quant_matmul: x2 must be 2-D [K, N]")
-    _check(offset is None, "npu_quant_matmul: offset is not supported")
     _check(group_sizes is None, "npu_quant_matmul: group_sizes is not supported")
     out_dtype = _qmm_out_dtype(output_dtype)
-    _check(out_dtype in (torch.int32, torch.bfloat16, torch.float16, torch.float32),
-           "npu_quant_matmul: output_dtype must be int32, bf16, fp16 or fp32 (int8 requantisation is not supported)")
+    _check(out_dtype in (torch.int8, torch.int32, torch.bfloat16, torch.float16, torch.float32),
+           "npu_quant_matmul: output_dtype must be int8, int32, bf16, fp16 or fp32")
+    _check(offset is None or out_dtype == torch.int8, "npu_quant_matmul: offset applies to int8 output only")
     k = x1.shape[-1]
     _check(x2.shape[0] == k, f"npu_quant_matmul: K mismatch {k} vs {x2.shape[0]}")
     n = x2.shape[1]
@@ -323,10 +323,14 @@ def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
         return out
     if k == 0:
         return out.zero_()
-    ws_bytes = _lib.query("tai_quant_matmul_workspace_size", m, k, n)
+    off = _f32(offset)
+    if off is not None:
+        _check(off.numel() in (1, n), "npu_quant_matmul: offset must have 1 or N entries")
+    ws_bytes = _lib.query("tai_quant_matmul_workspace_size", m, k, n, _DT[out_dtype])
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x1.device) if ws_bytes else None
     _lib.call("tai_quant_matmul", _p(a), _p(w), m, k, n, layout, _p(sc), sc.numel() if sc is not None else 0,
-              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _p(ws), ws_bytes, _stream(a))
+              _p(off), off.numel() if off is not None else 0, _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out),
+              _p(ws), ws_bytes, _stream(a))
     return out
 
 

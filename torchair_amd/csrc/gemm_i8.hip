@@ -1470,7 +1470,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
 
 using namespace tai;
 
-extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n) {
+static size_t quant_matmul_ws_base(int64_t m, int64_t k, int64_t n) {
   if (m <= 0 || n <= 0) return 0;
   if (transpose_ok(m, k, n)) return static_cast<size_t>(k) * static_cast<size_t>(n) + 256;  // [N, K] copy of x2
   if (skinny_fit(m, k, n)) {
@@ -1482,10 +1482,65 @@ extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t 
   return p.split > 1 ? static_cast<size_t>(p.split) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4 + 256 : 0;
 }
 
+// int8 output: y = clamp(rint(f + offset[n]), -128, 127) of the fp32 result f (fp32 add, then round
+// half to even); 4 elements per thread.
+__global__ __launch_bounds__(256) void requant_i8_kernel(const float* __restrict__ f, const float* __restrict__ offset,
+                                                         int64_t offset_len, int64_t m, int64_t n, int8_t* __restrict__ y) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= m * n) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (i + q >= m * n) break;
+    const int64_t col = (i + q) % n;
+    float v = f[i + q];
+    if (offset) v = v + offset[offset_len == 1 ? 0 : col];
+    y[i + q] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(rintf(v), -128.0f), 127.0f)));
+  }
+}
+
+static int quant_matmul_impl(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
+                             const float* scale, int64_t scale_len, const float* pertoken_scale, const void* bias,
+                             int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream);
+
+extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t n, int out_dtype) {
+  const size_t base = (quant_matmul_ws_base(m, k, n) + 255) / 256 * 256;
+  if (out_dtype != TAI_DT_INT8 || m <= 0 || n <= 0) return quant_matmul_ws_base(m, k, n);
+  return base + static_cast<size_t>(m) * static_cast<size_t>(n) * sizeof(float) + 256;
+}
+
 extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
-                                const float* scale, int64_t scale_len, const float* pertoken_scale, const void* bias,
-                                int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes,
-                                void* stream) {
+                                const float* scale, int64_t scale_len, const float* offset, int64_t offset_len,
+                                const float* pertoken_scale, const void* bias, int bias_dtype, int out_dtype, void* out,
+                                void* workspace, size_t ws_bytes, void* stream) {
+  if (out_dtype != TAI_DT_INT8) {
+    TAI_CHECK_ARG(offset == nullptr, "tai_quant_matmul: offset applies to int8 output only");
+    return quant_matmul_impl(x1, x2, m, k, n, x2_layout, scale, scale_len, pertoken_scale, bias, bias_dtype, out_dtype,
+                             out, workspace, ws_bytes, stream);
+  }
+  TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 0, "tai_quant_matmul: negative size");
+  TAI_CHECK_ARG(scale != nullptr, "tai_quant_matmul: int8 output needs scale");
+  TAI_CHECK_ARG(offset == nullptr || offset_len == 1 || offset_len == n, "tai_quant_matmul: offset must have 1 or n "
+                "entries");
+  TAI_CHECK_ARG(bias == nullptr || bias_dtype == TAI_DT_INT32, "tai_quant_matmul: int8 output takes an int32 bias only");
+  if (m == 0 || n == 0) return TAI_OK;
+  const size_t base = (quant_matmul_ws_base(m, k, n) + 255) / 256 * 256;
+  const size_t need = tai_quant_matmul_workspace_size(m, k, n, out_dtype);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("tai_quant_matmul: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  float* f = reinterpret_cast<float*>(static_cast<char*>(workspace) + base);
+  const int rc = quant_matmul_impl(x1, x2, m, k, n, x2_layout, scale, scale_len, pertoken_scale, bias, bias_dtype,
+                                   TAI_DT_FP32, f, workspace, base, stream);
+  if (rc != TAI_OK) return rc;
+  requant_i8_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 1024))), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      f, offset, offset_len, m, n, static_cast<int8_t*>(out));
+  return launch_status("tai_quant_matmul");
+}
+
+static int quant_matmul_impl(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
+                             const float* scale, int64_t scale_len, const float* pertoken_scale, const void* bias,
+                             int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 0, "tai_quant_matmul: negative size");
   TAI_CHECK_ARG(x2_layout == TAI_LAYOUT_KN || x2_layout == TAI_LAYOUT_NK, "tai_quant_matmul: x2_layout");
   TAI_CHECK_ARG(out_dtype == TAI_DT_INT32 || out_dtype == TAI_DT_BF16 || out_dtype == TAI_DT_FP16 ||
@@ -1515,7 +1570,7 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
       if (!skinny_launch(g, x2_layout, p, st)) return launch_status("tai_quant_matmul (skinny LDS attribute)");
       return launch_status("tai_quant_matmul");
     }
-    const size_t need = tai_quant_matmul_workspace_size(m, k, n);
+    const size_t need = quant_matmul_ws_base(m, k, n);
     if (workspace == nullptr || ws_bytes < need) {
       set_error("tai_quant_matmul: workspace of %zu bytes, need %zu", ws_bytes, need);
       return TAI_ERR_WORKSPACE;
@@ -1541,7 +1596,7 @@ extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, i
       launch_cfg<SkinnyCfg>(g, x2_layout, st);
       return launch_status("tai_quant_matmul");
     }
-    const size_t need = tai_quant_matmul_workspace_size(m, k, n);
+    const size_t need = quant_matmul_ws_base(m, k, n);
     if (workspace == nullptr || ws_bytes < need) {
       set_error("tai_quant_matmul: workspace of %zu bytes, need %zu", ws_bytes, need);
       return TAI_ERR_WORKSPACE;
