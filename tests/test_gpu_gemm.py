@@ -190,3 +190,43 @@ def test_quant_matmul_int8_output(m, k, n, layout):
     assert_int8_close(out.cpu().numpy(), want)
     if k >= 256:
         assert (want == 127).any() and (want == -128).any()  # saturation is exercised
+
+
+# Multi-tensor npu_grouped_matmul: one x per group (group_list absent) with per-group weights, scales and
+# biases (split_item 0/1: one output per group, 2/3: concatenated), and one x with groups along M
+# returned per group (split_item 0/1).
+@pytest.mark.parametrize("split_item", [0, 1, 2, 3])
+def test_grouped_matmul_multi_tensor(split_item):
+    g = gen(23)
+    ms, k, n = [37, 0, 129], 256, 192
+    xs = [rand_i8((m, k), g) for m in ms]
+    ws = [rand_i8((k, n), g) for _ in ms]
+    scs = [uniform((n,), g, 1e-3, 1e-2) for _ in ms]
+    bis = [uniform((n,), g, -1, 1) for _ in ms]
+    pts = uniform((sum(ms),), g, 1e-3, 1e-2)
+    outs = torch.ops.npu.npu_grouped_matmul([x.to(DEV) for x in xs], [w.to(DEV) for w in ws],
+                                            scale=[s.to(DEV) for s in scs], bias=[b.to(DEV) for b in bis],
+                                            per_token_scale=[pts.to(DEV)], split_item=split_item,
+                                            output_dtype=torch.bfloat16)
+    wants, r0 = [], 0
+    for x, w, s, b, m in zip(xs, ws, scs, bis, ms):
+        wants.append(G.quant_matmul(x.numpy(), w.numpy(), s.numpy(), pts[r0:r0 + m].numpy(), b.numpy(), "bf16"))
+        r0 += m
+    if split_item in (2, 3):
+        assert len(outs) == 1
+        assert_close(f32np(outs[0]), np.concatenate(wants, 0))
+    else:
+        assert len(outs) == 3
+        for o, want in zip(outs, wants):
+            assert_close(f32np(o), want)
+
+
+def test_grouped_matmul_per_group_outputs():
+    g = gen(24)
+    x, w, counts = _gmm_case(g, 6, 400, 128, 256)
+    whole = torch.ops.npu.npu_grouped_matmul([x.to(DEV)], [w.to(DEV)], group_list=counts.to(DEV), split_item=3,
+                                             group_type=0, group_list_type=1, output_dtype=torch.int32)[0]
+    parts = torch.ops.npu.npu_grouped_matmul([x.to(DEV)], [w.to(DEV)], group_list=counts.tolist(), split_item=0,
+                                             group_type=0, group_list_type=1, output_dtype=torch.int32)
+    assert [p.shape[0] for p in parts] == counts.tolist()
+    torch.testing.assert_close(torch.cat(parts, 0), whole[:int(counts.sum())], rtol=0, atol=0)

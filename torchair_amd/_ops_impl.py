@@ -357,28 +357,65 @@ def _gmm_out_dtype(x, output_dtype):
     return dtype_of_code(code)
 
 
+def _gmm_group_rows(group_list, group_list_type, e):
+    """Host list of the rows of each group (cumulative ends or counts)."""
+    vals = [int(v) for v in (group_list.tolist() if isinstance(group_list, torch.Tensor) else group_list)]
+    _check(len(vals) == e, f"npu_grouped_matmul: group_list has {len(vals)} entries for {e} groups")
+    if group_list_type == 1:
+        return vals
+    out, prev = [], 0
+    for v in vals:
+        out.append(max(v - prev, 0))
+        prev = max(prev, v)
+    return out
+
+
+def _gmm_pairs(x, weight):
+    """Multi-tensor form: one x per group (group_list absent); weights as a list or one stacked tensor."""
+    ws = list(weight) if len(weight) > 1 else ([weight[0]] if weight[0].dim() == 2 else list(weight[0].unbind(0)))
+    _check(len(ws) == len(x), f"npu_grouped_matmul: {len(x)} x tensors need {len(x)} weights, got {len(ws)}")
+    return ws
+
+
 def _gmm_fake(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
               per_token_scale=None, group_list=None, activation_input=None, activation_quant_scale=None,
               activation_quant_offset=None, split_item=0, group_type=None, group_list_type=0, act_type=0,
               tuning_config=None, output_dtype=None):
+    od = _gmm_out_dtype(x, output_dtype)
+    dev = x[0].device
+    if group_list is None:  # per-group pairs
+        ws = _gmm_pairs(x, weight)
+        outs = [torch.empty([xi.shape[0], wi.shape[-1]], dtype=od, device=dev) for xi, wi in zip(x, ws)]
+        if split_item in (2, 3):
+            return [torch.empty([sum(o.shape[0] for o in outs), outs[0].shape[1]], dtype=od, device=dev)]
+        return outs
     n = weight[0].shape[-1]
     m = x[0].shape[0]
-    return [torch.empty([m, n], dtype=_gmm_out_dtype(x, output_dtype), device=x[0].device)]
+    if split_item in (0, 1):
+        _check(not isinstance(group_list, torch.Tensor),
+               "npu_grouped_matmul: split_item 0/1 with groups along M need a list-valued group_list to trace "
+               "(the output shapes depend on it)")
+        rows = _gmm_group_rows(group_list, group_list_type, len(group_list))
+        return [torch.empty([r, n], dtype=od, device=dev) for r in rows]
+    return [torch.empty([m, n], dtype=od, device=dev)]
 
 
 def _gmm_cuda(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=None, antiquant_offset=None,
               per_token_scale=None, group_list=None, activation_input=None, activation_quant_scale=None,
               activation_quant_offset=None, split_item=0, group_type=None, group_list_type=0, act_type=0,
               tuning_config=None, output_dtype=None):
-    """npu_grouped_matmul int8 path, split_item 2/3, group_type 0 (grouped_matmul.py:210-365)."""
-    _check(len(x) == 1, "npu_grouped_matmul: a single x tensor (split_item 2/3) is supported")
-    _check(split_item in (2, 3), "npu_grouped_matmul: split_item must be 2 or 3")
-    _check(group_type in (None, 0), "npu_grouped_matmul: only group_type 0 (groups along M) is supported")
-    _check(group_list is not None, "npu_grouped_matmul: group_list is required")
+    """npu_grouped_matmul int8 path (grouped_matmul.py:210-365): one x with groups along M (group_type 0,
+    group_list given), or one x per group (group_list absent); split_item 0/1 return one output per group,
+    2/3 one output over all rows."""
+    _check(split_item in (0, 1, 2, 3), "npu_grouped_matmul: split_item must be 0, 1, 2 or 3")
     _check(not (offset or antiquant_scale or antiquant_offset or activation_input or activation_quant_scale
                 or activation_quant_offset), "npu_grouped_matmul: offset/antiquant/activation inputs are not supported")
     _check(act_type in (None, 0), "npu_grouped_matmul: act_type must be 0")
     _check(group_list_type in (0, 1), "npu_grouped_matmul: group_list_type must be 0 (cumsum) or 1 (count)")
+    if group_list is None:
+        return _gmm_pairs_cuda(x, weight, bias, scale, per_token_scale, split_item, output_dtype)
+    _check(len(x) == 1, "npu_grouped_matmul: with a group_list, x is a single [M, K] tensor")
+    _check(group_type in (None, 0), "npu_grouped_matmul: only group_type 0 (groups along M) is supported")
     xt = x[0]
     _on_gpu(xt, *weight)
     _check(xt.dtype == torch.int8, "npu_grouped_matmul: only the int8 (W8A8) path is supported")
@@ -423,13 +460,58 @@ def _gmm_cuda(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=
     _check(out_dtype == torch.int32 or sc is not None, "npu_grouped_matmul: floating output needs scale")
     xc = xt.contiguous()
     out = torch.empty([m, n], dtype=out_dtype, device=xt.device)
-    if m == 0 or n == 0:
+    if m > 0 and n > 0:
+        ws_bytes = _lib.query("tai_grouped_matmul_workspace_size", m, n, e)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xt.device)
+        _lib.call("tai_grouped_matmul", _p(xc), _p(wl), m, k, n, e, layout, _p(gl), int(group_list_type), _p(sc),
+                  _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _p(ws), ws_bytes, _stream(xc))
+    if split_item in (2, 3):
         return [out]
-    ws_bytes = _lib.query("tai_grouped_matmul_workspace_size", m, n, e)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xt.device)
-    _lib.call("tai_grouped_matmul", _p(xc), _p(wl), m, k, n, e, layout, _p(gl), int(group_list_type), _p(sc),
-              _p(pts), _p(bi), bias_dt, _DT[out_dtype], _p(out), _p(ws), ws_bytes, _stream(xc))
-    return [out]
+    # one output per group: the rows of each group (the split needs the group sizes on the host)
+    rows = _gmm_group_rows(group_list, group_list_type, e)
+    outs, r0 = [], 0
+    for r in rows:
+        r = min(r, m - r0)
+        outs.append(out[r0:r0 + r].clone())
+        r0 += r
+    return outs
+
+
+def _gmm_pairs_cuda(x, weight, bias, scale, per_token_scale, split_item, output_dtype):
+    """One x per group: y_i = x_i @ w_i with group i's scale and bias; per_token_scale holds the rows of
+    all groups in order. Each pair runs the dense W8A8 GEMM."""
+    ws = _gmm_pairs(x, weight)
+    g = len(x)
+    out_dtype = _gmm_out_dtype(x, output_dtype)
+    _check(out_dtype in (torch.int32, torch.bfloat16, torch.float16, torch.float32),
+           "npu_grouped_matmul: output_dtype must be int32, bf16, fp16 or fp32 for int8 inputs")
+
+    def per_group(lst, name):
+        if not lst:
+            return [None] * g
+        if len(lst) == g:
+            return list(lst)
+        _check(len(lst) == 1 and lst[0].dim() == 2 and lst[0].shape[0] == g,
+               f"npu_grouped_matmul: {name} must hold one tensor per group or one stacked [G, N] tensor")
+        return list(lst[0].unbind(0))
+
+    scs, bis = per_group(scale, "scale"), per_group(bias, "bias")
+    pts_all = _f32(per_token_scale[0]) if per_token_scale else None
+    _check(out_dtype == torch.int32 or all(s is not None for s in scs), "npu_grouped_matmul: floating output needs scale")
+    outs, r0 = [], 0
+    for xi, wi, si, bi in zip(x, ws, scs, bis):
+        _check(xi.dtype == torch.int8 and wi.dtype == torch.int8, "npu_grouped_matmul: only the int8 (W8A8) path is "
+                                                                  "supported")
+        _check(wi.dim() == 2 and xi.shape[-1] == wi.shape[0], "npu_grouped_matmul: x_i [M_i, K] needs w_i [K, N_i]")
+        rows = xi.numel() // xi.shape[-1] if xi.shape[-1] else 0
+        pts = pts_all[r0:r0 + rows] if pts_all is not None else None
+        r0 += rows
+        one = torch.ones(1, device=xi.device)
+        outs.append(_qmm_cuda(xi, wi, si if si is not None else one, pertoken_scale=pts, bias=bi,
+                              output_dtype=out_dtype))
+    if split_item in (2, 3):
+        return [torch.cat([o.reshape(-1, o.shape[-1]) for o in outs], 0)]
+    return outs
 
 
 _define("npu", "npu_grouped_matmul(Tensor[] x, Tensor[] weight, " + _GMM_TAIL.format(gl="Tensor? group_list=None"),
