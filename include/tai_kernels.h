@@ -336,6 +336,51 @@ int tai_fia_prefill(const void* q, const void* k, const void* v, int64_t b, int6
 size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv);
 
 /* ---------------------------------------------------------------------------------------
+ * npu_fused_infer_attention_score, general path (same reference interface: ge.FusedInferAttentionScore
+ * emitted by python/torchair/_ge_concrete_graph/ge_converter/custom/fused_infer_attention_score.py:4-109;
+ * atten_mask / sparse_mode / query_rope / key_rope: prototype experiment_ops.h:3878-3965):
+ * an explicit attention mask (sparse_mode 0/1), an MLA latent cache in bf16 or fp16, or head dims
+ * the tiled kernels do not take. One wave per query row; fp32 arithmetic throughout.
+ * query = [q1 (dk1) | q2 (dk2)], key = [k1 (dk1) | k2 (dk2)], value = v (dv <= 512); all of dtype.
+ * Strides are elements (batch, pos, head) for q1 / q2 / out; for k1 / k2 / v (batch, pos, kv head),
+ * or with a block table (block, slot, kv head): token t of sequence b at block
+ * block_table[b * max_blocks + t / block_size], slot t % block_size.
+ * mask: NULL or bytes with element (batch, query, kv) at the given strides (0 to broadcast); nonzero
+ * = masked out. The band rule of tai_fia_prefill (mask_origin, pre_tokens, next_tokens) applies too.
+ * A query that sees nothing gets 0 and lse -inf; rows at or past seq_lens_q[b] are 0.
+ * lse: NULL or [b, hq, s_q] fp32 (natural-log logsumexp of the scaled scores).
+ * ------------------------------------------------------------------------------------- */
+typedef struct tai_fia_general_args {
+  int dtype;
+  int dk1, dk2, dv;
+  int64_t b, s_q, s_kv, hq, hkv;
+  const void* q1;
+  int64_t q1_strides[3];
+  const void* q2;
+  int64_t q2_strides[3];
+  const void* k1;
+  int64_t k1_strides[3];
+  const void* k2;
+  int64_t k2_strides[3];
+  const void* v;
+  int64_t v_strides[3];
+  const int32_t* block_table;
+  int64_t max_blocks;
+  int64_t block_size;
+  const int64_t* seq_lens_q;
+  const int64_t* seq_lens_kv;
+  const uint8_t* mask;
+  int64_t mask_strides[3];
+  int64_t mask_origin;
+  int64_t pre_tokens, next_tokens;
+  float scale;
+  void* out;
+  int64_t out_strides[3];
+  float* lse;
+} tai_fia_general_args;
+int tai_fia_general(const tai_fia_general_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache
  * (query_rope/key_rope given, key_antiquant_mode 1 = per-token scale).
  * q_nope: [b, hq, dn] bf16, q_rope: [b, hq, dr] bf16.

@@ -485,12 +485,14 @@ def band_mask(lq: int, lk: int, origin: int, pre: int, nxt: int) -> np.ndarray:
     return ok
 
 
-def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None):
+def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None, mask=None):
     """npu_fused_infer_attention_score, dense prefill. q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D].
 
     causal 1 (sparse_mode 3, right-down): query i sees kv j <= i + (Lkv - Lq); causal 2
     (sparse_mode 2, left-up): j <= i; 0: no mask. band = (origin, pre, next) replaces causal with
-    band_mask's rule. Rows at or past Lq are zero.
+    band_mask's rule. mask: an explicit atten_mask [B or 1, Sq, Skv] (nonzero = masked out, the
+    converter's atten_mask input, .../custom/fused_infer_attention_score.py:4-109), combined with the
+    rest. Rows at or past Lq are zero.
     Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
     """
     q = np.asarray(q, F32)
@@ -504,22 +506,26 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=No
         lk = skv if seq_kv is None else int(seq_kv[b])
         ii = np.arange(lq)[:, None]
         jj = np.arange(lk)[None, :]
-        mask = None
+        vis = None
         if band is not None:
-            mask = band_mask(lq, lk, *band)
+            vis = band_mask(lq, lk, *band)
         elif causal == 1:
-            mask = jj <= ii + (lk - lq)
+            vis = jj <= ii + (lk - lq)
         elif causal == 2:
-            mask = jj <= ii
+            vis = jj <= ii
+        if mask is not None:
+            mb = np.asarray(mask)
+            mb = mb[0 if mb.shape[0] == 1 else b, :lq, :lk] == 0
+            vis = mb if vis is None else (vis & mb)
         for h in range(hq):
             o, l = _softmax_attend(q[b, :lq, h], np.asarray(k[b, :lk, h // g], F32),
-                                   np.asarray(v[b, :lk, h // g], F32), scale, mask)
+                                   np.asarray(v[b, :lk, h // g], F32), scale, vis)
             out[b, :lq, h] = o
             lse[b, h, :lq] = l
     return out, lse
 
 
-def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float):
+def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float, mask=None):
     """npu_fused_infer_attention_score with a block table and several query tokens per sequence
     (chunked prefill / multi-token decode). q [B,Sq,Hq,D]; caches [blocks, bs, Hkv, D]; token t of
     sequence b at cache[block_table[b, t // bs], t % bs] (the paged rule of paged_decode_attention);
@@ -535,7 +541,7 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
         pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
         k[b, :L] = np.asarray(k_cache[pages], F32).reshape(-1, hkv, d)[:L]
         v[b, :L] = np.asarray(v_cache[pages], F32).reshape(-1, hkv, d)[:L]
-    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band)
+    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask)
 
 
 def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_lens, scale: float):

@@ -407,3 +407,72 @@ def test_prefill_fp16_rising_logits_take_the_rescaling_pass():
     assert np.isfinite(f32np(out)).all()
     assert_close(f32np(out), want)
     _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)
+
+
+# Explicit atten_mask (sparse_mode 1, and 0 with a band), head dims the tiled kernels do not take, and an
+# MLA latent in bf16: the general kernel.
+@pytest.mark.parametrize("sparse_mode,mask_shape,band", [(1, "B1SS", None), (0, "SS", (0, 60, 5)), (0, "BSS", None)])
+def test_prefill_explicit_mask(sparse_mode, mask_shape, band):
+    gen = torch.Generator().manual_seed(119)
+    b, s, hq, hkv, d = 2, 150, 8, 2, 128
+    q = torch.randn(b, s, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=gen).to(torch.bfloat16)
+    full = torch.rand(b, s, s, generator=gen) < 0.3
+    full[:, 5, :] = True  # a query that sees nothing
+    mask = {"B1SS": full[:, None], "SS": full[0], "BSS": full}[mask_shape]
+    lq, lkv = torch.tensor([150, 90]), torch.tensor([150, 120])
+    kw = dict(atten_mask=mask.to(DEV))
+    if band is not None:
+        kw.update(pre_tokens=band[1], next_tokens=band[2])
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lq, lkv, hq, hkv, "BSND", sparse_mode, lse=True, **kw)
+    m3 = mask.numpy().reshape(-1, s, s)
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lq.numpy(), lkv.numpy(), 0, 1.0 / math.sqrt(d),
+                                   band=band, mask=m3.astype(np.uint8))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)
+
+
+@pytest.mark.parametrize("d", [96, 192])
+def test_prefill_other_head_dims(d):
+    gen = torch.Generator().manual_seed(120)
+    b, s, hq, hkv = 2, 70, 4, 2
+    q = torch.randn(b, s, hq, d, generator=gen).half()
+    k = torch.randn(b, s, hkv, d, generator=gen).half()
+    v = torch.randn(b, s, hkv, d, generator=gen).half()
+    lens = torch.tensor([70, 33])
+    out, lse = _prefill(q.to(DEV), k.to(DEV), v.to(DEV), lens, lens, hq, hkv, "BSND", 3, lse=True)
+    want, wl = G.prefill_attention(f32np(q), f32np(k), f32np(v), lens.numpy(), lens.numpy(), 1, 1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(b, hq, s), wl)
+
+
+def test_paged_explicit_mask():
+    lq, lkv = [3, 1], [200, 77]
+    hq, hkv, d, bs = 8, 2, 128, 64
+    q, k4, v4, bt = _paged_seq_case(lq, lkv, hq, hkv, d, bs, 121)
+    gen = torch.Generator().manual_seed(122)
+    mask = torch.rand(2, 1, 3, 200, generator=gen) < 0.5
+    out, lse = _paged_seq(q, k4, v4, bt, lq, lkv, hq, hkv, bs, "BSH", "BSH", sparse_mode=1, atten_mask=mask.to(DEV))
+    want, wl = G.paged_prefill_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lq, lkv,
+                                         (0, 2147483647, 2147483647), 1.0 / math.sqrt(d),
+                                         mask=mask[:, 0].numpy().astype(np.uint8))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(2, hq, 3), wl)
+
+
+def test_mla_bf16_latent():
+    lens, h, bs = [300, 65, 1], 16, 64
+    qn, qr, ckv, cs, kr, bt = _mla_case(lens, h, bs, 123)
+    lat = (torch.randn(ckv.shape, generator=torch.Generator().manual_seed(124)) * 0.5).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(192)
+    out, lse = torch.ops.air.npu_fused_infer_attention_score(
+        qn.to(DEV), lat.to(DEV), lat.to(DEV), query_rope=qr.to(DEV), key_rope=kr.to(DEV), block_table=bt.to(DEV),
+        actual_seq_lengths_kv=torch.tensor(lens, device=DEV), num_heads=h, num_key_value_heads=1,
+        input_layout="BSND", block_size=bs, scale=scale, softmax_lse_flag=True)
+    assert out.shape == (len(lens), 1, h, 512) and out.dtype == torch.bfloat16
+    ones = np.ones(cs.shape, np.float32)
+    want, wl = G.mla_decode_attention(f32np(qn[:, 0]), f32np(qr[:, 0]), f32np(lat[:, :, 0]), ones, f32np(kr[:, :, 0]),
+                                      bt.numpy(), lens, scale)
+    assert_close(f32np(out[:, 0]), want)
+    _assert_lse(lse.reshape(len(lens), h).cpu().numpy(), wl)

@@ -387,3 +387,24 @@ def test_quant_matmul_int8_output_rule():
     v = acc * 0.0625 + off.astype(np.float64)
     want = np.clip(np.round(v), -128, 127)  # numpy rounds half to even, like rint
     np.testing.assert_array_equal(got, want.astype(np.int8))
+
+
+def test_explicit_mask_rule():
+    q = RNG.standard_normal((2, 5, 2, 4)).astype(np.float32)
+    k = RNG.standard_normal((2, 7, 1, 4)).astype(np.float32)
+    v = RNG.standard_normal((2, 7, 1, 4)).astype(np.float32)
+    big = 2147483647
+    # the lower-triangle mask (1 above the diagonal) equals the top-left causal rule
+    tri = np.triu(np.ones((5, 7), np.uint8), 1)[None]
+    o1, l1 = G.prefill_attention(q, k, v, None, None, 0, 0.4, mask=tri)
+    o2, l2 = G.prefill_attention(q, k, v, None, None, 2, 0.4)
+    np.testing.assert_allclose(o1, o2, rtol=1e-6)
+    np.testing.assert_allclose(l1, l2, rtol=1e-6)
+    # a mask leaving one token per query returns that token's value row, per batch
+    one = np.ones((2, 5, 7), np.uint8)
+    pick = RNG.integers(0, 7, (2, 5))
+    for b in range(2):
+        one[b, np.arange(5), pick[b]] = 0
+    o3, _ = G.prefill_attention(q, k, v, None, None, 0, 0.4, band=(0, big, big), mask=one)
+    for b in range(2):
+        np.testing.assert_allclose(o3[b, :, 0], v[b, pick[b], 0], rtol=1e-6)

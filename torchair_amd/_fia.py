@@ -17,6 +17,7 @@ so a captured graph replays correctly with new lengths.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -210,7 +211,7 @@ def fia_cuda(query, key, value, **kw):
     seq_kv = _lens_tensor(kw.get("actual_seq_lengths_kv"), query.device)
     seq_q = _lens_tensor(kw.get("actual_seq_lengths"), query.device)
 
-    mask_origin, pre, nxt = _mask_params(kw)
+    mask_origin, pre, nxt, explicit = _mask_params(kw)
 
     if block_table is not None:
         _check(ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql,
@@ -222,8 +223,11 @@ def fia_cuda(query, key, value, **kw):
         bt = block_table.to(torch.int32).contiguous()
         _check(bt.dim() == 2 and bt.size(0) == b, "npu_fused_infer_attention_score: block_table must be [B, max_blocks]")
         if kw.get("query_rope") is not None:
-            _check(s == 1, "npu_fused_infer_attention_score: MLA serves one query token per sequence")
-            return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
+            if key.dtype == torch.int8:
+                _check(s == 1, "npu_fused_infer_attention_score: MLA serves one query token per sequence")
+                return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
+            return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
+                                scale, mask_origin, pre, nxt, explicit, stream)
         dt = _half_code(query, key, value)
         d = _value_d(block_table, value, query, ql, n_kv)
         if key.dim() == 3:
@@ -239,6 +243,11 @@ def fia_cuda(query, key, value, **kw):
                "npu_fused_infer_attention_score: key/value caches must share shape and a dense head dim")
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
+        if explicit or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)):
+            _check(ql != "TND", "npu_fused_infer_attention_score: the general path takes BSH/BSND/BNSD queries")
+            kstr = [sb, ss, sh]
+            return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, kstr, kstr,
+                                 bt, bs, seq_q, seq_kv, mask_origin, pre, nxt, explicit, kw, scale, stream)
         # one query token that the mask leaves the whole prefix: the decode kernel
         if s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0)):
             q = query.contiguous()
@@ -263,6 +272,10 @@ def fia_cuda(query, key, value, **kw):
            "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
     dt = _half_code(query, key, value)
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
+    if explicit or d not in (64, 128) or _value_d(None, value, query, ql, n_kv) != d:
+        return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt,
+                             _strides_bshd(key, ql, n_kv), _strides_bshd(value, ql, n_kv), None, 0, seq_q, seq_kv,
+                             mask_origin, pre, nxt, explicit, kw, scale, stream)
     s_kv = key.size(2) if ql == "BNSD" else key.size(1)
     qs = _strides_bshd(query, ql, hq)
     ks = _strides_bshd(key, ql, n_kv)
@@ -282,22 +295,108 @@ def _mask_params(kw):
     sparse_mode 0: band of pre/next tokens from the top-left (no bound by default); 2: top-left causal;
     3: bottom-right causal; 4: band of pre/next tokens from the bottom-right. Modes 2-4 take the fixed
     compressed triangle as atten_mask (torch_npu's 2048 x 2048 convention); its contents are implied by
-    the mode and not read. An explicit mask (mode 0 or 1) is not supported."""
+    the mode and not read. Modes 0 and 1 read an explicit atten_mask (nonzero = masked out; mode 0 also
+    applies the band), which the general kernel serves. Returns (origin, pre, next, explicit)."""
     sparse_mode = int(kw.get("sparse_mode", 0))
     pre = int(kw.get("pre_tokens", _NO_BOUND))
     nxt = int(kw.get("next_tokens", _NO_BOUND))
+    explicit = kw.get("atten_mask") is not None and sparse_mode in (0, 1)
     if sparse_mode == 0:
-        _check(kw.get("atten_mask") is None,
-               "npu_fused_infer_attention_score: explicit atten_mask with sparse_mode 0 is not supported; use "
-               "sparse_mode 2/3 for causal masks or pre_tokens/next_tokens for a band")
-        return 0, pre, nxt
+        return 0, pre, nxt, explicit
+    if sparse_mode == 1:
+        _check(explicit, "npu_fused_infer_attention_score: sparse_mode 1 needs atten_mask")
+        return 0, _NO_BOUND, _NO_BOUND, True
     if sparse_mode == 2:
-        return 0, _NO_BOUND, 0
+        return 0, _NO_BOUND, 0, False
     if sparse_mode == 3:
-        return 1, _NO_BOUND, 0
+        return 1, _NO_BOUND, 0, False
     if sparse_mode == 4:
-        return 1, pre, nxt
-    raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported (0, 2, 3, 4)")
+        return 1, pre, nxt, False
+    raise RuntimeError(f"npu_fused_infer_attention_score: sparse_mode {sparse_mode} is not supported (0-4)")
+
+
+def _mask_bytes(mask, b, s_q):
+    """An explicit atten_mask as bytes (nonzero = masked out) with (batch, query, kv) strides; a leading
+    batch dim of 1, or none, broadcasts. Shapes [Sq, Skv], [B, Sq, Skv], [B, 1, Sq, Skv]."""
+    m = mask if mask.dtype in (torch.bool, torch.uint8, torch.int8) else (mask != 0)
+    m = m.to(torch.uint8) if m.dtype == torch.bool else m.view(torch.uint8) if m.dtype == torch.int8 else m
+    if m.dim() == 4:
+        _check(m.size(1) == 1, "npu_fused_infer_attention_score: atten_mask [B, N, Sq, Skv] needs N == 1")
+        m = m[:, 0]
+    if m.dim() == 2:
+        m = m.unsqueeze(0)
+    _check(m.dim() == 3 and m.size(0) in (1, b) and m.size(1) >= s_q,
+           "npu_fused_infer_attention_score: atten_mask must be [Sq, Skv], [B, Sq, Skv] or [B, 1, Sq, Skv]")
+    m = m.contiguous()
+    st = [0 if m.size(0) == 1 else m.stride(0), m.stride(1), m.stride(2)]
+    return m, st
+
+
+def _general_args(dt, b, s_q, s_kv, hq, n_kv, dk1, dk2, dv, q1, q1s, q2, q2s, k1, k1s, k2, k2s, v, vs, bt, bs,
+                  seq_q, seq_kv, mask, mask_st, mask_origin, pre, nxt, scale, out, os_, lse):
+    a = _lib.FiaGeneralArgs()
+    a.dtype, a.dk1, a.dk2, a.dv = dt, dk1, dk2, dv
+    a.b, a.s_q, a.s_kv, a.hq, a.hkv = b, s_q, s_kv, hq, n_kv
+    a.q1, a.q1_strides = q1.data_ptr(), _lib._I64x3(*q1s)
+    a.q2, a.q2_strides = (q2.data_ptr() if q2 is not None else None), _lib._I64x3(*(q2s or [0, 0, 0]))
+    a.k1, a.k1_strides = k1.data_ptr(), _lib._I64x3(*k1s)
+    a.k2, a.k2_strides = (k2.data_ptr() if k2 is not None else None), _lib._I64x3(*(k2s or [0, 0, 0]))
+    a.v, a.v_strides = v.data_ptr(), _lib._I64x3(*vs)
+    a.block_table = bt.data_ptr() if bt is not None else None
+    a.max_blocks = bt.size(1) if bt is not None else 0
+    a.block_size = bs
+    a.seq_lens_q = seq_q.data_ptr() if seq_q is not None else None
+    a.seq_lens_kv = seq_kv.data_ptr() if seq_kv is not None else None
+    a.mask = mask.data_ptr() if mask is not None else None
+    a.mask_strides = _lib._I64x3(*(mask_st or [0, 0, 0]))
+    a.mask_origin, a.pre_tokens, a.next_tokens, a.scale = mask_origin, pre, nxt, scale
+    a.out, a.out_strides = out.data_ptr(), _lib._I64x3(*os_)
+    a.lse = lse.data_ptr() if lse is not None else None
+    return a
+
+
+def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, ks, vs, bt, bs, seq_q, seq_kv,
+                  mask_origin, pre, nxt, explicit, kw, scale, stream):
+    """The general kernel for GQA/MHA: explicit masks and head dims the tiled kernels do not take."""
+    b, s_q, hq, _ = _bsnd(query, ql, num_heads)
+    dv = _value_d(bt, value, query, ql, n_kv)
+    mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
+    s_kv = (bt.size(1) * bs) if bt is not None else (key.size(2) if ql == "BNSD" else key.size(1))
+    if mask is not None:
+        _check(mask.size(2) >= (max(seq_kv.tolist()) if seq_kv is not None else s_kv),
+               "npu_fused_infer_attention_score: atten_mask covers fewer kv positions than the sequences hold")
+    a = _general_args(dt, b, s_q, s_kv, hq, n_kv, d, 0, dv, query, _strides_bshd(query, ql, hq), None, None,
+                      key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale,
+                      out, _strides_bshd(out, ql, hq), lse if want_lse else None)
+    _lib.call("tai_fia_general", ctypes.byref(a), stream)
+    return out, lse
+
+
+def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv, scale,
+                 mask_origin, pre, nxt, explicit, stream):
+    """MLA with a bf16 / fp16 latent cache: key = [latent | key_rope], value = latent, one kv head."""
+    q_rope, k_rope = kw["query_rope"], kw.get("key_rope")
+    _check(k_rope is not None, "npu_fused_infer_attention_score: MLA needs key_rope")
+    _check(n_kv == 1, "npu_fused_infer_attention_score: MLA latent cache has one kv head")
+    _check(ql in ("BSH", "BSND", "BNSD"), "npu_fused_infer_attention_score: MLA takes BSH/BSND/BNSD queries")
+    dt = _half_code(query, key, value)
+    _check(q_rope.dtype == query.dtype and k_rope.dtype == query.dtype,
+           "npu_fused_infer_attention_score: MLA query_rope/key_rope must have the query's dtype")
+    b, s_q, hq, dn = _bsnd(query, ql, num_heads)
+    dr = _bsnd(q_rope, ql, num_heads)[3]
+    nblk = key.size(0)
+    kc = key.reshape(nblk, -1, dn)
+    bs = kc.size(1)
+    kr = k_rope.reshape(nblk, bs, dr)
+    _check(kc.stride(-1) == 1 and kr.stride(-1) == 1, "npu_fused_infer_attention_score: caches need a dense last dim")
+    mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
+    kst = [kc.stride(0), kc.stride(1), 0]
+    a = _general_args(dt, b, s_q, bt.size(1) * bs, hq, 1, dn, dr, dn, query, _strides_bshd(query, ql, hq), q_rope,
+                      _strides_bshd(q_rope, ql, hq), kc, kst, kr, [kr.stride(0), kr.stride(1), 0], kc, kst, bt, bs,
+                      seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale, out, _strides_bshd(out, ql, hq),
+                      lse if want_lse else None)
+    _lib.call("tai_fia_general", ctypes.byref(a), stream)
+    return out, lse
 
 
 def _half_code(query, key, value) -> int:

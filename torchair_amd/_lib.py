@@ -18,6 +18,23 @@ DT_NONE = -1
 LAYOUT_KN, LAYOUT_NK = 0, 1
 
 _P = c_void_p
+_I64x3 = c_int64 * 3
+
+
+class FiaGeneralArgs(ctypes.Structure):
+    """tai_fia_general_args (include/tai_kernels.h)."""
+    _fields_ = [("dtype", c_int), ("dk1", c_int), ("dk2", c_int), ("dv", c_int),
+                ("b", c_int64), ("s_q", c_int64), ("s_kv", c_int64), ("hq", c_int64), ("hkv", c_int64),
+                ("q1", _P), ("q1_strides", _I64x3), ("q2", _P), ("q2_strides", _I64x3),
+                ("k1", _P), ("k1_strides", _I64x3), ("k2", _P), ("k2_strides", _I64x3),
+                ("v", _P), ("v_strides", _I64x3),
+                ("block_table", _P), ("max_blocks", c_int64), ("block_size", c_int64),
+                ("seq_lens_q", _P), ("seq_lens_kv", _P),
+                ("mask", _P), ("mask_strides", _I64x3), ("mask_origin", c_int64),
+                ("pre_tokens", c_int64), ("next_tokens", c_int64), ("scale", c_float),
+                ("out", _P), ("out_strides", _I64x3), ("lse", _P)]
+
+
 _SIGS = {
     "tai_last_error": (c_char_p, []),
     "tai_abi_version": (c_int, []),
@@ -74,6 +91,7 @@ _SIGS = {
     "tai_kv_rmsnorm_rope_cache": (
         c_int, [_P, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int, c_int, c_float, _P, c_int, _P, c_int, c_int64,
                 c_int64, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tai_fia_general": (c_int, [ctypes.POINTER(FiaGeneralArgs), _P]),
     "tai_fia_mla_decode_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int]),
     "tai_fia_mla_decode": (
         c_int, [_P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_float, _P, _P, _P,

@@ -1,0 +1,158 @@
+// npu_fused_infer_attention_score, general path: an explicit attention mask, a bf16 / fp16 MLA
+// latent, or head dims the tiled kernels do not take. One wave per (sequence, query head, query
+// row); a 64-token chunk of keys puts one token on each lane (its score is a dot product against the
+// query, held in LDS as fp32), the chunk's softmax statistics are wave reductions, and the value rows
+// are accumulated with the lane owning value dims lane, lane + 64, ... Every product and sum is fp32.
+#include "common.h"
+
+namespace tai {
+namespace {
+
+constexpr int kGenWaves = 4;
+constexpr int kGenMaxDk = 640;   // query/key dims (k1 + k2)
+constexpr int kGenMaxDv = 512;   // value dims
+constexpr int kGenDvPerLane = kGenMaxDv / 64;
+
+__device__ __forceinline__ float half_to_f32(uint16_t v, bool f16) { return f16 ? f16_to_f32(v) : bf16_to_f32(v); }
+
+struct GenArgs {
+  tai_fia_general_args a;
+  bool f16;
+};
+
+__device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const int64_t* st, int64_t b, int64_t tok, int kvh) {
+  if (a.block_table) {
+    const int64_t blk = a.block_table[b * a.max_blocks + tok / a.block_size];
+    return blk * st[0] + (tok % a.block_size) * st[1] + kvh * st[2];
+  }
+  return b * st[0] + tok * st[1] + kvh * st[2];
+}
+
+__global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga) {
+  const tai_fia_general_args& a = ga.a;
+  const bool f16 = ga.f16;
+  __shared__ float qs[kGenWaves][kGenMaxDk];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // (b, h, i), i fastest; the launch's last workgroup may hold waves past the end, which run item 0
+  // to the barrier and then stop
+  const int64_t item0 = static_cast<int64_t>(blockIdx.x) * kGenWaves + w;
+  const bool in_range = item0 < a.b * a.hq * a.s_q;
+  const int64_t item = in_range ? item0 : 0;
+  const int64_t i = item % a.s_q, h = (item / a.s_q) % a.hq, b = item / (a.s_q * a.hq);
+  const int kvh = static_cast<int>(h / (a.hq / a.hkv));
+  const int64_t lq = a.seq_lens_q ? a.seq_lens_q[b] : a.s_q;
+  const int64_t lk = a.seq_lens_kv ? a.seq_lens_kv[b] : a.s_kv;
+  uint16_t* op = static_cast<uint16_t*>(a.out) + b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
+  const int dk = a.dk1 + a.dk2;
+  // the query as fp32 in this wave's LDS row
+  {
+    const uint16_t* q1 = static_cast<const uint16_t*>(a.q1) + b * a.q1_strides[0] + i * a.q1_strides[1] + h * a.q1_strides[2];
+    const uint16_t* q2 = a.q2 ? static_cast<const uint16_t*>(a.q2) + b * a.q2_strides[0] + i * a.q2_strides[1] +
+                                    h * a.q2_strides[2]
+                              : nullptr;
+    for (int d = lane; d < dk; d += 64) qs[w][d] = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
+  }
+  __syncthreads();  // (each wave reads only its own row; the barrier orders the LDS writes)
+  if (!in_range) return;
+  // visible kv range of query i
+  const int64_t off = a.mask_origin ? lk - lq : 0;
+  const int64_t hi = i < lq ? imin64(lk, i + off + a.next_tokens + 1) : 0;
+  const int64_t lo = imax64(0, i + off - a.pre_tokens);
+  float m = -INFINITY, l = 0.0f;
+  float o[kGenDvPerLane];
+#pragma unroll
+  for (int e = 0; e < kGenDvPerLane; ++e) o[e] = 0.0f;
+  const uint16_t* k1 = static_cast<const uint16_t*>(a.k1);
+  const uint16_t* k2 = static_cast<const uint16_t*>(a.k2);
+  const uint16_t* vv = static_cast<const uint16_t*>(a.v);
+  for (int64_t t0 = lo; t0 < hi; t0 += 64) {
+    const int64_t j = t0 + lane;
+    bool valid = j < hi;
+    if (valid && a.mask) valid = a.mask[b * a.mask_strides[0] + i * a.mask_strides[1] + j * a.mask_strides[2]] == 0;
+    float s = -INFINITY;
+    if (valid) {
+      float acc = 0.0f;
+      const uint16_t* kr = k1 + gen_row(a, a.k1_strides, b, j, kvh);
+      for (int d = 0; d < a.dk1; d += 8) {
+        const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
+        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc += half_to_f32(static_cast<uint16_t>(wd[q] & 0xffffu), f16) * qs[w][d + 2 * q];
+          acc += half_to_f32(static_cast<uint16_t>(wd[q] >> 16), f16) * qs[w][d + 2 * q + 1];
+        }
+      }
+      if (a.dk2) {
+        const uint16_t* kr2 = k2 + gen_row(a, a.k2_strides, b, j, kvh);
+        for (int d = 0; d < a.dk2; ++d) acc += half_to_f32(kr2[d], f16) * qs[w][a.dk1 + d];
+      }
+      s = acc * a.scale;
+    }
+    const float mc = wave_max(s);
+    if (mc == -INFINITY) continue;  // nothing visible in this chunk
+    const float m_new = fmaxf(m, mc);
+    const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+    const float p = valid ? expf(s - m_new) : 0.0f;
+    l = l * alpha + wave_sum(p);
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) o[e] *= alpha;
+    const int64_t nj = imin64(64, hi - t0);
+    for (int jj = 0; jj < nj; ++jj) {
+      const float pj = __shfl(p, jj, 64);
+      if (pj == 0.0f) continue;  // masked (wave-uniform)
+      const uint16_t* vr = vv + gen_row(a, a.v_strides, b, t0 + jj, kvh);
+#pragma unroll
+      for (int e = 0; e < kGenDvPerLane; ++e) {
+        const int d = lane + 64 * e;
+        if (d < a.dv) o[e] += pj * half_to_f32(vr[d], f16);
+      }
+    }
+    m = m_new;
+  }
+  const bool live = i < lq && l > 0.0f;
+  const float inv = live ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int e = 0; e < kGenDvPerLane; ++e) {
+    const int d = lane + 64 * e;
+    if (d < a.dv) {
+      const float r = o[e] * inv;
+      op[d] = f16 ? f32_to_f16(r) : f32_to_bf16(r);
+    }
+  }
+  if (a.lse && lane == 0 && i < a.s_q) a.lse[(b * a.hq + h) * a.s_q + i] = live ? m + logf(l) : -INFINITY;
+}
+
+}  // namespace
+}  // namespace tai
+
+using namespace tai;
+
+extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
+  TAI_CHECK_ARG(args != nullptr, "tai_fia_general: null arguments");
+  const tai_fia_general_args& a = *args;
+  TAI_CHECK_ARG(a.dtype == TAI_DT_BF16 || a.dtype == TAI_DT_FP16, "tai_fia_general: dtype %d not supported (bf16, fp16)",
+                a.dtype);
+  TAI_CHECK_ARG(a.b >= 0 && a.s_q >= 0 && a.s_kv >= 0 && a.hq > 0 && a.hkv > 0 && a.hq % a.hkv == 0,
+                "tai_fia_general: bad sizes or head counts");
+  TAI_CHECK_ARG(a.dk1 > 0 && a.dk1 % 8 == 0 && a.dk2 >= 0 && a.dk1 + a.dk2 <= kGenMaxDk && a.dv > 0 && a.dv <= kGenMaxDv,
+                "tai_fia_general: key dims (%d + %d) must be a multiple of 8 and at most %d in all, value dims at most %d",
+                a.dk1, a.dk2, kGenMaxDk, kGenMaxDv);
+  TAI_CHECK_ARG(a.dk2 == 0 || (a.q2 && a.k2), "tai_fia_general: a second key part needs q2 and k2");
+  TAI_CHECK_ARG(a.mask_origin == 0 || a.mask_origin == 1, "tai_fia_general: mask_origin must be 0 or 1");
+  TAI_CHECK_ARG(a.block_table == nullptr || (a.block_size > 0 && a.max_blocks > 0 && a.seq_lens_kv),
+                "tai_fia_general: paged K/V need block_size, max_blocks and seq_lens_kv");
+  if (a.b == 0 || a.s_q == 0) return TAI_OK;
+  TAI_CHECK_ARG(a.q1 && a.k1 && a.v && a.out, "tai_fia_general: null pointer");
+  TAI_CHECK_ARG((reinterpret_cast<uintptr_t>(a.k1) % 16) == 0 && a.k1_strides[0] % 8 == 0 && a.k1_strides[1] % 8 == 0 &&
+                    a.k1_strides[2] % 8 == 0,
+                "tai_fia_general: key rows must be 16-byte aligned");
+  GenArgs ga{a, a.dtype == TAI_DT_FP16};
+  // pre / next at or beyond 2^40 tokens are no bound
+  constexpr int64_t kNoBound = int64_t(1) << 40;
+  ga.a.pre_tokens = imin64(imax64(a.pre_tokens, -kNoBound), kNoBound);
+  ga.a.next_tokens = imin64(imax64(a.next_tokens, -kNoBound), kNoBound);
+  const int64_t waves = a.b * a.hq * a.s_q;
+  fia_general_kernel<<<dim3(static_cast<unsigned>(cdiv(waves, kGenWaves))), 64 * kGenWaves, 0,
+                       static_cast<hipStream_t>(stream)>>>(ga);
+  return launch_status("tai_fia_general");
+}
