@@ -233,7 +233,7 @@ def bench_gemm(torch, dev, iters=20):
     one = torch.ones(1, device=dev)
     res = {}
     for name, bb in (("kn", b), ("nk", b.t().contiguous().t())):
-        for _ in range(3):
+        for _ in range(10):  # warm-up: the engine clock settles
             torch.ops.npu.npu_quant_matmul(a, bb, one, output_dtype=torch.int32)
         e0, e1 = _events(torch)
         e0.record()
@@ -411,7 +411,7 @@ def bench_decode(torch, dev, iters=50, cpu=False):
 
 
 # ----------------------------------------------------------------------------- causal prefill (config 3)
-def bench_prefill(torch, dev, iters=10, cpu=False):
+def bench_prefill(torch, dev, iters=30, cpu=False):
     g = _cpu_gen(torch, 3)
     B, S, HQ, HKV, D = 4, 4096, 32, 8, 128
     q = torch.randn(B, S, HQ * D, generator=g).to(torch.bfloat16).to(dev)
@@ -424,7 +424,9 @@ def bench_prefill(torch, dev, iters=10, cpu=False):
             q, k, v, actual_seq_lengths=lens, actual_seq_lengths_kv=lens, num_heads=HQ, num_key_value_heads=HKV,
             input_layout="BSH", scale=1.0 / D ** 0.5, sparse_mode=3)
 
-    for _ in range(2):
+    # warm-up long enough for the engine clock to settle (the first ~10 calls of a cold GPU run up to
+    # 20% slower)
+    for _ in range(20):
         run()
     e0, e1 = _events(torch)
     e0.record()
@@ -454,7 +456,7 @@ def bench_prefill(torch, dev, iters=10, cpu=False):
 
 
 # ----------------------------------------------------------------------------- MLA decode (config 5)
-def bench_mla(torch, dev, iters=20, cpu=False):
+def bench_mla(torch, dev, iters=30, cpu=False):
     g = _cpu_gen(torch, 4)
     B, H, DN, DR, BS = 128, 128, 512, 64, 128
     lens = torch.randint(2048, 8193, (B,), generator=g)
@@ -479,7 +481,7 @@ def bench_mla(torch, dev, iters=20, cpu=False):
             block_table=bt, actual_seq_lengths_kv=lens, num_heads=H, num_key_value_heads=1, input_layout="BSND",
             block_size=BS, scale=1.0 / 192 ** 0.5)
 
-    for _ in range(2):
+    for _ in range(10):  # warm-up: the engine clock settles
         run()
     e0, e1 = _events(torch)
     e0.record()
