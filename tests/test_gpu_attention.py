@@ -461,6 +461,19 @@ def test_paged_explicit_mask():
     _assert_lse(lse.cpu().numpy().reshape(2, hq, 3), wl)
 
 
+@pytest.mark.parametrize("lq", [1, 3])
+def test_paged_small_blocks(lq):
+    """Block sizes that are not a multiple of 32 tokens take the general kernel."""
+    lqs, lkv = [lq, 1], [100, 37]
+    hq, hkv, d, bs = 8, 2, 128, 16
+    q, k4, v4, bt = _paged_seq_case(lqs, lkv, hq, hkv, d, bs, 125)
+    out, lse = _paged_seq(q, k4, v4, bt, lqs, lkv, hq, hkv, bs, "BSH", "BSH", sparse_mode=3)
+    want, wl = G.paged_prefill_attention(f32np(q), f32np(k4), f32np(v4), bt.numpy(), lqs, lkv,
+                                         (1, 2147483647, 0), 1.0 / math.sqrt(d))
+    assert_close(f32np(out), want)
+    _assert_lse(lse.cpu().numpy().reshape(2, hq, lq), wl)
+
+
 def test_mla_bf16_latent():
     lens, h, bs = [300, 65, 1], 16, 64
     qn, qr, ckv, cs, kr, bt = _mla_case(lens, h, bs, 123)

@@ -243,7 +243,8 @@ def fia_cuda(query, key, value, **kw):
                "npu_fused_infer_attention_score: key/value caches must share shape and a dense head dim")
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
-        if explicit or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)):
+        # the tiled kernels step through pages 32 tokens at a time
+        if explicit or bs % 32 != 0 or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)):
             _check(ql != "TND", "npu_fused_infer_attention_score: the general path takes BSH/BSND/BNSD queries")
             kstr = [sb, ss, sh]
             return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, kstr, kstr,

@@ -478,8 +478,9 @@ DecWs dec_ws(int64_t b, int hkv, int d) {
 // Per wave, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 puts one query per lane (column), so the
 // online-softmax rescale of O^T is a per-lane scalar and P^T leaves the S^T registers already in
 // the B-operand layout of O^T = V^T P^T.
-// K/V tiles go through a three-stage ring filled with global_load_lds (16 bytes per lane, no
-// register round trip): two tiles are in flight while one is used. LDS rows are the tile's token
+// K/V tiles go through a four-slot ring filled with global_load_lds (16 bytes per lane, no
+// register round trip): two tiles are in flight while one is used and the fourth slot is still
+// being read by waves that have not yet passed the barrier. LDS rows are the tile's token
 // rows with 16-byte chunks XOR-swizzled by row, so the K fragment reads (32 rows, same chunk) and
 // the transposing V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes) are free of bank
 // conflicts.
@@ -1805,7 +1806,7 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.n_qt = static_cast<int>(cdiv(s_q, kPQ));
   a.units_per_bk = a.n_qt * a.g;
   a.blocks_per_bk = static_cast<int>(cdiv(a.units_per_bk, kPWaves));
-  // the three-stage ring needs more LDS than a workgroup gets by default (set once per process)
+  // the four-slot ring needs more LDS than a workgroup gets by default (set once per process)
   static const bool lds_ok = [] {
     auto set = [](const void* f, int bytes) {
       return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
