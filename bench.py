@@ -373,7 +373,7 @@ def bench_decode(torch, dev, iters=50, cpu=False):
         run()
     except RuntimeError as e:
         return {"status": "unavailable", "error": str(e)[:200]}
-    for _ in range(3):
+    for _ in range(60):  # warm-up: the engine clock settles
         run()
     e0, e1 = _events(torch)
     e0.record()
@@ -424,9 +424,9 @@ def bench_prefill(torch, dev, iters=30, cpu=False):
             q, k, v, actual_seq_lengths=lens, actual_seq_lengths_kv=lens, num_heads=HQ, num_key_value_heads=HKV,
             input_layout="BSH", scale=1.0 / D ** 0.5, sparse_mode=3)
 
-    # warm-up long enough for the engine clock to settle (the first ~10 calls of a cold GPU run up to
-    # 20% slower)
-    for _ in range(20):
+    # warm-up long enough for the engine clock to settle (the first ~100 calls after the int8 GEMMs run
+    # up to 20% slower)
+    for _ in range(150):
         run()
     e0, e1 = _events(torch)
     e0.record()
@@ -481,7 +481,7 @@ def bench_mla(torch, dev, iters=30, cpu=False):
             block_table=bt, actual_seq_lengths_kv=lens, num_heads=H, num_key_value_heads=1, input_layout="BSND",
             block_size=BS, scale=1.0 / 192 ** 0.5)
 
-    for _ in range(10):  # warm-up: the engine clock settles
+    for _ in range(60):  # warm-up: the engine clock settles
         run()
     e0, e1 = _events(torch)
     e0.record()
