@@ -84,6 +84,21 @@ def test_dsq_grouped_cfg4_slice():
     _dsq_check(x, ws, act, True, gidx=counts)
 
 
+def test_dsq_many_rows_ragged_groups():
+    """Config-4-sized row counts: ragged groups, empty groups, rows past the grouped total."""
+    g = gen(14)
+    counts = torch.randint(0, 130, (64,), generator=g, dtype=torch.int64)
+    counts[5] = 0
+    counts[6] = 1
+    rows = int(counts.sum()) + 7
+    rows += 1 if rows % 4 == 0 else 0
+    assert rows >= 4096
+    x, ws, act = _dsq_inputs(rows, 2048, g, groups=64)
+    _dsq_check(x, ws, act, True, gidx=counts)
+    x2, ws2, act2 = _dsq_inputs(4099, 2048, g)
+    _dsq_check(x2, ws2, act2, False)
+
+
 def test_dsq_bias_quant_scale_and_odd_n():
     g = gen(5)
     x, ws, act = _dsq_inputs(33, 100, g)
