@@ -112,6 +112,39 @@ class MoeLayer:
                                      output_dtype=torch.bfloat16)[0]
         return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
 
+    def module(self):
+        """The prescribed composition as a module (weights as parameters, sharing this layer's
+        storage), for torch.compile(backend=get_npu_backend())."""
+        torch = self.torch
+        layer = self
+
+        class Moe(torch.nn.Module):
+            def __init__(self):
+                super().__init__()
+                p = lambda t: torch.nn.Parameter(t, requires_grad=False)  # noqa: E731
+                self.bias, self.s_gu, self.s_d = p(layer.bias), p(layer.s_gu), p(layer.s_d)
+                self.w_gu, self.w_d = p(layer.w_gu), p(layer.w_d)
+
+            def forward(self, x, logits):
+                npu = torch.ops.npu
+                y, idx, _ = npu.npu_moe_gating_top_k(logits, layer.K, bias=self.bias, k_group=4, group_count=8,
+                                                     group_select_mode=1, renorm=0, norm_type=1,
+                                                     routed_scaling_factor=1.0, eps=1e-20)
+                ex, ri, counts, _ = npu.npu_moe_init_routing_v2(x, idx, active_num=layer.T * layer.K,
+                                                                expert_num=layer.E, expert_tokens_num_type=1,
+                                                                expert_tokens_num_flag=True, row_idx_type=0)
+                q, s = npu.npu_dynamic_quant(ex)
+                acc = npu.npu_grouped_matmul([q], [self.w_gu], group_list=counts, split_item=3, group_type=0,
+                                             group_list_type=1, output_dtype=torch.int32)[0]
+                q2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=self.s_gu, activation_scale=s,
+                                                      group_index=counts, activate_left=True, quant_mode=1)
+                out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2],
+                                             group_list=counts, split_item=3, group_type=0, group_list_type=1,
+                                             output_dtype=torch.bfloat16)[0]
+                return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
+
+        return Moe()
+
     def gmm1_bytes(self):
         T, H, K, I = self.T, self.H, self.K, self.I
         # weights of the experts that received rows + int8 rows + int32 out (an expert with no rows is never read)
@@ -139,8 +172,9 @@ def bench_moe(torch, dev, steps, warmup):
 
 def bench_moe_variants(torch, layer, iters=10):
     """ms per step of the config-4 layer with the fused gate_up op, with the routing's fused dynamic
-    quant (npu_moe_init_routing_v2 quant_mode 1, bit-identical), and of the prescribed composition
-    replayed from a hipGraph (launch gaps removed)."""
+    quant (npu_moe_init_routing_v2 quant_mode 1, bit-identical), of the prescribed composition
+    replayed from a hipGraph (launch gaps removed), and of that composition compiled through
+    get_npu_backend (reduce-overhead mode)."""
     from torchair_amd.graph import HipGraphRunner
     out = {}
     # the runner captures per input signature; the router logits are passed as a static input (no copy)
@@ -158,6 +192,27 @@ def bench_moe_variants(torch, layer, iters=10):
         e1.record()
         torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / iters, 4)
+    # the product path: the prescribed composition compiled through get_npu_backend (pattern passes,
+    # converters, hipGraph capture of the lowered graph); the routing + quant pattern is folded into
+    # the routing op, bit for bit
+    import torchair_amd
+    cfg = torchair_amd.CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    compiled = torch.compile(layer.module(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
+    for _ in range(3):
+        got = compiled(layer.x, layer.logits)
+    torch.cuda.synchronize()
+    out["compiled_matches_eager"] = bool(torch.equal(got, layer.step()))
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(iters):
+        compiled(layer.x, layer.logits)
+    e1.record()
+    torch.cuda.synchronize()
+    out["compiled_graph_ms"] = round(e0.elapsed_time(e1) / iters, 4)
+    out["compiled_graph_tokens_per_s"] = round(MoeLayer.T / (out["compiled_graph_ms"] * 1e-3), 1)
+    from torchair_amd import graph as tai_graph, patterns as tai_patterns
+    out["compiled_graph_stats"] = {"patterns": dict(tai_patterns.stats), "graph": dict(tai_graph.stats)}
     out["fused_gate_up_tokens_per_s"] = round(MoeLayer.T / (out["fused_gate_up_ms"] * 1e-3), 1)
     out["fused_routing_quant_tokens_per_s"] = round(MoeLayer.T / (out["fused_routing_quant_ms"] * 1e-3), 1)
     out["hipgraph_tokens_per_s"] = round(MoeLayer.T / (out["hipgraph_ms"] * 1e-3), 1)

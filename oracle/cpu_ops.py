@@ -102,6 +102,11 @@ def register() -> None:
         n = t * k
         rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
         lo, hi = (active_expert_range[0], active_expert_range[1]) if active_expert_range else (0, expert_num)
+        if quant_mode == 1:  # dynamic quant of every expanded row (no smooth scale)
+            ex, ri, tok, _ = G.moe_init_routing_v2(_np(x), expert_idx.numpy(), None, rows, lo, hi,
+                                                   expert_tokens_num_type, row_idx_type)
+            q, s = G.dynamic_quant(ex)
+            return _t(q), _t(ri), _t(tok), _t(s)
         ex, ri, tok, es = G.moe_init_routing_v2(_np(x), expert_idx.numpy(), _np(scale), rows, lo, hi,
                                                 expert_tokens_num_type, row_idx_type)
         es_t = _t(es) if es is not None else torch.empty(0, dtype=torch.float32)

@@ -253,3 +253,46 @@ def test_pattern_pass_keeps_graph_order_when_x_out_is_used_before_the_quant():
     gm2.graph.lint()
     for a, b in zip(gm2(x1, x2, sm), block2(x1, x2, sm)):
         assert torch.equal(a, b)
+
+
+def test_pattern_pass_fuses_init_routing_dynamic_quant_on_cpu():
+    """Routing whose expanded rows feed only a plain per-token quant becomes the routing op's quant
+    mode 1; the compiled result equals the eager composition, bit for bit. A quant with smooth
+    scales, or expanded rows with another user, is left alone."""
+    from oracle import cpu_ops
+    from torchair_amd.patterns import fuse_init_routing_dynamic_quant
+    cpu_ops.register()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(16, 64, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(8, generator=g)[:2] for _ in range(16)]).to(torch.int32)
+    sm = torch.rand(64, generator=g) + 0.5
+
+    def block(x, idx):
+        ex, ri, tok, _ = torch.ops.npu.npu_moe_init_routing_v2(x, idx, active_num=32, expert_num=8,
+                                                               expert_tokens_num_type=1, expert_tokens_num_flag=True)
+        q, s = torch.ops.npu.npu_dynamic_quant(ex)
+        return q, s, ri, tok
+
+    gm = torch.fx.symbolic_trace(block)
+    assert fuse_init_routing_dynamic_quant(gm) == 1
+    calls = [n for n in gm.graph.nodes if n.op == "call_function"]
+    assert torch.ops.npu.npu_dynamic_quant.default not in {n.target for n in calls}
+    assert [n.kwargs["quant_mode"] for n in calls if n.target == torch.ops.npu.npu_moe_init_routing_v2.default] == [1]
+    for a, b in zip(gm(x, idx), block(x, idx)):
+        assert torch.equal(a, b)
+    fn = torch.compile(block, backend=get_npu_backend(), fullgraph=True)
+    for a, b in zip(fn(x, idx), block(x, idx)):
+        assert torch.equal(a, b)
+
+    def smoothed(x, idx):
+        ex, ri, tok, _ = torch.ops.npu.npu_moe_init_routing_v2(x, idx, expert_num=8)
+        return torch.ops.npu.npu_dynamic_quant(ex, smooth_scales=sm)
+
+    def rows_also_used(x, idx):
+        ex, ri, tok, _ = torch.ops.npu.npu_moe_init_routing_v2(x, idx, expert_num=8)
+        return torch.ops.npu.npu_dynamic_quant(ex), ex.float().sum()
+
+    for f in (smoothed, rows_also_used):
+        gm2 = torch.fx.symbolic_trace(f)
+        assert fuse_init_routing_dynamic_quant(gm2) == 0
+        gm2.graph.lint()

@@ -204,3 +204,47 @@ def test_compiled_cache_write_updates_the_callers_cache():
     torch.cuda.synchronize()
     assert torch.equal(kc2.view(-1, hkv, d)[perm[:t].to(DEV)], key)
     assert tai_graph.stats["captures"] == caps + 2
+
+
+class _MoeFront(torch.nn.Module):
+    """Gating, routing, per-token quant and the gate_up grouped GEMM of a MoE layer; the pattern pass
+    folds the quant into the routing op (quant_mode 1)."""
+
+    def __init__(self, h, e, inter, g):
+        super().__init__()
+        p = lambda t: torch.nn.Parameter(t.to(DEV), requires_grad=False)  # noqa: E731
+        self.bias = p(torch.randn(e, generator=g) * 0.1)
+        self.w = p(torch.randint(-127, 128, (e, h, 2 * inter), generator=g, dtype=torch.int8))
+        self.e = e
+
+    def forward(self, x, logits):
+        npu = torch.ops.npu
+        _, idx, _ = npu.npu_moe_gating_top_k(logits, 8, bias=self.bias, k_group=4, group_count=8, group_select_mode=1,
+                                             renorm=0, norm_type=1, routed_scaling_factor=1.0, eps=1e-20)
+        ex, ri, counts, _ = npu.npu_moe_init_routing_v2(x, idx, active_num=x.shape[0] * 8, expert_num=self.e,
+                                                        expert_tokens_num_type=1, expert_tokens_num_flag=True,
+                                                        row_idx_type=0)
+        q, s = npu.npu_dynamic_quant(ex)
+        acc = npu.npu_grouped_matmul([q], [self.w], group_list=counts, split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.int32)[0]
+        return acc, s, ri, counts
+
+
+def test_compiled_moe_front_folds_the_quant_into_routing():
+    from torchair_amd import patterns
+    g = torch.Generator().manual_seed(51)
+    t, h, e, inter = 512, 1024, 64, 256
+    mod = _MoeFront(h, e, inter, g)
+    fused0 = patterns.stats["init_routing_dynamic_quant"]
+    fn = torch.compile(mod, backend=_backend(), fullgraph=True)
+    caps = tai_graph.stats["captures"]
+    for i in range(3):
+        x = torch.randn(t, h, generator=g).to(torch.bfloat16).to(DEV)
+        logits = torch.randn(t, e, generator=g).to(DEV)
+        got = [o.clone() for o in fn(x, logits)]
+        want = mod(x, logits)
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), f"call {i}: compiled front differs from eager"
+        _churn()
+    assert patterns.stats["init_routing_dynamic_quant"] == fused0 + 1
+    assert tai_graph.stats["captures"] == caps + 1

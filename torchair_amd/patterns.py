@@ -7,6 +7,13 @@ npu_dynamic_quant(y, smooth_scales=s) becomes npu_add_rms_norm_dynamic_quant(x1,
 smooth_scale1=s, epsilon=eps, output_mask=[True, False]); the fused kernel quantises y rounded to
 the input dtype, so the rewrite changes no value. A match whose rstd output is used, or whose
 quant has other arguments than smooth_scales, is left alone.
+
+npu_moe_init_routing_v2 + dynamic_quant -> npu_moe_init_routing_v2(quant_mode=1): routing without
+quantisation whose expanded rows feed only a symmetric per-token int8 npu_dynamic_quant (no smooth
+scales, no group index) becomes the routing op with its dynamic quant mode (experiment_ops.h:2167),
+whose expanded rows and scales are the quantised rows and their scales. The routing kernel quantises
+each token row once and gathers the int8 rows, which equals quantising every gathered copy, so the
+rewrite changes no value. This pattern has no counterpart among the reference's passes.
 """
 from __future__ import annotations
 
@@ -17,6 +24,9 @@ import torch
 import torch.fx
 
 logger = logging.getLogger("torchair_amd")
+
+# rewrites applied so far in this process, per pattern (diagnostics and tests)
+stats = {"add_rms_norm_dynamic_quant": 0, "init_routing_dynamic_quant": 0}
 
 
 def _getitems(node: torch.fx.Node):
@@ -92,10 +102,74 @@ def fuse_add_rms_norm_dynamic_quant(gm: torch.fx.GraphModule) -> int:
     if fused:
         gm.graph.lint()
         gm.recompile()
+        stats["add_rms_norm_dynamic_quant"] += fused
         logger.debug("fused %d add_rms_norm + dynamic_quant pair(s)", fused)
+    return fused
+
+
+def _plain_dynamic_quant(quant: torch.fx.Node, rows: torch.fx.Node) -> bool:
+    """npu_dynamic_quant(rows) as symmetric per-token int8 without smooth scales or groups."""
+    if quant.args != (rows,):
+        return False
+    kw = dict(quant.kwargs)
+    ok = {"smooth_scales": (None,), "group_index": (None,), "dst_type": (None, 1, torch.int8),
+          "quant_mode": (None, "pertoken"), "dst_type_max": (None, 0.0)}
+    return all(k in ok and any(v is a or v == a for a in ok[k]) for k, v in kw.items())
+
+
+def fuse_init_routing_dynamic_quant(gm: torch.fx.GraphModule) -> int:
+    npu = torch.ops.npu
+    if not hasattr(npu, "npu_moe_init_routing_v2"):
+        return 0
+    fused = 0
+    for route in list(gm.graph.nodes):
+        if not _calls(route, npu.npu_moe_init_routing_v2) or len(route.args) != 2:
+            continue
+        kw = dict(route.kwargs)
+        if kw.get("quant_mode", -1) != -1 or kw.get("scale") is not None or kw.get("offset") is not None:
+            continue
+        outs = _getitems(route)
+        if outs is None:
+            continue
+        live = {i: [u for u in us if u.users] for i, us in outs.items()}
+        if live.get(3) or len(live.get(0, [])) != 1:
+            continue
+        rows = live[0][0]
+        if len(rows.users) != 1:
+            continue
+        quant = next(iter(rows.users))
+        if not _calls(quant, npu.npu_dynamic_quant) or not _plain_dynamic_quant(quant, rows):
+            continue
+        qouts = _getitems(quant)
+        if qouts is None:
+            continue
+        kw["quant_mode"] = 1
+        with gm.graph.inserting_after(route):
+            node = gm.graph.call_function(npu.npu_moe_init_routing_v2.default, route.args, kw)
+        # quant outputs 0 / 1 become the routing's expanded rows / expanded scales; its other outputs
+        # move over unchanged
+        for users, dst_idx in ((qouts.get(0, []), 0), (qouts.get(1, []), 3), (outs.get(1, []), 1), (outs.get(2, []), 2)):
+            for u in users:
+                with gm.graph.inserting_after(node):
+                    new = gm.graph.call_function(operator.getitem, (node, dst_idx))
+                u.replace_all_uses_with(new)
+                gm.graph.erase_node(u)
+        gm.graph.erase_node(quant)
+        for us in outs.values():
+            for u in us:
+                if u in gm.graph.nodes and not u.users:
+                    gm.graph.erase_node(u)
+        gm.graph.erase_node(route)
+        fused += 1
+    if fused:
+        gm.graph.lint()
+        gm.recompile()
+        stats["init_routing_dynamic_quant"] += fused
+        logger.debug("fused %d init_routing_v2 + dynamic_quant pair(s)", fused)
     return fused
 
 
 def apply_pattern_passes(gm: torch.fx.GraphModule) -> torch.fx.GraphModule:
     fuse_add_rms_norm_dynamic_quant(gm)
+    fuse_init_routing_dynamic_quant(gm)
     return gm
