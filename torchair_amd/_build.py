@@ -29,7 +29,7 @@ COMMON_FLAGS = [
     "-Wno-unused-result",
 ]
 # Files whose float arithmetic must follow the CPU oracle's operation order exactly.
-NO_CONTRACT = {"quant.hip", "moe_routing.hip", "norm_cache.hip"}
+NO_CONTRACT = {"quant.hip", "moe_routing.hip", "norm_cache.hip", "gemm_i8.hip"}
 
 
 INCLUDE = PKG.parent / "include"

@@ -59,7 +59,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ float f16_to_f32(uint16_t v) {
   return __half2float(__ushort_as_half(v));
 }
+// fp32 -> fp16, round to nearest even, from a value already rounded to fp32: the empty asm keeps
+// the compiler from fusing the multiply that produced f into the conversion (v_fma_mix*_f16 rounds
+// once, to fp16, where the op rounds to fp32 first)
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  asm("" : "+v"(f));
   return __half_as_ushort(__float2half_rn(f));
 }
 
