@@ -3,7 +3,9 @@
 Headline (value): DeepSeek-V3-shaped quantized MoE layer in tokens/s:
   gating_top_k -> init_routing_v2 -> dynamic_quant -> grouped_matmul (W8A8 gate_up, int32)
   -> dequant_swiglu_quant -> grouped_matmul (W8A8 down, bf16) -> finalize_routing,
-with every input resident in HBM before the timed region. Side measurements in the same JSON
+as a module compiled with torch.compile(backend=get_npu_backend()) in reduce-overhead mode (the
+product path: pattern passes, converters, hipGraph replay), with every input resident in HBM before
+the timed region; the eager composition is timed beside it. Side measurements in the same JSON
 line: paged GQA decode attention (config 2) HBM GB/s, the W8A8 GEMM at M=N=K=8192 and the
 config-1 MLP. `roofline` is for the dominant kernel (the gate_up grouped GEMM), timed with HIP
 events on its stream inside the timed region; `cpu_baseline` times the CPU oracle on a bounded
@@ -151,30 +153,62 @@ class MoeLayer:
         return self.active_experts * H * 2 * I + T * K * H + T * K * 2 * I * 4
 
 
+def compile_layer(torch, layer):
+    """The product path: the prescribed composition through torch.compile(backend=get_npu_backend())
+    in reduce-overhead mode (pattern passes, converters, hipGraph capture of the lowered graph; the
+    routing + dynamic-quant pattern is folded into the routing op, bit for bit)."""
+    import torchair_amd
+    cfg = torchair_amd.CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    return torch.compile(layer.module(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
+
+
 def bench_moe(torch, dev, steps, warmup):
+    """Headline: `steps` layer steps through the compiled product path (the first call, which traces,
+    compiles and captures the graph, is set-up; then `warmup` untimed steps). The same number of
+    eager steps of the prescribed composition follow, outside the timed region: HIP events on the
+    stream bracket their gate_up GEMM (the roofline kernel; the compiled graph runs the same kernel
+    on the same inputs), and their output is compared with the compiled one."""
     layer = MoeLayer(torch, dev)
+    compiled = compile_layer(torch, layer)
+    got = compiled(layer.x, layer.logits)
+    torch.cuda.synchronize()
     for _ in range(warmup):
-        layer.step()
+        compiled(layer.x, layer.logits)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        layer.step(record=True)
+        compiled(layer.x, layer.logits)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
+    for _ in range(2):
+        layer.step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        layer.step(record=True)
+    torch.cuda.synchronize()
+    dt_eager = (time.perf_counter() - t1) / steps
+    matches = bool(torch.equal(got, layer.step()))
     gmm_ms = sum(a.elapsed_time(b) for a, b in layer.gmm1_events) / len(layer.gmm1_events)
     achieved = layer.gmm1_bytes() / (gmm_ms * 1e-3) / 1e9
     roof = {"kernel": "tai_grouped_matmul (gate_up, int32 out)", "bound": "hbm", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(), "avg_ms": round(gmm_ms, 4),
-            "algorithmic_bytes": layer.gmm1_bytes(), "active_experts": layer.active_experts}
-    return layer, dt, roof
+            "algorithmic_bytes": layer.gmm1_bytes(), "active_experts": layer.active_experts,
+            "timed_on": "the eager steps after the timed region (same kernel and inputs as the compiled graph)"}
+    from torchair_amd import graph as tai_graph, patterns as tai_patterns
+    eager = {"eager_prescribed_ms": round(dt_eager * 1e3, 4),
+             "eager_prescribed_tokens_per_s": round(MoeLayer.T / dt_eager, 1),
+             "compiled_matches_eager": matches,
+             "compiled_graph_stats": {"patterns": dict(tai_patterns.stats), "graph": dict(tai_graph.stats)}}
+    return layer, dt, roof, eager
 
 
 def bench_moe_variants(torch, layer, iters=10):
-    """ms per step of the config-4 layer with the fused gate_up op, with the routing's fused dynamic
-    quant (npu_moe_init_routing_v2 quant_mode 1, bit-identical), of the prescribed composition
-    replayed from a hipGraph (launch gaps removed), and of that composition compiled through
-    get_npu_backend (reduce-overhead mode)."""
+    """ms per step of the config-4 layer (eager) with the fused gate_up op, with the routing's fused
+    dynamic quant (npu_moe_init_routing_v2 quant_mode 1, bit-identical), and of the prescribed
+    composition replayed from a hipGraph captured directly (no compiler)."""
     from torchair_amd.graph import HipGraphRunner
     out = {}
     # the runner captures per input signature; the router logits are passed as a static input (no copy)
@@ -192,27 +226,6 @@ def bench_moe_variants(torch, layer, iters=10):
         e1.record()
         torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / iters, 4)
-    # the product path: the prescribed composition compiled through get_npu_backend (pattern passes,
-    # converters, hipGraph capture of the lowered graph); the routing + quant pattern is folded into
-    # the routing op, bit for bit
-    import torchair_amd
-    cfg = torchair_amd.CompilerConfig()
-    cfg.mode = "reduce-overhead"
-    compiled = torch.compile(layer.module(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
-    for _ in range(3):
-        got = compiled(layer.x, layer.logits)
-    torch.cuda.synchronize()
-    out["compiled_matches_eager"] = bool(torch.equal(got, layer.step()))
-    e0, e1 = _events(torch)
-    e0.record()
-    for _ in range(iters):
-        compiled(layer.x, layer.logits)
-    e1.record()
-    torch.cuda.synchronize()
-    out["compiled_graph_ms"] = round(e0.elapsed_time(e1) / iters, 4)
-    out["compiled_graph_tokens_per_s"] = round(MoeLayer.T / (out["compiled_graph_ms"] * 1e-3), 1)
-    from torchair_amd import graph as tai_graph, patterns as tai_patterns
-    out["compiled_graph_stats"] = {"patterns": dict(tai_patterns.stats), "graph": dict(tai_graph.stats)}
     out["fused_gate_up_tokens_per_s"] = round(MoeLayer.T / (out["fused_gate_up_ms"] * 1e-3), 1)
     out["fused_routing_quant_tokens_per_s"] = round(MoeLayer.T / (out["fused_routing_quant_ms"] * 1e-3), 1)
     out["hipgraph_tokens_per_s"] = round(MoeLayer.T / (out["hipgraph_ms"] * 1e-3), 1)
@@ -691,7 +704,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of side benches to run (moe,norm,gemm,mlp,decode,prefill,mla; 'none' for the MoE layer "
@@ -705,8 +718,8 @@ def main():
 
     dev = "cuda:0"
     torch.cuda.synchronize()
-    layer, dt, roof = bench_moe(torch, dev, args.steps, args.warmup)
-    extra = {}
+    layer, dt, roof, eager = bench_moe(torch, dev, args.steps, args.warmup)
+    extra = {"moe_layer_eager": eager}
     only = set(filter(None, args.only.split(","))) or {"gemm", "mlp", "decode", "prefill", "mla", "moe", "norm"}
     if "moe" in only:
         extra["moe_layer_variants"] = bench_moe_variants(torch, layer)
@@ -735,7 +748,10 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "int8 (W8A8, int32 accumulate; bf16 activations)",
         "data": "synthetic (seeded randn/randint of the config shapes, random-init weights)",
         "config": {"workload": "DeepSeek-V3-shaped quantized MoE layer, T=4096 H=7168 E=256 top-8 I=2048 "
-                               "(BASELINE config 4), all experts on one GPU", "global_batch": MoeLayer.T,
+                               "(BASELINE config 4), all experts on one GPU",
+                   "path": "torch.compile(layer, backend=get_npu_backend(CompilerConfig(mode='reduce-overhead'))): "
+                           "pattern passes, converters, hipGraph replay of the lowered graph",
+                   "global_batch": MoeLayer.T,
                    "seq_len": 1, "parallelism": "single GPU"},
         "roofline": roof, "cpu_baseline": cpu_moe, "extra": extra,
     }
