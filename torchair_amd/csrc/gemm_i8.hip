@@ -591,26 +591,35 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&
       }
       rmax[i][r] = m;
     }
-  // max over the 32 lanes that share a row, then over the waves that share the row (LDS)
+  // Max over the 32 lanes that share a row (lanes of one half-wave hold one row's columns), as a
+  // reduce-scatter: at the step with lane offset o each lane keeps half of its live row values and
+  // sends the partner the other half, so 16 + 8 + 4 + 2 + 1 shuffles leave lane l (of its half)
+  // with the max of row value l (i = l / 16, r = l % 16); then over the waves sharing the row (LDS).
+  float v[32];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int t = 0; t < 32; ++t) v[t] = rmax[t >> 4][t & 15];
+  const int l32 = lane & 31;
+  auto halve = [&](auto half) {  // one step: 2 * H live values -> H, lane offset H
+    constexpr int H = decltype(half)::value;
+    const bool up = (l32 & H) != 0;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float m = rmax[i][r];
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      rmax[i][r] = m;
+    for (int t = 0; t < H; ++t) {
+      const float keep = up ? v[t + H] : v[t];
+      const float send = up ? v[t] : v[t + H];
+      v[t] = fmaxf(keep, __shfl_xor(send, H, 64));
     }
+  };
+  halve(std::integral_constant<int, 16>());
+  halve(std::integral_constant<int, 8>());
+  halve(std::integral_constant<int, 4>());
+  halve(std::integral_constant<int, 2>());
+  halve(std::integral_constant<int, 1>());
   float* red = reinterpret_cast<float*>(smem);  // [WN][kBM]
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if ((lane & 31) == 0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        red[wn * C::kBM + lr] = rmax[i][r];
-      }
+  {
+    const int i = l32 >> 4, r = l32 & 15;
+    const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    red[wn * C::kBM + lr] = v[0];
   }
   __syncthreads();
   for (int lr = threadIdx.x; lr < rows && lr < C::kBM; lr += C::kThreads) {
