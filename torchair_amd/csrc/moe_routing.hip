@@ -1,9 +1,9 @@
 // MoE routing on one GPU: npu_moe_gating_top_k, npu_moe_init_routing(_v2) and
 // npu_moe_finalize_routing - the single-GPU share of expert dispatch/combine.
 //
-// gating_top_k : one wave per token row; scores staged in LDS, group scores and the
-//                iterative arg-max run with wave shuffles. Sigmoid/softmax are evaluated in
-//                fp64 and rounded once to fp32 so the expert choice is reproducible.
+// gating_top_k : one wave per token row; scores staged in LDS for the group scores, then the
+//                iterative arg-max over registers with wave shuffles. Sigmoid/softmax are
+//                evaluated in fp64 and rounded once to fp32 so the expert choice is reproducible.
 // init_routing : stable counting sort of the t*k routing slots by expert, in four launches
 //                (chunk histograms -> per-expert scan -> in-chunk ranks -> row gather).
 //                Every kernel writes all of its outputs, so no memset is needed and the
@@ -43,8 +43,6 @@ __global__ __launch_bounds__(256) void gating_topk_kernel(GateArgs a) {
   __shared__ float s_sb[4][kMaxExperts];   // selection scores s + bias
   __shared__ float s_gs[4][kMaxGroups];    // group scores
   __shared__ int s_keep[4][kMaxGroups];
-  __shared__ float s_selw[4][32];
-  __shared__ int s_seli[4][32];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
   const bool valid = row < a.t;
@@ -109,39 +107,43 @@ __global__ __launch_bounds__(256) void gating_topk_kernel(GateArgs a) {
     __syncthreads();
   }
 
-  // k rounds of arg-max: larger score wins, equal scores go to the lower expert id.
-  float wsum = 0.0f;
+  // k rounds of arg-max: larger score wins, equal scores go to the lower expert id. The selection
+  // scores stay in registers (lane holds experts lane + 64q), so a round is a local scan and one
+  // wave reduction, with no LDS traffic and no barrier; lane r keeps the id chosen in round r.
+  if (!valid) return;
+  constexpr int kNV = kMaxExperts / 64;
+  const int nq = (E + 63) / 64;
+  float v[kNV];
+#pragma unroll
+  for (int q = 0; q < kNV; ++q) v[q] = (q < nq && lane + 64 * q < E) ? sb[lane + 64 * q] : -INFINITY;
+  int my_sel = 0;
   for (int r = 0; r < a.k; ++r) {
     float bv = -INFINITY;
     int bi = kMaxExperts;
-    if (valid) {
-      for (int j = lane; j < E; j += 64) {
-        float v = sb[j];
-        if (better(v, j, bv, bi)) { bv = v; bi = j; }
-      }
-    }
+#pragma unroll
+    for (int q = 0; q < kNV; ++q)
+      if (q < nq && better(v[q], lane + 64 * q, bv, bi)) { bv = v[q]; bi = lane + 64 * q; }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       float ov = __shfl_xor(bv, o, 64);
       int oi = __shfl_xor(bi, o, 64);
       if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
-    __syncthreads();
-    if (valid && lane == 0) {
-      sb[bi] = -INFINITY;
-      s_seli[w][r] = bi;
-      s_selw[w][r] = sc[bi];
-    }
-    __syncthreads();
-    if (valid) wsum = wsum + s_selw[w][r];
+    bi = __builtin_amdgcn_readfirstlane(bi);
+#pragma unroll
+    for (int q = 0; q < kNV; ++q)
+      if (lane + 64 * q == bi) v[q] = -INFINITY;
+    if (lane == r) my_sel = bi;
   }
-  if (!valid) return;
+  const float myw = lane < a.k ? sc[my_sel] : 0.0f;
+  float wsum = 0.0f;
+  for (int r = 0; r < a.k; ++r) wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myw), r));
   if (lane < a.k) {
-    float v = s_selw[w][lane];
-    if (a.norm_type == 1) v = v / (wsum + a.eps);
-    v = v * a.rsf;
-    store_from_f32(a.y, a.x_dt, row * a.k + lane, v);
-    a.idx[row * a.k + lane] = s_seli[w][lane];
+    float wv = myw;
+    if (a.norm_type == 1) wv = wv / (wsum + a.eps);
+    wv = wv * a.rsf;
+    store_from_f32(a.y, a.x_dt, row * a.k + lane, wv);
+    a.idx[row * a.k + lane] = my_sel;
   }
   if (a.out_flag && a.out)
     for (int j = lane; j < E; j += 64) a.out[row * E + j] = sc[j];
