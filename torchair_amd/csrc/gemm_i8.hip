@@ -389,17 +389,17 @@ __global__ __launch_bounds__(1024) void group_tiles_kernel(const int64_t* __rest
   const int64_t covered = ng > 0 ? end[ng - 1] : 0;
   const int64_t zero_tiles = (m - covered + bm - 1) / bm;
   if (threadIdx.x == 0) *live = real + zero_tiles;
-  for (int64_t s = threadIdx.x; s < slots; s += blockDim.x) {
+  // each group writes its own slots (a thread per group, one store per row tile), then the zero-fill
+  // and unused slots follow
+  for (int64_t e = threadIdx.x; e < ng; e += blockDim.x) {
+    const int64_t nt = (end[e] - beg[e] + bm - 1) / bm;
+    for (int64_t j = 0; j < nt; ++j)
+      map[tp[e] + j] = make_int4(static_cast<int>(e), static_cast<int>(beg[e]), static_cast<int>(end[e]),
+                                 static_cast<int>(j));
+  }
+  for (int64_t s = real + threadIdx.x; s < slots; s += blockDim.x) {
     int4 t = make_int4(-1, 0, 0, 0);
-    if (s < real) {
-      int64_t lo = 0, hi = ng - 1;  // last e with tp[e] <= s
-      while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (tp[mid] <= s) lo = mid; else hi = mid - 1;
-      }
-      t = make_int4(static_cast<int>(lo), static_cast<int>(beg[lo]), static_cast<int>(end[lo]),
-                    static_cast<int>(s - tp[lo]));
-    } else if (s < real + zero_tiles) {
+    if (s < real + zero_tiles) {
       const int64_t r0 = covered + (s - real) * bm;
       t = make_int4(-2, static_cast<int>(r0), static_cast<int>(min<int64_t>(r0 + bm, m)), 0);
     }
