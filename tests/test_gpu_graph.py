@@ -248,3 +248,42 @@ def test_compiled_moe_front_folds_the_quant_into_routing():
         _churn()
     assert patterns.stats["init_routing_dynamic_quant"] == fused0 + 1
     assert tai_graph.stats["captures"] == caps + 1
+
+
+class _Quant(torch.nn.Module):
+    def forward(self, x):
+        return torch.ops.npu.npu_dynamic_quant(x)
+
+
+def test_compiled_inputs_by_address_replay_in_place_and_capture_anew_at_a_new_address():
+    """debug.aclgraph.clone_input = False: the graph reads the caller's input tensor itself. New values
+    written into the same tensor replay without a capture; a tensor at another address captures a
+    second graph; going back to the first tensor replays the first graph."""
+    cfg = torchair_amd.CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    cfg.debug.aclgraph.clone_input = False
+    fn = torch.compile(_Quant(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(70)
+    xa = torch.randn(64, 512, generator=g, device=DEV).to(torch.bfloat16)
+    xb = torch.randn(64, 512, generator=g, device=DEV).to(torch.bfloat16)
+
+    def check(x):
+        q, s = fn(x)
+        wq, ws = torch.ops.npu.npu_dynamic_quant(x)
+        assert torch.equal(q, wq) and torch.equal(s, ws)
+
+    c0 = tai_graph.stats["captures"]
+    check(xa)
+    c1 = tai_graph.stats["captures"]
+    assert c1 == c0 + 1
+    for _ in range(2):
+        xa.copy_(torch.randn(64, 512, generator=g, device=DEV).to(torch.bfloat16))
+        _churn()
+        check(xa)
+    assert tai_graph.stats["captures"] == c1
+    check(xb)
+    assert tai_graph.stats["captures"] == c1 + 1
+    xa.copy_(torch.randn(64, 512, generator=g, device=DEV).to(torch.bfloat16))
+    check(xa)
+    assert tai_graph.stats["captures"] == c1 + 1
