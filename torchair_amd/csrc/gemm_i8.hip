@@ -950,10 +950,16 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
                                                               (static_cast<int64_t>(row0 + lr) * g.n + wcol0) * ES +
                                                               16 * (lane % LPR));
             // grouped launches write rows that the next op streams once: non-temporal stores (down
-            // projection -2%); split-K partials, re-read at once by the reduction, and dense outputs
-            // keep the default policy
-            if (nt_out) __builtin_nontemporal_store(tai_u32x4_t{v.x, v.y, v.z, v.w}, dst);
-            else *dst = tai_u32x4_t{v.x, v.y, v.z, v.w};
+            // projection -2%, the config-4 GEMM + quant + GEMM + finalize chain -0.7%); split-K
+            // partials, re-read at once by the reduction, and dense outputs keep the default policy
+            if (nt_out) {
+              // the `nt` bit written by hand: the compiler's non-temporal store builtin sets no cache
+              // policy on gfx950
+              const v4i d{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+              asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(dst), "v"(d) : "memory");
+            } else {
+              *dst = tai_u32x4_t{v.x, v.y, v.z, v.w};
+            }
           }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
