@@ -161,7 +161,8 @@ def compile_layer(torch, layer):
     cfg = torchair_amd.CompilerConfig()
     cfg.mode = "reduce-overhead"
     # inputs used by address (the reference's debug.aclgraph.clone_input option): a serving loop that
-    # refills the same input buffers replays the graph without copying them; another address captures anew
+    # refills the same input buffers replays the graph without copying them; a tensor at another address is
+    # copied into the capture-time one
     cfg.debug.aclgraph.clone_input = False
     return torch.compile(layer.module(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
 

@@ -230,3 +230,18 @@ def test_grouped_matmul_per_group_outputs():
                                              group_type=0, group_list_type=1, output_dtype=torch.int32)
     assert [p.shape[0] for p in parts] == counts.tolist()
     torch.testing.assert_close(torch.cat(parts, 0), whole[:int(counts.sum())], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dt", [torch.int64, torch.uint64])
+def test_packed_int64_scales_are_refused(dt):
+    """npu_trans_quant_param packs scales into int64 words; the ops refuse them instead of converting
+    the words numerically."""
+    g = gen(25)
+    x, w = rand_i8((8, 64), g).to(DEV), rand_i8((64, 32), g).to(DEV)
+    scale = torch.ones(32, dtype=dt, device=DEV)
+    with pytest.raises(RuntimeError, match="packed int64 scales"):
+        torch.ops.npu.npu_quant_matmul(x, w, scale, output_dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="packed int64 scales"):
+        torch.ops.npu.npu_grouped_matmul([x], [w.unsqueeze(0)], scale=[scale.unsqueeze(0)],
+                                         group_list=torch.tensor([8], device=DEV), split_item=3, group_type=0,
+                                         group_list_type=1, output_dtype=torch.bfloat16)

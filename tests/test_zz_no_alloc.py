@@ -59,6 +59,13 @@ def test_noalloc_rejects_sizes_beyond_its_scratch():
     limit = _lib.query("tai_grouped_matmul_noalloc_max_scratch")
     m = 1 << 20
     assert _lib.query("tai_grouped_matmul_workspace_size", m, 64, 8) > limit
+    # real buffers of the full problem size, so that the call would stay in bounds even if the size
+    # check were ever bypassed
+    x = torch.zeros(m, 64, dtype=torch.int8, device=DEV)
+    w = torch.zeros(8, 64, 64, dtype=torch.int8, device=DEV)
+    gl = torch.full((8,), m // 8, dtype=torch.int64, device=DEV)
+    out = torch.empty(m, 64, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="no-allocation"):
-        _lib.call("tai_grouped_matmul_noalloc", 16, 16, m, 64, 64, 8, _lib.LAYOUT_KN, 16, 1, None, None, None,
-                  _lib.DT_NONE, _lib.DT_INT32, 16, None)
+        _lib.call("tai_grouped_matmul_noalloc", x.data_ptr(), w.data_ptr(), m, 64, 64, 8, _lib.LAYOUT_KN,
+                  gl.data_ptr(), 1, None, None, None, _lib.DT_NONE, _lib.DT_INT32, out.data_ptr(), None)
+    torch.cuda.synchronize()

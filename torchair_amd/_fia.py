@@ -151,16 +151,18 @@ def _lens_tensor(v, device) -> Optional[torch.Tensor]:
         return v.to(device=device, dtype=torch.int64).contiguous()
     vals = tuple(int(x) for x in v)
     if torch.device(device).type == "cuda":
-        from .graph import preparing_capture
-        if preparing_capture() and vals not in _PINNED_LENS:
+        from .graph import capture_resources, preparing_capture
+        pinned = capture_resources()
+        key = ("fia_lens", vals)
+        if preparing_capture() and pinned is not None and key not in pinned:
             # The list is a constant of the graph about to be captured (other values capture anew).
             # A blocking host-to-device copy cannot be captured, so the captured graph copies the
-            # lengths from a pinned host buffer kept for the life of the process, which every replay
-            # re-reads. It is allocated here, in the warm-up run before the capture: pinned memory
-            # cannot be allocated while a stream is captured.
-            _PINNED_LENS[vals] = torch.tensor(vals, dtype=torch.int64).pin_memory()
+            # lengths from a pinned host buffer, owned by that graph, which every replay re-reads.
+            # It is allocated here, in the warm-up run before the capture: pinned memory cannot be
+            # allocated while a stream is captured.
+            pinned[key] = torch.tensor(vals, dtype=torch.int64).pin_memory()
         if torch.cuda.is_current_stream_capturing():
-            host = _PINNED_LENS.get(vals)
+            host = pinned.get(key) if pinned is not None else None
             if host is None:
                 raise RuntimeError("npu_fused_infer_attention_score: list-valued sequence lengths under hipGraph "
                                    "capture need a warm-up run first (or pass them as a device tensor)")
@@ -169,8 +171,6 @@ def _lens_tensor(v, device) -> Optional[torch.Tensor]:
             return out
     return torch.tensor(vals, dtype=torch.int64, device=device)
 
-
-_PINNED_LENS: dict = {}
 
 
 def _check(cond, msg):

@@ -305,9 +305,12 @@ def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
     a = x1.contiguous()
     m = a.numel() // k if k else 0
     w, layout = _weight_layout(x2)
+    # npu_trans_quant_param packs an fp32 scale (and offset) into int64 words; converting those words
+    # numerically would give meaningless scales, so they are refused
+    _check(scale is None or scale.dtype not in (torch.int64, torch.uint64),
+           "npu_quant_matmul: packed int64 scales are not supported; pass fp32")
     sc = _f32(scale) if scale is not None else None
     if sc is not None:
-        _check(scale.dtype != torch.int64, "npu_quant_matmul: packed int64 scales are not supported; pass fp32")
         _check(sc.numel() in (1, n), "npu_quant_matmul: scale must have 1 or N entries")
     pts = _f32(pertoken_scale)
     if pts is not None:
@@ -443,8 +446,9 @@ def _gmm_cuda(x, weight, *, bias=None, scale=None, offset=None, antiquant_scale=
         wl, layout = w3.contiguous(), LAYOUT_KN
     sc = None
     if scale:
+        _check(all(t.dtype not in (torch.int64, torch.uint64) for t in scale),
+               "npu_grouped_matmul: packed int64 scales are not supported; pass fp32")
         sc = _f32(scale[0] if len(scale) == 1 else torch.stack(list(scale)))
-        _check(scale[0].dtype != torch.int64, "npu_grouped_matmul: packed int64 scales are not supported; pass fp32")
         _check(sc.numel() == e * n, "npu_grouped_matmul: scale must be [E, N]")
     pts = _f32(per_token_scale[0]) if per_token_scale else None
     m = xt.shape[0]

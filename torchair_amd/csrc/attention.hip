@@ -102,6 +102,13 @@ struct DecodeArgs {
   float* part_ml;  // [slot, hkv, 16, 2]
 };
 
+// A sequence length read on the device, clamped to [0, cap]: a length past the cache extent the
+// block table can address (max_blocks * block_size) would otherwise index past the sequence's
+// block-table row into other sequences' blocks.
+__device__ __forceinline__ int64_t clamp_len(int64_t v, int64_t cap) { return v < 0 ? 0 : (v > cap ? cap : v); }
+template <class A>
+__device__ __forceinline__ int64_t kv_len(const A& a, int64_t b) { return clamp_len(a.lens[b], a.max_blocks * a.bs); }
+
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -338,13 +345,13 @@ void paged_decode_kernel(DecodeArgs a) {
   const int64_t r = blockIdx.x / a.hkv;
   const int64_t nb = a.b, R = a.nranges;
   int64_t mine = 0;
-  for (int64_t c = lane; c < nb; c += 64) mine += dec_units(a.lens[c]);
+  for (int64_t c = lane; c < nb; c += 64) mine += dec_units(kv_len(a, c));
   const int64_t S = uniform64(wave_sum64(mine));
   if (blockIdx.x == 0) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? dec_units(a.lens[i]) : 0;
+      const int64_t n = i < nb ? dec_units(kv_len(a, i)) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       if (i < nb) a.steps[1 + i] = incl - n;
       carry = __shfl(incl, 63, 64);
@@ -359,7 +366,7 @@ void paged_decode_kernel(DecodeArgs a) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? dec_units(a.lens[i]) : 0;
+      const int64_t n = i < nb ? dec_units(kv_len(a, i)) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       const uint64_t hit = __ballot(i < nb && n > 0 && incl - n <= x && x < incl);
       if (hit) {
@@ -374,7 +381,7 @@ void paged_decode_kernel(DecodeArgs a) {
   b = uniform64(b);
   pb = uniform64(pb);
   for (int64_t g = g0; g < g1;) {
-    const int64_t len = a.lens[b];
+    const int64_t len = kv_len(a, b);
     const int64_t n = dec_units(len);
     const int64_t seg = min(g1 - g, pb + n - x);
     // units [u0, u1) of this sequence; the first kDecSegCost carry no tokens
@@ -388,7 +395,7 @@ void paged_decode_kernel(DecodeArgs a) {
       pb += n;
       do {
         ++b;
-      } while (g < g1 && b < nb && dec_units(a.lens[b]) == 0);
+      } while (g < g1 && b < nb && dec_units(kv_len(a, b)) == 0);
     }
   }
 }
@@ -407,7 +414,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
   const int64_t b = bh / a.hq;
   const int kvh = h / a.g, hi = h % a.g;
   // the length and the step prefix are loaded together (the prefix is valid for every b)
-  const int64_t len = a.lens[b], S = a.steps[0], x0 = a.steps[1 + b], R = a.nranges;
+  const int64_t len = kv_len(a, b), S = a.steps[0], x0 = a.steps[1 + b], R = a.nranges;
   const int64_t n = dec_steps(len);
   uint16_t* o = out + (b * a.hq + h) * D + E * lane;
   if (n == 0) {
@@ -501,6 +508,7 @@ struct PrefillArgs {
   const int64_t* lkv;
   int64_t b;
   int64_t s_q, s_kv;
+  int64_t kv_cap;  // longest kv length the inputs hold: s_kv, or max_blocks * block_size when paged
   int hq, hkv, g;
   // Visible kv positions of query i (both clamped to [0, len_kv)): -pre <= j - i - off <= next, with
   // off = len_kv - len_q (bottom-right origin) or 0 (top-left origin). A causal mask is next = 0.
@@ -645,8 +653,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int64_t blk, 
   const bool unit_ok = unit < a.units_per_bk;
   const int qt = unit_ok ? unit / a.g : 0;
   const int head = kvh * a.g + (unit_ok ? unit % a.g : 0);
-  const int64_t Lq = a.lq ? a.lq[b] : a.s_q;
-  const int64_t Lkv = a.lkv ? a.lkv[b] : a.s_kv;
+  const int64_t Lq = a.lq ? clamp_len(a.lq[b], a.s_q) : a.s_q;
+  const int64_t Lkv = a.lkv ? clamp_len(a.lkv[b], a.kv_cap) : a.s_kv;
   const int64_t off = a.origin_rd ? Lkv - Lq : 0;
   const int64_t q0 = static_cast<int64_t>(qt) * kPQ;
   const int64_t myq = q0 + col;
@@ -1510,14 +1518,14 @@ void mla_decode_kernel(MlaArgs a) {
   }
   bool ov_seen = false;
   int64_t mine = 0;
-  for (int64_t c = lane; c < nb; c += 64) mine += mla_steps(a.lens[c]);
+  for (int64_t c = lane; c < nb; c += 64) mine += mla_steps(kv_len(a, c));
   const int64_t S = uniform64(wave_sum64(mine));
   const int64_t W = S * a.hgroups;
   if (!RESCALE && wg == 0 && threadIdx.x < 64) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? mla_steps(a.lens[i]) : 0;
+      const int64_t n = i < nb ? mla_steps(kv_len(a, i)) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       if (i < nb) a.steps[1 + i] = incl - n;
       carry = __shfl(incl, 63, 64);
@@ -1536,7 +1544,7 @@ void mla_decode_kernel(MlaArgs a) {
     int64_t carry = 0;
     for (int64_t c = 0; c < nb; c += 64) {
       const int64_t i = c + lane;
-      const int64_t n = i < nb ? mla_steps(a.lens[i]) : 0;
+      const int64_t n = i < nb ? mla_steps(kv_len(a, i)) : 0;
       const int64_t incl = wave_incl_scan64(n, lane) + carry;
       const uint64_t hit = __ballot(i < nb && n > 0 && incl - n <= x && x < incl);
       if (hit) {
@@ -1551,7 +1559,7 @@ void mla_decode_kernel(MlaArgs a) {
   b = uniform64(b);
   pb = uniform64(pb);
   for (int64_t g = g0; g < g1;) {
-    const int64_t len = a.lens[b];
+    const int64_t len = kv_len(a, b);
     const int64_t n = mla_steps(len);
     const int64_t seg = min(g1 - g, pb + n - x);
     const int64_t t_begin = (x - pb) * kMlaStep;
@@ -1568,7 +1576,7 @@ void mla_decode_kernel(MlaArgs a) {
       pb += n;
       do {
         if (++b == nb) { b = 0; pb = 0; x = 0; ++hg; }
-      } while (g < g1 && mla_steps(a.lens[b]) == 0);
+      } while (g < g1 && mla_steps(kv_len(a, b)) == 0);
     }
   }
   if (!RESCALE && lane == 0) *wgflag = ov_seen ? 1 : 0;
@@ -1589,7 +1597,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a, uint16_t* o
   const int h0 = static_cast<int>(blockIdx.x % per_b) * kMlaCombineHeads + 2 * wv;
   if (h0 >= a.hq) return;
   const bool two = h0 + 1 < a.hq;
-  const int64_t n = mla_steps(a.lens[b]);
+  const int64_t n = mla_steps(kv_len(a, b));
   uint4* o0 = reinterpret_cast<uint4*>(out + (b * a.hq + h0) * DN) + lane;
   uint4* o1 = reinterpret_cast<uint4*>(out + (b * a.hq + h0 + 1) * DN) + lane;
   if (n == 0) {
@@ -1793,6 +1801,7 @@ extern "C" int tai_fia_prefill(const void* q, const void* k, const void* v, int6
   a.lse = lse;
   for (int i = 0; i < 3; ++i) { a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = out_strides[i]; }
   a.lq = seq_lens_q; a.lkv = seq_lens_kv; a.b = b; a.s_q = s_q; a.s_kv = s_kv;
+  a.kv_cap = block_table ? max_blocks * block_size : s_kv;
   a.hq = hq; a.hkv = hkv; a.g = hq / hkv;
   // pre / next beyond 2^40 tokens are no bound (keeps the kernel's position arithmetic in range)
   constexpr int64_t kNoBound = int64_t(1) << 40;

@@ -40,8 +40,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const int64_t item = in_range ? item0 : 0;
   const int64_t i = item % a.s_q, h = (item / a.s_q) % a.hq, b = item / (a.s_q * a.hq);
   const int kvh = static_cast<int>(h / (a.hq / a.hkv));
-  const int64_t lq = a.seq_lens_q ? a.seq_lens_q[b] : a.s_q;
-  const int64_t lk = a.seq_lens_kv ? a.seq_lens_kv[b] : a.s_kv;
+  // lengths read on the device are clamped to what the inputs hold (s_q; s_kv, or the blocks a
+  // block-table row can address)
+  const int64_t lq = a.seq_lens_q ? imax64(0, imin64(a.seq_lens_q[b], a.s_q)) : a.s_q;
+  const int64_t kv_cap = a.block_table ? a.max_blocks * a.block_size : a.s_kv;
+  const int64_t lk = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
   uint16_t* op = static_cast<uint16_t*>(a.out) + b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
   const int dk = a.dk1 + a.dk2;
   // the query as fp32 in this wave's LDS row

@@ -31,14 +31,21 @@ def preparing_capture() -> bool:
     return getattr(_state, "warmup", False)
 
 
-def _signature(args: Sequence[Any], by_pointer: Sequence[bool]) -> Tuple:
+def capture_resources():
+    """The dict of host-side resources owned by the graph being prepared or captured on this thread
+    (None outside a capture). Ops keep what a captured graph reads at replay time (pinned buffers)
+    there, so it lives exactly as long as that graph."""
+    return getattr(_state, "resources", None)
+
+
+def _signature(args: Sequence[Any], pinned: Sequence[bool]) -> Tuple:
     sig = []
-    for a, ptr in zip(args, by_pointer):
+    for a, pin in zip(args, pinned):
         if isinstance(a, torch.Tensor):
-            # an input used in place is part of the captured graph by its address: another address
-            # captures anew, as the reference re-captures when a mutated input moves
-            # (acl_graph.py:1195, 1368-1372)
-            sig.append(("T", tuple(a.shape), tuple(a.stride()), a.dtype, str(a.device), a.data_ptr() if ptr else None))
+            # a parameter or an input the graph writes in place is part of the captured graph by its
+            # address: another address captures anew, as the reference re-captures when a mutated
+            # input or a parameter moves (acl_graph.py:1195, 1361-1372)
+            sig.append(("T", tuple(a.shape), tuple(a.stride()), a.dtype, str(a.device), a.data_ptr() if pin else None))
         else:
             sig.append(("V", a))
     return tuple(sig)
@@ -47,18 +54,32 @@ def _signature(args: Sequence[Any], by_pointer: Sequence[bool]) -> Tuple:
 class _Captured:
     """One captured graph. Inputs passed by pointer (parameters, inputs the graph writes in place,
     or every tensor when ``clone_input`` is off) are used as they are; the others are copied into
-    graph-owned buffers before each replay."""
+    graph-owned buffers before each replay. A by-pointer input that is neither a parameter nor
+    written in place is retained at its capture-time address; a replay that passes another tensor
+    there copies it into the retained one first (acl_graph.py:1329-1337)."""
 
-    def __init__(self, fn: Callable, args: Sequence[Any], by_pointer: Sequence[bool]):
+    def __init__(self, fn: Callable, args: Sequence[Any], by_pointer: Sequence[bool], pinned: Sequence[bool]):
         self.copy_idx: List[int] = []
+        self.moved_idx: List[Tuple[int, int]] = []
         self.inputs: List[Any] = []
-        for i, (a, ptr) in enumerate(zip(args, by_pointer)):
+        for i, (a, ptr, pin) in enumerate(zip(args, by_pointer, pinned)):
             if isinstance(a, torch.Tensor) and not ptr:
                 self.copy_idx.append(i)
                 self.inputs.append(a.clone())
             else:
+                if isinstance(a, torch.Tensor) and not pin:
+                    self.moved_idx.append((i, a.data_ptr()))
                 self.inputs.append(a)
         dev = next((a.device for a in args if isinstance(a, torch.Tensor)), torch.device("cuda"))
+        self.resources: Dict[Any, Any] = {}
+        _state.resources = self.resources
+        try:
+            self._capture(fn, dev)
+        finally:
+            _state.resources = None
+        stats["captures"] += 1
+
+    def _capture(self, fn: Callable, dev: torch.device):
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -74,11 +95,13 @@ class _Captured:
         with torch.cuda.graph(self.graph):
             out = fn(*self.inputs)
         self.outputs = out
-        stats["captures"] += 1
 
     def run(self, args: Sequence[Any]):
         for i in self.copy_idx:
             self.inputs[i].copy_(args[i])
+        for i, ptr in self.moved_idx:
+            if args[i].data_ptr() != ptr:
+                self.inputs[i].copy_(args[i])
         self.graph.replay()
         return self.outputs
 
@@ -103,11 +126,16 @@ class HipGraphRunner:
         return [isinstance(a, torch.Tensor) and (not self.clone_input or isinstance(a, torch.nn.Parameter)
                                                  or i in self.mutated_inputs) for i, a in enumerate(args)]
 
+    def _pinned(self, args) -> List[bool]:
+        return [isinstance(a, torch.Tensor) and (isinstance(a, torch.nn.Parameter) or i in self.mutated_inputs)
+                for i, a in enumerate(args)]
+
     def __call__(self, *args):
         if not any(isinstance(a, torch.Tensor) and a.is_cuda for a in args):
             return self.fn(*args)
         by_ptr = self._by_pointer(args)
-        key = _signature(args, by_ptr)
+        pinned = self._pinned(args)
+        key = _signature(args, pinned)
         entry = self.graphs.get(key)
         if entry is None:
             if len(self.graphs) >= self.capture_limit:
@@ -116,7 +144,7 @@ class HipGraphRunner:
                     self._warned = True
                 stats["eager_fallbacks"] += 1
                 return self.fn(*args)
-            entry = _Captured(self.fn, args, by_ptr)
+            entry = _Captured(self.fn, args, by_ptr, pinned)
             self.graphs[key] = entry
             out = entry.first_outputs
             entry.first_outputs = None
