@@ -72,3 +72,15 @@ def test_mla_fast_pass_reads_no_mfma_result_early(tmp_path):
     body = text[start:text.index("s_endpgm", start)].splitlines()
     assert any("v_mfma_f32_32x32x16_bf16 v[" in l for l in body), "expected VGPR-destination MFMAs"
     assert hazards(body) == []
+
+
+def test_no_inline_asm_vector_memory_stores():
+    """A vector-memory store written as inline asm hides its data registers from the compiler's hazard
+    recognizer: the next VALU may overwrite them before the store has read them (a >8-byte store
+    reads its data over several cycles), which corrupted grouped-GEMM output rows. Stores with a
+    cache policy use the compiler's non-temporal store on a global-address-space pointer instead."""
+    csrc = SRC.parent
+    pat = re.compile(r'asm\s+volatile\(\s*"\s*(global|buffer|flat|scratch)_store')
+    offenders = [f"{p.name}:{i + 1}" for p in sorted(csrc.glob("*.hip"))
+                 for i, line in enumerate(p.read_text().splitlines()) if pat.search(line)]
+    assert offenders == []

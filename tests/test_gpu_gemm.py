@@ -245,3 +245,28 @@ def test_packed_int64_scales_are_refused(dt):
         torch.ops.npu.npu_grouped_matmul([x], [w.unsqueeze(0)], scale=[scale.unsqueeze(0)],
                                          group_list=torch.tensor([8], device=DEV), split_item=3, group_type=0,
                                          group_list_type=1, output_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("out", ["int32", "bf16"])
+def test_grouped_matmul_mixed_tiles(out):
+    """[K, N] weights with n % 512 == 0 run 128 x 512 and 256 x 256 tiles side by side: groups of
+    1 to 5 row slots of 128 (odd last slots stay 128 x 512), an empty group and 5 trailing rows past
+    the grouped total (zero-filled)."""
+    g = gen(26)
+    counts = torch.tensor([1, 128, 129, 256, 0, 257, 384, 385, 600, 64], dtype=torch.int64)
+    x, w, counts = _gmm_case(g, len(counts), 0, 192, 1024, counts)
+    kw = {}
+    if out == "bf16":
+        sc = uniform((len(counts), 1024), g, 1e-3, 1e-2)
+        pts = uniform((x.shape[0],), g, 1e-3, 1e-2)
+        kw = dict(scale=[sc.to(DEV)], per_token_scale=[pts.to(DEV)])
+    got = torch.ops.npu.npu_grouped_matmul([x.to(DEV)], [w.to(DEV)], group_list=counts.to(DEV), split_item=3,
+                                           group_type=0, group_list_type=1,
+                                           output_dtype=torch.int32 if out == "int32" else torch.bfloat16, **kw)[0]
+    acc = G.grouped_matmul(x.numpy(), w.numpy(), counts.numpy(), 1, out_dtype="int32")
+    if out == "int32":
+        np.testing.assert_array_equal(got.cpu().numpy(), acc)
+    else:
+        want = G.grouped_matmul(x.numpy(), w.numpy(), counts.numpy(), 1, scale=sc.numpy(), per_token_scale=pts.numpy(),
+                                out_dtype="bf16")
+        np.testing.assert_array_equal(f32np(got), want)

@@ -122,6 +122,41 @@ __device__ __forceinline__ int grouped_tile(const GemmArgs& g, int64_t L, int bm
   return t.x;
 }
 
+// Mixed tiles (grouped [K, N] weights, n % 512 == 0). The slot table is built for 128-row tiles and
+// each slot stands for n_tiles units of 128 x 512 outputs. A group with rt >= 2 row slots runs its
+// first 2 * (rt / 2) slots as 256-row tiles of 256 columns (the same number of units), so each of its
+// weight slices is read by half as many row tiles; an odd last slot stays a 128 x 512 tile. Tall
+// tiles that share a 256-column slice are consecutive in L, as in grouped_tile.
+__device__ __forceinline__ int grouped_tile_mixed(const GemmArgs& g, int64_t L, int& row0, int& row1, int64_t& nt,
+                                                  int64_t& rt_out, bool& tall) {
+  const int64_t s0 = L / g.n_tiles;
+  const int4 t = g.tile_map[s0];
+  tall = false;
+  rt_out = 1;
+  if (t.x < 0) {
+    row0 = t.y;
+    row1 = t.z;
+    nt = L % g.n_tiles;
+    return t.x;
+  }
+  const int64_t first = s0 - t.w;
+  const int64_t rt = (static_cast<int64_t>(t.z) - t.y + 127) / 128;
+  const int64_t pairs = rt / 2;
+  const int64_t off = L - first * g.n_tiles;
+  if (off < pairs * 2 * g.n_tiles) {
+    tall = true;
+    nt = off / pairs;
+    row0 = t.y + static_cast<int>(off % pairs) * 256;
+    row1 = row0 + 256 < t.z ? row0 + 256 : t.z;
+  } else {
+    nt = off - pairs * 2 * g.n_tiles;
+    row0 = t.y + static_cast<int>(pairs) * 256;
+    row1 = t.z;
+  }
+  rt_out = pairs + (rt & 1);  // row tiles that read this tile's weight columns
+  return t.x;
+}
+
 // 4x4 byte transpose: in[r] holds bytes (r,0..3); out[c] holds bytes (0..3,c).
 __device__ __forceinline__ void transpose4x4(const uint32_t (&in)[4], uint32_t (&out)[4]) {
   const uint32_t lo01 = perm_b32(in[1], in[0], 0x05010400u);
@@ -630,28 +665,14 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&
   }
 }
 
+// One tile of the big-tile kernel: rows [row0, row1) of group e (dense: e = 0), column tile nt,
+// linear tile id L (split-K slice); row_tiles = row tiles of the group that share this tile's
+// weight slice. e = -1: nothing to do, e = -2: zero-fill rows past the grouped total.
 template <int LAYOUT, int OUT, class C>
-__global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g) {
+__device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_t L, int e, int row0, int row1,
+                                         int64_t nt, int64_t row_tiles) {
   constexpr int WN = C::kBN / 128;
   constexpr int kBigBK = C::kBK;
-  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-
-  const int64_t L = tile_id(g, blockIdx.x);
-  if (L < 0) return;
-  int64_t slot = 0, nt, row_tiles = 0;
-  int e = 0, row0, row1;
-  if (g.tile_map) {
-    e = grouped_tile(g, L, C::kBM, row0, row1, nt, row_tiles);
-  } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
-    constexpr int64_t GM = 8;
-    const int64_t per_group = GM * g.n_tiles;
-    const int64_t Lt = g.k_split > 1 ? L % (g.m_slots * g.n_tiles) : L;  // split-K: slice = L / tiles
-    const int64_t first = (Lt / per_group) * GM;
-    const int64_t gsize = g.m_slots - first < GM ? g.m_slots - first : GM;
-    const int64_t in = Lt % per_group;
-    slot = first + in % gsize;
-    nt = in / gsize;
-  }
   const int64_t n0 = nt * C::kBN;
   if (g.tile_map) {
     if (e == -1) return;
@@ -674,9 +695,6 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
       }
       return;
     }
-  } else {
-    row0 = static_cast<int>(slot * C::kBM);
-    row1 = row0 + C::kBM < g.m ? row0 + C::kBM : static_cast<int>(g.m);
   }
   const int rows = row1 - row0;
   const int8_t* bgrp = g.b + static_cast<int64_t>(e) * g.b_group_stride;
@@ -953,10 +971,11 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
             // projection -2%, the config-4 GEMM + quant + GEMM + finalize chain -0.7%); split-K
             // partials, re-read at once by the reduction, and dense outputs keep the default policy
             if (nt_out) {
-              // the `nt` bit written by hand: the compiler's non-temporal store builtin sets no cache
-              // policy on gfx950
+              // a compiler-visible store (an inline-asm store hid its data registers from the
+              // hazard recognizer, which then let the next VALU overwrite them too early)
               const v4i d{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-              asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(dst), "v"(d) : "memory");
+              typedef __attribute__((address_space(1))) v4i gv4i;
+              __builtin_nontemporal_store(d, (gv4i*)(reinterpret_cast<uintptr_t>(dst)));
             } else {
               *dst = tai_u32x4_t{v.x, v.y, v.z, v.w};
             }
@@ -989,6 +1008,30 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g)
       }
     }
   }
+}
+
+template <int LAYOUT, int OUT, class C>
+__global__ __launch_bounds__(C::kThreads, 2) void gemm_i8_big_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const int64_t L = tile_id(g, blockIdx.x);
+  if (L < 0) return;
+  int64_t nt, row_tiles = 0;
+  int e = 0, row0, row1;
+  if (g.tile_map) {
+    e = grouped_tile(g, L, C::kBM, row0, row1, nt, row_tiles);
+  } else {  // dense: groups of 8 row tiles walk the column tiles together (A and B reuse in L2)
+    constexpr int64_t GM = 8;
+    const int64_t per_group = GM * g.n_tiles;
+    const int64_t Lt = g.k_split > 1 ? L % (g.m_slots * g.n_tiles) : L;  // split-K: slice = L / tiles
+    const int64_t first = (Lt / per_group) * GM;
+    const int64_t gsize = g.m_slots - first < GM ? g.m_slots - first : GM;
+    const int64_t in = Lt % per_group;
+    const int64_t slot = first + in % gsize;
+    nt = in / gsize;
+    row0 = static_cast<int>(slot * C::kBM);
+    row1 = row0 + C::kBM < g.m ? row0 + C::kBM : static_cast<int>(g.m);
+  }
+  big_tile<LAYOUT, OUT, C>(g, smem, L, e, row0, row1, nt, row_tiles);
 }
 
 // Tile configurations used by the host (8 waves of 64 x 128, 256 x 256 tiles):
@@ -1051,6 +1094,55 @@ bool cfg_available() {
     return ok;
   }();
   return cached;
+}
+
+// Grouped [K, N] weights with mixed tiles (grouped_tile_mixed): 128 x 512 (GrpKnSel) or 256 x 256.
+using MixTall = BigCfg<4, 2, 64, 4>;
+#ifndef TAI_MIXED
+#define TAI_MIXED 1
+#endif
+template <int OUT>
+__global__ __launch_bounds__(GrpKnSel::kThreads, 2) void gemm_i8_mixed_kernel(GemmArgs g) {
+  static_assert(GrpKnSel::kThreads == MixTall::kThreads && GrpKnSel::kBN == 512 && MixTall::kBM == 256,
+                "mixed tiles: both shapes cover 128 x 512 outputs with one workgroup size");
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const int64_t L = tile_id(g, blockIdx.x);
+  if (L < 0) return;
+  int64_t nt, row_tiles;
+  int row0, row1;
+  bool tall;
+  const int e = grouped_tile_mixed(g, L, row0, row1, nt, row_tiles, tall);
+  if (tall) big_tile<TAI_LAYOUT_KN, OUT, MixTall>(g, smem, L, e, row0, row1, nt, row_tiles);
+  else big_tile<TAI_LAYOUT_KN, OUT, GrpKnSel>(g, smem, L, e, row0, row1, nt, row_tiles);
+}
+
+bool mixed_available() {
+  static const bool ok = [] {
+    if (!cfg_available<GrpKnSel>()) return false;
+    constexpr int lds = GrpKnSel::kLds > MixTall::kLds ? GrpKnSel::kLds : MixTall::kLds;
+    auto set = [](const void* f) {
+      return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess;
+    };
+    const bool r = set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_INT32>)) &&
+                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_BF16>)) &&
+                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_FP16>)) &&
+                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_FP32>));
+    (void)hipGetLastError();
+    return r;
+  }();
+  return ok;
+}
+
+void launch_mixed(const GemmArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(g.m_slots * g.n_tiles));
+  constexpr int T = GrpKnSel::kThreads;
+  constexpr size_t L = GrpKnSel::kLds > MixTall::kLds ? GrpKnSel::kLds : MixTall::kLds;
+  switch (g.out_dt) {
+    case TAI_DT_INT32: gemm_i8_mixed_kernel<TAI_DT_INT32><<<grid, T, L, st>>>(g); break;
+    case TAI_DT_BF16: gemm_i8_mixed_kernel<TAI_DT_BF16><<<grid, T, L, st>>>(g); break;
+    case TAI_DT_FP16: gemm_i8_mixed_kernel<TAI_DT_FP16><<<grid, T, L, st>>>(g); break;
+    default: gemm_i8_mixed_kernel<TAI_DT_FP32><<<grid, T, L, st>>>(g); break;
+  }
 }
 
 template <class C, int LAYOUT>
@@ -1790,7 +1882,8 @@ static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m,
     gemm_i8_generic_kernel<<<dim3(static_cast<unsigned>(cdiv(m * n, 256))), 256, 0, st>>>(g, w_layout, row_group);
     return launch_status("tai_grouped_matmul");
   }
-  if (big && kn) launch_cfg<GrpKnSel>(g, w_layout, st);
+  if (big && kn && TAI_MIXED && n % GrpKnSel::kBN == 0 && mixed_available()) launch_mixed(g, st);
+  else if (big && kn) launch_cfg<GrpKnSel>(g, w_layout, st);
   else if (big) launch_cfg<GrpSel>(g, w_layout, st);
   else launch_tile<128, 128>(g, w_layout, st);
   return launch_status("tai_grouped_matmul");
