@@ -620,7 +620,7 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&
         const int64_t oc = n0 / 2 + 64 * wn + 32 * j + (lane & 31);
         const float dg = (static_cast<float>(acc[i][j][r]) * wg[j]) * xs;
         const float du = (static_cast<float>(acc[i][j + 2][r]) * wu[j]) * xs;
-        const float hv = (dg / (1.0f + expf(-dg))) * du;
+        const float hv = silu_f32(dg) * du;
         if (live) g.h[static_cast<int64_t>(row0 + lr) * n2 + oc] = hv;
         m = fmaxf(m, fabsf(hv));
       }
@@ -1557,16 +1557,13 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
   float amax = 0.0f;
   for (int64_t p = lane; p < nparts; p += 64) amax = fmaxf(amax, part[row * nparts + p]);
   amax = wave_max(amax);
-  const float sc = amax / 127.0f;
+  const float sc = amax / 127.0f, inv = rcp_f32(sc);
   for (int64_t c = 4 * lane; c < n2; c += 256) {
     const float4 v = *reinterpret_cast<const float4*>(h + row * n2 + c);
     const float vv[4] = {v.x, v.y, v.z, v.w};
     uint32_t word = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(vv[q] / sc), -128.0f), 127.0f);
-      word |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(r)))) << (8 * q);
-    }
+    for (int q = 0; q < 4; ++q) word |= static_cast<uint32_t>(static_cast<uint8_t>(quant_i8(vv[q], sc, inv))) << (8 * q);
     *reinterpret_cast<uint32_t*>(y + row * n2 + c) = word;
   }
   if (lane == 0) scale[row] = sc;

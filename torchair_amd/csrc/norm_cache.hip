@@ -73,11 +73,8 @@ __device__ __forceinline__ void load8_f32_or_one(const float* p, int64_t idx, fl
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-__device__ __forceinline__ int8_t quant1(float v, float scale) {
-  if (scale == 0.0f) return 0;
-  const float q = fminf(fmaxf(rintf(v / scale), -128.0f), 127.0f);
-  return static_cast<int8_t>(static_cast<int>(q));
-}
+// rint(v / scale) saturated to int8 (the IEEE divide's result; see quant_i8)
+__device__ __forceinline__ int8_t quant1(float v, float scale) { return quant_i8(v, scale, rcp_f32(scale)); }
 
 __device__ __forceinline__ uint2 pack8(const float (&v)[kVec], float scale) {
   uint32_t w[2] = {0, 0};

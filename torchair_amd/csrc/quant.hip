@@ -41,12 +41,8 @@ struct Vec8 {  // loads 8 elements as fp32 (non-temporal: the quantiser reads it
   }
 };
 
-__device__ __forceinline__ int8_t quant1(float v, float scale) {
-  if (scale == 0.0f) return 0;
-  float q = rintf(v / scale);
-  q = fminf(fmaxf(q, -128.0f), 127.0f);
-  return static_cast<int8_t>(static_cast<int>(q));
-}
+// rint(v / scale) saturated to int8 (the IEEE divide's result; see quant_i8)
+__device__ __forceinline__ int8_t quant1(float v, float scale) { return quant_i8(v, scale, rcp_f32(scale)); }
 
 __device__ __forceinline__ uint2 pack8(const float (&v)[kVec], float scale) {
   uint32_t w[2] = {0, 0};
@@ -201,112 +197,138 @@ struct DsqArgs {
   float* scale;
 };
 
-__device__ __forceinline__ float silu(float a) { return a / (1.0f + expf(-a)); }
+__device__ __forceinline__ float silu(float a) { return silu_f32(a); }
 
-// Finds the group of `row` from per-group row counts with a workgroup-wide scan (one count per
-// thread per pass, wave scans joined through LDS). Returns -1 when the row is past the total.
-// Every thread of the workgroup must call it.
-__device__ int64_t group_of_row_counts(const void* counts, int dt, int64_t ng, int64_t row) {
-  __shared__ int64_t red[16];
-  __shared__ int64_t found;
-  if (threadIdx.x == 0) found = -1;
-  const int nw = static_cast<int>(blockDim.x >> 6);
-  int64_t carry = 0;
-  for (int64_t base = 0; base < ng; base += blockDim.x) {
-    const int64_t g = base + threadIdx.x;
-    const int64_t c = g < ng ? load_index(counts, dt, g) : 0;
-    const int64_t end = carry + block_incl_scan<false>(c, red);
-    if (g < ng && row >= end - c && row < end) found = g;
-    for (int i = 0; i < nw; ++i) carry += red[i];
-    __syncthreads();
-    if (found >= 0 || carry > row) break;
-  }
-  return found;
-}
-
-// One workgroup of TPB threads per row; each thread owns NV groups of 4 output columns.
-template <int NV, int TPB = 256>
+#ifndef TAI_DSQ_NT
+#define TAI_DSQ_NT 1
+#endif
+#ifndef TAI_DSQ_RPB
+#define TAI_DSQ_RPB 2
+#endif
+// RPB consecutive rows per workgroup of TPB threads; each thread owns NV groups of 4 output columns
+// of every row. All rows' int32 loads go out first, then each wave finds the rows' groups on its own
+// (a row usually shares its predecessor's group, which is then reused), so the per-row cost of the
+// group lookup and of the workgroup reduction is shared by RPB rows.
+template <int NV, int TPB = 256, int RPB = 1>
 __global__ __launch_bounds__(TPB) void dsq_kernel(DsqArgs a) {
-  __shared__ float red[TPB / 64];
-  const int64_t row = blockIdx.x;
+  __shared__ float red[RPB][TPB / 64];
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB;
   const int tid = threadIdx.x;
   const int64_t n = a.n, n2 = 2 * a.n;
   const int64_t ng4 = n / 4;
-  const int32_t* xr = a.x + row * n2;
-  // The row's int32 values do not depend on its group: their loads go out before the lookup.
-  int4 xa[NV], xb[NV];
+  // The rows' int32 values do not depend on their groups: their loads go out before the lookups.
+  int4 xa[RPB][NV], xb[RPB][NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
-    if (c < ng4) {
-      xa[i] = *reinterpret_cast<const int4*>(xr + 4 * c);
-      xb[i] = *reinterpret_cast<const int4*>(xr + n + 4 * c);
-    }
-  }
-  int64_t g = 0;
-  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row);
-  if (g < 0) {  // row beyond the grouped rows
-    for (int64_t c = tid; c < ng4; c += TPB)
-      *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = 0u;
-    if (tid == 0) a.scale[row] = 0.0f;
-    return;
-  }
-  const float* ws = a.ws ? a.ws + g * n2 : nullptr;
-  const float* qs = a.qs ? a.qs + g * n : nullptr;
-  const float act = a.as ? a.as[row] : 1.0f;
-  const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
-  const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
-
-  float v[NV][4];
-  float amax = 0.0f;
+  for (int r = 0; r < RPB; ++r) {
+    const int32_t* xr = a.x + (row0 + r < a.rows ? row0 + r : row0) * n2;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
-    if (c < ng4) {
-      const int64_t j = 4 * c;
-      int ia[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w}, ib[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
-      if (bi) {
-        int4 ba = *reinterpret_cast<const int4*>(bi + j), bb = *reinterpret_cast<const int4*>(bi + n + j);
-        ia[0] += ba.x; ia[1] += ba.y; ia[2] += ba.z; ia[3] += ba.w;
-        ib[0] += bb.x; ib[1] += bb.y; ib[2] += bb.z; ib[3] += bb.w;
-      }
-      float wa[4] = {1.f, 1.f, 1.f, 1.f}, wb[4] = {1.f, 1.f, 1.f, 1.f};
-      if (ws) {
-        float4 p = *reinterpret_cast<const float4*>(ws + j), q = *reinterpret_cast<const float4*>(ws + n + j);
-        wa[0] = p.x; wa[1] = p.y; wa[2] = p.z; wa[3] = p.w;
-        wb[0] = q.x; wb[1] = q.y; wb[2] = q.z; wb[3] = q.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float da = static_cast<float>(ia[e]) * wa[e];
-        float db = static_cast<float>(ib[e]) * wb[e];
-        if (a.as) { da *= act; db *= act; }
-        if (bf) { da += bf[j + e]; db += bf[n + j + e]; }
-        float r = a.left ? silu(da) * db : da * silu(db);
-        if (qs) r *= qs[j + e];
-        v[i][e] = r;
-        amax = fmaxf(amax, fabsf(r));
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + static_cast<int64_t>(i) * TPB;
+      if (c < ng4) {
+#if TAI_DSQ_NT
+        xa[r][i] = load_nt_i4(xr + 4 * c);  // each int32 input is read once
+        xb[r][i] = load_nt_i4(xr + n + 4 * c);
+#else
+        xa[r][i] = *reinterpret_cast<const int4*>(xr + 4 * c);
+        xb[r][i] = *reinterpret_cast<const int4*>(xr + n + 4 * c);
+#endif
       }
     }
   }
-  amax = wave_max(amax);
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  int64_t grp[RPB];
+  {
+    int64_t g = -1, gbeg = 0, gend = 0;  // last group found and its row range
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) {
+      const int64_t row = row0 + r;
+      if (a.gidx == nullptr) {
+        grp[r] = 0;
+      } else if (g >= 0 && row >= gbeg && row < gend) {
+        grp[r] = g;
+      } else {
+        g = group_of_row_wave(a.gidx, a.gidx_dt, a.ngroups, row, gbeg, gend);
+        grp[r] = g;
+      }
+    }
+  }
+  float v[RPB][NV][4];
+  float amax[RPB];
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    amax[r] = 0.0f;
+    const int64_t g = grp[r];
+    if (g < 0) {  // row past the grouped rows (or past the end): y 0, scale 0
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[r][i][e] = 0.0f;
+      continue;
+    }
+    const int64_t row = row0 + r;
+    const float* ws = a.ws ? a.ws + g * n2 : nullptr;
+    const float* qs = a.qs ? a.qs + g * n : nullptr;
+    const float act = a.as ? a.as[row < a.rows ? row : 0] : 1.0f;
+    const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
+    const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + static_cast<int64_t>(i) * TPB;
+      if (c < ng4) {
+        const int64_t j = 4 * c;
+        int ia[4] = {xa[r][i].x, xa[r][i].y, xa[r][i].z, xa[r][i].w};
+        int ib[4] = {xb[r][i].x, xb[r][i].y, xb[r][i].z, xb[r][i].w};
+        if (bi) {
+          int4 ba = *reinterpret_cast<const int4*>(bi + j), bb = *reinterpret_cast<const int4*>(bi + n + j);
+          ia[0] += ba.x; ia[1] += ba.y; ia[2] += ba.z; ia[3] += ba.w;
+          ib[0] += bb.x; ib[1] += bb.y; ib[2] += bb.z; ib[3] += bb.w;
+        }
+        float wa[4] = {1.f, 1.f, 1.f, 1.f}, wb[4] = {1.f, 1.f, 1.f, 1.f};
+        if (ws) {
+          float4 p = *reinterpret_cast<const float4*>(ws + j), q = *reinterpret_cast<const float4*>(ws + n + j);
+          wa[0] = p.x; wa[1] = p.y; wa[2] = p.z; wa[3] = p.w;
+          wb[0] = q.x; wb[1] = q.y; wb[2] = q.z; wb[3] = q.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float da = static_cast<float>(ia[e]) * wa[e];
+          float db = static_cast<float>(ib[e]) * wb[e];
+          if (a.as) { da *= act; db *= act; }
+          if (bf) { da += bf[j + e]; db += bf[n + j + e]; }
+          float rv = a.left ? silu(da) * db : da * silu(db);
+          if (qs) rv *= qs[j + e];
+          v[r][i][e] = rv;
+          amax[r] = fmaxf(amax[r], fabsf(rv));
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    const float m = wave_max(amax[r]);
+    if ((tid & 63) == 0) red[r][tid >> 6] = m;
+  }
   __syncthreads();
-  amax = red[0];
 #pragma unroll
-  for (int q = 1; q < TPB / 64; ++q) amax = fmaxf(amax, red[q]);
-  const float scale = amax / 127.0f;
+  for (int r = 0; r < RPB; ++r) {
+    const int64_t row = row0 + r;
+    if (row >= a.rows) break;
+    float m = red[r][0];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * TPB;
-    if (c < ng4) {
-      uint32_t w = 0;
+    for (int q = 1; q < TPB / 64; ++q) m = fmaxf(m, red[r][q]);
+    const float scale = m / 127.0f, inv = rcp_f32(scale);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w |= static_cast<uint32_t>(static_cast<uint8_t>(quant1(v[i][e], scale))) << (8 * e);
-      *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = w;
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + static_cast<int64_t>(i) * TPB;
+      if (c < ng4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w |= static_cast<uint32_t>(static_cast<uint8_t>(quant_i8(v[r][i][e], scale, inv))) << (8 * e);
+        *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = w;
+      }
     }
+    if (tid == 0) a.scale[row] = scale;
   }
-  if (tid == 0) a.scale[row] = scale;
 }
 
 // Any n: two passes over global memory.
@@ -315,7 +337,7 @@ __global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
   const int64_t row = blockIdx.x;
   const int64_t n = a.n, n2 = 2 * a.n;
   int64_t g = 0;
-  if (a.gidx != nullptr) g = group_of_row_counts(a.gidx, a.gidx_dt, a.ngroups, row);
+  if (a.gidx != nullptr) g = group_of_row_wave(a.gidx, a.gidx_dt, a.ngroups, row);
   if (g < 0) {
     for (int64_t c = threadIdx.x; c < n; c += blockDim.x) a.y[row * n + c] = 0;
     if (threadIdx.x == 0) a.scale[row] = 0.0f;
@@ -502,7 +524,9 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
   if (aligned && rows <= 512 && ng4 > 512 && ng4 <= 1024 * 2) {
     if (ng4 <= 1024) dsq_kernel<1, 1024><<<grid, 1024, 0, st>>>(a);
     else dsq_kernel<2, 1024><<<grid, 1024, 0, st>>>(a);
-  } else if (aligned && ng4 <= 256 * 2) dsq_kernel<2><<<grid, 256, 0, st>>>(a);
+  } else if (aligned && ng4 <= 256 * 2) {
+    dsq_kernel<2, 256, TAI_DSQ_RPB><<<dim3(static_cast<unsigned>(cdiv(rows, TAI_DSQ_RPB))), 256, 0, st>>>(a);
+  }
   else if (aligned && ng4 <= 256 * 4) dsq_kernel<4><<<grid, 256, 0, st>>>(a);
   else if (aligned && ng4 <= 256 * 8) dsq_kernel<8><<<grid, 256, 0, st>>>(a);
   else dsq_generic_kernel<<<grid, 256, 0, st>>>(a);
