@@ -57,6 +57,11 @@ int tai_abi_version(void);
 /* Hash of the sources and build flags the library was compiled from. The Python loader refuses a
  * library whose id differs from the hash of the sources beside it (a stale build). */
 const char* tai_build_id(void);
+/* Measurement helper, no counterpart in the reference: reads read_bytes of src once (non-temporal
+ * 16-byte loads) and then writes write_bytes to dst. Its known byte counts give the read-dominated
+ * HBM rate that the benchmark compares read-heavy kernels with. Sizes: multiples of 16 bytes,
+ * write_bytes <= read_bytes (the words written are copies of words read). */
+int tai_calib_read_stream(const void* src, size_t read_bytes, void* dst, size_t write_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_dynamic_quant: symmetric per-row int8 quantisation.

@@ -39,6 +39,7 @@ _SIGS = {
     "tai_last_error": (c_char_p, []),
     "tai_abi_version": (c_int, []),
     "tai_build_id": (c_char_p, []),
+    "tai_calib_read_stream": (c_int, [_P, c_size_t, _P, c_size_t, _P]),
     "tai_dynamic_quant": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P]),
     "tai_dequant_swiglu_quant": (
         c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, c_int, c_int64, c_int, _P, _P, _P]),
