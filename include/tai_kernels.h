@@ -382,6 +382,25 @@ typedef struct tai_fia_general_args {
   void* out;
   int64_t out_strides[3];
   float* lse;
+  /* int8 key / value caches (kv_dtype = TAI_DT_INT8; 0 = the query's dtype), dequantised as
+   * (x + offset) * scale: mode 0 per channel, fp32 [hkv * dk1] (key) / [hkv * dv] (value); mode 1 per
+   * token, fp32 element (b, t) at b * tok_stride + t. A null offset is 0. Replaces the key/value
+   * antiquant inputs of ge.FusedInferAttentionScore (experiment_ops.h:3922-3932). */
+  int64_t kv_dtype;
+  const float* k_scale;
+  const float* k_offset;
+  int64_t k_quant_mode;
+  const float* v_scale;
+  const float* v_offset;
+  int64_t v_quant_mode;
+  int64_t tok_stride;
+  /* int8 attention_out (out_dtype = TAI_DT_INT8; 0 = the query's dtype): clamp(rint(o * out_scale +
+   * out_offset), -128, 127), fp32 scale / offset of out_scale_len = 1 or hq * dv entries (channel
+   * h * dv + d); a null offset is 0. Replaces quant_scale2 / quant_offset2 (experiment_ops.h:3943). */
+  int64_t out_dtype;
+  const float* out_scale;
+  const float* out_offset;
+  int64_t out_scale_len;
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 

@@ -544,6 +544,49 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
     return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask)
 
 
+def antiquant_kv(x, scale, offset=None, mode: int = 0):
+    """Dequantisation of an int8 key / value of npu_fused_infer_attention_score:
+    (x + offset) * scale in fp32. x is [B, S, Hkv, D] (dense, or gathered from a paged cache in
+    sequence order); mode 0 (per channel): scale / offset hold Hkv * D values; mode 1 (per token):
+    scale / offset are [B, S'] with S' >= S, token t of sequence b taking entry (b, t).
+
+    The inputs are the antiquant tensors of the prototype (experiment_ops.h:3922-3932:
+    antiquant_scale / antiquant_offset, key_/value_antiquant_scale / _offset with antiquant_mode,
+    key_/value_antiquant_mode), passed on unchanged by the converter
+    (.../custom/fused_infer_attention_score.py:16-27). The formula is the antiquant rule
+    (x + offset) * scale; the reference holds no kernel that fixes its rounding, so it is pinned here by
+    reduction (scale 1 and offset 0 give the integer values themselves; per-channel and per-token
+    scales of one value equal each other).
+    """
+    x = np.asarray(x, F32)
+    b_cnt, s_len, hkv, d = x.shape
+    sc = np.asarray(scale, F32)
+    of = np.zeros_like(sc) if offset is None else np.asarray(offset, F32)
+    if mode == 0:
+        sc = sc.reshape(1, 1, hkv, d)
+        of = of.reshape(1, 1, hkv, d)
+    else:
+        sc = sc.reshape(b_cnt, -1)[:, :s_len].reshape(b_cnt, s_len, 1, 1)
+        of = of.reshape(b_cnt, -1)[:, :s_len].reshape(b_cnt, s_len, 1, 1)
+    return ((x + of) * sc).astype(F32)
+
+
+def quant_attention_out(out, scale2, offset2=None):
+    """int8 attention_out of npu_fused_infer_attention_score with quant_scale2 / quant_offset2
+    (experiment_ops.h:3943; prototype inputs :3925-3926): clamp(rint(o * scale + offset), -128, 127) in
+    fp32, round half to even. out is [B, S, Hq, D] fp32; scale / offset hold 1 value (per tensor) or
+    Hq * D values (channel h * D + d)."""
+    out = np.asarray(out, F32)
+    hq, d = out.shape[2], out.shape[3]
+    sc = np.asarray(scale2, F32).reshape(-1)
+    of = np.zeros_like(sc) if offset2 is None else np.asarray(offset2, F32).reshape(-1)
+    if sc.size != 1:
+        sc = sc.reshape(hq, d)
+        of = of.reshape(hq, d)
+    y = (out * sc).astype(F32) + of
+    return np.clip(np.rint(y.astype(F32)), -128, 127).astype(np.int8)
+
+
 def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_lens, scale: float):
     """npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache.
 

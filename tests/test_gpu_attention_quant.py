@@ -1,0 +1,185 @@
+"""GPU parity: npu_fused_infer_attention_score with int8 key / value caches (antiquant scales and
+offsets, per channel and per token, the separate key_/value_ and the combined antiquant_* forms)
+and with int8 attention_out (quant_scale2 / quant_offset2), against the oracle: attention over the
+dequantised caches (oracle.golden.antiquant_kv), then quant_attention_out for the int8 output.
+Bars: bf16 outputs rtol = atol = 1e-2; int8 outputs within 1 LSB on at most 0.1% of elements."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import torchair_amd  # noqa: F401
+from oracle import golden as G
+from tests.helpers import assert_close, assert_int8_close, f32np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FIA = torch.ops.npu.npu_fused_infer_attention_score
+
+
+def _i8(shape, g):
+    return torch.randint(-128, 128, shape, generator=g, dtype=torch.int8)
+
+
+def _lse(lse, b, hq, s):
+    got = lse.cpu().numpy().reshape(b, hq, s)
+    return np.where(np.isfinite(got), got, -1e30)
+
+
+@pytest.mark.parametrize("with_offset", [False, True])
+def test_dense_prefill_int8_kv_per_channel(with_offset):
+    g = torch.Generator().manual_seed(150)
+    b, s, hq, hkv, d = 2, 96, 8, 2, 128
+    q = torch.randn(b, s, hq, d, generator=g).to(torch.bfloat16)
+    k, v = _i8((b, s, hkv, d), g), _i8((b, s, hkv, d), g)
+    ks = torch.rand(hkv * d, generator=g) * 0.02 + 0.005
+    vs = torch.rand(hkv * d, generator=g) * 0.02 + 0.005
+    ko = (torch.rand(hkv * d, generator=g) * 4 - 2) if with_offset else None
+    vo = (torch.rand(hkv * d, generator=g) * 4 - 2) if with_offset else None
+    lens = [96, 50]
+    kw = dict(key_antiquant_scale=ks.to(DEV), value_antiquant_scale=vs.to(DEV))
+    if with_offset:
+        kw.update(key_antiquant_offset=ko.to(DEV), value_antiquant_offset=vo.to(DEV))
+    out, lse = FIA(q.reshape(b, s, hq * d).to(DEV), k.reshape(b, s, hkv * d).to(DEV), v.reshape(b, s, hkv * d).to(DEV),
+                   actual_seq_lengths=lens, actual_seq_lengths_kv=lens, num_heads=hq, num_key_value_heads=hkv,
+                   input_layout="BSH", scale=1 / math.sqrt(d), sparse_mode=3, softmax_lse_flag=True, **kw)
+    kd = G.antiquant_kv(k.numpy(), ks.numpy(), None if ko is None else ko.numpy(), 0)
+    vd = G.antiquant_kv(v.numpy(), vs.numpy(), None if vo is None else vo.numpy(), 0)
+    want, wl = G.prefill_attention(f32np(q), kd, vd, np.array(lens), np.array(lens), 1, 1 / math.sqrt(d))
+    assert out.dtype == torch.bfloat16
+    assert_close(f32np(out.reshape(b, s, hq, d)), want)
+    np.testing.assert_allclose(_lse(lse, b, hq, s), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+def _paged(lens, hkv, d, bs, g, gen_kv):
+    b = len(lens)
+    nb = [(L + bs - 1) // bs for L in lens]
+    total = sum(nb) + 2
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(b, max(nb), dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    kc, vc = gen_kv((total, bs, hkv, d)), gen_kv((total, bs, hkv, d))
+    return kc, vc, bt
+
+
+def _gather(cache, bt, lens, bs):
+    b, lmax = len(lens), max(lens)
+    out = np.zeros((b, lmax) + tuple(cache.shape[2:]), cache.dtype)
+    for i, L in enumerate(lens):
+        pages = bt[i, :(L + bs - 1) // bs].numpy().astype(np.int64)
+        out[i, :L] = cache[pages].reshape((-1,) + tuple(cache.shape[2:]))[:L]
+    return out
+
+
+@pytest.mark.parametrize("combined", [False, True])
+def test_paged_decode_int8_kv_per_token(combined):
+    """Per-token scales / offsets [B, S] (key_/value_antiquant_mode 1, or the combined [2, B, S]
+    antiquant_scale with antiquant_mode 1) over a paged int8 cache, one query token per sequence."""
+    g = torch.Generator().manual_seed(151)
+    lens, hq, hkv, d, bs = [300, 1, 129, 64], 16, 4, 128, 64
+    b = len(lens)
+    kc, vc, bt = _paged(lens, hkv, d, bs, g, lambda sh: _i8(sh, g))
+    smax = bt.shape[1] * bs
+    ks, vs = torch.rand(b, smax, generator=g) * 0.02 + 0.005, torch.rand(b, smax, generator=g) * 0.02 + 0.005
+    ko, vo = torch.rand(b, smax, generator=g) * 4 - 2, torch.rand(b, smax, generator=g) * 4 - 2
+    q = torch.randn(b, 1, hq * d, generator=g).to(torch.bfloat16)
+    if combined:
+        kw = dict(antiquant_scale=torch.stack([ks, vs]).to(DEV), antiquant_offset=torch.stack([ko, vo]).to(DEV),
+                  antiquant_mode=1)
+    else:
+        kw = dict(key_antiquant_scale=ks.to(DEV), key_antiquant_offset=ko.to(DEV), value_antiquant_scale=vs.to(DEV),
+                  value_antiquant_offset=vo.to(DEV), key_antiquant_mode=1, value_antiquant_mode=1)
+    out, lse = FIA(q.to(DEV), kc.reshape(-1, bs, hkv * d).to(DEV), vc.reshape(-1, bs, hkv * d).to(DEV),
+                   block_table=bt.to(DEV), actual_seq_lengths_kv=lens, num_heads=hq, num_key_value_heads=hkv,
+                   input_layout="BSH", block_size=bs, scale=1 / math.sqrt(d), softmax_lse_flag=True, **kw)
+    kd = G.antiquant_kv(_gather(kc.numpy(), bt, lens, bs), ks.numpy(), ko.numpy(), 1)
+    vd = G.antiquant_kv(_gather(vc.numpy(), bt, lens, bs), vs.numpy(), vo.numpy(), 1)
+    want, wl = G.prefill_attention(f32np(q.reshape(b, 1, hq, d)), kd, vd, np.ones(b, np.int64), np.array(lens), 1,
+                                   1 / math.sqrt(d))
+    assert_close(f32np(out.reshape(b, 1, hq, d)), want)
+    np.testing.assert_allclose(_lse(lse, b, hq, 1), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+def test_paged_multi_token_int8_kv_per_channel_bnsd_cache():
+    """Legacy combined antiquant_scale [2, Hkv * D] per channel, a [blocks, Hkv, bs, D] cache, three
+    query tokens per sequence (bottom-right causal)."""
+    g = torch.Generator().manual_seed(152)
+    lens, lq, hq, hkv, d, bs = [200, 77], 3, 8, 2, 64, 32
+    b = len(lens)
+    kc, vc, bt = _paged(lens, hkv, d, bs, g, lambda sh: _i8(sh, g))
+    sc = torch.rand(2, hkv * d, generator=g) * 0.02 + 0.005
+    q = torch.randn(b, lq, hq * d, generator=g).to(torch.bfloat16)
+    out, _ = FIA(q.to(DEV), kc.permute(0, 2, 1, 3).contiguous().to(DEV), vc.permute(0, 2, 1, 3).contiguous().to(DEV),
+                 block_table=bt.to(DEV), actual_seq_lengths=[lq] * b, actual_seq_lengths_kv=lens, num_heads=hq,
+                 num_key_value_heads=hkv, input_layout="BSH", block_size=bs, scale=1 / math.sqrt(d), sparse_mode=3,
+                 antiquant_scale=sc.to(DEV), antiquant_mode=0)
+    kd = G.antiquant_kv(_gather(kc.numpy(), bt, lens, bs), sc[0].numpy(), None, 0)
+    vd = G.antiquant_kv(_gather(vc.numpy(), bt, lens, bs), sc[1].numpy(), None, 0)
+    want, _ = G.prefill_attention(f32np(q.reshape(b, lq, hq, d)), kd, vd, np.full(b, lq), np.array(lens), 1,
+                                  1 / math.sqrt(d))
+    assert_close(f32np(out.reshape(b, lq, hq, d)), want)
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_int8_attention_out(per_channel):
+    """quant_scale2 (+ quant_offset2) gives an int8 attention_out: rint(o * scale + offset) saturated."""
+    g = torch.Generator().manual_seed(153)
+    b, s, hq, hkv, d = 2, 70, 4, 2, 128
+    q = torch.randn(b, s, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=g).to(torch.bfloat16)
+    n = hq * d if per_channel else 1
+    qs2 = torch.rand(n, generator=g) * 200 + 20
+    qo2 = torch.rand(n, generator=g) * 6 - 3
+    out, _ = FIA(q.to(DEV), k.to(DEV), v.to(DEV), num_heads=hq, num_key_value_heads=hkv, input_layout="BSND",
+                 scale=1 / math.sqrt(d), sparse_mode=3, actual_seq_lengths=[70, 33], actual_seq_lengths_kv=[70, 33],
+                 quant_scale2=qs2.to(DEV), quant_offset2=qo2.to(DEV))
+    assert out.dtype == torch.int8 and out.shape == (b, s, hq, d)
+    o, _ = G.prefill_attention(f32np(q), f32np(k), f32np(v), np.array([70, 33]), np.array([70, 33]), 1,
+                               1 / math.sqrt(d))
+    want = G.quant_attention_out(o, qs2.numpy(), qo2.numpy())
+    assert_int8_close(out.cpu().numpy(), want)
+
+
+def test_int8_kv_and_int8_out_paged_decode_through_the_compiled_graph():
+    """int8 cache, per-channel scales and an int8 output, compiled with get_npu_backend and replayed
+    from the captured graph with new lengths."""
+    g = torch.Generator().manual_seed(154)
+    lens, hq, hkv, d, bs = [500, 130, 7], 8, 8, 128, 128
+    b = len(lens)
+    kc, vc, bt = _paged(lens, hkv, d, bs, g, lambda sh: _i8(sh, g))
+    ks, vs = torch.rand(hkv * d, generator=g) * 0.02, torch.rand(hkv * d, generator=g) * 0.02
+    qs2 = torch.tensor([60.0])
+
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.register_buffer("ks", ks.to(DEV))
+            self.register_buffer("vs", vs.to(DEV))
+            self.register_buffer("qs2", qs2.to(DEV))
+
+        def forward(self, q, kc, vc, bt, lens):
+            # air:: takes the lengths as a device tensor (npu:: takes SymInt[])
+            return torch.ops.air.npu_fused_infer_attention_score(
+                q, kc, vc, block_table=bt, actual_seq_lengths_kv=lens, num_heads=hq, num_key_value_heads=hkv,
+                input_layout="BSH", block_size=bs, scale=1 / math.sqrt(d), key_antiquant_scale=self.ks,
+                value_antiquant_scale=self.vs, quant_scale2=self.qs2)[0]
+
+    cfg = torchair_amd.CompilerConfig()
+    cfg.mode = "reduce-overhead"
+    fn = torch.compile(M(), backend=torchair_amd.get_npu_backend(compiler_config=cfg), fullgraph=True)
+    kcd = kc.reshape(-1, bs, hkv * d).to(DEV)
+    vcd = vc.reshape(-1, bs, hkv * d).to(DEV)
+    for step_lens in (lens, [499, 1, 128]):
+        q = torch.randn(b, 1, hq * d, generator=g).to(torch.bfloat16)
+        out = fn(q.to(DEV), kcd, vcd, bt.to(DEV), torch.tensor(step_lens, device=DEV))
+        torch.cuda.synchronize()
+        kd = G.antiquant_kv(_gather(kc.numpy(), bt, step_lens, bs), ks.numpy(), None, 0)
+        vd = G.antiquant_kv(_gather(vc.numpy(), bt, step_lens, bs), vs.numpy(), None, 0)
+        o, _ = G.prefill_attention(f32np(q.reshape(b, 1, hq, d)), kd, vd, np.ones(b, np.int64), np.array(step_lens),
+                                   1, 1 / math.sqrt(d))
+        assert_int8_close(out.reshape(b, 1, hq, d).cpu().numpy(), G.quant_attention_out(o, qs2.numpy()))

@@ -408,3 +408,48 @@ def test_explicit_mask_rule():
     o3, _ = G.prefill_attention(q, k, v, None, None, 0, 0.4, band=(0, big, big), mask=one)
     for b in range(2):
         np.testing.assert_allclose(o3[b, :, 0], v[b, pick[b], 0], rtol=1e-6)
+
+
+# ----------------------------------------------------------------------------- int8 KV / int8 attention_out
+def test_antiquant_kv_reductions():
+    rng = np.random.default_rng(40)
+    x = rng.integers(-128, 128, (2, 6, 3, 8)).astype(np.int8)
+    # scale 1, offset 0: the integers themselves
+    np.testing.assert_array_equal(G.antiquant_kv(x, np.ones(24)), x.astype(np.float32))
+    # a per-channel scale that is one value everywhere equals a per-token scale of that value
+    c = np.float32(0.0123)
+    pc = G.antiquant_kv(x, np.full(24, c), np.full(24, 3.0), mode=0)
+    pt = G.antiquant_kv(x, np.full((2, 9), c), np.full((2, 9), 3.0), mode=1)
+    np.testing.assert_array_equal(pc, pt)
+    # closed form of one element per mode: (x + offset) * scale
+    sc = rng.random(24).astype(np.float32)
+    of = rng.random(24).astype(np.float32)
+    got = G.antiquant_kv(x, sc, of, mode=0)
+    assert got[1, 4, 2, 5] == np.float32((np.float32(x[1, 4, 2, 5]) + of[2 * 8 + 5]) * sc[2 * 8 + 5])
+    st = rng.random((2, 6)).astype(np.float32)
+    so = rng.random((2, 6)).astype(np.float32)
+    got = G.antiquant_kv(x, st, so, mode=1)
+    assert got[0, 3, 1, 7] == np.float32((np.float32(x[0, 3, 1, 7]) + so[0, 3]) * st[0, 3])
+
+
+def test_quant_attention_out_known_answers():
+    o = np.array([0.5, 1.5, -2.5, 2.5, 200.0, -300.0, 0.49, -0.51], np.float32).reshape(1, 1, 1, 8)
+    np.testing.assert_array_equal(G.quant_attention_out(o, [1.0]).reshape(-1), [0, 2, -2, 2, 127, -128, 0, -1])
+    # per channel: channel h * D + d
+    sc = np.arange(1, 9, dtype=np.float32)
+    of = np.full(8, -0.25, np.float32)
+    np.testing.assert_array_equal(G.quant_attention_out(np.ones((1, 1, 1, 8), np.float32), sc, of).reshape(-1),
+                                  [1, 2, 3, 4, 5, 6, 7, 8])
+
+
+def test_int8_kv_attention_reduces_to_float_attention_on_integer_values():
+    """With scale 1 and offset 0 the int8 cache is the float attention over the integer values."""
+    rng = np.random.default_rng(41)
+    q = rng.standard_normal((1, 4, 2, 8)).astype(np.float32) * 0.1
+    k = rng.integers(-128, 128, (1, 7, 1, 8)).astype(np.int8)
+    v = rng.integers(-128, 128, (1, 7, 1, 8)).astype(np.int8)
+    kd, vd = G.antiquant_kv(k, np.ones(8)), G.antiquant_kv(v, np.ones(8))
+    out, lse = G.prefill_attention(q, kd, vd, None, None, 1, 0.3)
+    want, wl = G.prefill_attention(q, k.astype(np.float32), v.astype(np.float32), None, None, 1, 0.3)
+    np.testing.assert_array_equal(out, want)
+    np.testing.assert_array_equal(lse, wl)

@@ -138,9 +138,8 @@ def fia_fake(query, key, value, **kw):
     return out, lse
 
 
-_UNSUPPORTED = ("pse_shift", "dequant_scale1", "quant_scale1", "dequant_scale2", "quant_scale2", "quant_offset2",
-                "antiquant_scale", "antiquant_offset", "query_padding_size", "kv_padding_size", "key_antiquant_offset",
-                "value_antiquant_offset", "key_shared_prefix", "value_shared_prefix", "actual_shared_prefix_len",
+_UNSUPPORTED = ("pse_shift", "dequant_scale1", "quant_scale1", "dequant_scale2", "query_padding_size",
+                "kv_padding_size", "key_shared_prefix", "value_shared_prefix", "actual_shared_prefix_len",
                 "key_rope_antiquant_scale")
 
 
@@ -212,6 +211,21 @@ def fia_cuda(query, key, value, **kw):
     seq_q = _lens_tensor(kw.get("actual_seq_lengths"), query.device)
 
     mask_origin, pre, nxt, explicit = _mask_params(kw)
+    # int8 key / value caches (GQA / MHA) and int8 attention_out take the general kernel
+    quant_out = kw.get("quant_scale2") is not None
+    kv8 = key.dtype == torch.int8 and kw.get("query_rope") is None
+    _check(kw.get("quant_offset2") is None or quant_out, "npu_fused_infer_attention_score: quant_offset2 needs "
+           "quant_scale2")
+    if kw.get("query_rope") is None:
+        for name in ("key_antiquant_scale", "key_antiquant_offset", "value_antiquant_scale", "value_antiquant_offset",
+                     "antiquant_scale", "antiquant_offset"):
+            _check(kw.get(name) is None or kv8, f"npu_fused_infer_attention_score: {name} applies to int8 key/value")
+    else:
+        for name in ("key_antiquant_offset", "value_antiquant_scale", "value_antiquant_offset", "antiquant_scale",
+                     "antiquant_offset"):
+            _check(kw.get(name) is None, f"npu_fused_infer_attention_score: {name} is not supported with MLA")
+        _check(not quant_out, "npu_fused_infer_attention_score: int8 attention_out (quant_scale2) is served for "
+               "GQA/MHA, not MLA")
 
     if block_table is not None:
         _check(ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql,
@@ -228,7 +242,7 @@ def fia_cuda(query, key, value, **kw):
                 return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
             return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
                                 scale, mask_origin, pre, nxt, explicit, stream)
-        dt = _half_code(query, key, value)
+        dt = _half_code(query, key, value, kv8)
         d = _value_d(block_table, value, query, ql, n_kv)
         if key.dim() == 3:
             bs = key.size(1)
@@ -244,11 +258,13 @@ def fia_cuda(query, key, value, **kw):
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
         # the tiled kernels step through pages 32 tokens at a time
-        if explicit or bs % 32 != 0 or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)):
+        if (explicit or kv8 or quant_out or bs % 32 != 0 or d not in (64, 128, 256)
+                or (s > 1 and d not in (64, 128))):
             _check(ql != "TND", "npu_fused_infer_attention_score: the general path takes BSH/BSND/BNSD queries")
             kstr = [sb, ss, sh]
             return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, kstr, kstr,
-                                 bt, bs, seq_q, seq_kv, mask_origin, pre, nxt, explicit, kw, scale, stream)
+                                 bt, bs, seq_q, seq_kv, mask_origin, pre, nxt, explicit, kw, scale, stream,
+                                 kv8=kv8, quant_out=quant_out)
         # one query token that the mask leaves the whole prefix: the decode kernel
         if s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0)):
             q = query.contiguous()
@@ -271,12 +287,12 @@ def fia_cuda(query, key, value, **kw):
     # ---------------------------------------------------------------- dense prefill
     _check(ql in ("BSH", "BSND", "BNSD") and ol == ql,
            "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
-    dt = _half_code(query, key, value)
+    dt = _half_code(query, key, value, kv8)
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
-    if explicit or d not in (64, 128) or _value_d(None, value, query, ql, n_kv) != d:
+    if explicit or kv8 or quant_out or d not in (64, 128) or _value_d(None, value, query, ql, n_kv) != d:
         return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt,
                              _strides_bshd(key, ql, n_kv), _strides_bshd(value, ql, n_kv), None, 0, seq_q, seq_kv,
-                             mask_origin, pre, nxt, explicit, kw, scale, stream)
+                             mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=kv8, quant_out=quant_out)
     s_kv = key.size(2) if ql == "BNSD" else key.size(1)
     qs = _strides_bshd(query, ql, hq)
     ks = _strides_bshd(key, ql, n_kv)
@@ -356,9 +372,74 @@ def _general_args(dt, b, s_q, s_kv, hq, n_kv, dk1, dk2, dv, q1, q1s, q2, q2s, k1
     return a
 
 
+def _antiquant_params(a, kw, b, n_kv, dk, dv, keep):
+    """Fills the int8 key/value fields of tai_fia_general_args: (x + offset) * scale per channel (mode 0,
+    [Hkv * D] in any layout the op takes: [H], [N, D], [N, 1, D], [1, N, 1, D]) or per token (mode 1,
+    [B, S] or [1, B, S]). key_/value_antiquant_* with key_/value_antiquant_mode, or the combined
+    antiquant_scale / antiquant_offset of leading dim 2 (key, value) with antiquant_mode
+    (experiment_ops.h:3922-3932; the converter passes them on, fused_infer_attention_score.py:16-27)."""
+    ks, ko, km = kw.get("key_antiquant_scale"), kw.get("key_antiquant_offset"), int(kw.get("key_antiquant_mode", 0))
+    vs, vo, vm = (kw.get("value_antiquant_scale"), kw.get("value_antiquant_offset"),
+                  int(kw.get("value_antiquant_mode", 0)))
+    if ks is None and vs is None and kw.get("antiquant_scale") is not None:
+        both, both_o = kw["antiquant_scale"], kw.get("antiquant_offset")
+        _check(both.size(0) == 2 and (both_o is None or both_o.size(0) == 2),
+               "npu_fused_infer_attention_score: antiquant_scale / antiquant_offset hold key and value (leading dim 2)")
+        ks, vs = both[0], both[1]
+        ko, vo = (both_o[0], both_o[1]) if both_o is not None else (None, None)
+        km = vm = int(kw.get("antiquant_mode", 0))
+    _check(ks is not None and vs is not None, "npu_fused_infer_attention_score: int8 key/value need antiquant scales "
+           "(key_antiquant_scale and value_antiquant_scale, or antiquant_scale)")
+    _check(km in (0, 1) and vm in (0, 1), "npu_fused_infer_attention_score: antiquant modes 0 (per channel) and 1 "
+           "(per token) are supported")
+    tok = 0
+
+    def flat(t, mode, d, what):
+        nonlocal tok
+        if t is None:
+            return None
+        t = t.to(torch.float32).contiguous()
+        if mode == 0:
+            _check(t.numel() == n_kv * d, f"npu_fused_infer_attention_score: per-channel {what} needs Hkv * D = "
+                   f"{n_kv * d} entries, got {t.numel()}")
+            t = t.reshape(-1)
+        else:
+            _check(t.numel() % b == 0 and t.numel() > 0, f"npu_fused_infer_attention_score: per-token {what} must be "
+                   "[B, S] or [1, B, S]")
+            t = t.reshape(b, -1)
+            _check(tok in (0, t.size(1)), "npu_fused_infer_attention_score: per-token key and value scales must cover "
+                   "the same positions")
+            tok = t.size(1)
+        keep.append(t)
+        return t
+
+    a.kv_dtype = _lib.DT_INT8
+    for attr, t, mode, d, what in (("k_scale", ks, km, dk, "key scale"), ("k_offset", ko, km, dk, "key offset"),
+                                   ("v_scale", vs, vm, dv, "value scale"), ("v_offset", vo, vm, dv, "value offset")):
+        f = flat(t, mode, d, what)
+        setattr(a, attr, f.data_ptr() if f is not None else None)
+    a.k_quant_mode, a.v_quant_mode, a.tok_stride = km, vm, tok
+
+
+def _out_quant_params(a, kw, hq, dv, keep):
+    """int8 attention_out: clamp(rint(o * quant_scale2 + quant_offset2)), per tensor (1 entry) or per
+    channel (Hq * Dv entries, channel h * Dv + d) (experiment_ops.h:3943)."""
+    qs = kw["quant_scale2"].to(torch.float32).contiguous().reshape(-1)
+    _check(qs.numel() in (1, hq * dv), "npu_fused_infer_attention_score: quant_scale2 must have 1 or N * D entries")
+    qo = kw.get("quant_offset2")
+    if qo is not None:
+        qo = qo.to(torch.float32).contiguous().reshape(-1)
+        _check(qo.numel() == qs.numel(), "npu_fused_infer_attention_score: quant_offset2 must match quant_scale2")
+        keep.append(qo)
+    keep.append(qs)
+    a.out_dtype, a.out_scale, a.out_scale_len = _lib.DT_INT8, qs.data_ptr(), qs.numel()
+    a.out_offset = qo.data_ptr() if qo is not None else None
+
+
 def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, ks, vs, bt, bs, seq_q, seq_kv,
-                  mask_origin, pre, nxt, explicit, kw, scale, stream):
-    """The general kernel for GQA/MHA: explicit masks and head dims the tiled kernels do not take."""
+                  mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=False, quant_out=False):
+    """The general kernel for GQA/MHA: explicit masks, head dims the tiled kernels do not take, int8
+    key/value caches and int8 attention_out."""
     b, s_q, hq, _ = _bsnd(query, ql, num_heads)
     dv = _value_d(bt, value, query, ql, n_kv)
     mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
@@ -369,6 +450,13 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
     a = _general_args(dt, b, s_q, s_kv, hq, n_kv, d, 0, dv, query, _strides_bshd(query, ql, hq), None, None,
                       key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale,
                       out, _strides_bshd(out, ql, hq), lse if want_lse else None)
+    keep = []  # fp32 copies of the scales, alive until the launch is queued (stream-ordered frees)
+    if kv8:
+        _check(key.dtype == torch.int8 and value.dtype == torch.int8,
+               "npu_fused_infer_attention_score: int8 key needs an int8 value")
+        _antiquant_params(a, kw, b, n_kv, d, dv, keep)
+    if quant_out:
+        _out_quant_params(a, kw, hq, dv, keep)
     _lib.call("tai_fia_general", ctypes.byref(a), stream)
     return out, lse
 
@@ -400,10 +488,15 @@ def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv,
     return out, lse
 
 
-def _half_code(query, key, value) -> int:
-    """ScalarType code of the attention element type: bf16 or fp16, the same for query, key and value."""
-    _check(query.dtype in (torch.bfloat16, torch.float16) and key.dtype == query.dtype and value.dtype == query.dtype,
-           "npu_fused_infer_attention_score: query/key/value must all be bf16 or all fp16")
+def _half_code(query, key, value, kv8=False) -> int:
+    """ScalarType code of the attention element type: bf16 or fp16, the same for query, key and value
+    (kv8: int8 key and value caches beside a bf16 / fp16 query)."""
+    if kv8:
+        _check(query.dtype in (torch.bfloat16, torch.float16) and value.dtype == torch.int8,
+               "npu_fused_infer_attention_score: int8 key/value take a bf16 or fp16 query and an int8 value")
+    else:
+        _check(query.dtype in (torch.bfloat16, torch.float16) and key.dtype == query.dtype and
+               value.dtype == query.dtype, "npu_fused_infer_attention_score: query/key/value must all be bf16 or all fp16")
     return DT_BF16 if query.dtype == torch.bfloat16 else DT_FP16
 
 

@@ -32,7 +32,10 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("seq_lens_q", _P), ("seq_lens_kv", _P),
                 ("mask", _P), ("mask_strides", _I64x3), ("mask_origin", c_int64),
                 ("pre_tokens", c_int64), ("next_tokens", c_int64), ("scale", c_float),
-                ("out", _P), ("out_strides", _I64x3), ("lse", _P)]
+                ("out", _P), ("out_strides", _I64x3), ("lse", _P),
+                ("kv_dtype", c_int64), ("k_scale", _P), ("k_offset", _P), ("k_quant_mode", c_int64),
+                ("v_scale", _P), ("v_offset", _P), ("v_quant_mode", c_int64), ("tok_stride", c_int64),
+                ("out_dtype", c_int64), ("out_scale", _P), ("out_offset", _P), ("out_scale_len", c_int64)]
 
 
 _SIGS = {

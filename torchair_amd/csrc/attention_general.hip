@@ -1,5 +1,6 @@
 // npu_fused_infer_attention_score, general path: an explicit attention mask, a bf16 / fp16 MLA
-// latent, or head dims the tiled kernels do not take. One wave per (sequence, query head, query
+// latent, head dims the tiled kernels do not take, int8 key / value caches with their antiquant
+// scales and offsets, and int8 attention_out. One wave per (sequence, query head, query
 // row); a 64-token chunk of keys puts one token on each lane (its score is a dot product against the
 // query, held in LDS as fp32), the chunk's softmax statistics are wave reductions, and the value rows
 // are accumulated with the lane owning value dims lane, lane + 64, ... Every product and sum is fp32.
@@ -20,6 +21,13 @@ struct GenArgs {
   bool f16;
 };
 
+// (x + offset) * scale of an int8 key / value element: per channel (index c) or per token (b, t)
+__device__ __forceinline__ float antiquant(float x, const float* sc, const float* of, int64_t mode, int64_t tok_stride,
+                                           int64_t b, int64_t t, int64_t c) {
+  const int64_t i = mode == 0 ? c : b * tok_stride + t;
+  return (x + (of ? of[i] : 0.0f)) * sc[i];
+}
+
 __device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const int64_t* st, int64_t b, int64_t tok, int kvh) {
   if (a.block_table) {
     const int64_t blk = a.block_table[b * a.max_blocks + tok / a.block_size];
@@ -28,6 +36,7 @@ __device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const 
   return b * st[0] + tok * st[1] + kvh * st[2];
 }
 
+template <bool KV8>
 __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga) {
   const tai_fia_general_args& a = ga.a;
   const bool f16 = ga.f16;
@@ -43,9 +52,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   // lengths read on the device are clamped to what the inputs hold (s_q; s_kv, or the blocks a
   // block-table row can address)
   const int64_t lq = a.seq_lens_q ? imax64(0, imin64(a.seq_lens_q[b], a.s_q)) : a.s_q;
-  const int64_t kv_cap = a.block_table ? a.max_blocks * a.block_size : a.s_kv;
+  int64_t kv_cap = a.block_table ? a.max_blocks * a.block_size : a.s_kv;
+  // per-token antiquant scales hold tok_stride positions per sequence
+  if (KV8 && (a.k_quant_mode == 1 || a.v_quant_mode == 1)) kv_cap = imin64(kv_cap, a.tok_stride);
   const int64_t lk = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
-  uint16_t* op = static_cast<uint16_t*>(a.out) + b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
+  const int64_t o_off = b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
   const int dk = a.dk1 + a.dk2;
   // the query as fp32 in this wave's LDS row
   {
@@ -75,14 +86,28 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     float s = -INFINITY;
     if (valid) {
       float acc = 0.0f;
-      const uint16_t* kr = k1 + gen_row(a, a.k1_strides, b, j, kvh);
-      for (int d = 0; d < a.dk1; d += 8) {
-        const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
-        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+      if constexpr (KV8) {
+        const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j, kvh);
+        for (int d = 0; d < a.dk1; d += 8) {
+          const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
+          const uint32_t wd[2] = {u.x, u.y};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc += half_to_f32(static_cast<uint16_t>(wd[q] & 0xffffu), f16) * qs[w][d + 2 * q];
-          acc += half_to_f32(static_cast<uint16_t>(wd[q] >> 16), f16) * qs[w][d + 2 * q + 1];
+          for (int q = 0; q < 8; ++q) {
+            const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
+            acc += antiquant(x, a.k_scale, a.k_offset, a.k_quant_mode, a.tok_stride, b, j,
+                             static_cast<int64_t>(kvh) * a.dk1 + d + q) * qs[w][d + q];
+          }
+        }
+      } else {
+        const uint16_t* kr = k1 + gen_row(a, a.k1_strides, b, j, kvh);
+        for (int d = 0; d < a.dk1; d += 8) {
+          const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
+          const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc += half_to_f32(static_cast<uint16_t>(wd[q] & 0xffffu), f16) * qs[w][d + 2 * q];
+            acc += half_to_f32(static_cast<uint16_t>(wd[q] >> 16), f16) * qs[w][d + 2 * q + 1];
+          }
         }
       }
       if (a.dk2) {
@@ -103,11 +128,22 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     for (int jj = 0; jj < nj; ++jj) {
       const float pj = __shfl(p, jj, 64);
       if (pj == 0.0f) continue;  // masked (wave-uniform)
-      const uint16_t* vr = vv + gen_row(a, a.v_strides, b, t0 + jj, kvh);
+      if constexpr (KV8) {
+        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj, kvh);
 #pragma unroll
-      for (int e = 0; e < kGenDvPerLane; ++e) {
-        const int d = lane + 64 * e;
-        if (d < a.dv) o[e] += pj * half_to_f32(vr[d], f16);
+        for (int e = 0; e < kGenDvPerLane; ++e) {
+          const int d = lane + 64 * e;
+          if (d < a.dv)
+            o[e] += pj * antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset, a.v_quant_mode, a.tok_stride, b,
+                                   t0 + jj, static_cast<int64_t>(kvh) * a.dv + d);
+        }
+      } else {
+        const uint16_t* vr = vv + gen_row(a, a.v_strides, b, t0 + jj, kvh);
+#pragma unroll
+        for (int e = 0; e < kGenDvPerLane; ++e) {
+          const int d = lane + 64 * e;
+          if (d < a.dv) o[e] += pj * half_to_f32(vr[d], f16);
+        }
       }
     }
     m = m_new;
@@ -119,7 +155,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     const int d = lane + 64 * e;
     if (d < a.dv) {
       const float r = o[e] * inv;
-      op[d] = f16 ? f32_to_f16(r) : f32_to_bf16(r);
+      if (a.out_dtype == TAI_DT_INT8) {
+        // quant_scale2 / quant_offset2: rint(o * scale + offset) saturated to int8
+        const int64_t c = a.out_scale_len == 1 ? 0 : h * a.dv + d;
+        const float y = __fadd_rn(__fmul_rn(r, a.out_scale[c]), a.out_offset ? a.out_offset[c] : 0.0f);
+        static_cast<int8_t*>(a.out)[o_off + d] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(rintf(y), -128.0f), 127.0f)));
+      } else {
+        static_cast<uint16_t*>(a.out)[o_off + d] = f16 ? f32_to_f16(r) : f32_to_bf16(r);
+      }
     }
   }
   if (a.lse && lane == 0 && i < a.s_q) a.lse[(b * a.hq + h) * a.s_q + i] = live ? m + logf(l) : -INFINITY;
@@ -146,16 +189,34 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
                 "tai_fia_general: paged K/V need block_size, max_blocks and seq_lens_kv");
   if (a.b == 0 || a.s_q == 0) return TAI_OK;
   TAI_CHECK_ARG(a.q1 && a.k1 && a.v && a.out, "tai_fia_general: null pointer");
-  TAI_CHECK_ARG((reinterpret_cast<uintptr_t>(a.k1) % 16) == 0 && a.k1_strides[0] % 8 == 0 && a.k1_strides[1] % 8 == 0 &&
-                    a.k1_strides[2] % 8 == 0,
-                "tai_fia_general: key rows must be 16-byte aligned");
+  const bool kv8 = a.kv_dtype == TAI_DT_INT8;
+  TAI_CHECK_ARG(a.kv_dtype == 0 || kv8, "tai_fia_general: kv_dtype %lld not supported (0 or int8)",
+                static_cast<long long>(a.kv_dtype));
+  TAI_CHECK_ARG(a.out_dtype == 0 || a.out_dtype == TAI_DT_INT8, "tai_fia_general: out_dtype %lld not supported (0 or "
+                "int8)", static_cast<long long>(a.out_dtype));
+  if (kv8) {
+    TAI_CHECK_ARG(a.k_scale && a.v_scale, "tai_fia_general: int8 key / value need k_scale and v_scale");
+    TAI_CHECK_ARG((a.k_quant_mode == 0 || a.k_quant_mode == 1) && (a.v_quant_mode == 0 || a.v_quant_mode == 1),
+                  "tai_fia_general: antiquant modes must be 0 (per channel) or 1 (per token)");
+    TAI_CHECK_ARG(a.dk2 == 0, "tai_fia_general: int8 key / value take one key part");
+    TAI_CHECK_ARG((a.k_quant_mode == 0 && a.v_quant_mode == 0) || a.tok_stride > 0,
+                  "tai_fia_general: per-token scales need tok_stride > 0");
+  }
+  if (a.out_dtype == TAI_DT_INT8)
+    TAI_CHECK_ARG(a.out_scale && (a.out_scale_len == 1 || a.out_scale_len == a.hq * a.dv),
+                  "tai_fia_general: int8 out needs out_scale of 1 or hq * dv entries");
+  const int kalign = kv8 ? 8 : 16, kel = 8;
+  TAI_CHECK_ARG((reinterpret_cast<uintptr_t>(a.k1) % kalign) == 0 && a.k1_strides[0] % kel == 0 &&
+                    a.k1_strides[1] % kel == 0 && a.k1_strides[2] % kel == 0,
+                "tai_fia_general: key rows must be %d-byte aligned", kalign);
   GenArgs ga{a, a.dtype == TAI_DT_FP16};
   // pre / next at or beyond 2^40 tokens are no bound
   constexpr int64_t kNoBound = int64_t(1) << 40;
   ga.a.pre_tokens = imin64(imax64(a.pre_tokens, -kNoBound), kNoBound);
   ga.a.next_tokens = imin64(imax64(a.next_tokens, -kNoBound), kNoBound);
   const int64_t waves = a.b * a.hq * a.s_q;
-  fia_general_kernel<<<dim3(static_cast<unsigned>(cdiv(waves, kGenWaves))), 64 * kGenWaves, 0,
-                       static_cast<hipStream_t>(stream)>>>(ga);
+  const dim3 grid(static_cast<unsigned>(cdiv(waves, kGenWaves)));
+  if (kv8) fia_general_kernel<true><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
+  else fia_general_kernel<false><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
   return launch_status("tai_fia_general");
 }

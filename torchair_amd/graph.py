@@ -70,7 +70,7 @@ class _Captured:
                 if isinstance(a, torch.Tensor) and not pin:
                     self.moved_idx.append((i, a.data_ptr()))
                 self.inputs.append(a)
-        dev = next((a.device for a in args if isinstance(a, torch.Tensor)), torch.device("cuda"))
+        dev = next((a.device for a in args if isinstance(a, torch.Tensor) and a.is_cuda), torch.device("cuda"))
         self.resources: Dict[Any, Any] = {}
         _state.resources = self.resources
         try:
