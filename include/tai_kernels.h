@@ -384,7 +384,9 @@ typedef struct tai_fia_general_args {
   float* lse;
   /* int8 key / value caches (kv_dtype = TAI_DT_INT8; 0 = the query's dtype), dequantised as
    * (x + offset) * scale: mode 0 per channel, fp32 [hkv * dk1] (key) / [hkv * dv] (value); mode 1 per
-   * token, fp32 element (b, t) at b * tok_stride + t. A null offset is 0. Replaces the key/value
+   * token, fp32 element (b, t) at b * tok_stride + t; mode 2 per cache slot of a paged cache, element
+   * block * block_size + slot (the MLA latent scale layout). A null offset is 0. A second key part
+   * (k2, the MLA rope key) stays in the query's dtype. Replaces the key/value
    * antiquant inputs of ge.FusedInferAttentionScore (experiment_ops.h:3922-3932). */
   int64_t kv_dtype;
   const float* k_scale;

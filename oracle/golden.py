@@ -618,6 +618,38 @@ def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq
     return out, lse
 
 
+def mla_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_q, seq_kv, band, scale: float):
+    """MLA over a paged latent cache with several query tokens per sequence (MTP / speculative
+    decode): the arguments of mla_decode_attention with q_nope [B,Sq,H,Dn], q_rope [B,Sq,H,Dr] and
+    band = (origin, pre, next) as in band_mask; ckv_scale None for a bf16 / fp16 latent. Query i of
+    sequence b (i < seq_q[b]) attends to latent tokens j < seq_kv[b] that the band leaves visible.
+    Returns (out [B,Sq,H,Dn] fp32, lse [B,H,Sq]); with one query token it is mla_decode_attention.
+    """
+    qn = np.asarray(q_nope, F32)
+    qr = np.asarray(q_rope, F32)
+    b_cnt, sq, h, dn = qn.shape
+    bs = ckv.shape[1]
+    out = np.zeros((b_cnt, sq, h, dn), F32)
+    lse = np.full((b_cnt, h, sq), -np.inf, F32)
+    for b in range(b_cnt):
+        L, lq = int(seq_kv[b]), int(seq_q[b])
+        if L <= 0 or lq <= 0:
+            continue
+        pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
+        c = np.asarray(ckv[pages], F32).reshape(-1, dn)[:L]
+        if ckv_scale is not None:
+            c = (c * np.asarray(ckv_scale[pages], F32).reshape(-1)[:L, None]).astype(F32)
+        kr = np.asarray(krope[pages], F32).reshape(-1, krope.shape[-1])[:L]
+        kk = np.concatenate([c, kr], axis=1)
+        vis = band_mask(lq, L, *band)
+        for hh in range(h):
+            qk = np.concatenate([qn[b, :lq, hh], qr[b, :lq, hh]], axis=1)
+            o, l = _softmax_attend(qk, kk, c, scale, vis)
+            out[b, :lq, hh] = o
+            lse[b, hh, :lq] = l
+    return out, lse
+
+
 # ----------------------------------------------------------------------------- RMS norm family
 def _rms(x: np.ndarray, eps: float) -> np.ndarray:
     """rstd per row of fp32 x: 1 / sqrt(mean(x^2) + eps); the sum in float64, rounded once."""

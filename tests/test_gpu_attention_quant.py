@@ -183,3 +183,39 @@ def test_int8_kv_and_int8_out_paged_decode_through_the_compiled_graph():
         o, _ = G.prefill_attention(f32np(q.reshape(b, 1, hq, d)), kd, vd, np.ones(b, np.int64), np.array(step_lens),
                                    1, 1 / math.sqrt(d))
         assert_int8_close(out.reshape(b, 1, hq, d).cpu().numpy(), G.quant_attention_out(o, qs2.numpy()))
+
+
+@pytest.mark.parametrize("sq,mask_kw,band", [(2, dict(sparse_mode=3), (1, 2147483647, 0)),
+                                             (4, dict(sparse_mode=3), (1, 2147483647, 0)),
+                                             (1, dict(sparse_mode=4, pre_tokens=100, next_tokens=0), (1, 100, 0))])
+def test_mla_int8_latent_several_query_tokens(sq, mask_kw, band):
+    """The int8 MLA latent with several query tokens per sequence (MTP / speculative decode) or a
+    window takes the general kernel with per-cache-slot scales."""
+    g = torch.Generator().manual_seed(155)
+    lens, h, bs, dn, dr = [300, 65, 7], 16, 64, 512, 64
+    b = len(lens)
+    nb = [(L + bs - 1) // bs for L in lens]
+    total = sum(nb) + 2
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(b, max(nb), dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    qn = torch.randn(b, sq, h, dn, generator=g).to(torch.bfloat16)
+    qr = torch.randn(b, sq, h, dr, generator=g).to(torch.bfloat16)
+    ckv = _i8((total, bs, 1, dn), g)
+    cs = torch.rand(total, bs, generator=g) * 9e-3 + 1e-3
+    kr = torch.randn(total, bs, 1, dr, generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(192)
+    out, lse = torch.ops.air.npu_fused_infer_attention_score(
+        qn.to(DEV), ckv.to(DEV), ckv.to(DEV), query_rope=qr.to(DEV), key_rope=kr.to(DEV),
+        key_antiquant_scale=cs.to(DEV), key_antiquant_mode=1, block_table=bt.to(DEV),
+        actual_seq_lengths=torch.full((b,), sq, device=DEV), actual_seq_lengths_kv=torch.tensor(lens, device=DEV),
+        num_heads=h, num_key_value_heads=1, input_layout="BSND", block_size=bs, scale=scale, softmax_lse_flag=True,
+        **mask_kw)
+    want, wl = G.mla_attention(f32np(qn), f32np(qr), ckv[:, :, 0].numpy(), cs.numpy(), f32np(kr[:, :, 0]), bt.numpy(),
+                               [sq] * b, lens, band, scale)
+    assert out.shape == (b, sq, h, dn)
+    assert_close(f32np(out), want)
+    np.testing.assert_allclose(_lse(lse, b, h, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)

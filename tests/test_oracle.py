@@ -453,3 +453,28 @@ def test_int8_kv_attention_reduces_to_float_attention_on_integer_values():
     want, wl = G.prefill_attention(q, k.astype(np.float32), v.astype(np.float32), None, None, 1, 0.3)
     np.testing.assert_array_equal(out, want)
     np.testing.assert_array_equal(lse, wl)
+
+
+def test_mla_attention_with_one_query_token_is_mla_decode():
+    rng = np.random.default_rng(42)
+    b, h, dn, dr, bs = 3, 4, 16, 8, 4
+    lens = [9, 1, 6]
+    nblk = 8
+    bt = np.stack([rng.permutation(nblk)[:3] for _ in range(b)]).astype(np.int32)
+    qn = rng.standard_normal((b, h, dn)).astype(np.float32)
+    qr = rng.standard_normal((b, h, dr)).astype(np.float32)
+    ckv = rng.integers(-128, 128, (nblk, bs, dn)).astype(np.int8)
+    cs = rng.random((nblk, bs)).astype(np.float32) * 0.01
+    kr = rng.standard_normal((nblk, bs, dr)).astype(np.float32)
+    want, wl = G.mla_decode_attention(qn, qr, ckv, cs, kr, bt, lens, 0.2)
+    got, gl = G.mla_attention(qn[:, None], qr[:, None], ckv, cs, kr, bt, [1] * b, lens, (1, 2147483647, 0), 0.2)
+    # (per-head against all-heads fp32 products: equal up to summation order)
+    np.testing.assert_allclose(got[:, 0], want, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gl[:, :, 0], wl, rtol=1e-6, atol=1e-6)
+    # a later query token of a causal (bottom-right) sequence sees one more latent token than the one before
+    got2, _ = G.mla_attention(np.repeat(qn[:, None], 2, 1), np.repeat(qr[:, None], 2, 1), ckv, cs, kr, bt, [2] * b,
+                              lens, (1, 2147483647, 0), 0.2)
+    np.testing.assert_allclose(got2[:, 1], want, rtol=1e-5, atol=1e-6)
+    # the first of two tokens sees one latent token fewer: it equals decode over lens - 1
+    want0, _ = G.mla_decode_attention(qn, qr, ckv, cs, kr, bt, [x - 1 for x in lens], 0.2)
+    np.testing.assert_allclose(got2[:, 0], want0, rtol=1e-5, atol=1e-6)

@@ -237,9 +237,10 @@ def fia_cuda(query, key, value, **kw):
         bt = block_table.to(torch.int32).contiguous()
         _check(bt.dim() == 2 and bt.size(0) == b, "npu_fused_infer_attention_score: block_table must be [B, max_blocks]")
         if kw.get("query_rope") is not None:
-            if key.dtype == torch.int8:
-                _check(s == 1, "npu_fused_infer_attention_score: MLA serves one query token per sequence")
+            whole_prefix = pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
+            if key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit:
                 return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
+            # several query tokens (MTP / speculative decode), bands and masks: the general kernel
             return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
                                 scale, mask_origin, pre, nxt, explicit, stream)
         dt = _half_code(query, key, value, kv8)
@@ -463,12 +464,15 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
 
 def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv, scale,
                  mask_origin, pre, nxt, explicit, stream):
-    """MLA with a bf16 / fp16 latent cache: key = [latent | key_rope], value = latent, one kv head."""
+    """MLA on the general kernel: key = [latent | key_rope], value = latent, one kv head. The latent is
+    bf16 / fp16, or int8 with one fp32 scale per cache slot (key_antiquant_scale [blocks, bs],
+    key_antiquant_mode 1, as for the one-token kernel), then dequantised as latent * scale."""
     q_rope, k_rope = kw["query_rope"], kw.get("key_rope")
     _check(k_rope is not None, "npu_fused_infer_attention_score: MLA needs key_rope")
     _check(n_kv == 1, "npu_fused_infer_attention_score: MLA latent cache has one kv head")
     _check(ql in ("BSH", "BSND", "BNSD"), "npu_fused_infer_attention_score: MLA takes BSH/BSND/BNSD queries")
-    dt = _half_code(query, key, value)
+    kv8 = key.dtype == torch.int8
+    dt = _half_code(query, key, value, kv8)
     _check(q_rope.dtype == query.dtype and k_rope.dtype == query.dtype,
            "npu_fused_infer_attention_score: MLA query_rope/key_rope must have the query's dtype")
     b, s_q, hq, dn = _bsnd(query, ql, num_heads)
@@ -484,6 +488,16 @@ def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv,
                       _strides_bshd(q_rope, ql, hq), kc, kst, kr, [kr.stride(0), kr.stride(1), 0], kc, kst, bt, bs,
                       seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale, out, _strides_bshd(out, ql, hq),
                       lse if want_lse else None)
+    ks = None
+    if kv8:
+        k_scale = kw.get("key_antiquant_scale")
+        _check(k_scale is not None and int(kw.get("key_antiquant_mode", 0)) == 1,
+               "npu_fused_infer_attention_score: an int8 MLA latent needs per-token key_antiquant_scale "
+               "(key_antiquant_mode=1)")
+        ks = k_scale.to(torch.float32).contiguous()
+        _check(ks.numel() == nblk * bs, "npu_fused_infer_attention_score: key_antiquant_scale must hold one fp32 per "
+                                        "cached token ([blocks, bs])")
+        a.kv_dtype, a.k_scale, a.v_scale, a.k_quant_mode, a.v_quant_mode = _lib.DT_INT8, ks.data_ptr(), ks.data_ptr(), 2, 2
     _lib.call("tai_fia_general", ctypes.byref(a), stream)
     return out, lse
 

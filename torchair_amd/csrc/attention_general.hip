@@ -21,10 +21,17 @@ struct GenArgs {
   bool f16;
 };
 
-// (x + offset) * scale of an int8 key / value element: per channel (index c) or per token (b, t)
-__device__ __forceinline__ float antiquant(float x, const float* sc, const float* of, int64_t mode, int64_t tok_stride,
-                                           int64_t b, int64_t t, int64_t c) {
-  const int64_t i = mode == 0 ? c : b * tok_stride + t;
+// Index of an antiquant scale: per channel (mode 0, channel c), per token (mode 1, (b, t)) or per
+// cache slot (mode 2, paged caches: block_table[b][t / bs] * bs + t % bs, the MLA latent scale layout)
+__device__ __forceinline__ int64_t antiquant_index(const tai_fia_general_args& a, int64_t mode, int64_t b, int64_t t,
+                                                   int64_t c) {
+  if (mode == 0) return c;
+  if (mode == 1) return b * a.tok_stride + t;
+  return static_cast<int64_t>(a.block_table[b * a.max_blocks + t / a.block_size]) * a.block_size + t % a.block_size;
+}
+
+// (x + offset) * scale of an int8 key / value element
+__device__ __forceinline__ float antiquant(float x, const float* sc, const float* of, int64_t i) {
   return (x + (of ? of[i] : 0.0f)) * sc[i];
 }
 
@@ -94,8 +101,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
-            acc += antiquant(x, a.k_scale, a.k_offset, a.k_quant_mode, a.tok_stride, b, j,
-                             static_cast<int64_t>(kvh) * a.dk1 + d + q) * qs[w][d + q];
+            acc += antiquant(x, a.k_scale, a.k_offset,
+                             antiquant_index(a, a.k_quant_mode, b, j, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
+                   qs[w][d + q];
           }
         }
       } else {
@@ -134,8 +142,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         for (int e = 0; e < kGenDvPerLane; ++e) {
           const int d = lane + 64 * e;
           if (d < a.dv)
-            o[e] += pj * antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset, a.v_quant_mode, a.tok_stride, b,
-                                   t0 + jj, static_cast<int64_t>(kvh) * a.dv + d);
+            o[e] += pj * antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
+                                   antiquant_index(a, a.v_quant_mode, b, t0 + jj, static_cast<int64_t>(kvh) * a.dv + d));
         }
       } else {
         const uint16_t* vr = vv + gen_row(a, a.v_strides, b, t0 + jj, kvh);
@@ -196,10 +204,11 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
                 "int8)", static_cast<long long>(a.out_dtype));
   if (kv8) {
     TAI_CHECK_ARG(a.k_scale && a.v_scale, "tai_fia_general: int8 key / value need k_scale and v_scale");
-    TAI_CHECK_ARG((a.k_quant_mode == 0 || a.k_quant_mode == 1) && (a.v_quant_mode == 0 || a.v_quant_mode == 1),
-                  "tai_fia_general: antiquant modes must be 0 (per channel) or 1 (per token)");
-    TAI_CHECK_ARG(a.dk2 == 0, "tai_fia_general: int8 key / value take one key part");
-    TAI_CHECK_ARG((a.k_quant_mode == 0 && a.v_quant_mode == 0) || a.tok_stride > 0,
+    TAI_CHECK_ARG(a.k_quant_mode >= 0 && a.k_quant_mode <= 2 && a.v_quant_mode >= 0 && a.v_quant_mode <= 2,
+                  "tai_fia_general: antiquant modes must be 0 (per channel), 1 (per token) or 2 (per cache slot)");
+    TAI_CHECK_ARG((a.k_quant_mode != 2 && a.v_quant_mode != 2) || a.block_table,
+                  "tai_fia_general: per-slot antiquant scales need a paged cache");
+    TAI_CHECK_ARG((a.k_quant_mode != 1 && a.v_quant_mode != 1) || a.tok_stride > 0,
                   "tai_fia_general: per-token scales need tok_stride > 0");
   }
   if (a.out_dtype == TAI_DT_INT8)
