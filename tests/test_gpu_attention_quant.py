@@ -185,14 +185,15 @@ def test_int8_kv_and_int8_out_paged_decode_through_the_compiled_graph():
         assert_int8_close(out.reshape(b, 1, hq, d).cpu().numpy(), G.quant_attention_out(o, qs2.numpy()))
 
 
-@pytest.mark.parametrize("sq,mask_kw,band", [(2, dict(sparse_mode=3), (1, 2147483647, 0)),
-                                             (4, dict(sparse_mode=3), (1, 2147483647, 0)),
-                                             (1, dict(sparse_mode=4, pre_tokens=100, next_tokens=0), (1, 100, 0))])
-def test_mla_int8_latent_several_query_tokens(sq, mask_kw, band):
-    """The int8 MLA latent with several query tokens per sequence (MTP / speculative decode) or a
-    window takes the general kernel with per-cache-slot scales."""
+@pytest.mark.parametrize("sq,mask_kw,band,bs", [(2, dict(sparse_mode=3), (1, 2147483647, 0), 64),
+                                                (4, dict(sparse_mode=3), (1, 2147483647, 0), 64),
+                                                (1, dict(sparse_mode=4, pre_tokens=100, next_tokens=0), (1, 100, 0), 64),
+                                                (1, dict(sparse_mode=3), (1, 2147483647, 0), 16)])
+def test_mla_int8_latent_several_query_tokens(sq, mask_kw, band, bs):
+    """The int8 MLA latent with several query tokens per sequence (MTP / speculative decode), a window,
+    or pages that are not a multiple of 32 tokens takes the general kernel with per-cache-slot scales."""
     g = torch.Generator().manual_seed(155)
-    lens, h, bs, dn, dr = [300, 65, 7], 16, 64, 512, 64
+    lens, h, dn, dr = [300, 65, 7], 16, 512, 64
     b = len(lens)
     nb = [(L + bs - 1) // bs for L in lens]
     total = sum(nb) + 2

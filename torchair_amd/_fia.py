@@ -238,7 +238,8 @@ def fia_cuda(query, key, value, **kw):
         _check(bt.dim() == 2 and bt.size(0) == b, "npu_fused_infer_attention_score: block_table must be [B, max_blocks]")
         if kw.get("query_rope") is not None:
             whole_prefix = pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
-            if key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit:
+            # (the one-token kernel steps through pages 32 tokens at a time; key is [blocks, bs, (1,) Dn])
+            if key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit and key.size(1) % 32 == 0:
                 return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
             # several query tokens (MTP / speculative decode), bands and masks: the general kernel
             return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
