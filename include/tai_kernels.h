@@ -257,6 +257,33 @@ int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t, int64_t h,
                             int32_t* expanded_row_idx, int64_t* expert_tokens,
                             float* expanded_scale, void* workspace, size_t ws_bytes, void* stream);
 
+/* npu_moe_init_routing_v2 with drop_pad_mode 1 (experiment_ops.h:2160-2189 drop_pad_mode /
+ * expert_capacity; converter .../custom/npu_moe_init_routing_v2.py:41-91): expert e of
+ * [expert_start, expert_end) owns rows [e * capacity, (e + 1) * capacity) of expanded_x [E * capacity, h];
+ * its slots, in slot order, fill them and the rest are dropped (expanded_row_idx -1). Unfilled rows are
+ * zero. expert_tokens: every slot routed to the expert (count, or cumsum for type 0). expanded_scale
+ * (with scale [t]): [E * capacity], 0 on unfilled rows. */
+size_t tai_moe_init_routing_v2_droppad_workspace_size(int64_t t, int k, int64_t num_experts,
+                                                      int64_t capacity);
+int tai_moe_init_routing_v2_droppad(const void* x, int elem_bytes, int64_t t, int64_t h,
+                                    const int32_t* expert_idx, int k, const float* scale,
+                                    int64_t capacity, int expert_start, int expert_end,
+                                    int expert_tokens_num_type, void* expanded_x,
+                                    int32_t* expanded_row_idx, int64_t* expert_tokens,
+                                    float* expanded_scale, void* workspace, size_t ws_bytes,
+                                    void* stream);
+
+/* quant_mode 0 (static) of npu_moe_init_routing_v2 (experiment_ops.h:2160-2189; scale / offset of
+ * MoeInitRoutingV3 :2140-2158): y = clamp(rint(x * scale + offset), -128, 127) over [rows, cols] of
+ * x_dtype (bf16 / fp16 / fp32), each operation rounded once. scale / offset (offset may be NULL): one
+ * value (per_col 0) or cols values (per_col 1) for each of scale_groups groups; a row's group is
+ * row / group_rows (group_rows > 0) or found in the cumulative group_ends of num_groups entries
+ * (scale_groups 1: every row uses group 0). */
+int tai_static_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, const float* scale,
+                          const float* offset, int64_t scale_groups, int per_col, const void* group_ends,
+                          int group_ends_dtype, int64_t num_groups, int64_t group_rows, int8_t* y,
+                          void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * npu_moe_init_routing (legacy). Replaces ge.MoeInitRouting emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/moe_init_routing.py:10-21

@@ -366,6 +366,64 @@ def moe_init_routing_v2(x, expert_idx, scale=None, active_rows: Optional[int] = 
     return ex, ri, tokens, es
 
 
+def moe_init_routing_v2_droppad(x, expert_idx, capacity: int, scale=None, expert_start: int = 0,
+                                expert_end: Optional[int] = None, expert_tokens_num_type: int = 0):
+    """npu_moe_init_routing_v2 with drop_pad_mode 1 and expert_capacity (prototype
+    experiment_ops.h:2160-2189: drop_pad_mode 1 = dropPad, expert_capacity = the max tokens of every
+    expert; converter .../custom/npu_moe_init_routing_v2.py:41-91). Expert e (of the range) owns rows
+    [e * capacity, (e + 1) * capacity) of expanded_x; its slots, in the dropless order (stable by slot
+    t * k + j), fill them and slots past the capacity are dropped (row index -1); unfilled rows are
+    zero. expert_tokens counts every slot routed to the expert (cumsum for type 0). Returns
+    (expanded_x [E * capacity, H], expanded_row_idx [T * k], expert_tokens, expanded_scale_or_None).
+    The reference holds no kernel or test for this mode; the layout is pinned against the dropless
+    routing (capacity >= the largest expert count gives its rows, placed at each expert's block).
+    """
+    x = np.asarray(x)
+    ei = np.asarray(expert_idx, np.int64)
+    t, k = ei.shape
+    n = t * k
+    if expert_end is None:
+        expert_end = int(ei.max()) + 1 if n else 1
+    bins = expert_end - expert_start
+    flat = ei.reshape(-1)
+    ex = np.zeros((bins * capacity,) + x.shape[1:], x.dtype)
+    ri = np.full(n, -1, np.int32)
+    es = None if scale is None else np.zeros(bins * capacity, F32)
+    fill = np.zeros(bins, np.int64)
+    for p in range(n):  # slots in order: the stable per-expert order
+        e = int(flat[p]) - expert_start
+        if e < 0 or e >= bins:
+            continue
+        if fill[e] < capacity:
+            q = e * capacity + fill[e]
+            ri[p] = q
+            ex[q] = x[p // k]
+            if es is not None:
+                es[q] = np.asarray(scale, F32)[p // k]
+        fill[e] += 1
+    counts = fill.astype(np.int64)
+    tokens = np.cumsum(counts) if expert_tokens_num_type == 0 else counts
+    return ex, ri, tokens, es
+
+
+def static_quant_rows(x, scale, offset=None, group_of_row=None):
+    """quant_mode 0 (static) of npu_moe_init_routing_v2 (prototype experiment_ops.h:2160-2189; the scale and
+    offset inputs of MoeInitRoutingV3 :2140-2158, offset [experts, 1] or [experts, H]):
+    y = clamp(rint(x * scale + offset), -128, 127) in fp32, each operation rounded once. scale / offset
+    are [1], [G, 1] or [G, H] (G groups, a row taking group_of_row[row]) or [1, H]; offset None is 0.
+    The reference holds no kernel for it; pinned by known answers (round half to even, saturation).
+    """
+    x = np.asarray(x, F32)
+    rows, h = x.shape
+    sc = np.asarray(scale, F32)
+    of = np.zeros_like(sc) if offset is None else np.asarray(offset, F32)
+    sc2 = sc.reshape(-1, 1) if sc.ndim <= 1 or sc.shape[-1] == 1 else sc.reshape(-1, h)
+    of2 = of.reshape(sc2.shape)
+    g = np.zeros(rows, np.int64) if group_of_row is None or sc2.shape[0] == 1 else np.asarray(group_of_row, np.int64)
+    y = (x * sc2[g]).astype(F32) + of2[g]
+    return np.clip(np.rint(y.astype(F32)), -128, 127).astype(np.int8)
+
+
 def moe_init_routing(x, row_idx, expert_idx, active_num: int):
     """npu_moe_init_routing (legacy). Follows .../custom/moe_init_routing.py:4-21 and prototype
     experiment_ops.h:2112-2135. Returns (expanded_x, expanded_row_idx, expanded_expert_idx)."""

@@ -5,7 +5,7 @@ import torch
 
 import torchair_amd  # noqa: F401
 from oracle import golden as G
-from tests.helpers import assert_close, f32np, gen, randn
+from tests.helpers import assert_close, assert_int8_close, f32np, gen, randn
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -166,3 +166,93 @@ def test_routing_round_trip():
     y = torch.ops.npu.npu_moe_finalize_routing(ex, None, None, None, w, ri, idx.to(DEV), drop_pad_mode=2)
     assert_close(f32np(y), f32np(x))
     assert int(tok[-1]) == t * k
+
+
+# ----------------------------------------------------------------------------- drop-pad, static / smooth quant
+@pytest.mark.parametrize("cap", [1, 7, 64])
+def test_init_routing_v2_drop_pad(cap):
+    """drop_pad_mode 1: expert e owns rows [e * cap, (e + 1) * cap); slots past the capacity are dropped;
+    unfilled rows are zero; the gathered per-token scale follows its row."""
+    g = gen(34)
+    t, h, e, k = 300, 64, 16, 4
+    x, idx = _routing_inputs(t, h, e, k, g)
+    scale = torch.rand(t, generator=g)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), scale=scale.to(DEV), expert_capacity=cap, expert_num=e, drop_pad_mode=1,
+        expert_tokens_num_type=1, expert_tokens_num_flag=True)
+    wex, wri, wtok, wes = G.moe_init_routing_v2_droppad(f32np(x), idx.numpy(), cap, scale.numpy(), 0, e, 1)
+    assert ex.shape == (e * cap, h)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    np.testing.assert_array_equal(f32np(ex), wex)
+    np.testing.assert_array_equal(es.cpu().numpy(), wes)
+
+
+def test_init_routing_v2_drop_pad_dynamic_quant_and_range():
+    """drop-pad with quant_mode 1 (no smooth scale) over an active expert range: the int8 rows and scales
+    of npu_dynamic_quant's token rows, placed by the drop-pad rule."""
+    g = gen(35)
+    t, h, e, k, cap = 257, 128, 32, 8, 40
+    x, idx = _routing_inputs(t, h, e, k, g)
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), expert_capacity=cap, expert_num=e, drop_pad_mode=1, quant_mode=1,
+        active_expert_range=[3, 19], expert_tokens_num_type=0)
+    q, s = G.dynamic_quant(f32np(x))
+    wex, wri, wtok, wes = G.moe_init_routing_v2_droppad(q, idx.numpy(), cap, s, 3, 19, 0)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    np.testing.assert_array_equal(ex.cpu().numpy(), wex)
+    np.testing.assert_array_equal(es.cpu().numpy(), wes)
+
+
+@pytest.mark.parametrize("drop_pad", [0, 1])
+@pytest.mark.parametrize("shared", [False, True])
+def test_init_routing_v2_dynamic_quant_smooth(drop_pad, shared):
+    """quant_mode 1 with a smooth scale ([1, H] shared, or [E, H] per expert): each expanded row is x * smooth
+    of its expert, quantised per row (int8 within 1 LSB on at most 0.1%, scales rtol 1e-6)."""
+    g = gen(36)
+    t, h, e, k, cap = 200, 256, 16, 4, 64
+    x, idx = _routing_inputs(t, h, e, k, g)
+    sm = torch.rand(1 if shared else e, h, generator=g) + 0.5
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), scale=sm.to(DEV), expert_capacity=cap, expert_num=e, drop_pad_mode=drop_pad,
+        quant_mode=1, active_num=t * k, expert_tokens_num_type=1)
+    if drop_pad:
+        bex, wri, wtok, _ = G.moe_init_routing_v2_droppad(f32np(x), idx.numpy(), cap, None, 0, e, 1)
+        ends = np.arange(1, e + 1) * cap
+    else:
+        bex, wri, wtok, _ = G.moe_init_routing_v2(f32np(x), idx.numpy(), None, t * k, 0, e, 1, 0)
+        ends = np.cumsum(wtok)
+    if shared:
+        wq, ws = G.dynamic_quant(bex, sm.numpy().reshape(h))
+    else:
+        wq, ws = G.dynamic_quant(bex, sm.numpy(), group_index=ends)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok)
+    assert_int8_close(ex.cpu().numpy(), wq)
+    np.testing.assert_allclose(es.cpu().numpy(), ws, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("drop_pad", [0, 1])
+@pytest.mark.parametrize("form", ["tensor", "expert_channel", "expert"])
+def test_init_routing_v2_static_quant(drop_pad, form):
+    """quant_mode 0: clamp(rint(x * scale + offset)) with per-tensor, per-expert or per-expert-and-channel
+    scale and offset, bit for bit."""
+    g = gen(37)
+    t, h, e, k, cap = 150, 64, 8, 3, 80
+    x, idx = _routing_inputs(t, h, e, k, g)
+    shape = {"tensor": (1,), "expert_channel": (e, h), "expert": (e, 1)}[form]
+    sc = torch.rand(shape, generator=g) * 40 + 10
+    of = torch.rand(shape, generator=g) * 4 - 2
+    ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+        x.to(DEV), idx.to(DEV), scale=sc.to(DEV), offset=of.to(DEV), expert_capacity=cap, expert_num=e,
+        drop_pad_mode=drop_pad, quant_mode=0, expert_tokens_num_type=1)
+    if drop_pad:
+        bex, wri, wtok, _ = G.moe_init_routing_v2_droppad(f32np(x), idx.numpy(), cap, None, 0, e, 1)
+        grp = np.arange(e * cap) // cap
+    else:
+        bex, wri, wtok, _ = G.moe_init_routing_v2(f32np(x), idx.numpy(), None, t * k, 0, e, 1, 0)
+        grp = np.repeat(np.arange(e), wtok)
+    assert ex.dtype == torch.int8 and es.numel() == 0
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri)
+    np.testing.assert_array_equal(ex.cpu().numpy(), G.static_quant_rows(bex, sc.numpy(), of.numpy(), grp))

@@ -478,3 +478,38 @@ def test_mla_attention_with_one_query_token_is_mla_decode():
     # the first of two tokens sees one latent token fewer: it equals decode over lens - 1
     want0, _ = G.mla_decode_attention(qn, qr, ckv, cs, kr, bt, [x - 1 for x in lens], 0.2)
     np.testing.assert_allclose(got2[:, 0], want0, rtol=1e-5, atol=1e-6)
+
+
+def test_droppad_routing_against_dropless():
+    rng = np.random.default_rng(43)
+    t, k, e, h = 20, 3, 6, 4
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    ei = rng.integers(0, e, (t, k)).astype(np.int32)
+    dx, dri, dtok, _ = G.moe_init_routing_v2(x, ei, expert_start=0, expert_end=e, expert_tokens_num_type=1)
+    cap = int(dtok.max())
+    px, pri, ptok, _ = G.moe_init_routing_v2_droppad(x, ei, cap, expert_start=0, expert_end=e,
+                                                     expert_tokens_num_type=1)
+    np.testing.assert_array_equal(ptok, dtok)
+    starts = np.concatenate([[0], np.cumsum(dtok)[:-1]])
+    for ex_ in range(e):
+        np.testing.assert_array_equal(px[ex_ * cap:ex_ * cap + dtok[ex_]], dx[starts[ex_]:starts[ex_] + dtok[ex_]])
+        assert not px[ex_ * cap + dtok[ex_]:(ex_ + 1) * cap].any()
+    # a slot's padded row = its expert's block + its dropless rank
+    fe = ei.reshape(-1)
+    np.testing.assert_array_equal(pri, fe * cap + (dri - starts[fe]))
+    # capacity 1 keeps the first slot (in slot order) of every expert and drops the rest
+    _, ri1, _, _ = G.moe_init_routing_v2_droppad(x, ei, 1, expert_start=0, expert_end=e)
+    for ex_ in range(e):
+        slots = np.nonzero(fe == ex_)[0]
+        if len(slots):
+            assert ri1[slots[0]] == ex_ and (ri1[slots[1:]] == -1).all()
+
+
+def test_static_quant_rows_known_answers():
+    x = np.array([[0.5, 1.5, -2.5, 300.0], [1.0, 2.0, 3.0, 4.0]], np.float32)
+    np.testing.assert_array_equal(G.static_quant_rows(x, [1.0]), [[0, 2, -2, 127], [1, 2, 3, 4]])
+    # per group, per column scale and offset: rint(x * s + o)
+    sc = np.array([[1.0, 1.0, 1.0, 1.0], [2.0, 0.5, 1.0, -1.0]], np.float32)
+    of = np.array([[0.0, 0.0, 0.0, 0.0], [0.25, 0.0, -0.5, 0.0]], np.float32)
+    np.testing.assert_array_equal(G.static_quant_rows(x, sc, of, group_of_row=[1, 0]),
+                                  [[1, 1, -3, -128], [1, 2, 3, 4]])

@@ -72,6 +72,12 @@ _SIGS = {
         c_int, [_P, c_int, c_int64, c_int64, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                 c_float, c_float, _P, _P, _P, _P]),
     "tai_moe_init_routing_workspace_size": (c_size_t, [c_int64, c_int, c_int64]),
+    "tai_moe_init_routing_v2_droppad_workspace_size": (c_size_t, [c_int64, c_int, c_int64, c_int64]),
+    "tai_moe_init_routing_v2_droppad": (
+        c_int, [_P, c_int, c_int64, c_int64, _P, c_int, _P, c_int64, c_int, c_int, c_int, _P, _P, _P, _P, _P, c_size_t,
+                _P]),
+    "tai_static_quant_rows": (
+        c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int64, c_int, _P, c_int, c_int64, c_int64, _P, _P]),
     "tai_moe_init_routing_v2": (
         c_int, [_P, c_int, c_int64, c_int64, _P, c_int, _P, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P,
                 _P, _P, c_size_t, _P]),

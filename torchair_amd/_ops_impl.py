@@ -610,59 +610,129 @@ def _init_routing_v2_fake(x, expert_idx, *, scale=None, offset=None, active_num=
                           quant_mode=-1, active_expert_range=(), row_idx_type=0):
     t, k = expert_idx.shape
     n = t * k
-    rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
     lo, hi = _v2_expert_range(expert_num, active_expert_range)
-    dyn = quant_mode == 1
-    return (x.new_empty((rows, x.shape[1]), dtype=torch.int8 if dyn else x.dtype),
+    if drop_pad_mode == 1:  # expert e owns rows [e * capacity, (e + 1) * capacity)
+        rows = max(hi - lo, 0) * max(expert_capacity, 0)
+    else:
+        rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
+    quant = quant_mode in (0, 1)
+    # expanded_scale: the gathered scale (unquantised), the per-row scale (dynamic); none for static
+    n_scale = rows if ((scale is not None and quant_mode == -1) or quant_mode == 1) else 0
+    return (x.new_empty((rows, x.shape[1]), dtype=torch.int8 if quant else x.dtype),
             x.new_empty((n,), dtype=torch.int32),
             x.new_empty((max(hi - lo, 0),), dtype=torch.int64),
-            x.new_empty((rows if (scale is not None or dyn) else 0,), dtype=torch.float32))
+            x.new_empty((n_scale,), dtype=torch.float32))
 
 
-def _init_routing_v2_cuda(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1,
-                          expert_num=-1, drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False,
-                          quant_mode=-1, active_expert_range=(), row_idx_type=0):
-    """npu_moe_init_routing_v2, dropless (npu_moe_init_routing_v2.py:41-91).
-
-    quant_mode 1 (dynamic, experiment_ops.h:2167) without smooth scales: every expanded row is the
-    symmetric per-row int8 quantisation of its token row and expanded_scale holds that row's scale.
-    A token row and its copies quantise identically, so the T token rows are quantised once (the
-    npu_dynamic_quant kernel) and the int8 rows and scales are gathered."""
-    _on_gpu(x, expert_idx, scale)
-    _check(drop_pad_mode == 0, "npu_moe_init_routing_v2: only drop_pad_mode 0 (dropless) is supported")
-    _check(quant_mode in (-1, 1), "npu_moe_init_routing_v2: quant_mode -1 (none) or 1 (dynamic) is supported")
-    if quant_mode == 1:
-        _check(scale is None and offset is None,
-               "npu_moe_init_routing_v2: quant_mode 1 is supported without smooth scale or offset")
-        _check(x.dim() == 2, "npu_moe_init_routing_v2: x [T,H] and expert_idx [T,k]")
-        q, s = torch.ops.npu.npu_dynamic_quant(x)
-        return _init_routing_v2_cuda(q, expert_idx, scale=s, active_num=active_num, expert_capacity=expert_capacity,
-                                     expert_num=expert_num, drop_pad_mode=drop_pad_mode,
-                                     expert_tokens_num_type=expert_tokens_num_type,
-                                     expert_tokens_num_flag=expert_tokens_num_flag, quant_mode=-1,
-                                     active_expert_range=active_expert_range, row_idx_type=row_idx_type)
-    _check(offset is None, "npu_moe_init_routing_v2: offset is not supported")
+def _route_v2(x, expert_idx, scale, active_num, expert_capacity, expert_num, drop_pad_mode, expert_tokens_num_type,
+              active_expert_range, row_idx_type):
+    """Routing without quantisation: (expanded_x, expanded_row_idx, expert_tokens, expanded_scale)."""
     _check(expert_tokens_num_type in (0, 1), "npu_moe_init_routing_v2: expert_tokens_num_type must be 0 or 1")
     _check(x.dim() == 2 and expert_idx.dim() == 2 and expert_idx.shape[0] == x.shape[0],
            "npu_moe_init_routing_v2: x [T,H] and expert_idx [T,k]")
     _check(expert_idx.dtype == torch.int32, "npu_moe_init_routing_v2: expert_idx must be int32")
     lo, hi = _v2_expert_range(expert_num, active_expert_range)
     _check(hi > lo >= 0, "npu_moe_init_routing_v2: expert_num or active_expert_range is required")
-    ex, ri, tok, es = _init_routing_v2_fake(x, expert_idx, scale=scale, active_num=active_num, expert_num=expert_num,
-                                            active_expert_range=active_expert_range)
+    if drop_pad_mode == 1:
+        _check(expert_capacity is not None and expert_capacity > 0,
+               "npu_moe_init_routing_v2: drop_pad_mode 1 needs expert_capacity > 0")
+    ex, ri, tok, es = _init_routing_v2_fake(x, expert_idx, scale=scale, active_num=active_num,
+                                            expert_capacity=expert_capacity, expert_num=expert_num,
+                                            drop_pad_mode=drop_pad_mode, active_expert_range=active_expert_range)
     t, k = expert_idx.shape
-    if t == 0:
-        return ex, ri, tok.zero_(), es
     xc, ec = x.contiguous(), expert_idx.contiguous()
     sc = _f32(scale)
     if sc is not None:
         _check(sc.numel() == t, "npu_moe_init_routing_v2: scale must have T entries")
+    if drop_pad_mode == 1:
+        ws_bytes = _lib.query("tai_moe_init_routing_v2_droppad_workspace_size", t, k, hi - lo, expert_capacity)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        _lib.call("tai_moe_init_routing_v2_droppad", _p(xc), xc.element_size(), t, xc.shape[1], _p(ec), k, _p(sc),
+                  expert_capacity, lo, hi, int(expert_tokens_num_type), _p(ex), _p(ri), _p(tok),
+                  _p(es) if sc is not None else None, _p(ws), ws_bytes, _stream(xc))
+        return ex, ri, tok, es
+    if t == 0:
+        return ex, ri, tok.zero_(), es
     ws_bytes = _lib.query("tai_moe_init_routing_workspace_size", t, k, hi - lo)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     _lib.call("tai_moe_init_routing_v2", _p(xc), xc.element_size(), t, xc.shape[1], _p(ec), k, _p(sc), ex.shape[0],
               lo, hi, int(expert_tokens_num_type), int(row_idx_type), _p(ex), _p(ri), _p(tok),
               _p(es) if sc is not None else None, _p(ws), ws_bytes, _stream(xc))
     return ex, ri, tok, es
+
+
+def _group_ends(tok, expert_tokens_num_type, drop_pad_mode, capacity, n_groups, device):
+    """Cumulative row ends of the experts' row blocks of expanded_x (int64, on the device)."""
+    if drop_pad_mode == 1:
+        return torch.arange(1, n_groups + 1, dtype=torch.int64, device=device) * capacity
+    return tok if expert_tokens_num_type == 0 else torch.cumsum(tok, 0)
+
+
+def _init_routing_v2_cuda(x, expert_idx, *, scale=None, offset=None, active_num=-1, expert_capacity=-1,
+                          expert_num=-1, drop_pad_mode=0, expert_tokens_num_type=0, expert_tokens_num_flag=False,
+                          quant_mode=-1, active_expert_range=(), row_idx_type=0):
+    """npu_moe_init_routing_v2 (npu_moe_init_routing_v2.py:41-91; prototype experiment_ops.h:2138-2190).
+
+    drop_pad_mode 0 (dropless) or 1 (dropPad with expert_capacity: expert e owns rows
+    [e * capacity, (e + 1) * capacity), slots past the capacity are dropped, unfilled rows are zero).
+    quant_mode -1: no quantisation (scale [T], if given, is gathered into expanded_scale).
+    quant_mode 1 (dynamic) without scale: every expanded row is the symmetric per-row int8 quantisation
+    of its token row and expanded_scale holds that row's scale; a token row and its copies quantise
+    identically, so the T token rows are quantised once (the npu_dynamic_quant kernel) and the int8
+    rows and scales are gathered. With a smooth scale ([1, H] or [E, H]) each expanded row is x * smooth
+    of its expert, then quantised per row (npu_dynamic_quant with the experts' row blocks as groups).
+    quant_mode 0 (static): y = clamp(rint(x * scale + offset)) with scale / offset of [1], [E, 1],
+    [1, H] or [E, H] (per expert, per channel); no expanded_scale."""
+    _on_gpu(x, expert_idx, scale, offset)
+    _check(drop_pad_mode in (0, 1), "npu_moe_init_routing_v2: drop_pad_mode must be 0 (dropless) or 1 (dropPad)")
+    _check(quant_mode in (-1, 0, 1), "npu_moe_init_routing_v2: quant_mode -1 (none), 0 (static) or 1 (dynamic) is "
+           "supported")
+    lo, hi = _v2_expert_range(expert_num, active_expert_range)
+    n_e = hi - lo
+    h = x.shape[-1]
+    route = dict(active_num=active_num, expert_capacity=expert_capacity, expert_num=expert_num,
+                 drop_pad_mode=drop_pad_mode, expert_tokens_num_type=expert_tokens_num_type,
+                 active_expert_range=active_expert_range, row_idx_type=row_idx_type)
+    if quant_mode == 1 and scale is None:
+        _check(offset is None, "npu_moe_init_routing_v2: quant_mode 1 takes no offset")
+        _check(x.dim() == 2, "npu_moe_init_routing_v2: x [T,H] and expert_idx [T,k]")
+        q, s = torch.ops.npu.npu_dynamic_quant(x)
+        return _route_v2(q, expert_idx, s, **route)
+    if quant_mode == 1:  # smooth scales per expert (or shared), then per-row dynamic quantisation
+        _check(offset is None, "npu_moe_init_routing_v2: quant_mode 1 takes no offset")
+        sm = _f32(scale)
+        _check(sm.numel() in (h, n_e * h), "npu_moe_init_routing_v2: the smooth scale must be [1, H] or [E, H]")
+        ex, ri, tok, _ = _route_v2(x, expert_idx, None, **route)
+        if sm.numel() == h:
+            q, s = torch.ops.npu.npu_dynamic_quant(ex, smooth_scales=sm.reshape(h))
+        else:
+            ends = _group_ends(tok, expert_tokens_num_type, drop_pad_mode, expert_capacity, n_e, x.device)
+            q, s = torch.ops.npu.npu_dynamic_quant(ex, smooth_scales=sm.reshape(n_e, h), group_index=ends)
+        return q, ri, tok, s
+    if quant_mode == 0:
+        _check(scale is not None, "npu_moe_init_routing_v2: quant_mode 0 (static) needs scale")
+        sc = _f32(scale)
+        ofs = _f32(offset)
+        # [1] per tensor, [H] / [1, H] per channel, [E, 1] per expert, [E, H] per expert and channel
+        if scale.dim() >= 2:
+            groups, cols = scale.numel() // scale.shape[-1], scale.shape[-1]
+        else:
+            groups, cols = 1, scale.numel()
+        _check(groups in (1, n_e) and cols in (1, h), "npu_moe_init_routing_v2: static scale must be [1], [H], [1, H], "
+               "[E, 1] or [E, H]")
+        _check(ofs is None or ofs.numel() == sc.numel(), "npu_moe_init_routing_v2: offset must match scale")
+        per_col = 1 if (cols == h and h != 1) else 0
+        ex, ri, tok, _ = _route_v2(x, expert_idx, None, **route)
+        y = torch.empty(ex.shape, dtype=torch.int8, device=x.device)
+        ends = None
+        if groups > 1 and drop_pad_mode == 0:
+            ends = _group_ends(tok, expert_tokens_num_type, 0, 0, n_e, x.device)
+        _lib.call("tai_static_quant_rows", _p(ex), _DT[ex.dtype], ex.shape[0], h, _p(sc), _p(ofs), groups, per_col,
+                  _p(ends), DT_INT64 if ends is not None else DT_NONE, n_e if ends is not None else 0,
+                  expert_capacity if (groups > 1 and drop_pad_mode == 1) else 0, _p(y), _stream(ex))
+        return y, ri, tok, x.new_empty((0,), dtype=torch.float32)
+    _check(offset is None, "npu_moe_init_routing_v2: offset applies to quant_mode 0")
+    return _route_v2(x, expert_idx, scale, **route)
 
 
 _define("npu", "npu_moe_init_routing_v2(Tensor x, Tensor expert_idx, *, Tensor? scale=None, Tensor? offset=None, "

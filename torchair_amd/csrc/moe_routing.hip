@@ -341,6 +341,62 @@ __global__ __launch_bounds__(256) void route_gather_kernel(const void* __restric
   if (escale && lane == 0) escale[i] = scale[src_row];
 }
 
+// ---------------------------------------------------------------------------- drop-pad routing
+// npu_moe_init_routing_v2 with drop_pad_mode 1: expert e (of the range) owns rows [e * cap, (e + 1) * cap)
+// of expanded_x; a slot's rank among its expert's slots (the dropless order: stable by slot) places it
+// at e * cap + rank, and slots of rank >= cap are dropped (row index -1). Rows no slot fills are zero.
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = v;
+}
+
+// dropless destination of slot p (row_idx[p], from route_place_kernel mode 0) -> padded position;
+// one thread per slot; the per-expert bases are the exclusive scan of the expert totals (bins <= 1024)
+__global__ __launch_bounds__(1024) void route_droppad_kernel(const int32_t* __restrict__ eidx, int64_t n, int e0,
+                                                             int bins, const int32_t* __restrict__ bintot, int64_t cap,
+                                                             int32_t* __restrict__ row_idx,
+                                                             int32_t* __restrict__ pad2src) {
+  __shared__ int32_t base[1024];
+  __shared__ int32_t red[16];
+  const int b = threadIdx.x;
+  const int32_t v = b < bins ? bintot[b] : 0;
+  const int32_t incl = block_incl_scan<false>(v, red);
+  if (b < bins) base[b] = incl - v;
+  __syncthreads();
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * 1024 + threadIdx.x; p < n; p += static_cast<int64_t>(gridDim.x) * 1024) {
+    const int32_t d = row_idx[p];
+    if (d < 0) continue;
+    const int e = eidx[p] - e0;
+    const int64_t rank = d - base[e];
+    if (rank < cap) {
+      const int64_t q = static_cast<int64_t>(e) * cap + rank;
+      row_idx[p] = static_cast<int32_t>(q);
+      pad2src[q] = static_cast<int32_t>(p);
+    } else {
+      row_idx[p] = -1;
+    }
+  }
+}
+
+// expanded_x[q] = x[pad2src[q] / k] or zeros; one wave per padded row
+__global__ __launch_bounds__(256) void route_pad_gather_kernel(const void* __restrict__ x, int64_t row_bytes, int k,
+                                                               const int32_t* __restrict__ pad2src, int64_t rows,
+                                                               void* __restrict__ ex, const float* __restrict__ scale,
+                                                               float* __restrict__ escale) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (q >= rows) return;
+  const int32_t p = pad2src[q];
+  char* dst = static_cast<char*>(ex) + q * row_bytes;
+  const char* src = p >= 0 ? static_cast<const char*>(x) + static_cast<int64_t>(p / k) * row_bytes : nullptr;
+  for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src ? src[o] : char(0);
+  if (escale && lane == 0) escale[q] = p >= 0 ? scale[p / k] : 0.0f;
+}
+
+__global__ __launch_bounds__(1024) void route_zero_tokens_kernel(int64_t* __restrict__ tokens, int bins) {
+  for (int b = threadIdx.x; b < bins; b += 1024) tokens[b] = 0;
+}
+
 // ============================================================================ finalize
 struct FinArgs {
   const void* ex;
@@ -520,6 +576,62 @@ extern "C" int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t,
                      row_idx_type, expanded_row_idx, nullptr, nullptr, expert_tokens, expert_tokens_num_type == 0,
                      scale, expanded_scale, expanded_x, workspace, ws_bytes, static_cast<hipStream_t>(stream),
                      "tai_moe_init_routing_v2");
+}
+
+extern "C" size_t tai_moe_init_routing_v2_droppad_workspace_size(int64_t t, int k, int64_t num_experts,
+                                                                 int64_t capacity) {
+  return route_ws_bytes(t * k, num_experts) + align256(sizeof(int32_t) * num_experts * capacity);
+}
+
+extern "C" int tai_moe_init_routing_v2_droppad(const void* x, int elem_bytes, int64_t t, int64_t h,
+                                               const int32_t* expert_idx, int k, const float* scale,
+                                               int64_t capacity, int expert_start, int expert_end,
+                                               int expert_tokens_num_type, void* expanded_x,
+                                               int32_t* expanded_row_idx, int64_t* expert_tokens,
+                                               float* expanded_scale, void* workspace, size_t ws_bytes,
+                                               void* stream) {
+  const char* name = "tai_moe_init_routing_v2_droppad";
+  TAI_CHECK_ARG(t >= 0 && h >= 0 && k > 0 && capacity > 0, "%s: bad sizes (capacity must be > 0)", name);
+  TAI_CHECK_ARG(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4, "%s: elem_bytes", name);
+  TAI_CHECK_ARG(expert_start >= 0 && expert_end > expert_start && expert_end - expert_start <= 1024,
+                "%s: expert range must hold 1..1024 experts", name);
+  TAI_CHECK_ARG(expert_tokens_num_type == 0 || expert_tokens_num_type == 1,
+                "%s: expert_tokens_num_type must be 0 (cumsum) or 1 (count)", name);
+  TAI_CHECK_ARG(scale == nullptr || expanded_scale != nullptr, "%s: expanded_scale missing", name);
+  const int bins = expert_end - expert_start;
+  const int64_t rows = static_cast<int64_t>(bins) * capacity;
+  TAI_CHECK_ARG(rows < (1ll << 31), "%s: experts * capacity must be < 2^31", name);
+  const size_t need = tai_moe_init_routing_v2_droppad_workspace_size(t, k, bins, capacity);
+  if (workspace == nullptr || ws_bytes < need) {
+    set_error("%s: workspace of %zu bytes, need %zu", name, ws_bytes, need);
+    return TAI_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = t * k;
+  TAI_CHECK_ARG(n < (1ll << 31), "%s: t*k must be < 2^31", name);
+  const size_t rws = route_ws_bytes(n, bins);
+  int32_t* pad2src = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + rws);
+  fill_i32_kernel<<<dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(rows, 256), 4096))), 256, 0, st>>>(pad2src, rows, -1);
+  if (n > 0) {
+    RouteWs w = carve_route_ws(workspace, n, bins);
+    const int64_t chunks = cdiv(n, kChunk);
+    route_hist_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, sizeof(int32_t) * bins, st>>>(expert_idx, n,
+                                                                                                 expert_start, bins,
+                                                                                                 w.hist);
+    route_bin_scan_kernel<<<dim3(static_cast<unsigned>(bins)), 64, 0, st>>>(w.hist, chunks, w.bintot);
+    route_place_kernel<<<dim3(static_cast<unsigned>(chunks)), kChunk, 0, st>>>(
+        expert_idx, n, expert_start, bins, w.hist, w.bintot, expert_tokens, expert_tokens_num_type == 0, w.total,
+        w.dst2src, 0, expanded_row_idx, nullptr, nullptr);
+    route_droppad_kernel<<<dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(n, 1024), 1024))), 1024, 0, st>>>(
+        expert_idx, n, expert_start, bins, w.bintot, capacity, expanded_row_idx, pad2src);
+  } else if (expert_tokens) {
+    // no slots: every expert count (and cumsum) is 0
+    route_zero_tokens_kernel<<<1, 1024, 0, st>>>(expert_tokens, bins);
+  }
+  if (rows > 0 && h > 0)
+    route_pad_gather_kernel<<<dim3(static_cast<unsigned>(cdiv(rows, 4))), 256, 0, st>>>(
+        x, static_cast<int64_t>(elem_bytes) * h, k, pad2src, rows, expanded_x, scale, expanded_scale);
+  return launch_status(name);
 }
 
 extern "C" int tai_moe_init_routing(const void* x, int elem_bytes, int64_t t, int64_t h,

@@ -476,6 +476,70 @@ __global__ __launch_bounds__(256) void dq2_apply_kernel(Dq2Args a) {
 
 using namespace tai;
 
+namespace tai {
+namespace {
+// Static per-tensor / per-group quantisation of rows: y = clamp(rint(x * scale + offset), -128, 127),
+// the product and the sum each rounded once. The row's group is row / group_rows (group_rows > 0),
+// found in the cumulative group ends (group_ends), or 0; scale / offset hold one value or one per
+// column for each group (scale_groups 1: shared by all groups). One thread per element.
+struct StaticQuantArgs {
+  const void* x;
+  int dt;
+  int64_t rows, cols;
+  const float* scale;
+  const float* offset;
+  int64_t scale_groups;
+  int per_col;
+  const void* ends;
+  int ends_dt;
+  int64_t ngroups;
+  int64_t group_rows;
+  int8_t* y;
+};
+
+__global__ __launch_bounds__(256) void static_quant_kernel(StaticQuantArgs a) {
+  const int64_t total = a.rows * a.cols;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / a.cols, c = i % a.cols;
+    int64_t g = 0;
+    if (a.group_rows > 0) g = r / a.group_rows;
+    else if (a.ends) g = group_of_row_cumsum(a.ends, a.ends_dt, a.ngroups, r);
+    if (a.scale_groups == 1) g = 0;
+    const int64_t si = g * (a.per_col ? a.cols : 1) + (a.per_col ? c : 0);
+    float v;
+    if (a.dt == TAI_DT_FP32) v = static_cast<const float*>(a.x)[i];
+    else if (a.dt == TAI_DT_BF16) v = bf16_to_f32(static_cast<const uint16_t*>(a.x)[i]);
+    else v = f16_to_f32(static_cast<const uint16_t*>(a.x)[i]);
+    const float q = __fadd_rn(__fmul_rn(v, a.scale[si]), a.offset ? a.offset[si] : 0.0f);
+    a.y[i] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(rintf(q), -128.0f), 127.0f)));
+  }
+}
+}  // namespace
+}  // namespace tai
+
+extern "C" int tai_static_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, const float* scale,
+                                     const float* offset, int64_t scale_groups, int per_col, const void* group_ends,
+                                     int group_ends_dtype, int64_t num_groups, int64_t group_rows, int8_t* y,
+                                     void* stream) {
+  using namespace tai;
+  TAI_CHECK_ARG(rows >= 0 && cols >= 0 && scale_groups >= 1 && (per_col == 0 || per_col == 1),
+                "tai_static_quant_rows: bad sizes");
+  TAI_CHECK_ARG(x_dtype == TAI_DT_BF16 || x_dtype == TAI_DT_FP16 || x_dtype == TAI_DT_FP32,
+                "tai_static_quant_rows: x must be bf16, fp16 or fp32");
+  TAI_CHECK_ARG(scale_groups == 1 || group_rows > 0 || (group_ends && num_groups == scale_groups),
+                "tai_static_quant_rows: per-group scales need group_rows or group_ends of scale_groups entries");
+  TAI_CHECK_ARG(group_ends == nullptr || group_ends_dtype == TAI_DT_INT64 || group_ends_dtype == TAI_DT_INT32,
+                "tai_static_quant_rows: group_ends must be int32 or int64");
+  if (rows == 0 || cols == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && scale && y, "tai_static_quant_rows: null pointer");
+  StaticQuantArgs a{x, x_dtype, rows, cols, scale, offset, scale_groups, per_col, group_ends, group_ends_dtype,
+                    num_groups, group_rows, y};
+  const int64_t blocks = std::min<int64_t>(cdiv(rows * cols, 256), 65536);
+  static_quant_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return launch_status("tai_static_quant_rows");
+}
+
 extern "C" int tai_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t cols,
                                  const float* smooth_scales, const void* group_index,
                                  int group_index_dtype, int64_t num_groups, int8_t* y, float* scale,
