@@ -116,6 +116,17 @@ int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t n2,
                              const void* bias, int bias_dtype, const float* quant_scale,
                              const void* group_index, int group_index_dtype, int64_t num_groups,
                              int activate_left, int8_t* y, float* scale, void* stream);
+/* The same with quant_mode 0 (static, the converter's default, npu_dequant_swiglu_quant.py:26-28 ->
+ * ge.DequantSwigluQuant quant_mode "static", experiment_ops.h:3765-3812): y = clamp(rint(h * quant_scale
+ * + quant_offset)) with h the SwiGLU output, quant_scale / quant_offset (offset may be NULL) of G * n
+ * entries, each operation rounded once; scale is written as 0. quant_mode 1 is the dynamic mode above
+ * (quant_offset must be NULL). */
+int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, int64_t n2,
+                                    const float* weight_scale, const float* activation_scale,
+                                    const void* bias, int bias_dtype, const float* quant_scale,
+                                    const float* quant_offset, const void* group_index,
+                                    int group_index_dtype, int64_t num_groups, int activate_left,
+                                    int quant_mode, int8_t* y, float* scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_quant_matmul (W8A8): acc = x1 @ x2 with exact int32 accumulation, then

@@ -59,7 +59,7 @@ def register() -> None:
             swiglu_mode=0, clamp_limit=7.0, glu_alpha=1.702, glu_bias=1.0):
         b = None if bias is None else (bias.numpy() if bias.dtype == torch.int32 else _np(bias))
         y, s = G.dequant_swiglu_quant(x.numpy(), _np(weight_scale), _np(activation_scale), b, _np(quant_scale),
-                                      _np(group_index), activate_left)
+                                      _np(group_index), activate_left, quant_mode, _np(quant_offset))
         return _t(y), _t(s)
 
     def qmm(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None, x1_dtype=None,

@@ -148,8 +148,13 @@ def silu(a: np.ndarray) -> np.ndarray:
 
 
 def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None, bias=None, quant_scale=None,
-                         group_index=None, activate_left: bool = False) -> Tuple[np.ndarray, np.ndarray]:
-    """npu_dequant_swiglu_quant, quant_mode=1 (dynamic), swiglu_mode 0, round_mode 0 (rint).
+                         group_index=None, activate_left: bool = False, quant_mode: int = 1,
+                         quant_offset=None) -> Tuple[np.ndarray, np.ndarray]:
+    """npu_dequant_swiglu_quant, swiglu_mode 0, round_mode 0 (rint). quant_mode 1 (dynamic): per-row
+    symmetric int8 of h * quant_scale. quant_mode 0 (static, the converter's default "static",
+    npu_dequant_swiglu_quant.py:26-28): y = clamp(rint(h * quant_scale + quant_offset)) with scale 0 (the
+    reference holds no kernel fixing it; the formula is the static quantisation rule, pinned by known
+    answers).
 
     Follows .../custom/npu_dequant_swiglu_quant.py:5-47 (round_mode 0 -> "rint", quant_mode 1 ->
     "dynamic"), prototype experiment_ops.h:3765-3812 (activate_left semantics) and the meta rule
@@ -190,7 +195,12 @@ def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None
     r = (silu(a) * b2).astype(F32) if activate_left else (a * silu(b2)).astype(F32)
     if quant_scale is not None:
         r = (r * np.asarray(quant_scale, F32).reshape(ng, n)[grp]).astype(F32)
-    q, s = _quant_rows(r)
+    if quant_mode == 0:
+        of = np.zeros((ng, n), F32) if quant_offset is None else np.asarray(quant_offset, F32).reshape(ng, n)
+        q = np.clip(np.rint((r + of[grp]).astype(F32)), -128, 127).astype(np.int8)
+        s = np.zeros(rows, F32)
+    else:
+        q, s = _quant_rows(r)
     q[~live] = 0
     s[~live] = 0
     return q.reshape(x.shape[:-1] + (n,)), s.reshape(x.shape[:-1])

@@ -133,3 +133,25 @@ def test_dynamic_quant_v2(asym, quant_mode, qmax, dtype):
     np.testing.assert_allclose(s.cpu().numpy(), ws, rtol=1e-6, atol=0)
     if asym:
         np.testing.assert_allclose(off.cpu().numpy(), woff, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("grouped", [False, True])
+def test_dequant_swiglu_quant_static_mode(grouped):
+    """quant_mode 0 (static): clamp(rint(h * quant_scale + quant_offset)), scale 0, against the oracle
+    (int8 within 1 LSB on at most 0.1%: h differs from the oracle's by the SwiGLU's reciprocal)."""
+    g = torch.Generator().manual_seed(90)
+    rows, n = 300, 1024
+    x = torch.randint(-30000, 30000, (rows, 2 * n), generator=g, dtype=torch.int32)
+    ng = 4 if grouped else 1
+    counts = torch.tensor([100, 0, 120, 50], dtype=torch.int64) if grouped else None
+    ws = torch.rand(ng, 2 * n, generator=g) * 1e-3
+    act = torch.rand(rows, generator=g) * 0.1
+    qs = torch.rand(ng, n, generator=g) * 20 + 1
+    qo = torch.rand(ng, n, generator=g) * 2 - 1
+    y, s = torch.ops.npu.npu_dequant_swiglu_quant(
+        x.to(DEV), weight_scale=ws.to(DEV), activation_scale=act.to(DEV), quant_scale=qs.to(DEV),
+        quant_offset=qo.to(DEV), group_index=counts.to(DEV) if grouped else None, activate_left=True, quant_mode=0)
+    wy, wsc = G.dequant_swiglu_quant(x.numpy(), ws.numpy(), act.numpy(), None, qs.numpy(),
+                                     counts.numpy() if grouped else None, True, 0, qo.numpy())
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_array_equal(s.cpu().numpy(), wsc)

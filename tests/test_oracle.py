@@ -513,3 +513,18 @@ def test_static_quant_rows_known_answers():
     of = np.array([[0.0, 0.0, 0.0, 0.0], [0.25, 0.0, -0.5, 0.0]], np.float32)
     np.testing.assert_array_equal(G.static_quant_rows(x, sc, of, group_of_row=[1, 0]),
                                   [[1, 1, -3, -128], [1, 2, 3, 4]])
+
+
+def test_dequant_swiglu_quant_static_known_answer():
+    """quant_mode 0: clamp(rint(h * quant_scale + quant_offset)), scale 0; h from the dynamic path's
+    composition (scale 1 / quant_scale 1 gives h itself)."""
+    x = np.array([[10, -4, 3, 2]], np.int32)  # a = [10, -4], b = [3, 2]
+    h = (G.silu(np.float32([10.0, -4.0])) * np.float32([3.0, 2.0])).astype(np.float32)
+    y, s = G.dequant_swiglu_quant(x, activate_left=True, quant_mode=0, quant_scale=np.float32([2.0, 10.0]),
+                                  quant_offset=np.float32([0.5, -1.0]))
+    want = np.clip(np.rint(h * np.float32([2.0, 10.0]) + np.float32([0.5, -1.0])), -128, 127).astype(np.int8)
+    np.testing.assert_array_equal(y, want.reshape(1, 2))
+    assert s[0] == 0
+    # saturation: h[0] ~ 30 times 10 is past 127, h[1] ~ -0.14 times 1000 is past -128
+    y2, _ = G.dequant_swiglu_quant(x, activate_left=True, quant_mode=0, quant_scale=np.float32([10.0, 1000.0]))
+    np.testing.assert_array_equal(y2, [[127, -128]])

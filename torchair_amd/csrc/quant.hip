@@ -195,7 +195,20 @@ struct DsqArgs {
   int left;
   int8_t* y;
   float* scale;
+  // static mode (quant_mode 0): y = clamp(rint(h * quant_scale + quant_offset)); scale output 0
+  const float* qo;
+  int stat;
 };
+
+// int8 of one SwiGLU output v (already multiplied by quant_scale): dynamic, rint(v / scale) with
+// inv = rcp(scale); static, rint(v + offset)
+__device__ __forceinline__ int8_t dsq_out(const DsqArgs& a, float v, float scale, float inv, const float* qo, int64_t j) {
+  if (a.stat) {
+    const float q = __fadd_rn(v, qo ? qo[j] : 0.0f);
+    return static_cast<int8_t>(static_cast<int>(fminf(fmaxf(rintf(q), -128.0f), 127.0f)));
+  }
+  return quant_i8(v, scale, inv);
+}
 
 __device__ __forceinline__ float silu(float a) { return silu_f32(a); }
 
@@ -315,15 +328,18 @@ __global__ __launch_bounds__(TPB) void dsq_kernel(DsqArgs a) {
     float m = red[r][0];
 #pragma unroll
     for (int q = 1; q < TPB / 64; ++q) m = fmaxf(m, red[r][q]);
-    const float scale = m / 127.0f, inv = rcp_f32(scale);
+    const float scale = a.stat ? 0.0f : m / 127.0f, inv = rcp_f32(scale);
+    const float* qo = (a.stat && a.qo && grp[r] >= 0) ? a.qo + grp[r] * n : nullptr;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int64_t c = tid + static_cast<int64_t>(i) * TPB;
       if (c < ng4) {
         uint32_t w = 0;
+        if (grp[r] >= 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w |= static_cast<uint32_t>(static_cast<uint8_t>(quant_i8(v[r][i][e], scale, inv))) << (8 * e);
+          for (int e = 0; e < 4; ++e)
+            w |= static_cast<uint32_t>(static_cast<uint8_t>(dsq_out(a, v[r][i][e], scale, inv, qo, 4 * c + e))) << (8 * e);
+        }
         *reinterpret_cast<uint32_t*>(a.y + row * n + 4 * c) = w;
       }
     }
@@ -362,8 +378,9 @@ __global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
   float amax = 0.0f;
   for (int64_t j = threadIdx.x; j < n; j += blockDim.x) amax = fmaxf(amax, fabsf(value(j)));
   amax = block_max(amax, red);
-  const float scale = amax / 127.0f;
-  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) a.y[row * n + j] = quant1(value(j), scale);
+  const float scale = a.stat ? 0.0f : amax / 127.0f, inv = rcp_f32(scale);
+  const float* qo = (a.stat && a.qo) ? a.qo + g * n : nullptr;
+  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) a.y[row * n + j] = dsq_out(a, value(j), scale, inv, qo, j);
   if (threadIdx.x == 0) a.scale[row] = scale;
 }
 
@@ -567,6 +584,22 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
                                         const void* group_index, int group_index_dtype,
                                         int64_t num_groups, int activate_left, int8_t* y,
                                         float* scale, void* stream) {
+  return tai_dequant_swiglu_quant_static(x, rows, n2, weight_scale, activation_scale, bias, bias_dtype, quant_scale,
+                                         nullptr, group_index, group_index_dtype, num_groups, activate_left, 1, y,
+                                         scale, stream);
+}
+
+extern "C" int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, int64_t n2,
+                                               const float* weight_scale, const float* activation_scale,
+                                               const void* bias, int bias_dtype, const float* quant_scale,
+                                               const float* quant_offset, const void* group_index,
+                                               int group_index_dtype, int64_t num_groups, int activate_left,
+                                               int quant_mode, int8_t* y, float* scale, void* stream) {
+  TAI_CHECK_ARG(quant_mode == 0 || quant_mode == 1, "tai_dequant_swiglu_quant: quant_mode must be 0 (static) or 1 "
+                "(dynamic)");
+  TAI_CHECK_ARG(quant_mode == 0 || quant_offset == nullptr, "tai_dequant_swiglu_quant: quant_offset applies to the "
+                "static mode");
+  TAI_CHECK_ARG(quant_mode == 1 || quant_scale != nullptr, "tai_dequant_swiglu_quant: the static mode needs quant_scale");
   TAI_CHECK_ARG(rows >= 0 && n2 >= 0 && n2 % 2 == 0, "tai_dequant_swiglu_quant: last dim must be even");
   if (rows == 0) return TAI_OK;
   TAI_CHECK_ARG(x && y && scale, "tai_dequant_swiglu_quant: null pointer");
@@ -577,7 +610,8 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
   TAI_CHECK_ARG(group_index == nullptr || group_index_dtype == TAI_DT_INT32 || group_index_dtype == TAI_DT_INT64,
                 "tai_dequant_swiglu_quant: group_index must be int32 or int64");
   DsqArgs a{x, rows, n2 / 2, weight_scale, activation_scale, bias, bias_dtype, quant_scale,
-            group_index, group_index_dtype, group_index ? num_groups : 1, activate_left, y, scale};
+            group_index, group_index_dtype, group_index ? num_groups : 1, activate_left, y, scale, quant_offset,
+            quant_mode == 0 ? 1 : 0};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = n2 / 2;
   auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
