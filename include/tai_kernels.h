@@ -441,6 +441,12 @@ typedef struct tai_fia_general_args {
   const float* out_scale;
   const float* out_offset;
   int64_t out_scale_len;
+  /* pse_shift (NULL: none): a positional bias of the query's dtype added to the scaled scores,
+   * softmax(scale * q.k + pse) (experiment_ops.h:3915 pse_shift; the converter passes pse_type 0,
+   * fused_infer_attention_score.py:94-109); element (b, h, i, j) at the dot of (b, h, i, j) with
+   * pse_strides (a stride 0 broadcasts). */
+  const void* pse;
+  int64_t pse_strides[4];
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 

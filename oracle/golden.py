@@ -490,9 +490,13 @@ def moe_finalize_routing(expanded, skip1, skip2, bias, scales, src_to_dst, exper
 
 
 # ----------------------------------------------------------------------------- attention
-def _softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, mask: Optional[np.ndarray] = None):
-    """q [n, d], k [L, d], v [L, dv] -> (out [n, dv], lse [n]); fp32, masked entries excluded."""
+def _softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, mask: Optional[np.ndarray] = None,
+                    bias: Optional[np.ndarray] = None):
+    """q [n, d], k [L, d], v [L, dv] -> (out [n, dv], lse [n]); fp32, masked entries excluded; bias [n, L]
+    (pse_shift) is added to the scaled scores."""
     s = (q.astype(F32) @ k.astype(F32).T) * F32(scale)
+    if bias is not None:
+        s = (s + np.asarray(bias, F32)).astype(F32)
     if mask is not None:
         s = np.where(mask, s, -np.inf)
     m = np.max(s, axis=1, keepdims=True) if s.shape[1] else np.full((s.shape[0], 1), -np.inf, F32)
@@ -553,14 +557,17 @@ def band_mask(lq: int, lk: int, origin: int, pre: int, nxt: int) -> np.ndarray:
     return ok
 
 
-def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None, mask=None):
+def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None, mask=None, pse=None):
     """npu_fused_infer_attention_score, dense prefill. q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D].
 
     causal 1 (sparse_mode 3, right-down): query i sees kv j <= i + (Lkv - Lq); causal 2
     (sparse_mode 2, left-up): j <= i; 0: no mask. band = (origin, pre, next) replaces causal with
     band_mask's rule. mask: an explicit atten_mask [B or 1, Sq, Skv] (nonzero = masked out, the
     converter's atten_mask input, .../custom/fused_infer_attention_score.py:4-109), combined with the
-    rest. Rows at or past Lq are zero.
+    rest. pse: pse_shift [B or 1, Hq, >= Sq, >= Skv], added to the scaled scores before the softmax,
+    softmax(scale * q.k + pse) (the converter passes pse_type 0, .../custom/fused_infer_attention_score.py:
+    94-109; the formula is the one of the public operator documentation, unpinned by the reference beyond
+    the reduction pse = 0 -> no pse). Rows at or past Lq are zero.
     Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
     """
     q = np.asarray(q, F32)
@@ -586,14 +593,19 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=No
             mb = mb[0 if mb.shape[0] == 1 else b, :lq, :lk] == 0
             vis = mb if vis is None else (vis & mb)
         for h in range(hq):
+            bias = None
+            if pse is not None:
+                pb = np.asarray(pse, F32)
+                bias = pb[0 if pb.shape[0] == 1 else b, h, :lq, :lk]
             o, l = _softmax_attend(q[b, :lq, h], np.asarray(k[b, :lk, h // g], F32),
-                                   np.asarray(v[b, :lk, h // g], F32), scale, vis)
+                                   np.asarray(v[b, :lk, h // g], F32), scale, vis, bias)
             out[b, :lq, h] = o
             lse[b, h, :lq] = l
     return out, lse
 
 
-def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float, mask=None):
+def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float, mask=None,
+                            pse=None):
     """npu_fused_infer_attention_score with a block table and several query tokens per sequence
     (chunked prefill / multi-token decode). q [B,Sq,Hq,D]; caches [blocks, bs, Hkv, D]; token t of
     sequence b at cache[block_table[b, t // bs], t % bs] (the paged rule of paged_decode_attention);
@@ -609,7 +621,7 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
         pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
         k[b, :L] = np.asarray(k_cache[pages], F32).reshape(-1, hkv, d)[:L]
         v[b, :L] = np.asarray(v_cache[pages], F32).reshape(-1, hkv, d)[:L]
-    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask)
+    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask, pse=pse)
 
 
 def antiquant_kv(x, scale, offset=None, mode: int = 0):

@@ -220,3 +220,36 @@ def test_mla_int8_latent_several_query_tokens(sq, mask_kw, band, bs):
     assert out.shape == (b, sq, h, dn)
     assert_close(f32np(out), want)
     np.testing.assert_allclose(_lse(lse, b, h, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_pse_shift(paged):
+    """pse_shift [B or 1, N, S_q, S_kv] added to the scaled scores: softmax(scale * q.k + pse)."""
+    g = torch.Generator().manual_seed(156)
+    b, sq, hq, hkv, d = 2, 5, 8, 2, 128
+    lq, lkv = [5, 3], [130, 64]
+    pb = 1 if paged else b
+    if paged:
+        bs = 64
+        kc, vc, bt = _paged(lkv, hkv, d, bs, g, lambda sh: torch.randn(sh, generator=g).to(torch.bfloat16))
+        skv = bt.shape[1] * bs
+    else:
+        skv = 130
+        k = torch.randn(b, skv, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(b, skv, hkv, d, generator=g).to(torch.bfloat16)
+    pse = (torch.randn(pb, hq, sq, skv, generator=g) * 2).to(torch.bfloat16)
+    q = torch.randn(b, sq, hq * d, generator=g).to(torch.bfloat16)
+    kw = dict(actual_seq_lengths=lq, actual_seq_lengths_kv=lkv, num_heads=hq, num_key_value_heads=hkv,
+              input_layout="BSH", scale=1 / math.sqrt(d), sparse_mode=3, softmax_lse_flag=True,
+              pse_shift=pse.to(DEV))
+    if paged:
+        out, lse = FIA(q.to(DEV), kc.reshape(-1, bs, hkv * d).to(DEV), vc.reshape(-1, bs, hkv * d).to(DEV),
+                       block_table=bt.to(DEV), block_size=bs, **kw)
+        kd, vd = _gather(f32np(kc), bt, lkv, bs), _gather(f32np(vc), bt, lkv, bs)
+    else:
+        out, lse = FIA(q.to(DEV), k.reshape(b, skv, hkv * d).to(DEV), v.reshape(b, skv, hkv * d).to(DEV), **kw)
+        kd, vd = f32np(k), f32np(v)
+    want, wl = G.prefill_attention(f32np(q.reshape(b, sq, hq, d)), kd, vd, np.array(lq), np.array(lkv), 1,
+                                   1 / math.sqrt(d), pse=f32np(pse))
+    assert_close(f32np(out.reshape(b, sq, hq, d)), want)
+    np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)

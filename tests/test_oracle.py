@@ -528,3 +528,27 @@ def test_dequant_swiglu_quant_static_known_answer():
     # saturation: h[0] ~ 30 times 10 is past 127, h[1] ~ -0.14 times 1000 is past -128
     y2, _ = G.dequant_swiglu_quant(x, activate_left=True, quant_mode=0, quant_scale=np.float32([10.0, 1000.0]))
     np.testing.assert_array_equal(y2, [[127, -128]])
+
+
+def test_pse_shift_reductions():
+    """pse = 0 is no pse; a pse constant along the kv axis changes nothing in the output (softmax shift)
+    and adds itself to the lse; a -inf pse column masks that key out."""
+    rng = np.random.default_rng(44)
+    q = rng.standard_normal((2, 5, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 7, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 7, 2, 8)).astype(np.float32)
+    base, bl = G.prefill_attention(q, k, v, None, None, 0, 0.3)
+    z, zl = G.prefill_attention(q, k, v, None, None, 0, 0.3, pse=np.zeros((1, 4, 5, 7), np.float32))
+    np.testing.assert_array_equal(z, base)
+    np.testing.assert_array_equal(zl, bl)
+    c = rng.standard_normal((2, 4, 5, 1)).astype(np.float32).repeat(7, axis=3)
+    o, ol = G.prefill_attention(q, k, v, None, None, 0, 0.3, pse=c)
+    np.testing.assert_allclose(o, base, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ol, bl + c[:, :, :, 0], rtol=1e-5, atol=1e-5)
+    m = np.zeros((1, 4, 5, 7), np.float32)
+    m[..., 3] = -np.inf
+    mask = np.zeros((1, 5, 7), np.uint8)
+    mask[..., 3] = 1
+    o2, _ = G.prefill_attention(q, k, v, None, None, 0, 0.3, pse=m)
+    o3, _ = G.prefill_attention(q, k, v, None, None, 0, 0.3, mask=mask)
+    np.testing.assert_array_equal(o2, o3)

@@ -138,7 +138,7 @@ def fia_fake(query, key, value, **kw):
     return out, lse
 
 
-_UNSUPPORTED = ("pse_shift", "dequant_scale1", "quant_scale1", "dequant_scale2", "query_padding_size",
+_UNSUPPORTED = ("dequant_scale1", "quant_scale1", "dequant_scale2", "query_padding_size",
                 "kv_padding_size", "key_shared_prefix", "value_shared_prefix", "actual_shared_prefix_len",
                 "key_rope_antiquant_scale")
 
@@ -214,6 +214,9 @@ def fia_cuda(query, key, value, **kw):
     # int8 key / value caches (GQA / MHA) and int8 attention_out take the general kernel
     quant_out = kw.get("quant_scale2") is not None
     kv8 = key.dtype == torch.int8 and kw.get("query_rope") is None
+    pse = kw.get("pse_shift")
+    _check(pse is None or kw.get("query_rope") is None, "npu_fused_infer_attention_score: pse_shift is served for "
+           "GQA/MHA, not MLA")
     _check(kw.get("quant_offset2") is None or quant_out, "npu_fused_infer_attention_score: quant_offset2 needs "
            "quant_scale2")
     if kw.get("query_rope") is None:
@@ -260,7 +263,7 @@ def fia_cuda(query, key, value, **kw):
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
         # the tiled kernels step through pages 32 tokens at a time
-        if (explicit or kv8 or quant_out or bs % 32 != 0 or d not in (64, 128, 256)
+        if (explicit or kv8 or quant_out or pse is not None or bs % 32 != 0 or d not in (64, 128, 256)
                 or (s > 1 and d not in (64, 128))):
             _check(ql != "TND", "npu_fused_infer_attention_score: the general path takes BSH/BSND/BNSD queries")
             kstr = [sb, ss, sh]
@@ -291,7 +294,8 @@ def fia_cuda(query, key, value, **kw):
            "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
     dt = _half_code(query, key, value, kv8)
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
-    if explicit or kv8 or quant_out or d not in (64, 128) or _value_d(None, value, query, ql, n_kv) != d:
+    if (explicit or kv8 or quant_out or pse is not None or d not in (64, 128)
+            or _value_d(None, value, query, ql, n_kv) != d):
         return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt,
                              _strides_bshd(key, ql, n_kv), _strides_bshd(value, ql, n_kv), None, 0, seq_q, seq_kv,
                              mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=kv8, quant_out=quant_out)
@@ -453,6 +457,14 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
                       key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale,
                       out, _strides_bshd(out, ql, hq), lse if want_lse else None)
     keep = []  # fp32 copies of the scales, alive until the launch is queued (stream-ordered frees)
+    pse = kw.get("pse_shift")
+    if pse is not None:
+        _check(pse.dtype == query.dtype and pse.dim() == 4 and pse.size(0) in (1, b) and pse.size(1) == hq
+               and pse.size(2) >= s_q and pse.size(3) >= s_kv,
+               "npu_fused_infer_attention_score: pse_shift must be [B or 1, N, >= S_q, >= S_kv] of the query's dtype")
+        a.pse = pse.data_ptr()
+        a.pse_strides = (ctypes.c_int64 * 4)(0 if pse.size(0) == 1 else pse.stride(0), pse.stride(1), pse.stride(2),
+                                             pse.stride(3))
     if kv8:
         _check(key.dtype == torch.int8 and value.dtype == torch.int8,
                "npu_fused_infer_attention_score: int8 key needs an int8 value")

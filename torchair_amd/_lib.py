@@ -35,7 +35,8 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("out", _P), ("out_strides", _I64x3), ("lse", _P),
                 ("kv_dtype", c_int64), ("k_scale", _P), ("k_offset", _P), ("k_quant_mode", c_int64),
                 ("v_scale", _P), ("v_offset", _P), ("v_quant_mode", c_int64), ("tok_stride", c_int64),
-                ("out_dtype", c_int64), ("out_scale", _P), ("out_offset", _P), ("out_scale_len", c_int64)]
+                ("out_dtype", c_int64), ("out_scale", _P), ("out_offset", _P), ("out_scale_len", c_int64),
+                ("pse", _P), ("pse_strides", c_int64 * 4)]
 
 
 _SIGS = {

@@ -123,6 +123,10 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         for (int d = 0; d < a.dk2; ++d) acc += half_to_f32(kr2[d], f16) * qs[w][a.dk1 + d];
       }
       s = acc * a.scale;
+      if (a.pse)
+        s += half_to_f32(static_cast<const uint16_t*>(a.pse)[b * a.pse_strides[0] + h * a.pse_strides[1] +
+                                                              i * a.pse_strides[2] + j * a.pse_strides[3]],
+                         f16);
     }
     const float mc = wave_max(s);
     if (mc == -INFINITY) continue;  // nothing visible in this chunk
