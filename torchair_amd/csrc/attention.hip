@@ -1058,10 +1058,11 @@ struct MlaArgs {
 
 // Raw ring stage: [latent 32 x 512 B][rope 32 x 128 B][one 256 B scale slot per wave].
 // bf16 tile: [latent 32 x 1 KB][rope 32 x 128 B][scale 32 x 4 B].
-// Latent chunk c of tile row r sits at chunk c ^ X(r), X(r) = ((r & 7) << 1) | ((r >> 3) & 1): 16
-// rows at one chunk hit 16 distinct 16-byte bank groups, and so do 4 consecutive rows x 2 chunks
-// (the transposing reads). X only moves the low four bits, so chunk 16q + c' is 256 q bytes past
-// chunk c' ^ X(r), and X(r + 16) = X(r). Rope chunk c of row r (raw and tile) sits at c ^ ((r >> 1) & 7).
+// Latent chunk c of tile row r sits at chunk c ^ X(r), X(r) = ((r & 3) << 2) | ((r >> 2) & 3): 16
+// rows at one chunk hit 16 distinct 16-byte bank groups (the K reads, 16 lanes a pass), and 4
+// consecutive rows x 4 chunks hit all 16 (the transposing V reads, 32 lanes a pass: X(r) >> 2
+// differs over the 4 rows, so chunk sets {0..3} ^ X(r) are disjoint). X only moves the low four
+// bits, so chunk 16q + c' is 256 q bytes past chunk c' ^ X(r), and X(r + 16) = X(r). Rope chunk c of row r (raw and tile) sits at c ^ ((r >> 1) & 7).
 constexpr int kMlaLatBytes = kMlaStep * 512;
 constexpr int kMlaRopeOff = kMlaLatBytes;
 constexpr int kMlaScaleOff = kMlaRopeOff + kMlaStep * 128;
@@ -1072,7 +1073,7 @@ constexpr int kMlaTile = kMlaTScale + kMlaStep * 4;
 constexpr int kMlaLds = kMlaRing * kMlaRaw + 2 * kMlaTile;
 static_assert(kMlaLds <= 160 * 1024, "LDS budget");
 
-__device__ __forceinline__ int mla_x(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int mla_x(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 
 template <int IMM>
@@ -1228,19 +1229,18 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, bool& 
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)smem));
   const uint32_t tiles = lds0 + kMlaRing * kMlaRaw;
   // Raw step s -> bf16 tile t. Latent: 2048 units of 8 bytes, eight per thread: unit u is row
-  // 8w + 4(u / 4) + lane / 16, 8-byte source unit (= bf16 chunk) 16(u % 4) + lane % 16. Rope rows
-  // and scales are copied as they are (16 bytes per thread; scales by threads 0-7).
+  // 8w + u, 8-byte source unit (= bf16 chunk) lane, so each 32-lane read pass covers 256 contiguous
+  // bytes of one raw row. Rope rows and scales are copied as they are (16 bytes per thread; scales
+  // by threads 0-7).
   auto convert = [&](int s, auto t_c) __attribute__((always_inline)) {
     constexpr int T = decltype(t_c)::value * kMlaTile;
     const uint32_t raw = lds0 + (s % kMlaRing) * kMlaRaw;
-    const int rsub = lane >> 4;
     v2i_t r[8];
     v4i_t rope, scl;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int row = 8 * w + 4 * (u / 4) + rsub;
-      const int c = 16 * (u % 4) + (lane & 15);
-      asm volatile("ds_read_b64 %0, %1" : "=v"(r[u]) : "v"(raw + row * 512 + 8 * c));
+      const int row = 8 * w + u;
+      asm volatile("ds_read_b64 %0, %1" : "=v"(r[u]) : "v"(raw + row * 512 + 8 * lane));
     }
     lds_read_b128<kMlaRopeOff>(rope, raw + 16 * tid);
     lds_read_b128<kMlaScaleOff>(scl, raw + 16 * (tid & 7));
@@ -1250,8 +1250,8 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, char* smem, bool& 
     asm volatile("" : "+v"(rope), "+v"(scl));
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int row = 8 * w + 4 * (u / 4) + rsub;
-      const int c = 16 * (u % 4) + (lane & 15);
+      const int row = 8 * w + u;
+      const int c = lane;
       uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
