@@ -152,6 +152,13 @@ int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, i
                      int x2_layout, const float* scale, int64_t scale_len, const float* offset,
                      int64_t offset_len, const float* pertoken_scale, const void* bias, int bias_dtype,
                      int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream);
+/* Weight prepacking for tai_quant_matmul, no counterpart in the reference's interface (the NPU's
+ * weights are cast to their own format at load time, npu_format_cast): a [K, N] int8 weight is
+ * transposed once into [N, K] storage, which the GEMM reads as x2_layout TAI_LAYOUT_NK.
+ * tai_quant_matmul_prepack_wanted says whether an M x K x N product takes that path (tall products;
+ * otherwise the [K, N] kernel is as fast). The transpose needs k % 64 == 0 and n % 256 == 0. */
+int tai_transpose_kn_to_nk(const int8_t* b, int64_t k, int64_t n, int8_t* out, void* stream);
+int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n);
 
 /* ---------------------------------------------------------------------------------------
  * npu_grouped_matmul, int8 path with split_item 2/3 and group_type 0 (groups along M):

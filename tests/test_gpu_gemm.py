@@ -270,3 +270,19 @@ def test_grouped_matmul_mixed_tiles(out):
         want = G.grouped_matmul(x.numpy(), w.numpy(), counts.numpy(), 1, scale=sc.numpy(), per_token_scale=pts.numpy(),
                                 out_dtype="bf16")
         np.testing.assert_array_equal(f32np(got), want)
+
+
+def test_quant_matmul_kn_weight_prepacked_once_and_refreshed_on_write():
+    """A tall product with a [K, N] weight runs the [N, K] kernel on a copy transposed once per weight:
+    exact on the first call and on a repeat, and again after the weight is written in place."""
+    from torchair_amd import _ops_impl
+    g = gen(27)
+    m, k, n = 4096, 512, 768
+    x = rand_i8((m, k), g).to(DEV)
+    w = rand_i8((k, n), g).to(DEV)
+    for step in range(3):
+        if step == 2:
+            w.mul_(-1)  # in place: the cached copy is stale and must be rebuilt
+        got = torch.ops.npu.npu_quant_matmul(x, w, torch.ones(1, device=DEV), output_dtype=torch.int32)
+        np.testing.assert_array_equal(got.cpu().numpy(), G.int_matmul(x.cpu().numpy(), w.cpu().numpy()))
+        assert id(w) in _ops_impl._NK_CACHE

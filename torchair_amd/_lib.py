@@ -53,6 +53,8 @@ _SIGS = {
     "tai_dynamic_quant_v2": (
         c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, c_int, c_int, c_float, _P, _P, _P, _P, c_size_t,
                 _P]),
+    "tai_transpose_kn_to_nk": (c_int, [_P, c_int64, c_int64, _P, _P]),
+    "tai_quant_matmul_prepack_wanted": (c_int, [c_int64, c_int64, c_int64]),
     "tai_quant_matmul_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
     "tai_quant_matmul": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, _P, _P,

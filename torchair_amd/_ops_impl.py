@@ -15,6 +15,7 @@ registered here: calling these ops on CPU tensors raises.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import List, Optional, Sequence
 
 import torch
@@ -287,6 +288,30 @@ def _qmm_fake(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
     return torch.empty(shape, dtype=_qmm_out_dtype(output_dtype), device=x1.device)
 
 
+# [N, K] copies of [K, N] int8 weights, made once per weight (the NPU's counterpart is the format cast
+# of weights at load time). Keyed by the tensor object; an entry is dropped with its weight, and a
+# weight written in place (its version moves) or moved to another address is transposed anew.
+_NK_CACHE: dict = {}
+
+
+def _prepacked_nk(w: torch.Tensor, m: int):
+    """[N, K] storage of the contiguous [K, N] int8 weight w when a product of m rows takes the [N, K]
+    kernel (tall products), else None."""
+    k, n = w.shape
+    if not w.is_contiguous() or not _lib.query("tai_quant_matmul_prepack_wanted", m, k, n):
+        return None
+    key = id(w)
+    ent = _NK_CACHE.get(key)
+    if ent is not None and ent[0]() is w and ent[1] == w._version and ent[2] == w.data_ptr():
+        return ent[3]
+    if torch.cuda.is_current_stream_capturing():
+        return None  # no allocation inside a capture: the kernel transposes into its workspace
+    nk = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    _lib.call("tai_transpose_kn_to_nk", _p(w), k, n, _p(nk), _stream(w))
+    _NK_CACHE[key] = (weakref.ref(w, lambda _r, key=key: _NK_CACHE.pop(key, None)), w._version, w.data_ptr(), nk)
+    return nk
+
+
 def _weight_layout(w: torch.Tensor):
     """Returns (tensor, layout) with the last two dims either [K,N] row-major or a [N,K] row-major storage."""
     if w.is_contiguous():
@@ -314,6 +339,10 @@ def _qmm_cuda(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, out
     a = x1.contiguous()
     m = a.numel() // k if k else 0
     w, layout = _weight_layout(x2)
+    if layout == LAYOUT_KN:
+        nk = _prepacked_nk(w, m)
+        if nk is not None:
+            w, layout = nk, LAYOUT_NK
     # npu_trans_quant_param packs an fp32 scale (and offset) into int64 words; converting those words
     # numerically would give meaningless scales, so they are refused
     _check(scale is None or scale.dtype not in (torch.int64, torch.uint64),

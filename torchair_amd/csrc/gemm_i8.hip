@@ -1612,6 +1612,18 @@ extern "C" size_t tai_quant_matmul_workspace_size(int64_t m, int64_t k, int64_t 
   return base + static_cast<size_t>(m) * static_cast<size_t>(n) * sizeof(float) + 256;
 }
 
+extern "C" int tai_transpose_kn_to_nk(const int8_t* b, int64_t k, int64_t n, int8_t* out, void* stream) {
+  TAI_CHECK_ARG(k >= 0 && n >= 0, "tai_transpose_kn_to_nk: negative size");
+  TAI_UNSUPPORTED(k % 64 != 0 || n % 256 != 0, "tai_transpose_kn_to_nk: needs k %% 64 == 0 and n %% 256 == 0");
+  if (k == 0 || n == 0) return TAI_OK;
+  TAI_CHECK_ARG(b && out, "tai_transpose_kn_to_nk: null pointer");
+  transpose_i8_kernel<<<dim3(static_cast<unsigned>((k / 64) * (n / 256))), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      b, k, n, out);
+  return launch_status("tai_transpose_kn_to_nk");
+}
+
+extern "C" int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n) { return transpose_ok(m, k, n) ? 1 : 0; }
+
 extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
                                 const float* scale, int64_t scale_len, const float* offset, int64_t offset_len,
                                 const float* pertoken_scale, const void* bias, int bias_dtype, int out_dtype, void* out,
