@@ -598,15 +598,13 @@ def bench_mla(torch, dev, iters=30, cpu=False):
 
 
 # ----------------------------------------------------------------------------- CPU baseline (oracle)
-def cpu_baseline(layer, sample_experts=8):
+def cpu_baseline(layer):
     """The MoE layer on the host through the CPU debug path: the oracle registered as the npu ops' CPU
     kernels, gating -> init_routing -> dynamic_quant and finalize compiled with
     torch.compile(backend=get_npu_backend()), on the very inputs of the GPU run (copied back from HBM).
-    All 4096 tokens are routed, quantised and finalized (one timed run after a warm-up compile run).
-    The expert chain (gate_up int32 -> dequant_swiglu_quant -> down bf16) runs for a sample of
-    experts spread over the row-count distribution (smallest, largest and evenly spaced ranks), each
-    timed once after one untimed call; a least-squares fit time = a + b * rows over the sample gives
-    every live expert's time."""
+    All 4096 tokens are routed, quantised and finalized (one timed run after a warm-up compile run),
+    and the expert chain (gate_up int32 -> dequant_swiglu_quant -> down bf16) runs for every live
+    expert, each timed once (one untimed call of the first warms the path)."""
     import torch
     from oracle import cpu_ops
     from torchair_amd import get_npu_backend
@@ -642,8 +640,6 @@ def cpu_baseline(layer, sample_experts=8):
     cnt = counts.numpy()
     ends = np.cumsum(cnt)
     live = [e for e in range(L.E) if cnt[e] > 0]
-    order = sorted(live, key=lambda e: cnt[e])
-    picks = sorted({order[round(i * (len(order) - 1) / (sample_experts - 1))] for i in range(sample_experts)})
     one = torch.ones(1)
 
     def expert(e):
@@ -658,27 +654,20 @@ def cpu_baseline(layer, sample_experts=8):
             return npu.npu_quant_matmul(q2, w_d, s_d, pertoken_scale=s2, output_dtype=torch.bfloat16)
         return run
 
-    expert(picks[0])()  # warm-up
-    rows, secs = [], []
-    for e in picks:
-        run = expert(e)
+    expert(live[0])()  # warm-up
+    t_exp = 0.0
+    for e in live:
+        run = expert(e)  # (the weights' host copies are made outside the timed call)
         t0 = time.perf_counter()
         run()
-        secs.append(time.perf_counter() - t0)
-        rows.append(int(cnt[e]))
-    if len(set(rows)) >= 2:
-        b_fit, a_fit = np.polyfit(np.array(rows, np.float64), np.array(secs), 1)
-    else:
-        a_fit, b_fit = float(np.mean(secs)), 0.0
-    t_exp = float(sum(a_fit + b_fit * cnt[e] for e in live))
+        t_exp += time.perf_counter() - t0
     total = t_route + t_fin + t_exp
     return {"value": round(L.T / total, 2), "unit": "tokens/s", "cores": _cpu_threads(), "kind": "port",
             "sample": f"numpy oracle as the npu ops' CPU kernels under torch.compile(backend=get_npu_backend()), on "
-                      f"the GPU run's inputs: routing + quant ({t_route:.1f} s) and finalize ({t_fin:.1f} s) for all "
-                      f"{L.T} tokens, one timed run each after a warm-up; expert chains of {len(picks)} of "
-                      f"{len(live)} live experts (rows {min(rows)}-{max(rows)}, {sum(secs):.1f} s), each timed once "
-                      f"after a warm-up call, fitted as {a_fit * 1e3:.0f} ms + {b_fit * 1e3:.3f} ms/row and summed "
-                      f"over all live experts ({t_exp:.1f} s)"}
+                      f"the GPU run's inputs, the whole layer: routing + quant ({t_route:.1f} s) and finalize "
+                      f"({t_fin:.1f} s) for all {L.T} tokens, one timed run each after a warm-up, and the expert "
+                      f"chains of all {len(live)} live experts ({int(cnt.sum())} rows, {t_exp:.1f} s), each timed "
+                      f"once"}
 
 
 # ----------------------------------------------------------------------------- counter calibration
