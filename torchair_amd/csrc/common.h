@@ -170,10 +170,13 @@ __device__ __forceinline__ int8_t quant_i8(float v, float scale, float inv) {
 
 __device__ __forceinline__ float rcp_f32(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// silu(a) = a / (1 + exp(-a)), the divide by the hardware reciprocal (1 ulp). Every SwiGLU path
-// (dequant_swiglu_quant and the fused grouped-GEMM epilogue) uses this one definition, so they agree
-// bit for bit.
-__device__ __forceinline__ float silu_f32(float a) { return a * rcp_f32(1.0f + expf(-a)); }
+// silu(a) = a / (1 + exp(-a)) from the hardware exp2 and reciprocal: exp(-a) = exp2(-a * log2(e)),
+// within a few ulp for the |a| that matter (the product's rounding grows with |a|, and past |a| ~ 20
+// the term is 0 or a itself), the divide within 1 ulp. Every SwiGLU path (dequant_swiglu_quant and the
+// fused grouped-GEMM epilogue) uses this one definition, so they agree bit for bit.
+__device__ __forceinline__ float silu_f32(float a) {
+  return a * rcp_f32(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
+}
 
 __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t v, int lane) {
 #pragma unroll

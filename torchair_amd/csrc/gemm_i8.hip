@@ -53,7 +53,7 @@ struct GemmArgs {
   int64_t n_tiles;
   const int64_t* live_slots;  // grouped: slots in use (real + zero-fill tiles), written by the prologue
   float* h;          // SwiGLU epilogue: silu(gate) * up, fp32 [m, n / 2]
-  float* amax_part;  // SwiGLU epilogue: per-row max |h| of each column tile, [m, n_tiles]
+  float* amax_part;  // SwiGLU epilogue: per-row max |h| of each 64-output-column part, [m, n / 128]
   // split-K (dense, int32 partials): k_split slices of k_per K stages each; slice s writes its raw
   // accumulators to out + s * m * n
   int64_t k_split;
@@ -587,49 +587,72 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
 }
 
 // SwiGLU epilogue of npu_grouped_matmul_swiglu_quant_v2 (the arithmetic of npu_dequant_swiglu_quant
-// with activate_left): d = (float(acc) * weight_scale[col]) * x_scale[row]; h = silu(d_gate) * d_up
-// with silu(a) = a / (1 + exp(-a)). Writes h (fp32) and, per row, the max |h| over this tile's
-// output columns; a second kernel turns them into the per-row int8 quantisation.
+// with activate_left): d = (float(acc) * weight_scale[col]) * x_scale[row]; h = silu(d_gate) * d_up.
+// Writes h (fp32) and, per row, the max |h| over each wave's 64 output columns (part index
+// (first output column) / 64); a second kernel turns them into the per-row int8 quantisation.
 // Accumulator blocks j = 0, 1 hold gate columns and j = 2, 3 the matching up columns (weight_col).
+// h leaves through a wave-private LDS region as 16-byte non-temporal stores along the rows.
 template <class C>
 __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&acc)[2][4], int e, int row0, int rows,
-                                                int64_t n0, int64_t nt, int w, int lane, int8_t* smem) {
+                                                int64_t n0, int w, int lane, int8_t* smem) {
 #pragma clang fp contract(off)
   constexpr int WN = C::kBN / 128;
   const int wm = w / WN, wn = w % WN;
   const int64_t n2 = g.n / 2;
+  const int64_t oc0 = n0 / 2 + 64 * wn;  // this wave's first output column
   const float* ws = g.scale + e * g.scale_group_stride;
   float wg[2], wu[2];  // weight scales of this lane's gate / up columns
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t oc = n0 / 2 + 64 * wn + 32 * j + (lane & 31);
+    const int64_t oc = oc0 + 32 * j + (lane & 31);
     wg[j] = ws[oc];
     wu[j] = ws[oc + n2];
   }
+  // one x_scale per lane (row wm * 64 + lane), handed to the lanes that need it by a cross-lane read
+  const float my_xs = g.pts[row0 + min(wm * 64 + lane, rows - 1)];
+  constexpr int RB = 64 * 4 + 16;  // LDS row bytes of a 16-row slice (64 fp32 + pad)
+  static_assert(8 * 16 * RB <= C::kLds, "epilogue staging must fit in the ring");
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is past the ring
+  char* wreg = reinterpret_cast<char*>(smem) + w * (16 * RB);
   float rmax[2][16];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const bool live = lr < rows;
-      const float xs = live ? g.pts[row0 + lr] : 0.0f;
-      float m = 0.0f;
+    for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t oc = n0 / 2 + 64 * wn + 32 * j + (lane & 31);
-        const float dg = (static_cast<float>(acc[i][j][r]) * wg[j]) * xs;
-        const float du = (static_cast<float>(acc[i][j + 2][r]) * wu[j]) * xs;
-        const float hv = silu_f32(dg) * du;
-        if (live) g.h[static_cast<int64_t>(row0 + lr) * n2 + oc] = hv;
-        m = fmaxf(m, fabsf(hv));
+      for (int rr = 0; rr < 8; ++rr) {
+        const int r = 8 * hh + rr;
+        const int sl = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);  // row within the 16-row slice
+        const float xs = __shfl(my_xs, i * 32 + 16 * hh + sl, 64);
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float dg = (static_cast<float>(acc[i][j][r]) * wg[j]) * xs;
+          const float du = (static_cast<float>(acc[i][j + 2][r]) * wu[j]) * xs;
+          const float hv = silu_f32(dg) * du;
+          *reinterpret_cast<float*>(wreg + sl * RB + (32 * j + (lane & 31)) * 4) = hv;
+          m = fmaxf(m, fabsf(hv));
+        }
+        rmax[i][r] = m;
       }
-      rmax[i][r] = m;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int sl = 4 * q + (lane >> 4);
+        const int lr = wm * 64 + i * 32 + 16 * hh + sl;
+        const v4i v = *reinterpret_cast<const v4i*>(wreg + sl * RB + 16 * (lane & 15));
+        if (lr < rows) {
+          typedef __attribute__((address_space(1))) v4i gv4i;
+          float* dst = g.h + static_cast<int64_t>(row0 + lr) * n2 + oc0 + 4 * (lane & 15);
+          __builtin_nontemporal_store(v, (gv4i*)(reinterpret_cast<uintptr_t>(dst)));
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next slice
     }
   // Max over the 32 lanes that share a row (lanes of one half-wave hold one row's columns), as a
   // reduce-scatter: at the step with lane offset o each lane keeps half of its live row values and
   // sends the partner the other half, so 16 + 8 + 4 + 2 + 1 shuffles leave lane l (of its half)
-  // with the max of row value l (i = l / 16, r = l % 16); then over the waves sharing the row (LDS).
+  // with the max of row value l (i = l / 16, r = l % 16).
   float v[32];
 #pragma unroll
   for (int t = 0; t < 32; ++t) v[t] = rmax[t >> 4][t & 15];
@@ -649,20 +672,9 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& g, const v16i (&
   halve(std::integral_constant<int, 4>());
   halve(std::integral_constant<int, 2>());
   halve(std::integral_constant<int, 1>());
-  float* red = reinterpret_cast<float*>(smem);  // [WN][kBM]
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  {
-    const int i = l32 >> 4, r = l32 & 15;
-    const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    red[wn * C::kBM + lr] = v[0];
-  }
-  __syncthreads();
-  for (int lr = threadIdx.x; lr < rows && lr < C::kBM; lr += C::kThreads) {
-    float m = red[lr];
-#pragma unroll
-    for (int q = 1; q < WN; ++q) m = fmaxf(m, red[q * C::kBM + lr]);
-    g.amax_part[static_cast<int64_t>(row0 + lr) * g.n_tiles + nt] = m;
-  }
+  const int i = l32 >> 4, r = l32 & 15;
+  const int lr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+  if (lr < rows) g.amax_part[static_cast<int64_t>(row0 + lr) * (g.n / 128) + oc0 / 64] = v[0];
 }
 
 // One tile of the big-tile kernel: rows [row0, row1) of group e (dense: e = 0), column tile nt,
@@ -683,7 +695,8 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
           const int64_t r = row0 + idx / (C::kBN / 2), c = o0 + idx % (C::kBN / 2);
           if (c < n2) g.h[r * n2 + c] = 0.0f;
         }
-        for (int r = row0 + threadIdx.x; r < row1; r += C::kThreads) g.amax_part[r * g.n_tiles + nt] = 0.0f;
+        for (int idx = threadIdx.x; idx < (row1 - row0) * WN; idx += C::kThreads)  // the tile's 64-column parts
+          g.amax_part[(row0 + idx / WN) * (g.n / 128) + o0 / 64 + idx % WN] = 0.0f;
       } else {
         for (int idx = threadIdx.x; idx < (row1 - row0) * C::kBN; idx += C::kThreads) {
           const int64_t r = row0 + idx / C::kBN, c = n0 + idx % C::kBN;
@@ -883,7 +896,7 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
   else dispatch(std::integral_constant<int, 0>());
 
   if constexpr (OUT == kOutSwiglu) {
-    swiglu_epilogue<C>(g, acc, e, row0, rows, n0, nt, w, lane, smem);
+    swiglu_epilogue<C>(g, acc, e, row0, rows, n0, w, lane, smem);
     return;
   }
   // Epilogue, specialised on the output dtype so the accumulators stay in registers.
@@ -1126,7 +1139,8 @@ bool mixed_available() {
     const bool r = set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_INT32>)) &&
                    set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_BF16>)) &&
                    set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_FP16>)) &&
-                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_FP32>));
+                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<TAI_DT_FP32>)) &&
+                   set(reinterpret_cast<const void*>(&gemm_i8_mixed_kernel<kOutSwiglu>));
     (void)hipGetLastError();
     return r;
   }();
@@ -1141,6 +1155,7 @@ void launch_mixed(const GemmArgs& g, hipStream_t st) {
     case TAI_DT_INT32: gemm_i8_mixed_kernel<TAI_DT_INT32><<<grid, T, L, st>>>(g); break;
     case TAI_DT_BF16: gemm_i8_mixed_kernel<TAI_DT_BF16><<<grid, T, L, st>>>(g); break;
     case TAI_DT_FP16: gemm_i8_mixed_kernel<TAI_DT_FP16><<<grid, T, L, st>>>(g); break;
+    case kOutSwiglu: gemm_i8_mixed_kernel<kOutSwiglu><<<grid, T, L, st>>>(g); break;
     default: gemm_i8_mixed_kernel<TAI_DT_FP32><<<grid, T, L, st>>>(g); break;
   }
 }
@@ -1953,8 +1968,9 @@ extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* we
              map, slots, n_tiles, live, h, part};
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type,
                                                                               m, bm, map, slots, live, nullptr);
-  if (kn) launch_cfg<GrpKnSel>(g, w_layout, st);
+  if (kn && TAI_MIXED && n % GrpKnSel::kBN == 0 && mixed_available()) launch_mixed(g, st);
+  else if (kn) launch_cfg<GrpKnSel>(g, w_layout, st);
   else launch_cfg<GrpSel>(g, w_layout, st);
-  swiglu_quant_kernel<<<dim3(static_cast<unsigned>(cdiv(m, 4))), 256, 0, st>>>(h, part, n_tiles, m, n / 2, y, y_scale);
+  swiglu_quant_kernel<<<dim3(static_cast<unsigned>(cdiv(m, 4))), 256, 0, st>>>(h, part, n / 128, m, n / 2, y, y_scale);
   return launch_status("tai_grouped_matmul_swiglu_quant");
 }
