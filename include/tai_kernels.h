@@ -155,8 +155,9 @@ int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, i
 /* Weight prepacking for tai_quant_matmul, no counterpart in the reference's interface (the NPU's
  * weights are cast to their own format at load time, npu_format_cast): a [K, N] int8 weight is
  * transposed once into [N, K] storage, which the GEMM reads as x2_layout TAI_LAYOUT_NK.
- * tai_quant_matmul_prepack_wanted says whether an M x K x N product takes that path (tall products;
- * otherwise the [K, N] kernel is as fast). The transpose needs k % 64 == 0 and n % 256 == 0. */
+ * tai_quant_matmul_prepack_wanted says whether an M x K x N product takes that path (tall products, and
+ * decode-sized ones of at most 128 rows, whose weight stream is contiguous per row in [N, K] storage).
+ * The transpose needs k % 64 == 0 and n % 256 == 0. */
 int tai_transpose_kn_to_nk(const int8_t* b, int64_t k, int64_t n, int8_t* out, void* stream);
 int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n);
 

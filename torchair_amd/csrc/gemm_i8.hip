@@ -1265,8 +1265,10 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
   using Sh = SkinnyShape<MI, BN>;
   constexpr int D = Sh::kD, NJ = BN / 32, NL = Sh::kNL;
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-  const int64_t L = xcd_remap(blockIdx.x, g.n_tiles * g.k_split);  // consecutive slabs share an XCD's L2
-  const int64_t slab = L / g.k_split, ks = L % g.k_split;
+  // consecutive ids (the K slices and row tiles of one slab, then the next slabs) share an XCD's L2
+  const int64_t L = xcd_remap(blockIdx.x, g.n_tiles * g.m_slots * g.k_split);
+  const int64_t ks = L % g.k_split, rt = (L / g.k_split) % g.m_slots, slab = L / (g.k_split * g.m_slots);
+  const int64_t rb = rt * MI * 32;  // first row of this row tile
   const int64_t n0 = slab * BN;
   const int64_t nk = g.k / 64;
   const int64_t kb = ks * g.k_per;
@@ -1275,7 +1277,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ns = kb + w < ke ? static_cast<int>((ke - kb - w + 3) / 4) : 0;  // stages kb + w + 4t of this wave
   int8_t* ring = smem + w * D * Sh::kSlot;
-  const int m = static_cast<int>(g.m);
+  const int m = static_cast<int>(g.m - rb < MI * 32 ? g.m - rb : MI * 32);  // rows of this row tile
 
   // weight source of load q relative to the stage's first K row, and the LDS placement: lane L of a
   // load fills bytes 16L .. 16L + 15 of its 1 KB
@@ -1316,7 +1318,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
   for (int q = 0; q < 2 * MI; ++q) {
     const int r = 16 * q + lane / 4;
     const int c = (lane & 3) ^ ((r >> 2) & 3);
-    asrc[q] = g.a + static_cast<int64_t>(r < m ? r : m - 1) * g.k + 16 * c;
+    asrc[q] = g.a + (rb + (r < m ? r : m - 1)) * g.k + 16 * c;
   }
   auto issue_a = [&](int t, int slot) {
     const int64_t k0 = stage_k(t);
@@ -1433,7 +1435,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
       const int4 v = *reinterpret_cast<const int4*>(red + q * kTileWords + row * Sh::kRowWords + c4);
       s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
-    const int64_t o = static_cast<int64_t>(row) * g.n + col;
+    const int64_t o = (rb + row) * g.n + col;
     if (partial) {
       *reinterpret_cast<int4*>(static_cast<int32_t*>(g.out) + ks * g.m * g.n + o) = s;
       continue;
@@ -1447,7 +1449,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
       *reinterpret_cast<int4*>(static_cast<int32_t*>(g.out) + o) = make_int4(v[0], v[1], v[2], v[3]);
       continue;
     }
-    const float pt = g.pts ? g.pts[row] : 1.0f;
+    const float pt = g.pts ? g.pts[rb + row] : 1.0f;
     float f[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1471,20 +1473,29 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_skinny_kernel(GemmArgs g) {
 // the config-1 down projection the split plus its reduction takes 15 us, one workgroup per slab 21 us).
 struct SkinnyPlan {
   int bn, mi;
-  int64_t slabs, split, per;
+  int64_t slabs, row_tiles, split, per;
 };
 
 bool skinny_fit(int64_t m, int64_t k, int64_t n) {
   return m >= 1 && m <= 128 && k >= 64 && k % 64 == 0 && n >= 16 && n % 16 == 0 && n < (1ll << 31);
 }
 
+#ifndef TAI_SK_ROWTILES
+#define TAI_SK_ROWTILES 1
+#endif
 SkinnyPlan skinny_fit_plan(int64_t m, int64_t k, int64_t n) {
   SkinnyPlan p{};
-  p.mi = m <= 32 ? 1 : (m <= 64 ? 2 : 4);
   p.bn = cdiv(n, 64) >= 128 ? 64 : 32;
   p.slabs = cdiv(n, p.bn);
+  // 65..128 rows over few slabs (which would split K four ways or more): two row tiles of 64 instead,
+  // so K splits half as often and the partials to sum halve (config-1 down projection 12.3 -> 10.0 us
+  // with [N, K] weights; with 176 slabs, as in its gate_up, the row tiles measured slower)
+  const bool split_rows = TAI_SK_ROWTILES && m > 64 && p.slabs < 128;
+  p.mi = m <= 32 ? 1 : (m <= 64 || split_rows ? 2 : 4);
+  p.row_tiles = cdiv(m, 32 * p.mi);
   const int64_t nk = k / 64;
-  int64_t want = (256 + p.slabs / 2) / p.slabs;
+  const int64_t units = p.slabs * p.row_tiles;
+  int64_t want = (256 + units / 2) / units;
   const int64_t cap = nk / 4 > 1 ? nk / 4 : 1;
   want = want < 1 ? 1 : (want > cap ? cap : want);
   p.per = cdiv(nk, want);
@@ -1499,7 +1510,7 @@ bool skinny_launch_one(const GemmArgs& g, hipStream_t st) {
                                                 hipFuncAttributeMaxDynamicSharedMemorySize, Sh::kLds) == hipSuccess;
   if (!ready) return false;
   gemm_i8_skinny_kernel<LAYOUT, MI, BN>
-      <<<dim3(static_cast<unsigned>(g.n_tiles * g.k_split)), 256, Sh::kLds, st>>>(g);
+      <<<dim3(static_cast<unsigned>(g.n_tiles * g.m_slots * g.k_split)), 256, Sh::kLds, st>>>(g);
   return true;
 }
 
@@ -1637,7 +1648,13 @@ extern "C" int tai_transpose_kn_to_nk(const int8_t* b, int64_t k, int64_t n, int
   return launch_status("tai_transpose_kn_to_nk");
 }
 
-extern "C" int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n) { return transpose_ok(m, k, n) ? 1 : 0; }
+extern "C" int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n) {
+  // tall products (the [N, K] big kernel) and decode-sized ones (the skinny kernel streams each
+  // weight row's K range contiguously from [N, K] storage instead of 32- or 64-byte pieces of every
+  // [K, N] row: config-1 gate_up 12.4 -> 10.7 us)
+  const bool tiles = k % 64 == 0 && n % 256 == 0;
+  return (transpose_ok(m, k, n) || (tiles && skinny_fit(m, k, n))) ? 1 : 0;
+}
 
 extern "C" int tai_quant_matmul(const int8_t* x1, const int8_t* x2, int64_t m, int64_t k, int64_t n, int x2_layout,
                                 const float* scale, int64_t scale_len, const float* offset, int64_t offset_len,
@@ -1695,6 +1712,7 @@ static int quant_matmul_impl(const int8_t* x1, const int8_t* x2, int64_t m, int6
   if (skinny_fit(m, k, n)) {
     const SkinnyPlan p = skinny_fit_plan(m, k, n);
     g.n_tiles = p.slabs;
+    g.m_slots = p.row_tiles;
     g.k_split = p.split;
     g.k_per = p.per;
     if (p.split == 1) {
