@@ -455,6 +455,17 @@ typedef struct tai_fia_general_args {
    * pse_strides (a stride 0 broadcasts). */
   const void* pse;
   int64_t pse_strides[4];
+  /* shared prefix (k_prefix NULL: none; experiment_ops.h:3933-3935 key_shared_prefix /
+   * value_shared_prefix / actual_shared_prefix_len): prefix_len[0] rows of k_prefix / v_prefix (query
+   * dtype, element (t, kv head) at t * prefix_strides[0] + h * prefix_strides[1]) precede every
+   * sequence's keys and values; a sequence then holds prefix_len + its own kv length positions, over
+   * which the masks apply. */
+  const void* k_prefix;
+  const void* v_prefix;
+  int64_t k_prefix_strides[2];
+  int64_t v_prefix_strides[2];
+  const int64_t* prefix_len;
+  int64_t prefix_cap;  /* rows the prefix tensors hold (prefix_len is clamped to it) */
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 

@@ -624,6 +624,27 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
     return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask, pse=pse)
 
 
+def with_shared_prefix(k, v, seq_kv, k_prefix, v_prefix, prefix_len: int):
+    """Shared prefix of npu_fused_infer_attention_score (key_shared_prefix / value_shared_prefix /
+    actual_shared_prefix_len, prototype experiment_ops.h:3933-3935, passed on by the converter,
+    .../custom/fused_infer_attention_score.py:29-31, 94-109): the first prefix_len rows of the
+    [Sp, Hkv, D] prefix precede every sequence's own keys and values. k/v [B, Skv, Hkv, D]; returns
+    (k', v' [B, prefix_len + Skv, Hkv, D], seq_kv' [B]) for prefill_attention, whose atten_mask,
+    pse_shift and causal offsets then index the concatenated positions."""
+    k, v = np.asarray(k, F32), np.asarray(v, F32)
+    b_cnt, skv = k.shape[0], k.shape[1]
+    lp = int(prefix_len)
+    lens = [skv if seq_kv is None else int(seq_kv[b]) for b in range(b_cnt)]
+    kk = np.zeros((b_cnt, lp + skv) + k.shape[2:], F32)
+    vv = np.zeros((b_cnt, lp + skv) + v.shape[2:], F32)
+    for b in range(b_cnt):
+        kk[b, :lp] = np.asarray(k_prefix, F32)[:lp]
+        vv[b, :lp] = np.asarray(v_prefix, F32)[:lp]
+        kk[b, lp:lp + lens[b]] = k[b, :lens[b]]
+        vv[b, lp:lp + lens[b]] = v[b, :lens[b]]
+    return kk, vv, np.asarray([lp + x for x in lens], np.int64)
+
+
 def antiquant_kv(x, scale, offset=None, mode: int = 0):
     """Dequantisation of an int8 key / value of npu_fused_infer_attention_score:
     (x + offset) * scale in fp32. x is [B, S, Hkv, D] (dense, or gathered from a paged cache in

@@ -253,3 +253,47 @@ def test_pse_shift(paged):
                                    1 / math.sqrt(d), pse=f32np(pse))
     assert_close(f32np(out.reshape(b, sq, hq, d)), want)
     np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("layout,paged", [("BSH", False), ("BNSD", False), ("BSH", True)])
+def test_shared_prefix(layout, paged):
+    """key_shared_prefix / value_shared_prefix: actual_shared_prefix_len rows shared by every sequence
+    precede its own keys; the causal rule counts them as kv positions."""
+    g = torch.Generator().manual_seed(157)
+    b, sq, hq, hkv, d = 3, 4, 8, 2, 128
+    lq, lkv, sp, lp = [4, 2, 4], [70, 1, 33], 96, 77
+    kp = torch.randn(sp, hkv, d, generator=g).to(torch.bfloat16)
+    vp = torch.randn(sp, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b, sq, hq, d, generator=g).to(torch.bfloat16)
+    kw = dict(actual_seq_lengths=lq, actual_seq_lengths_kv=lkv, num_heads=hq, num_key_value_heads=hkv,
+              input_layout=layout, scale=1 / math.sqrt(d), sparse_mode=3, softmax_lse_flag=True,
+              actual_shared_prefix_len=[lp])
+    if layout == "BNSD":
+        kw.update(key_shared_prefix=kp.permute(1, 0, 2)[None].contiguous().to(DEV),
+                  value_shared_prefix=vp.permute(1, 0, 2)[None].contiguous().to(DEV))
+        qd = q.permute(0, 2, 1, 3).contiguous().to(DEV)
+    else:
+        kw.update(key_shared_prefix=kp.reshape(1, sp, hkv * d).to(DEV),
+                  value_shared_prefix=vp.reshape(1, sp, hkv * d).to(DEV))
+        qd = q.reshape(b, sq, hq * d).to(DEV)
+    if paged:
+        bs = 64
+        kc, vc, bt = _paged(lkv, hkv, d, bs, g, lambda sh: torch.randn(sh, generator=g).to(torch.bfloat16))
+        out, lse = FIA(qd, kc.reshape(-1, bs, hkv * d).to(DEV), vc.reshape(-1, bs, hkv * d).to(DEV),
+                       block_table=bt.to(DEV), block_size=bs, **kw)
+        kd, vd = _gather(f32np(kc), bt, lkv, bs), _gather(f32np(vc), bt, lkv, bs)
+    else:
+        skv = 70
+        k = torch.randn(b, skv, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(b, skv, hkv, d, generator=g).to(torch.bfloat16)
+        if layout == "BNSD":
+            out, lse = FIA(qd, k.permute(0, 2, 1, 3).contiguous().to(DEV), v.permute(0, 2, 1, 3).contiguous().to(DEV),
+                           **kw)
+        else:
+            out, lse = FIA(qd, k.reshape(b, skv, hkv * d).to(DEV), v.reshape(b, skv, hkv * d).to(DEV), **kw)
+        kd, vd = f32np(k), f32np(v)
+    kk, vv, ll = G.with_shared_prefix(kd, vd, np.array(lkv), f32np(kp), f32np(vp), lp)
+    want, wl = G.prefill_attention(f32np(q), kk, vv, np.array(lq), ll, 1, 1 / math.sqrt(d))
+    got = out.cpu() if layout != "BNSD" else out.cpu().permute(0, 2, 1, 3)
+    assert_close(f32np(got.reshape(b, sq, hq, d)), want)
+    np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)

@@ -552,3 +552,26 @@ def test_pse_shift_reductions():
     o2, _ = G.prefill_attention(q, k, v, None, None, 0, 0.3, pse=m)
     o3, _ = G.prefill_attention(q, k, v, None, None, 0, 0.3, mask=mask)
     np.testing.assert_array_equal(o2, o3)
+
+
+def test_shared_prefix_reductions():
+    """A shared prefix of length 0 changes nothing; when every sequence's keys start with the same
+    rows, splitting those rows off into the shared prefix gives the same attention."""
+    rng = np.random.default_rng(45)
+    q = rng.standard_normal((2, 3, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 9, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 9, 2, 8)).astype(np.float32)
+    lens = np.array([9, 6])
+    kp, vp = rng.standard_normal((5, 2, 8)).astype(np.float32), rng.standard_normal((5, 2, 8)).astype(np.float32)
+    k0, v0, l0 = G.with_shared_prefix(k, v, lens, kp, vp, 0)
+    np.testing.assert_array_equal(k0[0], k[0])
+    np.testing.assert_array_equal(v0[1, :6], v[1, :6])
+    assert not k0[1, 6:].any()
+    np.testing.assert_array_equal(l0, lens)
+    k[:, :4], v[:, :4] = kp[:4], vp[:4]
+    base, bl = G.prefill_attention(q, k, v, None, lens, 1, 0.3)
+    kk, vv, ll = G.with_shared_prefix(k[:, 4:], v[:, 4:], lens - 4, kp, vp, 4)
+    np.testing.assert_array_equal(ll, lens)
+    o, ol = G.prefill_attention(q, kk, vv, None, ll, 1, 0.3)
+    np.testing.assert_allclose(o, base, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(ol, bl, rtol=1e-6, atol=1e-6)

@@ -139,8 +139,7 @@ def fia_fake(query, key, value, **kw):
 
 
 _UNSUPPORTED = ("dequant_scale1", "quant_scale1", "dequant_scale2", "query_padding_size",
-                "kv_padding_size", "key_shared_prefix", "value_shared_prefix", "actual_shared_prefix_len",
-                "key_rope_antiquant_scale")
+                "kv_padding_size", "key_rope_antiquant_scale")
 
 
 def _lens_tensor(v, device) -> Optional[torch.Tensor]:
@@ -217,6 +216,14 @@ def fia_cuda(query, key, value, **kw):
     pse = kw.get("pse_shift")
     _check(pse is None or kw.get("query_rope") is None, "npu_fused_infer_attention_score: pse_shift is served for "
            "GQA/MHA, not MLA")
+    prefix = kw.get("key_shared_prefix") is not None
+    _check(prefix == (kw.get("value_shared_prefix") is not None), "npu_fused_infer_attention_score: "
+           "key_shared_prefix and value_shared_prefix come together")
+    _check(not prefix or (kw.get("query_rope") is None and not kv8), "npu_fused_infer_attention_score: a shared "
+           "prefix is served for GQA/MHA with a float cache")
+    _check(prefix or kw.get("actual_shared_prefix_len") is None, "npu_fused_infer_attention_score: "
+           "actual_shared_prefix_len needs key_shared_prefix")
+    pse = pse if pse is not None else (True if prefix else None)  # both take the general kernel
     _check(kw.get("quant_offset2") is None or quant_out, "npu_fused_infer_attention_score: quant_offset2 needs "
            "quant_scale2")
     if kw.get("query_rope") is None:
@@ -427,6 +434,42 @@ def _antiquant_params(a, kw, b, n_kv, dk, dv, keep):
     a.k_quant_mode, a.v_quant_mode, a.tok_stride = km, vm, tok
 
 
+def _prefix_params(a, kw, ql, n_kv, dk, dv, query, keep) -> int:
+    """Shared prefix (experiment_ops.h:3933-3935; the converter passes key_shared_prefix,
+    value_shared_prefix and actual_shared_prefix_len on, fused_infer_attention_score.py:29-31, 94-109):
+    [1, Sp, H] (BSH), [1, Sp, N, D] (BSND) or [1, N, Sp, D] (BNSD) keys and values that precede every
+    sequence's own; actual_shared_prefix_len (one value, default Sp) of them are used."""
+    kp, vp = kw["key_shared_prefix"], kw["value_shared_prefix"]
+    _check(kp.dtype == query.dtype and vp.dtype == query.dtype and kp.size(0) == 1 and vp.size(0) == 1,
+           "npu_fused_infer_attention_score: shared prefixes are [1, ...] of the query's dtype")
+
+    def pos_head(t, d):
+        if ql == "BSH":
+            _check(t.dim() == 3 and t.size(2) == n_kv * d and t.stride(2) == 1,
+                   "npu_fused_infer_attention_score: a BSH shared prefix is [1, Sp, Hkv * D]")
+            return t.size(1), [t.stride(1), d]
+        if ql == "BSND":
+            _check(t.dim() == 4 and t.size(2) == n_kv and t.size(3) == d and t.stride(3) == 1,
+                   "npu_fused_infer_attention_score: a BSND shared prefix is [1, Sp, Hkv, D]")
+            return t.size(1), [t.stride(1), t.stride(2)]
+        _check(t.dim() == 4 and t.size(1) == n_kv and t.size(3) == d and t.stride(3) == 1,
+               "npu_fused_infer_attention_score: a BNSD shared prefix is [1, Hkv, Sp, D]")
+        return t.size(2), [t.stride(2), t.stride(1)]
+
+    sp, ks = pos_head(kp, dk)
+    spv, vs = pos_head(vp, dv)
+    _check(sp == spv, "npu_fused_infer_attention_score: key and value shared prefixes differ in length")
+    ln = kw.get("actual_shared_prefix_len")
+    lt = _lens_tensor(ln if ln is not None else [sp], query.device)
+    _check(lt.numel() == 1, "npu_fused_infer_attention_score: actual_shared_prefix_len holds one length")
+    a.k_prefix, a.v_prefix = kp.data_ptr(), vp.data_ptr()
+    a.k_prefix_strides = (ctypes.c_int64 * 2)(*ks)
+    a.v_prefix_strides = (ctypes.c_int64 * 2)(*vs)
+    a.prefix_len, a.prefix_cap = lt.data_ptr(), sp
+    keep.append(lt)
+    return sp
+
+
 def _out_quant_params(a, kw, hq, dv, keep):
     """int8 attention_out: clamp(rint(o * quant_scale2 + quant_offset2)), per tensor (1 entry) or per
     channel (Hq * Dv entries, channel h * Dv + d) (experiment_ops.h:3943)."""
@@ -450,17 +493,19 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
     dv = _value_d(bt, value, query, ql, n_kv)
     mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
     s_kv = (bt.size(1) * bs) if bt is not None else (key.size(2) if ql == "BNSD" else key.size(1))
-    if mask is not None:
-        _check(mask.size(2) >= (max(seq_kv.tolist()) if seq_kv is not None else s_kv),
-               "npu_fused_infer_attention_score: atten_mask covers fewer kv positions than the sequences hold")
     a = _general_args(dt, b, s_q, s_kv, hq, n_kv, d, 0, dv, query, _strides_bshd(query, ql, hq), None, None,
                       key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale,
                       out, _strides_bshd(out, ql, hq), lse if want_lse else None)
     keep = []  # fp32 copies of the scales, alive until the launch is queued (stream-ordered frees)
+    # Masks and position shifts index keys in the concatenated [shared prefix, own keys] space.
+    sp = _prefix_params(a, kw, ql, n_kv, d, dv, query, keep) if kw.get("key_shared_prefix") is not None else 0
+    if mask is not None:
+        _check(mask.size(2) >= sp + (max(seq_kv.tolist()) if seq_kv is not None else s_kv),
+               "npu_fused_infer_attention_score: atten_mask covers fewer kv positions than the sequences hold")
     pse = kw.get("pse_shift")
     if pse is not None:
         _check(pse.dtype == query.dtype and pse.dim() == 4 and pse.size(0) in (1, b) and pse.size(1) == hq
-               and pse.size(2) >= s_q and pse.size(3) >= s_kv,
+               and pse.size(2) >= s_q and pse.size(3) >= sp + s_kv,
                "npu_fused_infer_attention_score: pse_shift must be [B or 1, N, >= S_q, >= S_kv] of the query's dtype")
         a.pse = pse.data_ptr()
         a.pse_strides = (ctypes.c_int64 * 4)(0 if pse.size(0) == 1 else pse.stride(0), pse.stride(1), pse.stride(2),

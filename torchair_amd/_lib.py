@@ -36,7 +36,9 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("kv_dtype", c_int64), ("k_scale", _P), ("k_offset", _P), ("k_quant_mode", c_int64),
                 ("v_scale", _P), ("v_offset", _P), ("v_quant_mode", c_int64), ("tok_stride", c_int64),
                 ("out_dtype", c_int64), ("out_scale", _P), ("out_offset", _P), ("out_scale_len", c_int64),
-                ("pse", _P), ("pse_strides", c_int64 * 4)]
+                ("pse", _P), ("pse_strides", c_int64 * 4),
+                ("k_prefix", _P), ("v_prefix", _P), ("k_prefix_strides", c_int64 * 2),
+                ("v_prefix_strides", c_int64 * 2), ("prefix_len", _P), ("prefix_cap", c_int64)]
 
 
 _SIGS = {

@@ -62,7 +62,10 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   int64_t kv_cap = a.block_table ? a.max_blocks * a.block_size : a.s_kv;
   // per-token antiquant scales hold tok_stride positions per sequence
   if (KV8 && (a.k_quant_mode == 1 || a.v_quant_mode == 1)) kv_cap = imin64(kv_cap, a.tok_stride);
-  const int64_t lk = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
+  const int64_t lk_own = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
+  // a shared prefix precedes every sequence's own keys: positions [0, lp) read the prefix tensors
+  const int64_t lp = a.k_prefix ? imax64(0, imin64(a.prefix_len[0], a.prefix_cap)) : 0;
+  const int64_t lk = lp + lk_own;
   const int64_t o_off = b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
   const int dk = a.dk1 + a.dk2;
   // the query as fp32 in this wave's LDS row
@@ -107,7 +110,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
           }
         }
       } else {
-        const uint16_t* kr = k1 + gen_row(a, a.k1_strides, b, j, kvh);
+        const uint16_t* kr = j < lp ? static_cast<const uint16_t*>(a.k_prefix) + j * a.k_prefix_strides[0] +
+                                          kvh * a.k_prefix_strides[1]
+                                    : k1 + gen_row(a, a.k1_strides, b, j - lp, kvh);
         for (int d = 0; d < a.dk1; d += 8) {
           const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
           const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -119,7 +124,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         }
       }
       if (a.dk2) {
-        const uint16_t* kr2 = k2 + gen_row(a, a.k2_strides, b, j, kvh);
+        const uint16_t* kr2 = k2 + gen_row(a, a.k2_strides, b, j - lp, kvh);
         for (int d = 0; d < a.dk2; ++d) acc += half_to_f32(kr2[d], f16) * qs[w][a.dk1 + d];
       }
       s = acc * a.scale;
@@ -150,7 +155,10 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
                                    antiquant_index(a, a.v_quant_mode, b, t0 + jj, static_cast<int64_t>(kvh) * a.dv + d));
         }
       } else {
-        const uint16_t* vr = vv + gen_row(a, a.v_strides, b, t0 + jj, kvh);
+        const int64_t t = t0 + jj;
+        const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
+                                          kvh * a.v_prefix_strides[1]
+                                    : vv + gen_row(a, a.v_strides, b, t - lp, kvh);
 #pragma unroll
         for (int e = 0; e < kGenDvPerLane; ++e) {
           const int d = lane + 64 * e;
@@ -215,6 +223,11 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
     TAI_CHECK_ARG((a.k_quant_mode != 1 && a.v_quant_mode != 1) || a.tok_stride > 0,
                   "tai_fia_general: per-token scales need tok_stride > 0");
   }
+  TAI_CHECK_ARG(a.k_prefix == nullptr || (a.v_prefix && a.prefix_len && !kv8 && a.dk2 == 0),
+                "tai_fia_general: a shared prefix needs v_prefix and prefix_len, a float cache and one key part");
+  TAI_CHECK_ARG(a.k_prefix == nullptr || ((reinterpret_cast<uintptr_t>(a.k_prefix) % 16) == 0 &&
+                                          a.k_prefix_strides[0] % 8 == 0 && a.k_prefix_strides[1] % 8 == 0),
+                "tai_fia_general: shared-prefix key rows must be 16-byte aligned");
   if (a.out_dtype == TAI_DT_INT8)
     TAI_CHECK_ARG(a.out_scale && (a.out_scale_len == 1 || a.out_scale_len == a.hq * a.dv),
                   "tai_fia_general: int8 out needs out_scale of 1 or hq * dv entries");
