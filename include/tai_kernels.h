@@ -47,6 +47,10 @@ extern "C" {
 /* Layout of the second GEMM operand. */
 #define TAI_LAYOUT_KN 0 /* row-major [K, N] (N contiguous) */
 #define TAI_LAYOUT_NK 1 /* row-major [N, K] (K contiguous): the transpose_x2 / weight.t() view */
+/* [K, N] with the gate and up halves of a SwiGLU weight interleaved in 64-column blocks: column
+   128t + j is gate column 64t + j for j < 64 and up column N/2 + 64t + j - 64 otherwise
+   (tai_grouped_matmul_swiglu_quant only; tai_swiglu_pack_kn writes it) */
+#define TAI_LAYOUT_KN_SWIGLU 2
 
 /* Cache layouts of npu_scatter_pa_kv_cache (cache_mode). */
 #define TAI_CACHE_NORM 0  /* [num_blocks, block_size, row]: a slot's row is contiguous */
@@ -201,11 +205,16 @@ int tai_grouped_matmul_noalloc(const int8_t* x, const int8_t* weight, int64_t m,
  * Replaces ge.GroupedMatmulSwigluQuantV2 emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/grouped_matmul_swiglu_quant_v2.py:86-166
  *   (prototype fusion_ops.h:769-789).
- * x: [m, k] int8; weight: [num_groups, k, n] (_KN) or [num_groups, n, k] (_NK) int8;
- * weight_scale: [num_groups, n] fp32; x_scale: [m] fp32; y: [m, n/2] int8; y_scale: [m] fp32.
+ * x: [m, k] int8; weight: [num_groups, k, n] (_KN, or _KN_SWIGLU with gate / up interleaved) or
+ * [num_groups, n, k] (_NK) int8; weight_scale: [num_groups, n] fp32 (unpermuted); x_scale: [m] fp32; y: [m, n/2] int8; y_scale: [m] fp32.
  * Needs k % 64 == 0 and (n / 2) % 256 (_KN) or % 128 (_NK) == 0; TAI_ERR_UNSUPPORTED otherwise.
  * ------------------------------------------------------------------------------------- */
 size_t tai_grouped_matmul_swiglu_quant_workspace_size(int64_t m, int64_t n, int64_t num_groups);
+/* Weight prepacking for tai_grouped_matmul_swiglu_quant, no counterpart in the reference's interface
+ * (the NPU casts weights to its own format at load time, npu_format_cast): writes the
+ * TAI_LAYOUT_KN_SWIGLU copy of a [rows, n] int8 weight (rows = num_groups * k; n % 128 == 0), whose
+ * tiles then read each weight row's columns contiguously instead of as separate gate and up pieces. */
+int tai_swiglu_pack_kn(const int8_t* w, int64_t rows, int64_t n, int8_t* out, void* stream);
 int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, int64_t m, int64_t k,
                                     int64_t n, int64_t num_groups, int w_layout,
                                     const int64_t* group_list, int group_list_type,

@@ -114,3 +114,36 @@ def test_finalize_routing_on_the_moe_routing_path():
     ref = npu.npu_moe_finalize_routing(out, None, None, None, y_w, ri, idx, drop_pad_mode=2)
     # bf16 rounding of the 8 rows and of the output: errors scale with the terms, not their sum
     np.testing.assert_allclose(ref.float().cpu().numpy(), want, rtol=3e-2, atol=0.15)
+
+
+def test_swiglu_packed_weight_layout_and_cache():
+    """[E, K, N] weights are packed once (gate / up interleaved in 64-column blocks) and the packed copy
+    is rebuilt when the weight is written in place; results equal the unpacked layout bit for bit."""
+    from torchair_amd import _gmm_fused as F
+    g = gen(13)
+    counts = [70, 0, 200, 9]
+    x, w, ws, xs, cnt = _case(g, counts, 256, 1024)
+    xd, wd, wsd, xsd, cd = x.to(DEV), w.to(DEV), ws.to(DEV), xs.to(DEV), cnt.to(DEV)
+    p = F._swiglu_packed(wd)
+    e, k, n = w.shape
+    want = w.view(e, k, 2, n // 128, 64).permute(0, 1, 3, 2, 4).reshape(e, k, n)
+    assert torch.equal(p.cpu(), want)
+    assert F._swiglu_packed(wd) is p  # cached
+    y, s = npu.npu_grouped_matmul_swiglu_quant_v2(xd, [wd], [wsd], xsd, cd, group_list_type=1)
+    # the unpacked [K, N] layout through the C ABI
+    from torchair_amd import _lib
+    nbytes = _lib.query("tai_grouped_matmul_swiglu_quant_workspace_size", x.shape[0], n, e)
+    wsp = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    y0 = torch.empty_like(y)
+    s0 = torch.empty_like(s)
+    _lib.call("tai_grouped_matmul_swiglu_quant", xd.data_ptr(), wd.data_ptr(), x.shape[0], k, n, e, _lib.LAYOUT_KN,
+              cd.data_ptr(), 1, wsd.data_ptr(), xsd.data_ptr(), y0.data_ptr(), s0.data_ptr(), wsp.data_ptr(), nbytes,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0) and torch.equal(s, s0)
+    wd[1:3] = -wd[1:3]  # in-place write: the packed copy is stale
+    p2 = F._swiglu_packed(wd)
+    assert torch.equal(p2.cpu(), wd.cpu().view(e, k, 2, n // 128, 64).permute(0, 1, 3, 2, 4).reshape(e, k, n))
+    y3, _ = npu.npu_grouped_matmul_swiglu_quant_v2(xd, [wd], [wsd], xsd, cd, group_list_type=1)
+    wy, _ = G.grouped_matmul_swiglu_quant(x.numpy(), wd.cpu().numpy(), ws.numpy(), xs.numpy(), cnt.numpy(), 1)
+    assert_int8_close(y3.cpu().numpy(), wy)

@@ -8,10 +8,12 @@ Both take the W8A8 weights of all experts stacked as [E, K, N] (or the transpose
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _lib
-from ._lib import DT_NONE, LAYOUT_KN, LAYOUT_NK
+from ._lib import DT_NONE, LAYOUT_KN, LAYOUT_KN_SWIGLU, LAYOUT_NK
 from ._ops_impl import _DT, _check, _define, _f32, _on_gpu, _p, _stream
 
 
@@ -22,6 +24,36 @@ def _weight_layout(name, w3):
     if w3.transpose(1, 2).is_contiguous():
         return w3.transpose(1, 2), LAYOUT_NK
     return w3.contiguous(), LAYOUT_KN
+
+
+# Gate / up interleaved copies of [E, K, N] SwiGLU weights (TAI_LAYOUT_KN_SWIGLU), made once per weight
+# like the NPU's load-time format cast. Keyed by the weight's storage (address and shape), so aliases
+# of one weight (a Parameter made from a tensor shares its storage and version counter) share one
+# copy; an entry is dropped with the tensor that made it, and a weight written in place (its version
+# moves) is packed anew.
+_SWI_CACHE: dict = {}
+
+
+def _swiglu_packed(w3: torch.Tensor):
+    """The TAI_LAYOUT_KN_SWIGLU copy of the contiguous [E, K, N] weight w3, or None (N % 512 != 0,
+    or under hipGraph capture before a warm-up made it: nothing is allocated during a capture)."""
+    e, k, n = w3.shape
+    if not w3.is_contiguous() or n % 512 != 0:
+        return None
+    key = (w3.data_ptr(), tuple(w3.shape), w3.device.index)
+    ent = _SWI_CACHE.get(key)
+    if ent is not None and ent[0]() is not None and ent[1] == w3._version:
+        return ent[3]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    packed = torch.empty_like(w3)
+    _lib.call("tai_swiglu_pack_kn", _p(w3), e * k, n, _p(packed), _stream(w3))
+    def drop(ref, key=key):
+        if _SWI_CACHE.get(key, (None,))[0] is ref:  # not an entry made since by another tensor
+            del _SWI_CACHE[key]
+
+    _SWI_CACHE[key] = (weakref.ref(w3, drop), w3._version, None, packed)
+    return packed
 
 
 def _group_list(name, group_list, e, device):
@@ -58,6 +90,10 @@ def _gsq_cuda(x, weight, weight_scale, x_scale, group_list, *, smooth_scale=None
     wl, layout = _weight_layout(name, weight[0])
     e, k, n = weight[0].shape
     _check(x.shape[1] == k and n % 2 == 0, f"{name}: x is [M, K] and the weight [E, K, N] with N even")
+    if layout == LAYOUT_KN:
+        packed = _swiglu_packed(wl)
+        if packed is not None:
+            wl, layout = packed, LAYOUT_KN_SWIGLU
     ws = _f32(weight_scale[0])
     _check(ws.numel() == e * n, f"{name}: weight_scale must be [E, N]")
     xs = _f32(x_scale)

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libtai_kernels.so"
 # torch ScalarType codes used as dtype tags across the C ABI
 DT_UINT8, DT_INT8, DT_INT16, DT_INT32, DT_INT64, DT_FP16, DT_FP32, DT_BF16 = 0, 1, 2, 3, 4, 5, 6, 15
 DT_NONE = -1
-LAYOUT_KN, LAYOUT_NK = 0, 1
+LAYOUT_KN, LAYOUT_NK, LAYOUT_KN_SWIGLU = 0, 1, 2
 
 _P = c_void_p
 _I64x3 = c_int64 * 3
@@ -69,6 +69,7 @@ _SIGS = {
     "tai_grouped_matmul_noalloc": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P, _P]),
     "tai_grouped_matmul_swiglu_quant_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "tai_swiglu_pack_kn": (c_int, [_P, c_int64, c_int64, _P, _P]),
     "tai_grouped_matmul_swiglu_quant": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, _P, _P, c_size_t, _P]),
     "tai_grouped_matmul_finalize_routing_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),

@@ -58,6 +58,10 @@ struct GemmArgs {
   // accumulators to out + s * m * n
   int64_t k_split;
   int64_t k_per;
+  // SwiGLU epilogue: the weight is stored with gate and up interleaved in 64-column blocks (block 2t
+  // holds gate columns 64t .. 64t + 63, block 2t + 1 the matching up columns), so a tile's columns
+  // are contiguous in the weight rows
+  int swi_packed;
 };
 
 // Output code of the fused SwiGLU epilogue (npu_grouped_matmul_swiglu_quant_v2).
@@ -72,6 +76,7 @@ __device__ __forceinline__ int64_t weight_col(const GemmArgs& g, int64_t n0, int
   if constexpr (!SWI) {
     return n0 + tc;
   } else {
+    if (g.swi_packed) return n0 + tc;
     const int w = tc & 127;
     return (w < 64 ? 0 : g.n / 2) + n0 / 2 + 64 * (tc >> 7) + (w & 63);
   }
@@ -1648,6 +1653,33 @@ extern "C" int tai_transpose_kn_to_nk(const int8_t* b, int64_t k, int64_t n, int
   return launch_status("tai_transpose_kn_to_nk");
 }
 
+// [rows, n] int8 -> the same rows with 64-column blocks reordered: output block 2t is input block t
+// (a gate block), output block 2t + 1 is input block n / 128 + t (the matching up block). One thread
+// per 16 bytes.
+__global__ __launch_bounds__(256) void swiglu_pack_kernel(const int8_t* __restrict__ src, int64_t rows, int64_t n,
+                                                          int8_t* __restrict__ dst) {
+  const int64_t per_row = n / 16;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * per_row) return;
+  const int64_t r = i / per_row, c = (i % per_row) * 16;  // output column
+  const int64_t blk = c / 64, j = c % 64;
+  const int64_t sc = (blk & 1 ? n / 2 : 0) + 64 * (blk >> 1) + j;
+  *reinterpret_cast<uint4*>(dst + r * n + c) = *reinterpret_cast<const uint4*>(src + r * n + sc);
+}
+
+extern "C" int tai_swiglu_pack_kn(const int8_t* w, int64_t rows, int64_t n, int8_t* out, void* stream) {
+  TAI_CHECK_ARG(rows >= 0 && n >= 0, "tai_swiglu_pack_kn: negative size");
+  TAI_CHECK_ARG(n % 128 == 0, "tai_swiglu_pack_kn: n must be a multiple of 128");
+  if (rows == 0 || n == 0) return TAI_OK;
+  TAI_CHECK_ARG(w && out && w != out, "tai_swiglu_pack_kn: null or aliased pointer");
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
+  TAI_CHECK_ARG(al(w) && al(out), "tai_swiglu_pack_kn: 16-byte aligned pointers");
+  const int64_t threads = rows * (n / 16);
+  swiglu_pack_kernel<<<dim3(static_cast<unsigned>(cdiv(threads, 256))), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w, rows, n, out);
+  return launch_status("tai_swiglu_pack_kn");
+}
+
 extern "C" int tai_quant_matmul_prepack_wanted(int64_t m, int64_t k, int64_t n) {
   // tall products (the [N, K] big kernel) and decode-sized ones (the skinny kernel streams each
   // weight row's K range contiguously from [N, K] storage instead of 32- or 64-byte pieces of every
@@ -1952,7 +1984,10 @@ extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* we
                                                void* stream) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 2 && num_groups >= 1, "tai_grouped_matmul_swiglu_quant: bad sizes");
   TAI_CHECK_ARG(num_groups <= 2048, "tai_grouped_matmul_swiglu_quant: at most 2048 groups");
-  TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK, "tai_grouped_matmul_swiglu_quant: w_layout");
+  TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK || w_layout == TAI_LAYOUT_KN_SWIGLU,
+                "tai_grouped_matmul_swiglu_quant: w_layout");
+  const bool packed = w_layout == TAI_LAYOUT_KN_SWIGLU;
+  if (packed) w_layout = TAI_LAYOUT_KN;
   TAI_CHECK_ARG(group_list_type == 0 || group_list_type == 1, "tai_grouped_matmul_swiglu_quant: group_list_type");
   TAI_CHECK_ARG(group_list && weight_scale && x_scale, "tai_grouped_matmul_swiglu_quant: group_list, weight_scale and "
                 "x_scale are required");
@@ -1984,6 +2019,7 @@ extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* we
   const int64_t n_tiles = (n / 2) / (bn / 2);
   GemmArgs g{x, weight, m, k, n, k * n, weight_scale, n, n, x_scale, nullptr, 0, n, kOutSwiglu, nullptr,
              map, slots, n_tiles, live, h, part};
+  g.swi_packed = packed ? 1 : 0;
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type,
                                                                               m, bm, map, slots, live, nullptr);
   if (kn && TAI_MIXED && n % GrpKnSel::kBN == 0 && mixed_available()) launch_mixed(g, st);
