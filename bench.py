@@ -62,7 +62,7 @@ class MoeLayer:
         self.gmm1_events = []
         self.active_experts = None
 
-    def step(self, record=False, fused_quant=False):
+    def step(self, fused_quant=False):
         torch = self.torch
         npu = torch.ops.npu
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
@@ -81,11 +81,35 @@ class MoeLayer:
             q, s = npu.npu_dynamic_quant(ex)
         if self.active_experts is None:
             self.active_experts = int((counts > 0).sum().item())  # routing is fixed: same logits every step
+        acc = npu.npu_grouped_matmul([q], [self.w_gu], group_list=counts, split_item=3, group_type=0,
+                                     group_list_type=1, output_dtype=torch.int32)[0]
+        q2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=self.s_gu, activation_scale=s, group_index=counts,
+                                              activate_left=True, quant_mode=1)
+        out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
+                                     split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.bfloat16)[0]
+        return npu.npu_moe_finalize_routing(out, None, None, None, y, ri, idx, drop_pad_mode=2)
+
+    def step_gather(self, record=False):
+        """The layer as the compiled graph runs it after its pattern passes: the routing quantises the
+        token rows and returns each expanded row's token row instead of copying the rows
+        (tai::moe_init_routing_v2_rows), and the gate_up GEMM gathers its rows itself
+        (tai::grouped_matmul_gather); bit-identical to the prescribed composition. record=True
+        brackets the gate_up GEMM with HIP events."""
+        torch = self.torch
+        npu, tai = torch.ops.npu, torch.ops.tai
+        y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
+                                             group_select_mode=1, renorm=0, norm_type=1,
+                                             routed_scaling_factor=1.0, eps=1e-20)
+        q, a_rows, ri, counts, s = tai.moe_init_routing_v2_rows(self.x, idx, active_num=self.T * self.K,
+                                                                expert_num=self.E, expert_tokens_num_type=1,
+                                                                row_idx_type=0)
+        if self.active_experts is None:
+            self.active_experts = int((counts > 0).sum().item())
         if record:
             e0, e1 = _events(torch)
             e0.record()
-        acc = npu.npu_grouped_matmul([q], [self.w_gu], group_list=counts, split_item=3, group_type=0,
-                                     group_list_type=1, output_dtype=torch.int32)[0]
+        acc = tai.grouped_matmul_gather(q, a_rows, self.w_gu, counts, group_list_type=1, output_dtype=torch.int32)
         if record:
             e1.record()
             self.gmm1_events.append((e0, e1))
@@ -149,14 +173,16 @@ class MoeLayer:
 
     def gmm1_bytes(self):
         T, H, K, I = self.T, self.H, self.K, self.I
-        # weights of the experts that received rows + int8 rows + int32 out (an expert with no rows is never read)
-        return self.active_experts * H * 2 * I + T * K * H + T * K * 2 * I * 4
+        # weights of the experts that received rows (an expert with no rows is never read) + the int8 token
+        # rows it gathers (each token row once: T * H, not T * K * H) + its row map + int32 out
+        return self.active_experts * H * 2 * I + T * H + T * K * 4 + T * K * 2 * I * 4
 
 
 def compile_layer(torch, layer):
     """The product path: the prescribed composition through torch.compile(backend=get_npu_backend())
     in reduce-overhead mode (pattern passes, converters, hipGraph capture of the lowered graph; the
-    routing + dynamic-quant pattern is folded into the routing op, bit for bit)."""
+    routing + dynamic-quant pattern is folded into the routing op, and the routing into the gate_up
+    GEMM, which gathers its rows; both bit for bit)."""
     import torchair_amd
     cfg = torchair_amd.CompilerConfig()
     cfg.mode = "reduce-overhead"
@@ -171,8 +197,9 @@ def bench_moe(torch, dev, steps, warmup):
     """Headline: `steps` layer steps through the compiled product path (the first call, which traces,
     compiles and captures the graph, is set-up; then `warmup` untimed steps). The same number of
     eager steps of the prescribed composition follow, outside the timed region: HIP events on the
-    stream bracket their gate_up GEMM (the roofline kernel; the compiled graph runs the same kernel
-    on the same inputs), and their output is compared with the compiled one."""
+    stream bracket their gate_up GEMM (the roofline kernel) in the form the compiled graph runs it
+    (rows gathered from the quantised token rows, step_gather), and the outputs are compared with the
+    compiled one."""
     layer = MoeLayer(torch, dev)
     compiled = compile_layer(torch, layer)
     got = compiled(layer.x, layer.logits)
@@ -190,17 +217,23 @@ def bench_moe(torch, dev, steps, warmup):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     for _ in range(steps):
-        layer.step(record=True)
+        layer.step()
     torch.cuda.synchronize()
     dt_eager = (time.perf_counter() - t1) / steps
     matches = bool(torch.equal(got, layer.step()))
+    layer.step_gather()
+    for _ in range(steps):
+        layer.step_gather(record=True)
+    torch.cuda.synchronize()
+    matches = matches and bool(torch.equal(got, layer.step_gather()))
     gmm_ms = sum(a.elapsed_time(b) for a, b in layer.gmm1_events) / len(layer.gmm1_events)
     achieved = layer.gmm1_bytes() / (gmm_ms * 1e-3) / 1e9
-    roof = {"kernel": "tai_grouped_matmul (gate_up, int32 out)", "bound": "hbm", "achieved": round(achieved, 1),
+    roof = {"kernel": "tai_grouped_matmul_gather (gate_up, int32 out, rows gathered)", "bound": "hbm",
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(), "avg_ms": round(gmm_ms, 4),
             "algorithmic_bytes": layer.gmm1_bytes(), "active_experts": layer.active_experts,
-            "timed_on": "the eager steps after the timed region (same kernel and inputs as the compiled graph)"}
+            "timed_on": "eager steps after the timed region (the kernel and inputs of the compiled graph)"}
     from torchair_amd import graph as tai_graph, patterns as tai_patterns
     eager = {"eager_prescribed_ms": round(dt_eager * 1e3, 4),
              "eager_prescribed_tokens_per_s": round(MoeLayer.T / dt_eager, 1),

@@ -184,6 +184,17 @@ int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t m, int64_t
                        int group_list_type, const float* scale, const float* per_token_scale,
                        const void* bias, int bias_dtype, int out_dtype, void* out,
                        void* workspace, size_t ws_bytes, void* stream);
+/* The same product with its rows gathered, no counterpart in the reference's interface (it serves
+ * the compiled graph's fusion of npu_moe_init_routing_v2 into the GEMM that consumes its expanded
+ * rows, so those rows are never materialised): product row r reads row a_rows[r] of x [x_rows, k]
+ * (indices are clamped to [0, x_rows)); a_rows: [m] int32 (tai_moe_init_routing_v2_rows writes it).
+ * Workspace as tai_grouped_matmul_workspace_size(m, n, num_groups). */
+int tai_grouped_matmul_gather(const int8_t* x, int64_t x_rows, const int32_t* a_rows,
+                              const int8_t* weight, int64_t m, int64_t k, int64_t n, int64_t num_groups,
+                              int w_layout, const int64_t* group_list, int group_list_type,
+                              const float* scale, const float* per_token_scale, const void* bias,
+                              int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes,
+                              void* stream);
 
 /* No counterpart in the reference. tai_grouped_matmul without a workspace argument and without
  * any allocation, for callers that cannot allocate device memory (code under hipGraph capture,
@@ -284,6 +295,16 @@ int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t, int64_t h,
                             int expert_tokens_num_type, int row_idx_type, void* expanded_x,
                             int32_t* expanded_row_idx, int64_t* expert_tokens,
                             float* expanded_scale, void* workspace, size_t ws_bytes, void* stream);
+/* The same routing without expanded_x, no counterpart in the reference's interface (the compiled
+ * graph's fusion of the routing into the grouped GEMM that consumes its rows): a_rows [active_rows]
+ * int32 = src(i) / k, the token row that expanded row i copies (0 past the routed total), for
+ * tai_grouped_matmul_gather; expanded_row_idx, expert_tokens and expanded_scale as above. Workspace
+ * as tai_moe_init_routing_workspace_size. */
+int tai_moe_init_routing_v2_rows(int64_t t, const int32_t* expert_idx, int k, const float* scale,
+                                 int64_t active_rows, int expert_start, int expert_end,
+                                 int expert_tokens_num_type, int row_idx_type, int32_t* a_rows,
+                                 int32_t* expanded_row_idx, int64_t* expert_tokens,
+                                 float* expanded_scale, void* workspace, size_t ws_bytes, void* stream);
 
 /* npu_moe_init_routing_v2 with drop_pad_mode 1 (experiment_ops.h:2160-2189 drop_pad_mode /
  * expert_capacity; converter .../custom/npu_moe_init_routing_v2.py:41-91): expert e of

@@ -112,6 +112,36 @@ def register() -> None:
         es_t = _t(es) if es is not None else torch.empty(0, dtype=torch.float32)
         return _t(ex, x.dtype), _t(ri), _t(tok), es_t
 
+    def init_v2_rows(x, expert_idx, *, active_num=-1, expert_num=-1, expert_tokens_num_type=0,
+                     active_expert_range=(), row_idx_type=0):
+        # tai::moe_init_routing_v2_rows: the routing of the quantised token rows, with the token row
+        # of every expanded row in place of the rows themselves
+        t, k = expert_idx.shape
+        n = t * k
+        rows = n if (active_num is None or active_num <= 0 or active_num >= n) else active_num
+        lo, hi = (active_expert_range[0], active_expert_range[1]) if active_expert_range else (0, expert_num)
+        q, s = G.dynamic_quant(_np(x))
+        _, ri, tok, es = G.moe_init_routing_v2(q, expert_idx.numpy(), s, rows, lo, hi, expert_tokens_num_type,
+                                               row_idx_type)
+        a_rows = np.zeros(rows, np.int32)
+        ri = np.asarray(ri)
+        if row_idx_type == 0:
+            for p_, d in enumerate(ri):
+                if 0 <= d < rows:
+                    a_rows[d] = p_ // k
+        else:
+            for d in range(min(rows, len(ri))):
+                if ri[d] >= 0:
+                    a_rows[d] = ri[d] // k
+        return _t(q), _t(a_rows), _t(ri), _t(tok), _t(es)
+
+    def gmm_gather(x, a_rows, weight, group_list, *, scale=None, per_token_scale=None, bias=None,
+                   group_list_type=0, output_dtype=None):
+        xs = [x[a_rows.long()]]
+        return gmm(xs, [weight], bias=None if bias is None else [bias], scale=None if scale is None else [scale],
+                   per_token_scale=None if per_token_scale is None else [per_token_scale], group_list=group_list,
+                   split_item=3, group_type=0, group_list_type=group_list_type, output_dtype=output_dtype)[0]
+
     def init_legacy(x, row_idx, expert_idx, active_num):
         ex, ri, ei = G.moe_init_routing(_np(x), row_idx.numpy(), expert_idx.numpy(), active_num)
         return _t(ex, x.dtype), _t(ri), _t(ei)
@@ -222,6 +252,8 @@ def register() -> None:
         lib.impl("npu_quant_matmul", qmm, "CPU")
         lib.impl("npu_grouped_matmul", gmm, "CPU")
         lib.impl("npu_moe_init_routing_v2", init_v2, "CPU")
+        LIBS["tai"].impl("moe_init_routing_v2_rows", init_v2_rows, "CPU")
+        LIBS["tai"].impl("grouped_matmul_gather", gmm_gather, "CPU")
         lib.impl("npu_moe_init_routing", init_legacy, "CPU")
         lib.impl("npu_moe_finalize_routing", finalize, "CPU")
     for ns in ("npu", "npu_inference"):

@@ -296,3 +296,59 @@ def test_pattern_pass_fuses_init_routing_dynamic_quant_on_cpu():
         gm2 = torch.fx.symbolic_trace(f)
         assert fuse_init_routing_dynamic_quant(gm2) == 0
         gm2.graph.lint()
+
+
+def test_pattern_pass_fuses_routing_into_grouped_matmul_on_cpu():
+    """Dynamic-quant routing whose expanded rows feed only a grouped GEMM becomes the routing without
+    the row copy plus a GEMM that gathers its rows; the compiled result equals the eager composition
+    bit for bit (also with the routing's scales as the GEMM's per-token scales). Expanded rows with
+    another user are left alone."""
+    from oracle import cpu_ops
+    from torchair_amd.patterns import fuse_init_routing_dynamic_quant, fuse_routing_grouped_matmul, stats
+    cpu_ops.register()
+    g = torch.Generator().manual_seed(7)
+    t, h, e, k, n = 12, 64, 4, 2, 32
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)]).to(torch.int32)
+    w = torch.randint(-127, 128, (e, h, n), generator=g, dtype=torch.int8)
+    ws = torch.rand(e, n, generator=g) * 0.01 + 1e-3
+    npu = torch.ops.npu
+
+    def block(x, idx):
+        ex, ri, tok, _ = npu.npu_moe_init_routing_v2(x, idx, active_num=t * k, expert_num=e,
+                                                     expert_tokens_num_type=1, expert_tokens_num_flag=True)
+        q, s = npu.npu_dynamic_quant(ex)
+        acc = npu.npu_grouped_matmul([q], [w], group_list=tok, split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.int32)[0]
+        return acc, ri, tok
+
+    def scaled(x, idx):
+        q, ri, tok, s = npu.npu_moe_init_routing_v2(x, idx, active_num=t * k, expert_num=e, expert_tokens_num_type=1,
+                                                    expert_tokens_num_flag=True, quant_mode=1)
+        return npu.npu_grouped_matmul([q], [w], scale=[ws], per_token_scale=[s], group_list=tok, split_item=3,
+                                      group_type=0, group_list_type=1, output_dtype=torch.bfloat16)[0], s
+
+    for f, n_routes in ((block, 1), (scaled, 1)):
+        gm = torch.fx.symbolic_trace(f)
+        fuse_init_routing_dynamic_quant(gm)
+        assert fuse_routing_grouped_matmul(gm) == n_routes
+        targets = {nd.target for nd in gm.graph.nodes if nd.op == "call_function"}
+        assert torch.ops.tai.grouped_matmul_gather.default in targets
+        assert not {npu.npu_grouped_matmul, npu.npu_grouped_matmul.default} & targets
+        for a, b in zip(gm(x, idx), f(x, idx)):
+            assert torch.equal(a, b)
+    before = stats["routing_grouped_matmul"]
+    fn = torch.compile(block, backend=get_npu_backend(), fullgraph=True)
+    for a, b in zip(fn(x, idx), block(x, idx)):
+        assert torch.equal(a, b)
+    assert stats["routing_grouped_matmul"] == before + 1
+
+    def rows_also_used(x, idx):
+        q, ri, tok, s = npu.npu_moe_init_routing_v2(x, idx, active_num=t * k, expert_num=e, expert_tokens_num_type=1,
+                                                    expert_tokens_num_flag=True, quant_mode=1)
+        acc = npu.npu_grouped_matmul([q], [w], group_list=tok, split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.int32)[0]
+        return acc, q.sum()
+
+    gm2 = torch.fx.symbolic_trace(rows_also_used)
+    assert fuse_routing_grouped_matmul(gm2) == 0

@@ -65,6 +65,9 @@ _SIGS = {
     "tai_grouped_matmul": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P,
                 _P, c_size_t, _P]),
+    "tai_grouped_matmul_gather": (
+        c_int, [_P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int,
+                _P, _P, c_size_t, _P]),
     "tai_grouped_matmul_noalloc_max_scratch": (c_size_t, []),
     "tai_grouped_matmul_noalloc": (
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P, _P]),
@@ -89,6 +92,8 @@ _SIGS = {
     "tai_moe_init_routing_v2": (
         c_int, [_P, c_int, c_int64, c_int64, _P, c_int, _P, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P,
                 _P, _P, c_size_t, _P]),
+    "tai_moe_init_routing_v2_rows": (
+        c_int, [c_int64, _P, c_int, _P, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P, c_size_t, _P]),
     "tai_moe_init_routing": (
         c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P, _P, _P, c_size_t, _P]),
     "tai_moe_finalize_routing": (

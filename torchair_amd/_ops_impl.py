@@ -863,3 +863,4 @@ _define("air", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
 from . import _norm_cache  # noqa: E402,F401  (RMS-norm family and KV-cache writers)
 
 from . import _gmm_fused  # noqa: E402,F401  (fused MoE grouped GEMMs)
+from . import _moe_fused  # noqa: E402,F401  (routing -> grouped GEMM fusion of the compiled graph)

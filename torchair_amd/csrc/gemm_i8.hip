@@ -62,7 +62,18 @@ struct GemmArgs {
   // holds gate columns 64t .. 64t + 63, block 2t + 1 the matching up columns), so a tile's columns
   // are contiguous in the weight rows
   int swi_packed;
+  // grouped gather: row r of the product reads row a_rows[r] of a (clamped to [0, a_src_rows)); NULL
+  // reads row r
+  const int32_t* a_rows;
+  int64_t a_src_rows;
 };
+
+// Row of a that product row r reads.
+__device__ __forceinline__ int64_t a_row(const GemmArgs& g, int64_t r) {
+  if (g.a_rows == nullptr) return r;
+  const int64_t s = g.a_rows[r];
+  return s < 0 ? 0 : (s < g.a_src_rows ? s : g.a_src_rows - 1);
+}
 
 // Output code of the fused SwiGLU epilogue (npu_grouped_matmul_swiglu_quant_v2).
 constexpr int kOutSwiglu = 100;
@@ -194,7 +205,7 @@ struct Tile {
     for (int i = 0; i < kAChunks; ++i) {
       const int c = tid + i * 256, r = c >> 2, kc = c & 3;
       const int64_t kk = k0 + kc * 16;
-      ra[i] = (r < rows && kk < g.k) ? *reinterpret_cast<const uint4*>(g.a + (row0 + r) * g.k + kk)
+      ra[i] = (r < rows && kk < g.k) ? *reinterpret_cast<const uint4*>(g.a + a_row(g, row0 + r) * g.k + kk)
                                      : make_uint4(0, 0, 0, 0);
     }
     if constexpr (LAYOUT == TAI_LAYOUT_NK) {
@@ -372,10 +383,11 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmArgs g, int la
     return;
   }
   const int8_t* bgrp = g.b + static_cast<int64_t>(e) * g.b_group_stride;
+  const int8_t* arow = g.a + a_row(g, row) * g.k;
   int32_t acc = 0;
   for (int64_t kk = 0; kk < g.k; ++kk) {
     const int32_t bv = layout == TAI_LAYOUT_NK ? bgrp[col * g.k + kk] : bgrp[kk * g.n + col];
-    acc += static_cast<int32_t>(g.a[row * g.k + kk]) * bv;
+    acc += static_cast<int32_t>(arow[kk]) * bv;
   }
   if (g.bias && g.bias_dt == TAI_DT_INT32) acc += static_cast<const int32_t*>(g.bias)[e * g.bias_group_stride + col];
   const float* bias_f = (g.bias && g.bias_dt == TAI_DT_FP32)
@@ -552,7 +564,7 @@ __device__ __forceinline__ void lgkm_wait() {
 // stage's loads are split so that the workgroup's waves do not all queue in the address unit at
 // the same moment after a barrier).
 template <int LAYOUT, class C, bool SWI = false, int PART = 0, int BPOL = 0>
-__device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, int row0, int rows,
+__device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t* bgrp, const int64_t* aoff,
                                                 int64_t n0, int64_t k0, int8_t* stage, int w, int lane) {
   constexpr int BK = C::kBK, CPR = C::kCpr, RPI = 1024 / BK;  // rows per 1 KB instruction
   constexpr int kFirst = (C::kLoads + 1) / 2;
@@ -563,8 +575,7 @@ __device__ __forceinline__ void big_issue_stage(const GemmArgs& g, const int8_t*
     const int q = C::kALoads * w + i;
     const int row = RPI * q + lane / CPR;
     const int c = (lane % CPR) ^ ((row >> C::kRowShift) & (CPR - 1));
-    const int rr = row < rows ? row : (rows > 0 ? rows - 1 : 0);
-    const int8_t* src = g.a + static_cast<int64_t>(row0 + rr) * g.k + k0 + 16 * c;
+    const int8_t* src = g.a + aoff[i] + k0 + 16 * c;
     __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)(stage + q * 1024), 16, 0, 0);
   }
   int8_t* bst = stage + C::kBM * BK;
@@ -719,6 +730,16 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = w / WN, wn = w % WN;
+  // source row offsets of this lane's A loads (rows past the tile re-read its last row; their sums
+  // are never stored), fixed for the whole tile; a gathered product reads them first, ahead of the
+  // epilogue operands, so no wait for them drains anything issued later
+  int64_t aoff[C::kALoads];
+#pragma unroll
+  for (int i = 0; i < C::kALoads; ++i) {
+    const int row = (1024 / C::kBK) * (C::kALoads * w + i) + lane / C::kCpr;
+    const int rr = row < rows ? row : (rows > 0 ? rows - 1 : 0);
+    aoff[i] = a_row(g, row0 + rr) * g.k;
+  }
   const int act_m = max(0, min(2, (rows - wm * 64 + 31) / 32));
   const int64_t ncols = g.n - n0 - wn * 128;
   const int act_n = ncols <= 0 ? 0 : (ncols >= 128 ? 4 : static_cast<int>((ncols + 31) / 32));
@@ -819,7 +840,7 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
 #pragma unroll
     for (int s = 0; s < C::kStages - 1; ++s)
       if (s < nk)
-        big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, row0, rows, n0, kb0 + s * kBigBK, smem + s * C::kStage,
+        big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, aoff, n0, kb0 + s * kBigBK, smem + s * C::kStage,
                                                              w, lane);
     constexpr int NF = NI == 0 ? 0 : NI + (LAYOUT == TAI_LAYOUT_KN ? 8 : 4);  // LDS reads per step
     v4i fa[2][NI > 0 ? NI : 1], fb[2][4];
@@ -851,7 +872,7 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
     wait_stage(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (C::kStages - 1 < nk)
-      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, row0, rows, n0, kb0 + (C::kStages - 1) * kBigBK,
+      big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 0, BP>(g, bgrp, aoff, n0, kb0 + (C::kStages - 1) * kBigBK,
                                  smem + (C::kStages - 1) * C::kStage, w, lane);
     fetch(0, smem, 0);
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -871,7 +892,7 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
             // stage's first MFMA step (every load is still issued before the next stage wait)
             if (kt + C::kStages < nk)
               big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, kSplit ? 1 : 0, BP>(
-                  g, bgrp, row0, rows, n0, kb0 + (kt + C::kStages) * kBigBK,
+                  g, bgrp, aoff, n0, kb0 + (kt + C::kStages) * kBigBK,
                   smem + (static_cast<int>(kt) % C::kStages) * C::kStage, w, lane);
             fetch(cur ^ 1, smem + ((static_cast<int>(kt) + 1) % C::kStages) * C::kStage, 0);
           }
@@ -880,7 +901,7 @@ __device__ __forceinline__ void big_tile(const GemmArgs& g, int8_t* smem, int64_
         mfma(cur);
         if constexpr (kSplit) {
           if (kk == 0 && kt >= 1 && kt - 1 + C::kStages < nk)
-            big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 2, BP>(g, bgrp, row0, rows, n0, kb0 + (kt - 1 + C::kStages) * kBigBK,
+            big_issue_stage<LAYOUT, C, OUT == kOutSwiglu, 2, BP>(g, bgrp, aoff, n0, kb0 + (kt - 1 + C::kStages) * kBigBK,
                                                            smem + ((static_cast<int>(kt) - 1) % C::kStages) * C::kStage,
                                                            w, lane);
         }
@@ -1837,7 +1858,8 @@ static int quant_matmul_impl(const int8_t* x1, const int8_t* x2, int64_t m, int6
 static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
                                int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
                                const float* scale, const float* per_token_scale, const void* bias, int bias_dtype,
-                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream);
+                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream,
+                               const int32_t* a_rows = nullptr, int64_t a_src_rows = 0);
 
 extern "C" size_t tai_grouped_matmul_workspace_size(int64_t m, int64_t n, int64_t num_groups) {
   (void)n;
@@ -1851,6 +1873,19 @@ extern "C" int tai_grouped_matmul(const int8_t* x, const int8_t* weight, int64_t
                                   int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream) {
   return grouped_matmul_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, scale,
                              per_token_scale, bias, bias_dtype, out_dtype, out, workspace, ws_bytes, stream);
+}
+
+extern "C" int tai_grouped_matmul_gather(const int8_t* x, int64_t x_rows, const int32_t* a_rows,
+                                         const int8_t* weight, int64_t m, int64_t k, int64_t n, int64_t num_groups,
+                                         int w_layout, const int64_t* group_list, int group_list_type,
+                                         const float* scale, const float* per_token_scale, const void* bias,
+                                         int bias_dtype, int out_dtype, void* out, void* workspace, size_t ws_bytes,
+                                         void* stream) {
+  TAI_CHECK_ARG(x_rows >= 0, "tai_grouped_matmul_gather: x_rows must be >= 0");
+  if (m > 0 && n > 0) TAI_CHECK_ARG(a_rows && x_rows > 0, "tai_grouped_matmul_gather: a_rows and x rows are required");
+  return grouped_matmul_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, scale,
+                             per_token_scale, bias, bias_dtype, out_dtype, out, workspace, ws_bytes, stream, a_rows,
+                             x_rows);
 }
 
 // ----------------------------------------------------------------------------- no-allocation variant
@@ -1915,7 +1950,8 @@ extern "C" int tai_grouped_matmul_noalloc(const int8_t* x, const int8_t* weight,
 static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
                                int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
                                const float* scale, const float* per_token_scale, const void* bias, int bias_dtype,
-                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream) {
+                               int out_dtype, void* out, void* workspace, size_t ws_bytes, void* stream,
+                               const int32_t* a_rows, int64_t a_src_rows) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 0 && num_groups >= 1, "tai_grouped_matmul: bad sizes");
   TAI_CHECK_ARG(num_groups <= 2048, "tai_grouped_matmul: at most 2048 groups");
   TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK, "tai_grouped_matmul: w_layout");
@@ -1948,6 +1984,8 @@ static int grouped_matmul_impl(const int8_t* x, const int8_t* weight, int64_t m,
                                                   sizeof(int4) * grouped_map_slots(m, num_groups, kMinBM));
   GemmArgs g{x, weight, m, k, n, k * n, scale, n, n, per_token_scale, bias, bias_dtype, n, out_dtype, out,
              map, slots, cdiv(n, bn), live};
+  g.a_rows = a_rows;
+  g.a_src_rows = a_src_rows;
   const bool fast = fast_path_ok(g, w_layout);
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type, m,
                                                                               bm, map, slots, live,

@@ -341,6 +341,23 @@ __global__ __launch_bounds__(256) void route_gather_kernel(const void* __restric
   if (escale && lane == 0) escale[i] = scale[src_row];
 }
 
+// K4 without the copy: a_rows[i] = the token row of expanded row i (0 past the routed total), for a
+// GEMM that gathers its rows itself; the scale is gathered as by route_gather_kernel.
+__global__ __launch_bounds__(256) void route_rows_kernel(int k, const int32_t* __restrict__ dst2src,
+                                                         const int32_t* __restrict__ total, int64_t active_rows,
+                                                         int64_t n, int32_t* __restrict__ a_rows,
+                                                         const float* __restrict__ scale, float* __restrict__ escale,
+                                                         int tail_mode, int32_t* __restrict__ row_idx) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t valid = *total;
+  if (tail_mode == 1 && i >= valid) row_idx[i] = -1;
+  if (i >= active_rows) return;
+  const int32_t src = i < valid ? dst2src[i] / k : 0;
+  a_rows[i] = src;
+  if (escale) escale[i] = i < valid ? scale[src] : 0.0f;
+}
+
 // ---------------------------------------------------------------------------- drop-pad routing
 // npu_moe_init_routing_v2 with drop_pad_mode 1: expert e (of the range) owns rows [e * cap, (e + 1) * cap)
 // of expanded_x; a slot's rank among its expert's slots (the dropless order: stable by slot) places it
@@ -532,7 +549,7 @@ static int run_routing(const void* x, int elem_bytes, int64_t t, int64_t h, cons
                        int e0, int bins, int64_t active_rows, int mode, int32_t* row_idx,
                        const int32_t* legacy_row, int32_t* eout, int64_t* tokens, int tokens_cumsum,
                        const float* scale, float* escale, void* ex, void* ws, size_t ws_bytes,
-                       hipStream_t st, const char* name) {
+                       hipStream_t st, const char* name, int32_t* a_rows = nullptr) {
   const int64_t n = t * k;
   TAI_CHECK_ARG(n < (1ll << 31), "%s: t*k must be < 2^31", name);
   TAI_CHECK_ARG(bins >= 1 && bins <= 1024, "%s: expert range must hold 1..1024 experts", name);
@@ -550,6 +567,11 @@ static int run_routing(const void* x, int elem_bytes, int64_t t, int64_t h, cons
                                                                           tokens, tokens_cumsum, w.total, w.dst2src,
                                                                           mode, row_idx, legacy_row, eout);
   const int tail_mode = (mode == 1) ? 1 : 0;
+  if (a_rows) {
+    route_rows_kernel<<<dim3(static_cast<unsigned>(cdiv(n, 256))), 256, 0, st>>>(
+        k, w.dst2src, w.total, active_rows, n, a_rows, scale, escale, tail_mode, row_idx);
+    return launch_status(name);
+  }
   route_gather_kernel<<<dim3(static_cast<unsigned>(cdiv(n, 4))), 256, 0, st>>>(
       x, static_cast<int64_t>(elem_bytes) * h, t, k, w.dst2src, w.total, active_rows, n, ex, scale, escale,
       tail_mode, row_idx, legacy_row);
@@ -576,6 +598,25 @@ extern "C" int tai_moe_init_routing_v2(const void* x, int elem_bytes, int64_t t,
                      row_idx_type, expanded_row_idx, nullptr, nullptr, expert_tokens, expert_tokens_num_type == 0,
                      scale, expanded_scale, expanded_x, workspace, ws_bytes, static_cast<hipStream_t>(stream),
                      "tai_moe_init_routing_v2");
+}
+
+extern "C" int tai_moe_init_routing_v2_rows(int64_t t, const int32_t* expert_idx, int k, const float* scale,
+                                            int64_t active_rows, int expert_start, int expert_end,
+                                            int expert_tokens_num_type, int row_idx_type, int32_t* a_rows,
+                                            int32_t* expanded_row_idx, int64_t* expert_tokens,
+                                            float* expanded_scale, void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(t >= 0 && k > 0, "tai_moe_init_routing_v2_rows: bad sizes");
+  TAI_CHECK_ARG(expert_start >= 0 && expert_end > expert_start, "tai_moe_init_routing_v2_rows: expert range");
+  TAI_CHECK_ARG(row_idx_type == 0 || row_idx_type == 1, "tai_moe_init_routing_v2_rows: row_idx_type must be 0 or 1");
+  TAI_CHECK_ARG(expert_tokens_num_type == 0 || expert_tokens_num_type == 1,
+                "tai_moe_init_routing_v2_rows: expert_tokens_num_type must be 0 (cumsum) or 1 (count)");
+  TAI_CHECK_ARG(active_rows >= 0 && active_rows <= t * k, "tai_moe_init_routing_v2_rows: active rows");
+  TAI_CHECK_ARG(scale == nullptr || expanded_scale != nullptr, "tai_moe_init_routing_v2_rows: expanded_scale missing");
+  TAI_CHECK_ARG(t == 0 || a_rows != nullptr, "tai_moe_init_routing_v2_rows: a_rows is required");
+  return run_routing(nullptr, 1, t, 0, expert_idx, k, expert_start, expert_end - expert_start, active_rows,
+                     row_idx_type, expanded_row_idx, nullptr, nullptr, expert_tokens, expert_tokens_num_type == 0,
+                     scale, expanded_scale, nullptr, workspace, ws_bytes, static_cast<hipStream_t>(stream),
+                     "tai_moe_init_routing_v2_rows", a_rows);
 }
 
 extern "C" size_t tai_moe_init_routing_v2_droppad_workspace_size(int64_t t, int k, int64_t num_experts,

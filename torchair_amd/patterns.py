@@ -14,6 +14,13 @@ scales, no group index) becomes the routing op with its dynamic quant mode (expe
 whose expanded rows and scales are the quantised rows and their scales. The routing kernel quantises
 each token row once and gathers the int8 rows, which equals quantising every gathered copy, so the
 rewrite changes no value. This pattern has no counterpart among the reference's passes.
+
+npu_moe_init_routing_v2(quant_mode=1) + npu_grouped_matmul -> tai::moe_init_routing_v2_rows +
+tai::grouped_matmul_gather: dynamic-quant routing (dropless, no smooth scale) whose expanded rows feed
+only the x of a grouped GEMM (groups along M, one output) becomes the routing without the copy of the
+rows, and the GEMM reads each product row from the quantised token rows through the routing's row map
+(the same int8 bytes, so the rewrite changes no value; at DeepSeek-V3 decode shapes it saves writing
+and re-reading T * k rows). This pattern has no counterpart among the reference's passes.
 """
 from __future__ import annotations
 
@@ -26,7 +33,7 @@ import torch.fx
 logger = logging.getLogger("torchair_amd")
 
 # rewrites applied so far in this process, per pattern (diagnostics and tests)
-stats = {"add_rms_norm_dynamic_quant": 0, "init_routing_dynamic_quant": 0}
+stats = {"add_rms_norm_dynamic_quant": 0, "init_routing_dynamic_quant": 0, "routing_grouped_matmul": 0}
 
 
 def _getitems(node: torch.fx.Node):
@@ -169,7 +176,102 @@ def fuse_init_routing_dynamic_quant(gm: torch.fx.GraphModule) -> int:
     return fused
 
 
+def _gather_gmm_kwargs(gmm: torch.fx.Node, rows: torch.fx.Node):
+    """kwargs of tai::grouped_matmul_gather for npu_grouped_matmul([rows], [w], ...) with groups along M,
+    one output over all rows and nothing the gather op does not take; None otherwise."""
+    if len(gmm.args) != 2 or not all(isinstance(a, (list, tuple)) and len(a) == 1 for a in gmm.args):
+        return None
+    if gmm.args[0][0] is not rows or gmm.args[1][0] is rows:
+        return None
+    kw = dict(gmm.kwargs)
+    if not isinstance(kw.get("group_list"), torch.fx.Node) or kw.get("group_list_type", 0) not in (0, 1):
+        return None
+    if kw.get("split_item") not in (2, 3) or kw.get("group_type") not in (None, 0) or kw.get("act_type") not in (None, 0):
+        return None
+    out = {"group_list_type": kw.get("group_list_type", 0), "output_dtype": kw.get("output_dtype")}
+    for name in ("scale", "per_token_scale", "bias"):
+        v = kw.get(name)
+        if v is None or (isinstance(v, (list, tuple)) and not v):
+            continue
+        if not (isinstance(v, (list, tuple)) and len(v) == 1 and isinstance(v[0], torch.fx.Node)):
+            return None
+        out[name] = v[0]
+    free = {"group_list", "group_list_type", "split_item", "group_type", "act_type", "output_dtype", "tuning_config",
+            "scale", "per_token_scale", "bias"}
+    if any(not (v is None or (isinstance(v, (list, tuple)) and not v)) for k, v in kw.items() if k not in free):
+        return None
+    return out
+
+
+def fuse_routing_grouped_matmul(gm: torch.fx.GraphModule) -> int:
+    npu, tai = torch.ops.npu, getattr(torch.ops, "tai", None)
+    if tai is None or not hasattr(tai, "grouped_matmul_gather") or not hasattr(npu, "npu_moe_init_routing_v2"):
+        return 0
+    fused = 0
+    for route in list(gm.graph.nodes):
+        if not _calls(route, npu.npu_moe_init_routing_v2) or len(route.args) != 2:
+            continue
+        kw = dict(route.kwargs)
+        if kw.get("quant_mode") != 1 or kw.get("scale") is not None or kw.get("offset") is not None:
+            continue
+        if kw.get("drop_pad_mode", 0) not in (0, None):
+            continue
+        allowed = {"quant_mode", "scale", "offset", "drop_pad_mode", "active_num", "expert_num", "expert_capacity",
+                   "expert_tokens_num_type", "expert_tokens_num_flag", "active_expert_range", "row_idx_type"}
+        if set(kw) - allowed:
+            continue
+        outs = _getitems(route)
+        if outs is None:
+            continue
+        live0 = [u for u in outs.get(0, []) if u.users]
+        if len(live0) != 1 or len(live0[0].users) != 1:
+            continue
+        rows = live0[0]
+        gmm = next(iter(rows.users))
+        if not _calls(gmm, npu.npu_grouped_matmul):
+            continue
+        gkw = _gather_gmm_kwargs(gmm, rows)
+        gouts = _getitems(gmm) if gkw is not None else None
+        if gouts is None or set(gouts) - {0}:
+            continue
+        rkw = {k: kw[k] for k in ("active_num", "expert_num", "expert_tokens_num_type", "row_idx_type") if k in kw}
+        if kw.get("active_expert_range"):
+            rkw["active_expert_range"] = list(kw["active_expert_range"])
+        with gm.graph.inserting_after(route):
+            node = gm.graph.call_function(tai.moe_init_routing_v2_rows.default, route.args, rkw)
+        with gm.graph.inserting_after(node):
+            q = gm.graph.call_function(operator.getitem, (node, 0))
+        with gm.graph.inserting_after(q):
+            a_rows = gm.graph.call_function(operator.getitem, (node, 1))
+        # the routing's other outputs move over: row index, token counts, scales
+        for src_idx, dst_idx in ((1, 2), (2, 3), (3, 4)):
+            for u in outs.get(src_idx, []):
+                with gm.graph.inserting_after(a_rows):
+                    new = gm.graph.call_function(operator.getitem, (node, dst_idx))
+                u.replace_all_uses_with(new)
+                gm.graph.erase_node(u)
+        gkw = _gather_gmm_kwargs(gmm, rows)  # again: operands that were routing outputs moved over
+        with gm.graph.inserting_before(gmm):
+            gnode = gm.graph.call_function(tai.grouped_matmul_gather.default,
+                                           (q, a_rows, gmm.args[1][0], gmm.kwargs["group_list"]), gkw)
+        for u in gouts.get(0, []):
+            u.replace_all_uses_with(gnode)
+            gm.graph.erase_node(u)
+        gm.graph.erase_node(gmm)
+        for u in outs.get(0, []):
+            gm.graph.erase_node(u)
+        gm.graph.erase_node(route)
+        fused += 1
+    if fused:
+        gm.graph.lint()
+        gm.recompile()
+        stats["routing_grouped_matmul"] += fused
+        logger.debug("fused %d init_routing_v2 + grouped_matmul pair(s)", fused)
+    return fused
+
+
 def apply_pattern_passes(gm: torch.fx.GraphModule) -> torch.fx.GraphModule:
     fuse_add_rms_norm_dynamic_quant(gm)
     fuse_init_routing_dynamic_quant(gm)
+    fuse_routing_grouped_matmul(gm)
     return gm
