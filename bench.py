@@ -7,8 +7,8 @@ as a module compiled with torch.compile(backend=get_npu_backend()) in reduce-ove
 product path: pattern passes, converters, hipGraph replay), with every input resident in HBM before
 the timed region; the eager composition is timed beside it. Side measurements in the same JSON
 line: paged GQA decode attention (config 2) HBM GB/s, the W8A8 GEMM at M=N=K=8192 and the
-config-1 MLP. `roofline` is for the dominant kernel (the gate_up grouped GEMM), timed with HIP
-events on its stream inside the timed region; `cpu_baseline` times the CPU oracle on a bounded
+config-1 MLP. `roofline` is for the dominant op (the gate_up grouped GEMM with its fused SwiGLU
+quant), timed with HIP events on its stream inside the timed region; `cpu_baseline` times the CPU oracle on a bounded
 sample of the same layer.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
@@ -93,9 +93,9 @@ class MoeLayer:
     def step_gather(self, record=False):
         """The layer as the compiled graph runs it after its pattern passes: the routing quantises the
         token rows and returns each expanded row's token row instead of copying the rows
-        (tai::moe_init_routing_v2_rows), and the gate_up GEMM gathers its rows itself
-        (tai::grouped_matmul_gather); bit-identical to the prescribed composition. record=True
-        brackets the gate_up GEMM with HIP events."""
+        (tai::moe_init_routing_v2_rows), and the gate_up GEMM gathers its rows itself, with the
+        dequant + SwiGLU + quant as its epilogue (tai::grouped_matmul_swiglu_quant_gather);
+        bit-identical to the prescribed composition. record=True brackets the gate_up op with HIP events."""
         torch = self.torch
         npu, tai = torch.ops.npu, torch.ops.tai
         y, idx, _ = npu.npu_moe_gating_top_k(self.logits, self.K, bias=self.bias, k_group=4, group_count=8,
@@ -109,12 +109,10 @@ class MoeLayer:
         if record:
             e0, e1 = _events(torch)
             e0.record()
-        acc = tai.grouped_matmul_gather(q, a_rows, self.w_gu, counts, group_list_type=1, output_dtype=torch.int32)
+        q2, s2 = tai.grouped_matmul_swiglu_quant_gather(q, a_rows, self.w_gu, self.s_gu, s, counts, group_list_type=1)
         if record:
             e1.record()
             self.gmm1_events.append((e0, e1))
-        q2, s2 = npu.npu_dequant_swiglu_quant(acc, weight_scale=self.s_gu, activation_scale=s, group_index=counts,
-                                              activate_left=True, quant_mode=1)
         out = npu.npu_grouped_matmul([q2], [self.w_d], scale=[self.s_d], per_token_scale=[s2], group_list=counts,
                                      split_item=3, group_type=0, group_list_type=1,
                                      output_dtype=torch.bfloat16)[0]
@@ -173,16 +171,18 @@ class MoeLayer:
 
     def gmm1_bytes(self):
         T, H, K, I = self.T, self.H, self.K, self.I
-        # weights of the experts that received rows (an expert with no rows is never read) + the int8 token
-        # rows it gathers (each token row once: T * H, not T * K * H) + its row map + int32 out
-        return self.active_experts * H * 2 * I + T * H + T * K * 4 + T * K * 2 * I * 4
+        # the gate_up op's operands: weights of the experts that received rows (an expert with no rows is
+        # never read) + the int8 token rows it gathers (each token row once: T * H, not T * K * H) + its
+        # row map and per-row scales + int8 out and its scales (the fp32 SwiGLU rows its GEMM kernel hands
+        # to its quantisation kernel are not operands)
+        return self.active_experts * H * 2 * I + T * H + 2 * T * K * 4 + T * K * I + T * K * 4
 
 
 def compile_layer(torch, layer):
     """The product path: the prescribed composition through torch.compile(backend=get_npu_backend())
     in reduce-overhead mode (pattern passes, converters, hipGraph capture of the lowered graph; the
-    routing + dynamic-quant pattern is folded into the routing op, and the routing into the gate_up
-    GEMM, which gathers its rows; both bit for bit)."""
+    routing + dynamic-quant pattern is folded into the routing op, the routing into the gate_up GEMM,
+    which gathers its rows, and the dequant_swiglu_quant into that GEMM's epilogue; all bit for bit)."""
     import torchair_amd
     cfg = torchair_amd.CompilerConfig()
     cfg.mode = "reduce-overhead"
@@ -197,9 +197,9 @@ def bench_moe(torch, dev, steps, warmup):
     """Headline: `steps` layer steps through the compiled product path (the first call, which traces,
     compiles and captures the graph, is set-up; then `warmup` untimed steps). The same number of
     eager steps of the prescribed composition follow, outside the timed region: HIP events on the
-    stream bracket their gate_up GEMM (the roofline kernel) in the form the compiled graph runs it
-    (rows gathered from the quantised token rows, step_gather), and the outputs are compared with the
-    compiled one."""
+    stream bracket their gate_up op (the roofline op: its GEMM kernel and the row-quantisation kernel
+    of its epilogue) in the form the compiled graph runs it (step_gather), and the outputs are compared
+    with the compiled one."""
     layer = MoeLayer(torch, dev)
     compiled = compile_layer(torch, layer)
     got = compiled(layer.x, layer.logits)
@@ -228,7 +228,8 @@ def bench_moe(torch, dev, steps, warmup):
     matches = matches and bool(torch.equal(got, layer.step_gather()))
     gmm_ms = sum(a.elapsed_time(b) for a, b in layer.gmm1_events) / len(layer.gmm1_events)
     achieved = layer.gmm1_bytes() / (gmm_ms * 1e-3) / 1e9
-    roof = {"kernel": "tai_grouped_matmul_gather (gate_up, int32 out, rows gathered)", "bound": "hbm",
+    roof = {"kernel": "tai_grouped_matmul_swiglu_quant_gather (gate_up GEMM, rows gathered, SwiGLU epilogue; "
+                      "+ its row-quantisation kernel)", "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _measured_traffic(), "avg_ms": round(gmm_ms, 4),

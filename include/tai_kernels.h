@@ -221,6 +221,15 @@ int tai_grouped_matmul_noalloc(const int8_t* x, const int8_t* weight, int64_t m,
  * Needs k % 64 == 0 and (n / 2) % 256 (_KN) or % 128 (_NK) == 0; TAI_ERR_UNSUPPORTED otherwise.
  * ------------------------------------------------------------------------------------- */
 size_t tai_grouped_matmul_swiglu_quant_workspace_size(int64_t m, int64_t n, int64_t num_groups);
+/* The same op with its rows gathered, no counterpart in the reference's interface (the compiled graph's
+ * fusion of the routing into the gate_up GEMM): product row r reads row a_rows[r] of x [x_rows, k]
+ * (clamped to [0, x_rows)), as tai_grouped_matmul_gather. */
+int tai_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const int32_t* a_rows,
+                                           const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                                           int64_t num_groups, int w_layout, const int64_t* group_list,
+                                           int group_list_type, const float* weight_scale,
+                                           const float* x_scale, int8_t* y, float* y_scale,
+                                           void* workspace, size_t ws_bytes, void* stream);
 /* Weight prepacking for tai_grouped_matmul_swiglu_quant, no counterpart in the reference's interface
  * (the NPU casts weights to its own format at load time, npu_format_cast): writes the
  * TAI_LAYOUT_KN_SWIGLU copy of a [rows, n] int8 weight (rows = num_groups * k; n % 128 == 0), whose

@@ -142,6 +142,9 @@ def register() -> None:
                    per_token_scale=None if per_token_scale is None else [per_token_scale], group_list=group_list,
                    split_item=3, group_type=0, group_list_type=group_list_type, output_dtype=output_dtype)[0]
 
+    def gsq_gather(x, a_rows, weight, weight_scale, x_scale, group_list, *, group_list_type=0):
+        return gsq(x[a_rows.long()], [weight], [weight_scale], x_scale, group_list, group_list_type=group_list_type)
+
     def init_legacy(x, row_idx, expert_idx, active_num):
         ex, ri, ei = G.moe_init_routing(_np(x), row_idx.numpy(), expert_idx.numpy(), active_num)
         return _t(ex, x.dtype), _t(ri), _t(ei)
@@ -254,6 +257,7 @@ def register() -> None:
         lib.impl("npu_moe_init_routing_v2", init_v2, "CPU")
         LIBS["tai"].impl("moe_init_routing_v2_rows", init_v2_rows, "CPU")
         LIBS["tai"].impl("grouped_matmul_gather", gmm_gather, "CPU")
+        LIBS["tai"].impl("grouped_matmul_swiglu_quant_gather", gsq_gather, "CPU")
         lib.impl("npu_moe_init_routing", init_legacy, "CPU")
         lib.impl("npu_moe_finalize_routing", finalize, "CPU")
     for ns in ("npu", "npu_inference"):

@@ -343,6 +343,25 @@ def test_pattern_pass_fuses_routing_into_grouped_matmul_on_cpu():
         assert torch.equal(a, b)
     assert stats["routing_grouped_matmul"] == before + 1
 
+    ws = torch.rand(e, n, generator=g) * 0.01 + 1e-3
+
+    def swiglu(x, idx):
+        q, ri, tok, s = npu.npu_moe_init_routing_v2(x, idx, active_num=t * k, expert_num=e, expert_tokens_num_type=1,
+                                                    expert_tokens_num_flag=True, quant_mode=1)
+        acc = npu.npu_grouped_matmul([q], [w], group_list=tok, split_item=3, group_type=0, group_list_type=1,
+                                     output_dtype=torch.int32)[0]
+        return npu.npu_dequant_swiglu_quant(acc, weight_scale=ws, activation_scale=s, group_index=tok,
+                                            activate_left=True, quant_mode=1)
+
+    from torchair_amd.patterns import fuse_gather_dequant_swiglu_quant
+    gm = torch.fx.symbolic_trace(swiglu)
+    assert fuse_routing_grouped_matmul(gm) == 1 and fuse_gather_dequant_swiglu_quant(gm) == 1
+    targets = {nd.target for nd in gm.graph.nodes if nd.op == "call_function"}
+    assert torch.ops.tai.grouped_matmul_swiglu_quant_gather.default in targets
+    assert not {npu.npu_dequant_swiglu_quant, npu.npu_dequant_swiglu_quant.default} & targets
+    for a, b in zip(gm(x, idx), swiglu(x, idx)):
+        assert torch.equal(a, b)
+
     def rows_also_used(x, idx):
         q, ri, tok, s = npu.npu_moe_init_routing_v2(x, idx, active_num=t * k, expert_num=e, expert_tokens_num_type=1,
                                                     expert_tokens_num_flag=True, quant_mode=1)

@@ -134,3 +134,54 @@ def _gather_cuda(x, a_rows, weight, group_list, *, scale=None, per_token_scale=N
 _define("grouped_matmul_gather(Tensor x, Tensor a_rows, Tensor weight, Tensor group_list, *, Tensor? scale=None, "
         "Tensor? per_token_scale=None, Tensor? bias=None, int group_list_type=0, ScalarType? output_dtype=None) "
         "-> Tensor", _gather_fake, _gather_cuda)
+
+
+# ============================================================================ gathered gate_up + SwiGLU quant
+def _gsq_gather_fake(x, a_rows, weight, weight_scale, x_scale, group_list, *, group_list_type=0):
+    m = a_rows.shape[0]
+    return (x.new_empty((m, weight.shape[-1] // 2), dtype=torch.int8), x.new_empty((m,), dtype=torch.float32))
+
+
+def _gsq_gather_cuda(x, a_rows, weight, weight_scale, x_scale, group_list, *, group_list_type=0):
+    """npu_grouped_matmul_swiglu_quant_v2(x[a_rows], [weight], [weight_scale], x_scale, group_list) with the
+    rows gathered by the kernel; the fold of tai::grouped_matmul_gather(int32) + npu_dequant_swiglu_quant."""
+    from ._gmm_fused import _swiglu_packed
+    from ._lib import LAYOUT_KN_SWIGLU
+    name = "tai::grouped_matmul_swiglu_quant_gather"
+    _on_gpu(x, a_rows, weight, weight_scale, x_scale, group_list)
+    _check(x.dtype == torch.int8 and x.dim() == 2, f"{name}: x must be int8 [T, K]")
+    _check(a_rows.dtype == torch.int32 and a_rows.dim() == 1, f"{name}: a_rows must be int32 [M]")
+    _check(weight.dtype == torch.int8 and weight.dim() == 3, f"{name}: weight must be int8 [E, K, N]")
+    _check(group_list_type in (0, 1), f"{name}: group_list_type must be 0 (cumsum) or 1 (count)")
+    e, k, n = weight.shape
+    _check(x.shape[1] == k and n % 2 == 0, f"{name}: x is [T, K] and the weight [E, K, N] with N even")
+    if weight.is_contiguous():
+        wl, layout = weight, LAYOUT_KN
+        packed = _swiglu_packed(weight)
+        if packed is not None:
+            wl, layout = packed, LAYOUT_KN_SWIGLU
+    elif weight.transpose(1, 2).is_contiguous():
+        wl, layout = weight.transpose(1, 2), LAYOUT_NK
+    else:
+        wl, layout = weight.contiguous(), LAYOUT_KN
+    ws = _f32(weight_scale)
+    _check(ws.numel() == e * n, f"{name}: weight_scale must be [E, N]")
+    m = a_rows.shape[0]
+    xs = _f32(x_scale)
+    _check(xs.numel() == m, f"{name}: x_scale must have M entries")
+    gl = group_list.to(torch.int64).contiguous()
+    _check(gl.numel() == e, f"{name}: group_list has {gl.numel()} entries, weight has {e} groups")
+    y, ys = _gsq_gather_fake(x, a_rows, weight, weight_scale, x_scale, group_list)
+    if m == 0:
+        return y, ys
+    xc, rc = x.contiguous(), a_rows.contiguous()
+    nbytes = _lib.query("tai_grouped_matmul_swiglu_quant_workspace_size", m, n, e)
+    wsp = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    _lib.call("tai_grouped_matmul_swiglu_quant_gather", _p(xc), xc.shape[0], _p(rc), _p(wl), m, k, n, e, layout,
+              _p(gl), int(group_list_type), _p(ws), _p(xs), _p(y), _p(ys), _p(wsp), nbytes, _stream(xc))
+    return y, ys
+
+
+_define("grouped_matmul_swiglu_quant_gather(Tensor x, Tensor a_rows, Tensor weight, Tensor weight_scale, "
+        "Tensor x_scale, Tensor group_list, *, int group_list_type=0) -> (Tensor, Tensor)",
+        _gsq_gather_fake, _gsq_gather_cuda)

@@ -2015,11 +2015,38 @@ extern "C" size_t tai_grouped_matmul_swiglu_quant_workspace_size(int64_t m, int6
   return swiglu_ws_parts(m, n, num_groups, nullptr, nullptr);
 }
 
+static int swiglu_quant_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                             int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
+                             const float* weight_scale, const float* x_scale, int8_t* y, float* y_scale,
+                             void* workspace, size_t ws_bytes, void* stream, const int32_t* a_rows,
+                             int64_t a_src_rows);
+
 extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
                                                int64_t num_groups, int w_layout, const int64_t* group_list,
                                                int group_list_type, const float* weight_scale, const float* x_scale,
                                                int8_t* y, float* y_scale, void* workspace, size_t ws_bytes,
                                                void* stream) {
+  return swiglu_quant_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, weight_scale,
+                           x_scale, y, y_scale, workspace, ws_bytes, stream, nullptr, 0);
+}
+
+extern "C" int tai_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const int32_t* a_rows,
+                                                      const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                                                      int64_t num_groups, int w_layout, const int64_t* group_list,
+                                                      int group_list_type, const float* weight_scale,
+                                                      const float* x_scale, int8_t* y, float* y_scale,
+                                                      void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(x_rows >= 0, "tai_grouped_matmul_swiglu_quant_gather: x_rows must be >= 0");
+  if (m > 0) TAI_CHECK_ARG(a_rows && x_rows > 0, "tai_grouped_matmul_swiglu_quant_gather: a_rows and x rows are required");
+  return swiglu_quant_impl(x, weight, m, k, n, num_groups, w_layout, group_list, group_list_type, weight_scale,
+                           x_scale, y, y_scale, workspace, ws_bytes, stream, a_rows, x_rows);
+}
+
+static int swiglu_quant_impl(const int8_t* x, const int8_t* weight, int64_t m, int64_t k, int64_t n,
+                             int64_t num_groups, int w_layout, const int64_t* group_list, int group_list_type,
+                             const float* weight_scale, const float* x_scale, int8_t* y, float* y_scale,
+                             void* workspace, size_t ws_bytes, void* stream, const int32_t* a_rows,
+                             int64_t a_src_rows) {
   TAI_CHECK_ARG(m >= 0 && k >= 0 && n >= 2 && num_groups >= 1, "tai_grouped_matmul_swiglu_quant: bad sizes");
   TAI_CHECK_ARG(num_groups <= 2048, "tai_grouped_matmul_swiglu_quant: at most 2048 groups");
   TAI_CHECK_ARG(w_layout == TAI_LAYOUT_KN || w_layout == TAI_LAYOUT_NK || w_layout == TAI_LAYOUT_KN_SWIGLU,
@@ -2058,6 +2085,8 @@ extern "C" int tai_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* we
   GemmArgs g{x, weight, m, k, n, k * n, weight_scale, n, n, x_scale, nullptr, 0, n, kOutSwiglu, nullptr,
              map, slots, n_tiles, live, h, part};
   g.swi_packed = packed ? 1 : 0;
+  g.a_rows = a_rows;
+  g.a_src_rows = a_src_rows;
   group_tiles_kernel<<<1, 1024, sizeof(int64_t) * (3 * num_groups + 1), st>>>(group_list, num_groups, group_list_type,
                                                                               m, bm, map, slots, live, nullptr);
   if (kn && TAI_MIXED && n % GrpKnSel::kBN == 0 && mixed_available()) launch_mixed(g, st);

@@ -33,7 +33,8 @@ import torch.fx
 logger = logging.getLogger("torchair_amd")
 
 # rewrites applied so far in this process, per pattern (diagnostics and tests)
-stats = {"add_rms_norm_dynamic_quant": 0, "init_routing_dynamic_quant": 0, "routing_grouped_matmul": 0}
+stats = {"add_rms_norm_dynamic_quant": 0, "init_routing_dynamic_quant": 0, "routing_grouped_matmul": 0,
+         "gather_dequant_swiglu_quant": 0}
 
 
 def _getitems(node: torch.fx.Node):
@@ -270,8 +271,57 @@ def fuse_routing_grouped_matmul(gm: torch.fx.GraphModule) -> int:
     return fused
 
 
+def fuse_gather_dequant_swiglu_quant(gm: torch.fx.GraphModule) -> int:
+    tai, npu = getattr(torch.ops, "tai", None), torch.ops.npu
+    if tai is None or not hasattr(tai, "grouped_matmul_swiglu_quant_gather"):
+        return 0
+    fused = 0
+    for gmm in list(gm.graph.nodes):
+        if not _calls(gmm, tai.grouped_matmul_gather) or len(gmm.args) != 4 or len(gmm.users) != 1:
+            continue
+        kw = dict(gmm.kwargs)
+        if kw.get("output_dtype") not in (torch.int32, 3) or kw.get("group_list_type") != 1:
+            continue
+        if any(kw.get(k) is not None for k in ("scale", "per_token_scale", "bias")):
+            continue
+        dsq = next(iter(gmm.users))
+        if not _calls(dsq, npu.npu_dequant_swiglu_quant) or dsq.args != (gmm,):
+            continue
+        dkw = dict(dsq.kwargs)
+        counts = gmm.args[3]
+        ok = {"weight_scale", "activation_scale", "group_index", "activate_left", "quant_mode", "dst_type",
+              "round_mode", "activate_dim", "swiglu_mode", "bias", "quant_scale", "quant_offset"}
+        if set(dkw) - ok or dkw.get("group_index") is not counts or dkw.get("activate_left") is not True:
+            continue
+        if dkw.get("quant_mode") != 1 or dkw.get("dst_type") not in (None, 1) or dkw.get("round_mode") not in (None, 0):
+            continue
+        if dkw.get("activate_dim") not in (None, -1, 1) or dkw.get("swiglu_mode", 0) != 0:
+            continue
+        if any(dkw.get(k) is not None for k in ("bias", "quant_scale", "quant_offset")):
+            continue
+        if not isinstance(dkw.get("weight_scale"), torch.fx.Node) or not isinstance(dkw.get("activation_scale"),
+                                                                                     torch.fx.Node):
+            continue
+        x, a_rows, w = gmm.args[:3]
+        with gm.graph.inserting_before(dsq):
+            node = gm.graph.call_function(tai.grouped_matmul_swiglu_quant_gather.default,
+                                          (x, a_rows, w, dkw["weight_scale"], dkw["activation_scale"], counts),
+                                          {"group_list_type": 1})
+        dsq.replace_all_uses_with(node)  # both return (y, scale)
+        gm.graph.erase_node(dsq)
+        gm.graph.erase_node(gmm)
+        fused += 1
+    if fused:
+        gm.graph.lint()
+        gm.recompile()
+        stats["gather_dequant_swiglu_quant"] += fused
+        logger.debug("fused %d grouped_matmul_gather + dequant_swiglu_quant pair(s)", fused)
+    return fused
+
+
 def apply_pattern_passes(gm: torch.fx.GraphModule) -> torch.fx.GraphModule:
     fuse_add_rms_norm_dynamic_quant(gm)
     fuse_init_routing_dynamic_quant(gm)
     fuse_routing_grouped_matmul(gm)
+    fuse_gather_dequant_swiglu_quant(gm)
     return gm
