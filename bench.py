@@ -429,7 +429,9 @@ def bench_mlp(torch, dev, iters=50, cpu=False):
         e1.record()
         torch.cuda.synchronize()
         out[name + "_us"] = round(e0.elapsed_time(e1) / iters * 1e3, 2)
-    algo = T * H * 2 + H * 2 * I + T * 2 * I * 4 * 2 + I * H + T * I + T * H * 2
+    # the MLP's operands: x, both weights, their scales and the output (the intermediates between the ops
+    # are not operands of the layer)
+    algo = T * H * 2 + H * 2 * I + I * H + 2 * I * 4 + H * 4 + T * H * 2
     out["algorithmic_MB"] = round(algo / 1e6, 2)
     out["hbm_frac_hipgraph"] = round(algo / (out["hipgraph_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     if cpu:
