@@ -50,6 +50,22 @@ def test_gating_ties_pick_lower_index():
     assert idx.cpu()[0].tolist() == [0, 1, 2, 3]
 
 
+@pytest.mark.parametrize("groups,k_group,mode", [(8, 4, 1), (8, 3, 0), (1, 1, 1), (8, 8, 1)])
+def test_gating_256_experts_register_path(groups, k_group, mode):
+    """E = 256 with sigmoid scores takes the register-resident kernel (8 groups of 32 or no groups): the
+    oracle's choices and weights, including rows with tied scores, tied group scores and a bf16 input."""
+    g = gen(32)
+    x = torch.randn(1037, 256, generator=g)
+    x[3] = 0.0                      # every score tied
+    x[4, ::7] = 2.0                 # ties across groups
+    x[5, 32:64] = 1.5               # one group of equal maxima (top-2 = 2 * max)
+    bias = torch.randn(256, generator=g) * 0.1
+    _gate_check(x, 8, bias, k_group=k_group, group_count=groups, group_select_mode=mode, norm_type=1, out_flag=True,
+                routed_scaling_factor=2.5)
+    _gate_check(x.to(torch.bfloat16), 6, bias.to(torch.bfloat16), k_group=k_group, group_count=groups,
+                group_select_mode=mode, norm_type=1)
+
+
 def _routing_inputs(t, h, e, k, g):
     x = randn((t, h), g)
     logits = torch.randn(t, e, generator=g)

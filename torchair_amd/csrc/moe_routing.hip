@@ -149,6 +149,97 @@ __global__ __launch_bounds__(256) void gating_topk_kernel(GateArgs a) {
     for (int j = lane; j < E; j += 64) a.out[row * E + j] = sc[j];
 }
 
+// The common DeepSeek-V3 shape (256 experts, sigmoid scores, no groups or 8 groups of 32) with every
+// score in registers: lane l holds experts l + 64 q, q = 0..3, so expert group 2 q + (l >= 32) is one
+// half-wave of slice q and its top-2 sum comes from butterfly merges of per-lane top-2 pairs, with no
+// LDS and no workgroup barrier. Same arithmetic and tie rules as gating_topk_kernel, so the same result.
+__global__ __launch_bounds__(256) void gating_topk_256_kernel(GateArgs a) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (row >= a.t) return;
+  float sc[4], v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = lane + 64 * q;
+    const double xv = static_cast<double>(load_as_f32(a.x, a.x_dt, row * 256 + j));
+    sc[q] = static_cast<float>(1.0 / (1.0 + exp(-xv)));
+    v[q] = a.bias ? sc[q] + load_as_f32(a.bias, a.bias_dt, j) : sc[q];
+  }
+  if (a.group_count == 8) {
+    // top-2 of each half-wave (32 experts of one group), merged pairwise: (t1, t2) keep the largest
+    // and second largest values counted with multiplicity
+    float gsc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float t1 = v[q], t2 = -INFINITY;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) {
+        const float u1 = __shfl_xor(t1, o, 64), u2 = __shfl_xor(t2, o, 64);
+        const float n1 = fmaxf(t1, u1);
+        t2 = fmaxf(fminf(t1, u1), fmaxf(t2, u2));
+        t1 = n1;
+      }
+      gsc[q] = a.group_select_mode == 1 ? t1 + t2 : t1;
+    }
+    float gs[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      gs[2 * q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsc[q]), 0));
+      gs[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsc[q]), 32));
+    }
+    bool keep[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      int rank = 0;
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh) rank += better(gs[hh], hh, gs[g], g) ? 1 : 0;
+      keep[g] = rank < a.k_group;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool kept = lane < 32 ? keep[2 * q] : keep[2 * q + 1];
+      if (!kept) v[q] = -INFINITY;
+    }
+  }
+  int my_sel = 0;
+  for (int r = 0; r < a.k; ++r) {
+    float bv = -INFINITY;
+    int bi = kMaxExperts;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (better(v[q], lane + 64 * q, bv, bi)) { bv = v[q]; bi = lane + 64 * q; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      float ov = __shfl_xor(bv, o, 64);
+      int oi = __shfl_xor(bi, o, 64);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    bi = __builtin_amdgcn_readfirstlane(bi);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (lane + 64 * q == bi) v[q] = -INFINITY;
+    if (lane == r) my_sel = bi;
+  }
+  // the normalised score of this lane's selected expert, from the lane that holds it
+  const int sq = my_sel >> 6, sl = my_sel & 63;
+  float s0 = __shfl(sc[0], sl, 64), s1 = __shfl(sc[1], sl, 64), s2 = __shfl(sc[2], sl, 64), s3 = __shfl(sc[3], sl, 64);
+  const float picked = sq == 0 ? s0 : (sq == 1 ? s1 : (sq == 2 ? s2 : s3));
+  const float myw = lane < a.k ? picked : 0.0f;
+  float wsum = 0.0f;
+  for (int r = 0; r < a.k; ++r) wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myw), r));
+  if (lane < a.k) {
+    float wv = myw;
+    wv = wv / (wsum + a.eps);
+    wv = wv * a.rsf;
+    store_from_f32(a.y, a.x_dt, row * a.k + lane, wv);
+    a.idx[row * a.k + lane] = my_sel;
+  }
+  if (a.out_flag && a.out) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a.out[row * 256 + lane + 64 * q] = sc[q];
+  }
+}
+
 // ============================================================================ init routing
 constexpr int kChunk = 256;  // routing slots per chunk (one per thread)
 
@@ -536,7 +627,11 @@ extern "C" int tai_moe_gating_top_k(const void* x, int x_dtype, int64_t t, int64
   TAI_CHECK_ARG(x && y && expert_idx, "tai_moe_gating_top_k: null pointer");
   GateArgs a{x, x_dtype, t, e, k, bias, bias_dtype, k_group, group_count, group_select_mode, norm_type,
              out_flag, routed_scaling_factor, eps, y, expert_idx, out};
-  gating_topk_kernel<<<dim3(static_cast<unsigned>(cdiv(t, 4))), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  const bool fast = e == 256 && norm_type == 1 && (group_count == 1 || group_count == 8);
+  if (fast)
+    gating_topk_256_kernel<<<dim3(static_cast<unsigned>(cdiv(t, 4))), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  else
+    gating_topk_kernel<<<dim3(static_cast<unsigned>(cdiv(t, 4))), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("tai_moe_gating_top_k");
 }
 
