@@ -415,7 +415,8 @@ def bench_mlp(torch, dev, iters=50, cpu=False):
         return npu.npu_quant_matmul(q2, wd, sd, pertoken_scale=s2, output_dtype=torch.bfloat16)
 
     from torchair_amd.graph import HipGraphRunner
-    runner = HipGraphRunner(mlp)
+    # inputs by address, as the headline layer runs (clone_input=False): the resident x is not copied per replay
+    runner = HipGraphRunner(mlp, clone_input=False)
     for _ in range(3):
         runner(x)
         mlp(x)
