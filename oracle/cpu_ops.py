@@ -145,6 +145,33 @@ def register() -> None:
     def gsq_gather(x, a_rows, weight, weight_scale, x_scale, group_list, *, group_list_type=0):
         return gsq(x[a_rows.long()], [weight], [weight_scale], x_scale, group_list, group_list_type=group_list_type)
 
+    def fia_v2(query, key, value, *, pse_shift=None, atten_mask=None, actual_seq_qlen=None, actual_seq_kvlen=None,
+               block_table=None, num_query_heads=1, num_key_value_heads=0, softmax_scale=1.0, pre_tokens=2147483647,
+               next_tokens=2147483647, input_layout="BSH", sparse_mode=0, return_softmax_lse=False, **unused):
+        # dense prefill of npu_fused_infer_attention_score_v2 (BSH / BSND / BNSD, no mask or a causal
+        # sparse_mode 2 / 3): prefill_attention over [B, S, N, D] views
+        assert block_table is None and pse_shift is None and atten_mask is None
+        assert all(v in (None, 0, False) for v in unused.values()), "only the dense prefill cases are served"
+        hq = num_query_heads
+        hkv = num_key_value_heads or hq
+
+        def bsnd(t, n):
+            if input_layout == "BSH":
+                return t.reshape(t.shape[0], t.shape[1], n, -1)
+            return t.permute(0, 2, 1, 3) if input_layout == "BNSD" else t
+        q, k, v = bsnd(query, hq), bsnd(key, hkv), bsnd(value, hkv)
+        causal = {0: 0, 2: 2, 3: 1}[sparse_mode]
+        sq = None if actual_seq_qlen is None else np.asarray(actual_seq_qlen)
+        skv = None if actual_seq_kvlen is None else np.asarray(actual_seq_kvlen)
+        o, lse = G.prefill_attention(_np(q), _np(k), _np(v), sq, skv, causal, softmax_scale)
+        out = _t(o, query.dtype)
+        if input_layout == "BSH":
+            out = out.reshape(query.shape[0], query.shape[1], -1)
+        elif input_layout == "BNSD":
+            out = out.permute(0, 2, 1, 3).contiguous()
+        lse_t = _t(lse).unsqueeze(-1) if return_softmax_lse else torch.empty(0, dtype=torch.float32)
+        return out, lse_t
+
     def init_legacy(x, row_idx, expert_idx, active_num):
         ex, ri, ei = G.moe_init_routing(_np(x), row_idx.numpy(), expert_idx.numpy(), active_num)
         return _t(ex, x.dtype), _t(ri), _t(ei)
@@ -258,6 +285,7 @@ def register() -> None:
         LIBS["tai"].impl("moe_init_routing_v2_rows", init_v2_rows, "CPU")
         LIBS["tai"].impl("grouped_matmul_gather", gmm_gather, "CPU")
         LIBS["tai"].impl("grouped_matmul_swiglu_quant_gather", gsq_gather, "CPU")
+        LIBS["air"].impl("npu_fused_infer_attention_score_v2", fia_v2, "CPU")
         lib.impl("npu_moe_init_routing", init_legacy, "CPU")
         lib.impl("npu_moe_finalize_routing", finalize, "CPU")
     for ns in ("npu", "npu_inference"):

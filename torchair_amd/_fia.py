@@ -622,3 +622,70 @@ def _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv,
               bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, dn, dr, bs, scale, out.data_ptr(),
               lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
     return out, lse
+
+
+# ============================================================================ npu_fused_infer_attention_score_v2
+# python/torchair/ops/_npu_fused_infer_attention_score_v2.py:14-30 (air:: schema, tensor lengths) and
+# .../custom/fused_infer_attention_score_v2.py:14-60 (npu::, list or tensor lengths): the same operator
+# under renamed arguments, lowered to the same FusedInferAttentionScore node (:166-181), so it maps onto
+# the v1 implementation argument for argument. Arguments of v2 with no v1 counterpart that this build
+# does not serve (query quantisation, the softmax quant scale, learnable_sink, dtype reinterpretations)
+# are refused.
+_V2_UNSUPPORTED = ("dequant_scale_query", "quant_scale_p", "learnable_sink", "query_dtype", "key_dtype", "value_dtype",
+                   "query_rope_dtype", "key_rope_dtype", "key_shared_prefix_dtype", "value_shared_prefix_dtype",
+                   "dequant_scale_query_dtype", "dequant_scale_key_dtype", "dequant_scale_value_dtype",
+                   "dequant_scale_key_rope_dtype")
+
+
+def _v2_to_v1(kw: dict, check: bool = True) -> dict:
+    name = "npu_fused_infer_attention_score_v2"
+    if check:
+        for k in _V2_UNSUPPORTED:
+            _check(kw.get(k) is None, f"{name}: {k} is not supported")
+        _check(kw.get("query_quant_mode", 0) == 0, f"{name}: query_quant_mode must be 0")
+    m = {"pse_shift": "pse_shift", "atten_mask": "atten_mask", "actual_seq_qlen": "actual_seq_lengths",
+         "actual_seq_kvlen": "actual_seq_lengths_kv", "block_table": "block_table",
+         "dequant_scale_key": "key_antiquant_scale", "dequant_offset_key": "key_antiquant_offset",
+         "dequant_scale_value": "value_antiquant_scale", "dequant_offset_value": "value_antiquant_offset",
+         "dequant_scale_key_rope": "key_rope_antiquant_scale", "quant_scale_out": "quant_scale2",
+         "quant_offset_out": "quant_offset2", "query_rope": "query_rope", "key_rope": "key_rope",
+         "num_query_heads": "num_heads", "num_key_value_heads": "num_key_value_heads", "softmax_scale": "scale",
+         "pre_tokens": "pre_tokens", "next_tokens": "next_tokens", "input_layout": "input_layout",
+         "sparse_mode": "sparse_mode", "block_size": "block_size", "inner_precise": "inner_precise",
+         "key_quant_mode": "key_antiquant_mode", "value_quant_mode": "value_antiquant_mode",
+         "return_softmax_lse": "softmax_lse_flag"}
+    return {m[k]: v for k, v in kw.items() if k in m}
+
+
+def _v2_out_dtype(kw: dict, query):
+    """attention_out dtype of the v2 meta rule (_npu_fused_infer_attention_score_v2.py:396-412): int8 (or
+    out_dtype) with quant_scale_out, else the query dtype (int8 / fp8 queries are not served)."""
+    od = kw.get("out_dtype")
+    if kw.get("quant_scale_out") is not None:
+        if od is None:
+            return torch.int8
+        from ._ops_impl import dtype_of_code, scalar_type_code
+        return dtype_of_code(scalar_type_code(od))
+    _check(od is None or od in (query.dtype, _torch_code(query.dtype)),
+           "npu_fused_infer_attention_score_v2: out_dtype applies with quant_scale_out")
+    return query.dtype
+
+
+def _torch_code(dt):
+    from ._ops_impl import scalar_type_code
+    return scalar_type_code(dt)
+
+
+def fia_v2_fake(query, key, value, **kw):
+    out, lse = fia_fake(query, key, value, **_v2_to_v1(kw, check=False))
+    od = _v2_out_dtype(kw, query)
+    return (out if out.dtype == od else out.new_empty(out.shape, dtype=od)), lse
+
+
+def fia_v2_cuda(query, key, value, **kw):
+    """ROCm implementation of npu_fused_infer_attention_score_v2: the v1 kernels under the v1 names."""
+    od = _v2_out_dtype(kw, query)
+    out, lse = fia_cuda(query, key, value, **_v2_to_v1(kw))
+    _check(out.dtype == od, "npu_fused_infer_attention_score_v2: out_dtype does not match the served output")
+    return out, lse
+

@@ -860,6 +860,28 @@ _define("air", "npu_fused_infer_attention_score(" + _FIA_ARGS.format(
     tail="int key_antiquant_mode=0, int value_antiquant_mode=0, bool softmax_lse_flag=False"),
     _fia.fia_fake, _fia.fia_cuda)
 
+# npu_fused_infer_attention_score_v2: air:: (python/torchair/ops/_npu_fused_infer_attention_score_v2.py:16-30,
+# tensor lengths) and npu:: (torch_npu's op, list lengths, converter .../custom/fused_infer_attention_score_v2.py:14)
+_FIA_V2_ARGS = ("Tensor query, Tensor key, Tensor value, *, Tensor? query_rope=None, Tensor? key_rope=None, "
+                "Tensor? pse_shift=None, Tensor? atten_mask=None, {seq} actual_seq_qlen=None, "
+                "{seq} actual_seq_kvlen=None, Tensor? block_table=None, Tensor? dequant_scale_query=None, "
+                "Tensor? dequant_scale_key=None, Tensor? dequant_offset_key=None, Tensor? dequant_scale_value=None, "
+                "Tensor? dequant_offset_value=None, Tensor? dequant_scale_key_rope=None, "
+                "Tensor? quant_scale_out=None, Tensor? quant_offset_out=None, Tensor? quant_scale_p=None, "
+                "Tensor? learnable_sink=None, int num_query_heads=1, int num_key_value_heads=0, "
+                "float softmax_scale=1.0, int pre_tokens=2147483647, int next_tokens=2147483647, "
+                "str input_layout=\"BSH\", int sparse_mode=0, int block_size=0, int query_quant_mode=0, "
+                "int key_quant_mode=0, int value_quant_mode=0, int inner_precise=0, bool return_softmax_lse=False, "
+                "int? query_dtype=None, int? key_dtype=None, int? value_dtype=None, int? query_rope_dtype=None, "
+                "int? key_rope_dtype=None, int? key_shared_prefix_dtype=None, int? value_shared_prefix_dtype=None, "
+                "int? dequant_scale_query_dtype=None, int? dequant_scale_key_dtype=None, "
+                "int? dequant_scale_value_dtype=None, int? dequant_scale_key_rope_dtype=None, int? out_dtype=None) "
+                "-> (Tensor, Tensor)")
+_define("air", "npu_fused_infer_attention_score_v2(" + _FIA_V2_ARGS.format(seq="Tensor?"), _fia.fia_v2_fake,
+        _fia.fia_v2_cuda)
+_define("npu", "npu_fused_infer_attention_score_v2(" + _FIA_V2_ARGS.format(seq="SymInt[]?"), _fia.fia_v2_fake,
+        _fia.fia_v2_cuda)
+
 from . import _norm_cache  # noqa: E402,F401  (RMS-norm family and KV-cache writers)
 
 from . import _gmm_fused  # noqa: E402,F401  (fused MoE grouped GEMMs)

@@ -78,6 +78,20 @@ register_fx_node_ge_converter(npu.npu_fused_infer_attention_score.default)(
     _identity(npu.npu_fused_infer_attention_score.default))
 register_fx_node_ge_converter(air.npu_fused_infer_attention_score.default)(
     _identity(air.npu_fused_infer_attention_score.default))
+# python/torchair/ops/_npu_fused_infer_attention_score_v2.py:48-62 (its declared cases) and
+# .../custom/fused_infer_attention_score_v2.py:14
+declare_supported([
+    Support(torch.empty(1, 2048, 40 * 128, dtype=torch.float16), torch.empty(1, 2048, 40 * 128, dtype=torch.float16),
+            torch.empty(1, 2048, 40 * 128, dtype=torch.float16), num_query_heads=40, input_layout="BSH"),
+    Support(torch.empty(1, 40, 2048, 128, dtype=torch.float16), torch.empty(1, 40, 2048, 128, dtype=torch.float16),
+            torch.empty(1, 40, 2048, 128, dtype=torch.float16), num_query_heads=40, input_layout="BNSD"),
+    Support(torch.empty(1, 40, 2048, 128, dtype=torch.float16), torch.empty(1, 40, 2048, 128, dtype=torch.float16),
+            torch.empty(1, 40, 2048, 128, dtype=torch.float16), input_layout="BNSD", num_query_heads=40,
+            softmax_scale=0.0884),
+])(register_fx_node_ge_converter(air.npu_fused_infer_attention_score_v2.default)(
+    _identity(air.npu_fused_infer_attention_score_v2.default)))
+register_fx_node_ge_converter(npu.npu_fused_infer_attention_score_v2.default)(
+    _identity(npu.npu_fused_infer_attention_score_v2.default))
 # .../custom/npu_add_rms_norm.py:4-13, npu_add_rms_norm_dynamic_quant.py:8-21
 register_fx_node_ge_converter(npu.npu_add_rms_norm.default)(_identity(npu.npu_add_rms_norm.default))
 # .../custom/npu_add_rms_norm_dynamic_quant.py:4-7
