@@ -103,6 +103,15 @@ int tai_dynamic_quant_v2(const void* x, int x_dtype, int64_t rows, int64_t cols,
                          void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * npu_swiglu: y = silu(a) * b, a and b the first and second halves of x along one dimension;
+ * x viewed as [outer, 2 * n, inner] (the split dimension in the middle), y as [outer, n, inner];
+ * bf16 / fp16 / fp32 (dtype), fp32 arithmetic, one rounding to the dtype.
+ * Replaces ge.SwiGlu emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_swiglu.py:4-14.
+ * ------------------------------------------------------------------------------------- */
+int tai_swiglu(const void* x, int dtype, int64_t outer, int64_t n, int64_t inner, void* y, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * npu_dequant_swiglu_quant (quant_mode=1 dynamic, swiglu_mode=0, round_mode=0 rint).
  * Replaces ge.DequantSwigluQuant emitted by
  *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_dequant_swiglu_quant.py:5-47
@@ -282,6 +291,17 @@ int tai_moe_gating_top_k(const void* x, int x_dtype, int64_t t, int64_t e, int k
                          int group_select_mode, int renorm, int norm_type, int out_flag,
                          float routed_scaling_factor, float eps, void* y, int32_t* expert_idx,
                          float* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * npu_moe_compute_expert_tokens: out[e] = the number of entries of the ascending sorted_experts
+ * [n] int32 that are <= e, for e < num_experts (the end row of each expert, the cumulative
+ * group_list of the legacy routing path).
+ * Replaces ge.MoeComputeExpertTokens emitted by
+ *   python/torchair/_ge_concrete_graph/ge_converter/custom/npu_moe_compute_expert_tokens.py:4-11
+ *   (prototype experiment_ops.h:3550-3563).
+ * ------------------------------------------------------------------------------------- */
+int tai_moe_compute_expert_tokens(const int32_t* sorted_experts, int64_t n, int64_t num_experts,
+                                  int32_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_moe_init_routing_v2 (dropless, drop_pad_mode 0, quant_mode -1).

@@ -172,6 +172,12 @@ def register() -> None:
         lse_t = _t(lse).unsqueeze(-1) if return_softmax_lse else torch.empty(0, dtype=torch.float32)
         return out, lse_t
 
+    def swiglu(x, dim=-1):
+        return _t(G.swiglu(_np(x), dim, _NAMES[x.dtype]), x.dtype)
+
+    def cet(sorted_experts, num_experts):
+        return _t(G.moe_compute_expert_tokens(sorted_experts.numpy(), num_experts))
+
     def init_legacy(x, row_idx, expert_idx, active_num):
         ex, ri, ei = G.moe_init_routing(_np(x), row_idx.numpy(), expert_idx.numpy(), active_num)
         return _t(ex, x.dtype), _t(ri), _t(ei)
@@ -287,6 +293,8 @@ def register() -> None:
         LIBS["tai"].impl("grouped_matmul_swiglu_quant_gather", gsq_gather, "CPU")
         LIBS["air"].impl("npu_fused_infer_attention_score_v2", fia_v2, "CPU")
         lib.impl("npu_moe_init_routing", init_legacy, "CPU")
+        lib.impl("npu_swiglu", swiglu, "CPU")
+        lib.impl("npu_moe_compute_expert_tokens", cet, "CPU")
         lib.impl("npu_moe_finalize_routing", finalize, "CPU")
     for ns in ("npu", "npu_inference"):
         LIBS[ns].impl("npu_dequant_swiglu_quant", dsq, "CPU")

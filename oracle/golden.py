@@ -952,3 +952,28 @@ def grouped_matmul_finalize_routing(x, w, group_list, group_list_type: int = 1, 
         y[shared_input_offset:shared_input_offset + s.shape[0]] = (
             y[shared_input_offset:shared_input_offset + s.shape[0]] + (F32(shared_input_weight) * s).astype(F32))
     return y
+
+
+def swiglu(x, dim: int = -1, out_dtype: str = "fp32"):
+    """npu_swiglu (converter .../custom/npu_swiglu.py:4-14, ge.SwiGlu): y = silu(a) * b, where a and b
+    are the first and second halves of x along `dim`, in fp32, rounded once to the output dtype
+    ("bf16" / "fp16" / "fp32"). Which half is activated is the operator's documented convention (the
+    reference holds only the converter); pinned by reductions in the tests (b = 1 gives silu(a), a = 0
+    gives 0, a large gives about a * b)."""
+    x = np.asarray(x, F32)
+    n = x.shape[dim] // 2
+    a = np.take(x, np.arange(n), axis=dim)
+    b = np.take(x, np.arange(n, 2 * n), axis=dim)
+    with np.errstate(over="ignore"):
+        y = ((a / (F32(1) + np.exp(-a))) * b).astype(F32)
+    return round_to(y, out_dtype)
+
+
+def moe_compute_expert_tokens(sorted_experts, num_experts: int):
+    """npu_moe_compute_expert_tokens (converter .../custom/npu_moe_compute_expert_tokens.py:4-11,
+    prototype experiment_ops.h:3550-3563: "finds the position of the last row processed by each expert
+    in the sorted_experts array"): out[e] = the number of entries of the ascending array that are <= e,
+    int32 [num_experts]."""
+    se = np.asarray(sorted_experts, np.int64)
+    return np.searchsorted(se, np.arange(num_experts, dtype=np.int64), side="right").astype(np.int32)
+

@@ -272,3 +272,12 @@ def test_init_routing_v2_static_quant(drop_pad, form):
     assert ex.dtype == torch.int8 and es.numel() == 0
     np.testing.assert_array_equal(ri.cpu().numpy(), wri)
     np.testing.assert_array_equal(ex.cpu().numpy(), G.static_quant_rows(bex, sc.numpy(), of.numpy(), grp))
+
+
+def test_moe_compute_expert_tokens():
+    g = gen(33)
+    for n, e in ((0, 16), (1, 1), (32768, 256), (1000, 64)):
+        se = torch.sort(torch.randint(0, e + 2, (n,), generator=g)).values.to(torch.int32)  # ids past E too
+        got = torch.ops.npu.npu_moe_compute_expert_tokens(se.to(DEV), e)
+        assert got.dtype == torch.int32 and got.shape == (e,)
+        np.testing.assert_array_equal(got.cpu().numpy(), G.moe_compute_expert_tokens(se.numpy(), e))

@@ -5,7 +5,7 @@ import torch
 
 import torchair_amd  # noqa: F401
 from oracle import golden as G
-from tests.helpers import assert_int8_close, f32np, gen, randn, uniform
+from tests.helpers import assert_close, assert_int8_close, f32np, gen, randn, uniform
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -155,3 +155,20 @@ def test_dequant_swiglu_quant_static_mode(grouped):
                                      counts.numpy() if grouped else None, True, 0, qo.numpy())
     assert_int8_close(y.cpu().numpy(), wy)
     np.testing.assert_array_equal(s.cpu().numpy(), wsc)
+
+
+@pytest.mark.parametrize("dt,name", [(torch.float32, "fp32"), (torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+@pytest.mark.parametrize("shape,dim", [((128, 11264), -1), ((6, 10, 4), 1), ((8, 3, 5), 0)])
+def test_swiglu(dt, name, shape, dim):
+    """npu_swiglu against the oracle: fp32 within a few ulp (the hardware exp2 and reciprocal), bf16 / fp16
+    within one rounding of the output."""
+    g = gen(34)
+    x = (torch.randn(shape, generator=g) * 3).to(dt)
+    y = torch.ops.npu.npu_swiglu(x.to(DEV), dim=dim)
+    want = G.swiglu(f32np(x), dim, name)
+    got = f32np(y)
+    assert y.dtype == dt and got.shape == want.shape
+    if dt == torch.float32:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    else:
+        assert_close(got, want)

@@ -575,3 +575,27 @@ def test_shared_prefix_reductions():
     o, ol = G.prefill_attention(q, kk, vv, None, ll, 1, 0.3)
     np.testing.assert_allclose(o, base, rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(ol, bl, rtol=1e-6, atol=1e-6)
+
+
+def test_swiglu_reductions():
+    """b = 1 gives silu(a) = a * sigmoid(a) (scipy's expit); a = 0 gives 0; the split along another
+    dimension equals the transposed last-dimension split."""
+    from scipy.special import expit
+    rng = np.random.default_rng(46)
+    a = rng.standard_normal((5, 6)).astype(np.float32) * 4
+    x = np.concatenate([a, np.ones_like(a)], axis=1)
+    np.testing.assert_allclose(G.swiglu(x), a * expit(a), rtol=2e-6, atol=1e-7)
+    x0 = np.concatenate([np.zeros_like(a), a], axis=1)
+    assert not G.swiglu(x0).any()
+    y = rng.standard_normal((8, 3)).astype(np.float32)
+    np.testing.assert_array_equal(G.swiglu(y, dim=0), G.swiglu(y.T, dim=-1).T)
+    assert G.swiglu(y.T, out_dtype="bf16").dtype == np.float32
+
+
+def test_moe_compute_expert_tokens_brute_force():
+    rng = np.random.default_rng(47)
+    for n, e in ((0, 4), (50, 8), (300, 40)):
+        se = np.sort(rng.integers(0, e + 3, n)).astype(np.int32)  # ids past the expert range too
+        got = G.moe_compute_expert_tokens(se, e)
+        want = np.array([(se <= k).sum() for k in range(e)], np.int32)
+        np.testing.assert_array_equal(got, want)

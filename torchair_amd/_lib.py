@@ -73,6 +73,8 @@ _SIGS = {
         c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, c_int, c_int, _P, _P]),
     "tai_grouped_matmul_swiglu_quant_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "tai_swiglu_pack_kn": (c_int, [_P, c_int64, c_int64, _P, _P]),
+    "tai_swiglu": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, _P]),
+    "tai_moe_compute_expert_tokens": (c_int, [_P, c_int64, c_int64, _P, _P]),
     "tai_grouped_matmul_swiglu_quant_gather": (
         c_int, [_P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_int, _P, _P, _P, _P, _P, c_size_t,
                 _P]),

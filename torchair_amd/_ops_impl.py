@@ -274,6 +274,53 @@ _define("npu", _DSQ_SCHEMA, _dsq_fake, _dsq_cuda)
 _define("npu_inference", _DSQ_SCHEMA, _dsq_fake, _dsq_cuda)
 
 
+# ============================================================================ npu_swiglu
+def _swiglu_fake(x, dim=-1):
+    d = dim % x.dim() if x.dim() else 0
+    _check(x.dim() > 0 and x.shape[d] % 2 == 0, "npu_swiglu: the split dimension must have an even size")
+    shape = list(x.shape)
+    shape[d] //= 2
+    return x.new_empty(shape)
+
+
+def _swiglu_cuda(x, dim=-1):
+    """npu_swiglu (.../custom/npu_swiglu.py:4-14): silu of the first half of `dim` times the second half."""
+    _on_gpu(x)
+    _check(x.dtype in (torch.bfloat16, torch.float16, torch.float32), "npu_swiglu: x must be bf16, fp16 or fp32")
+    y = _swiglu_fake(x, dim)
+    d = dim % x.dim()
+    xc = x.contiguous()
+    outer = math.prod(xc.shape[:d])
+    inner = math.prod(xc.shape[d + 1:])
+    n = xc.shape[d] // 2
+    if y.numel():
+        _lib.call("tai_swiglu", _p(xc), _DT[xc.dtype], outer, n, inner, _p(y), _stream(xc))
+    return y
+
+
+_define("npu", "npu_swiglu(Tensor self, int dim=-1) -> Tensor", _swiglu_fake, _swiglu_cuda)
+
+
+# ============================================================================ npu_moe_compute_expert_tokens
+def _cet_fake(sorted_experts, num_experts):
+    return sorted_experts.new_empty((num_experts,), dtype=torch.int32)
+
+
+def _cet_cuda(sorted_experts, num_experts):
+    """npu_moe_compute_expert_tokens (.../custom/npu_moe_compute_expert_tokens.py:4-11): the end row of each
+    expert in the ascending expert ids of the legacy routing."""
+    _on_gpu(sorted_experts)
+    _check(sorted_experts.dtype == torch.int32, "npu_moe_compute_expert_tokens: sorted_experts must be int32")
+    _check(0 < num_experts < 2147483647, "npu_moe_compute_expert_tokens: num_experts must be positive")
+    se = sorted_experts.contiguous()
+    out = _cet_fake(se, num_experts)
+    _lib.call("tai_moe_compute_expert_tokens", _p(se), se.numel(), num_experts, _p(out), _stream(se))
+    return out
+
+
+_define("npu", "npu_moe_compute_expert_tokens(Tensor sorted_experts, int num_experts) -> Tensor", _cet_fake, _cet_cuda)
+
+
 # ============================================================================ npu_quant_matmul
 def _qmm_out_dtype(output_dtype) -> torch.dtype:
     code = scalar_type_code(output_dtype)

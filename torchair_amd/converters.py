@@ -117,3 +117,12 @@ register_fx_node_ge_converter(npu.npu_grouped_matmul_swiglu_quant_v2.default)(
     _identity(npu.npu_grouped_matmul_swiglu_quant_v2.default))
 register_fx_node_ge_converter(npu.npu_grouped_matmul_finalize_routing.default)(
     _identity(npu.npu_grouped_matmul_finalize_routing.default))
+
+# .../custom/npu_swiglu.py:4-14 (its declared cases)
+declare_supported([
+    Support(torch.empty(2, 2, dtype=torch.float32)),
+    Support(torch.empty(2, 2, dtype=torch.float16)),
+])(register_fx_node_ge_converter(npu.npu_swiglu.default)(_identity(npu.npu_swiglu.default)))
+# .../custom/npu_moe_compute_expert_tokens.py:4-11
+register_fx_node_ge_converter(npu.npu_moe_compute_expert_tokens.default)(
+    _identity(npu.npu_moe_compute_expert_tokens.default))

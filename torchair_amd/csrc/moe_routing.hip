@@ -989,3 +989,34 @@ extern "C" int tai_grouped_matmul_finalize_routing(const int8_t* x, const int8_t
   gfr_gather_kernel<<<dim3(static_cast<unsigned>(output_bs)), 256, 0, st>>>(a);
   return launch_status("tai_grouped_matmul_finalize_routing");
 }
+
+// ----------------------------------------------------------------------------- compute_expert_tokens
+// out[e] = the number of entries of the ascending `sorted` that are <= e (the end of expert e's rows),
+// one binary search per expert.
+namespace tai {
+namespace {
+__global__ __launch_bounds__(256) void expert_tokens_kernel(const int32_t* __restrict__ sorted, int64_t n,
+                                                            int64_t num_experts, int32_t* __restrict__ out) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= num_experts) return;
+  int64_t lo = 0, hi = n;  // first index with sorted[index] > e
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(sorted[mid]) <= e) lo = mid + 1; else hi = mid;
+  }
+  out[e] = static_cast<int32_t>(lo);
+}
+}  // namespace
+}  // namespace tai
+
+extern "C" int tai_moe_compute_expert_tokens(const int32_t* sorted_experts, int64_t n, int64_t num_experts,
+                                             int32_t* out, void* stream) {
+  TAI_CHECK_ARG(n >= 0 && n < (1ll << 31), "tai_moe_compute_expert_tokens: n must be in [0, 2^31)");
+  TAI_CHECK_ARG(num_experts > 0 && num_experts < 2147483647ll,
+                "tai_moe_compute_expert_tokens: num_experts must be in (0, 2^31 - 1)");
+  TAI_CHECK_ARG(out && (n == 0 || sorted_experts), "tai_moe_compute_expert_tokens: null pointer");
+  tai::expert_tokens_kernel<<<dim3(static_cast<unsigned>(cdiv(num_experts, 256))), 256, 0,
+                              static_cast<hipStream_t>(stream)>>>(sorted_experts, n, num_experts, out);
+  return launch_status("tai_moe_compute_expert_tokens");
+}
+

@@ -667,3 +667,36 @@ extern "C" int tai_dynamic_quant_v2(const void* x, int x_dtype, int64_t rows, in
   dq2_apply_kernel<<<grid, 256, 0, st>>>(a);
   return launch_status("tai_dynamic_quant_v2");
 }
+
+// ----------------------------------------------------------------------------- npu_swiglu
+// y = silu(a) * b with a, b the two halves of x along one dimension, viewed as [outer, 2 * n, inner]:
+// a = x[o, j, i], b = x[o, n + j, i] for j < n; fp32 arithmetic, one rounding to the output dtype.
+namespace tai {
+namespace {
+__global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ x, int dt, int64_t outer, int64_t n,
+                                                     int64_t inner, void* __restrict__ y) {
+  const int64_t total = outer * n * inner;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t i = idx % inner, j = (idx / inner) % n, o = idx / (inner * n);
+    const int64_t xa = (o * 2 * n + j) * inner + i;
+    const float a = load_as_f32(x, dt, xa), b = load_as_f32(x, dt, xa + n * inner);
+    store_from_f32(y, dt, idx, silu_f32(a) * b);
+  }
+}
+}  // namespace
+}  // namespace tai
+
+extern "C" int tai_swiglu(const void* x, int dtype, int64_t outer, int64_t n, int64_t inner, void* y, void* stream) {
+  TAI_CHECK_ARG(dtype == TAI_DT_BF16 || dtype == TAI_DT_FP16 || dtype == TAI_DT_FP32,
+                "tai_swiglu: dtype %d not supported (bf16, fp16, fp32)", dtype);
+  TAI_CHECK_ARG(outer >= 0 && n >= 0 && inner >= 0, "tai_swiglu: negative size");
+  const int64_t total = outer * n * inner;
+  if (total == 0) return TAI_OK;
+  TAI_CHECK_ARG(x && y, "tai_swiglu: null pointer");
+  const int64_t blocks = cdiv(total, 256) < 65536 ? cdiv(total, 256) : 65536;
+  swiglu_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(x, dtype, outer, n,
+                                                                                                   inner, y);
+  return launch_status("tai_swiglu");
+}
+
