@@ -1136,7 +1136,10 @@ bool cfg_available() {
 }
 
 // Grouped [K, N] weights with mixed tiles (grouped_tile_mixed): 128 x 512 (GrpKnSel) or 256 x 256.
-using MixTall = BigCfg<4, 2, 64, 4>;
+#ifndef TAI_MIX_TALL
+#define TAI_MIX_TALL BigCfg<4, 2, 64, 4>
+#endif
+using MixTall = TAI_MIX_TALL;
 #ifndef TAI_MIXED
 #define TAI_MIXED 1
 #endif
