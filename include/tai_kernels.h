@@ -525,6 +525,14 @@ typedef struct tai_fia_general_args {
   int64_t v_prefix_strides[2];
   const int64_t* prefix_len;
   int64_t prefix_cap;  /* rows the prefix tensors hold (prefix_len is clamped to it) */
+  /* packed sequences (the TND / NTD layouts, _npu_fused_infer_attention_score.py:171-180, 227-239;
+   * NULL: the batched layouts). q_cum: b cumulative query ends, sequence b owning packed query rows
+   * [q_cum[b-1], q_cum[b]) (from 0 for b = 0) of the s_q rows; query / out element (t, h) at
+   * t * strides[1] + h * strides[2] (strides[0] unused) and lse (t, h) at t * hq + h; rows past the
+   * last end write zeros and lse -inf. kv_cum (dense keys and values only, NULL: per-batch rows at
+   * strides[0]): the same for the s_kv packed key / value rows. */
+  const int64_t* q_cum;
+  const int64_t* kv_cum;
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 

@@ -624,6 +624,51 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
     return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask, pse=pse)
 
 
+def cum_to_lens(cum) -> np.ndarray:
+    """Per-sequence lengths of cumulative ends (the TND actual_seq_lengths convention)."""
+    c = np.concatenate([[0], np.asarray(cum, np.int64)])
+    return np.diff(c)
+
+
+def unpack_tnd(x, cum, smax: int):
+    """Packed rows [T, N, D] (TND; sequence b holds rows [cum[b-1], cum[b])) -> [B, smax, N, D], the rows
+    past each sequence's length zero. The TND / NTD query layouts of npu_fused_infer_attention_score
+    (python/torchair/ops/_npu_fused_infer_attention_score.py:171-180, 227-239, 300-327)."""
+    x = np.asarray(x)
+    lens = cum_to_lens(cum)
+    out = np.zeros((len(lens), smax) + x.shape[1:], x.dtype)
+    start = 0
+    for b, ln in enumerate(lens):
+        out[b, :ln] = x[start:start + ln]
+        start += ln
+    return out
+
+
+def pack_tnd(x, lens):
+    """The inverse of unpack_tnd: [B, S, N, D] with per-sequence lengths -> [sum(lens), N, D]."""
+    x = np.asarray(x)
+    return np.concatenate([x[b, :int(ln)] for b, ln in enumerate(lens)], axis=0)
+
+
+def packed_prefill_attention(q, k, v, cum_q, cum_kv, causal: int, scale: float, band=None, mask=None):
+    """npu_fused_infer_attention_score with packed TND queries, keys and values: q [Tq, Hq, D], k/v
+    [Tkv, Hkv, D]; actual_seq_lengths / actual_seq_lengths_kv are cumulative ends (torch_npu's TND
+    convention; the reference fixes only the TND shapes, _npu_fused_infer_attention_score.py:227-239 and
+    the lse [T, N, 1] of :319-327). Each sequence is attended as prefill_attention attends a batch row.
+    Returns (out fp32 [Tq, Hq, Dv], lse [Tq, Hq]); rows past the last end are zero (lse -inf)."""
+    lq, lk = cum_to_lens(cum_q), cum_to_lens(cum_kv)
+    sq, skv = max(int(lq.max(initial=0)), 1), max(int(lk.max(initial=0)), 1)
+    o, l = prefill_attention(unpack_tnd(q, cum_q, sq), unpack_tnd(k, cum_kv, skv), unpack_tnd(v, cum_kv, skv),
+                             lq, lk, causal, scale, band=band, mask=mask)
+    tq = np.asarray(q).shape[0]
+    out = np.zeros((tq,) + o.shape[2:], F32)
+    lse = np.full((tq, o.shape[2]), -np.inf, F32)
+    n = int(lq.sum())
+    out[:n] = pack_tnd(o, lq)
+    lse[:n] = pack_tnd(np.transpose(l, (0, 2, 1)), lq)
+    return out, lse
+
+
 def with_shared_prefix(k, v, seq_kv, k_prefix, v_prefix, prefix_len: int):
     """Shared prefix of npu_fused_infer_attention_score (key_shared_prefix / value_shared_prefix /
     actual_shared_prefix_len, prototype experiment_ops.h:3933-3935, passed on by the converter,

@@ -327,6 +327,25 @@ def test_paged_prefill_gather_and_decode_case():
     np.testing.assert_allclose(l1[:, :, 0], ld, rtol=1e-5)
 
 
+def test_packed_tnd_attention_is_per_sequence_attention():
+    # Each packed sequence attended alone (a batch of one, no length arguments) gives its rows; the
+    # padding rows past the last end are zero with lse -inf; pack and unpack are inverses.
+    lq, lk, hq, hkv, d = [3, 1, 5], [4, 7, 5], 4, 2, 8
+    cq, ck = np.cumsum(lq), np.cumsum(lk)
+    q = RNG.standard_normal((sum(lq) + 2, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((sum(lk), hkv, d)).astype(np.float32)
+    v = RNG.standard_normal((sum(lk), hkv, d)).astype(np.float32)
+    out, lse = G.packed_prefill_attention(q, k, v, cq, ck, 1, 0.4)
+    for b in range(3):
+        qs, ks = slice(cq[b] - lq[b], cq[b]), slice(ck[b] - lk[b], ck[b])
+        o, l = G.prefill_attention(q[None, qs], k[None, ks], v[None, ks], None, None, 1, 0.4)
+        np.testing.assert_allclose(out[qs], o[0], rtol=1e-6)
+        np.testing.assert_allclose(lse[qs], l[0].T, rtol=1e-6)
+    assert (out[sum(lq):] == 0).all() and np.isneginf(lse[sum(lq):]).all()
+    np.testing.assert_array_equal(G.pack_tnd(G.unpack_tnd(k, ck, 7), lk), k)
+    assert G.cum_to_lens([2, 2, 9]).tolist() == [2, 0, 7]
+
+
 def test_mla_equals_gqa_on_dequantised_latent():
     L = [7, 20]
     bs, dn, dr, h = 4, 16, 4, 3

@@ -186,7 +186,31 @@ def _strides_bshd(t: torch.Tensor, layout: str, heads: int):
         return [t.stride(0), t.stride(1), t.stride(2)]
     if layout == "BNSD":
         return [t.stride(0), t.stride(2), t.stride(1)]
+    if layout == "TND":  # packed rows: no batch stride
+        return [0, t.stride(0), t.stride(1)]
+    if layout == "NTD":
+        return [0, t.stride(1), t.stride(0)]
     raise RuntimeError(f"npu_fused_infer_attention_score: layout {layout} not supported for prefill")
+
+
+_PACKED = ("TND", "NTD")
+
+
+def _one_token_each(query, ql, ol, kw, b):
+    """A TND query of one token per sequence (T == B and actual_seq_lengths absent or the host list
+    1..B), which the one-token kernels serve as [B, N, D]."""
+    if ql != "TND" or ol != "TND" or query.size(0) != b:
+        return False
+    v = kw.get("actual_seq_lengths")
+    if v is None:
+        return True
+    return not isinstance(v, torch.Tensor) and [int(x) for x in v] == list(range(1, b + 1))
+
+
+def _max_run(cum: torch.Tensor) -> int:
+    """The longest sequence of cumulative ends (a host sync; explicit masks are sized against it)."""
+    c = [0] + cum.tolist()
+    return max([c[i + 1] - c[i] for i in range(len(c) - 1)] + [0])
 
 
 def fia_cuda(query, key, value, **kw):
@@ -238,9 +262,11 @@ def fia_cuda(query, key, value, **kw):
                "GQA/MHA, not MLA")
 
     if block_table is not None:
-        _check(ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql,
-               "npu_fused_infer_attention_score: paged attention supports BSH/BSND/BNSD/TND without layout change")
-        b = query.size(0)
+        packed = ql in _PACKED and not _one_token_each(query, ql, ol, kw, block_table.size(0))
+        _check(packed or (ql in ("BSH", "BSND", "BNSD", "TND") and ol == ql),
+               "npu_fused_infer_attention_score: paged attention supports BSH/BSND/BNSD/TND without layout change "
+               "(and packed TND/NTD queries)")
+        b = block_table.size(0) if packed else query.size(0)
         s = 1 if ql == "TND" else _bsnd(query, ql, num_heads)[1]
         _check(seq_kv is not None and seq_kv.numel() == b,
                "npu_fused_infer_attention_score: actual_seq_lengths_kv is required with block_table")
@@ -249,11 +275,12 @@ def fia_cuda(query, key, value, **kw):
         if kw.get("query_rope") is not None:
             whole_prefix = pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
             # (the one-token kernel steps through pages 32 tokens at a time; key is [blocks, bs, (1,) Dn])
-            if key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit and key.size(1) % 32 == 0:
+            if (key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit and key.size(1) % 32 == 0
+                    and not packed):
                 return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
             # several query tokens (MTP / speculative decode), bands and masks: the general kernel
             return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
-                                scale, mask_origin, pre, nxt, explicit, stream)
+                                scale, mask_origin, pre, nxt, explicit, stream, ol=ol)
         dt = _half_code(query, key, value, kv8)
         d = _value_d(block_table, value, query, ql, n_kv)
         if key.dim() == 3:
@@ -271,12 +298,11 @@ def fia_cuda(query, key, value, **kw):
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
         # the tiled kernels step through pages 32 tokens at a time
         if (explicit or kv8 or quant_out or pse is not None or bs % 32 != 0 or d not in (64, 128, 256)
-                or (s > 1 and d not in (64, 128))):
-            _check(ql != "TND", "npu_fused_infer_attention_score: the general path takes BSH/BSND/BNSD queries")
+                or (s > 1 and d not in (64, 128)) or packed):
             kstr = [sb, ss, sh]
             return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, kstr, kstr,
                                  bt, bs, seq_q, seq_kv, mask_origin, pre, nxt, explicit, kw, scale, stream,
-                                 kv8=kv8, quant_out=quant_out)
+                                 kv8=kv8, quant_out=quant_out, ol=ol)
         # one query token that the mask leaves the whole prefix: the decode kernel
         if s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0)):
             q = query.contiguous()
@@ -287,8 +313,6 @@ def fia_cuda(query, key, value, **kw):
                       lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
             return out, lse
         # query sequences over the paged cache (chunked prefill, multi-token decode)
-        _check(ql != "TND", "npu_fused_infer_attention_score: paged attention with several query tokens takes "
-                            "BSH/BSND/BNSD queries")
         b, s_q, hq, d = _bsnd(query, ql, num_heads)
         qs = _strides_bshd(query, ql, hq)
         os_ = _strides_bshd(out, ol, hq)
@@ -297,9 +321,18 @@ def fia_cuda(query, key, value, **kw):
                              kstr, os_, seq_q, seq_kv, mask_origin, pre, nxt, bt, bs, sb, sb, scale, stream)
 
     # ---------------------------------------------------------------- dense prefill
-    _check(ql in ("BSH", "BSND", "BNSD") and ol == ql,
-           "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change")
+    _check(ql in _PACKED or (ql in ("BSH", "BSND", "BNSD") and ol == ql),
+           "npu_fused_infer_attention_score: prefill supports BSH/BSND/BNSD without layout change, and packed "
+           "TND/NTD queries")
+    _check(kw.get("query_rope") is None, "npu_fused_infer_attention_score: MLA needs a paged latent cache (block_table)")
     dt = _half_code(query, key, value, kv8)
+    if ql in _PACKED:
+        _check(key.dim() == 3 and value.dim() == 3, "npu_fused_infer_attention_score: packed keys/values are "
+               f"[T, N, D] ({ql})")
+        d = _tnd(query, ql)[2]
+        return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt,
+                             _strides_bshd(key, ql, n_kv), _strides_bshd(value, ql, n_kv), None, 0, seq_q, seq_kv,
+                             mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=kv8, quant_out=quant_out, ol=ol)
     b, s_q, hq, d = _bsnd(query, ql, num_heads)
     if (explicit or kv8 or quant_out or pse is not None or d not in (64, 128)
             or _value_d(None, value, query, ql, n_kv) != d):
@@ -485,22 +518,59 @@ def _out_quant_params(a, kw, hq, dv, keep):
     a.out_offset = qo.data_ptr() if qo is not None else None
 
 
+def _packed_lens(a, ql, query, bt, seq_q, seq_kv):
+    """Packed TND / NTD queries: the sequences' query rows end at the cumulative actual_seq_lengths
+    (torch_npu's TND convention); dense keys/values are packed the same way (cumulative
+    actual_seq_lengths_kv), a paged cache takes per-sequence actual_seq_lengths_kv. Returns the
+    sequence count and the longest query and kv runs (host values, for explicit-mask checks)."""
+    _check(seq_q is not None, f"npu_fused_infer_attention_score: {ql} queries need actual_seq_lengths "
+           "(cumulative query ends)")
+    b = seq_q.numel()
+    _check(seq_kv is not None and seq_kv.numel() == b, f"npu_fused_infer_attention_score: {ql} needs "
+           "actual_seq_lengths_kv with one entry per sequence")
+    if bt is not None:
+        _check(bt.size(0) == b, "npu_fused_infer_attention_score: block_table must have a row per sequence")
+    a.q_cum, a.seq_lens_q = seq_q.data_ptr(), None
+    if bt is None:
+        a.kv_cum, a.seq_lens_kv = seq_kv.data_ptr(), None
+    return b
+
+
 def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, ks, vs, bt, bs, seq_q, seq_kv,
-                  mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=False, quant_out=False):
+                  mask_origin, pre, nxt, explicit, kw, scale, stream, kv8=False, quant_out=False, ol=None):
     """The general kernel for GQA/MHA: explicit masks, head dims the tiled kernels do not take, int8
-    key/value caches and int8 attention_out."""
-    b, s_q, hq, _ = _bsnd(query, ql, num_heads)
+    key/value caches, int8 attention_out and packed (TND / NTD) queries."""
+    ol = ol or ql
+    packed = ql in _PACKED
+    if packed:
+        _check(kw.get("pse_shift") is None and kw.get("key_shared_prefix") is None,
+               f"npu_fused_infer_attention_score: pse_shift and a shared prefix take batched layouts, not {ql}")
+        s_q, hq, _ = _tnd(query, ql)
+        b = seq_q.numel() if seq_q is not None else 0
+    else:
+        b, s_q, hq, _ = _bsnd(query, ql, num_heads)
     dv = _value_d(bt, value, query, ql, n_kv)
-    mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
-    s_kv = (bt.size(1) * bs) if bt is not None else (key.size(2) if ql == "BNSD" else key.size(1))
+    if bt is not None:
+        s_kv = bt.size(1) * bs
+    elif packed:
+        s_kv = key.size(0) if ql == "TND" else key.size(1)
+    else:
+        s_kv = key.size(2) if ql == "BNSD" else key.size(1)
     a = _general_args(dt, b, s_q, s_kv, hq, n_kv, d, 0, dv, query, _strides_bshd(query, ql, hq), None, None,
-                      key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale,
-                      out, _strides_bshd(out, ql, hq), lse if want_lse else None)
-    keep = []  # fp32 copies of the scales, alive until the launch is queued (stream-ordered frees)
+                      key, ks, None, None, value, vs, bt, bs, seq_q, seq_kv, None, None, mask_origin, pre, nxt, scale,
+                      out, _strides_bshd(out, ol, hq), lse if want_lse else None)
+    if packed:
+        b = _packed_lens(a, ql, query, bt, seq_q, seq_kv)
+    mask = None
+    if explicit:
+        mask, mst = _mask_bytes(kw["atten_mask"], b, _max_run(seq_q) if packed else s_q)
+        a.mask, a.mask_strides = mask.data_ptr(), _lib._I64x3(*mst)
+    keep = [mask]  # (and the fp32 copies of the scales) alive until the launch is queued (stream-ordered frees)
     # Masks and position shifts index keys in the concatenated [shared prefix, own keys] space.
     sp = _prefix_params(a, kw, ql, n_kv, d, dv, query, keep) if kw.get("key_shared_prefix") is not None else 0
     if mask is not None:
-        _check(mask.size(2) >= sp + (max(seq_kv.tolist()) if seq_kv is not None else s_kv),
+        kv_max = (_max_run(seq_kv) if packed and bt is None else max(seq_kv.tolist())) if seq_kv is not None else s_kv
+        _check(mask.size(2) >= sp + kv_max,
                "npu_fused_infer_attention_score: atten_mask covers fewer kv positions than the sequences hold")
     pse = kw.get("pse_shift")
     if pse is not None:
@@ -521,31 +591,44 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
 
 
 def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv, scale,
-                 mask_origin, pre, nxt, explicit, stream):
+                 mask_origin, pre, nxt, explicit, stream, ol=None):
     """MLA on the general kernel: key = [latent | key_rope], value = latent, one kv head. The latent is
     bf16 / fp16, or int8 with one fp32 scale per cache slot (key_antiquant_scale [blocks, bs],
     key_antiquant_mode 1, as for the one-token kernel), then dequantised as latent * scale."""
     q_rope, k_rope = kw["query_rope"], kw.get("key_rope")
     _check(k_rope is not None, "npu_fused_infer_attention_score: MLA needs key_rope")
     _check(n_kv == 1, "npu_fused_infer_attention_score: MLA latent cache has one kv head")
-    _check(ql in ("BSH", "BSND", "BNSD"), "npu_fused_infer_attention_score: MLA takes BSH/BSND/BNSD queries")
+    ol = ol or ql
+    packed = ql in _PACKED
+    _check(ql in ("BSH", "BSND", "BNSD") or packed, "npu_fused_infer_attention_score: MLA takes BSH/BSND/BNSD or "
+           "packed TND/NTD queries")
     kv8 = key.dtype == torch.int8
     dt = _half_code(query, key, value, kv8)
     _check(q_rope.dtype == query.dtype and k_rope.dtype == query.dtype,
            "npu_fused_infer_attention_score: MLA query_rope/key_rope must have the query's dtype")
-    b, s_q, hq, dn = _bsnd(query, ql, num_heads)
-    dr = _bsnd(q_rope, ql, num_heads)[3]
+    if packed:
+        s_q, hq, dn = _tnd(query, ql)
+        dr = _tnd(q_rope, ql)[2]
+        b = seq_q.numel() if seq_q is not None else 0
+    else:
+        b, s_q, hq, dn = _bsnd(query, ql, num_heads)
+        dr = _bsnd(q_rope, ql, num_heads)[3]
     nblk = key.size(0)
     kc = key.reshape(nblk, -1, dn)
     bs = kc.size(1)
     kr = k_rope.reshape(nblk, bs, dr)
     _check(kc.stride(-1) == 1 and kr.stride(-1) == 1, "npu_fused_infer_attention_score: caches need a dense last dim")
-    mask, mst = _mask_bytes(kw["atten_mask"], b, s_q) if explicit else (None, None)
     kst = [kc.stride(0), kc.stride(1), 0]
     a = _general_args(dt, b, s_q, bt.size(1) * bs, hq, 1, dn, dr, dn, query, _strides_bshd(query, ql, hq), q_rope,
                       _strides_bshd(q_rope, ql, hq), kc, kst, kr, [kr.stride(0), kr.stride(1), 0], kc, kst, bt, bs,
-                      seq_q, seq_kv, mask, mst, mask_origin, pre, nxt, scale, out, _strides_bshd(out, ql, hq),
+                      seq_q, seq_kv, None, None, mask_origin, pre, nxt, scale, out, _strides_bshd(out, ol, hq),
                       lse if want_lse else None)
+    if packed:
+        b = _packed_lens(a, ql, query, bt, seq_q, seq_kv)
+    mask = None
+    if explicit:
+        mask, mst = _mask_bytes(kw["atten_mask"], b, _max_run(seq_q) if packed else s_q)
+        a.mask, a.mask_strides = mask.data_ptr(), _lib._I64x3(*mst)
     ks = None
     if kv8:
         k_scale = kw.get("key_antiquant_scale")

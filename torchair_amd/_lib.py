@@ -38,7 +38,8 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("out_dtype", c_int64), ("out_scale", _P), ("out_offset", _P), ("out_scale_len", c_int64),
                 ("pse", _P), ("pse_strides", c_int64 * 4),
                 ("k_prefix", _P), ("v_prefix", _P), ("k_prefix_strides", c_int64 * 2),
-                ("v_prefix_strides", c_int64 * 2), ("prefix_len", _P), ("prefix_cap", c_int64)]
+                ("v_prefix_strides", c_int64 * 2), ("prefix_len", _P), ("prefix_cap", c_int64),
+                ("q_cum", _P), ("kv_cum", _P)]
 
 
 _SIGS = {

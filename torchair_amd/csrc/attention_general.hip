@@ -52,26 +52,59 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   // (b, h, i), i fastest; the launch's last workgroup may hold waves past the end, which run item 0
   // to the barrier and then stop
   const int64_t item0 = static_cast<int64_t>(blockIdx.x) * kGenWaves + w;
-  const bool in_range = item0 < a.b * a.hq * a.s_q;
+  const bool in_range = item0 < (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
   const int64_t item = in_range ? item0 : 0;
-  const int64_t i = item % a.s_q, h = (item / a.s_q) % a.hq, b = item / (a.s_q * a.hq);
+  // (qb, qt): the batch and row that address query, out and lse; (b, i): the sequence and the
+  // query's position in it. Batched layouts: qb = b, qt = i. Packed: qb = 0, qt = the packed row,
+  // and its sequence is found in q_cum (rows past the last end have lq = 0: zeros and lse -inf).
+  int64_t i = item % a.s_q, h = (item / a.s_q) % a.hq, b = item / (a.s_q * a.hq);
+  const int64_t qt = i, qb = a.q_cum ? 0 : b;
+  int64_t lq, kv_base = 0;
+  if (a.q_cum) {
+    int64_t lo = 0, hi = a.b;  // the first sequence whose end lies past qt
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (a.q_cum[mid] > qt) hi = mid; else lo = mid + 1;
+    }
+    if (lo < a.b) {
+      const int64_t end = imin64(a.q_cum[lo], a.s_q);
+      const int64_t start = lo ? imax64(0, imin64(a.q_cum[lo - 1], end)) : 0;
+      b = lo;
+      i = qt - start;
+      lq = end - start;
+    } else {
+      b = 0;
+      i = 0;
+      lq = 0;
+    }
+  } else {
+    lq = a.seq_lens_q ? imax64(0, imin64(a.seq_lens_q[b], a.s_q)) : a.s_q;
+  }
   const int kvh = static_cast<int>(h / (a.hq / a.hkv));
   // lengths read on the device are clamped to what the inputs hold (s_q; s_kv, or the blocks a
   // block-table row can address)
-  const int64_t lq = a.seq_lens_q ? imax64(0, imin64(a.seq_lens_q[b], a.s_q)) : a.s_q;
   int64_t kv_cap = a.block_table ? a.max_blocks * a.block_size : a.s_kv;
   // per-token antiquant scales hold tok_stride positions per sequence
   if (KV8 && (a.k_quant_mode == 1 || a.v_quant_mode == 1)) kv_cap = imin64(kv_cap, a.tok_stride);
-  const int64_t lk_own = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
+  int64_t lk_own;
+  if (a.kv_cum) {
+    const int64_t end = imax64(0, imin64(a.kv_cum[b], a.s_kv));
+    kv_base = b ? imax64(0, imin64(a.kv_cum[b - 1], end)) : 0;
+    lk_own = end - kv_base;
+  } else {
+    lk_own = a.seq_lens_kv ? imax64(0, imin64(a.seq_lens_kv[b], kv_cap)) : a.s_kv;
+  }
   // a shared prefix precedes every sequence's own keys: positions [0, lp) read the prefix tensors
   const int64_t lp = a.k_prefix ? imax64(0, imin64(a.prefix_len[0], a.prefix_cap)) : 0;
   const int64_t lk = lp + lk_own;
-  const int64_t o_off = b * a.out_strides[0] + i * a.out_strides[1] + h * a.out_strides[2];
+  // own key j of the sequence is row kv_base + j (packed) of batch b
+  const int64_t kb = kv_base - lp;
+  const int64_t o_off = qb * a.out_strides[0] + qt * a.out_strides[1] + h * a.out_strides[2];
   const int dk = a.dk1 + a.dk2;
   // the query as fp32 in this wave's LDS row
   {
-    const uint16_t* q1 = static_cast<const uint16_t*>(a.q1) + b * a.q1_strides[0] + i * a.q1_strides[1] + h * a.q1_strides[2];
-    const uint16_t* q2 = a.q2 ? static_cast<const uint16_t*>(a.q2) + b * a.q2_strides[0] + i * a.q2_strides[1] +
+    const uint16_t* q1 = static_cast<const uint16_t*>(a.q1) + qb * a.q1_strides[0] + qt * a.q1_strides[1] + h * a.q1_strides[2];
+    const uint16_t* q2 = a.q2 ? static_cast<const uint16_t*>(a.q2) + qb * a.q2_strides[0] + qt * a.q2_strides[1] +
                                     h * a.q2_strides[2]
                               : nullptr;
     for (int d = lane; d < dk; d += 64) qs[w][d] = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
@@ -97,7 +130,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     if (valid) {
       float acc = 0.0f;
       if constexpr (KV8) {
-        const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j, kvh);
+        const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j + kv_base, kvh);
         for (int d = 0; d < a.dk1; d += 8) {
           const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
           const uint32_t wd[2] = {u.x, u.y};
@@ -112,7 +145,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       } else {
         const uint16_t* kr = j < lp ? static_cast<const uint16_t*>(a.k_prefix) + j * a.k_prefix_strides[0] +
                                           kvh * a.k_prefix_strides[1]
-                                    : k1 + gen_row(a, a.k1_strides, b, j - lp, kvh);
+                                    : k1 + gen_row(a, a.k1_strides, b, j + kb, kvh);
         for (int d = 0; d < a.dk1; d += 8) {
           const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
           const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -124,7 +157,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         }
       }
       if (a.dk2) {
-        const uint16_t* kr2 = k2 + gen_row(a, a.k2_strides, b, j - lp, kvh);
+        const uint16_t* kr2 = k2 + gen_row(a, a.k2_strides, b, j + kb, kvh);
         for (int d = 0; d < a.dk2; ++d) acc += half_to_f32(kr2[d], f16) * qs[w][a.dk1 + d];
       }
       s = acc * a.scale;
@@ -146,7 +179,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       const float pj = __shfl(p, jj, 64);
       if (pj == 0.0f) continue;  // masked (wave-uniform)
       if constexpr (KV8) {
-        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj, kvh);
+        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kv_base, kvh);
 #pragma unroll
         for (int e = 0; e < kGenDvPerLane; ++e) {
           const int d = lane + 64 * e;
@@ -158,7 +191,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         const int64_t t = t0 + jj;
         const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
                                           kvh * a.v_prefix_strides[1]
-                                    : vv + gen_row(a, a.v_strides, b, t - lp, kvh);
+                                    : vv + gen_row(a, a.v_strides, b, t + kb, kvh);
 #pragma unroll
         for (int e = 0; e < kGenDvPerLane; ++e) {
           const int d = lane + 64 * e;
@@ -185,7 +218,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       }
     }
   }
-  if (a.lse && lane == 0 && i < a.s_q) a.lse[(b * a.hq + h) * a.s_q + i] = live ? m + logf(l) : -INFINITY;
+  if (a.lse && lane == 0)
+    a.lse[a.q_cum ? qt * a.hq + h : (b * a.hq + h) * a.s_q + i] = live ? m + logf(l) : -INFINITY;
 }
 
 }  // namespace
@@ -214,6 +248,10 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
                 static_cast<long long>(a.kv_dtype));
   TAI_CHECK_ARG(a.out_dtype == 0 || a.out_dtype == TAI_DT_INT8, "tai_fia_general: out_dtype %lld not supported (0 or "
                 "int8)", static_cast<long long>(a.out_dtype));
+  TAI_CHECK_ARG(a.kv_cum == nullptr || (a.q_cum && !a.block_table),
+                "tai_fia_general: packed keys (kv_cum) go with packed queries (q_cum) and dense keys");
+  TAI_CHECK_ARG(a.kv_cum == nullptr || !kv8 || (a.k_quant_mode == 0 && a.v_quant_mode == 0),
+                "tai_fia_general: packed int8 keys take per-channel antiquant scales");
   if (kv8) {
     TAI_CHECK_ARG(a.k_scale && a.v_scale, "tai_fia_general: int8 key / value need k_scale and v_scale");
     TAI_CHECK_ARG(a.k_quant_mode >= 0 && a.k_quant_mode <= 2 && a.v_quant_mode >= 0 && a.v_quant_mode <= 2,
@@ -240,7 +278,7 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
   constexpr int64_t kNoBound = int64_t(1) << 40;
   ga.a.pre_tokens = imin64(imax64(a.pre_tokens, -kNoBound), kNoBound);
   ga.a.next_tokens = imin64(imax64(a.next_tokens, -kNoBound), kNoBound);
-  const int64_t waves = a.b * a.hq * a.s_q;
+  const int64_t waves = (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
   const dim3 grid(static_cast<unsigned>(cdiv(waves, kGenWaves)));
   if (kv8) fia_general_kernel<true><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
   else fia_general_kernel<false><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
