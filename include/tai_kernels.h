@@ -518,7 +518,8 @@ typedef struct tai_fia_general_args {
    * value_shared_prefix / actual_shared_prefix_len): prefix_len[0] rows of k_prefix / v_prefix (query
    * dtype, element (t, kv head) at t * prefix_strides[0] + h * prefix_strides[1]) precede every
    * sequence's keys and values; a sequence then holds prefix_len + its own kv length positions, over
-   * which the masks apply. */
+   * which the masks apply. With an int8 cache the prefix stays in the query's dtype and the antiquant
+   * scales index the sequence's own positions. */
   const void* k_prefix;
   const void* v_prefix;
   int64_t k_prefix_strides[2];

@@ -297,3 +297,44 @@ def test_shared_prefix(layout, paged):
     got = out.cpu() if layout != "BNSD" else out.cpu().permute(0, 2, 1, 3)
     assert_close(f32np(got.reshape(b, sq, hq, d)), want)
     np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_shared_prefix_int8_cache(paged):
+    """A bf16 shared prefix ahead of int8 own keys/values: the prefix rows are read as they are, the
+    own rows dequantised with scales indexed by the sequence's own positions (per token on the paged
+    cache, per channel on the dense one)."""
+    g = torch.Generator().manual_seed(158)
+    b, sq, hq, hkv, d = 2, 3, 8, 2, 128
+    lq, lkv, sp, lp = [3, 1], [90, 17], 40, 33
+    kp = torch.randn(sp, hkv, d, generator=g).to(torch.bfloat16)
+    vp = torch.randn(sp, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b, sq, hq, d, generator=g).to(torch.bfloat16)
+    kw = dict(actual_seq_lengths=lq, actual_seq_lengths_kv=lkv, num_heads=hq, num_key_value_heads=hkv,
+              input_layout="BSH", scale=1 / math.sqrt(d), sparse_mode=3, softmax_lse_flag=True,
+              actual_shared_prefix_len=[lp], key_shared_prefix=kp.reshape(1, sp, hkv * d).to(DEV),
+              value_shared_prefix=vp.reshape(1, sp, hkv * d).to(DEV))
+    if paged:
+        bs = 32
+        kc, vc, bt = _paged(lkv, hkv, d, bs, g, lambda sh: _i8(sh, g))
+        smax = bt.shape[1] * bs
+        ks, vs = torch.rand(b, smax, generator=g) * 0.02 + 0.005, torch.rand(b, smax, generator=g) * 0.02 + 0.005
+        out, lse = FIA(q.reshape(b, sq, hq * d).to(DEV), kc.reshape(-1, bs, hkv * d).to(DEV),
+                       vc.reshape(-1, bs, hkv * d).to(DEV), block_table=bt.to(DEV), block_size=bs,
+                       key_antiquant_scale=ks.to(DEV), value_antiquant_scale=vs.to(DEV), key_antiquant_mode=1,
+                       value_antiquant_mode=1, **kw)
+        kd = G.antiquant_kv(_gather(kc.numpy(), bt, lkv, bs), ks.numpy(), None, 1)
+        vd = G.antiquant_kv(_gather(vc.numpy(), bt, lkv, bs), vs.numpy(), None, 1)
+    else:
+        skv = 90
+        k, v = _i8((b, skv, hkv, d), g), _i8((b, skv, hkv, d), g)
+        ks, vs = torch.rand(hkv * d, generator=g) * 0.02 + 0.005, torch.rand(hkv * d, generator=g) * 0.02 + 0.005
+        out, lse = FIA(q.reshape(b, sq, hq * d).to(DEV), k.reshape(b, skv, hkv * d).to(DEV),
+                       v.reshape(b, skv, hkv * d).to(DEV), key_antiquant_scale=ks.to(DEV),
+                       value_antiquant_scale=vs.to(DEV), **kw)
+        kd = G.antiquant_kv(k.numpy(), ks.numpy(), None, 0)
+        vd = G.antiquant_kv(v.numpy(), vs.numpy(), None, 0)
+    kk, vv, ll = G.with_shared_prefix(kd, vd, np.array(lkv), f32np(kp), f32np(vp), lp)
+    want, wl = G.prefill_attention(f32np(q), kk, vv, np.array(lq), ll, 1, 1 / math.sqrt(d))
+    assert_close(f32np(out.reshape(b, sq, hq, d)), want)
+    np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)

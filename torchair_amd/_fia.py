@@ -243,8 +243,8 @@ def fia_cuda(query, key, value, **kw):
     prefix = kw.get("key_shared_prefix") is not None
     _check(prefix == (kw.get("value_shared_prefix") is not None), "npu_fused_infer_attention_score: "
            "key_shared_prefix and value_shared_prefix come together")
-    _check(not prefix or (kw.get("query_rope") is None and not kv8), "npu_fused_infer_attention_score: a shared "
-           "prefix is served for GQA/MHA with a float cache")
+    _check(not prefix or kw.get("query_rope") is None, "npu_fused_infer_attention_score: a shared prefix is served "
+           "for GQA/MHA")
     _check(prefix or kw.get("actual_shared_prefix_len") is None, "npu_fused_infer_attention_score: "
            "actual_shared_prefix_len needs key_shared_prefix")
     pse = pse if pse is not None else (True if prefix else None)  # both take the general kernel

@@ -129,8 +129,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     float s = -INFINITY;
     if (valid) {
       float acc = 0.0f;
-      if constexpr (KV8) {
-        const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j + kv_base, kvh);
+      // int8 own keys (shared-prefix rows, j < lp, stay in the query's dtype)
+      if (KV8 && j >= lp) {
+        const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j + kb, kvh);
         for (int d = 0; d < a.dk1; d += 8) {
           const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
           const uint32_t wd[2] = {u.x, u.y};
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
           for (int q = 0; q < 8; ++q) {
             const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
             acc += antiquant(x, a.k_scale, a.k_offset,
-                             antiquant_index(a, a.k_quant_mode, b, j, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
+                             antiquant_index(a, a.k_quant_mode, b, j - lp, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
                    qs[w][d + q];
           }
         }
@@ -178,14 +179,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     for (int jj = 0; jj < nj; ++jj) {
       const float pj = __shfl(p, jj, 64);
       if (pj == 0.0f) continue;  // masked (wave-uniform)
-      if constexpr (KV8) {
-        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kv_base, kvh);
+      if (KV8 && t0 + jj >= lp) {
+        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kb, kvh);
 #pragma unroll
         for (int e = 0; e < kGenDvPerLane; ++e) {
           const int d = lane + 64 * e;
           if (d < a.dv)
             o[e] += pj * antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
-                                   antiquant_index(a, a.v_quant_mode, b, t0 + jj, static_cast<int64_t>(kvh) * a.dv + d));
+                                   antiquant_index(a, a.v_quant_mode, b, t0 + jj - lp, static_cast<int64_t>(kvh) * a.dv + d));
         }
       } else {
         const int64_t t = t0 + jj;
@@ -261,8 +262,8 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
     TAI_CHECK_ARG((a.k_quant_mode != 1 && a.v_quant_mode != 1) || a.tok_stride > 0,
                   "tai_fia_general: per-token scales need tok_stride > 0");
   }
-  TAI_CHECK_ARG(a.k_prefix == nullptr || (a.v_prefix && a.prefix_len && !kv8 && a.dk2 == 0),
-                "tai_fia_general: a shared prefix needs v_prefix and prefix_len, a float cache and one key part");
+  TAI_CHECK_ARG(a.k_prefix == nullptr || (a.v_prefix && a.prefix_len && a.dk2 == 0),
+                "tai_fia_general: a shared prefix needs v_prefix and prefix_len and one key part");
   TAI_CHECK_ARG(a.k_prefix == nullptr || ((reinterpret_cast<uintptr_t>(a.k_prefix) % 16) == 0 &&
                                           a.k_prefix_strides[0] % 8 == 0 && a.k_prefix_strides[1] % 8 == 0),
                 "tai_fia_general: shared-prefix key rows must be 16-byte aligned");
