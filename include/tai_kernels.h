@@ -534,6 +534,16 @@ typedef struct tai_fia_general_args {
    * strides[0]): the same for the s_kv packed key / value rows. */
   const int64_t* q_cum;
   const int64_t* kv_cum;
+  /* int8 query (q_dtype = TAI_DT_INT8; 0 = the dtype's): query, key and value are int8 (kv_dtype int8,
+   * no antiquant scales, one key part) and dtype names the output (fp16 / bf16). One fp32 each:
+   * S = (float(q.k) * deq_scale1[0]) * scale; m, l = max S, sum exp(S - m);
+   * P8 = clamp(rint(exp(S - m) * quant_scale1[0]), 0, 127); O = (float(P8.V) * deq_scale2[0]) / l,
+   * both products exact int32 sums. Replaces dequant_scale1 / quant_scale1 / dequant_scale2 of
+   * ge.FusedInferAttentionScore (experiment_ops.h:3888-3890). */
+  int64_t q_dtype;
+  const float* deq_scale1;
+  const float* quant_scale1;
+  const float* deq_scale2;
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 

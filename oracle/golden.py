@@ -733,6 +733,49 @@ def quant_attention_out(out, scale2, offset2=None):
     return np.clip(np.rint(y.astype(F32)), -128, 127).astype(np.int8)
 
 
+def quant_query_attention(q, k, v, dequant_scale1: float, quant_scale1: float, dequant_scale2: float, seq_q, seq_kv,
+                          band, scale: float, mask=None):
+    """npu_fused_infer_attention_score with an int8 query, key and value (dequant_scale1, quant_scale1,
+    dequant_scale2; prototype experiment_ops.h:3878-3912 types them UINT64 / fp32 / UINT64, an fp32 in
+    the low 32 bits of each UINT64; the reference fixes no formula, so this convention is parity
+    unpinned beyond the checks of its tests):
+      S = (float(int32 q.k) * dequant_scale1) * scale over the visible keys (band / mask as in
+          prefill_attention), m = max S, l = sum exp(S - m) in fp32;
+      P8 = clamp(rint(exp(S - m) * quant_scale1), 0, 127) (int8, the query-side quantisation of P);
+      O = (float(int32 P8.V) * dequant_scale2) / l.
+    q [B, Sq, Hq, D], k/v [B, Skv, Hkv, D] int8; returns (out fp32 [B, Sq, Hq, D], lse [B, Hq, Sq] of S)."""
+    q, k, v = (np.asarray(t, np.int64) for t in (q, k, v))
+    b_cnt, sq, hq, d = q.shape
+    skv, hkv, dv = k.shape[1], k.shape[2], v.shape[3]
+    g = hq // hkv
+    out = np.zeros((b_cnt, sq, hq, dv), F32)
+    lse = np.full((b_cnt, hq, sq), -np.inf, F32)
+    for bi in range(b_cnt):
+        lq = sq if seq_q is None else int(seq_q[bi])
+        lk = skv if seq_kv is None else int(seq_kv[bi])
+        vis = band_mask(lq, lk, *band)
+        if mask is not None:
+            mb = np.asarray(mask)
+            vis = vis & (mb[0 if mb.shape[0] == 1 else bi, :lq, :lk] == 0)
+        for h in range(hq):
+            dot = q[bi, :lq, h] @ k[bi, :lk, h // g].T                      # exact int32 values
+            s = ((dot.astype(F32) * F32(dequant_scale1)).astype(F32) * F32(scale)).astype(F32)
+            s = np.where(vis, s, -np.inf)
+            m = s.max(axis=1, keepdims=True) if lk else np.full((lq, 1), -np.inf, F32)
+            live = np.isfinite(m[:, 0])
+            ms = np.where(np.isfinite(m), m, 0).astype(F32)
+            p = np.where(vis, np.exp((s - ms).astype(F32)), 0).astype(F32)
+            l = p.sum(axis=1, dtype=F32)
+            p8 = np.clip(np.rint((p * F32(quant_scale1)).astype(F32)), 0, 127).astype(np.int64)
+            acc = p8 @ v[bi, :lk, h // g]                                   # exact int32 values
+            o = (acc.astype(F32) * F32(dequant_scale2)).astype(F32)
+            with np.errstate(invalid="ignore", divide="ignore"):
+                o = np.where(live[:, None] & (l[:, None] > 0), o / np.where(l > 0, l, 1)[:, None], 0).astype(F32)
+                lse[bi, h, :lq] = np.where(live, ms[:, 0] + np.log(np.where(l > 0, l, 1)), -np.inf)
+            out[bi, :lq, h] = o
+    return out, lse
+
+
 def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_lens, scale: float):
     """npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache.
 

@@ -338,3 +338,62 @@ def test_shared_prefix_int8_cache(paged):
     want, wl = G.prefill_attention(f32np(q), kk, vv, np.array(lq), ll, 1, 1 / math.sqrt(d))
     assert_close(f32np(out.reshape(b, sq, hq, d)), want)
     np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+def _u64(x):
+    """An fp32 value in the low 32 bits of a UINT64 tensor (the prototype's dequant_scale format)."""
+    return torch.tensor([int(np.array([x], np.float32).view(np.uint32)[0])], dtype=torch.int64)
+
+
+@pytest.mark.parametrize("paged,scale_form,out8", [(False, "f32", False), (False, "u64", True), (True, "u64", False)])
+def test_int8_query(paged, scale_form, out8):
+    """An int8 query, key and value with dequant_scale1 / quant_scale1 / dequant_scale2 (per tensor; the
+    dequant scales as fp32 or as UINT64 carrying an fp32): the oracle's two-pass convention, fp16 out
+    (or int8 with quant_scale2). Tolerance: a P8 that rounds the other way between the device's and
+    numpy's exp moves an output by at most 127 * dequant_scale2 / l <= 0.0127, hence atol 2e-2."""
+    g = torch.Generator().manual_seed(159)
+    b, sq, hq, hkv, d = 2, 4, 8, 2, 128
+    lq, lkv = [4, 1], ([300, 77] if paged else [96, 50])
+    d1, q1, d2 = 4e-4, 127.0, 1e-4
+    q = _i8((b, sq, hq, d), g)
+    kw = dict(actual_seq_lengths=lq, actual_seq_lengths_kv=lkv, num_heads=hq, num_key_value_heads=hkv,
+              input_layout="BSH", scale=1 / math.sqrt(d), sparse_mode=3, softmax_lse_flag=True,
+              quant_scale1=torch.tensor([q1], device=DEV))
+    if scale_form == "u64":
+        kw.update(dequant_scale1=_u64(d1).to(DEV), dequant_scale2=_u64(d2).to(DEV))
+    else:
+        kw.update(dequant_scale1=torch.tensor([d1], device=DEV), dequant_scale2=torch.tensor([d2], device=DEV))
+    if out8:
+        kw["quant_scale2"] = torch.tensor([50.0], device=DEV)
+    if paged:
+        bs = 64
+        kc, vc, bt = _paged(lkv, hkv, d, bs, g, lambda sh: _i8(sh, g))
+        out, lse = FIA(q.reshape(b, sq, hq * d).to(DEV), kc.reshape(-1, bs, hkv * d).to(DEV),
+                       vc.reshape(-1, bs, hkv * d).to(DEV), block_table=bt.to(DEV), block_size=bs, **kw)
+        kd, vd = _gather(kc.numpy(), bt, lkv, bs), _gather(vc.numpy(), bt, lkv, bs)
+    else:
+        skv = 96
+        k, v = _i8((b, skv, hkv, d), g), _i8((b, skv, hkv, d), g)
+        out, lse = FIA(q.reshape(b, sq, hq * d).to(DEV), k.reshape(b, skv, hkv * d).to(DEV),
+                       v.reshape(b, skv, hkv * d).to(DEV), **kw)
+        kd, vd = k.numpy(), v.numpy()
+    want, wl = G.quant_query_attention(q.numpy(), kd, vd, d1, q1, d2, lq, lkv, (1, 2147483647, 0), 1 / math.sqrt(d))
+    if out8:
+        assert out.dtype == torch.int8
+        got = out.reshape(b, sq, hq, d).cpu().numpy().astype(np.int32)
+        exp8 = G.quant_attention_out(want, [50.0]).astype(np.int32)
+        assert np.abs(got - exp8).max() <= 1
+    else:
+        assert out.dtype == torch.float16
+        assert_close(f32np(out.reshape(b, sq, hq, d)), want, atol=2e-2)
+    np.testing.assert_allclose(_lse(lse, b, hq, sq), np.where(np.isfinite(wl), wl, -1e30), rtol=1e-3, atol=1e-3)
+
+
+def test_int8_query_argument_errors():
+    q = torch.zeros(1, 1, 128, dtype=torch.int8, device=DEV)
+    one = torch.ones(1, device=DEV)
+    with pytest.raises(RuntimeError, match="dequant_scale1"):
+        FIA(q, q, q, num_heads=1, dequant_scale1=one)
+    x = torch.zeros(1, 1, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="int8 query"):
+        FIA(x, x, x, num_heads=1, dequant_scale1=one, quant_scale1=one, dequant_scale2=one)

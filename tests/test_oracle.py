@@ -618,3 +618,35 @@ def test_moe_compute_expert_tokens_brute_force():
         got = G.moe_compute_expert_tokens(se, e)
         want = np.array([(se <= k).sum() for k in range(e)], np.int32)
         np.testing.assert_array_equal(got, want)
+
+
+def test_quant_query_attention_pins():
+    # (1) one visible key: P = 1, P8 = rint(quant_scale1), O = P8 * v * dequant_scale2 exactly
+    q = RNG.integers(-128, 128, (1, 3, 2, 16))
+    k = RNG.integers(-128, 128, (1, 5, 1, 16))
+    v = RNG.integers(-128, 128, (1, 5, 1, 16))
+    big = 2147483647
+    out, _ = G.quant_query_attention(q, k, v, 0.01, 100.0, 0.5, None, None, (0, 0, 0), 0.3)  # diagonal band
+    for i in range(3):
+        np.testing.assert_array_equal(out[0, i], np.broadcast_to(100 * v[0, i, 0] * 0.5, (2, 16)).astype(np.float32))
+    # (2) against float attention: with quant_scale1 = 127 each P8 is within 0.5 of 127 * P, so
+    #     O / (127 * dequant_scale2) differs from softmax attention by at most 0.5 * sum|v| / (127 * l)
+    q = RNG.integers(-128, 128, (2, 6, 4, 32))
+    k = RNG.integers(-128, 128, (2, 9, 2, 32))
+    v = RNG.integers(-128, 128, (2, 9, 2, 32))
+    d1, d2, sc = 1e-4, 0.02, 1 / math.sqrt(32)
+    out, lse = G.quant_query_attention(q, k, v, d1, 127.0, d2, [6, 4], [9, 7], (1, big, 0), sc)
+    ref, rl = G.prefill_attention((q * d1).astype(np.float32), k.astype(np.float32), v.astype(np.float32), [6, 4],
+                                  [9, 7], 1, sc)
+    bound = 0.5 * np.abs(v).sum(axis=1).max() / 127 + 1e-3
+    assert np.abs(out / (127 * d2) - ref).max() <= bound
+    assert np.abs(out / (127 * d2) - ref).max() > 0  # P really is quantised
+    np.testing.assert_allclose(np.where(np.isfinite(lse), lse, 0), np.where(np.isfinite(rl), rl, 0), rtol=1e-5, atol=1e-5)
+    # (3) identical value rows c: O = c * dequant_scale2 * sum(P8) / l
+    vc = np.broadcast_to(RNG.integers(-128, 128, (1, 1, 1, 32)), (1, 9, 1, 32))
+    out, _ = G.quant_query_attention(q[:1, :, :2], k[:1, :, :1], vc, d1, 90.0, d2, None, None, (0, big, big), sc)
+    s = ((q[0, :, :2].astype(np.int64) @ k[0, :, 0].T.astype(np.int64)).astype(np.float32) * np.float32(d1)) * np.float32(sc)
+    p = np.exp(s - s.max(-1, keepdims=True)).astype(np.float32)
+    p8 = np.clip(np.rint(p * np.float32(90.0)), 0, 127)
+    want = vc[0, 0, 0][None, None] * d2 * (p8.sum(-1) / p.sum(-1))[..., None]
+    np.testing.assert_allclose(out[0], want, rtol=1e-5)

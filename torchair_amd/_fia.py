@@ -138,8 +138,8 @@ def fia_fake(query, key, value, **kw):
     return out, lse
 
 
-_UNSUPPORTED = ("dequant_scale1", "quant_scale1", "dequant_scale2", "query_padding_size",
-                "kv_padding_size", "key_rope_antiquant_scale")
+_UNSUPPORTED = ("query_padding_size", "kv_padding_size", "key_rope_antiquant_scale")
+_QQ_SCALES = ("dequant_scale1", "quant_scale1", "dequant_scale2")
 
 
 def _lens_tensor(v, device) -> Optional[torch.Tensor]:
@@ -237,6 +237,16 @@ def fia_cuda(query, key, value, **kw):
     # int8 key / value caches (GQA / MHA) and int8 attention_out take the general kernel
     quant_out = kw.get("quant_scale2") is not None
     kv8 = key.dtype == torch.int8 and kw.get("query_rope") is None
+    qq = query.dtype == torch.int8
+    _check(qq == all(kw.get(n) is not None for n in _QQ_SCALES) and (qq or all(kw.get(n) is None for n in _QQ_SCALES)),
+           "npu_fused_infer_attention_score: an int8 query takes dequant_scale1, quant_scale1 and dequant_scale2 "
+           "(and they apply to an int8 query only)")
+    if qq:
+        _check(kw.get("query_rope") is None and kw.get("pse_shift") is None and kw.get("key_shared_prefix") is None
+               and all(kw.get(n) is None for n in ("key_antiquant_scale", "key_antiquant_offset", "value_antiquant_scale",
+                                                  "value_antiquant_offset", "antiquant_scale", "antiquant_offset")),
+               "npu_fused_infer_attention_score: an int8 query is served for GQA/MHA without antiquant scales, pse_shift "
+               "or a shared prefix")
     pse = kw.get("pse_shift")
     _check(pse is None or kw.get("query_rope") is None, "npu_fused_infer_attention_score: pse_shift is served for "
            "GQA/MHA, not MLA")
@@ -503,6 +513,15 @@ def _prefix_params(a, kw, ql, n_kv, dk, dv, query, keep) -> int:
     return sp
 
 
+def _one_scale(t, name):
+    """One fp32 scale on the device from a float tensor or a UINT64 one carrying an fp32 in its low 32
+    bits (the prototype types dequant_scale1 / dequant_scale2 UINT64, experiment_ops.h:3888-3890)."""
+    _check(t.numel() == 1, f"npu_fused_infer_attention_score: {name} holds one (per-tensor) value")
+    if t.dtype in (torch.int64, torch.uint64):
+        t = t.reshape(1).contiguous().view(torch.int32)[0:1].view(torch.float32)
+    return t.to(torch.float32).reshape(1).contiguous()
+
+
 def _out_quant_params(a, kw, hq, dv, keep):
     """int8 attention_out: clamp(rint(o * quant_scale2 + quant_offset2)), per tensor (1 entry) or per
     channel (Hq * Dv entries, channel h * Dv + d) (experiment_ops.h:3943)."""
@@ -580,7 +599,14 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
         a.pse = pse.data_ptr()
         a.pse_strides = (ctypes.c_int64 * 4)(0 if pse.size(0) == 1 else pse.stride(0), pse.stride(1), pse.stride(2),
                                              pse.stride(3))
-    if kv8:
+    if query.dtype == torch.int8:
+        a.kv_dtype, a.q_dtype = _lib.DT_INT8, _lib.DT_INT8
+        for attr, name in (("deq_scale1", "dequant_scale1"), ("quant_scale1", "quant_scale1"),
+                           ("deq_scale2", "dequant_scale2")):
+            t = _one_scale(kw[name], name)
+            keep.append(t)
+            setattr(a, attr, t.data_ptr())
+    elif kv8:
         _check(key.dtype == torch.int8 and value.dtype == torch.int8,
                "npu_fused_infer_attention_score: int8 key needs an int8 value")
         _antiquant_params(a, kw, b, n_kv, d, dv, keep)
@@ -646,6 +672,10 @@ def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv,
 def _half_code(query, key, value, kv8=False) -> int:
     """ScalarType code of the attention element type: bf16 or fp16, the same for query, key and value
     (kv8: int8 key and value caches beside a bf16 / fp16 query)."""
+    if query.dtype == torch.int8:  # the meta rule: an int8 query gives an fp16 attention_out
+        _check(key.dtype == torch.int8 and value.dtype == torch.int8,
+               "npu_fused_infer_attention_score: an int8 query takes an int8 key and value")
+        return DT_FP16
     if kv8:
         _check(query.dtype in (torch.bfloat16, torch.float16) and value.dtype == torch.int8,
                "npu_fused_infer_attention_score: int8 key/value take a bf16 or fp16 query and an int8 value")

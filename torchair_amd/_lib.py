@@ -39,7 +39,8 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("pse", _P), ("pse_strides", c_int64 * 4),
                 ("k_prefix", _P), ("v_prefix", _P), ("k_prefix_strides", c_int64 * 2),
                 ("v_prefix_strides", c_int64 * 2), ("prefix_len", _P), ("prefix_cap", c_int64),
-                ("q_cum", _P), ("kv_cum", _P)]
+                ("q_cum", _P), ("kv_cum", _P), ("q_dtype", c_int64), ("deq_scale1", _P), ("quant_scale1", _P),
+                ("deq_scale2", _P)]
 
 
 _SIGS = {

@@ -107,7 +107,13 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     const uint16_t* q2 = a.q2 ? static_cast<const uint16_t*>(a.q2) + qb * a.q2_strides[0] + qt * a.q2_strides[1] +
                                     h * a.q2_strides[2]
                               : nullptr;
-    for (int d = lane; d < dk; d += 64) qs[w][d] = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
+    if (KV8 && a.q_dtype == TAI_DT_INT8) {
+      const int8_t* q8 = static_cast<const int8_t*>(a.q1) + qb * a.q1_strides[0] + qt * a.q1_strides[1] +
+                         h * a.q1_strides[2];
+      for (int d = lane; d < dk; d += 64) qs[w][d] = static_cast<float>(q8[d]);
+    } else {
+      for (int d = lane; d < dk; d += 64) qs[w][d] = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
+    }
   }
   __syncthreads();  // (each wave reads only its own row; the barrier orders the LDS writes)
   if (!in_range) return;
@@ -122,6 +128,58 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const uint16_t* k1 = static_cast<const uint16_t*>(a.k1);
   const uint16_t* k2 = static_cast<const uint16_t*>(a.k2);
   const uint16_t* vv = static_cast<const uint16_t*>(a.v);
+  if (KV8 && a.q_dtype == TAI_DT_INT8) {
+    // int8 query, key and value: two passes over the visible keys, the first for the row max and sum,
+    // the second quantising P against the final max (so the result does not depend on the chunking) and
+    // accumulating P8.V exactly in int32. Each score's q.k sum is of integer products below 2^24 in
+    // magnitude, exact in fp32 in any order.
+    auto score = [&](int64_t j, bool& valid) -> float {
+      valid = j < hi;
+      if (valid && a.mask) valid = a.mask[b * a.mask_strides[0] + i * a.mask_strides[1] + j * a.mask_strides[2]] == 0;
+      if (!valid) return -INFINITY;
+      const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j + kb, kvh);
+      float acc = 0.0f;
+      for (int d = 0; d < a.dk1; d += 8) {
+        const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
+        const uint32_t wd[2] = {u.x, u.y};
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          acc += static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu)) * qs[w][d + q];
+      }
+      return __fmul_rn(__fmul_rn(acc, a.deq_scale1[0]), a.scale);
+    };
+    for (int64_t t0 = lo; t0 < hi; t0 += 64) {
+      bool valid;
+      const float s = score(t0 + lane, valid);
+      const float mc = wave_max(s);
+      if (mc == -INFINITY) continue;
+      const float m_new = fmaxf(m, mc);
+      l = l * (m == -INFINITY ? 0.0f : expf(m - m_new)) + wave_sum(valid ? expf(s - m_new) : 0.0f);
+      m = m_new;
+    }
+    int32_t oi[kGenDvPerLane];
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) oi[e] = 0;
+    const float qs1 = a.quant_scale1[0];
+    for (int64_t t0 = lo; t0 < hi && m != -INFINITY; t0 += 64) {
+      bool valid;
+      const float s = score(t0 + lane, valid);
+      const int p8 = valid ? static_cast<int>(fminf(fmaxf(rintf(__fmul_rn(expf(s - m), qs1)), 0.0f), 127.0f)) : 0;
+      const int64_t nj = imin64(64, hi - t0);
+      for (int jj = 0; jj < nj; ++jj) {
+        const int pj = __shfl(p8, jj, 64);
+        if (pj == 0) continue;  // masked or rounded to zero (wave-uniform)
+        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kb, kvh);
+#pragma unroll
+        for (int e = 0; e < kGenDvPerLane; ++e) {
+          const int d = lane + 64 * e;
+          if (d < a.dv) oi[e] += pj * static_cast<int32_t>(vr[d]);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) o[e] = __fmul_rn(static_cast<float>(oi[e]), a.deq_scale2[0]);
+  } else
   for (int64_t t0 = lo; t0 < hi; t0 += 64) {
     const int64_t j = t0 + lane;
     bool valid = j < hi;
@@ -249,12 +307,19 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
                 static_cast<long long>(a.kv_dtype));
   TAI_CHECK_ARG(a.out_dtype == 0 || a.out_dtype == TAI_DT_INT8, "tai_fia_general: out_dtype %lld not supported (0 or "
                 "int8)", static_cast<long long>(a.out_dtype));
+  const bool qq = a.q_dtype == TAI_DT_INT8;
+  TAI_CHECK_ARG(a.q_dtype == 0 || qq, "tai_fia_general: q_dtype %lld not supported (0 or int8)",
+                static_cast<long long>(a.q_dtype));
+  TAI_CHECK_ARG(!qq || (kv8 && a.deq_scale1 && a.quant_scale1 && a.deq_scale2 && !a.k_scale && !a.v_scale &&
+                        a.dk2 == 0 && !a.k_prefix && !a.pse),
+                "tai_fia_general: an int8 query needs int8 key / value without antiquant scales, the three "
+                "scales, one key part, no shared prefix and no pse");
   TAI_CHECK_ARG(a.kv_cum == nullptr || (a.q_cum && !a.block_table),
                 "tai_fia_general: packed keys (kv_cum) go with packed queries (q_cum) and dense keys");
   TAI_CHECK_ARG(a.kv_cum == nullptr || !kv8 || (a.k_quant_mode == 0 && a.v_quant_mode == 0),
                 "tai_fia_general: packed int8 keys take per-channel antiquant scales");
   if (kv8) {
-    TAI_CHECK_ARG(a.k_scale && a.v_scale, "tai_fia_general: int8 key / value need k_scale and v_scale");
+    TAI_CHECK_ARG(qq || (a.k_scale && a.v_scale), "tai_fia_general: int8 key / value need k_scale and v_scale");
     TAI_CHECK_ARG(a.k_quant_mode >= 0 && a.k_quant_mode <= 2 && a.v_quant_mode >= 0 && a.v_quant_mode <= 2,
                   "tai_fia_general: antiquant modes must be 0 (per channel), 1 (per token) or 2 (per cache slot)");
     TAI_CHECK_ARG((a.k_quant_mode != 2 && a.v_quant_mode != 2) || a.block_table,
