@@ -147,3 +147,36 @@ def test_swiglu_packed_weight_layout_and_cache():
     y3, _ = npu.npu_grouped_matmul_swiglu_quant_v2(xd, [wd], [wsd], xsd, cd, group_list_type=1)
     wy, _ = G.grouped_matmul_swiglu_quant(x.numpy(), wd.cpu().numpy(), ws.numpy(), xs.numpy(), cnt.numpy(), 1)
     assert_int8_close(y3.cpu().numpy(), wy)
+
+
+@pytest.mark.parametrize("bias_kind,smooth_kind", [("int32", "per_group"), ("fp32", "shared"), (None, "per_group"),
+                                                   ("int32", None)])
+def test_swiglu_quant_v2_smooth_scale_and_bias(bias_kind, smooth_kind):
+    """smooth_scale and bias: the grouped GEMM's int32 accumulators, then dequant_swiglu_quant with the
+    bias (int32 before, fp32 after the dequantisation) and the smooth scale as its quant_scale."""
+    g = gen(13)
+    counts, k, n = [7, 0, 130, 33], 256, 512
+    e = len(counts)
+    x, w, ws, xs, cnt = _case(g, counts, k, n, int(sum(counts)) + 2)
+    kw = {}
+    bias = sm = None
+    if bias_kind == "int32":
+        bias = torch.randint(-5000, 5000, (e, n), generator=g, dtype=torch.int32)
+    elif bias_kind == "fp32":
+        bias = uniform((e, n), g, -0.5, 0.5)
+    if smooth_kind == "per_group":
+        sm = uniform((e, n // 2), g, 0.5, 2.0)
+    elif smooth_kind == "shared":
+        sm = uniform((n // 2,), g, 0.5, 2.0)
+    if bias is not None:
+        kw["bias"] = bias.to(DEV)
+    if sm is not None:
+        kw["smooth_scale"] = sm.to(DEV)
+    y, s = npu.npu_grouped_matmul_swiglu_quant_v2(x.to(DEV), [w.to(DEV)], [ws.to(DEV)], xs.to(DEV),
+                                                  torch.cumsum(cnt, 0).to(DEV), group_list_type=0, **kw)
+    acc = G.grouped_matmul(x.numpy(), w.numpy(), cnt.numpy(), 1, out_dtype="int32")
+    smn = None if sm is None else np.broadcast_to(sm.numpy().reshape(-1, n // 2), (e, n // 2))
+    wy, wsc = G.dequant_swiglu_quant(acc, ws.numpy(), xs.numpy(), None if bias is None else bias.numpy(), smn,
+                                     cnt.numpy(), activate_left=True)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)

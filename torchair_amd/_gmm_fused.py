@@ -79,8 +79,7 @@ def _gsq_cuda(x, weight, weight_scale, x_scale, group_list, *, smooth_scale=None
     name = "npu_grouped_matmul_swiglu_quant_v2"
     _on_gpu(x, x_scale, *weight, *weight_scale)
     _check(len(weight) == 1 and len(weight_scale) == 1, f"{name}: one stacked weight and weight_scale are supported")
-    _check(smooth_scale is None and bias is None and not weight_assist_matrix,
-           f"{name}: smooth_scale, bias and weight_assist_matrix are not supported")
+    _check(not weight_assist_matrix, f"{name}: weight_assist_matrix is not supported")
     _check(dequant_mode in (None, 0) and quant_mode in (None, 0) and quant_dtype in (None, 1),
            f"{name}: only dequant_mode 0 with per-token int8 quantisation (quant_mode 0, quant_dtype 1) is supported")
     _check(x_dtype is None and weight_dtype is None and weight_scale_dtype is None and x_scale_dtype is None,
@@ -100,6 +99,8 @@ def _gsq_cuda(x, weight, weight_scale, x_scale, group_list, *, smooth_scale=None
     m = x.shape[0]
     _check(xs.numel() == m, f"{name}: x_scale must have M entries")
     gl = _group_list(name, group_list, e, x.device)
+    if smooth_scale is not None or bias is not None:
+        return _gsq_composed(name, x, weight[0], ws, xs, gl, group_list_type, smooth_scale, bias, e, n)
     y, ys = _gsq_fake(x, weight, weight_scale, x_scale, group_list)
     if m == 0:
         return y, ys
@@ -109,6 +110,31 @@ def _gsq_cuda(x, weight, weight_scale, x_scale, group_list, *, smooth_scale=None
     _lib.call("tai_grouped_matmul_swiglu_quant", _p(xc), _p(wl), m, k, n, e, layout, _p(gl), int(group_list_type),
               _p(ws), _p(xs), _p(y), _p(ys), _p(wsp), nbytes, _stream(xc))
     return y, ys
+
+
+def _gsq_composed(name, x, weight, ws, xs, gl, group_list_type, smooth_scale, bias, e, n):
+    """smooth_scale and bias run the op as its two halves, both on the GPU kernels: the int32 grouped
+    GEMM (npu_grouped_matmul) and npu_dequant_swiglu_quant with activate_left, dynamic quantisation,
+    the bias (int32 added to the accumulators before the dequantisation, fp32 after it; [E, N]) and the
+    smooth scale as its quant_scale (h * smooth_scale[group] before the per-row quantisation;
+    [E, N/2] or [N/2] shared by the groups). The GE op takes both inputs
+    (grouped_matmul_swiglu_quant_v2.py:146-161) without fixing their arithmetic; this is the fold's
+    reading of them."""
+    if smooth_scale is not None:
+        sm = smooth_scale.to(torch.float32)
+        _check(sm.numel() in (n // 2, e * n // 2), f"{name}: smooth_scale must be [E, N/2] or [N/2]")
+        sm = sm.reshape(-1, n // 2).expand(e, n // 2).contiguous()
+    else:
+        sm = None
+    if bias is not None:
+        _check(bias.numel() == e * n and bias.dtype in (torch.int32, torch.float32, torch.float16, torch.bfloat16),
+               f"{name}: bias must be [E, N] int32 or float")
+        bias = bias.reshape(e, n)
+    acc = torch.ops.npu.npu_grouped_matmul([x], [weight], group_list=gl, split_item=3, group_type=0,
+                                           group_list_type=group_list_type, output_dtype=torch.int32)[0]
+    counts = gl if group_list_type == 1 else torch.diff(gl, prepend=gl.new_zeros(1))
+    return torch.ops.npu.npu_dequant_swiglu_quant(acc, weight_scale=ws.reshape(e, n), activation_scale=xs, bias=bias,
+                                                  quant_scale=sm, group_index=counts, activate_left=True, quant_mode=1)
 
 
 _define("npu", "npu_grouped_matmul_swiglu_quant_v2(Tensor x, Tensor[] weight, Tensor[] weight_scale, Tensor x_scale, "
