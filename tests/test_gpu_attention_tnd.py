@@ -177,3 +177,30 @@ def test_packed_layout_errors():
     with pytest.raises(RuntimeError, match="pse_shift"):
         FIA(q, q, q, num_heads=2, input_layout="TND", actual_seq_lengths=[4], actual_seq_lengths_kv=[4],
             pse_shift=torch.zeros(1, 2, 4, 4, dtype=torch.bfloat16, device=DEV))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_dense_packed_random_shapes(seed):
+    """Seeded random packed batches: 1-6 sequences (empty ones included), GQA ratios, head dims 64-256
+    and the band / causal modes, against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    g = torch.Generator().manual_seed(1000 + seed)
+    b = int(rng.integers(1, 7))
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 4]))
+    d = int(rng.choice([64, 96, 128, 256]))
+    lq = rng.integers(0, 40, b).tolist()
+    lk = [int(x + rng.integers(0, 30)) for x in lq]
+    mode = int(rng.choice([0, 2, 3, 4]))
+    pre, nxt = int(rng.integers(1, 20)), int(rng.integers(0, 5))
+    kw = dict(sparse_mode=mode)
+    if mode in (0, 4):
+        kw.update(pre_tokens=pre, next_tokens=nxt)
+    band = {0: (0, pre, nxt), 2: (0, 2147483647, 0), 3: (1, 2147483647, 0), 4: (1, pre, nxt)}[mode]
+    q, k, v = _packed_inputs(g, lq, lk, hq, hkv, d, pad=int(rng.integers(0, 3)))
+    cq, ck = np.cumsum(lq).tolist(), np.cumsum(lk).tolist()
+    out, lse = FIA(q.to(DEV), k.to(DEV), v.to(DEV), actual_seq_lengths=cq, actual_seq_lengths_kv=ck, num_heads=hq,
+                   num_key_value_heads=hkv, input_layout="TND", scale=1 / math.sqrt(d), softmax_lse_flag=True, **kw)
+    want, wl = G.packed_prefill_attention(f32np(q), f32np(k), f32np(v), cq, ck, 0, 1 / math.sqrt(d), band=band)
+    assert_close(f32np(out), want)
+    np.testing.assert_allclose(_lse_np(lse.cpu().numpy()[..., 0]), _lse_np(wl), rtol=1e-3, atol=1e-3)
