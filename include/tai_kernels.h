@@ -546,6 +546,9 @@ typedef struct tai_fia_general_args {
   const float* deq_scale2;
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
+/* sizeof(tai_fia_general_args) as compiled into the library (no counterpart in the reference): a
+ * binding that mirrors the struct (ctypes, cffi, JNI) checks its own layout against it at load. */
+size_t tai_fia_general_args_size(void);
 
 /* ---------------------------------------------------------------------------------------
  * npu_fused_infer_attention_score, MLA absorbed decode with an int8 latent cache

@@ -28,6 +28,8 @@ def test_library_exports_every_header_symbol():
         assert hasattr(lib, s), f"{s} missing from libtai_kernels.so"
     assert set(syms) == set(_lib.exported_symbols())
     assert lib.tai_abi_version() == 1
+    # the ctypes mirror of the attention argument struct has the library's size
+    assert lib.tai_fia_general_args_size() == __import__("ctypes").sizeof(_lib.FiaGeneralArgs)
 
 
 def test_library_build_id_matches_sources_and_stale_library_is_refused():

@@ -122,6 +122,7 @@ _SIGS = {
         c_int, [_P, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int, c_int, c_float, _P, c_int, _P, c_int, c_int64,
                 c_int64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tai_fia_general": (c_int, [ctypes.POINTER(FiaGeneralArgs), _P]),
+    "tai_fia_general_args_size": (c_size_t, []),
     "tai_fia_mla_decode_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int]),
     "tai_fia_mla_decode": (
         c_int, [_P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_float, _P, _P, _P,
@@ -153,6 +154,10 @@ def load() -> ctypes.CDLL:
                 fn.restype = res
                 fn.argtypes = args
             _check_fresh(lib)
+            if lib.tai_fia_general_args_size() != ctypes.sizeof(FiaGeneralArgs):
+                raise RuntimeError(
+                    f"{LIB_PATH}: tai_fia_general_args is {lib.tai_fia_general_args_size()} bytes in the library, "
+                    f"{ctypes.sizeof(FiaGeneralArgs)} in _lib.FiaGeneralArgs; the two layouts differ")
             _lib = lib
     return _lib
 

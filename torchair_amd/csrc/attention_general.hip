@@ -286,6 +286,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
 
 using namespace tai;
 
+extern "C" size_t tai_fia_general_args_size(void) { return sizeof(tai_fia_general_args); }
+
 extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
   TAI_CHECK_ARG(args != nullptr, "tai_fia_general: null arguments");
   const tai_fia_general_args& a = *args;
