@@ -373,3 +373,29 @@ def test_pattern_pass_fuses_routing_into_grouped_matmul_on_cpu():
 
     gm2 = torch.fx.symbolic_trace(rows_also_used)
     assert fuse_routing_grouped_matmul(gm2) == 0
+
+
+def test_fia_dense_key_value_shapes_are_checked_before_launch():
+    """Keys/values with fewer heads, another head dim or another batch than the query and
+    num_key_value_heads declare are refused on the host (the kernels trust these sizes)."""
+    from torchair_amd._fia import _dense_kv_check
+    q = torch.zeros(2, 5, 8 * 64)
+    good = torch.zeros(2, 7, 2 * 64)
+    _dense_kv_check(q, good, good, "BSH", 8, 2)
+    # too few heads, another batch, fewer value positions
+    for k, v in ((torch.zeros(2, 7, 64), good), (torch.zeros(1, 7, 128), good), (good, torch.zeros(2, 6, 128))):
+        with pytest.raises(RuntimeError):
+            _dense_kv_check(q, k, v, "BSH", 8, 2)
+    qn = torch.zeros(2, 8, 5, 64)
+    _dense_kv_check(qn, torch.zeros(2, 2, 7, 64), torch.zeros(2, 2, 7, 64), "BNSD", 8, 2)
+    with pytest.raises(RuntimeError):
+        _dense_kv_check(qn, torch.zeros(2, 1, 7, 64), torch.zeros(2, 1, 7, 64), "BNSD", 8, 2)
+    with pytest.raises(RuntimeError):
+        _dense_kv_check(qn, torch.zeros(2, 2, 7, 32), torch.zeros(2, 2, 7, 64), "BNSD", 8, 2)
+    qt = torch.zeros(9, 8, 64)
+    _dense_kv_check(qt, torch.zeros(11, 2, 64), torch.zeros(11, 2, 64), "TND", 8, 2)
+    _dense_kv_check(torch.zeros(8, 9, 64), torch.zeros(2, 11, 64), torch.zeros(2, 11, 64), "NTD", 8, 2)
+    with pytest.raises(RuntimeError):
+        _dense_kv_check(qt, torch.zeros(11, 1, 64), torch.zeros(11, 1, 64), "TND", 8, 2)
+    with pytest.raises(RuntimeError):
+        _dense_kv_check(qt, torch.zeros(11, 2, 64), torch.zeros(10, 2, 64), "TND", 8, 2)

@@ -336,9 +336,8 @@ def fia_cuda(query, key, value, **kw):
            "TND/NTD queries")
     _check(kw.get("query_rope") is None, "npu_fused_infer_attention_score: MLA needs a paged latent cache (block_table)")
     dt = _half_code(query, key, value, kv8)
+    _dense_kv_check(query, key, value, ql, num_heads, n_kv)
     if ql in _PACKED:
-        _check(key.dim() == 3 and value.dim() == 3, "npu_fused_infer_attention_score: packed keys/values are "
-               f"[T, N, D] ({ql})")
         d = _tnd(query, ql)[2]
         return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt,
                              _strides_bshd(key, ql, n_kv), _strides_bshd(value, ql, n_kv), None, 0, seq_q, seq_kv,
@@ -535,6 +534,32 @@ def _out_quant_params(a, kw, hq, dv, keep):
     keep.append(qs)
     a.out_dtype, a.out_scale, a.out_scale_len = _lib.DT_INT8, qs.data_ptr(), qs.numel()
     a.out_offset = qo.data_ptr() if qo is not None else None
+
+
+def _dense_kv_check(query, key, value, ql, num_heads, n_kv):
+    """Dense keys and values must hold what the kernels read: the query's batch, num_key_value_heads
+    heads, the query's head dim for the key, and the same positions in both."""
+    name = "npu_fused_infer_attention_score"
+    if ql in _PACKED:
+        _, _, dk = _tnd(query, ql)
+        _check(key.dim() == 3 and value.dim() == 3, f"{name}: packed keys/values are [T, N, D] ({ql})")
+        n_ax, t_ax = (1, 0) if ql == "TND" else (0, 1)
+        _check(key.size(n_ax) == n_kv and value.size(n_ax) == n_kv and key.size(2) == dk,
+               f"{name}: {ql} keys/values need {n_kv} heads and the key the query's head dim {dk}")
+        _check(value.size(t_ax) == key.size(t_ax), f"{name}: keys and values hold different token counts")
+        return
+    b, _, _, dk = _bsnd(query, ql, num_heads)
+    _check(key.dim() == query.dim() and value.dim() == query.dim() and key.size(0) == b and value.size(0) == b,
+           f"{name}: keys/values must have the query's layout and batch {b}")
+    dv = _value_d(None, value, query, ql, n_kv)
+    if ql == "BSH":
+        ok = key.size(2) == n_kv * dk and value.size(2) == n_kv * dv and value.size(1) == key.size(1)
+    elif ql == "BSND":
+        ok = key.shape[2:] == (n_kv, dk) and value.size(2) == n_kv and value.size(1) == key.size(1)
+    else:  # BNSD
+        ok = key.size(1) == n_kv and key.size(3) == dk and value.size(1) == n_kv and value.size(2) == key.size(2)
+    _check(ok, f"{name}: {ql} keys/values need {n_kv} heads of the query's head dim {dk} (key) and matching "
+           "positions")
 
 
 def _packed_lens(a, ql, query, bt, seq_q, seq_kv):
