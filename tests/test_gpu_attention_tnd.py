@@ -204,3 +204,47 @@ def test_dense_packed_random_shapes(seed):
     want, wl = G.packed_prefill_attention(f32np(q), f32np(k), f32np(v), cq, ck, 0, 1 / math.sqrt(d), band=band)
     assert_close(f32np(out), want)
     np.testing.assert_allclose(_lse_np(lse.cpu().numpy()[..., 0]), _lse_np(wl), rtol=1e-3, atol=1e-3)
+
+
+def test_packed_int8_kv_and_int8_out():
+    """Packed queries over int8 keys/values (per-channel scales) with an int8 attention_out."""
+    g = torch.Generator().manual_seed(175)
+    lq, lk, hq, hkv, d = [5, 0, 12], [9, 3, 12], 8, 2, 128
+    tq, tk = sum(lq), sum(lk)
+    q = torch.randn(tq, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randint(-128, 128, (tk, hkv, d), generator=g, dtype=torch.int8)
+    v = torch.randint(-128, 128, (tk, hkv, d), generator=g, dtype=torch.int8)
+    ks, vs = torch.rand(hkv * d, generator=g) * 0.02 + 0.005, torch.rand(hkv * d, generator=g) * 0.02 + 0.005
+    cq, ck = np.cumsum(lq).tolist(), np.cumsum(lk).tolist()
+    out, _ = FIA(q.to(DEV), k.to(DEV), v.to(DEV), actual_seq_lengths=cq, actual_seq_lengths_kv=ck, num_heads=hq,
+                 num_key_value_heads=hkv, input_layout="TND", scale=1 / math.sqrt(d), sparse_mode=3,
+                 key_antiquant_scale=ks.to(DEV), value_antiquant_scale=vs.to(DEV),
+                 quant_scale2=torch.tensor([40.0], device=DEV))
+    kd = G.antiquant_kv(k.numpy()[None], ks.numpy(), None, 0)[0]
+    vd = G.antiquant_kv(v.numpy()[None], vs.numpy(), None, 0)[0]
+    want, _ = G.packed_prefill_attention(f32np(q), kd, vd, cq, ck, 1, 1 / math.sqrt(d))
+    assert out.dtype == torch.int8 and out.shape == (tq, hq, d)
+    exp8 = G.quant_attention_out(want[:, None], [40.0])[:, 0].astype(np.int32)
+    assert np.abs(out.cpu().numpy().astype(np.int32) - exp8).max() <= 1
+
+
+def test_packed_int8_query():
+    """Packed int8 queries, keys and values with the three query-quant scales."""
+    g = torch.Generator().manual_seed(176)
+    lq, lk, hq, hkv, d = [3, 7], [20, 9], 4, 1, 64
+    tq, tk = sum(lq), sum(lk)
+    q = torch.randint(-128, 128, (tq, hq, d), generator=g, dtype=torch.int8)
+    k = torch.randint(-128, 128, (tk, hkv, d), generator=g, dtype=torch.int8)
+    v = torch.randint(-128, 128, (tk, hkv, d), generator=g, dtype=torch.int8)
+    cq, ck = np.cumsum(lq).tolist(), np.cumsum(lk).tolist()
+    d1, q1, d2 = 5e-4, 127.0, 1e-4
+    out, _ = FIA(q.to(DEV), k.to(DEV), v.to(DEV), actual_seq_lengths=cq, actual_seq_lengths_kv=ck, num_heads=hq,
+                 num_key_value_heads=hkv, input_layout="TND", scale=1 / math.sqrt(d), sparse_mode=3,
+                 dequant_scale1=torch.tensor([d1], device=DEV), quant_scale1=torch.tensor([q1], device=DEV),
+                 dequant_scale2=torch.tensor([d2], device=DEV))
+    want, _ = G.quant_query_attention(G.unpack_tnd(q.numpy(), cq, max(lq)), G.unpack_tnd(k.numpy(), ck, max(lk)),
+                                      G.unpack_tnd(v.numpy(), ck, max(lk)), d1, q1, d2, lq, lk, (1, 2147483647, 0),
+                                      1 / math.sqrt(d))
+    assert out.dtype == torch.float16
+    # atol: one P8 rounding the other way between the device's and numpy's exp (see test_int8_query)
+    assert_close(f32np(out), G.pack_tnd(want, lq), atol=2e-2)
