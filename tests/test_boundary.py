@@ -399,3 +399,24 @@ def test_fia_dense_key_value_shapes_are_checked_before_launch():
         _dense_kv_check(qt, torch.zeros(11, 1, 64), torch.zeros(11, 1, 64), "TND", 8, 2)
     with pytest.raises(RuntimeError):
         _dense_kv_check(qt, torch.zeros(11, 2, 64), torch.zeros(10, 2, 64), "TND", 8, 2)
+
+
+def test_fia_host_helpers_for_packed_layouts_and_quant_scales():
+    """Host logic of the packed layouts and the int8 query, without a GPU: which TND calls keep the
+    one-token kernels, the longest run of cumulative ends, and UINT64 scales carrying an fp32 in their
+    low 32 bits."""
+    from torchair_amd._fia import _max_run, _one_scale, _one_token_each
+    q = torch.zeros(4, 2, 64)
+    assert _one_token_each(q, "TND", "TND", {}, 4)
+    assert _one_token_each(q, "TND", "TND", {"actual_seq_lengths": [1, 2, 3, 4]}, 4)
+    assert not _one_token_each(q, "TND", "TND", {"actual_seq_lengths": [1, 2, 4, 4]}, 4)
+    assert not _one_token_each(q, "TND", "TND", {"actual_seq_lengths": torch.arange(1, 5)}, 4)  # device values
+    assert not _one_token_each(q, "TND", "NTD", {}, 4) and not _one_token_each(q, "TND", "TND", {}, 3)
+    assert _max_run(torch.tensor([3, 3, 10, 12])) == 7 and _max_run(torch.tensor([], dtype=torch.int64)) == 0
+    f = np.float32(0.0123)
+    bits = int(np.array([f]).view(np.uint32)[0]) | (5 << 40)  # high bits are not part of the scale
+    for t in (torch.tensor([bits], dtype=torch.int64), torch.tensor([0.0123], dtype=torch.float32)):
+        got = _one_scale(t, "dequant_scale1")
+        assert got.dtype == torch.float32 and got.numel() == 1 and got.item() == float(f)
+    with pytest.raises(RuntimeError, match="one"):
+        _one_scale(torch.ones(2), "quant_scale1")
