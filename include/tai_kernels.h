@@ -544,6 +544,10 @@ typedef struct tai_fia_general_args {
   const float* deq_scale1;
   const float* quant_scale1;
   const float* deq_scale2;
+  /* learnable_sink (NULL: none; experiment_ops.h:3940): one fp32 logit per query head, in the domain of
+   * the scaled scores, that joins the softmax denominator without a value row: softmax over
+   * [scores, sink] with the sink's column dropped. Not with the int8 query. */
+  const float* sink;
 } tai_fia_general_args;
 int tai_fia_general(const tai_fia_general_args* args, void* stream);
 /* sizeof(tai_fia_general_args) as compiled into the library (no counterpart in the reference): a

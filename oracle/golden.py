@@ -491,18 +491,23 @@ def moe_finalize_routing(expanded, skip1, skip2, bias, scales, src_to_dst, exper
 
 # ----------------------------------------------------------------------------- attention
 def _softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, mask: Optional[np.ndarray] = None,
-                    bias: Optional[np.ndarray] = None):
+                    bias: Optional[np.ndarray] = None, sink: Optional[float] = None):
     """q [n, d], k [L, d], v [L, dv] -> (out [n, dv], lse [n]); fp32, masked entries excluded; bias [n, L]
-    (pse_shift) is added to the scaled scores."""
+    (pse_shift) is added to the scaled scores; sink (learnable_sink, one logit) joins the softmax's
+    denominator and contributes no value: softmax over [scores, sink] with the sink's column dropped."""
     s = (q.astype(F32) @ k.astype(F32).T) * F32(scale)
     if bias is not None:
         s = (s + np.asarray(bias, F32)).astype(F32)
     if mask is not None:
         s = np.where(mask, s, -np.inf)
     m = np.max(s, axis=1, keepdims=True) if s.shape[1] else np.full((s.shape[0], 1), -np.inf, F32)
+    if sink is not None:
+        m = np.maximum(m, F32(sink))
     m_safe = np.where(np.isfinite(m), m, 0).astype(F32)
     p = np.exp(s - m_safe)
     den = np.sum(p, axis=1, keepdims=True)
+    if sink is not None:
+        den = (den + np.exp(F32(sink) - m_safe)).astype(F32)
     with np.errstate(invalid="ignore", divide="ignore"):
         o = np.where(den > 0, (p @ v.astype(F32)) / np.where(den > 0, den, 1), 0).astype(F32)
         lse = np.where(den[:, 0] > 0, m_safe[:, 0] + np.log(np.where(den[:, 0] > 0, den[:, 0], 1)), -np.inf)
@@ -557,7 +562,7 @@ def band_mask(lq: int, lk: int, origin: int, pre: int, nxt: int) -> np.ndarray:
     return ok
 
 
-def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None, mask=None, pse=None):
+def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=None, mask=None, pse=None, sink=None):
     """npu_fused_infer_attention_score, dense prefill. q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D].
 
     causal 1 (sparse_mode 3, right-down): query i sees kv j <= i + (Lkv - Lq); causal 2
@@ -567,7 +572,8 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=No
     rest. pse: pse_shift [B or 1, Hq, >= Sq, >= Skv], added to the scaled scores before the softmax,
     softmax(scale * q.k + pse) (the converter passes pse_type 0, .../custom/fused_infer_attention_score.py:
     94-109; the formula is the one of the public operator documentation, unpinned by the reference beyond
-    the reduction pse = 0 -> no pse). Rows at or past Lq are zero.
+    the reduction pse = 0 -> no pse). sink: learnable_sink [Hq] (one logit per query head in the scaled-score
+    domain, _softmax_attend's rule). Rows at or past Lq are zero.
     Returns (out fp32 [B,Sq,Hq,D], lse [B,Hq,Sq]).
     """
     q = np.asarray(q, F32)
@@ -598,14 +604,15 @@ def prefill_attention(q, k, v, seq_q, seq_kv, causal: int, scale: float, band=No
                 pb = np.asarray(pse, F32)
                 bias = pb[0 if pb.shape[0] == 1 else b, h, :lq, :lk]
             o, l = _softmax_attend(q[b, :lq, h], np.asarray(k[b, :lk, h // g], F32),
-                                   np.asarray(v[b, :lk, h // g], F32), scale, vis, bias)
+                                   np.asarray(v[b, :lk, h // g], F32), scale, vis, bias,
+                                   None if sink is None else float(np.asarray(sink, F32)[h]))
             out[b, :lq, h] = o
             lse[b, h, :lq] = l
     return out, lse
 
 
 def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, band, scale: float, mask=None,
-                            pse=None):
+                            pse=None, sink=None):
     """npu_fused_infer_attention_score with a block table and several query tokens per sequence
     (chunked prefill / multi-token decode). q [B,Sq,Hq,D]; caches [blocks, bs, Hkv, D]; token t of
     sequence b at cache[block_table[b, t // bs], t % bs] (the paged rule of paged_decode_attention);
@@ -621,7 +628,7 @@ def paged_prefill_attention(q, k_cache, v_cache, block_table, seq_q, seq_kv, ban
         pages = np.asarray(block_table[b][: (L + bs - 1) // bs], np.int64)
         k[b, :L] = np.asarray(k_cache[pages], F32).reshape(-1, hkv, d)[:L]
         v[b, :L] = np.asarray(v_cache[pages], F32).reshape(-1, hkv, d)[:L]
-    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask, pse=pse)
+    return prefill_attention(q, k, v, seq_q, seq_kv, 0, scale, band=band, mask=mask, pse=pse, sink=sink)
 
 
 def cum_to_lens(cum) -> np.ndarray:
@@ -650,7 +657,7 @@ def pack_tnd(x, lens):
     return np.concatenate([x[b, :int(ln)] for b, ln in enumerate(lens)], axis=0)
 
 
-def packed_prefill_attention(q, k, v, cum_q, cum_kv, causal: int, scale: float, band=None, mask=None):
+def packed_prefill_attention(q, k, v, cum_q, cum_kv, causal: int, scale: float, band=None, mask=None, sink=None):
     """npu_fused_infer_attention_score with packed TND queries, keys and values: q [Tq, Hq, D], k/v
     [Tkv, Hkv, D]; actual_seq_lengths / actual_seq_lengths_kv are cumulative ends (torch_npu's TND
     convention; the reference fixes only the TND shapes, _npu_fused_infer_attention_score.py:227-239 and
@@ -659,7 +666,7 @@ def packed_prefill_attention(q, k, v, cum_q, cum_kv, causal: int, scale: float, 
     lq, lk = cum_to_lens(cum_q), cum_to_lens(cum_kv)
     sq, skv = max(int(lq.max(initial=0)), 1), max(int(lk.max(initial=0)), 1)
     o, l = prefill_attention(unpack_tnd(q, cum_q, sq), unpack_tnd(k, cum_kv, skv), unpack_tnd(v, cum_kv, skv),
-                             lq, lk, causal, scale, band=band, mask=mask)
+                             lq, lk, causal, scale, band=band, mask=mask, sink=sink)
     tq = np.asarray(q).shape[0]
     out = np.zeros((tq,) + o.shape[2:], F32)
     lse = np.full((tq, o.shape[2]), -np.inf, F32)
@@ -807,7 +814,7 @@ def mla_decode_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq
     return out, lse
 
 
-def mla_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_q, seq_kv, band, scale: float):
+def mla_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_q, seq_kv, band, scale: float, sink=None):
     """MLA over a paged latent cache with several query tokens per sequence (MTP / speculative
     decode): the arguments of mla_decode_attention with q_nope [B,Sq,H,Dn], q_rope [B,Sq,H,Dr] and
     band = (origin, pre, next) as in band_mask; ckv_scale None for a bf16 / fp16 latent. Query i of
@@ -833,7 +840,7 @@ def mla_attention(q_nope, q_rope, ckv, ckv_scale, krope, block_table, seq_q, seq
         vis = band_mask(lq, L, *band)
         for hh in range(h):
             qk = np.concatenate([qn[b, :lq, hh], qr[b, :lq, hh]], axis=1)
-            o, l = _softmax_attend(qk, kk, c, scale, vis)
+            o, l = _softmax_attend(qk, kk, c, scale, vis, sink=None if sink is None else float(sink[hh]))
             out[b, :lq, hh] = o
             lse[b, hh, :lq] = l
     return out, lse

@@ -650,3 +650,27 @@ def test_quant_query_attention_pins():
     p8 = np.clip(np.rint(p * np.float32(90.0)), 0, 127)
     want = vc[0, 0, 0][None, None] * d2 * (p8.sum(-1) / p.sum(-1))[..., None]
     np.testing.assert_allclose(out[0], want, rtol=1e-5)
+
+
+def test_learnable_sink_is_a_key_with_a_zero_value():
+    # One query per batch row: a sink logit equals one more key, scored exactly that logit, whose value
+    # row is zero; a sink at -inf is no sink.
+    q = RNG.standard_normal((2, 1, 2, 8)).astype(np.float32)
+    k = RNG.standard_normal((2, 5, 1, 8)).astype(np.float32)
+    v = RNG.standard_normal((2, 5, 1, 8)).astype(np.float32)
+    sink = np.array([0.7, -1.3], np.float32)
+    out, lse = G.prefill_attention(q, k, v, None, None, 0, 0.5, sink=sink)
+    for b in range(2):
+        for h in range(2):
+            qv = q[b, 0, h].astype(np.float64)
+            kx = (qv * sink[h] / (0.5 * (qv @ qv)))[None]  # q . kx * 0.5 == sink[h]
+            kk = np.concatenate([k[b, :, 0], kx.astype(np.float32)])
+            vv = np.concatenate([v[b, :, 0], np.zeros((1, 8), np.float32)])
+            o2, l2 = G.prefill_attention(q[b:b + 1, :, h:h + 1], kk[None, :, None], vv[None, :, None], None, None, 0,
+                                         0.5)
+            np.testing.assert_allclose(out[b, 0, h], o2[0, 0, 0], rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(lse[b, h, 0], l2[0, 0, 0], rtol=1e-5)
+    o3, l3 = G.prefill_attention(q, k, v, None, None, 0, 0.5, sink=np.full(2, -np.inf, np.float32))
+    o4, l4 = G.prefill_attention(q, k, v, None, None, 0, 0.5)
+    np.testing.assert_array_equal(o3, o4)
+    np.testing.assert_array_equal(l3, l4)

@@ -257,7 +257,9 @@ def fia_cuda(query, key, value, **kw):
            "for GQA/MHA")
     _check(prefix or kw.get("actual_shared_prefix_len") is None, "npu_fused_infer_attention_score: "
            "actual_shared_prefix_len needs key_shared_prefix")
-    pse = pse if pse is not None else (True if prefix else None)  # both take the general kernel
+    sink = kw.get("learnable_sink")  # (the v2 op's input)
+    _check(sink is None or not qq, "npu_fused_infer_attention_score: learnable_sink is not served with an int8 query")
+    pse = pse if pse is not None else (True if prefix or sink is not None else None)  # all take the general kernel
     _check(kw.get("quant_offset2") is None or quant_out, "npu_fused_infer_attention_score: quant_offset2 needs "
            "quant_scale2")
     if kw.get("query_rope") is None:
@@ -286,7 +288,7 @@ def fia_cuda(query, key, value, **kw):
             whole_prefix = pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
             # (the one-token kernel steps through pages 32 tokens at a time; key is [blocks, bs, (1,) Dn])
             if (key.dtype == torch.int8 and s == 1 and whole_prefix and not explicit and key.size(1) % 32 == 0
-                    and not packed):
+                    and not packed and sink is None):
                 return _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv, scale, stream)
             # several query tokens (MTP / speculative decode), bands and masks: the general kernel
             return _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv, bt, seq_q, seq_kv,
@@ -512,6 +514,19 @@ def _prefix_params(a, kw, ql, n_kv, dk, dv, query, keep) -> int:
     return sp
 
 
+def _sink_param(a, kw, hq, keep):
+    """learnable_sink (the v2 op's input; prototype experiment_ops.h:3940, bf16): one logit per query
+    head that joins the softmax denominator without a value row."""
+    t = kw.get("learnable_sink")
+    if t is None:
+        return
+    t = t.to(torch.float32).reshape(-1).contiguous()
+    _check(t.numel() == hq, f"npu_fused_infer_attention_score: learnable_sink must hold one logit per query head "
+           f"({hq}), got {t.numel()}")
+    keep.append(t)
+    a.sink = t.data_ptr()
+
+
 def _one_scale(t, name):
     """One fp32 scale on the device from a float tensor or a UINT64 one carrying an fp32 in its low 32
     bits (the prototype types dequant_scale1 / dequant_scale2 UINT64, experiment_ops.h:3888-3890)."""
@@ -635,6 +650,7 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
         _check(key.dtype == torch.int8 and value.dtype == torch.int8,
                "npu_fused_infer_attention_score: int8 key needs an int8 value")
         _antiquant_params(a, kw, b, n_kv, d, dv, keep)
+    _sink_param(a, kw, hq, keep)
     if quant_out:
         _out_quant_params(a, kw, hq, dv, keep)
     _lib.call("tai_fia_general", ctypes.byref(a), stream)
@@ -690,6 +706,8 @@ def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv,
         _check(ks.numel() == nblk * bs, "npu_fused_infer_attention_score: key_antiquant_scale must hold one fp32 per "
                                         "cached token ([blocks, bs])")
         a.kv_dtype, a.k_scale, a.v_scale, a.k_quant_mode, a.v_quant_mode = _lib.DT_INT8, ks.data_ptr(), ks.data_ptr(), 2, 2
+    keep = []
+    _sink_param(a, kw, hq, keep)
     _lib.call("tai_fia_general", ctypes.byref(a), stream)
     return out, lse
 
@@ -767,9 +785,9 @@ def _mla(query, key, value, kw, out, lse, want_lse, num_heads, n_kv, bt, seq_kv,
 # .../custom/fused_infer_attention_score_v2.py:14-60 (npu::, list or tensor lengths): the same operator
 # under renamed arguments, lowered to the same FusedInferAttentionScore node (:166-181), so it maps onto
 # the v1 implementation argument for argument. Arguments of v2 with no v1 counterpart that this build
-# does not serve (query quantisation, the softmax quant scale, learnable_sink, dtype reinterpretations)
-# are refused.
-_V2_UNSUPPORTED = ("dequant_scale_query", "quant_scale_p", "learnable_sink", "query_dtype", "key_dtype", "value_dtype",
+# does not serve (query quantisation, the softmax quant scale, dtype reinterpretations) are refused;
+# learnable_sink is passed on to the v1 implementation, which serves it on the general kernel.
+_V2_UNSUPPORTED = ("dequant_scale_query", "quant_scale_p", "query_dtype", "key_dtype", "value_dtype",
                    "query_rope_dtype", "key_rope_dtype", "key_shared_prefix_dtype", "value_shared_prefix_dtype",
                    "dequant_scale_query_dtype", "dequant_scale_key_dtype", "dequant_scale_value_dtype",
                    "dequant_scale_key_rope_dtype")
@@ -791,7 +809,7 @@ def _v2_to_v1(kw: dict, check: bool = True) -> dict:
          "pre_tokens": "pre_tokens", "next_tokens": "next_tokens", "input_layout": "input_layout",
          "sparse_mode": "sparse_mode", "block_size": "block_size", "inner_precise": "inner_precise",
          "key_quant_mode": "key_antiquant_mode", "value_quant_mode": "value_antiquant_mode",
-         "return_softmax_lse": "softmax_lse_flag"}
+         "return_softmax_lse": "softmax_lse_flag", "learnable_sink": "learnable_sink"}
     return {m[k]: v for k, v in kw.items() if k in m}
 
 

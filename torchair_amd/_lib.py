@@ -40,7 +40,7 @@ class FiaGeneralArgs(ctypes.Structure):
                 ("k_prefix", _P), ("v_prefix", _P), ("k_prefix_strides", c_int64 * 2),
                 ("v_prefix_strides", c_int64 * 2), ("prefix_len", _P), ("prefix_cap", c_int64),
                 ("q_cum", _P), ("kv_cum", _P), ("q_dtype", c_int64), ("deq_scale1", _P), ("quant_scale1", _P),
-                ("deq_scale2", _P)]
+                ("deq_scale2", _P), ("sink", _P)]
 
 
 _SIGS = {

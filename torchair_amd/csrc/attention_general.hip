@@ -260,6 +260,16 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     }
     m = m_new;
   }
+  if (a.sink && i < lq && a.sink[h] != -INFINITY) {
+    // the sink joins the denominator: the reference max and the sum take it in, O gains nothing
+    const float sv = a.sink[h];
+    const float m2 = fmaxf(m, sv);
+    const float alpha = m == -INFINITY ? 0.0f : expf(m - m2);
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) o[e] *= alpha;
+    l = l * alpha + expf(sv - m2);
+    m = m2;
+  }
   const bool live = i < lq && l > 0.0f;
   const float inv = live ? 1.0f / l : 0.0f;
 #pragma unroll
@@ -313,9 +323,9 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
   TAI_CHECK_ARG(a.q_dtype == 0 || qq, "tai_fia_general: q_dtype %lld not supported (0 or int8)",
                 static_cast<long long>(a.q_dtype));
   TAI_CHECK_ARG(!qq || (kv8 && a.deq_scale1 && a.quant_scale1 && a.deq_scale2 && !a.k_scale && !a.v_scale &&
-                        a.dk2 == 0 && !a.k_prefix && !a.pse),
+                        a.dk2 == 0 && !a.k_prefix && !a.pse && !a.sink),
                 "tai_fia_general: an int8 query needs int8 key / value without antiquant scales, the three "
-                "scales, one key part, no shared prefix and no pse");
+                "scales, one key part, no shared prefix, pse or sink");
   TAI_CHECK_ARG(a.kv_cum == nullptr || (a.q_cum && !a.block_table),
                 "tai_fia_general: packed keys (kv_cum) go with packed queries (q_cum) and dense keys");
   TAI_CHECK_ARG(a.kv_cum == nullptr || !kv8 || (a.k_quant_mode == 0 && a.v_quant_mode == 0),
