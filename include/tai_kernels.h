@@ -140,6 +140,18 @@ int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, int64_t n2,
                                     const float* quant_offset, const void* group_index,
                                     int group_index_dtype, int64_t num_groups, int activate_left,
                                     int quant_mode, int8_t* y, float* scale, void* stream);
+/* swiglu_mode 1 of the same op (experiment_ops.h:3786-3790: "odd-even blocking" with clamp_limit,
+ * glu_alpha and glu_bias): output column j takes input columns 2j and 2j + 1 (after the dequantisation
+ * and bias, as above); the activated one (2j with activate_left, else 2j + 1) is clamped to at most
+ * clamp_limit, the other to [-clamp_limit, clamp_limit], and
+ * h = g * sigmoid(glu_alpha * g) * (l + glu_bias), then quant_scale and the quant_mode's quantisation. */
+int tai_dequant_swiglu_quant_clamped(const int32_t* x, int64_t rows, int64_t n2,
+                                     const float* weight_scale, const float* activation_scale,
+                                     const void* bias, int bias_dtype, const float* quant_scale,
+                                     const float* quant_offset, const void* group_index,
+                                     int group_index_dtype, int64_t num_groups, int activate_left,
+                                     int quant_mode, float clamp_limit, float glu_alpha, float glu_bias,
+                                     int8_t* y, float* scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_quant_matmul (W8A8): acc = x1 @ x2 with exact int32 accumulation, then

@@ -149,7 +149,8 @@ def silu(a: np.ndarray) -> np.ndarray:
 
 def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None, bias=None, quant_scale=None,
                          group_index=None, activate_left: bool = False, quant_mode: int = 1,
-                         quant_offset=None) -> Tuple[np.ndarray, np.ndarray]:
+                         quant_offset=None, swiglu_mode: int = 0, clamp_limit: float = 7.0, glu_alpha: float = 1.702,
+                         glu_bias: float = 1.0) -> Tuple[np.ndarray, np.ndarray]:
     """npu_dequant_swiglu_quant, swiglu_mode 0, round_mode 0 (rint). quant_mode 1 (dynamic): per-row
     symmetric int8 of h * quant_scale. quant_mode 0 (static, the converter's default "static",
     npu_dequant_swiglu_quant.py:26-28): y = clamp(rint(h * quant_scale + quant_offset)) with scale 0 (the
@@ -191,8 +192,20 @@ def dequant_swiglu_quant(x: np.ndarray, weight_scale=None, activation_scale=None
         d = (d * np.asarray(activation_scale, F32).reshape(rows, 1)).astype(F32)
     if bias_f is not None:
         d = (d + bias_f).astype(F32)
-    a, b2 = d[:, :n], d[:, n:]
-    r = (silu(a) * b2).astype(F32) if activate_left else (a * silu(b2)).astype(F32)
+    if swiglu_mode == 1:
+        # odd-even blocked columns (prototype experiment_ops.h:3786-3790): output j takes inputs 2j, 2j + 1;
+        # the activated one (2j with activate_left) is clamped above at clamp_limit, the other to
+        # [-clamp_limit, clamp_limit]; h = g * sigmoid(glu_alpha * g) * (l + glu_bias)
+        ev, od = d[:, 0::2], d[:, 1::2]
+        lim = F32(clamp_limit)
+        g = np.minimum(ev if activate_left else od, lim).astype(F32)
+        lin = np.clip(od if activate_left else ev, -lim, lim).astype(F32)
+        with np.errstate(over="ignore"):
+            sg = (F32(1.0) / (F32(1.0) + np.exp(-(F32(glu_alpha) * g).astype(F32)))).astype(F32)
+        r = ((g * sg).astype(F32) * (lin + F32(glu_bias)).astype(F32)).astype(F32)
+    else:
+        a, b2 = d[:, :n], d[:, n:]
+        r = (silu(a) * b2).astype(F32) if activate_left else (a * silu(b2)).astype(F32)
     if quant_scale is not None:
         r = (r * np.asarray(quant_scale, F32).reshape(ng, n)[grp]).astype(F32)
     if quant_mode == 0:

@@ -172,3 +172,32 @@ def test_swiglu(dt, name, shape, dim):
         np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
     else:
         assert_close(got, want)
+
+
+@pytest.mark.parametrize("left,quant_mode,grouped", [(True, 1, False), (False, 1, True), (True, 0, True)])
+def test_dequant_swiglu_quant_clamped_mode(left, quant_mode, grouped):
+    """swiglu_mode 1 (odd-even blocked columns, the clamped SwiGLU) against the oracle, with values on
+    both sides of the clamp limit, non-default glu_alpha / glu_bias / clamp_limit, bias and groups."""
+    g = torch.Generator().manual_seed(91)
+    rows, n = 260, 768
+    x = torch.randint(-40000, 40000, (rows, 2 * n), generator=g, dtype=torch.int32)
+    ng = 3 if grouped else 1
+    counts = torch.tensor([100, 0, 150], dtype=torch.int64) if grouped else None
+    ws = torch.rand(ng, 2 * n, generator=g) * 4e-4  # |dequantised| up to ~16: both sides of the limit
+    act = torch.rand(rows, generator=g) + 0.5
+    bias = torch.randint(-500, 500, (ng, 2 * n), generator=g, dtype=torch.int32)
+    qs = torch.rand(ng, n, generator=g) * 2 + 0.5
+    kw = dict(weight_scale=ws.to(DEV), activation_scale=act.to(DEV), bias=bias.to(DEV), quant_scale=qs.to(DEV),
+              group_index=counts.to(DEV) if grouped else None, activate_left=left, quant_mode=quant_mode,
+              swiglu_mode=1, clamp_limit=6.0, glu_alpha=1.5, glu_bias=0.75)
+    qo = None
+    if quant_mode == 0:
+        qo = torch.rand(ng, n, generator=g) * 2 - 1
+        kw["quant_offset"] = qo.to(DEV)
+    y, s = torch.ops.npu.npu_dequant_swiglu_quant(x.to(DEV), **kw)
+    wy, wsc = G.dequant_swiglu_quant(x.numpy(), ws.numpy(), act.numpy(), bias.numpy(), qs.numpy(),
+                                     counts.numpy() if grouped else None, left, quant_mode,
+                                     None if qo is None else qo.numpy(), swiglu_mode=1, clamp_limit=6.0,
+                                     glu_alpha=1.5, glu_bias=0.75)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)

@@ -674,3 +674,25 @@ def test_learnable_sink_is_a_key_with_a_zero_value():
     o4, l4 = G.prefill_attention(q, k, v, None, None, 0, 0.5)
     np.testing.assert_array_equal(o3, o4)
     np.testing.assert_array_equal(l3, l4)
+
+
+def test_dsq_swiglu_mode_1_pins():
+    # (1) no clamping, glu_alpha 1, glu_bias 0: the odd-even mode is the halves mode on the de-interleaved
+    #     columns (g * sigmoid(g) = silu(g))
+    x = RNG.integers(-3000, 3000, (6, 16)).astype(np.int32)
+    ws = RNG.uniform(1e-3, 2e-3, 16).astype(np.float32)
+    act = RNG.uniform(0.5, 1.5, 6).astype(np.float32)
+    perm = np.concatenate([np.arange(0, 16, 2), np.arange(1, 16, 2)])
+    for left in (True, False):
+        y1, s1 = G.dequant_swiglu_quant(x, ws, act, activate_left=left, swiglu_mode=1, clamp_limit=1e30,
+                                        glu_alpha=1.0, glu_bias=0.0)
+        y0, s0 = G.dequant_swiglu_quant(x[:, perm], ws[perm], act, activate_left=left)
+        # (g * sigmoid(g) rounds sigmoid first, silu divides once: the two differ by an ulp at most)
+        assert np.abs(y1.astype(int) - y0.astype(int)).max() <= 1
+        np.testing.assert_allclose(s1, s0, rtol=2.5e-7, atol=0)
+    # (2) the clamps, against float64 arithmetic: g = 10 -> 7, l = -9 -> -7 (limit 7, alpha 1.702, bias 1)
+    xk = np.array([[10, -9, 2, 3]], np.int32)  # pairs (10, -9) and (2, 3); even activated (activate_left)
+    y, s = G.dequant_swiglu_quant(xk, activate_left=True, swiglu_mode=1)
+    h = [7 / (1 + math.exp(-1.702 * 7)) * (-7 + 1), 2 / (1 + math.exp(-1.702 * 2)) * (3 + 1)]
+    assert abs(s[0] - max(abs(v) for v in h) / 127) <= 1e-6 * s[0]
+    np.testing.assert_array_equal(y[0], np.rint(np.array(h) / s[0]).astype(np.int8))

@@ -53,6 +53,9 @@ _SIGS = {
         c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, c_int, c_int64, c_int, _P, _P, _P]),
     "tai_dequant_swiglu_quant_static": (
         c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, _P, _P, _P]),
+    "tai_dequant_swiglu_quant_clamped": (
+        c_int, [_P, c_int64, c_int64, _P, _P, _P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_float, c_float,
+                c_float, _P, _P, _P]),
     "tai_dynamic_quant_v2_workspace_size": (c_size_t, [c_int64]),
     "tai_dynamic_quant_v2": (
         c_int, [_P, c_int, c_int64, c_int64, _P, _P, c_int, c_int64, c_int, c_int, c_float, _P, _P, _P, _P, c_size_t,

@@ -220,7 +220,9 @@ def _dsq_cuda(x, *, weight_scale=None, activation_scale=None, bias=None, quant_s
               group_index=None, activate_left=False, quant_mode=0, dst_type=None, round_mode=None, activate_dim=None,
               swiglu_mode=0, clamp_limit=7.0, glu_alpha=1.702, glu_bias=1.0):
     """npu_dequant_swiglu_quant (npu_dequant_swiglu_quant.py:5-47): quant_mode 1 (dynamic, per-row symmetric
-    int8 of h * quant_scale) or 0 (static: clamp(rint(h * quant_scale + quant_offset)), scale output 0)."""
+    int8 of h * quant_scale) or 0 (static: clamp(rint(h * quant_scale + quant_offset)), scale output 0);
+    swiglu_mode 0 (halves) or 1 (odd-even blocked columns, the clamped SwiGLU with clamp_limit, glu_alpha
+    and glu_bias; experiment_ops.h:3786-3790)."""
     _on_gpu(x, weight_scale, activation_scale, bias, quant_scale, quant_offset, group_index)
     y, scale = _dsq_fake(x, activate_dim=activate_dim, quant_mode=quant_mode)
     _check(activate_dim in (None, -1, x.dim() - 1), "npu_dequant_swiglu_quant: only the last dim can be activated")
@@ -229,7 +231,7 @@ def _dsq_cuda(x, *, weight_scale=None, activation_scale=None, bias=None, quant_s
     _check(quant_mode == 1 or quant_scale is not None, "npu_dequant_swiglu_quant: the static mode needs quant_scale")
     _check(dst_type in (None, 1), "npu_dequant_swiglu_quant: only int8 output (dst_type 1) is supported")
     _check(round_mode in (None, 0), "npu_dequant_swiglu_quant: only round_mode 0 (rint) is supported")
-    _check(swiglu_mode == 0, "npu_dequant_swiglu_quant: only swiglu_mode 0 is supported")
+    _check(swiglu_mode in (0, 1), "npu_dequant_swiglu_quant: swiglu_mode must be 0 or 1")
     _check(x.dtype == torch.int32, "npu_dequant_swiglu_quant: x must be int32")
     xc = x.contiguous()
     n2 = xc.shape[-1]
@@ -263,6 +265,11 @@ def _dsq_cuda(x, *, weight_scale=None, activation_scale=None, bias=None, quant_s
         gi = group_index.contiguous()
         _check(gi.dtype in (torch.int32, torch.int64), "npu_dequant_swiglu_quant: group_index must be int32/int64")
     if rows == 0:
+        return y, scale
+    if swiglu_mode == 1:
+        _lib.call("tai_dequant_swiglu_quant_clamped", _p(xc), rows, n2, _p(ws), _p(act), _p(bi), bias_dt, _p(qs),
+                  _p(qo), _p(gi), _DT[gi.dtype] if gi is not None else DT_NONE, ng, 1 if activate_left else 0,
+                  int(quant_mode), float(clamp_limit), float(glu_alpha), float(glu_bias), _p(y), _p(scale), _stream(xc))
         return y, scale
     _lib.call("tai_dequant_swiglu_quant_static", _p(xc), rows, n2, _p(ws), _p(act), _p(bi), bias_dt, _p(qs),
               _p(qo), _p(gi), _DT[gi.dtype] if gi is not None else DT_NONE, ng, 1 if activate_left else 0,

@@ -198,6 +198,9 @@ struct DsqArgs {
   // static mode (quant_mode 0): y = clamp(rint(h * quant_scale + quant_offset)); scale output 0
   const float* qo;
   int stat;
+  // swiglu_mode 1 (generic kernel only): output column j pairs input columns 2j and 2j + 1
+  int swi_mode;
+  float clamp_limit, glu_alpha, glu_bias;
 };
 
 // int8 of one SwiGLU output v (already multiplied by quant_scale): dynamic, rint(v / scale) with
@@ -364,7 +367,28 @@ __global__ __launch_bounds__(256) void dsq_generic_kernel(DsqArgs a) {
   const int32_t* bi = (a.bias && a.bias_dt == TAI_DT_INT32) ? static_cast<const int32_t*>(a.bias) + g * n2 : nullptr;
   const float* bf = (a.bias && a.bias_dt == TAI_DT_FP32) ? static_cast<const float*>(a.bias) + g * n2 : nullptr;
   const float act = a.as ? a.as[row] : 1.0f;
+  // dequantised input column c (before the activation)
+  auto pre = [&](int64_t c) {
+    int xv = a.x[row * n2 + c];
+    if (bi) xv += bi[c];
+    float d = static_cast<float>(xv) * (ws ? ws[c] : 1.0f);
+    if (a.as) d *= act;
+    if (bf) d += bf[c];
+    return d;
+  };
   auto value = [&](int64_t j) {
+    if (a.swi_mode == 1) {
+      // the clamped SwiGLU of odd-even blocked columns: the activated column (even with activate_left,
+      // else odd) clamped above, the linear one on both sides;
+      // h = g * sigmoid(glu_alpha * g) * (l + glu_bias)
+      const float ev = pre(2 * j), od = pre(2 * j + 1);
+      const float g = fminf(a.left ? ev : od, a.clamp_limit);
+      const float l = fminf(fmaxf(a.left ? od : ev, -a.clamp_limit), a.clamp_limit);
+      const float sg = rcp_f32(1.0f + __builtin_amdgcn_exp2f((a.glu_alpha * g) * -1.4426950408889634f));
+      float r = (g * sg) * (l + a.glu_bias);
+      if (qs) r *= qs[j];
+      return r;
+    }
     int xa = a.x[row * n2 + j], xb = a.x[row * n2 + n + j];
     if (bi) { xa += bi[j]; xb += bi[n + j]; }
     float da = static_cast<float>(xa) * (ws ? ws[j] : 1.0f);
@@ -589,12 +613,12 @@ extern "C" int tai_dequant_swiglu_quant(const int32_t* x, int64_t rows, int64_t 
                                          scale, stream);
 }
 
-extern "C" int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, int64_t n2,
-                                               const float* weight_scale, const float* activation_scale,
-                                               const void* bias, int bias_dtype, const float* quant_scale,
-                                               const float* quant_offset, const void* group_index,
-                                               int group_index_dtype, int64_t num_groups, int activate_left,
-                                               int quant_mode, int8_t* y, float* scale, void* stream) {
+namespace tai {
+namespace {
+int dsq_run(const int32_t* x, int64_t rows, int64_t n2, const float* weight_scale, const float* activation_scale,
+            const void* bias, int bias_dtype, const float* quant_scale, const float* quant_offset,
+            const void* group_index, int group_index_dtype, int64_t num_groups, int activate_left, int quant_mode,
+            int8_t* y, float* scale, void* stream, int swi_mode, float clamp_limit, float glu_alpha, float glu_bias) {
   TAI_CHECK_ARG(quant_mode == 0 || quant_mode == 1, "tai_dequant_swiglu_quant: quant_mode must be 0 (static) or 1 "
                 "(dynamic)");
   TAI_CHECK_ARG(quant_mode == 0 || quant_offset == nullptr, "tai_dequant_swiglu_quant: quant_offset applies to the "
@@ -611,8 +635,12 @@ extern "C" int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, i
                 "tai_dequant_swiglu_quant: group_index must be int32 or int64");
   DsqArgs a{x, rows, n2 / 2, weight_scale, activation_scale, bias, bias_dtype, quant_scale,
             group_index, group_index_dtype, group_index ? num_groups : 1, activate_left, y, scale, quant_offset,
-            quant_mode == 0 ? 1 : 0};
+            quant_mode == 0 ? 1 : 0, swi_mode, clamp_limit, glu_alpha, glu_bias};
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (swi_mode == 1) {
+    dsq_generic_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, st>>>(a);
+    return launch_status("tai_dequant_swiglu_quant_clamped");
+  }
   const int64_t n = n2 / 2;
   auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
   const bool aligned = n % 4 == 0 && al(x) && al(weight_scale) && al(bias) && (reinterpret_cast<uintptr_t>(y) % 4) == 0;
@@ -629,6 +657,30 @@ extern "C" int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, i
   else if (aligned && ng4 <= 256 * 8) dsq_kernel<8><<<grid, 256, 0, st>>>(a);
   else dsq_generic_kernel<<<grid, 256, 0, st>>>(a);
   return launch_status("tai_dequant_swiglu_quant");
+}
+}  // namespace
+}  // namespace tai
+
+extern "C" int tai_dequant_swiglu_quant_static(const int32_t* x, int64_t rows, int64_t n2,
+                                               const float* weight_scale, const float* activation_scale,
+                                               const void* bias, int bias_dtype, const float* quant_scale,
+                                               const float* quant_offset, const void* group_index,
+                                               int group_index_dtype, int64_t num_groups, int activate_left,
+                                               int quant_mode, int8_t* y, float* scale, void* stream) {
+  return dsq_run(x, rows, n2, weight_scale, activation_scale, bias, bias_dtype, quant_scale, quant_offset, group_index,
+                 group_index_dtype, num_groups, activate_left, quant_mode, y, scale, stream, 0, 0.0f, 0.0f, 0.0f);
+}
+
+extern "C" int tai_dequant_swiglu_quant_clamped(const int32_t* x, int64_t rows, int64_t n2,
+                                                const float* weight_scale, const float* activation_scale,
+                                                const void* bias, int bias_dtype, const float* quant_scale,
+                                                const float* quant_offset, const void* group_index,
+                                                int group_index_dtype, int64_t num_groups, int activate_left,
+                                                int quant_mode, float clamp_limit, float glu_alpha, float glu_bias,
+                                                int8_t* y, float* scale, void* stream) {
+  return dsq_run(x, rows, n2, weight_scale, activation_scale, bias, bias_dtype, quant_scale, quant_offset, group_index,
+                 group_index_dtype, num_groups, activate_left, quant_mode, y, scale, stream, 1, clamp_limit, glu_alpha,
+                 glu_bias);
 }
 
 extern "C" size_t tai_dynamic_quant_v2_workspace_size(int64_t rows) {
