@@ -420,3 +420,11 @@ def test_fia_host_helpers_for_packed_layouts_and_quant_scales():
         assert got.dtype == torch.float32 and got.numel() == 1 and got.item() == float(f)
     with pytest.raises(RuntimeError, match="one"):
         _one_scale(torch.ones(2), "quant_scale1")
+
+
+def test_ops_alias_exposes_the_reference_entry_points():
+    """torchair_amd.ops carries the fused-op functions of the reference's torchair.ops for this path."""
+    from torchair_amd import ops
+    for name in ("npu_fused_infer_attention_score", "npu_fused_infer_attention_score_v2"):
+        assert callable(getattr(ops, name))
+    assert ops.npu_dynamic_quant is torch.ops.npu.npu_dynamic_quant

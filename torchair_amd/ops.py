@@ -5,8 +5,16 @@ from . import _ops_impl  # noqa: F401
 
 
 def npu_fused_infer_attention_score(*args, **kwargs):
-    """torchair.ops.npu_fused_infer_attention_score (tensor sequence lengths), air:: namespace."""
+    """torchair.ops.npu_fused_infer_attention_score (python/torchair/ops/__init__.py:5-7; tensor sequence
+    lengths), the air:: op. The reference's eager impl of that op raises outside its max-autotune graph
+    mode (_npu_fused_infer_attention_score.py:36-42); here the kernels run in every mode."""
     return torch.ops.air.npu_fused_infer_attention_score(*args, **kwargs)
+
+
+def npu_fused_infer_attention_score_v2(*args, **kwargs):
+    """torchair.ops.npu_fused_infer_attention_score_v2 (python/torchair/ops/__init__.py:10-12), the air::
+    v2 op (tensor sequence lengths)."""
+    return torch.ops.air.npu_fused_infer_attention_score_v2(*args, **kwargs)
 
 
 npu_dynamic_quant = torch.ops.npu.npu_dynamic_quant
