@@ -428,3 +428,8 @@ def test_ops_alias_exposes_the_reference_entry_points():
     for name in ("npu_fused_infer_attention_score", "npu_fused_infer_attention_score_v2"):
         assert callable(getattr(ops, name))
     assert ops.npu_dynamic_quant is torch.ops.npu.npu_dynamic_quant
+    # every npu:: op this package defines is reachable through the alias
+    import re
+    src = "".join((ROOT / "torchair_amd" / f).read_text() for f in ("_ops_impl.py", "_norm_cache.py", "_gmm_fused.py"))
+    for name in set(re.findall(r'"(npu_[a-z0-9_]+)\(', src)):
+        assert hasattr(ops, name), name

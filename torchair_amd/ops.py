@@ -32,3 +32,7 @@ npu_kv_rmsnorm_rope_cache = torch.ops.npu.npu_kv_rmsnorm_rope_cache
 npu_kv_rmsnorm_rope_cache_v2 = torch.ops.npu.npu_kv_rmsnorm_rope_cache_v2
 npu_grouped_matmul_swiglu_quant_v2 = torch.ops.npu.npu_grouped_matmul_swiglu_quant_v2
 npu_grouped_matmul_finalize_routing = torch.ops.npu.npu_grouped_matmul_finalize_routing
+npu_dynamic_quant_asymmetric = torch.ops.npu.npu_dynamic_quant_asymmetric
+npu_swiglu = torch.ops.npu.npu_swiglu
+npu_moe_compute_expert_tokens = torch.ops.npu.npu_moe_compute_expert_tokens
+npu_scatter_pa_kv_cache_functional = torch.ops.npu.npu_scatter_pa_kv_cache_functional
