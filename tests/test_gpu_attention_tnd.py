@@ -248,3 +248,20 @@ def test_packed_int8_query():
     assert out.dtype == torch.float16
     # atol: one P8 rounding the other way between the device's and numpy's exp (see test_int8_query)
     assert_close(f32np(out), G.pack_tnd(want, lq), atol=2e-2)
+
+
+def test_one_token_tnd_on_the_general_kernel_without_lengths():
+    """A TND query of one token per sequence and no actual_seq_lengths, sent to the general kernel by an
+    int8 attention_out: its cumulative ends are implied (1..B)."""
+    g = torch.Generator().manual_seed(177)
+    lk, hq, hkv, d, bs = [300, 1, 129, 64], 8, 2, 128, 64
+    b = len(lk)
+    kc, vc, bt = _paged(lk, hkv, d, bs, g)
+    q = torch.randn(b, hq, d, generator=g).to(torch.bfloat16)
+    out, _ = FIA(q.to(DEV), kc.reshape(-1, bs, hkv * d).to(DEV), vc.reshape(-1, bs, hkv * d).to(DEV),
+                 block_table=bt.to(DEV), actual_seq_lengths_kv=lk, num_heads=hq, num_key_value_heads=hkv,
+                 input_layout="TND", block_size=bs, scale=1 / math.sqrt(d), quant_scale2=torch.tensor([60.0], device=DEV))
+    want, _ = G.paged_decode_attention(f32np(q), f32np(kc), f32np(vc), bt.numpy(), lk, 1 / math.sqrt(d))
+    assert out.dtype == torch.int8 and out.shape == (b, hq, d)
+    exp8 = G.quant_attention_out(want[:, None], [60.0])[:, 0].astype(np.int32)
+    assert np.abs(out.cpu().numpy().astype(np.int32) - exp8).max() <= 1

@@ -577,6 +577,14 @@ def _dense_kv_check(query, key, value, ql, num_heads, n_kv):
            "positions")
 
 
+def _one_token_ends(seq_q, bt, t, device):
+    """A packed query over a paged cache without actual_seq_lengths holds one token per sequence (T = B,
+    the one-token layout): its cumulative ends are 1..B."""
+    if seq_q is None and bt is not None and t == bt.size(0):
+        return torch.arange(1, t + 1, dtype=torch.int64, device=device)
+    return seq_q
+
+
 def _packed_lens(a, ql, query, bt, seq_q, seq_kv):
     """Packed TND / NTD queries: the sequences' query rows end at the cumulative actual_seq_lengths
     (torch_npu's TND convention); dense keys/values are packed the same way (cumulative
@@ -605,6 +613,7 @@ def _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d,
         _check(kw.get("pse_shift") is None and kw.get("key_shared_prefix") is None,
                f"npu_fused_infer_attention_score: pse_shift and a shared prefix take batched layouts, not {ql}")
         s_q, hq, _ = _tnd(query, ql)
+        seq_q = _one_token_ends(seq_q, bt, s_q, query.device)
         b = seq_q.numel() if seq_q is not None else 0
     else:
         b, s_q, hq, _ = _bsnd(query, ql, num_heads)
@@ -676,6 +685,7 @@ def _general_mla(query, key, value, kw, out, lse, want_lse, ql, num_heads, n_kv,
     if packed:
         s_q, hq, dn = _tnd(query, ql)
         dr = _tnd(q_rope, ql)[2]
+        seq_q = _one_token_ends(seq_q, bt, s_q, query.device)
         b = seq_q.numel() if seq_q is not None else 0
     else:
         b, s_q, hq, dn = _bsnd(query, ql, num_heads)
