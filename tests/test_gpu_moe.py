@@ -281,3 +281,48 @@ def test_moe_compute_expert_tokens():
         got = torch.ops.npu.npu_moe_compute_expert_tokens(se.to(DEV), e)
         assert got.dtype == torch.int32 and got.shape == (e,)
         np.testing.assert_array_equal(got.cpu().numpy(), G.moe_compute_expert_tokens(se.numpy(), e))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_init_routing_v2_random(seed):
+    """Seeded random routing bit-exact against the oracle: token and expert counts, top-k, the expert
+    range, active_num, dropless or drop-pad with a capacity, gather or scatter row indices, counts or
+    cumsum, with a per-token scale carried along (skewed routings included)."""
+    rng = np.random.default_rng(4000 + seed)
+    g = gen(4000 + seed)
+    t, e = int(rng.integers(1, 700)), int(rng.choice([8, 16, 64, 256]))
+    k = int(rng.integers(1, min(e, 8) + 1))
+    h = 16 * int(rng.integers(1, 9))
+    if rng.random() < 0.3:  # skewed: most slots on a few experts
+        idx = torch.from_numpy(np.stack([rng.permutation(min(e, 2 * k))[:k] for _ in range(t)]).astype(np.int32))
+    else:
+        idx = torch.from_numpy(np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32))
+    x = torch.randn(t, h, generator=g)
+    scale = torch.rand(t, generator=g)
+    lo = int(rng.integers(0, e // 2))
+    hi = int(rng.integers(lo + 1, e + 1))
+    tok_type = int(rng.integers(0, 2))
+    case = dict(t=t, e=e, k=k, h=h, lo=lo, hi=hi, tok_type=tok_type)
+    if rng.random() < 0.4:
+        cap = int(rng.integers(1, 3 * t * k // e + 2))
+        case["cap"] = cap
+        print("case", case, flush=True)
+        ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+            x.to(DEV), idx.to(DEV), scale=scale.to(DEV), expert_capacity=cap, expert_num=e, drop_pad_mode=1,
+            active_expert_range=[lo, hi], expert_tokens_num_type=tok_type, expert_tokens_num_flag=True)
+        wex, wri, wtok, wes = G.moe_init_routing_v2_droppad(f32np(x), idx.numpy(), cap, scale.numpy(), lo, hi,
+                                                            tok_type)
+    else:
+        active = int(rng.integers(1, t * k + 1))
+        row_type = int(rng.integers(0, 2))
+        case.update(active=active, row_type=row_type)
+        print("case", case, flush=True)
+        ex, ri, tok, es = torch.ops.npu.npu_moe_init_routing_v2(
+            x.to(DEV), idx.to(DEV), scale=scale.to(DEV), active_num=active, expert_num=e,
+            active_expert_range=[lo, hi], expert_tokens_num_type=tok_type, row_idx_type=row_type)
+        wex, wri, wtok, wes = G.moe_init_routing_v2(f32np(x), idx.numpy(), scale.numpy(), active, lo, hi, tok_type,
+                                                    row_type)
+    np.testing.assert_array_equal(ri.cpu().numpy(), wri, err_msg=str(case))
+    np.testing.assert_array_equal(tok.cpu().numpy(), wtok, err_msg=str(case))
+    np.testing.assert_array_equal(f32np(ex), wex, err_msg=str(case))
+    np.testing.assert_array_equal(es.cpu().numpy(), wes, err_msg=str(case))
