@@ -326,3 +326,35 @@ def test_init_routing_v2_random(seed):
     np.testing.assert_array_equal(tok.cpu().numpy(), wtok, err_msg=str(case))
     np.testing.assert_array_equal(f32np(ex), wex, err_msg=str(case))
     np.testing.assert_array_equal(es.cpu().numpy(), wes, err_msg=str(case))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_gating_top_k_random(seed):
+    """Seeded random npu_moe_gating_top_k bit-exact (ids) against the oracle: expert and group counts
+    (the 256-expert register kernel and the general one), k, k_group, group selection by max or top-2
+    sum, sigmoid or softmax scores, with or without bias and the normalised-score output."""
+    rng = np.random.default_rng(5000 + seed)
+    g = gen(5000 + seed)
+    e = int(rng.choice([16, 64, 128, 256, 256]))
+    group_count = int(rng.choice([c for c in (1, 2, 4, 8) if e % c == 0 and e // c >= 2]))
+    k_group = int(rng.integers(1, group_count + 1))
+    per_group = e // group_count
+    k = int(rng.integers(1, min(8, k_group * per_group) + 1))
+    mode = int(rng.integers(0, 2))
+    norm = int(rng.integers(0, 2))
+    t = int(rng.integers(1, 500))
+    x = torch.randn(t, e, generator=g)
+    bias = torch.randn(e, generator=g) * 0.1 if rng.random() < 0.6 else None
+    out_flag = bool(rng.integers(0, 2))
+    rsf = float(rng.choice([1.0, 2.5]))
+    case = dict(e=e, groups=group_count, k_group=k_group, k=k, mode=mode, norm=norm, t=t, bias=bias is not None)
+    print("case", case, flush=True)
+    y, idx, out = torch.ops.npu.npu_moe_gating_top_k(
+        x.to(DEV), k, bias=None if bias is None else bias.to(DEV), k_group=k_group, group_count=group_count,
+        group_select_mode=mode, renorm=0, norm_type=norm, out_flag=out_flag, routed_scaling_factor=rsf, eps=1e-20)
+    wy, widx, wout = G.moe_gating_top_k(x.numpy(), k, None if bias is None else bias.numpy(), k_group, group_count,
+                                        mode, 0, norm, out_flag, rsf, 1e-20)
+    np.testing.assert_array_equal(idx.cpu().numpy(), widx, err_msg=str(case))
+    np.testing.assert_allclose(y.cpu().numpy(), wy, rtol=1e-6, atol=1e-7, err_msg=str(case))
+    if out_flag:
+        np.testing.assert_allclose(out.cpu().numpy(), wout, rtol=1e-6, atol=1e-7, err_msg=str(case))
