@@ -201,3 +201,66 @@ def test_dequant_swiglu_quant_clamped_mode(left, quant_mode, grouped):
                                      glu_alpha=1.5, glu_bias=0.75)
     assert_int8_close(y.cpu().numpy(), wy)
     np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_dynamic_quant_random(seed):
+    """Seeded random npu_dynamic_quant shapes across the kernel variants (few and many rows, row widths
+    that are and are not multiples of 8, up to 16 K columns), dtypes, and smooth scales with groups."""
+    rng = np.random.default_rng(6000 + seed)
+    g = gen(6000 + seed)
+    rows = int(rng.choice([1, 3, 64, 700, 1500, 4100]))
+    cols = int(rng.choice([8, 96, 1000, 2048, 7168, 7170, 16384]))
+    dt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    x = randn((rows, cols), g, dt)
+    smooth = gidx = None
+    if rng.random() < 0.5:
+        ng = int(rng.integers(1, 5))
+        smooth = uniform((ng, cols), g, 0.5, 2.0)
+        ends = np.sort(rng.integers(0, rows + 1, ng))
+        ends[-1] = rows
+        gidx = torch.tensor(ends, dtype=torch.int64)
+    print("case", dict(rows=rows, cols=cols, dt=str(dt), groups=None if gidx is None else gidx.tolist()), flush=True)
+    _dq_check(x, smooth, gidx)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_dequant_swiglu_quant_random(seed):
+    """Seeded random npu_dequant_swiglu_quant: rows from 1 to thousands, n on and off the vector paths,
+    groups (with empty ones and rows past the total), int32 / fp32 bias, quant_scale, both activate sides,
+    dynamic and static quantisation, swiglu_mode 0 and 1."""
+    rng = np.random.default_rng(7000 + seed)
+    g = gen(7000 + seed)
+    rows = int(rng.choice([1, 5, 128, 513, 2000]))
+    n = int(rng.choice([4, 100, 512, 2048, 2049, 5632]))
+    grouped = rng.random() < 0.5
+    ng = int(rng.integers(1, 5)) if grouped else 1
+    x = torch.randint(-100000, 100000, (rows, 2 * n), generator=g, dtype=torch.int32)
+    ws = uniform((ng, 2 * n) if grouped else (2 * n,), g, 1e-4, 1e-3)
+    act = uniform((rows,), g, 0.005, 0.05) if rng.random() < 0.7 else None
+    bias = None
+    r = rng.random()
+    if r < 0.3:
+        bias = torch.randint(-1000, 1000, (ng, 2 * n) if grouped else (2 * n,), generator=g, dtype=torch.int32)
+    elif r < 0.5:
+        bias = uniform((ng, 2 * n) if grouped else (2 * n,), g, -0.5, 0.5)
+    qmode = int(rng.integers(0, 2))
+    qs = uniform((ng, n) if grouped else (n,), g, 0.5, 2.0) if (qmode == 0 or rng.random() < 0.5) else None
+    qo = uniform((ng, n) if grouped else (n,), g, -1.0, 1.0) if (qmode == 0 and rng.random() < 0.5) else None
+    gidx = torch.tensor(rng.integers(0, rows // max(ng, 1) + 2, ng), dtype=torch.int64) if grouped else None
+    left = bool(rng.integers(0, 2))
+    smode = int(rng.integers(0, 2))
+    case = dict(rows=rows, n=n, ng=ng, grouped=grouped, qmode=qmode, left=left, smode=smode,
+                bias=None if bias is None else str(bias.dtype))
+    print("case", case, flush=True)
+    y, s = torch.ops.npu.npu_dequant_swiglu_quant(
+        x.to(DEV), weight_scale=ws.to(DEV), activation_scale=None if act is None else act.to(DEV),
+        bias=None if bias is None else bias.to(DEV), quant_scale=None if qs is None else qs.to(DEV),
+        quant_offset=None if qo is None else qo.to(DEV), group_index=None if gidx is None else gidx.to(DEV),
+        activate_left=left, quant_mode=qmode, swiglu_mode=smode)
+    wy, wsc = G.dequant_swiglu_quant(x.numpy(), ws.numpy(), None if act is None else act.numpy(),
+                                     None if bias is None else bias.numpy(), None if qs is None else qs.numpy(),
+                                     None if gidx is None else gidx.numpy(), left, qmode,
+                                     None if qo is None else qo.numpy(), swiglu_mode=smode)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=1e-30, err_msg=str(case))
