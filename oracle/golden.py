@@ -477,6 +477,8 @@ def moe_finalize_routing(expanded, skip1, skip2, bias, scales, src_to_dst, exper
     s2d = np.asarray(src_to_dst, np.int64).reshape(-1)
     if scales is not None:
         t, k = np.asarray(scales).shape
+    elif expert_for_source_row is not None:
+        t, k = np.asarray(expert_for_source_row).shape
     else:
         t = np.asarray(skip1).shape[0]
         k = len(s2d) // t

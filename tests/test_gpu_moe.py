@@ -358,3 +358,37 @@ def test_gating_top_k_random(seed):
     np.testing.assert_allclose(y.cpu().numpy(), wy, rtol=1e-6, atol=1e-7, err_msg=str(case))
     if out_flag:
         np.testing.assert_allclose(out.cpu().numpy(), wout, rtol=1e-6, atol=1e-7, err_msg=str(case))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_finalize_routing_random(seed):
+    """Seeded random npu_moe_finalize_routing against the oracle: both slot conventions (drop_pad_mode 0,
+    k-major; 2, token-major), dropped rows (-1), skip inputs, per-expert bias, scales absent or given,
+    widths on and off the 16-byte path, bf16 / fp16 / fp32."""
+    rng = np.random.default_rng(8000 + seed)
+    g = gen(8000 + seed)
+    t, k = int(rng.integers(1, 300)), int(rng.integers(1, 9))
+    h = int(rng.choice([8, 64, 100, 7168]))
+    e = int(rng.integers(2, 40))
+    dt, name = [(torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")][int(rng.integers(0, 3))]
+    mode = int(rng.choice([0, 2]))
+    n = t * k
+    rows = n + int(rng.integers(0, 20))
+    ex = randn((rows, h), g, dt)
+    s2d = torch.randperm(rows, generator=g)[:n].to(torch.int32)
+    s2d[torch.rand(n, generator=g) < 0.1] = -1  # dropped slots
+    expert = torch.randint(0, e, (t, k), generator=g, dtype=torch.int32)
+    skip1 = randn((t, h), g, dt) if rng.random() < 0.5 else None
+    skip2 = randn((t, h), g, dt) if skip1 is not None and rng.random() < 0.5 else None
+    bias = randn((e, h), g, dt) if rng.random() < 0.5 else None
+    scales = torch.rand(t, k, generator=g).to(dt) if rng.random() < 0.8 else None
+    case = dict(t=t, k=k, h=h, e=e, dt=name, mode=mode, skip1=skip1 is not None, skip2=skip2 is not None,
+                bias=bias is not None, scales=scales is not None)
+    print("case", case, flush=True)
+    dv = lambda v: None if v is None else v.to(DEV)  # noqa: E731
+    y = torch.ops.npu.npu_moe_finalize_routing(dv(ex), dv(skip1), dv(skip2), dv(bias), dv(scales), dv(s2d),
+                                               dv(expert), drop_pad_mode=mode)
+    npf = lambda v: None if v is None else f32np(v)  # noqa: E731
+    want = G.moe_finalize_routing(f32np(ex), npf(skip1), npf(skip2), npf(bias), npf(scales), s2d.numpy(),
+                                  expert.numpy(), mode, name)
+    assert_close(f32np(y), want, rtol=2e-2, atol=2e-2)

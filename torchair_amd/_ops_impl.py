@@ -835,20 +835,24 @@ _define("npu", "npu_moe_init_routing_v2(Tensor x, Tensor expert_idx, *, Tensor? 
 
 
 # ============================================================================ npu_moe_finalize_routing
-def _finalize_dims(expanded, skip1, scales, src_to_dst):
+def _finalize_dims(expanded, skip1, scales, src_to_dst, expert=None):
+    """(tokens, k): from scales [T, k], else expert_for_source_row [T, k], else skip1's T rows."""
     if scales is not None:
         t, k = scales.shape
+    elif expert is not None and expert.dim() == 2:
+        t, k = expert.shape
     elif skip1 is not None:
         t = skip1.shape[0]
         k = src_to_dst.numel() // max(t, 1)
     else:
-        raise RuntimeError("npu_moe_finalize_routing: scales or skip1 is needed to know the token count")
+        raise RuntimeError("npu_moe_finalize_routing: scales, expert_for_source_row or skip1 is needed to know the "
+                           "token count")
     return t, k
 
 
 def _finalize_fake(expanded_permuted_rows, skip1, skip2, bias, scales, expanded_src_to_dst_row,
                    export_for_source_row, drop_pad_mode=0):
-    t, _ = _finalize_dims(expanded_permuted_rows, skip1, scales, expanded_src_to_dst_row)
+    t, _ = _finalize_dims(expanded_permuted_rows, skip1, scales, expanded_src_to_dst_row, export_for_source_row)
     return expanded_permuted_rows.new_empty((t, expanded_permuted_rows.shape[-1]))
 
 
@@ -859,7 +863,7 @@ def _finalize_cuda(expanded_permuted_rows, skip1, skip2, bias, scales, expanded_
     _on_gpu(ex, skip1, skip2, bias, scales, expanded_src_to_dst_row, export_for_source_row)
     mode = 0 if drop_pad_mode is None else int(drop_pad_mode)
     _check(mode in (0, 2), "npu_moe_finalize_routing: drop_pad_mode must be 0 (k-major slots) or 2 (token-major)")
-    t, k = _finalize_dims(ex, skip1, scales, expanded_src_to_dst_row)
+    t, k = _finalize_dims(ex, skip1, scales, expanded_src_to_dst_row, export_for_source_row)
     h = ex.shape[-1]
     y = ex.new_empty((t, h))
     dt = ex.dtype
