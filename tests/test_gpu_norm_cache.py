@@ -173,3 +173,44 @@ def test_kv_rmsnorm_rope_cache_int8_per_token_feeds_mla_decode():
     want, _ = G.mla_decode_attention(f32np(qn)[:, 0], f32np(qr)[:, 0], cc[:, :, 0].cpu().numpy(), tok.cpu().numpy(),
                                      f32np(kc[:, :, 0].cpu()), bt.numpy(), lens, 1.0 / 192 ** 0.5)
     assert_close(f32np(out[:, 0].cpu()), want)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_add_rms_norm_family_random(seed):
+    """Seeded random shapes (leading dims 1-3, widths on and off the vector paths, few and many rows),
+    dtypes, the optional smooth scales and beta, and one or two quantised outputs, against the oracle."""
+    rng = np.random.default_rng(9000 + seed)
+    g = gen(9000 + seed)
+    h = int(rng.choice([8, 24, 1000, 2048, 5120, 7168, 7170]))
+    lead = [int(x) for x in rng.integers(1, 12, int(rng.integers(1, 4)))]
+    if rng.random() < 0.3:
+        lead = [int(rng.integers(500, 3000))]  # many rows (the total stays at most a few thousand)
+    shape = tuple(lead) + (h,)
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    x1, x2 = randn(shape, g, dtype), randn(shape, g, dtype)
+    gamma = uniform((h,), g, 0.5, 1.5).to(dtype)
+    print("case", dict(shape=shape, dtype=str(dtype)), flush=True)
+    y, rstd, x = torch.ops.npu.npu_add_rms_norm(x1.to(DEV), x2.to(DEV), gamma.to(DEV), 1e-6)
+    wy, wr, wx = G.add_rms_norm(f32np(x1), f32np(x2), f32np(gamma), 1e-6, NAMES[dtype])
+    np.testing.assert_array_equal(f32np(x), wx)
+    np.testing.assert_allclose(rstd.cpu().numpy().reshape(wr.shape), wr, rtol=1e-5)
+    assert_close(f32np(y), wy)
+    if dtype == torch.float32:
+        return  # the fused quantising op takes half-precision inputs
+    sm1 = uniform((h,), g, 0.5, 2.0) if rng.random() < 0.7 else None
+    second = sm1 is not None and rng.random() < 0.5
+    sm2 = uniform((h,), g, 0.5, 2.0) if second else None
+    beta = randn((h,), g, dtype) if rng.random() < 0.5 else None
+    dv = lambda v: None if v is None else v.to(DEV)  # noqa: E731
+    y1, y2, xo, s1, s2 = torch.ops.npu.npu_add_rms_norm_dynamic_quant(
+        x1.to(DEV), x2.to(DEV), gamma.to(DEV), smooth_scale1=dv(sm1), smooth_scale2=dv(sm2), beta=dv(beta),
+        epsilon=1e-6, output_mask=[True, second])
+    npf = lambda v: None if v is None else f32np(v)  # noqa: E731
+    w1, w2, wx2, ws1, ws2 = G.add_rms_norm_dynamic_quant(f32np(x1), f32np(x2), f32np(gamma), npf(sm1), npf(sm2),
+                                                         npf(beta), 1e-6, second, NAMES[dtype])
+    assert_int8_close(y1.cpu().numpy(), w1)
+    np.testing.assert_array_equal(f32np(xo), wx2)
+    np.testing.assert_allclose(s1.cpu().numpy().reshape(ws1.shape), ws1, rtol=1e-5)
+    if second:
+        assert_int8_close(y2.cpu().numpy(), w2)
+        np.testing.assert_allclose(s2.cpu().numpy().reshape(ws2.shape), ws2, rtol=1e-5)
