@@ -214,3 +214,40 @@ def test_add_rms_norm_family_random(seed):
     if second:
         assert_int8_close(y2.cpu().numpy(), w2)
         np.testing.assert_allclose(s2.cpu().numpy().reshape(ws2.shape), ws2, rtol=1e-5)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_scatter_pa_kv_cache_random(seed):
+    """Seeded random npu_scatter_pa_kv_cache: token counts, heads, key / value widths, block counts and
+    sizes, dtypes, both cache layouts, skipped (negative) slots, int32 / int64 slot mappings."""
+    rng = np.random.default_rng(9500 + seed)
+    g = gen(9500 + seed)
+    dtype = [torch.bfloat16, torch.float16, torch.int8, torch.float32][int(rng.integers(0, 4))]
+    mode = "PA_NZ" if rng.random() < 0.4 else "Norm"
+    esz = torch.tensor([], dtype=dtype).element_size()
+    last = 32 // esz
+    h = int(rng.integers(1, 9))
+    dk = last * int(rng.integers(1, 9))
+    dv = last * int(rng.integers(1, 9))
+    nb, bs = int(rng.integers(1, 12)), int(rng.choice([16, 32, 64, 128]))
+    t = int(rng.integers(1, nb * bs + 1))
+    if dtype == torch.int8:
+        key = torch.randint(-127, 128, (t, h, dk), generator=g, dtype=torch.int8)
+        val = torch.randint(-127, 128, (t, h, dv), generator=g, dtype=torch.int8)
+    else:
+        key, val = randn((t, h, dk), g, dtype), randn((t, h, dv), g, dtype)
+    if mode == "Norm":
+        kc, vc = torch.zeros(nb, bs, h, dk, dtype=dtype), torch.zeros(nb, bs, h, dv, dtype=dtype)
+    else:
+        kc = torch.zeros(nb, h * dk // last, bs, last, dtype=dtype)
+        vc = torch.zeros(nb, h * dv // last, bs, last, dtype=dtype)
+    slots = torch.randperm(nb * bs, generator=g)[:t]
+    slots[torch.rand(t, generator=g) < 0.1] = -1
+    slots = slots.to(torch.int32 if rng.random() < 0.5 else torch.int64)
+    print("case", dict(dtype=str(dtype), mode=mode, t=t, h=h, dk=dk, dv=dv, nb=nb, bs=bs), flush=True)
+    ko, vo = torch.ops.npu.npu_scatter_pa_kv_cache_functional(key.to(DEV), val.to(DEV), kc.to(DEV), vc.to(DEV),
+                                                              slots.to(DEV), cache_mode=mode)
+    to_np = (lambda a: a.numpy()) if dtype in (torch.int8, torch.float32) else f32np
+    wk, wv = G.scatter_pa_kv_cache(to_np(key), to_np(val), to_np(kc), to_np(vc), slots.numpy(), mode)
+    np.testing.assert_array_equal(to_np(ko.cpu()), wk)
+    np.testing.assert_array_equal(to_np(vo.cpu()), wv)
