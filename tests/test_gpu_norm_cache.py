@@ -251,3 +251,53 @@ def test_scatter_pa_kv_cache_random(seed):
     wk, wv = G.scatter_pa_kv_cache(to_np(key), to_np(val), to_np(kc), to_np(vc), slots.numpy(), mode)
     np.testing.assert_array_equal(to_np(ko.cpu()), wk)
     np.testing.assert_array_equal(to_np(vo.cpu()), wv)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_kv_rmsnorm_rope_cache_random(seed):
+    """Seeded random MLA cache writes: batch and step counts, PA (block counts and sizes) or Norm
+    layouts, skipped rows, bf16 / fp16, and the int8 latent with per-token scales."""
+    rng = np.random.default_rng(9700 + seed)
+    g = gen(9700 + seed)
+    b, s = int(rng.integers(1, 6)), int(rng.integers(1, 40))
+    dtype = torch.bfloat16 if rng.random() < 0.6 else torch.float16
+    kv, gamma, cos, sin = _mla(g, b, s, dtype=dtype)
+    mode = "PA" if rng.random() < 0.7 else "Norm"
+    int8_lat = mode == "PA" and rng.random() < 0.5
+    case = dict(b=b, s=s, dtype=str(dtype), mode=mode, int8=int8_lat)
+    if mode == "PA":
+        bs = int(rng.choice([16, 32, 64, 128]))
+        nb = (b * s + bs - 1) // bs + int(rng.integers(0, 3))
+        idx = torch.randperm(nb * bs, generator=g)[:b * s].to(torch.int64)
+        kc = torch.zeros(nb, bs, 1, 64, dtype=dtype)
+        cc = torch.zeros(nb, bs, 1, 512, dtype=torch.int8 if int8_lat else dtype)
+    else:
+        scache = s + int(rng.integers(0, 8))
+        idx = torch.stack([torch.randperm(scache, generator=g)[:s] for _ in range(b)]).to(torch.int64)
+        kc = randn((b, 1, scache, 64), g, dtype)
+        cc = randn((b, 1, scache, 512), g, dtype)
+    idx.view(-1)[torch.rand(idx.numel(), generator=g) < 0.1] = -1
+    case["idx"] = tuple(idx.shape)
+    print("case", case, flush=True)
+    kd, cd = kc.to(DEV), cc.to(DEV)
+    kw = {}
+    tok = None
+    if int8_lat:
+        tok = torch.zeros(kc.shape[0], kc.shape[1], dtype=torch.float32, device=DEV)
+        kw["c_kv_scale"] = tok
+    kr, ckv = torch.ops.npu.npu_kv_rmsnorm_rope_cache_v2(kv.to(DEV), gamma.to(DEV), cos.to(DEV), sin.to(DEV),
+                                                         idx.to(DEV), kd, cd, epsilon=1e-5, cache_mode=mode, **kw)
+    name = NAMES[dtype]
+    res = G.kv_rmsnorm_rope_cache(f32np(kv), f32np(gamma), f32np(cos), f32np(sin), idx.numpy(), f32np(kc),
+                                  cc.numpy() if int8_lat else f32np(cc), 1e-5, mode,
+                                  c_kv_token_scale=np.zeros(tuple(kc.shape[:2]), np.float32) if int8_lat else None,
+                                  dtype=name)
+    wk, wc, wkr, wckv = res[:4]
+    np.testing.assert_array_equal(f32np(kr), wkr)
+    assert_close(f32np(ckv), wckv)
+    np.testing.assert_array_equal(f32np(kd.cpu()), wk)
+    if int8_lat:
+        assert_int8_close(cd.cpu().numpy(), wc)
+        np.testing.assert_allclose(tok.cpu().numpy(), res[4], rtol=1e-5)
+    else:
+        assert_close(f32np(cd.cpu()), wc)
