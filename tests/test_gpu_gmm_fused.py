@@ -180,3 +180,64 @@ def test_swiglu_quant_v2_smooth_scale_and_bias(bias_kind, smooth_kind):
                                      cnt.numpy(), activate_left=True)
     assert_int8_close(y.cpu().numpy(), wy)
     np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)
+
+
+_EDGE = [0, 1, 31, 32, 33, 64, 127, 128, 129, 255, 256, 257, 300]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_swiglu_quant_v2_random(seed):
+    """Seeded random npu_grouped_matmul_swiglu_quant_v2: group sizes at the tile boundaries (empty groups,
+    the 128- and 256-row tiles), rows past the total, K, N and both weight layouts, count and cumsum lists."""
+    rng = np.random.default_rng(10000 + seed)
+    g = gen(10000 + seed)
+    e = int(rng.integers(1, 8))
+    counts = [int(rng.choice(_EDGE)) for _ in range(e)]
+    layout = "KN" if rng.random() < 0.6 else "NK"
+    n = int(rng.choice([512, 1024, 1536]))
+    k = 128 * int(rng.integers(1, 12))
+    extra = int(rng.integers(0, 20))
+    list_type = int(rng.integers(0, 2))
+    x, w, ws, xs, cnt = _case(g, counts, k, n, sum(counts) + extra)
+    wd = w.to(DEV) if layout == "KN" else w.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    gl = cnt if list_type == 1 else torch.cumsum(cnt, 0)
+    print("case", dict(counts=counts, layout=layout, n=n, k=k, extra=extra, list_type=list_type), flush=True)
+    y, s = npu.npu_grouped_matmul_swiglu_quant_v2(x.to(DEV), [wd], [ws.to(DEV)], xs.to(DEV), gl.to(DEV),
+                                                  group_list_type=list_type)
+    wy, wsc = G.grouped_matmul_swiglu_quant(x.numpy(), w.numpy(), ws.numpy(), xs.numpy(), cnt.numpy(), 1)
+    assert_int8_close(y.cpu().numpy(), wy)
+    np.testing.assert_allclose(s.cpu().numpy(), wsc, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_finalize_routing_random(seed):
+    """Seeded random npu_grouped_matmul_finalize_routing: tokens, top-k, experts (some empty), K, N, both
+    weight layouts, with and without the shared input."""
+    rng = np.random.default_rng(10100 + seed)
+    g = gen(10100 + seed)
+    t, kk = int(rng.integers(1, 200)), int(rng.integers(1, 9))
+    e = int(rng.integers(kk, 3 * kk + 2))
+    k, n = 64 * int(rng.integers(1, 12)), int(rng.choice([128, 256, 384, 512, 1024]))
+    layout = "KN" if rng.random() < 0.5 else "NK"
+    idx = torch.stack([torch.randperm(e, generator=g)[:kk] for _ in range(t)]).to(torch.int32)
+    order = torch.argsort(idx.reshape(-1).to(torch.int64), stable=True)
+    row_index = (order // kk).to(torch.int64)
+    counts = torch.bincount(idx.reshape(-1).to(torch.int64), minlength=e)
+    x, w, sc, pts, _ = _case(g, counts.tolist(), k, n)
+    logit = uniform((t * kk,), g, 0.0, 1.0)
+    wd = w.to(DEV) if layout == "KN" else w.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    kw = {}
+    shared = None
+    if rng.random() < 0.5:
+        off = int(rng.integers(0, 5))
+        shared = torch.randn(max(t - off, 1), n, generator=g).to(torch.bfloat16)
+        kw = dict(shared_input=shared.to(DEV), shared_input_weight=0.25, shared_input_offset=off)
+    print("case", dict(t=t, kk=kk, e=e, k=k, n=n, layout=layout, shared=shared is not None), flush=True)
+    y = npu.npu_grouped_matmul_finalize_routing(x.to(DEV), wd, counts.to(DEV), scale=sc.to(DEV),
+                                                pertoken_scale=pts.to(DEV), logit=logit.to(DEV),
+                                                row_index=row_index.to(DEV), output_bs=t, group_list_type=1, **kw)
+    want = G.grouped_matmul_finalize_routing(x.numpy(), w.numpy(), counts.numpy(), 1, sc.numpy(), pts.numpy(), None,
+                                             logit.numpy(), row_index.numpy(),
+                                             None if shared is None else f32np(shared),
+                                             kw.get("shared_input_weight", 1.0), kw.get("shared_input_offset", 0), t)
+    assert_close(y.cpu().numpy(), want)
