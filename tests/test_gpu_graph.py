@@ -287,3 +287,36 @@ def test_compiled_inputs_by_address_replay_in_place_and_copy_a_moved_input():
         _churn()
         check(xb)
     assert tai_graph.stats["captures"] == c1
+
+
+def test_compiled_packed_tnd_chunked_prefill_is_captured():
+    """Packed TND queries over a paged cache with host-list cumulative ends (constants of the captured
+    graph) and an int8 attention_out: each replay equals eager."""
+    g = torch.Generator().manual_seed(53)
+    hq, hkv, d, bs, width = 8, 2, 128, 64, 8
+    lk = [100, 1, 300, 64]
+    lq = [2, 1, 5, 3]
+    b = len(lk)
+    cq = np.cumsum(lq).tolist()
+    nblk = b * width
+    kc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    bt = _paged(g, lk, nblk, width, bs, hkv, d).to(DEV)
+    qs = torch.tensor([25.0], device=DEV)
+
+    def step(q):
+        return torch.ops.npu.npu_fused_infer_attention_score(
+            q, kc, vc, actual_seq_lengths=cq, actual_seq_lengths_kv=lk, block_table=bt, num_heads=hq,
+            num_key_value_heads=hkv, input_layout="TND", block_size=bs, scale=1.0 / math.sqrt(d), sparse_mode=3,
+            quant_scale2=qs)[0]
+
+    fn = torch.compile(step, backend=_backend(), fullgraph=True)
+    caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+    for i in range(3):
+        q = torch.randn(sum(lq), hq, d, generator=g).to(torch.bfloat16).to(DEV)
+        got = fn(q).clone()
+        assert got.dtype == torch.int8
+        assert torch.equal(got, step(q)), f"replay {i}"
+        _churn()
+    assert tai_graph.stats["captures"] == caps + 1
+    assert tai_graph.stats["eager_fallbacks"] == falls
