@@ -320,3 +320,43 @@ def test_compiled_packed_tnd_chunked_prefill_is_captured():
         _churn()
     assert tai_graph.stats["captures"] == caps + 1
     assert tai_graph.stats["eager_fallbacks"] == falls
+
+
+def test_compiled_int8_query_and_learnable_sink_are_captured():
+    """The int8 query (UINT64 dequant scales, converted inside the op) and the v2 learnable_sink, each
+    captured once and equal to eager on every replay."""
+    g = torch.Generator().manual_seed(54)
+    b, s, hq, hkv, d = 2, 16, 4, 2, 64
+    k8 = torch.randint(-128, 128, (b, s, hkv * d), generator=g, dtype=torch.int8).to(DEV)
+    v8 = torch.randint(-128, 128, (b, s, hkv * d), generator=g, dtype=torch.int8).to(DEV)
+
+    def u64(x):
+        return torch.tensor([int(np.array([x], np.float32).view(np.uint32)[0])], dtype=torch.int64, device=DEV)
+
+    d1, q1, d2 = u64(4e-4), torch.tensor([127.0], device=DEV), u64(1e-4)
+
+    def step_q8(q):
+        return torch.ops.air.npu_fused_infer_attention_score(
+            q, k8, v8, num_heads=hq, num_key_value_heads=hkv, input_layout="BSH", scale=1 / math.sqrt(d),
+            sparse_mode=3, dequant_scale1=d1, quant_scale1=q1, dequant_scale2=d2)[0]
+
+    kb = torch.randn(b, s, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    vb = torch.randn(b, s, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    sink = torch.randn(hq, generator=g).to(torch.bfloat16).to(DEV)
+
+    def step_sink(q):
+        return torch.ops.air.npu_fused_infer_attention_score_v2(
+            q, kb, vb, num_query_heads=hq, num_key_value_heads=hkv, input_layout="BSH",
+            softmax_scale=1 / math.sqrt(d), sparse_mode=3, learnable_sink=sink)[0]
+
+    for step, make in ((step_q8, lambda: torch.randint(-128, 128, (b, s, hq * d), generator=g, dtype=torch.int8)),
+                       (step_sink, lambda: torch.randn(b, s, hq * d, generator=g).to(torch.bfloat16))):
+        fn = torch.compile(step, backend=_backend(), fullgraph=True)
+        caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+        for i in range(3):
+            q = make().to(DEV)
+            got = fn(q).clone()
+            assert torch.equal(got, step(q)), f"{step.__name__} replay {i}"
+            _churn()
+        assert tai_graph.stats["captures"] == caps + 1
+        assert tai_graph.stats["eager_fallbacks"] == falls
