@@ -19,6 +19,7 @@ __device__ __forceinline__ float half_to_f32(uint16_t v, bool f16) { return f16 
 struct GenArgs {
   tai_fia_general_args a;
   bool f16;
+  int parts;  // waves per (sequence, head, row): 1, 2 or 4, each taking every parts-th key chunk
 };
 
 // Index of an antiquant scale: per channel (mode 0, channel c), per token (mode 1, (b, t)) or per
@@ -48,10 +49,15 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const tai_fia_general_args& a = ga.a;
   const bool f16 = ga.f16;
   __shared__ float qs[kGenWaves][kGenMaxDk];
+  __shared__ float part_ml[kGenWaves][2];
+  __shared__ float part_o[kGenWaves][kGenMaxDv];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // parts waves share one item; wave `part` takes key chunks part, part + parts, ... and the
+  // group's first wave merges their softmax states through LDS
+  const int parts = ga.parts, part = w % parts;
   // (b, h, i), i fastest; the launch's last workgroup may hold waves past the end, which run item 0
-  // to the barrier and then stop
-  const int64_t item0 = static_cast<int64_t>(blockIdx.x) * kGenWaves + w;
+  // with no keys through the barriers and write nothing
+  const int64_t item0 = static_cast<int64_t>(blockIdx.x) * (kGenWaves / parts) + w / parts;
   const bool in_range = item0 < (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
   const int64_t item = in_range ? item0 : 0;
   // (qb, qt): the batch and row that address query, out and lse; (b, i): the sequence and the
@@ -116,10 +122,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     }
   }
   __syncthreads();  // (each wave reads only its own row; the barrier orders the LDS writes)
-  if (!in_range) return;
   // visible kv range of query i
   const int64_t off = a.mask_origin ? lk - lq : 0;
-  const int64_t hi = i < lq ? imin64(lk, i + off + a.next_tokens + 1) : 0;
+  const int64_t hi = in_range && i < lq ? imin64(lk, i + off + a.next_tokens + 1) : 0;
   const int64_t lo = imax64(0, i + off - a.pre_tokens);
   float m = -INFINITY, l = 0.0f;
   float o[kGenDvPerLane];
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
 #pragma unroll
     for (int e = 0; e < kGenDvPerLane; ++e) o[e] = __fmul_rn(static_cast<float>(oi[e]), a.deq_scale2[0]);
   } else
-  for (int64_t t0 = lo; t0 < hi; t0 += 64) {
+  for (int64_t t0 = lo + 64 * part; t0 < hi; t0 += 64 * parts) {
     const int64_t j = t0 + lane;
     bool valid = j < hi;
     if (valid && a.mask) valid = a.mask[b * a.mask_strides[0] + i * a.mask_strides[1] + j * a.mask_strides[2]] == 0;
@@ -233,33 +238,75 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     l = l * alpha + wave_sum(p);
 #pragma unroll
     for (int e = 0; e < kGenDvPerLane; ++e) o[e] *= alpha;
-    const int64_t nj = imin64(64, hi - t0);
-    for (int jj = 0; jj < nj; ++jj) {
-      const float pj = __shfl(p, jj, 64);
-      if (pj == 0.0f) continue;  // masked (wave-uniform)
-      if (KV8 && t0 + jj >= lp) {
-        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kb, kvh);
+    // P V, eight tokens at a time: the eight value rows' loads go out together before their products
+    // (one token at a time, each load waited out its own latency). Every token below nj lies inside
+    // the sequence, so its row is read even when its P is zero (a masked token adds 0 * v, no change).
+    const int nj = static_cast<int>(imin64(64, hi - t0));
+    constexpr int kU = 8;
+    for (int jj = 0; jj < nj; jj += kU) {
+      float pv[kU];
+      float val[kU][kGenDvPerLane];
 #pragma unroll
-        for (int e = 0; e < kGenDvPerLane; ++e) {
-          const int d = lane + 64 * e;
-          if (d < a.dv)
-            o[e] += pj * antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
-                                   antiquant_index(a, a.v_quant_mode, b, t0 + jj - lp, static_cast<int64_t>(kvh) * a.dv + d));
+      for (int u = 0; u < kU; ++u) {
+        const bool in = jj + u < nj;
+        pv[u] = __shfl(p, in ? jj + u : 0, 64);
+        const int64_t t = t0 + (in ? jj + u : 0);
+        if (KV8 && t >= lp) {
+          const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t + kb, kvh);
+#pragma unroll
+          for (int e = 0; e < kGenDvPerLane; ++e) {
+            const int d = lane + 64 * e;
+            val[u][e] = d < a.dv ? antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
+                                             antiquant_index(a, a.v_quant_mode, b, t - lp,
+                                                             static_cast<int64_t>(kvh) * a.dv + d))
+                                 : 0.0f;
+          }
+        } else {
+          const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
+                                            kvh * a.v_prefix_strides[1]
+                                      : vv + gen_row(a, a.v_strides, b, t + kb, kvh);
+#pragma unroll
+          for (int e = 0; e < kGenDvPerLane; ++e) {
+            const int d = lane + 64 * e;
+            val[u][e] = d < a.dv ? half_to_f32(vr[d], f16) : 0.0f;
+          }
         }
-      } else {
-        const int64_t t = t0 + jj;
-        const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
-                                          kvh * a.v_prefix_strides[1]
-                                    : vv + gen_row(a, a.v_strides, b, t + kb, kvh);
+      }
 #pragma unroll
-        for (int e = 0; e < kGenDvPerLane; ++e) {
-          const int d = lane + 64 * e;
-          if (d < a.dv) o[e] += pj * half_to_f32(vr[d], f16);
+      for (int u = 0; u < kU; ++u) {
+        if (jj + u < nj) {
+#pragma unroll
+          for (int e = 0; e < kGenDvPerLane; ++e) o[e] += pv[u] * val[u][e];
         }
       }
     }
     m = m_new;
   }
+  if (parts > 1) {
+    if (lane == 0) {
+      part_ml[w][0] = m;
+      part_ml[w][1] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) part_o[w][lane + 64 * e] = o[e];
+    __syncthreads();
+    if (part == 0) {
+      float mm = -INFINITY;
+      for (int p = 0; p < parts; ++p) mm = fmaxf(mm, part_ml[w + p][0]);
+      l = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kGenDvPerLane; ++e) o[e] = 0.0f;
+      for (int p = 0; p < parts; ++p) {
+        const float mp = part_ml[w + p][0];
+        const float f = mp == -INFINITY ? 0.0f : expf(mp - mm);
+        l += part_ml[w + p][1] * f;
+#pragma unroll
+        for (int e = 0; e < kGenDvPerLane; ++e) o[e] += part_o[w + p][lane + 64 * e] * f;
+      }
+      m = mm;
+    }
+  }
+  if (!in_range || part != 0) return;
   if (a.sink && i < lq && a.sink[h] != -INFINITY) {
     // the sink joins the denominator: the reference max and the sum take it in, O gains nothing
     const float sv = a.sink[h];
@@ -351,13 +398,17 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
   TAI_CHECK_ARG((reinterpret_cast<uintptr_t>(a.k1) % kalign) == 0 && a.k1_strides[0] % kel == 0 &&
                     a.k1_strides[1] % kel == 0 && a.k1_strides[2] % kel == 0,
                 "tai_fia_general: key rows must be %d-byte aligned", kalign);
-  GenArgs ga{a, a.dtype == TAI_DT_FP16};
+  GenArgs ga{a, a.dtype == TAI_DT_FP16, 1};
   // pre / next at or beyond 2^40 tokens are no bound
   constexpr int64_t kNoBound = int64_t(1) << 40;
   ga.a.pre_tokens = imin64(imax64(a.pre_tokens, -kNoBound), kNoBound);
   ga.a.next_tokens = imin64(imax64(a.next_tokens, -kNoBound), kNoBound);
-  const int64_t waves = (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
-  const dim3 grid(static_cast<unsigned>(cdiv(waves, kGenWaves)));
+  const int64_t items = (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
+  // few items over long key ranges: split each item's keys over 2 or 4 waves (the int8-query
+  // path's two passes need the whole row's max first and keep one wave per item)
+  const int64_t kv_span = (a.block_table ? a.max_blocks * a.block_size : a.s_kv) + (a.k_prefix ? a.prefix_cap : 0);
+  if (!qq && kv_span >= 256) ga.parts = items <= 4096 ? 4 : items <= 16384 ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(cdiv(items, kGenWaves / ga.parts)));
   if (kv8) fia_general_kernel<true><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
   else fia_general_kernel<false><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
   return launch_status("tai_fia_general");
