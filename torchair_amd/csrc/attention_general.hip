@@ -107,6 +107,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const int64_t kb = kv_base - lp;
   const int64_t o_off = qb * a.out_strides[0] + qt * a.out_strides[1] + h * a.out_strides[2];
   const int dk = a.dk1 + a.dk2;
+  const bool qq = KV8 && a.q_dtype == TAI_DT_INT8;
+  // per-channel int8 keys / values with no shared prefix fold their antiquant into the query / output
+  const bool fold_k = KV8 && !qq && a.k_quant_mode == 0 && !a.k_prefix;
+  const bool fold_v = KV8 && !qq && a.v_quant_mode == 0 && !a.v_prefix;
+  float k_bias = 0.0f;
   // the query as fp32 in this wave's LDS row
   {
     const uint16_t* q1 = static_cast<const uint16_t*>(a.q1) + qb * a.q1_strides[0] + qt * a.q1_strides[1] + h * a.q1_strides[2];
@@ -117,6 +122,20 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       const int8_t* q8 = static_cast<const int8_t*>(a.q1) + qb * a.q1_strides[0] + qt * a.q1_strides[1] +
                          h * a.q1_strides[2];
       for (int d = lane; d < dk; d += 64) qs[w][d] = static_cast<float>(q8[d]);
+    } else if (fold_k) {
+      // per-channel int8 keys: q.((k + off) * sc) = (q * sc).k + sum(q * sc * off), the scale folded
+      // into the query once per row
+      float kb = 0.0f;
+      for (int d = lane; d < dk; d += 64) {
+        float x = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
+        if (d < a.dk1) {
+          const int64_t c = static_cast<int64_t>(kvh) * a.dk1 + d;
+          x *= a.k_scale[c];
+          if (a.k_offset) kb += x * a.k_offset[c];
+        }
+        qs[w][d] = x;
+      }
+      k_bias = wave_sum(kb);
     } else {
       for (int d = lane; d < dk; d += 64) qs[w][d] = d < a.dk1 ? half_to_f32(q1[d], f16) : half_to_f32(q2[d - a.dk1], f16);
     }
@@ -133,7 +152,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const uint16_t* k1 = static_cast<const uint16_t*>(a.k1);
   const uint16_t* k2 = static_cast<const uint16_t*>(a.k2);
   const uint16_t* vv = static_cast<const uint16_t*>(a.v);
-  if (KV8 && a.q_dtype == TAI_DT_INT8) {
+  if (qq) {
     // int8 query, key and value: two passes over the visible keys, the first for the row max and sum,
     // the second quantising P against the final max (so the result does not depend on the chunking) and
     // accumulating P8.V exactly in int32. Each score's q.k sum is of integer products below 2^24 in
@@ -198,14 +217,21 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         for (int d = 0; d < a.dk1; d += 8) {
           const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
           const uint32_t wd[2] = {u.x, u.y};
+          if (fold_k) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
-            acc += antiquant(x, a.k_scale, a.k_offset,
-                             antiquant_index(a, a.k_quant_mode, b, j - lp, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
-                   qs[w][d + q];
+            for (int q = 0; q < 8; ++q)
+              acc += static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu)) * qs[w][d + q];
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
+              acc += antiquant(x, a.k_scale, a.k_offset,
+                               antiquant_index(a, a.k_quant_mode, b, j - lp, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
+                     qs[w][d + q];
+            }
           }
         }
+        acc += k_bias;
       } else {
         const uint16_t* kr = j < lp ? static_cast<const uint16_t*>(a.k_prefix) + j * a.k_prefix_strides[0] +
                                           kvh * a.k_prefix_strides[1]
@@ -256,10 +282,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
 #pragma unroll
           for (int e = 0; e < kGenDvPerLane; ++e) {
             const int d = lane + 64 * e;
-            val[u][e] = d < a.dv ? antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
+            val[u][e] = d >= a.dv ? 0.0f
+                        : fold_v ? static_cast<float>(vr[d])
+                                 : antiquant(static_cast<float>(vr[d]), a.v_scale, a.v_offset,
                                              antiquant_index(a, a.v_quant_mode, b, t - lp,
-                                                             static_cast<int64_t>(kvh) * a.dv + d))
-                                 : 0.0f;
+                                                             static_cast<int64_t>(kvh) * a.dv + d));
           }
         } else {
           const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
@@ -307,6 +334,17 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     }
   }
   if (!in_range || part != 0) return;
+  if (fold_v) {
+    // sum p (v + off) sc = (sum p v + off l) sc, per value channel
+#pragma unroll
+    for (int e = 0; e < kGenDvPerLane; ++e) {
+      const int d = lane + 64 * e;
+      if (d < a.dv) {
+        const int64_t c = static_cast<int64_t>(kvh) * a.dv + d;
+        o[e] = (o[e] + (a.v_offset ? a.v_offset[c] * l : 0.0f)) * a.v_scale[c];
+      }
+    }
+  }
   if (a.sink && i < lq && a.sink[h] != -INFINITY) {
     // the sink joins the denominator: the reference max and the sum take it in, O gains nothing
     const float sv = a.sink[h];
