@@ -4,6 +4,8 @@
 // row); a 64-token chunk of keys puts one token on each lane (its score is a dot product against the
 // query, held in LDS as fp32), the chunk's softmax statistics are wave reductions, and the value rows
 // are accumulated with the lane owning value dims lane, lane + 64, ... Every product and sum is fp32.
+#include <type_traits>
+
 #include "common.h"
 
 namespace tai {
@@ -44,7 +46,8 @@ __device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const 
   return b * st[0] + tok * st[1] + kvh * st[2];
 }
 
-template <bool KV8>
+// NE: value dims per lane (dv <= 64 * NE)
+template <bool KV8, int NE>
 __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga) {
   const tai_fia_general_args& a = ga.a;
   const bool f16 = ga.f16;
@@ -57,7 +60,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const int parts = ga.parts, part = w % parts;
   // (b, h, i), i fastest; the launch's last workgroup may hold waves past the end, which run item 0
   // with no keys through the barriers and write nothing
-  const int64_t item0 = static_cast<int64_t>(blockIdx.x) * (kGenWaves / parts) + w / parts;
+  // workgroups are dealt to the 8 XCDs in turn: renumber them so each XCD runs a contiguous range of
+  // items (a GQA group's heads, which read the same keys and values, then share one L2)
+  const uint32_t nblk = gridDim.x, xcd = blockIdx.x % 8u, per = nblk / 8u;
+  const uint32_t blk = xcd * per + min(xcd, nblk % 8u) + blockIdx.x / 8u;
+  const int64_t item0 = static_cast<int64_t>(blk) * (kGenWaves / parts) + w / parts;
   const bool in_range = item0 < (a.q_cum ? 1 : a.b) * a.hq * a.s_q;
   const int64_t item = in_range ? item0 : 0;
   // (qb, qt): the batch and row that address query, out and lse; (b, i): the sequence and the
@@ -146,9 +153,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   const int64_t hi = in_range && i < lq ? imin64(lk, i + off + a.next_tokens + 1) : 0;
   const int64_t lo = imax64(0, i + off - a.pre_tokens);
   float m = -INFINITY, l = 0.0f;
-  float o[kGenDvPerLane];
+  float o[NE];
 #pragma unroll
-  for (int e = 0; e < kGenDvPerLane; ++e) o[e] = 0.0f;
+  for (int e = 0; e < NE; ++e) o[e] = 0.0f;
   const uint16_t* k1 = static_cast<const uint16_t*>(a.k1);
   const uint16_t* k2 = static_cast<const uint16_t*>(a.k2);
   const uint16_t* vv = static_cast<const uint16_t*>(a.v);
@@ -181,9 +188,9 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       l = l * (m == -INFINITY ? 0.0f : expf(m - m_new)) + wave_sum(valid ? expf(s - m_new) : 0.0f);
       m = m_new;
     }
-    int32_t oi[kGenDvPerLane];
+    int32_t oi[NE];
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) oi[e] = 0;
+    for (int e = 0; e < NE; ++e) oi[e] = 0;
     const float qs1 = a.quant_scale1[0];
     for (int64_t t0 = lo; t0 < hi && m != -INFINITY; t0 += 64) {
       bool valid;
@@ -195,14 +202,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         if (pj == 0) continue;  // masked or rounded to zero (wave-uniform)
         const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kb, kvh);
 #pragma unroll
-        for (int e = 0; e < kGenDvPerLane; ++e) {
+        for (int e = 0; e < NE; ++e) {
           const int d = lane + 64 * e;
           if (d < a.dv) oi[e] += pj * static_cast<int32_t>(vr[d]);
         }
       }
     }
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) o[e] = __fmul_rn(static_cast<float>(oi[e]), a.deq_scale2[0]);
+    for (int e = 0; e < NE; ++e) o[e] = __fmul_rn(static_cast<float>(oi[e]), a.deq_scale2[0]);
   } else
   for (int64_t t0 = lo + 64 * part; t0 < hi; t0 += 64 * parts) {
     const int64_t j = t0 + lane;
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     const float p = valid ? expf(s - m_new) : 0.0f;
     l = l * alpha + wave_sum(p);
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) o[e] *= alpha;
+    for (int e = 0; e < NE; ++e) o[e] *= alpha;
     // P V, eight tokens at a time: the eight value rows' loads go out together before their products
     // (one token at a time, each load waited out its own latency). Every token below nj lies inside
     // the sequence, so its row is read even when its P is zero (a masked token adds 0 * v, no change).
@@ -271,7 +278,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     constexpr int kU = 8;
     for (int jj = 0; jj < nj; jj += kU) {
       float pv[kU];
-      float val[kU][kGenDvPerLane];
+      float val[kU][NE];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const bool in = jj + u < nj;
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         if (KV8 && t >= lp) {
           const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t + kb, kvh);
 #pragma unroll
-          for (int e = 0; e < kGenDvPerLane; ++e) {
+          for (int e = 0; e < NE; ++e) {
             const int d = lane + 64 * e;
             val[u][e] = d >= a.dv ? 0.0f
                         : fold_v ? static_cast<float>(vr[d])
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
                                             kvh * a.v_prefix_strides[1]
                                       : vv + gen_row(a, a.v_strides, b, t + kb, kvh);
 #pragma unroll
-          for (int e = 0; e < kGenDvPerLane; ++e) {
+          for (int e = 0; e < NE; ++e) {
             const int d = lane + 64 * e;
             val[u][e] = d < a.dv ? half_to_f32(vr[d], f16) : 0.0f;
           }
@@ -303,7 +310,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       for (int u = 0; u < kU; ++u) {
         if (jj + u < nj) {
 #pragma unroll
-          for (int e = 0; e < kGenDvPerLane; ++e) o[e] += pv[u] * val[u][e];
+          for (int e = 0; e < NE; ++e) o[e] += pv[u] * val[u][e];
         }
       }
     }
@@ -315,20 +322,20 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       part_ml[w][1] = l;
     }
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) part_o[w][lane + 64 * e] = o[e];
+    for (int e = 0; e < NE; ++e) part_o[w][lane + 64 * e] = o[e];
     __syncthreads();
     if (part == 0) {
       float mm = -INFINITY;
       for (int p = 0; p < parts; ++p) mm = fmaxf(mm, part_ml[w + p][0]);
       l = 0.0f;
 #pragma unroll
-      for (int e = 0; e < kGenDvPerLane; ++e) o[e] = 0.0f;
+      for (int e = 0; e < NE; ++e) o[e] = 0.0f;
       for (int p = 0; p < parts; ++p) {
         const float mp = part_ml[w + p][0];
         const float f = mp == -INFINITY ? 0.0f : expf(mp - mm);
         l += part_ml[w + p][1] * f;
 #pragma unroll
-        for (int e = 0; e < kGenDvPerLane; ++e) o[e] += part_o[w + p][lane + 64 * e] * f;
+        for (int e = 0; e < NE; ++e) o[e] += part_o[w + p][lane + 64 * e] * f;
       }
       m = mm;
     }
@@ -337,7 +344,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   if (fold_v) {
     // sum p (v + off) sc = (sum p v + off l) sc, per value channel
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) {
+    for (int e = 0; e < NE; ++e) {
       const int d = lane + 64 * e;
       if (d < a.dv) {
         const int64_t c = static_cast<int64_t>(kvh) * a.dv + d;
@@ -351,14 +358,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
     const float m2 = fmaxf(m, sv);
     const float alpha = m == -INFINITY ? 0.0f : expf(m - m2);
 #pragma unroll
-    for (int e = 0; e < kGenDvPerLane; ++e) o[e] *= alpha;
+    for (int e = 0; e < NE; ++e) o[e] *= alpha;
     l = l * alpha + expf(sv - m2);
     m = m2;
   }
   const bool live = i < lq && l > 0.0f;
   const float inv = live ? 1.0f / l : 0.0f;
 #pragma unroll
-  for (int e = 0; e < kGenDvPerLane; ++e) {
+  for (int e = 0; e < NE; ++e) {
     const int d = lane + 64 * e;
     if (d < a.dv) {
       const float r = o[e] * inv;
@@ -447,7 +454,14 @@ extern "C" int tai_fia_general(const tai_fia_general_args* args, void* stream) {
   const int64_t kv_span = (a.block_table ? a.max_blocks * a.block_size : a.s_kv) + (a.k_prefix ? a.prefix_cap : 0);
   if (!qq && kv_span >= 256) ga.parts = items <= 4096 ? 4 : items <= 16384 ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(cdiv(items, kGenWaves / ga.parts)));
-  if (kv8) fia_general_kernel<true><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
-  else fia_general_kernel<false><<<grid, 64 * kGenWaves, 0, static_cast<hipStream_t>(stream)>>>(ga);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto ne) {
+    constexpr int NE = decltype(ne)::value;
+    if (kv8) fia_general_kernel<true, NE><<<grid, 64 * kGenWaves, 0, st>>>(ga);
+    else fia_general_kernel<false, NE><<<grid, 64 * kGenWaves, 0, st>>>(ga);
+  };
+  if (a.dv <= 128) launch(std::integral_constant<int, 2>{});
+  else if (a.dv <= 256) launch(std::integral_constant<int, 4>{});
+  else launch(std::integral_constant<int, kGenDvPerLane>{});
   return launch_status("tai_fia_general");
 }
