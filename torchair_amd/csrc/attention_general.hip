@@ -40,8 +40,17 @@ __device__ __forceinline__ float antiquant(float x, const float* sc, const float
 
 __device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const int64_t* st, int64_t b, int64_t tok, int kvh) {
   if (a.block_table) {
-    const int64_t blk = a.block_table[b * a.max_blocks + tok / a.block_size];
-    return blk * st[0] + (tok % a.block_size) * st[1] + kvh * st[2];
+    int64_t tb, tr;  // tok / block_size, tok % block_size (32-bit division when both fit)
+    if (tok < (int64_t(1) << 31) && a.block_size < (int64_t(1) << 31)) {
+      const uint32_t t32 = static_cast<uint32_t>(tok), bs32 = static_cast<uint32_t>(a.block_size);
+      tb = t32 / bs32;
+      tr = t32 - static_cast<uint32_t>(tb) * bs32;
+    } else {
+      tb = tok / a.block_size;
+      tr = tok % a.block_size;
+    }
+    const int64_t blk = a.block_table[b * a.max_blocks + tb];
+    return blk * st[0] + tr * st[1] + kvh * st[2];
   }
   return b * st[0] + tok * st[1] + kvh * st[2];
 }
@@ -214,6 +223,8 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
   for (int64_t t0 = lo + 64 * part; t0 < hi; t0 += 64 * parts) {
     const int64_t j = t0 + lane;
     bool valid = j < hi;
+    // this lane's token's value row, handed to every lane of the P V loop by shuffles
+    const int64_t vrow = j < hi && j >= lp ? gen_row(a, a.v_strides, b, j + kb, kvh) : 0;
     if (valid && a.mask) valid = a.mask[b * a.mask_strides[0] + i * a.mask_strides[1] + j * a.mask_strides[2]] == 0;
     float s = -INFINITY;
     if (valid) {
@@ -282,10 +293,14 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const bool in = jj + u < nj;
-        pv[u] = __shfl(p, in ? jj + u : 0, 64);
-        const int64_t t = t0 + (in ? jj + u : 0);
+        const int src = in ? jj + u : 0;
+        pv[u] = __shfl(p, src, 64);
+        const int64_t t = t0 + src;
+        const int64_t vr_off = static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(vrow >> 32), src, 64))) << 32) |
+            static_cast<uint32_t>(__shfl(static_cast<int>(vrow & 0xffffffff), src, 64)));
         if (KV8 && t >= lp) {
-          const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t + kb, kvh);
+          const int8_t* vr = static_cast<const int8_t*>(a.v) + vr_off;
 #pragma unroll
           for (int e = 0; e < NE; ++e) {
             const int d = lane + 64 * e;
@@ -298,7 +313,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         } else {
           const uint16_t* vr = t < lp ? static_cast<const uint16_t*>(a.v_prefix) + t * a.v_prefix_strides[0] +
                                             kvh * a.v_prefix_strides[1]
-                                      : vv + gen_row(a, a.v_strides, b, t + kb, kvh);
+                                      : vv + vr_off;
 #pragma unroll
           for (int e = 0; e < NE; ++e) {
             const int d = lane + 64 * e;
