@@ -56,6 +56,13 @@ __device__ __forceinline__ int64_t gen_row(const tai_fia_general_args& a, const 
 }
 
 // NE: value dims per lane (dv <= 64 * NE)
+// lane src's 64-bit value, as two 32-bit shuffles
+__device__ __forceinline__ int64_t shfl64(int64_t v, int src) {
+  const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(v & 0xffffffff), src, 64));
+  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(v >> 32), src, 64));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 template <bool KV8, int NE>
 __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga) {
   const tai_fia_general_args& a = ga.a;
@@ -206,10 +213,11 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       const float s = score(t0 + lane, valid);
       const int p8 = valid ? static_cast<int>(fminf(fmaxf(rintf(__fmul_rn(expf(s - m), qs1)), 0.0f), 127.0f)) : 0;
       const int64_t nj = imin64(64, hi - t0);
+      const int64_t vrow = t0 + lane < hi ? gen_row(a, a.v_strides, b, t0 + lane + kb, kvh) : 0;
       for (int jj = 0; jj < nj; ++jj) {
         const int pj = __shfl(p8, jj, 64);
         if (pj == 0) continue;  // masked or rounded to zero (wave-uniform)
-        const int8_t* vr = static_cast<const int8_t*>(a.v) + gen_row(a, a.v_strides, b, t0 + jj + kb, kvh);
+        const int8_t* vr = static_cast<const int8_t*>(a.v) + shfl64(vrow, jj);
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
           const int d = lane + 64 * e;
@@ -232,20 +240,30 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
       // int8 own keys (shared-prefix rows, j < lp, stay in the query's dtype)
       if (KV8 && j >= lp) {
         const int8_t* kr = static_cast<const int8_t*>(a.k1) + gen_row(a, a.k1_strides, b, j + kb, kvh);
-        for (int d = 0; d < a.dk1; d += 8) {
-          const uint2 u = *reinterpret_cast<const uint2*>(kr + d);
-          const uint32_t wd[2] = {u.x, u.y};
-          if (fold_k) {
+        for (int d0 = 0; d0 < a.dk1; d0 += 64) {
+          // 64 dims at a time: the eight 8-byte loads go out before their products
+          uint2 uu[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-              acc += static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu)) * qs[w][d + q];
-          } else {
+          for (int g = 0; g < 8; ++g)
+            uu[g] = d0 + 8 * g < a.dk1 ? *reinterpret_cast<const uint2*>(kr + d0 + 8 * g) : make_uint2(0, 0);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
-              acc += antiquant(x, a.k_scale, a.k_offset,
-                               antiquant_index(a, a.k_quant_mode, b, j - lp, static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
-                     qs[w][d + q];
+          for (int g = 0; g < 8; ++g) {
+            const int d = d0 + 8 * g;
+            if (d >= a.dk1) continue;
+            const uint32_t wd[2] = {uu[g].x, uu[g].y};
+            if (fold_k) {
+#pragma unroll
+              for (int q = 0; q < 8; ++q)
+                acc += static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu)) * qs[w][d + q];
+            } else {
+#pragma unroll
+              for (int q = 0; q < 8; ++q) {
+                const float x = static_cast<float>(static_cast<int8_t>((wd[q >> 2] >> (8 * (q & 3))) & 0xffu));
+                acc += antiquant(x, a.k_scale, a.k_offset,
+                                 antiquant_index(a, a.k_quant_mode, b, j - lp,
+                                                 static_cast<int64_t>(kvh) * a.dk1 + d + q)) *
+                       qs[w][d + q];
+              }
             }
           }
         }
@@ -254,13 +272,23 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         const uint16_t* kr = j < lp ? static_cast<const uint16_t*>(a.k_prefix) + j * a.k_prefix_strides[0] +
                                           kvh * a.k_prefix_strides[1]
                                     : k1 + gen_row(a, a.k1_strides, b, j + kb, kvh);
-        for (int d = 0; d < a.dk1; d += 8) {
-          const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
-          const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+        // 64 dims at a time: the eight 16-byte loads go out before their products
+        for (int d0 = 0; d0 < a.dk1; d0 += 64) {
+          uint4 u[8];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc += half_to_f32(static_cast<uint16_t>(wd[q] & 0xffffu), f16) * qs[w][d + 2 * q];
-            acc += half_to_f32(static_cast<uint16_t>(wd[q] >> 16), f16) * qs[w][d + 2 * q + 1];
+          for (int g = 0; g < 8; ++g)
+            u[g] = d0 + 8 * g < a.dk1 ? *reinterpret_cast<const uint4*>(kr + d0 + 8 * g) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            if (d0 + 8 * g < a.dk1) {
+              const int d = d0 + 8 * g;
+              const uint32_t wd[4] = {u[g].x, u[g].y, u[g].z, u[g].w};
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                acc += half_to_f32(static_cast<uint16_t>(wd[q] & 0xffffu), f16) * qs[w][d + 2 * q];
+                acc += half_to_f32(static_cast<uint16_t>(wd[q] >> 16), f16) * qs[w][d + 2 * q + 1];
+              }
+            }
           }
         }
       }
@@ -296,9 +324,7 @@ __global__ __launch_bounds__(64 * kGenWaves) void fia_general_kernel(GenArgs ga)
         const int src = in ? jj + u : 0;
         pv[u] = __shfl(p, src, 64);
         const int64_t t = t0 + src;
-        const int64_t vr_off = static_cast<int64_t>(
-            (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(vrow >> 32), src, 64))) << 32) |
-            static_cast<uint32_t>(__shfl(static_cast<int>(vrow & 0xffffffff), src, 64)));
+        const int64_t vr_off = shfl64(vrow, src);
         if (KV8 && t >= lp) {
           const int8_t* vr = static_cast<const int8_t*>(a.v) + vr_off;
 #pragma unroll
