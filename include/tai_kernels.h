@@ -424,6 +424,15 @@ int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache
                          const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d, int dtype,
                          int block_size, float scale, void* out, float* lse, void* workspace,
                          size_t ws_bytes, void* stream);
+/* The same with learnable_sink (npu_fused_infer_attention_score_v2, prototype
+ * experiment_ops.h:3940): sink [hq] fp32, one logit per query head that joins each row's softmax max
+ * and denominator without a value row (a sink of -inf adds nothing). Workspace as above. */
+int tai_fia_paged_decode_sink(const void* q, const void* k_cache, const void* v_cache,
+                              int64_t stride_block, int64_t stride_slot, int64_t stride_head,
+                              const int32_t* block_table, int64_t max_blocks,
+                              const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d, int dtype,
+                              int block_size, float scale, const float* sink, void* out, float* lse,
+                              void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_fused_infer_attention_score with query sequences (GQA prefill, chunked prefill over a paged

@@ -259,7 +259,10 @@ def fia_cuda(query, key, value, **kw):
            "actual_shared_prefix_len needs key_shared_prefix")
     sink = kw.get("learnable_sink")  # (the v2 op's input)
     _check(sink is None or not qq, "npu_fused_infer_attention_score: learnable_sink is not served with an int8 query")
-    pse = pse if pse is not None else (True if prefix or sink is not None else None)  # all take the general kernel
+    # a sink with nothing else also runs on the one-token decode kernel (its merge takes the sink in);
+    # every other case with a prefix or a sink takes the general kernel
+    sink_only = pse is None and not prefix and sink is not None
+    pse = pse if pse is not None else (True if prefix or sink is not None else None)
     _check(kw.get("quant_offset2") is None or quant_out, "npu_fused_infer_attention_score: quant_offset2 needs "
            "quant_scale2")
     if kw.get("query_rope") is None:
@@ -308,21 +311,29 @@ def fia_cuda(query, key, value, **kw):
                "npu_fused_infer_attention_score: key/value caches must share shape and a dense head dim")
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
+        whole = s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
         # the tiled kernels step through pages 32 tokens at a time
-        if (explicit or kv8 or quant_out or pse is not None or bs % 32 != 0 or d not in (64, 128, 256)
-                or (s > 1 and d not in (64, 128)) or packed):
+        if (explicit or kv8 or quant_out or (pse is not None and not (sink_only and whole)) or bs % 32 != 0
+                or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)) or packed):
             kstr = [sb, ss, sh]
             return _general_call(query, key, value, out, lse, want_lse, ql, num_heads, n_kv, d, dt, kstr, kstr,
                                  bt, bs, seq_q, seq_kv, mask_origin, pre, nxt, explicit, kw, scale, stream,
                                  kv8=kv8, quant_out=quant_out, ol=ol)
         # one query token that the mask leaves the whole prefix: the decode kernel
-        if s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0)):
+        if whole:
             q = query.contiguous()
             ws_bytes = _lib.query("tai_fia_paged_decode_workspace_size", b, num_heads, d, bt.size(1), bs)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
-            _lib.call("tai_fia_paged_decode", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh,
-                      bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, dt, bs, scale, out.data_ptr(),
-                      lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+            head = (q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh, bt.data_ptr(), bt.size(1),
+                    seq_kv.data_ptr(), b, num_heads, n_kv, d, dt, bs, scale)
+            tail = (out.data_ptr(), lse.data_ptr() if want_lse else None, ws.data_ptr(), ws_bytes, stream)
+            if sink is not None:
+                sk = sink.to(torch.float32).reshape(-1).contiguous()
+                _check(sk.numel() == num_heads, f"npu_fused_infer_attention_score: learnable_sink must hold one logit "
+                       f"per query head ({num_heads}), got {sk.numel()}")
+                _lib.call("tai_fia_paged_decode_sink", *head, sk.data_ptr(), *tail)
+            else:
+                _lib.call("tai_fia_paged_decode", *head, *tail)
             return out, lse
         # query sequences over the paged cache (chunked prefill, multi-token decode)
         b, s_q, hq, d = _bsnd(query, ql, num_heads)

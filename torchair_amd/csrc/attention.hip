@@ -98,6 +98,7 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
   int nranges;     // step ranges of a launch (one wave per range and kv head)
   int64_t* steps;  // [0] = balance units of the batch, [1 + b] = units before sequence b
+  const float* sink;  // NULL or [hq] fp32: learnable_sink logits, joined to each row's max and sum by the merge
   float* part_o;   // [slot, hkv, 16, D], slot = range + sequence
   float* part_ml;  // [slot, hkv, 16, 2]
 };
@@ -417,10 +418,13 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
   const int64_t len = kv_len(a, b), S = a.steps[0], x0 = a.steps[1 + b], R = a.nranges;
   const int64_t n = dec_steps(len);
   uint16_t* o = out + (b * a.hq + h) * D + E * lane;
+  // the sink logit in log2 units (-inf: none)
+  const float sv = a.sink ? a.sink[h] * kLog2e : -INFINITY;
   if (n == 0) {
 #pragma unroll
     for (int e = 0; e < E; ++e) o[e] = 0;
-    if (lse && lane == 0) lse[b * a.hq + h] = -INFINITY;
+    // with no keys the sink alone makes the denominator: lse = the sink logit
+    if (lse && lane == 0) lse[b * a.hq + h] = sv != -INFINITY ? sv * kLn2 : -INFINITY;
     return;
   }
   // the sequence's units are [x0, x1); its tokens start kDecSegCost units in
@@ -450,6 +454,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
     den = den * c + w * l;
 #pragma unroll
     for (int e = 0; e < E; ++e) num[e] = num[e] * c + w * v[e];
+    M = m_new;
+  }
+  if (sv != -INFINITY) {
+    // the sink joins the denominator only: it rescales the row like one more partial with no value
+    const float m_new = fmaxf(M, sv);
+    const float c = exp2f(M - m_new);
+    den = den * c + exp2f(sv - m_new);
+#pragma unroll
+    for (int e = 0; e < E; ++e) num[e] *= c;
     M = m_new;
   }
 #pragma unroll
@@ -1698,11 +1711,11 @@ extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, 
   return need;
 }
 
-extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block,
-                                    int64_t stride_slot, int64_t stride_head, const int32_t* block_table,
-                                    int64_t max_blocks, const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
-                                    int dtype, int block_size, float scale, void* out, float* lse, void* workspace,
-                                    size_t ws_bytes, void* stream) {
+namespace {
+int paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block, int64_t stride_slot,
+                 int64_t stride_head, const int32_t* block_table, int64_t max_blocks, const int64_t* seq_lens_kv,
+                 int64_t b, int hq, int hkv, int d, int dtype, int block_size, float scale, const float* sink,
+                 void* out, float* lse, void* workspace, size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(b >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_paged_decode: heads must be a multiple of kv heads");
   TAI_UNSUPPORTED(dtype != TAI_DT_BF16 && dtype != TAI_DT_FP16, "tai_fia_paged_decode: dtype %d not supported (bf16, "
                   "fp16)", dtype);
@@ -1730,6 +1743,7 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
   a.steps = static_cast<int64_t*>(workspace);
   a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_o);
   a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_ml);
+  a.sink = sink;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nranges) * hkv));
   const dim3 cgrid(static_cast<unsigned>(cdiv(b * hq, 4)));
@@ -1754,6 +1768,29 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
   if (dtype == TAI_DT_FP16) launch(std::true_type());
   else launch(std::false_type());
   return launch_status("tai_fia_paged_decode");
+}
+}  // namespace
+
+extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block,
+                                    int64_t stride_slot, int64_t stride_head, const int32_t* block_table,
+                                    int64_t max_blocks, const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d,
+                                    int dtype, int block_size, float scale, void* out, float* lse, void* workspace,
+                                    size_t ws_bytes, void* stream) {
+  return paged_decode(q, k_cache, v_cache, stride_block, stride_slot, stride_head, block_table, max_blocks,
+                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, nullptr, out, lse, workspace, ws_bytes,
+                      stream);
+}
+
+extern "C" int tai_fia_paged_decode_sink(const void* q, const void* k_cache, const void* v_cache,
+                                         int64_t stride_block, int64_t stride_slot, int64_t stride_head,
+                                         const int32_t* block_table, int64_t max_blocks, const int64_t* seq_lens_kv,
+                                         int64_t b, int hq, int hkv, int d, int dtype, int block_size, float scale,
+                                         const float* sink, void* out, float* lse, void* workspace, size_t ws_bytes,
+                                         void* stream) {
+  TAI_CHECK_ARG(sink != nullptr, "tai_fia_paged_decode_sink: null sink");
+  return paged_decode(q, k_cache, v_cache, stride_block, stride_slot, stride_head, block_table, max_blocks,
+                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, sink, out, lse, workspace, ws_bytes,
+                      stream);
 }
 
 extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv) {
