@@ -433,6 +433,19 @@ int tai_fia_paged_decode_sink(const void* q, const void* k_cache, const void* v_
                               const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d, int dtype,
                               int block_size, float scale, const float* sink, void* out, float* lse,
                               void* workspace, size_t ws_bytes, void* stream);
+/* The same over int8 key / value caches with per-channel antiquant scales and no offsets
+ * (key_antiquant_scale / value_antiquant_scale, mode 0; prototype experiment_ops.h:3922-3932):
+ * k = k_cache * k_scale[h * d + c], v = v_cache * v_scale[h * d + c] (fp32, [hkv * d]). The pages the
+ * lengths cover are widened to 16-bit values in the workspace, the query takes the key scale and the
+ * merge the value scale. Caches are int8 with byte strides (multiples of 8). */
+size_t tai_fia_paged_decode_kv8_workspace_size(int64_t b, int hq, int hkv, int d, int64_t max_blocks,
+                                               int block_size);
+int tai_fia_paged_decode_kv8(const void* q, const int8_t* k_cache, const int8_t* v_cache,
+                             int64_t stride_block, int64_t stride_slot, int64_t stride_head,
+                             const int32_t* block_table, int64_t max_blocks,
+                             const int64_t* seq_lens_kv, int64_t b, int hq, int hkv, int d, int dtype,
+                             int block_size, float scale, const float* k_scale, const float* v_scale,
+                             void* out, float* lse, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * npu_fused_infer_attention_score with query sequences (GQA prefill, chunked prefill over a paged

@@ -129,4 +129,5 @@ def test_random_attention_configuration(seed):
     for i in range(b):
         np.testing.assert_allclose(np.where(np.isfinite(lse_np[i, :, :lq[i]]), lse_np[i, :, :lq[i]], -1e30),
                                    np.where(np.isfinite(wl[i, :, :lq[i]]), wl[i, :, :lq[i]], -1e30),
-                                   rtol=1e-3, atol=1e-3, err_msg=str(case))
+                                   # int8 one-token decode rounds q * key scale to bf16 for the MFMA
+                                   rtol=1e-3, atol=1e-2 if kv8 else 1e-3, err_msg=str(case))

@@ -18,6 +18,7 @@ so a captured graph replays correctly with new lengths.
 from __future__ import annotations
 
 import ctypes
+import types
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -312,6 +313,20 @@ def fia_cuda(query, key, value, **kw):
         blk = kw.get("block_size", 0) or bs
         _check(blk == bs, "npu_fused_infer_attention_score: block_size does not match the cache")
         whole = s == 1 and pre >= _NO_BOUND and (nxt >= _NO_BOUND or (mask_origin == 1 and nxt >= 0))
+        if (kv8 and whole and not explicit and not quant_out and pse is None and bs % 32 == 0 and d in (64, 128, 256)
+                and not packed and key.stride(-1) == 1 and value.stride() == key.stride()):
+            # one query token over int8 caches with per-channel scales and no offsets: the decode kernel
+            aq, keep = types.SimpleNamespace(), []
+            _antiquant_params(aq, kw, b, n_kv, d, d, keep)
+            if aq.k_quant_mode == 0 and aq.v_quant_mode == 0 and aq.k_offset is None and aq.v_offset is None:
+                q = query.contiguous()
+                ws_bytes = _lib.query("tai_fia_paged_decode_kv8_workspace_size", b, num_heads, n_kv, d, bt.size(1), bs)
+                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+                _lib.call("tai_fia_paged_decode_kv8", q.data_ptr(), key.data_ptr(), value.data_ptr(), sb, ss, sh,
+                          bt.data_ptr(), bt.size(1), seq_kv.data_ptr(), b, num_heads, n_kv, d, dt, bs, scale,
+                          aq.k_scale, aq.v_scale, out.data_ptr(), lse.data_ptr() if want_lse else None, ws.data_ptr(),
+                          ws_bytes, stream)
+                return out, lse
         # the tiled kernels step through pages 32 tokens at a time
         if (explicit or kv8 or quant_out or (pse is not None and not (sink_only and whole)) or bs % 32 != 0
                 or d not in (64, 128, 256) or (s > 1 and d not in (64, 128)) or packed):

@@ -115,6 +115,10 @@ _SIGS = {
     "tai_fia_paged_decode_sink": (
         c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
                 c_float, _P, _P, _P, _P, c_size_t, _P]),
+    "tai_fia_paged_decode_kv8_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int, c_int64, c_int]),
+    "tai_fia_paged_decode_kv8": (
+        c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
+                c_float, _P, _P, _P, _P, _P, c_size_t, _P]),
     "tai_fia_prefill_workspace_size": (c_size_t, [c_int64, c_int64, c_int, c_int]),
     "tai_fia_prefill": (
         c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int,

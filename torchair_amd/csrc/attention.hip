@@ -99,6 +99,7 @@ struct DecodeArgs {
   int nranges;     // step ranges of a launch (one wave per range and kv head)
   int64_t* steps;  // [0] = balance units of the batch, [1 + b] = units before sequence b
   const float* sink;  // NULL or [hq] fp32: learnable_sink logits, joined to each row's max and sum by the merge
+  const float* vsc;   // NULL or [hkv * D] fp32: per-channel value scales the merge applies (int8 caches)
   float* part_o;   // [slot, hkv, 16, D], slot = range + sequence
   float* part_ml;  // [slot, hkv, 16, 2]
 };
@@ -464,6 +465,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, uint1
 #pragma unroll
     for (int e = 0; e < E; ++e) num[e] *= c;
     M = m_new;
+  }
+  if (a.vsc) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) num[e] *= a.vsc[kvh * D + E * lane + e];
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) o[e] = Half<F16>::bits(den > 0.0f ? num[e] / den : 0.0f);
@@ -1712,10 +1717,60 @@ extern "C" size_t tai_fia_paged_decode_workspace_size(int64_t b, int hq, int d, 
 }
 
 namespace {
+// int8 pages -> 16-bit pages (the int8 values themselves, exact in bf16 and fp16): page p of sequence
+// s, for the pages its length covers, goes to staging page s * max_blocks + p, and bt2 maps it there.
+// One workgroup per (page, sequence); 8 bytes per thread step.
+__global__ __launch_bounds__(256) void kv8_widen_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v,
+                                                        int64_t sb, int64_t ss, int64_t sh, const int32_t* bt,
+                                                        int64_t max_blocks, const int64_t* lens, int bs, int hkv, int d,
+                                                        bool f16, uint16_t* kw, uint16_t* vw, int32_t* bt2) {
+  const int64_t page = blockIdx.x, seq = blockIdx.y;
+  const int64_t idx = seq * max_blocks + page;
+  if (threadIdx.x == 0) bt2[idx] = static_cast<int32_t>(idx);
+  const int64_t len = imax64(0, imin64(lens[seq], max_blocks * bs));
+  if (page * bs >= len) return;
+  const int64_t blk = bt[idx];
+  const int cpr = d / 8;  // 8-byte chunks per (slot, head) row
+  const int n = bs * hkv * cpr;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const int row = c / cpr, ch = c - row * cpr;
+    const int slot = row / hkv, head = row - slot * hkv;
+    const int64_t src = blk * sb + slot * ss + head * sh + 8 * ch;
+    const int64_t dst = (idx * bs + slot) * static_cast<int64_t>(hkv) * d + static_cast<int64_t>(head) * d + 8 * ch;
+    const uint2 ku = *reinterpret_cast<const uint2*>(k + src);
+    const uint2 vu = *reinterpret_cast<const uint2*>(v + src);
+    uint32_t ko[4], vo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t kwd = q < 2 ? ku.x : ku.y, vwd = q < 2 ? vu.x : vu.y;
+      const int sh0 = 16 * (q & 1);
+      auto cvt = [&](uint32_t wd, int s) {
+        const float x = static_cast<float>(static_cast<int8_t>((wd >> s) & 0xffu));
+        return static_cast<uint32_t>(f16 ? f32_to_f16(x) : f32_to_bf16(x));
+      };
+      ko[q] = cvt(kwd, sh0) | (cvt(kwd, sh0 + 8) << 16);
+      vo[q] = cvt(vwd, sh0) | (cvt(vwd, sh0 + 8) << 16);
+    }
+    *reinterpret_cast<uint4*>(kw + dst) = make_uint4(ko[0], ko[1], ko[2], ko[3]);
+    *reinterpret_cast<uint4*>(vw + dst) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+  }
+}
+
+// q * key scale per channel, rounded to the query's dtype: q.(k * sc) = (q * sc).k
+__global__ __launch_bounds__(256) void q_scale_kernel(const uint16_t* q, const float* ksc, int64_t n, int hq, int hkv,
+                                                      int d, bool f16, uint16_t* q2) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int dd = static_cast<int>(i % d);
+  const int h = static_cast<int>((i / d) % hq);
+  const float x = (f16 ? f16_to_f32(q[i]) : bf16_to_f32(q[i])) * ksc[(h / (hq / hkv)) * d + dd];
+  q2[i] = f16 ? f32_to_f16(x) : f32_to_bf16(x);
+}
+
 int paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_t stride_block, int64_t stride_slot,
                  int64_t stride_head, const int32_t* block_table, int64_t max_blocks, const int64_t* seq_lens_kv,
                  int64_t b, int hq, int hkv, int d, int dtype, int block_size, float scale, const float* sink,
-                 void* out, float* lse, void* workspace, size_t ws_bytes, void* stream) {
+                 const float* vsc, void* out, float* lse, void* workspace, size_t ws_bytes, void* stream) {
   TAI_CHECK_ARG(b >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "tai_fia_paged_decode: heads must be a multiple of kv heads");
   TAI_UNSUPPORTED(dtype != TAI_DT_BF16 && dtype != TAI_DT_FP16, "tai_fia_paged_decode: dtype %d not supported (bf16, "
                   "fp16)", dtype);
@@ -1744,6 +1799,7 @@ int paged_decode(const void* q, const void* k_cache, const void* v_cache, int64_
   a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_o);
   a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.part_ml);
   a.sink = sink;
+  a.vsc = vsc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nranges) * hkv));
   const dim3 cgrid(static_cast<unsigned>(cdiv(b * hq, 4)));
@@ -1777,8 +1833,8 @@ extern "C" int tai_fia_paged_decode(const void* q, const void* k_cache, const vo
                                     int dtype, int block_size, float scale, void* out, float* lse, void* workspace,
                                     size_t ws_bytes, void* stream) {
   return paged_decode(q, k_cache, v_cache, stride_block, stride_slot, stride_head, block_table, max_blocks,
-                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, nullptr, out, lse, workspace, ws_bytes,
-                      stream);
+                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, nullptr, nullptr, out, lse, workspace,
+                      ws_bytes, stream);
 }
 
 extern "C" int tai_fia_paged_decode_sink(const void* q, const void* k_cache, const void* v_cache,
@@ -1789,8 +1845,77 @@ extern "C" int tai_fia_paged_decode_sink(const void* q, const void* k_cache, con
                                          void* stream) {
   TAI_CHECK_ARG(sink != nullptr, "tai_fia_paged_decode_sink: null sink");
   return paged_decode(q, k_cache, v_cache, stride_block, stride_slot, stride_head, block_table, max_blocks,
-                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, sink, out, lse, workspace, ws_bytes,
-                      stream);
+                      seq_lens_kv, b, hq, hkv, d, dtype, block_size, scale, sink, nullptr, out, lse, workspace,
+                      ws_bytes, stream);
+}
+
+namespace {
+// int8 decode workspace: [decode workspace][k staging][v staging][bt2][q2], each 256-byte aligned
+struct Kv8Ws {
+  size_t kst, vst, bt2, q2, total;
+};
+Kv8Ws kv8_ws(int64_t b, int hq, int hkv, int d, int64_t max_blocks, int bs) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  Kv8Ws w;
+  const size_t st = static_cast<size_t>(b) * max_blocks * bs * hkv * d * 2;
+  w.kst = up(dec_ws(b, hkv, d).total);
+  w.vst = w.kst + up(st);
+  w.bt2 = w.vst + up(st);
+  w.q2 = w.bt2 + up(static_cast<size_t>(b) * max_blocks * 4);
+  w.total = w.q2 + up(static_cast<size_t>(b) * hq * d * 2);
+  return w;
+}
+}  // namespace
+
+extern "C" size_t tai_fia_paged_decode_kv8_workspace_size(int64_t b, int hq, int hkv, int d, int64_t max_blocks,
+                                                         int block_size) {
+  if (b <= 0 || hq <= 0 || hkv <= 0 || d <= 0 || max_blocks <= 0 || block_size <= 0) return 256;
+  return kv8_ws(b, hq, hkv, d, max_blocks, block_size).total;
+}
+
+extern "C" int tai_fia_paged_decode_kv8(const void* q, const int8_t* k_cache, const int8_t* v_cache,
+                                        int64_t stride_block, int64_t stride_slot, int64_t stride_head,
+                                        const int32_t* block_table, int64_t max_blocks, const int64_t* seq_lens_kv,
+                                        int64_t b, int hq, int hkv, int d, int dtype, int block_size, float scale,
+                                        const float* k_scale, const float* v_scale, void* out, float* lse,
+                                        void* workspace, size_t ws_bytes, void* stream) {
+  TAI_CHECK_ARG(b >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && max_blocks > 0,
+                "tai_fia_paged_decode_kv8: bad sizes or head counts");
+  TAI_UNSUPPORTED(dtype != TAI_DT_BF16 && dtype != TAI_DT_FP16, "tai_fia_paged_decode_kv8: dtype %d not supported "
+                  "(bf16, fp16)", dtype);
+  TAI_UNSUPPORTED(d != 64 && d != 128 && d != 256, "tai_fia_paged_decode_kv8: head_dim %d not supported (64/128/256)", d);
+  TAI_UNSUPPORTED(block_size <= 0 || block_size % kStep != 0, "tai_fia_paged_decode_kv8: block_size must be a "
+                  "multiple of %d", kStep);
+  TAI_CHECK_ARG((stride_slot % 8) == 0 && (stride_head % 8) == 0 && (stride_block % 8) == 0 &&
+                    (reinterpret_cast<uintptr_t>(k_cache) % 8) == 0 && (reinterpret_cast<uintptr_t>(v_cache) % 8) == 0,
+                "tai_fia_paged_decode_kv8: int8 cache rows must be 8-byte aligned");
+  if (b == 0) return TAI_OK;
+  TAI_CHECK_ARG(q && k_cache && v_cache && block_table && seq_lens_kv && out && k_scale && v_scale,
+                "tai_fia_paged_decode_kv8: null pointer");
+  const Kv8Ws w = kv8_ws(b, hq, hkv, d, max_blocks, block_size);
+  if (workspace == nullptr || ws_bytes < w.total) {
+    set_error("tai_fia_paged_decode_kv8: workspace of %zu bytes, need %zu", ws_bytes, w.total);
+    return TAI_ERR_WORKSPACE;
+  }
+  TAI_CHECK_ARG(max_blocks <= 65535 && b <= 65535 && b * max_blocks < (int64_t(1) << 31),
+                "tai_fia_paged_decode_kv8: at most 65535 sequences and 65535 pages per sequence");
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* kst = reinterpret_cast<uint16_t*>(ws + w.kst);
+  uint16_t* vst = reinterpret_cast<uint16_t*>(ws + w.vst);
+  int32_t* bt2 = reinterpret_cast<int32_t*>(ws + w.bt2);
+  uint16_t* q2 = reinterpret_cast<uint16_t*>(ws + w.q2);
+  const bool f16 = dtype == TAI_DT_FP16;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  kv8_widen_kernel<<<dim3(static_cast<unsigned>(max_blocks), static_cast<unsigned>(b)), 256, 0, st>>>(
+      k_cache, v_cache, stride_block, stride_slot, stride_head, block_table, max_blocks, seq_lens_kv, block_size, hkv,
+      d, f16, kst, vst, bt2);
+  const int64_t nq = b * hq * d;
+  q_scale_kernel<<<dim3(static_cast<unsigned>(cdiv(nq, 256))), 256, 0, st>>>(static_cast<const uint16_t*>(q), k_scale,
+                                                                              nq, hq, hkv, d, f16, q2);
+  if (launch_status("tai_fia_paged_decode_kv8") != TAI_OK) return TAI_ERR_LAUNCH;
+  const int64_t sslot = static_cast<int64_t>(hkv) * d;
+  return paged_decode(q2, kst, vst, sslot * block_size, sslot, d, bt2, max_blocks, seq_lens_kv, b, hq, hkv, d, dtype,
+                      block_size, scale, nullptr, v_scale, out, lse, workspace, w.kst, stream);
 }
 
 extern "C" size_t tai_fia_prefill_workspace_size(int64_t b, int64_t s_q, int hq, int hkv) {
