@@ -360,3 +360,47 @@ def test_compiled_int8_query_and_learnable_sink_are_captured():
             _churn()
         assert tai_graph.stats["captures"] == caps + 1
         assert tai_graph.stats["eager_fallbacks"] == falls
+
+
+def test_compiled_int8_cache_and_sink_decode_replay_with_new_lengths():
+    """The one-token decode over int8 caches (pages widened in the workspace, then the decode kernel) and
+    with a learnable_sink (taken in by the merge) captured once each; every replay, with new lengths and
+    block tables, equals the eager call."""
+    g = torch.Generator().manual_seed(53)
+    b, hq, hkv, d, bs, width = 8, 32, 8, 128, 64, 16
+    nblk = b * width
+    k8 = torch.randint(-128, 128, (nblk, bs, hkv * d), generator=g, dtype=torch.int8).to(DEV)
+    v8 = torch.randint(-128, 128, (nblk, bs, hkv * d), generator=g, dtype=torch.int8).to(DEV)
+    ks = (torch.rand(hkv * d, generator=g) * 0.02 + 0.005).to(DEV)
+    vs = (torch.rand(hkv * d, generator=g) * 0.02 + 0.005).to(DEV)
+    kc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(nblk, bs, hkv * d, generator=g).to(torch.bfloat16).to(DEV)
+    sink = (torch.randn(hq, generator=g) * 2).to(torch.bfloat16).to(DEV)
+
+    def step8(q, lens, bt):
+        return torch.ops.air.npu_fused_infer_attention_score(
+            q, k8, v8, actual_seq_lengths_kv=lens, block_table=bt, num_heads=hq, num_key_value_heads=hkv,
+            input_layout="BSH", block_size=bs, scale=1.0 / math.sqrt(d), key_antiquant_scale=ks,
+            value_antiquant_scale=vs)[0]
+
+    def step_sink(q, lens, bt):
+        return torch.ops.air.npu_fused_infer_attention_score_v2(
+            q, kc, vc, actual_seq_kvlen=lens, block_table=bt, num_query_heads=hq, num_key_value_heads=hkv,
+            input_layout="BSH", block_size=bs, softmax_scale=1.0 / math.sqrt(d), learnable_sink=sink)[0]
+
+    for step in (step8, step_sink):
+        fn = torch.compile(step, backend=_backend(), fullgraph=True)
+        caps, falls = tai_graph.stats["captures"], tai_graph.stats["eager_fallbacks"]
+        for i in range(4):
+            lens = torch.randint(1, width * bs + 1, (b,), generator=g)
+            if i == 2:
+                lens[3] = 0  # an empty sequence
+            bt = _paged(g, lens.tolist(), nblk, width, bs, hkv, d)
+            q = torch.randn(b, 1, hq * d, generator=g).to(torch.bfloat16)
+            print("case", step.__name__, "replay", i, flush=True)
+            got = fn(q.to(DEV), lens.to(DEV), bt.to(DEV)).clone()
+            want = step(q.to(DEV), lens.to(DEV), bt.to(DEV))
+            assert torch.equal(got, want), f"{step.__name__}: replay {i} differs from eager"
+            _churn()
+        assert tai_graph.stats["captures"] == caps + 1
+        assert tai_graph.stats["eager_fallbacks"] == falls
